@@ -1,0 +1,344 @@
+#!/usr/bin/env python3
+"""Benchmark of the eyebrowse attention hot path on one MI355X.
+
+Headline (`value`): BASELINE config 2 at its largest point: a Qwen3-0.6B-shaped batch-1
+decode step at L = 8191 (new token's K/V written at position 8191 by kv_write, then
+attention over 8192 keys of a max_seq 8192 f32 cache, 16 query / 8 KV heads, hd 128).
+value = KV bytes read per step (2 * keys * Hkv * hd * 4) * steps / time, in GB/s.
+
+One step = one HIP-graph launch of [kv_write K, kv_write V, attn_decode] (the kernels the
+library records for Attention::decode, crates/eyebrowse-nn/src/attention.rs:149-183).
+Steps rotate over enough distinct caches that the working set exceeds the 256 MB Infinity
+Cache, so the K/V bytes come from HBM. Inputs are resident in HBM before timing starts.
+
+Also reported: prefill TFLOP/s (2*H*hd*T*(T+1) algorithmic FLOPs) for the BASELINE
+prefill configs, decode GB/s at every BASELINE decode config, the roofline of the dominant
+kernel, and the CPU oracle timed on this host (cpu_baseline).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "prefill attn TFLOP/s + decode KV-read GB/s, as % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
+MALL_BYTES = 256 << 20
+
+
+# ------------------------------------------------------------------ HIP runtime via ctypes
+
+class Hip:
+    """The few HIP runtime calls the harness needs: events and stream capture."""
+
+    def __init__(self):
+        self.l = ctypes.CDLL("libamdhip64.so")
+        vp, pvp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        sig = {
+            "hipEventCreate": [pvp], "hipEventRecord": [vp, vp], "hipEventSynchronize": [vp],
+            "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), vp, vp],
+            "hipEventDestroy": [vp], "hipStreamBeginCapture": [vp, ctypes.c_int],
+            "hipStreamEndCapture": [vp, pvp],
+            "hipGraphInstantiate": [pvp, vp, vp, ctypes.c_char_p, ctypes.c_size_t],
+            "hipGraphLaunch": [vp, vp], "hipGraphExecDestroy": [vp], "hipGraphDestroy": [vp],
+            "hipStreamSynchronize": [vp], "hipDeviceSynchronize": [],
+        }
+        for name, args in sig.items():
+            f = getattr(self.l, name)
+            f.restype = ctypes.c_int
+            f.argtypes = args
+
+    def ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
+
+    def event(self):
+        e = ctypes.c_void_p()
+        self.ok(self.l.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e
+
+    def elapsed_ms(self, a, b):
+        self.ok(self.l.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self.ok(self.l.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return float(ms.value)
+
+    def capture(self, stream, fn):
+        """Record fn()'s launches on `stream` into an executable graph."""
+        s = ctypes.c_void_p(stream)
+        self.ok(self.l.hipStreamBeginCapture(s, 0), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = ctypes.c_void_p()
+            rc = self.l.hipStreamEndCapture(s, ctypes.byref(g))
+        self.ok(rc, "hipStreamEndCapture")
+        ge = ctypes.c_void_p()
+        self.ok(self.l.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0),
+                "hipGraphInstantiate")
+        self.ok(self.l.hipGraphDestroy(g), "hipGraphDestroy")
+        return ge
+
+    def launch(self, ge, stream):
+        self.ok(self.l.hipGraphLaunch(ge, ctypes.c_void_p(stream)), "hipGraphLaunch")
+
+    def time_loop(self, stream, n, body):
+        """Average ms of body(i) over n iterations, bracketed by HIP events on `stream`."""
+        a, b = self.event(), self.event()
+        s = ctypes.c_void_p(stream)
+        self.ok(self.l.hipStreamSynchronize(s), "hipStreamSynchronize")
+        self.ok(self.l.hipEventRecord(a, s), "hipEventRecord")
+        for i in range(n):
+            body(i)
+        self.ok(self.l.hipEventRecord(b, s), "hipEventRecord")
+        ms = self.elapsed_ms(a, b)
+        self.l.hipEventDestroy(a)
+        self.l.hipEventDestroy(b)
+        return ms / n
+
+
+# ------------------------------------------------------------------ workloads
+
+def randn(rng, shape):
+    return rng.standard_normal(shape, dtype=np.float32)
+
+
+class DecodeWorkload:
+    """Batch-1 decode step at position `pos` over `n_caches` distinct [max_seq, Hkv, hd]
+    K/V caches (rows 0..pos-1 filled), with the new token's K/V written at `pos`."""
+
+    def __init__(self, eb, hip, dev, H, Hkv, hd, max_seq, pos, scale, seed=0):
+        self.eb, self.hip, self.dev = eb, hip, dev
+        self.H, self.Hkv, self.hd, self.max_seq, self.pos, self.scale = H, Hkv, hd, max_seq, pos, scale
+        self.keys = pos + 1
+        self.kv_bytes = 2 * self.keys * Hkv * hd * 4
+        cache_bytes = 2 * max_seq * Hkv * hd * 4
+        self.n_caches = max(3, int(np.ceil(1.5 * MALL_BYTES / cache_bytes)) + 1)
+        rng = np.random.default_rng(seed)
+        kfill = randn(rng, (max_seq, Hkv, hd))
+        vfill = randn(rng, (max_seq, Hkv, hd))
+        self.caches = []
+        for _ in range(self.n_caches):
+            self.caches.append((eb.Tensor.from_f32(dev, kfill.shape, kfill),
+                                eb.Tensor.from_f32(dev, vfill.shape, vfill)))
+        del kfill, vfill
+        self.q = eb.Tensor.from_f32(dev, (H, hd), randn(rng, (H, hd)))
+        self.knew = eb.Tensor.from_f32(dev, (1, Hkv, hd), randn(rng, (1, Hkv, hd)))
+        self.vnew = eb.Tensor.from_f32(dev, (1, Hkv, hd), randn(rng, (1, Hkv, hd)))
+        self.o = eb.Tensor.empty(dev, (H, hd))
+        self.cus = dev.cu_count
+        self.wsn = eb.attn_decode_workspace_floats(H, Hkv, pos, hd, self.cus)
+        self.ws = eb.Tensor.empty(dev, (max(self.wsn, 1),))
+        st = dev.stream
+        self.step_graphs = [hip.capture(st, lambda c=c: self._step(c, True)) for c in self.caches]
+        self.attn_graphs = [hip.capture(st, lambda c=c: self._step(c, False)) for c in self.caches]
+
+    def _step(self, cache, with_write):
+        eb, st = self.eb, self.dev.stream
+        kc, vc = cache
+        if with_write:
+            eb.launch_kv_write(st, kc.data_ptr, kc.numel(), self.knew.data_ptr, self.knew.numel(),
+                               self.Hkv, 1, self.hd, self.max_seq, self.pos)
+            eb.launch_kv_write(st, vc.data_ptr, vc.numel(), self.vnew.data_ptr, self.vnew.numel(),
+                               self.Hkv, 1, self.hd, self.max_seq, self.pos)
+        eb.launch_attn_decode(st, self.q.data_ptr, self.q.numel(), kc.data_ptr, kc.numel(),
+                              vc.data_ptr, vc.numel(), self.o.data_ptr, self.o.numel(), self.H,
+                              self.Hkv, self.pos, self.hd, self.max_seq, self.scale,
+                              self.ws.data_ptr, self.wsn, self.cus)
+
+    def run_steps(self, n, graphs):
+        st = self.dev.stream
+        return self.hip.time_loop(st, n, lambda i: self.hip.launch(graphs[i % len(graphs)], st))
+
+    def close(self):
+        for g in self.step_graphs + self.attn_graphs:
+            self.hip.l.hipGraphExecDestroy(g)
+
+
+class PrefillWorkload:
+    """Causal prefill over T tokens: K/V written by kv_write into a [T, Hkv, hd] cache,
+    attention over the fresh K/V."""
+
+    def __init__(self, eb, dev, H, Hkv, hd, T, scale, seed=0):
+        self.eb, self.dev = eb, dev
+        self.H, self.Hkv, self.hd, self.T, self.scale = H, Hkv, hd, T, scale
+        self.flops = 2.0 * H * hd * T * (T + 1)
+        rng = np.random.default_rng(seed)
+        self.q = eb.Tensor.from_f32(dev, (T, H, hd), randn(rng, (T, H, hd)))
+        self.k = eb.Tensor.from_f32(dev, (T, Hkv, hd), randn(rng, (T, Hkv, hd)))
+        self.v = eb.Tensor.from_f32(dev, (T, Hkv, hd), randn(rng, (T, Hkv, hd)))
+        self.o = eb.Tensor.empty(dev, (T, H, hd))
+
+    def launch(self):
+        e = self.eb
+        e.launch_attn_prefill(self.dev.stream, self.q.data_ptr, self.q.numel(), self.k.data_ptr,
+                              self.k.numel(), self.v.data_ptr, self.v.numel(), self.o.data_ptr,
+                              self.o.numel(), self.H, self.Hkv, self.T, self.hd, self.scale)
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """The oracle (a C restatement of the reference's CPU attention,
+    crates/eyebrowse-kernels/src/testutil.rs:177-218) timed on this host's cores, single
+    thread, on the headline decode step (8192 keys, Qwen shape) repeated for ~budget_s."""
+    import oracle
+
+    H, Hkv, hd, max_seq, pos = 16, 8, 128, 8192, 8191
+    rng = np.random.default_rng(1)
+    q = randn(rng, (H, hd))
+    kc = randn(rng, (max_seq, Hkv, hd))
+    vc = randn(rng, (max_seq, Hkv, hd))
+    sc = float(oracle.default_scale(hd))
+    oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            break
+    kv_bytes = 2 * (pos + 1) * Hkv * hd * 4
+    gbs = kv_bytes * n / dt / 1e9
+
+    # prefill sample: the last 16 query rows of Qwen T=4096 (the heaviest rows)
+    T = 4096
+    pq, pk, pv = randn(rng, (T, H, hd)), randn(rng, (T, Hkv, hd)), randn(rng, (T, Hkv, hd))
+    rows = 16
+    t1 = time.perf_counter()
+    oracle.attn_prefill(pq, pk, pv, H, Hkv, T, hd, sc, rows=(T - rows, rows), threads=1)
+    pdt = time.perf_counter() - t1
+    pflops = sum(2.0 * 2 * H * hd * (i + 1) for i in range(T - rows, T))
+    return {
+        "value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"oracle attn_decode, Qwen3 shape 16/8 heads hd128, 8192 keys, {n} calls "
+                  f"in {dt:.1f} s, 1 thread",
+        "prefill_gflops": round(pflops / pdt / 1e9, 3),
+        "prefill_sample": f"oracle attn_prefill, Qwen3 T=4096, last {rows} rows, 1 thread, "
+                          f"{pdt:.1f} s",
+        "host_cpus": os.cpu_count(),
+    }
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["headline", "all"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the eyebrowse attention path is a single-device "
+              "workload and this build has no multi-GPU path (run with --gpus 1).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import eyebrowse_amd as eb
+    hip = Hip()
+    dev = eb.Device.new(0)
+    sc128 = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+
+    # Headline: Qwen decode L=8191.
+    head = DecodeWorkload(eb, hip, dev, 16, 8, 128, 8192, 8191, sc128)
+    head.run_steps(args.warmup, head.step_graphs)
+    dev.synchronize()
+    ms_step = head.run_steps(args.steps, head.step_graphs)
+    dev.synchronize()
+    value = head.kv_bytes / (ms_step * 1e-3) / 1e9
+    # Dominant kernel: attn_decode alone (split-KV pass + merge), same rotation.
+    ms_attn = head.run_steps(max(args.steps, 200), head.attn_graphs)
+    achieved = head.kv_bytes / (ms_attn * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tf):
+        traffic = json.load(open(tf)).get("decode_qwen_L8191")
+
+    extra = {}
+    if args.only == "all":
+        dec_cfgs = [("qwen_L512", 16, 8, 128, 8192, 512, sc128),
+                    ("qwen_L2048", 16, 8, 128, 8192, 2048, sc128),
+                    ("qwen_L4096", 16, 8, 128, 8192, 4096, sc128),
+                    ("mistral_keys8193", 32, 8, 128, 32768, 8192, sc128),
+                    ("mistral_keys32768", 32, 8, 128, 32768, 32767, sc128),
+                    ("gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0)]
+        for name, H, Hkv, hd, ms, pos, sc in dec_cfgs:
+            w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc)
+            w.run_steps(20, w.step_graphs)
+            t_step = w.run_steps(300, w.step_graphs)
+            t_attn = w.run_steps(300, w.attn_graphs)
+            extra[f"decode_{name}"] = {
+                "keys": pos + 1, "kv_bytes": w.kv_bytes, "ms_step": round(t_step, 5),
+                "step_GBs": round(w.kv_bytes / t_step / 1e6, 1),
+                "attn_ms": round(t_attn, 5), "attn_GBs": round(w.kv_bytes / t_attn / 1e6, 1),
+                "attn_frac_hbm": round(w.kv_bytes / t_attn / 1e6 / HBM_PEAK_GBS, 4)}
+            w.close()
+            del w
+            dev.synchronize()
+        pre_cfgs = [("qwen_T512", 16, 8, 128, 512, sc128),
+                    ("qwen_T2048", 16, 8, 128, 2048, sc128),
+                    ("qwen_T4096", 16, 8, 128, 4096, sc128),
+                    ("mistral_T4096", 32, 8, 128, 4096, sc128),
+                    ("gemma_T4096", 16, 8, 256, 4096, 1.0)]
+        for name, H, Hkv, hd, T, sc in pre_cfgs:
+            p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc)
+            for _ in range(3):
+                p.launch()
+            reps = 20 if T >= 2048 else 100
+            t = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+            tf_s = p.flops / (t * 1e-3) / 1e12
+            extra[f"prefill_{name}"] = {
+                "gflop": round(p.flops / 1e9, 3), "ms": round(t, 4), "TFLOPs": round(tf_s, 2),
+                "mfma": "fp32 (v_mfma_f32_32x32x2_f32)",
+                "frac_fp32_mfma_peak": round(tf_s / FP32_MFMA_PEAK_TFLOPS, 4)}
+            del p
+            dev.synchronize()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "qwen3-0.6b-shaped batch-1 decode step at L=8191: kv_write of the new "
+                        "token at pos 8191 + attention over 8192 keys (BASELINE configs[1])",
+            "n_heads": 16, "n_kv_heads": 8, "head_dim": 128, "max_seq": 8192, "pos": 8191,
+            "kv_caches_rotated": head.n_caches, "launch": "one hipGraph per step",
+        },
+        "roofline": {
+            "bound": "hbm", "kernel": "attn_decode (split-KV pass + log-sum-exp merge)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": head.kv_bytes, "avg_launch_ms": round(ms_attn, 6),
+        },
+        "extra": extra,
+    }
+    head.close()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,25 @@
+"""eyebrowse_amd: the eyebrowse attention hot path (prefill, decode, kv-write) on MI355X.
+
+The compute lives in ``libeyebrowse_hip.so`` (hand-written gfx950 HIP kernels behind the C
+ABI in ``include/eyebrowse_hip.h``); this package is a thin ctypes mirror of the
+reference's Rust interface:
+
+- ``gpu``: DType, EyebrowseError, Device, Tensor, Recorder (crates/eyebrowse-gpu);
+- ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels);
+- ``nn``: Rope, KvCache, Attention (crates/eyebrowse-nn).
+"""
+from ._lib import LIB_PATH, lib
+from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, OutOfMemory,
+                  Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
+from .kernels import (attn_decode, attn_decode_workspace_floats, attn_prefill, kv_write,
+                      launch_attn_decode, launch_attn_prefill, launch_kv_write, launch_rmsnorm,
+                      launch_rope, rmsnorm, rope)
+from .nn import Attention, KvCache, Rope
+
+__all__ = [
+    "LIB_PATH", "lib", "DType", "Device", "DeviceUnavailable", "EyebrowseError", "LoadError",
+    "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
+    "attn_decode_workspace_floats", "attn_prefill", "kv_write", "launch_attn_decode",
+    "launch_attn_prefill", "launch_kv_write", "launch_rmsnorm", "launch_rope", "rmsnorm", "rope",
+    "Attention", "KvCache", "Rope",
+]

@@ -1,0 +1,115 @@
+// kv_write, RMSNorm and RoPE for gfx950: the memory-bound steps around attention.
+//
+//  kv_write  (crates/eyebrowse-kernels/src/ops.rs:70-87,150-179): both sides are
+//            seq-major, so the write is one contiguous copy of count*hkv*hd floats to
+//            element offset dst*hkv*hd. 128-bit loads/stores when aligned; pure copies,
+//            so the result is bit-exact.
+//  rmsnorm   (crates/eyebrowse-kernels/src/rmsnorm.rs:6-64): one wave per row, the sum of
+//            squares reduced across the wave, y = x * (1/sqrt(ss/dim + eps)) * w.
+//  rope      (crates/eyebrowse-kernels/src/rope.rs:6-69): one thread per rotated pair.
+#include "eb_common.h"
+#include "eb_internal.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__global__ __launch_bounds__(kBlock) void kv_write_vec4_kernel(float4 *__restrict__ dst,
+                                                               const float4 *__restrict__ src,
+                                                               unsigned n4) {
+    unsigned stride = gridDim.x * kBlock;
+    for (unsigned i = blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(kBlock) void kv_write_scalar_kernel(float *__restrict__ dst,
+                                                                 const float *__restrict__ src,
+                                                                 unsigned n) {
+    unsigned stride = gridDim.x * kBlock;
+    for (unsigned i = blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+unsigned copy_grid(size_t n) {
+    size_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 4096) blocks = 4096;  // grid-stride beyond 16 blocks per CU
+    return blocks == 0 ? 1u : (unsigned)blocks;
+}
+
+// One wave per row; rows_per_block rows per 256-thread block.
+__global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float *__restrict__ x,
+                                                         const float *__restrict__ w,
+                                                         float *__restrict__ out, unsigned rows,
+                                                         unsigned dim, float eps) {
+    const unsigned lane = threadIdx.x & 63;
+    const unsigned row = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + (size_t)row * dim;
+    float ss = 0.0f;
+    for (unsigned i = lane; i < dim; i += 64) {
+        float t = xr[i];
+        ss += t * t;
+    }
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    float *orow = out + (size_t)row * dim;
+    for (unsigned i = lane; i < dim; i += 64) orow[i] = xr[i] * inv * w[i];
+}
+
+__global__ __launch_bounds__(kBlock) void rope_kernel(const float *__restrict__ x,
+                                                      const float *__restrict__ cosb,
+                                                      const float *__restrict__ sinb,
+                                                      float *__restrict__ out, unsigned total,
+                                                      unsigned n_heads, unsigned half,
+                                                      unsigned base_pos) {
+    unsigned idx = blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= total) return;
+    unsigned p = idx % half;
+    unsigned tmp = idx / half;
+    unsigned head = tmp % n_heads;
+    unsigned s = tmp / n_heads;
+    size_t base = ((size_t)s * n_heads + head) * (2 * half);
+    float c = cosb[(size_t)(s + base_pos) * half + p];
+    float sn = sinb[(size_t)(s + base_pos) * half + p];
+    float x1 = x[base + p];
+    float x2 = x[base + half + p];
+    out[base + p] = x1 * c - x2 * sn;
+    out[base + half + p] = x2 * c + x1 * sn;
+}
+
+}  // namespace
+
+namespace eb {
+
+eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t hkv,
+                          size_t count, size_t hd, size_t dst_start) {
+    size_t n = count * hkv * hd;
+    float *dst = cache + dst_start * hkv * hd;
+    bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) == 0;
+    if (aligned && n % 4 == 0) {
+        size_t n4 = n / 4;
+        kv_write_vec4_kernel<<<copy_grid(n4), kBlock, 0, st>>>(
+            reinterpret_cast<float4 *>(dst), reinterpret_cast<const float4 *>(src), (unsigned)n4);
+    } else {
+        kv_write_scalar_kernel<<<copy_grid(n), kBlock, 0, st>>>(dst, src, (unsigned)n);
+    }
+    return check_launch("kv_write");
+}
+
+eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
+                         size_t rows, size_t dim, float eps) {
+    unsigned blocks = (unsigned)((rows + 3) / 4);
+    rmsnorm_kernel<<<blocks, kBlock, 0, st>>>(x, w, out, (unsigned)rows, (unsigned)dim, eps);
+    return check_launch("rmsnorm");
+}
+
+eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,
+                      float *out, size_t seq, size_t n_heads, size_t hd, size_t base_pos) {
+    size_t total = seq * n_heads * (hd / 2);
+    if (total == 0) return EB_OK;
+    unsigned blocks = (unsigned)((total + kBlock - 1) / kBlock);
+    rope_kernel<<<blocks, kBlock, 0, st>>>(x, cosb, sinb, out, (unsigned)total,
+                                           (unsigned)n_heads, (unsigned)(hd / 2),
+                                           (unsigned)base_pos);
+    return check_launch("rope");
+}
+
+}  // namespace eb

@@ -1,0 +1,62 @@
+// Shared internals of libeyebrowse_hip: error plumbing, validation helpers and the
+// launch functions each kernel translation unit exports to the runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+
+#include "eyebrowse_hip.h"
+
+namespace eb {
+
+// Records a formatted message as this thread's last error and returns `st`.
+eb_status fail(eb_status st, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clears this thread's last error and returns EB_OK.
+eb_status ok();
+// Maps a HIP error to a status (hipErrorOutOfMemory -> EB_OUT_OF_MEMORY, else EB_OTHER)
+// and records `what` plus HIP's own message.
+eb_status hip_fail(hipError_t e, const char *what);
+
+#define EB_HIP_TRY(expr)                                              \
+    do {                                                              \
+        hipError_t eb_e_ = (expr);                                    \
+        if (eb_e_ != hipSuccess) return ::eb::hip_fail(eb_e_, #expr); \
+    } while (0)
+
+// After a launch: reports a launch-configuration error as EB_OTHER.
+eb_status check_launch(const char *kernel);
+
+// Shared argument checks. Each returns EB_OK or records why the shape is refused.
+eb_status check_ptr(const void *p, const char *name);
+eb_status check_numel(size_t have, size_t need, const char *name);
+eb_status check_heads(size_t h, size_t hkv);
+// Head dims the attention kernels are instantiated for.
+bool attn_head_dim_supported(size_t hd);
+// Largest element count a 32-bit-indexed kernel may address.
+constexpr size_t kMaxIndex = (size_t)1 << 31;
+
+// The device that owns a tensor.
+eb_device *tensor_device(const eb_tensor *t);
+
+// Compute units of the current device (cached per ordinal).
+int current_cu_count();
+
+// ---- kernel launchers (validated arguments, caller's stream) -------------------------
+eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t hkv,
+                          size_t count, size_t hd, size_t dst_start);
+eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
+                              float *o, size_t h, size_t hkv, size_t s, size_t hd,
+                              float scale);
+size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count);
+eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
+                             float *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                             float scale, float *ws, size_t ws_floats, int cu_count);
+eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
+                         size_t rows, size_t dim, float eps);
+eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,
+                      float *out, size_t seq, size_t n_heads, size_t hd, size_t base_pos);
+
+}  // namespace eb

@@ -1,0 +1,261 @@
+// eyebrowse-nn pieces around the attention kernels: Rope tables, KvCache and the
+// Attention forward between the projections.
+//
+//  - eb_rope_build_partial: crates/eyebrowse-nn/src/rope.rs:24-50 (host f64 tables).
+//  - eb_kv_cache_new_per_layer: crates/eyebrowse-nn/src/kv_cache.rs:29-50.
+//  - eb_attention_forward_qkv: crates/eyebrowse-nn/src/attention.rs:30-185 from the
+//    projected q/k/v on (the q/k/v/o projections are the caller's).
+#include <cmath>
+#include <memory>
+#include <vector>
+
+#include "eb_internal.h"
+
+struct eb_rope_tables {
+    eb_tensor *cos = nullptr;
+    eb_tensor *sin = nullptr;
+    size_t head_dim = 0;
+    size_t max_seq = 0;
+};
+
+struct eb_kv_cache {
+    std::vector<eb_tensor *> k, v;
+    size_t max_seq = 0;
+    size_t n_kv_heads = 0;
+};
+
+struct eb_attention {
+    eb_attention_desc d{};
+};
+
+using eb::fail;
+
+#define EB_TRY(expr)                      \
+    do {                                  \
+        eb_status eb_s_ = (expr);         \
+        if (eb_s_ != EB_OK) return eb_s_; \
+    } while (0)
+
+namespace {
+
+// Owns a tensor for the duration of a forward; released (back to the pool) on scope exit.
+struct Owned {
+    eb_tensor *t = nullptr;
+    Owned() = default;
+    explicit Owned(eb_tensor *x) : t(x) {}
+    Owned(const Owned &) = delete;
+    Owned &operator=(const Owned &) = delete;
+    ~Owned() { eb_tensor_release(t); }
+    eb_tensor *release() {
+        eb_tensor *x = t;
+        t = nullptr;
+        return x;
+    }
+};
+
+eb_device *tensor_device_of(const eb_tensor *t) { return eb::tensor_device(t); }
+
+}  // namespace
+
+extern "C" {
+
+eb_status eb_rope_build_partial(eb_device *dev, size_t max_seq, size_t head_dim,
+                                size_t rope_angles, float theta, eb_rope_tables **out) {
+    if (!dev || !out) return fail(EB_OTHER, "device/out is null");
+    if (head_dim == 0 || head_dim % 2 != 0)
+        return fail(EB_SHAPE_MISMATCH, "rope: head_dim must be even and positive");
+    *out = nullptr;
+    const size_t half = head_dim / 2;
+    std::vector<float> c(max_seq * half, 1.0f), s(max_seq * half, 0.0f);
+    const double th = (double)theta;
+    const double hd = (double)head_dim;
+    const size_t na = rope_angles < half ? rope_angles : half;
+    for (size_t p = 0; p < max_seq; ++p)
+        for (size_t kk = 0; kk < na; ++kk) {
+            double inv_freq = std::pow(th, -(2.0 * (double)kk) / hd);
+            double angle = (double)p * inv_freq;
+            c[p * half + kk] = (float)std::cos(angle);
+            s[p * half + kk] = (float)std::sin(angle);
+        }
+    auto r = std::make_unique<eb_rope_tables>();
+    const size_t shape[2] = {max_seq, half};
+    EB_TRY(eb_tensor_from_f32(dev, shape, 2, c.data(), c.size(), &r->cos));
+    eb_status st = eb_tensor_from_f32(dev, shape, 2, s.data(), s.size(), &r->sin);
+    if (st != EB_OK) {
+        eb_tensor_release(r->cos);
+        return st;
+    }
+    r->head_dim = head_dim;
+    r->max_seq = max_seq;
+    *out = r.release();
+    return eb::ok();
+}
+
+void eb_rope_tables_release(eb_rope_tables *rope) {
+    if (!rope) return;
+    eb_tensor_release(rope->cos);
+    eb_tensor_release(rope->sin);
+    delete rope;
+}
+
+const eb_tensor *eb_rope_tables_cos(const eb_rope_tables *rope) { return rope ? rope->cos : nullptr; }
+const eb_tensor *eb_rope_tables_sin(const eb_rope_tables *rope) { return rope ? rope->sin : nullptr; }
+
+eb_status eb_rope_apply(const eb_rope_tables *rope, eb_recorder *rec, const eb_tensor *x, size_t seq,
+                        size_t n_heads, size_t base_pos, eb_tensor **out) {
+    if (!rope || !rec || !x || !out) return fail(EB_OTHER, "rope_apply: null argument");
+    *out = nullptr;
+    if (base_pos + seq > rope->max_seq)
+        return fail(EB_SHAPE_MISMATCH, "rope_apply: positions up to %zu exceed the table (%zu)",
+                    base_pos + seq, rope->max_seq);
+    const size_t shape[3] = {seq, n_heads, rope->head_dim};
+    eb_tensor *o = nullptr;
+    EB_TRY(eb_tensor_empty(tensor_device_of(x), shape, 3, EB_F32, &o));
+    Owned guard(o);
+    EB_TRY(eb_rope(rec, x, rope->cos, rope->sin, o, seq, n_heads, rope->head_dim, base_pos));
+    *out = guard.release();
+    return eb::ok();
+}
+
+eb_status eb_kv_cache_new_per_layer(eb_device *dev, const size_t *head_dims, size_t n_layers,
+                                    size_t max_seq, size_t n_kv_heads, eb_kv_cache **out) {
+    if (!dev || !out || (n_layers > 0 && !head_dims))
+        return fail(EB_OTHER, "kv_cache: null argument");
+    *out = nullptr;
+    auto kv = std::make_unique<eb_kv_cache>();
+    kv->max_seq = max_seq;
+    kv->n_kv_heads = n_kv_heads;
+    for (size_t l = 0; l < n_layers; ++l) {
+        const size_t shape[3] = {max_seq, n_kv_heads, head_dims[l]};
+        eb_tensor *kt = nullptr, *vt = nullptr;
+        eb_status st = eb_tensor_empty(dev, shape, 3, EB_F32, &kt);
+        if (st == EB_OK) st = eb_tensor_empty(dev, shape, 3, EB_F32, &vt);
+        if (st != EB_OK) {
+            eb_tensor_release(kt);
+            eb_kv_cache_release(kv.release());
+            return st;
+        }
+        kv->k.push_back(kt);
+        kv->v.push_back(vt);
+    }
+    *out = kv.release();
+    return eb::ok();
+}
+
+void eb_kv_cache_release(eb_kv_cache *kv) {
+    if (!kv) return;
+    for (eb_tensor *t : kv->k) eb_tensor_release(t);
+    for (eb_tensor *t : kv->v) eb_tensor_release(t);
+    delete kv;
+}
+
+eb_tensor *eb_kv_cache_k(eb_kv_cache *kv, size_t layer) {
+    return (kv && layer < kv->k.size()) ? kv->k[layer] : nullptr;
+}
+eb_tensor *eb_kv_cache_v(eb_kv_cache *kv, size_t layer) {
+    return (kv && layer < kv->v.size()) ? kv->v[layer] : nullptr;
+}
+size_t eb_kv_cache_max_seq(const eb_kv_cache *kv) { return kv ? kv->max_seq : 0; }
+
+eb_status eb_attention_new(const eb_attention_desc *desc, eb_attention **out) {
+    if (!desc || !out) return fail(EB_OTHER, "attention_new: null argument");
+    *out = nullptr;
+    EB_TRY(eb::check_heads(desc->n_heads, desc->n_kv_heads));
+    if (!eb::attn_head_dim_supported(desc->head_dim))
+        return fail(EB_UNSUPPORTED_CONFIG, "attention: head_dim %zu not supported",
+                    desc->head_dim);
+    const eb_tensor *norms[3] = {desc->q_norm, desc->k_norm, desc->v_norm};
+    for (const eb_tensor *n : norms)
+        if (n && (eb_tensor_dtype(n) != EB_F32 || eb_tensor_numel(n) != desc->head_dim))
+            return fail(EB_SHAPE_MISMATCH, "attention: norm weights must be [head_dim] f32");
+    auto a = std::make_unique<eb_attention>();
+    a->d = *desc;
+    *out = a.release();
+    return eb::ok();
+}
+
+void eb_attention_release(eb_attention *attn) { delete attn; }
+
+}  // extern "C"
+
+namespace {
+
+// Optional per-head RMSNorm (attention.rs:62-73): rows x head_dim, or a pass-through.
+eb_status maybe_norm(eb_recorder *rec, const eb_tensor *w, const eb_tensor *x, size_t rows,
+                     size_t hd, float eps, Owned &holder, const eb_tensor **y) {
+    if (!w) {
+        *y = x;
+        return EB_OK;
+    }
+    const size_t shape[2] = {rows, hd};
+    eb_tensor *o = nullptr;
+    EB_TRY(eb_tensor_empty(tensor_device_of(x), shape, 2, EB_F32, &o));
+    holder.t = o;
+    EB_TRY(eb_rmsnorm(rec, x, w, o, rows, hd, eps));
+    *y = o;
+    return EB_OK;
+}
+
+}  // namespace
+
+extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recorder *rec,
+                                              const eb_tensor *q, const eb_tensor *k,
+                                              const eb_tensor *v, const eb_rope_tables *rope,
+                                              eb_kv_cache *kv, size_t layer, size_t rows,
+                                              size_t base_pos, eb_tensor **out) {
+    if (!attn || !rec || !q || !k || !v || !rope || !kv || !out)
+        return fail(EB_OTHER, "attention_forward: null argument");
+    *out = nullptr;
+    const eb_attention_desc &d = attn->d;
+    const size_t H = d.n_heads, Hkv = d.n_kv_heads, hd = d.head_dim;
+    if (layer >= kv->k.size())
+        return fail(EB_SHAPE_MISMATCH, "attention_forward: layer %zu of %zu", layer,
+                    kv->k.size());
+    if (rope->head_dim != hd)
+        return fail(EB_SHAPE_MISMATCH, "attention_forward: rope head_dim %zu != %zu",
+                    rope->head_dim, hd);
+    eb_tensor *kc = kv->k[layer], *vc = kv->v[layer];
+    if (eb_tensor_numel(kc) != kv->max_seq * Hkv * hd)
+        return fail(EB_SHAPE_MISMATCH, "attention_forward: cache layer is not [max_seq, %zu, %zu]",
+                    Hkv, hd);
+    if (rows == 0) return fail(EB_SHAPE_MISMATCH, "attention_forward: rows must be > 0");
+    // Routing rule of attention.rs:40.
+    const bool prefill = base_pos == 0 && rows > 1;
+    if (!prefill && rows != 1)
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attention_forward: %zu rows at base_pos %zu (chunked prefill is not part "
+                    "of the reference path)",
+                    rows, base_pos);
+    if (eb_tensor_numel(q) != rows * H * hd || eb_tensor_numel(k) != rows * Hkv * hd ||
+        eb_tensor_numel(v) != rows * Hkv * hd)
+        return fail(EB_SHAPE_MISMATCH, "attention_forward: q/k/v are not [rows, heads*head_dim]");
+
+    Owned qn_h, kn_h, vn_h;
+    const eb_tensor *qn = nullptr, *kn = nullptr, *vn = nullptr;
+    EB_TRY(maybe_norm(rec, d.q_norm, q, rows * H, hd, d.norm_eps, qn_h, &qn));
+    EB_TRY(maybe_norm(rec, d.k_norm, k, rows * Hkv, hd, d.norm_eps, kn_h, &kn));
+    EB_TRY(maybe_norm(rec, d.v_norm, v, rows * Hkv, hd, d.norm_eps, vn_h, &vn));
+
+    eb_tensor *qr_t = nullptr, *kr_t = nullptr;
+    EB_TRY(eb_rope_apply(rope, rec, qn, rows, H, base_pos, &qr_t));
+    Owned qr(qr_t);
+    EB_TRY(eb_rope_apply(rope, rec, kn, rows, Hkv, base_pos, &kr_t));
+    Owned kr(kr_t);
+
+    EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
+    EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
+
+    const size_t oshape[2] = {rows, H * hd};
+    eb_tensor *o_t = nullptr;
+    EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape, 2, EB_F32, &o_t));
+    Owned o(o_t);
+    if (prefill) {
+        // attention.rs:104-115 attends the fresh kr / v, not the cache.
+        EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
+    } else {
+        EB_TRY(eb_attn_decode(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, hd, kv->max_seq,
+                              d.scale));
+    }
+    *out = o.release();
+    return eb::ok();
+}

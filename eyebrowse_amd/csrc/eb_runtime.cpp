@@ -1,0 +1,653 @@
+// libeyebrowse_hip runtime: the eyebrowse-gpu substrate on HIP.
+//
+//  - eb_device: one HIP device, one stream (the reference has one wgpu queue,
+//    crates/eyebrowse-gpu/src/device.rs:20-28), an exact-size buffer pool
+//    (device.rs:82-110) and the split-KV decode workspace.
+//  - eb_tensor: a typed device buffer that goes back to the pool when released
+//    (crates/eyebrowse-gpu/src/tensor.rs:195-236).
+//  - eb_recorder: recording = enqueueing on the device stream; submit reports errors
+//    (crates/eyebrowse-gpu/src/recorder.rs:10-35).
+//  - The kernel entry points validate shapes and forward to the launchers in the
+//    kernel translation units.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "eb_internal.h"
+
+// ------------------------------------------------------------------ errors ---------------
+
+namespace eb {
+
+static thread_local std::string g_last_error;
+
+eb_status fail(eb_status st, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = std::string(eb_status_name(st)) + ": " + buf;
+    return st;
+}
+
+eb_status ok() {
+    g_last_error.clear();
+    return EB_OK;
+}
+
+eb_status hip_fail(hipError_t e, const char *what) {
+    eb_status st = (e == hipErrorOutOfMemory) ? EB_OUT_OF_MEMORY : EB_OTHER;
+    return fail(st, "%s failed: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+eb_status check_launch(const char *kernel) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(EB_OTHER, "launch of %s failed: %s", kernel,
+                                     hipGetErrorString(e));
+    return EB_OK;
+}
+
+eb_status check_ptr(const void *p, const char *name) {
+    if (p == nullptr) return fail(EB_SHAPE_MISMATCH, "%s is null", name);
+    return EB_OK;
+}
+
+eb_status check_numel(size_t have, size_t need, const char *name) {
+    if (have < need)
+        return fail(EB_SHAPE_MISMATCH, "%s holds %zu elements, the shape needs %zu", name, have,
+                    need);
+    if (need >= kMaxIndex)
+        return fail(EB_UNSUPPORTED_CONFIG, "%s needs %zu elements, above the 2^31 index limit",
+                    name, need);
+    return EB_OK;
+}
+
+eb_status check_heads(size_t h, size_t hkv) {
+    if (h == 0 || hkv == 0) return fail(EB_SHAPE_MISMATCH, "head counts must be positive");
+    if (h % hkv != 0)
+        return fail(EB_SHAPE_MISMATCH, "n_heads %zu is not a multiple of n_kv_heads %zu", h, hkv);
+    return EB_OK;
+}
+
+bool attn_head_dim_supported(size_t hd) {
+    switch (hd) {
+        case 4: case 8: case 16: case 32: case 64: case 128: case 256: return true;
+        default: return false;
+    }
+}
+
+int current_cu_count() {
+    static std::mutex mu;
+    static std::unordered_map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+        n = 256;
+    cache[dev] = n;
+    return n;
+}
+
+}  // namespace eb
+
+using eb::fail;
+
+// ------------------------------------------------------------------ handles --------------
+
+// Buffers at or below this size are recycled; larger ones are freed on release
+// (MAX_POOLED_BYTES, crates/eyebrowse-gpu/src/device.rs:12-14).
+static constexpr size_t kMaxPooledBytes = (size_t)64 << 20;
+
+struct eb_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    int cu_count = 256;
+    std::atomic<int> refs{1};
+    std::mutex pool_mu;
+    std::unordered_map<size_t, std::vector<void *>> pool;  // exact byte size -> free buffers
+    std::mutex ws_mu;
+    float *ws = nullptr;  // decode split workspace, grow-only, stream ordered
+    size_t ws_floats = 0;
+};
+
+struct eb_tensor {
+    eb_device *dev = nullptr;
+    void *ptr = nullptr;
+    std::vector<size_t> shape;
+    eb_dtype dtype = EB_F32;
+    size_t bytes = 0;  // allocation size
+    bool poolable = false;
+};
+
+struct eb_recorder {
+    eb_device *dev = nullptr;
+};
+
+static void device_retain(eb_device *d) { d->refs.fetch_add(1); }
+
+eb_device *eb::tensor_device(const eb_tensor *t) { return t ? t->dev : nullptr; }
+
+static void device_destroy(eb_device *d) {
+    (void)hipSetDevice(d->ordinal);
+    (void)hipStreamSynchronize(d->stream);
+    for (auto &kv : d->pool)
+        for (void *p : kv.second) (void)hipFree(p);
+    if (d->ws) (void)hipFree(d->ws);
+    (void)hipStreamDestroy(d->stream);
+    delete d;
+}
+
+static void device_unref(eb_device *d) {
+    if (d && d->refs.fetch_sub(1) == 1) device_destroy(d);
+}
+
+static size_t shape_numel(const size_t *shape, size_t ndim) {
+    size_t n = 1;
+    for (size_t i = 0; i < ndim; ++i) n *= shape[i];
+    return n;
+}
+
+extern "C" {
+
+const char *eb_last_error(void) { return eb::g_last_error.c_str(); }
+
+const char *eb_status_name(eb_status st) {
+    switch (st) {
+        case EB_OK: return "Ok";
+        case EB_DEVICE_UNAVAILABLE: return "DeviceUnavailable";
+        case EB_LOAD: return "Load";
+        case EB_UNSUPPORTED_CONFIG: return "UnsupportedConfig";
+        case EB_SHAPE_MISMATCH: return "ShapeMismatch";
+        case EB_OUT_OF_MEMORY: return "OutOfMemory";
+        case EB_OTHER: return "Other";
+    }
+    return "Unknown";
+}
+
+size_t eb_dtype_size(eb_dtype dt) {
+    switch (dt) {
+        case EB_F32: case EB_U32: case EB_I32: return 4;
+        case EB_F16: return 2;
+    }
+    return 0;
+}
+
+const char *eb_version(void) { return "eyebrowse_hip 0.1.0 (gfx950)"; }
+
+size_t eb_pool_max_bytes(void) { return kMaxPooledBytes; }
+
+// ---- device ---------------------------------------------------------------------------
+
+eb_status eb_device_new(int ordinal, eb_device **out) {
+    if (!out) return fail(EB_OTHER, "out is null");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return fail(EB_DEVICE_UNAVAILABLE, "no HIP device visible (%s)",
+                    e == hipSuccess ? "count 0" : hipGetErrorString(e));
+    if (ordinal < 0 || ordinal >= count)
+        return fail(EB_DEVICE_UNAVAILABLE, "device ordinal %d out of range (%d devices)",
+                    ordinal, count);
+    EB_HIP_TRY(hipSetDevice(ordinal));
+    auto *d = new eb_device();
+    d->ordinal = ordinal;
+    e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete d;
+        return eb::hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, ordinal) ==
+            hipSuccess &&
+        n > 0)
+        d->cu_count = n;
+    *out = d;
+    return eb::ok();
+}
+
+void eb_device_release(eb_device *dev) { device_unref(dev); }
+
+eb_status eb_device_synchronize(eb_device *dev) {
+    if (!dev) return fail(EB_OTHER, "device is null");
+    EB_HIP_TRY(hipSetDevice(dev->ordinal));
+    EB_HIP_TRY(hipStreamSynchronize(dev->stream));
+    return eb::ok();
+}
+
+void *eb_device_stream(eb_device *dev) { return dev ? (void *)dev->stream : nullptr; }
+
+int eb_device_cu_count(eb_device *dev) { return dev ? dev->cu_count : 0; }
+
+size_t eb_device_pooled(eb_device *dev, size_t bytes) {
+    if (!dev) return 0;
+    std::lock_guard<std::mutex> lk(dev->pool_mu);
+    auto it = dev->pool.find(bytes);
+    return it == dev->pool.end() ? 0 : it->second.size();
+}
+
+// ---- tensor ---------------------------------------------------------------------------
+
+static eb_status tensor_alloc(eb_device *dev, const size_t *shape, size_t ndim, eb_dtype dt,
+                              bool from_pool, eb_tensor **out) {
+    if (!dev) return fail(EB_OTHER, "device is null");
+    if (!out) return fail(EB_OTHER, "out is null");
+    if (ndim > 0 && !shape) return fail(EB_SHAPE_MISMATCH, "shape is null");
+    *out = nullptr;
+    size_t esz = eb_dtype_size(dt);
+    if (esz == 0) return fail(EB_OTHER, "unknown dtype %d", (int)dt);
+    size_t numel = shape_numel(shape, ndim);
+    // (numel * size).max(size): a zero-element tensor still owns one element
+    // (crates/eyebrowse-gpu/src/tensor.rs:228).
+    size_t bytes = numel * esz;
+    if (bytes < esz) bytes = esz;
+    void *p = nullptr;
+    bool poolable = bytes <= kMaxPooledBytes;
+    if (from_pool && poolable) {
+        std::lock_guard<std::mutex> lk(dev->pool_mu);
+        auto it = dev->pool.find(bytes);
+        if (it != dev->pool.end() && !it->second.empty()) {
+            p = it->second.back();
+            it->second.pop_back();
+        }
+    }
+    if (!p) {
+        EB_HIP_TRY(hipSetDevice(dev->ordinal));
+        EB_HIP_TRY(hipMalloc(&p, bytes));
+    }
+    auto *t = new eb_tensor();
+    t->dev = dev;
+    device_retain(dev);
+    t->ptr = p;
+    t->shape.assign(shape, shape + ndim);
+    t->dtype = dt;
+    t->bytes = bytes;
+    t->poolable = poolable;
+    *out = t;
+    return eb::ok();
+}
+
+eb_status eb_tensor_empty(eb_device *dev, const size_t *shape, size_t ndim, eb_dtype dt,
+                          eb_tensor **out) {
+    return tensor_alloc(dev, shape, ndim, dt, true, out);
+}
+
+static eb_status tensor_from_host(eb_device *dev, const size_t *shape, size_t ndim,
+                                  eb_dtype dt, const void *data, size_t n, eb_tensor **out) {
+    if (n != shape_numel(shape, ndim))
+        return fail(EB_SHAPE_MISMATCH, "from_host: data len %zu != shape numel %zu", n,
+                    shape_numel(shape, ndim));
+    if (n > 0 && !data) return fail(EB_SHAPE_MISMATCH, "from_host: data is null");
+    // Host-initialised tensors never draw from the pool (tensor.rs:238-257).
+    eb_status st = tensor_alloc(dev, shape, ndim, dt, false, out);
+    if (st != EB_OK) return st;
+    if (n > 0) {
+        hipError_t e = hipMemcpyAsync((*out)->ptr, data, n * eb_dtype_size(dt),
+                                      hipMemcpyHostToDevice, dev->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+        if (e != hipSuccess) {
+            eb_tensor_release(*out);
+            *out = nullptr;
+            return eb::hip_fail(e, "upload");
+        }
+    }
+    return eb::ok();
+}
+
+eb_status eb_tensor_from_f32(eb_device *dev, const size_t *shape, size_t ndim,
+                             const float *data, size_t n, eb_tensor **out) {
+    return tensor_from_host(dev, shape, ndim, EB_F32, data, n, out);
+}
+
+eb_status eb_tensor_from_u32(eb_device *dev, const size_t *shape, size_t ndim,
+                             const uint32_t *data, size_t n, eb_tensor **out) {
+    return tensor_from_host(dev, shape, ndim, EB_U32, data, n, out);
+}
+
+eb_status eb_tensor_read_bytes(const eb_tensor *t, void *host, size_t nbytes) {
+    if (!t) return fail(EB_OTHER, "tensor is null");
+    size_t want = shape_numel(t->shape.data(), t->shape.size()) * eb_dtype_size(t->dtype);
+    if (nbytes != want)
+        return fail(EB_SHAPE_MISMATCH, "read_bytes: asked for %zu bytes, tensor has %zu", nbytes,
+                    want);
+    if (nbytes == 0) return eb::ok();
+    if (!host) return fail(EB_SHAPE_MISMATCH, "read_bytes: host buffer is null");
+    EB_HIP_TRY(hipSetDevice(t->dev->ordinal));
+    EB_HIP_TRY(hipMemcpyAsync(host, t->ptr, nbytes, hipMemcpyDeviceToHost, t->dev->stream));
+    EB_HIP_TRY(hipStreamSynchronize(t->dev->stream));
+    return eb::ok();
+}
+
+eb_status eb_tensor_to_f32(const eb_tensor *t, float *host, size_t n) {
+    if (!t) return fail(EB_OTHER, "tensor is null");
+    if (t->dtype != EB_F32) return fail(EB_SHAPE_MISMATCH, "to_f32 on a non-f32 tensor");
+    return eb_tensor_read_bytes(t, host, n * sizeof(float));
+}
+
+void eb_tensor_release(eb_tensor *t) {
+    if (!t) return;
+    eb_device *d = t->dev;
+    if (t->poolable) {
+        // Stream-ordered reuse: every kernel runs on the device's single stream, so a
+        // later user of this buffer is queued after every earlier one.
+        std::lock_guard<std::mutex> lk(d->pool_mu);
+        d->pool[t->bytes].push_back(t->ptr);
+    } else {
+        (void)hipSetDevice(d->ordinal);
+        (void)hipStreamSynchronize(d->stream);
+        (void)hipFree(t->ptr);
+    }
+    delete t;
+    device_unref(d);
+}
+
+size_t eb_tensor_ndim(const eb_tensor *t) { return t ? t->shape.size() : 0; }
+size_t eb_tensor_dim(const eb_tensor *t, size_t i) {
+    return (t && i < t->shape.size()) ? t->shape[i] : 0;
+}
+size_t eb_tensor_numel(const eb_tensor *t) {
+    return t ? shape_numel(t->shape.data(), t->shape.size()) : 0;
+}
+size_t eb_tensor_nbytes(const eb_tensor *t) {
+    return t ? eb_tensor_numel(t) * eb_dtype_size(t->dtype) : 0;
+}
+eb_dtype eb_tensor_dtype(const eb_tensor *t) { return t ? t->dtype : EB_F32; }
+void *eb_tensor_data(const eb_tensor *t) { return t ? t->ptr : nullptr; }
+
+// ---- recorder -------------------------------------------------------------------------
+
+eb_status eb_recorder_new(eb_device *dev, eb_recorder **out) {
+    if (!dev || !out) return fail(EB_OTHER, "device/out is null");
+    auto *r = new eb_recorder();
+    r->dev = dev;
+    device_retain(dev);
+    *out = r;
+    return eb::ok();
+}
+
+eb_status eb_recorder_submit(eb_recorder *rec) {
+    if (!rec) return fail(EB_OTHER, "recorder is null");
+    hipError_t e = hipGetLastError();
+    eb_recorder_release(rec);
+    if (e != hipSuccess) return eb::hip_fail(e, "submit");
+    return eb::ok();
+}
+
+void eb_recorder_release(eb_recorder *rec) {
+    if (!rec) return;
+    device_unref(rec->dev);
+    delete rec;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ kernel entry points -
+
+static eb_status rec_ready(eb_recorder *rec) {
+    if (!rec) return fail(EB_OTHER, "recorder is null");
+    EB_HIP_TRY(hipSetDevice(rec->dev->ordinal));
+    return EB_OK;
+}
+
+static eb_status tensor_f32(const eb_tensor *t, const char *name, eb_device *dev) {
+    if (!t) return fail(EB_SHAPE_MISMATCH, "%s is null", name);
+    if (t->dtype != EB_F32) return fail(EB_SHAPE_MISMATCH, "%s must be f32", name);
+    if (t->dev != dev) return fail(EB_OTHER, "%s lives on another device", name);
+    return EB_OK;
+}
+
+#define EB_TRY(expr)                     \
+    do {                                 \
+        eb_status eb_s_ = (expr);        \
+        if (eb_s_ != EB_OK) return eb_s_; \
+    } while (0)
+
+// Float-buffer views with element counts, shared by the handle and raw entry points.
+static eb_status kv_write_checked(hipStream_t st, float *cache, size_t cache_n,
+                                  const float *src, size_t src_n, size_t hkv, size_t count,
+                                  size_t hd, size_t max_seq, size_t dst) {
+    if (hkv == 0 || hd == 0) return fail(EB_SHAPE_MISMATCH, "kv_write: hkv and hd must be > 0");
+    if (dst > max_seq || count > max_seq - dst)
+        return fail(EB_SHAPE_MISMATCH, "kv_write: rows [%zu, %zu) exceed max_seq %zu", dst,
+                    dst + count, max_seq);
+    EB_TRY(eb::check_numel(cache_n, max_seq * hkv * hd, "cache"));
+    EB_TRY(eb::check_numel(src_n, count * hkv * hd, "src"));
+    if (count == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(cache, "cache"));
+    EB_TRY(eb::check_ptr(src, "src"));
+    EB_TRY(eb::launch_kv_write(st, cache, src, hkv, count, hd, dst));
+    return eb::ok();
+}
+
+static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, const float *k,
+                                 size_t kn, const float *v, size_t vn, float *o, size_t on,
+                                 size_t h, size_t hkv, size_t s, size_t hd, float scale) {
+    EB_TRY(eb::check_heads(h, hkv));
+    if (!eb::attn_head_dim_supported(hd))
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_prefill: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)", hd);
+    EB_TRY(eb::check_numel(qn, s * h * hd, "q"));
+    EB_TRY(eb::check_numel(kn, s * hkv * hd, "k"));
+    EB_TRY(eb::check_numel(vn, s * hkv * hd, "v"));
+    EB_TRY(eb::check_numel(on, s * h * hd, "o"));
+    if (s == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(q, "q"));
+    EB_TRY(eb::check_ptr(k, "k"));
+    EB_TRY(eb::check_ptr(v, "v"));
+    EB_TRY(eb::check_ptr(o, "o"));
+    EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale));
+    return eb::ok();
+}
+
+static eb_status decode_shape_checked(const float *q, size_t qn, const float *kc, size_t kcn,
+                                      const float *vc, size_t vcn, const float *o, size_t on,
+                                      size_t h, size_t hkv, size_t pos, size_t hd,
+                                      size_t max_seq) {
+    EB_TRY(eb::check_heads(h, hkv));
+    if (!eb::attn_head_dim_supported(hd))
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_decode: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)", hd);
+    if (pos >= max_seq)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode: pos %zu >= max_seq %zu", pos, max_seq);
+    EB_TRY(eb::check_numel(qn, h * hd, "q"));
+    EB_TRY(eb::check_numel(kcn, max_seq * hkv * hd, "kcache"));
+    EB_TRY(eb::check_numel(vcn, max_seq * hkv * hd, "vcache"));
+    EB_TRY(eb::check_numel(on, h * hd, "o"));
+    EB_TRY(eb::check_ptr(q, "q"));
+    EB_TRY(eb::check_ptr(kc, "kcache"));
+    EB_TRY(eb::check_ptr(vc, "vcache"));
+    EB_TRY(eb::check_ptr(o, "o"));
+    return EB_OK;
+}
+
+static eb_status rmsnorm_checked(hipStream_t st, const float *x, size_t xn, const float *w,
+                                 size_t wn, float *out, size_t outn, size_t rows, size_t dim,
+                                 float eps) {
+    if (dim == 0) return fail(EB_SHAPE_MISMATCH, "rmsnorm: dim must be > 0");
+    EB_TRY(eb::check_numel(xn, rows * dim, "x"));
+    EB_TRY(eb::check_numel(wn, dim, "weight"));
+    EB_TRY(eb::check_numel(outn, rows * dim, "out"));
+    if (rows == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(x, "x"));
+    EB_TRY(eb::check_ptr(w, "weight"));
+    EB_TRY(eb::check_ptr(out, "out"));
+    EB_TRY(eb::launch_rmsnorm(st, x, w, out, rows, dim, eps));
+    return eb::ok();
+}
+
+static eb_status rope_checked(hipStream_t st, const float *x, size_t xn, const float *c,
+                              const float *s, size_t tn, float *out, size_t outn, size_t seq,
+                              size_t nh, size_t hd, size_t base_pos) {
+    if (hd == 0 || hd % 2 != 0) return fail(EB_SHAPE_MISMATCH, "rope: head_dim must be even");
+    EB_TRY(eb::check_numel(xn, seq * nh * hd, "x"));
+    EB_TRY(eb::check_numel(outn, seq * nh * hd, "out"));
+    EB_TRY(eb::check_numel(tn, (seq + base_pos) * (hd / 2), "cos/sin tables"));
+    if (seq == 0 || nh == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(x, "x"));
+    EB_TRY(eb::check_ptr(c, "cos"));
+    EB_TRY(eb::check_ptr(s, "sin"));
+    EB_TRY(eb::check_ptr(out, "out"));
+    EB_TRY(eb::launch_rope(st, x, c, s, out, seq, nh, hd, base_pos));
+    return eb::ok();
+}
+
+// Grows the device's decode workspace (stream ordered: hipFree waits for the device).
+static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
+    std::lock_guard<std::mutex> lk(dev->ws_mu);
+    if (floats > dev->ws_floats) {
+        if (dev->ws) {
+            EB_HIP_TRY(hipStreamSynchronize(dev->stream));
+            EB_HIP_TRY(hipFree(dev->ws));
+            dev->ws = nullptr;
+            dev->ws_floats = 0;
+        }
+        EB_HIP_TRY(hipMalloc((void **)&dev->ws, floats * sizeof(float)));
+        dev->ws_floats = floats;
+    }
+    *out = dev->ws;
+    return EB_OK;
+}
+
+extern "C" {
+
+eb_status eb_kv_write(eb_recorder *rec, eb_tensor *cache, const eb_tensor *src, size_t hkv,
+                      size_t count, size_t hd, size_t max_seq, size_t dst_start) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(cache, "cache", rec->dev));
+    EB_TRY(tensor_f32(src, "src", rec->dev));
+    return kv_write_checked(rec->dev->stream, (float *)cache->ptr, eb_tensor_numel(cache),
+                            (const float *)src->ptr, eb_tensor_numel(src), hkv, count, hd,
+                            max_seq, dst_start);
+}
+
+eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                          const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
+                          size_t hd, float scale) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(k, "k", rec->dev));
+    EB_TRY(tensor_f32(v, "v", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    return prefill_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
+                           (const float *)k->ptr, eb_tensor_numel(k), (const float *)v->ptr,
+                           eb_tensor_numel(v), (float *)o->ptr, eb_tensor_numel(o), h, hkv, s,
+                           hd, scale);
+}
+
+eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
+                         const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                         size_t pos, size_t hd, size_t max_seq, float scale) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
+    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q),
+                                (const float *)kcache->ptr, eb_tensor_numel(kcache),
+                                (const float *)vcache->ptr, eb_tensor_numel(vcache),
+                                (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
+                                max_seq));
+    eb_device *dev = rec->dev;
+    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
+    float *ws = nullptr;
+    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
+    EB_TRY(eb::launch_attn_decode(dev->stream, (const float *)q->ptr,
+                                  (const float *)kcache->ptr, (const float *)vcache->ptr,
+                                  (float *)o->ptr, h, hkv, pos, hd, scale, ws, wsn,
+                                  dev->cu_count));
+    return eb::ok();
+}
+
+eb_status eb_rmsnorm(eb_recorder *rec, const eb_tensor *x, const eb_tensor *weight,
+                     eb_tensor *out, size_t rows, size_t dim, float eps) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(x, "x", rec->dev));
+    EB_TRY(tensor_f32(weight, "weight", rec->dev));
+    EB_TRY(tensor_f32(out, "out", rec->dev));
+    return rmsnorm_checked(rec->dev->stream, (const float *)x->ptr, eb_tensor_numel(x),
+                           (const float *)weight->ptr, eb_tensor_numel(weight),
+                           (float *)out->ptr, eb_tensor_numel(out), rows, dim, eps);
+}
+
+eb_status eb_rope(eb_recorder *rec, const eb_tensor *x, const eb_tensor *cos,
+                  const eb_tensor *sin, eb_tensor *out, size_t seq, size_t n_heads,
+                  size_t head_dim, size_t base_pos) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(x, "x", rec->dev));
+    EB_TRY(tensor_f32(cos, "cos", rec->dev));
+    EB_TRY(tensor_f32(sin, "sin", rec->dev));
+    EB_TRY(tensor_f32(out, "out", rec->dev));
+    size_t tn = eb_tensor_numel(cos) < eb_tensor_numel(sin) ? eb_tensor_numel(cos)
+                                                            : eb_tensor_numel(sin);
+    return rope_checked(rec->dev->stream, (const float *)x->ptr, eb_tensor_numel(x),
+                        (const float *)cos->ptr, (const float *)sin->ptr, tn, (float *)out->ptr,
+                        eb_tensor_numel(out), seq, n_heads, head_dim, base_pos);
+}
+
+// ---- raw launches ---------------------------------------------------------------------
+
+eb_status eb_launch_kv_write(void *stream, float *cache, size_t cache_numel, const float *src,
+                             size_t src_numel, size_t hkv, size_t count, size_t hd,
+                             size_t max_seq, size_t dst_start) {
+    return kv_write_checked((hipStream_t)stream, cache, cache_numel, src, src_numel, hkv, count,
+                            hd, max_seq, dst_start);
+}
+
+eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel, const float *k,
+                                 size_t k_numel, const float *v, size_t v_numel, float *o,
+                                 size_t o_numel, size_t h, size_t hkv, size_t s, size_t hd,
+                                 float scale) {
+    return prefill_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
+                           h, hkv, s, hd, scale);
+}
+
+size_t eb_attn_decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd,
+                                       int cu_count) {
+    if (h == 0 || hkv == 0 || h % hkv != 0 || !eb::attn_head_dim_supported(hd)) return 0;
+    return eb::decode_workspace_floats(h, hkv, pos, hd, cu_count > 0 ? cu_count : 256);
+}
+
+eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel, const float *kc,
+                                size_t kc_numel, const float *vc, size_t vc_numel, float *o,
+                                size_t o_numel, size_t h, size_t hkv, size_t pos, size_t hd,
+                                size_t max_seq, float scale, float *workspace,
+                                size_t workspace_floats, int cu_count) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, o, h, hkv, pos, hd, scale,
+                                  workspace, workspace_floats, cus));
+    return eb::ok();
+}
+
+eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel, const float *weight,
+                            size_t w_numel, float *out, size_t out_numel, size_t rows,
+                            size_t dim, float eps) {
+    return rmsnorm_checked((hipStream_t)stream, x, x_numel, weight, w_numel, out, out_numel,
+                           rows, dim, eps);
+}
+
+eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const float *cos,
+                         const float *sin, size_t table_numel, float *out, size_t out_numel,
+                         size_t seq, size_t n_heads, size_t head_dim, size_t base_pos) {
+    return rope_checked((hipStream_t)stream, x, x_numel, cos, sin, table_numel, out, out_numel,
+                        seq, n_heads, head_dim, base_pos);
+}
+
+}  // extern "C"

@@ -1,0 +1,215 @@
+"""eyebrowse-core / eyebrowse-gpu mirror over the C ABI: DType, EyebrowseError, Device,
+Tensor, Recorder.
+
+Names and meaning follow crates/eyebrowse-core/src/lib.rs (DType, EyebrowseError) and
+crates/eyebrowse-gpu/src/{device,tensor,recorder}.rs. Kernel calls raise instead of
+returning ``()``.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+
+import numpy as np
+
+from ._lib import c_size, c_vp, lib
+
+
+class DType(enum.IntEnum):
+    """crates/eyebrowse-core/src/lib.rs:8-25."""
+    F32 = 0
+    F16 = 1
+    U32 = 2
+    I32 = 3
+
+    def size(self) -> int:
+        return int(lib().eb_dtype_size(int(self)))
+
+
+class EyebrowseError(RuntimeError):
+    """crates/eyebrowse-core/src/lib.rs:27-41; ``status`` is the eb_status code."""
+    status = 6
+
+
+class DeviceUnavailable(EyebrowseError):
+    status = 1
+
+
+class LoadError(EyebrowseError):
+    status = 2
+
+
+class UnsupportedConfig(EyebrowseError):
+    status = 3
+
+
+class ShapeMismatch(EyebrowseError):
+    status = 4
+
+
+class OutOfMemory(EyebrowseError):
+    status = 5
+
+
+_ERRORS = {c.status: c for c in (DeviceUnavailable, LoadError, UnsupportedConfig, ShapeMismatch,
+                                 OutOfMemory, EyebrowseError)}
+
+
+def check(status: int) -> None:
+    """Raise the EyebrowseError subclass for a non-zero eb_status."""
+    if status != 0:
+        msg = lib().eb_last_error().decode()
+        raise _ERRORS.get(status, EyebrowseError)(msg)
+
+
+def _shape_arr(shape):
+    shape = tuple(int(s) for s in shape)
+    return (c_size * max(1, len(shape)))(*shape), len(shape)
+
+
+class Device:
+    """Device (crates/eyebrowse-gpu/src/device.rs:20-110): one HIP device, one stream,
+    an exact-size buffer pool."""
+
+    def __init__(self, handle: int):
+        self._h = c_vp(handle)
+
+    @classmethod
+    def new(cls, ordinal: int = 0) -> "Device":
+        out = c_vp()
+        check(lib().eb_device_new(ordinal, ctypes.byref(out)))
+        return cls(out.value)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def synchronize(self) -> None:
+        check(lib().eb_device_synchronize(self._h))
+
+    @property
+    def stream(self) -> int:
+        return int(lib().eb_device_stream(self._h) or 0)
+
+    @property
+    def cu_count(self) -> int:
+        return int(lib().eb_device_cu_count(self._h))
+
+    def pooled(self, nbytes: int) -> int:
+        """Free pooled buffers of exactly ``nbytes`` (device.rs:63-70)."""
+        return int(lib().eb_device_pooled(self._h, nbytes))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().eb_device_release(h)
+            self._h = c_vp()
+
+
+class Tensor:
+    """Tensor (crates/eyebrowse-gpu/src/tensor.rs:195-319). Dropping it returns the buffer
+    to the pool."""
+
+    def __init__(self, handle: int, dev: Device):
+        self._h = c_vp(handle)
+        self.dev = dev
+
+    @classmethod
+    def empty(cls, dev: Device, shape, dtype: DType = DType.F32) -> "Tensor":
+        arr, n = _shape_arr(shape)
+        out = c_vp()
+        check(lib().eb_tensor_empty(dev.handle, arr, n, int(dtype), ctypes.byref(out)))
+        return cls(out.value, dev)
+
+    @classmethod
+    def from_f32(cls, dev: Device, shape, data) -> "Tensor":
+        a = np.ascontiguousarray(np.asarray(data, dtype=np.float32)).ravel()
+        arr, n = _shape_arr(shape)
+        out = c_vp()
+        check(lib().eb_tensor_from_f32(dev.handle, arr, n,
+                                       a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), a.size,
+                                       ctypes.byref(out)))
+        return cls(out.value, dev)
+
+    @classmethod
+    def from_u32(cls, dev: Device, shape, data) -> "Tensor":
+        a = np.ascontiguousarray(np.asarray(data, dtype=np.uint32)).ravel()
+        arr, n = _shape_arr(shape)
+        out = c_vp()
+        check(lib().eb_tensor_from_u32(dev.handle, arr, n,
+                                       a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), a.size,
+                                       ctypes.byref(out)))
+        return cls(out.value, dev)
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def shape(self) -> tuple:
+        l = lib()
+        return tuple(int(l.eb_tensor_dim(self._h, i)) for i in range(l.eb_tensor_ndim(self._h)))
+
+    @property
+    def dtype(self) -> DType:
+        return DType(lib().eb_tensor_dtype(self._h))
+
+    def numel(self) -> int:
+        return int(lib().eb_tensor_numel(self._h))
+
+    def byte_len(self) -> int:
+        return int(lib().eb_tensor_nbytes(self._h))
+
+    @property
+    def data_ptr(self) -> int:
+        return int(lib().eb_tensor_data(self._h) or 0)
+
+    def to_f32(self) -> np.ndarray:
+        out = np.empty(self.numel(), np.float32)
+        check(lib().eb_tensor_to_f32(self._h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                     out.size))
+        return out
+
+    def read_bytes(self) -> bytes:
+        buf = ctypes.create_string_buffer(self.byte_len())
+        check(lib().eb_tensor_read_bytes(self._h, buf, self.byte_len()))
+        return buf.raw
+
+    def release(self) -> None:
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().eb_tensor_release(h)
+            self._h = c_vp()
+
+    def __del__(self):
+        self.release()
+
+
+class Recorder:
+    """Recorder (crates/eyebrowse-gpu/src/recorder.rs:10-35): kernels recorded through it
+    run on the device stream in record order; ``submit`` reports launch errors."""
+
+    def __init__(self, dev: Device):
+        out = c_vp()
+        check(lib().eb_recorder_new(dev.handle, ctypes.byref(out)))
+        self._h = out
+        self.dev = dev
+
+    def device(self) -> Device:
+        return self.dev
+
+    @property
+    def handle(self):
+        if not self._h.value:
+            raise EyebrowseError("recorder already submitted")
+        return self._h
+
+    def submit(self) -> None:
+        h, self._h = self._h, c_vp()
+        check(lib().eb_recorder_submit(h))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().eb_recorder_release(h)
+            self._h = c_vp()

@@ -1,0 +1,83 @@
+"""eyebrowse-kernels entry points over the C ABI (same names and argument order as
+crates/eyebrowse-kernels/src/{attention,ops,rmsnorm,rope}.rs), plus the raw launches on
+caller-owned device memory.
+"""
+from __future__ import annotations
+
+from ._lib import lib
+from .gpu import Recorder, Tensor, check
+
+
+def attn_prefill(rec: Recorder, q: Tensor, k: Tensor, v: Tensor, o: Tensor, h: int, hkv: int,
+                 s: int, hd: int, scale: float) -> None:
+    """attention.rs:94-120: causal GQA prefill, q [s,h,hd], k/v [s,hkv,hd] -> o [s,h,hd]."""
+    check(lib().eb_attn_prefill(rec.handle, q.handle, k.handle, v.handle, o.handle, h, hkv, s,
+                                hd, scale))
+
+
+def attn_decode(rec: Recorder, q: Tensor, kcache: Tensor, vcache: Tensor, o: Tensor, h: int,
+                hkv: int, pos: int, hd: int, max_seq: int, scale: float) -> None:
+    """attention.rs:124-162: q [h,hd] attends keys 0..=pos of [max_seq,hkv,hd] caches."""
+    check(lib().eb_attn_decode(rec.handle, q.handle, kcache.handle, vcache.handle, o.handle, h,
+                               hkv, pos, hd, max_seq, scale))
+
+
+def kv_write(rec: Recorder, cache: Tensor, src: Tensor, hkv: int, count: int, hd: int,
+             max_seq: int, dst_start: int) -> None:
+    """ops.rs:150-179: copy src [count,hkv,hd] into cache rows dst_start.."""
+    check(lib().eb_kv_write(rec.handle, cache.handle, src.handle, hkv, count, hd, max_seq,
+                            dst_start))
+
+
+def rmsnorm(rec: Recorder, x: Tensor, weight: Tensor, out: Tensor, rows: int, dim: int,
+            eps: float) -> None:
+    """rmsnorm.rs:42-64."""
+    check(lib().eb_rmsnorm(rec.handle, x.handle, weight.handle, out.handle, rows, dim, eps))
+
+
+def rope(rec: Recorder, x: Tensor, cos: Tensor, sin: Tensor, out: Tensor, seq: int,
+         n_heads: int, head_dim: int, base_pos: int) -> None:
+    """rope.rs:38-69."""
+    check(lib().eb_rope(rec.handle, x.handle, cos.handle, sin.handle, out.handle, seq, n_heads,
+                        head_dim, base_pos))
+
+
+# ---- raw launches on caller memory (stream and pointers as ints) ------------------------
+
+def launch_kv_write(stream: int, cache: int, cache_numel: int, src: int, src_numel: int,
+                    hkv: int, count: int, hd: int, max_seq: int, dst_start: int) -> None:
+    check(lib().eb_launch_kv_write(stream, cache, cache_numel, src, src_numel, hkv, count, hd,
+                                   max_seq, dst_start))
+
+
+def launch_attn_prefill(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                        v_numel: int, o: int, o_numel: int, h: int, hkv: int, s: int, hd: int,
+                        scale: float) -> None:
+    check(lib().eb_launch_attn_prefill(stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
+                                       h, hkv, s, hd, scale))
+
+
+def attn_decode_workspace_floats(h: int, hkv: int, pos: int, hd: int, cu_count: int) -> int:
+    return int(lib().eb_attn_decode_workspace_floats(h, hkv, pos, hd, cu_count))
+
+
+def launch_attn_decode(stream: int, q: int, q_numel: int, kc: int, kc_numel: int, vc: int,
+                       vc_numel: int, o: int, o_numel: int, h: int, hkv: int, pos: int, hd: int,
+                       max_seq: int, scale: float, workspace: int, workspace_floats: int,
+                       cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                      o_numel, h, hkv, pos, hd, max_seq, scale, workspace,
+                                      workspace_floats, cu_count))
+
+
+def launch_rmsnorm(stream: int, x: int, x_numel: int, w: int, w_numel: int, out: int,
+                   out_numel: int, rows: int, dim: int, eps: float) -> None:
+    check(lib().eb_launch_rmsnorm(stream, x, x_numel, w, w_numel, out, out_numel, rows, dim,
+                                  eps))
+
+
+def launch_rope(stream: int, x: int, x_numel: int, cos: int, sin: int, table_numel: int,
+                out: int, out_numel: int, seq: int, n_heads: int, head_dim: int,
+                base_pos: int) -> None:
+    check(lib().eb_launch_rope(stream, x, x_numel, cos, sin, table_numel, out, out_numel, seq,
+                               n_heads, head_dim, base_pos))

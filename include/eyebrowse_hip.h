@@ -1,0 +1,222 @@
+/*
+ * eyebrowse_hip — MI355X (gfx950) attention hot path behind a C ABI.
+ *
+ * This header is the drop-in boundary for the eyebrowse runtime's attention path:
+ * the eyebrowse-gpu substrate (Device / Tensor / Recorder), the eyebrowse-kernels
+ * entry points (attn_prefill, attn_decode, kv_write, rmsnorm, rope) and the
+ * eyebrowse-nn pieces around them (Rope tables, KvCache, the Attention forward between
+ * the projections). Every declaration cites the reference interface it replaces
+ * (paths relative to the reference repository root).
+ *
+ * Conventions
+ *  - All tensors are f32, row-major, seq-major: q [S, H, HD], k/v [S, Hkv, HD], KV cache
+ *    [max_seq, Hkv, HD], o [S, H, HD]. Query head h reads KV head h / (H / Hkv).
+ *  - Functions return eb_status; on failure eb_last_error() holds a message (thread local).
+ *    The reference has no error channel (its kernels return `()`); a Rust shim keeps its
+ *    signatures by turning a non-OK status into a panic (see the integration notes).
+ *  - One device owns one HIP stream. Recording a kernel enqueues it on that stream, so
+ *    record order is execution order, as with the reference's single wgpu queue.
+ *  - Raw entry points (eb_launch_*) take a hipStream_t as void* and device pointers with
+ *    their element counts; they validate every size before touching the GPU.
+ */
+#ifndef EYEBROWSE_HIP_H
+#define EYEBROWSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Mirrors EyebrowseError (crates/eyebrowse-core/src/lib.rs:27-41), 0 = Ok. */
+typedef enum eb_status {
+    EB_OK = 0,
+    EB_DEVICE_UNAVAILABLE = 1,
+    EB_LOAD = 2,
+    EB_UNSUPPORTED_CONFIG = 3,
+    EB_SHAPE_MISMATCH = 4,
+    EB_OUT_OF_MEMORY = 5,
+    EB_OTHER = 6
+} eb_status;
+
+/* Mirrors DType (crates/eyebrowse-core/src/lib.rs:8-25). */
+typedef enum eb_dtype { EB_F32 = 0, EB_F16 = 1, EB_U32 = 2, EB_I32 = 3 } eb_dtype;
+
+typedef struct eb_device eb_device;
+typedef struct eb_tensor eb_tensor;
+typedef struct eb_recorder eb_recorder;
+typedef struct eb_rope_tables eb_rope_tables;
+typedef struct eb_kv_cache eb_kv_cache;
+typedef struct eb_attention eb_attention;
+
+/* ---- errors / types -------------------------------------------------------------- */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *eb_last_error(void);
+/* Name of a status ("Ok", "DeviceUnavailable", ...). */
+const char *eb_status_name(eb_status st);
+/* DType::size (crates/eyebrowse-core/src/lib.rs:14-24); 0 for an unknown dtype. */
+size_t eb_dtype_size(eb_dtype dt);
+/* Library version string. */
+const char *eb_version(void);
+
+/* ---- device (crates/eyebrowse-gpu/src/device.rs:20-110) --------------------------- */
+
+/* Device::new (device.rs:32-61): HIP device `ordinal`, one stream, an empty pool.
+ * EB_DEVICE_UNAVAILABLE when no GPU is visible. */
+eb_status eb_device_new(int ordinal, eb_device **out);
+/* Drop the caller's reference (the device lives while tensors/recorders hold it). */
+void eb_device_release(eb_device *dev);
+/* Wait for everything recorded on the device stream. */
+eb_status eb_device_synchronize(eb_device *dev);
+/* The device's hipStream_t, for callers that time or interleave their own work. */
+void *eb_device_stream(eb_device *dev);
+/* Compute units of the device (256 on MI355X). */
+int eb_device_cu_count(eb_device *dev);
+/* Number of free pooled buffers of exactly `bytes` (device.rs:63-70, test hook). */
+size_t eb_device_pooled(eb_device *dev, size_t bytes);
+/* Largest buffer the pool recycles, MAX_POOLED_BYTES (device.rs:12-14). */
+size_t eb_pool_max_bytes(void);
+
+/* ---- tensor (crates/eyebrowse-gpu/src/tensor.rs:34-157) --------------------------- */
+
+/* Tensor::empty (tensor.rs:226-236): uninitialised, drawn from the pool when a free
+ * buffer of the exact byte size exists (sizes <= eb_pool_max_bytes()). */
+eb_status eb_tensor_empty(eb_device *dev, const size_t *shape, size_t ndim, eb_dtype dt,
+                          eb_tensor **out);
+/* Tensor::from_f32 / from_u32 (tensor.rs:241-267): a fresh, never-pooled buffer
+ * initialised from host memory (n elements must equal the shape's element count). */
+eb_status eb_tensor_from_f32(eb_device *dev, const size_t *shape, size_t ndim,
+                             const float *data, size_t n, eb_tensor **out);
+eb_status eb_tensor_from_u32(eb_device *dev, const size_t *shape, size_t ndim,
+                             const uint32_t *data, size_t n, eb_tensor **out);
+/* Tensor::to_f32 / read_bytes (tensor.rs:279-318): waits for the stream, then copies.
+ * `n`/`nbytes` must equal the tensor's element / byte count. */
+eb_status eb_tensor_to_f32(const eb_tensor *t, float *host, size_t n);
+eb_status eb_tensor_read_bytes(const eb_tensor *t, void *host, size_t nbytes);
+/* Drop for Tensor (tensor.rs:41-47): back to the pool (or freed if larger). */
+void eb_tensor_release(eb_tensor *t);
+size_t eb_tensor_ndim(const eb_tensor *t);
+size_t eb_tensor_dim(const eb_tensor *t, size_t i);
+size_t eb_tensor_numel(const eb_tensor *t);
+size_t eb_tensor_nbytes(const eb_tensor *t);
+eb_dtype eb_tensor_dtype(const eb_tensor *t);
+/* Device address of the tensor's storage. */
+void *eb_tensor_data(const eb_tensor *t);
+
+/* ---- recorder (crates/eyebrowse-gpu/src/recorder.rs:10-35) ------------------------ */
+
+/* Recorder::new: kernels recorded through it are enqueued on the device stream. */
+eb_status eb_recorder_new(eb_device *dev, eb_recorder **out);
+/* Recorder::submit (recorder.rs:33-35): flush, report any launch error, release. */
+eb_status eb_recorder_submit(eb_recorder *rec);
+/* Drop a recorder without submitting (work already enqueued still runs). */
+void eb_recorder_release(eb_recorder *rec);
+
+/* ---- kernels (crates/eyebrowse-kernels/src) --------------------------------------- */
+
+/* attn_prefill (attention.rs:94-120): causal GQA attention over q [s,h,hd],
+ * k/v [s,hkv,hd] into o [s,h,hd], keys 0..=i for row i, online softmax. */
+eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                          const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
+                          size_t hd, float scale);
+/* attn_decode (attention.rs:124-162): q [h,hd] attends keys 0..=pos of the seq-major
+ * caches [max_seq,hkv,hd]; o [h,hd]. Split-KV with a log-sum-exp merge; the split
+ * workspace belongs to the device and is stream ordered. */
+eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
+                         const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                         size_t pos, size_t hd, size_t max_seq, float scale);
+/* kv_write (ops.rs:150-179): copy src [count,hkv,hd] into cache rows
+ * [dst_start, dst_start+count) of [max_seq,hkv,hd]; bit-exact. Unlike the reference,
+ * dst_start + count > max_seq is rejected (EB_SHAPE_MISMATCH). */
+eb_status eb_kv_write(eb_recorder *rec, eb_tensor *cache, const eb_tensor *src, size_t hkv,
+                      size_t count, size_t hd, size_t max_seq, size_t dst_start);
+/* rmsnorm (rmsnorm.rs:42-64): out = x / sqrt(mean(x^2) + eps) * weight per row. */
+eb_status eb_rmsnorm(eb_recorder *rec, const eb_tensor *x, const eb_tensor *weight,
+                     eb_tensor *out, size_t rows, size_t dim, float eps);
+/* rope (rope.rs:38-69): half-split rotary on x [seq,n_heads,hd] with cos/sin tables
+ * [max_seq,hd/2] read at rows base_pos.. */
+eb_status eb_rope(eb_recorder *rec, const eb_tensor *x, const eb_tensor *cos,
+                  const eb_tensor *sin, eb_tensor *out, size_t seq, size_t n_heads,
+                  size_t head_dim, size_t base_pos);
+
+/* ---- raw launches: the same kernels on caller memory ----------------------------- */
+
+eb_status eb_launch_kv_write(void *stream, float *cache, size_t cache_numel,
+                             const float *src, size_t src_numel, size_t hkv, size_t count,
+                             size_t hd, size_t max_seq, size_t dst_start);
+eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel,
+                                 const float *k, size_t k_numel, const float *v,
+                                 size_t v_numel, float *o, size_t o_numel, size_t h,
+                                 size_t hkv, size_t s, size_t hd, float scale);
+/* Floats of workspace eb_launch_attn_decode needs for this shape on this many CUs
+ * (0 when the split count is 1 and no workspace is used). */
+size_t eb_attn_decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd,
+                                       int cu_count);
+eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel,
+                                const float *kc, size_t kc_numel, const float *vc,
+                                size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                float scale, float *workspace, size_t workspace_floats,
+                                int cu_count);
+eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel,
+                            const float *weight, size_t w_numel, float *out,
+                            size_t out_numel, size_t rows, size_t dim, float eps);
+eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const float *cos,
+                         const float *sin, size_t table_numel, float *out, size_t out_numel,
+                         size_t seq, size_t n_heads, size_t head_dim, size_t base_pos);
+
+/* ---- nn (crates/eyebrowse-nn/src) -------------------------------------------------- */
+
+/* Rope::build_partial (rope.rs:24-50): host f64 tables -> f32 device tensors
+ * [max_seq, head_dim/2]; rope_angles = head_dim/2 is Rope::build (rope.rs:18-20). */
+eb_status eb_rope_build_partial(eb_device *dev, size_t max_seq, size_t head_dim,
+                                size_t rope_angles, float theta, eb_rope_tables **out);
+void eb_rope_tables_release(eb_rope_tables *rope);
+const eb_tensor *eb_rope_tables_cos(const eb_rope_tables *rope);
+const eb_tensor *eb_rope_tables_sin(const eb_rope_tables *rope);
+/* Rope::apply (rope.rs:54-75): returns a new tensor [seq, n_heads, head_dim]. */
+eb_status eb_rope_apply(const eb_rope_tables *rope, eb_recorder *rec, const eb_tensor *x,
+                        size_t seq, size_t n_heads, size_t base_pos, eb_tensor **out);
+
+/* KvCache::new_per_layer (kv_cache.rs:29-50): per layer l, K and V tensors
+ * [max_seq, n_kv_heads, head_dims[l]] from Tensor::empty. */
+eb_status eb_kv_cache_new_per_layer(eb_device *dev, const size_t *head_dims, size_t n_layers,
+                                    size_t max_seq, size_t n_kv_heads, eb_kv_cache **out);
+void eb_kv_cache_release(eb_kv_cache *kv);
+eb_tensor *eb_kv_cache_k(eb_kv_cache *kv, size_t layer);
+eb_tensor *eb_kv_cache_v(eb_kv_cache *kv, size_t layer);
+size_t eb_kv_cache_max_seq(const eb_kv_cache *kv);
+
+/* The Attention fields that matter between the projections
+ * (crates/eyebrowse-nn/src/attention.rs:10-23). Norm weights are [head_dim] f32
+ * tensors or NULL (None); the module keeps its own references. */
+typedef struct eb_attention_desc {
+    size_t n_heads;
+    size_t n_kv_heads;
+    size_t head_dim;
+    float scale;
+    float norm_eps;
+    const eb_tensor *q_norm; /* may be NULL */
+    const eb_tensor *k_norm; /* may be NULL */
+    const eb_tensor *v_norm; /* may be NULL */
+} eb_attention_desc;
+
+eb_status eb_attention_new(const eb_attention_desc *desc, eb_attention **out);
+void eb_attention_release(eb_attention *attn);
+/* Attention::forward (attention.rs:30-45, 49-117, 120-185) from the projected
+ * q [rows, n_heads*hd], k/v [rows, n_kv_heads*hd] on: optional q/k/v RMSNorm, RoPE at
+ * base_pos, kv_write of K and V at base_pos, then attn_prefill (base_pos == 0 and
+ * rows > 1) or attn_decode. *out is a new tensor [rows, n_heads*hd] (the input of
+ * o_proj). */
+eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recorder *rec,
+                                   const eb_tensor *q, const eb_tensor *k, const eb_tensor *v,
+                                   const eb_rope_tables *rope, eb_kv_cache *kv, size_t layer,
+                                   size_t rows, size_t base_pos, eb_tensor **out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EYEBROWSE_HIP_H */

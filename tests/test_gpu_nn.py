@@ -1,0 +1,256 @@
+"""The substrate and the eyebrowse-nn pieces on the GPU: buffer-pool semantics
+(crates/eyebrowse-gpu/src/device.rs:119-161), RMSNorm / RoPE kernels and tables
+(rmsnorm.rs:72-90, rope.rs:92-111, nn/src/rope.rs:82-104, nn/src/tests.rs:152-177),
+per-layer caches (kv_cache.rs:56-65), the Attention forward against the oracle chain,
+and the prefill/decode consistency invariant (nn/src/tests.rs:181-244)."""
+import numpy as np
+import pytest
+
+import eyebrowse_amd as eb
+import oracle
+from tests._gpu import assert_close, note, upload
+from tests._textbook import rel_l2_f64
+
+pytestmark = pytest.mark.gpu
+
+
+# ---------------------------------------------------------------- substrate -------------
+
+def test_empty_recycles_buffers_through_the_pool():
+    """device.rs:119-139, on a fresh device."""
+    note("pool recycle")
+    d = eb.Device.new(0)
+    size = 64 * 4
+    assert d.pooled(size) == 0
+    eb.Tensor.empty(d, (64,)).release()
+    assert d.pooled(size) == 1
+    t = eb.Tensor.empty(d, (64,))
+    assert d.pooled(size) == 0
+    t.release()
+    assert d.pooled(size) == 1
+
+
+def test_host_initialized_tensors_do_not_draw_from_the_pool():
+    """device.rs:141-161."""
+    note("pool host-initialized")
+    d = eb.Device.new(0)
+    eb.Tensor.empty(d, (4,)).release()
+    assert d.pooled(16) == 1
+    t = eb.Tensor.from_f32(d, (4,), [1.0, 2.0, 3.0, 4.0])
+    assert d.pooled(16) == 1
+    np.testing.assert_array_equal(t.to_f32(), [1, 2, 3, 4])
+    t.release()
+    assert d.pooled(16) == 1  # unpooled origin: freed, not recycled
+
+
+def test_large_buffers_bypass_the_pool():
+    d = eb.Device.new(0)
+    big = (64 << 20) // 4 + 1
+    eb.Tensor.empty(d, (big,)).release()
+    assert d.pooled(big * 4) == 0
+
+
+def test_upload_readback_round_trip(dev):
+    x = np.arange(1000, dtype=np.float32) * 0.5 - 3
+    t = eb.Tensor.from_f32(dev, (10, 100), x)
+    assert t.shape == (10, 100) and t.dtype == eb.DType.F32 and t.numel() == 1000
+    np.testing.assert_array_equal(t.to_f32(), x)
+    u = eb.Tensor.from_u32(dev, (3,), [1, 2, 0xFFFFFFFF])
+    assert np.frombuffer(u.read_bytes(), np.uint32).tolist() == [1, 2, 0xFFFFFFFF]
+
+
+def test_kv_cache_per_layer_shapes(dev):
+    """kv_cache.rs:56-65."""
+    cache = eb.KvCache.new_per_layer(dev, [16, 32], 8, 2)
+    assert cache.k[0].shape == (8, 2, 16) and cache.k[1].shape == (8, 2, 32)
+    assert cache.v[0].shape == (8, 2, 16) and cache.v[1].shape == (8, 2, 32)
+
+
+# ---------------------------------------------------------------- RMSNorm / RoPE --------
+
+def test_rmsnorm_reference_case(dev):
+    """rmsnorm.rs:72-90 (rows 3, dim 320 > 256); reference bar rel_l2 < 1e-4."""
+    note("rmsnorm reference case")
+    rows, dim, eps = 3, 320, 1e-6
+    x = (np.arange(rows * dim) % 17).astype(np.float32) * np.float32(0.05) - np.float32(0.4)
+    w = np.float32(1.0) + np.arange(dim, dtype=np.float32) * np.float32(0.001)
+    xt, wt = upload(dev, x.reshape(rows, dim)), upload(dev, w)
+    ot = eb.Tensor.empty(dev, (rows, dim))
+    rec = eb.Recorder(dev)
+    eb.rmsnorm(rec, xt, wt, ot, rows, dim, eps)
+    rec.submit()
+    want = oracle.rmsnorm(x, w, rows, dim, eps)
+    assert oracle.rel_l2(ot.to_f32(), want) < 1e-6
+
+
+def test_rmsnorm_gemma_heads(dev):
+    rows, dim = 4096 * 8, 256
+    x = oracle.randn((rows, dim), 3)
+    w = (1 + 0.1 * oracle.randn((dim,), 4)).astype(np.float32)
+    xt, wt = upload(dev, x), upload(dev, w)
+    ot = eb.Tensor.empty(dev, (rows, dim))
+    rec = eb.Recorder(dev)
+    eb.rmsnorm(rec, xt, wt, ot, rows, dim, 1e-6)
+    rec.submit()
+    assert oracle.rel_l2(ot.to_f32(), oracle.rmsnorm(x, w, rows, dim, 1e-6)) < 1e-6
+
+
+def test_rope_tables_match_oracle_bitwise(dev):
+    """Rope::build / build_partial tables (nn/src/rope.rs:24-50), both f64 then f32."""
+    for ms, hd, theta, ra in [(8, 4, 1e4, None), (5, 8, 1e4, 2), (300, 256, 1e6, 32)]:
+        r = eb.Rope.build(dev, ms, hd, theta) if ra is None else \
+            eb.Rope.build_partial(dev, ms, hd, ra, theta)
+        c, s = oracle.rope_tables(ms, hd, theta, rope_angles=ra)
+        assert r.cos.to_f32().tobytes() == c.tobytes()
+        assert r.sin.to_f32().tobytes() == s.tobytes()
+
+
+@pytest.mark.parametrize("seq,nh,hd,theta,ra,base", [
+    (4, 2, 8, 1e4, None, 0),          # rope.rs:92-111 reference case
+    (1, 16, 128, 1e6, None, 777),     # a decode row at base_pos
+    (300, 8, 256, 1e6, 32, 0),        # Gemma partial rotary
+])
+def test_rope_kernel(dev, seq, nh, hd, theta, ra, base):
+    note(f"rope seq={seq} nh={nh} hd={hd}")
+    ms = seq + base
+    if (seq, nh, hd) == (4, 2, 8):
+        x = np.arange(seq * nh * hd, dtype=np.float32) * np.float32(0.03) - np.float32(0.5)
+    else:
+        x = oracle.randn((seq * nh * hd,), 9)
+    r = eb.Rope.build(dev, ms, hd, theta) if ra is None else eb.Rope.build_partial(dev, ms, hd, ra, theta)
+    xt = upload(dev, x.reshape(seq, nh, hd))
+    rec = eb.Recorder(dev)
+    out = r.apply(rec, xt, seq, nh, base)
+    rec.submit()
+    c, s = oracle.rope_tables(ms, hd, theta, rope_angles=ra)
+    want = oracle.rope(x, c, s, seq, nh, hd, base)
+    got = out.to_f32()
+    assert oracle.rel_l2(got, want) < 1e-6
+    if ra is not None:  # pass-through pairs are exact
+        g3, x3 = got.reshape(seq, nh, hd), x.reshape(seq, nh, hd)
+        np.testing.assert_array_equal(g3[..., ra:hd // 2], x3[..., ra:hd // 2])
+        np.testing.assert_array_equal(g3[..., hd // 2 + ra:], x3[..., hd // 2 + ra:])
+
+
+# ---------------------------------------------------------------- Attention -------------
+
+def _oracle_chain(q, k, v, H, Hkv, hd, rows, base, gq, gk, gv, eps, rope_t, kc, vc, max_seq,
+                  scale):
+    c, s = rope_t
+    qn = oracle.rmsnorm(q, gq, rows * H, hd, eps) if gq is not None else q.ravel()
+    kn = oracle.rmsnorm(k, gk, rows * Hkv, hd, eps) if gk is not None else k.ravel()
+    vn = oracle.rmsnorm(v, gv, rows * Hkv, hd, eps) if gv is not None else v.ravel()
+    qr = oracle.rope(qn, c, s, rows, H, hd, base)
+    kr = oracle.rope(kn, c, s, rows, Hkv, hd, base)
+    kc = oracle.kv_write(kc, kr, Hkv, rows, hd, base)
+    vc = oracle.kv_write(vc, vn, Hkv, rows, hd, base)
+    if base == 0 and rows > 1:
+        o = oracle.attn_prefill(qr, kr, vn, H, Hkv, rows, hd, scale, threads=16)
+    else:
+        o = oracle.attn_decode(qr, kc, vc, H, Hkv, base, hd, max_seq, scale, threads=16)
+    return o.reshape(rows, H * hd), kc, vc
+
+
+def test_prefill_decode_consistency(dev):
+    """nn/src/tests.rs:181-244 from the projected q/k/v: prefill over 3 rows, then 3 decode
+    steps through a fresh cache; the last decode row equals prefill's last row (the
+    reference accepts rel_l2 < 2e-3; here the f32 bar)."""
+    note("attention prefill/decode consistency")
+    H, Hkv, hd, seq, max_seq = 4, 2, 4, 3, 8
+    x_q = oracle.prng(seq * H * hd, 21).reshape(seq, H * hd)
+    x_k = oracle.prng(seq * Hkv * hd, 22).reshape(seq, Hkv * hd)
+    x_v = oracle.prng(seq * Hkv * hd, 23).reshape(seq, Hkv * hd)
+    qn = upload(dev, oracle.prng(hd, 15))
+    kn = upload(dev, oracle.prng(hd, 16))
+    attn = eb.Attention(H, Hkv, hd, float(oracle.default_scale(hd)), q_norm=qn, k_norm=kn)
+    rope = eb.Rope.build(dev, max_seq, hd, 10000.0)
+    kv_p = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    rec = eb.Recorder(dev)
+    pre = attn.forward_qkv(rec, upload(dev, x_q), upload(dev, x_k), upload(dev, x_v), rope, kv_p,
+                           0, seq, 0)
+    rec.submit()
+    pre_out = pre.to_f32().reshape(seq, H * hd)
+    kv_d = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    last = None
+    for pos in range(seq):
+        rec = eb.Recorder(dev)
+        out = attn.forward_qkv(rec, upload(dev, x_q[pos:pos + 1]), upload(dev, x_k[pos:pos + 1]),
+                               upload(dev, x_v[pos:pos + 1]), rope, kv_d, 0, 1, pos)
+        rec.submit()
+        last = out.to_f32()
+    assert rel_l2_f64(last, pre_out[seq - 1]) < 2e-5
+    # both caches hold the same rows 0..seq-1
+    assert kv_p.k[0].to_f32()[: seq * Hkv * hd].tobytes() == kv_d.k[0].to_f32()[: seq * Hkv * hd].tobytes()
+
+
+def test_gemma_attention_forward(dev):
+    """BASELINE config 5 through Attention.forward_qkv: per-head QK-RMSNorm with learned
+    gains, weightless V-RMSNorm, partial RoPE (32 of 128 pairs, theta 1e6), scale 1.0,
+    hd 256; prefill T=4096 (row samples) then one decode step at pos 16383 of a
+    max_seq 16384 cache."""
+    H, Hkv, hd, eps = 16, 8, 256, 1e-6
+    T, max_seq = 4096, 16384
+    note(f"gemma attention prefill T={T}")
+    gq = (1 + 0.1 * oracle.randn((hd,), 4)).astype(np.float32)
+    gk = (1 + 0.1 * oracle.randn((hd,), 5)).astype(np.float32)
+    ones = np.ones(hd, np.float32)
+    attn = eb.Attention(H, Hkv, hd, 1.0, q_norm=upload(dev, gq), k_norm=upload(dev, gk),
+                        v_norm=upload(dev, ones), norm_eps=eps)
+    rope = eb.Rope.build_partial(dev, max_seq, hd, 32, 1e6)
+    rope_t = oracle.rope_tables(max_seq, hd, 1e6, rope_angles=32)
+    q = oracle.randn((T, H * hd), 1)
+    k = oracle.randn((T, Hkv * hd), 2)
+    v = oracle.randn((T, Hkv * hd), 3)
+    kv = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    rec = eb.Recorder(dev)
+    out = attn.forward_qkv(rec, upload(dev, q), upload(dev, k), upload(dev, v), rope, kv, 0, T, 0)
+    rec.submit()
+    got = out.to_f32().reshape(T, H * hd)
+    # oracle: norms + rope on the whole prompt, attention on row samples
+    qr = oracle.rope(oracle.rmsnorm(q, gq, T * H, hd, eps), *rope_t, T, H, hd)
+    kr = oracle.rope(oracle.rmsnorm(k, gk, T * Hkv, hd, eps), *rope_t, T, Hkv, hd)
+    vn = oracle.rmsnorm(v, ones, T * Hkv, hd, eps)
+    for row0, n in [(0, 24), (2000, 24), (T - 24, 24)]:
+        want = oracle.attn_prefill(qr, kr, vn, H, Hkv, T, hd, 1.0, rows=(row0, n), threads=16)
+        assert_close(got[row0:row0 + n], want[row0:row0 + n].reshape(n, H * hd),
+                     what=f"gemma prefill rows {row0}")
+    # the cache holds the post-RoPE K and the normed V (attention.rs:78-97)
+    kc_all = kv.k[0].to_f32()
+    assert kc_all[: T * Hkv * hd].tobytes() == kr.tobytes()
+    assert kv.v[0].to_f32()[: T * Hkv * hd].tobytes() == vn.tobytes()
+
+    # decode at pos 16383 over a filled cache
+    note("gemma attention decode pos=16383")
+    pos = max_seq - 1
+    kfill = oracle.randn((max_seq, Hkv, hd), 6)
+    vfill = oracle.randn((max_seq, Hkv, hd), 7)
+    kv2 = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, kv2.k[0], upload(dev, kfill), Hkv, max_seq, hd, max_seq, 0)
+    eb.kv_write(rec, kv2.v[0], upload(dev, vfill), Hkv, max_seq, hd, max_seq, 0)
+    rec.submit()
+    q1, k1, v1 = oracle.randn((1, H * hd), 8), oracle.randn((1, Hkv * hd), 9), oracle.randn((1, Hkv * hd), 10)
+    rec = eb.Recorder(dev)
+    o1 = attn.forward_qkv(rec, upload(dev, q1), upload(dev, k1), upload(dev, v1), rope, kv2, 0, 1, pos)
+    rec.submit()
+    want1, kc_w, _ = _oracle_chain(q1, k1, v1, H, Hkv, hd, 1, pos, gq, gk, ones, eps, rope_t,
+                                   kfill, vfill, max_seq, 1.0)
+    assert_close(o1.to_f32().reshape(1, H * hd), want1, what="gemma decode")
+    assert kv2.k[0].to_f32().tobytes() == kc_w.tobytes()
+
+
+def test_forward_routing_and_errors(dev):
+    H, Hkv, hd = 4, 2, 8
+    attn = eb.Attention(H, Hkv, hd, 0.3)
+    rope = eb.Rope.build(dev, 16, hd, 1e4)
+    kv = eb.KvCache.new(dev, 1, 16, Hkv, hd)
+    q = upload(dev, oracle.randn((2, H * hd), 1))
+    k = upload(dev, oracle.randn((2, Hkv * hd), 2))
+    rec = eb.Recorder(dev)
+    with pytest.raises(eb.UnsupportedConfig):       # 2 rows at base_pos 5: chunked prefill
+        attn.forward_qkv(rec, q, k, k, rope, kv, 0, 2, 5)
+    with pytest.raises(eb.ShapeMismatch):           # layer out of range
+        attn.forward_qkv(rec, q, k, k, rope, kv, 1, 2, 0)
+    rec.submit()
+    with pytest.raises(eb.UnsupportedConfig):
+        eb.Attention(H, Hkv, 6, 0.3)

@@ -1,0 +1,129 @@
+"""attn_prefill on the GPU against the oracle (crates/eyebrowse-kernels/src/testutil.rs:
+130-172 restated in oracle/oracle.c): the reference's own ramp case, the golden T=64
+config, ragged and odd shapes, and the full-size BASELINE configs checked on row samples
+(every query row of the kernel's output is also checked for finiteness and for the
+causal-prefix property)."""
+import numpy as np
+import pytest
+
+import eyebrowse_amd as eb
+import oracle
+from tests._gpu import assert_close, note, prefill, upload
+
+pytestmark = pytest.mark.gpu
+
+
+def test_reference_ramp_case(dev):
+    """attention.rs:175-202: h=2, hkv=1, s=5, hd=8; reference bar rel_l2 < 1e-4."""
+    note("prefill reference ramp case")
+    g = np.load("tests/golden/reference_ramp_cases.npz", allow_pickle=False)
+    h, hkv, s, hd = 2, 1, 5, 8
+    got = prefill(dev, g["prefill_q"].reshape(s, h, hd), g["prefill_k"].reshape(s, hkv, hd),
+                  g["prefill_v"].reshape(s, hkv, hd), h, hkv, s, hd, 1 / np.sqrt(np.float32(hd)))
+    assert oracle.rel_l2(got, g["prefill_o"]) < 1e-4
+    assert_close(got, g["prefill_o"].reshape(s, h, hd), what="ramp")
+
+
+def test_golden_qwen_t64(dev):
+    """BASELINE config 1 (T=64, 16/8 heads, hd 128) against the committed fixture."""
+    note("prefill golden qwen T=64")
+    g = np.load("tests/golden/qwen_t64_prefill.npz", allow_pickle=False)
+    T, H, Hkv, hd = int(g["T"]), int(g["H"]), int(g["Hkv"]), int(g["hd"])
+    got = prefill(dev, oracle.randn((T, H, hd), 1), oracle.randn((T, Hkv, hd), 2),
+                  oracle.randn((T, Hkv, hd), 3), H, Hkv, T, hd, float(g["scale"]))
+    assert_close(got, g["o"], what="golden T=64")
+
+
+@pytest.mark.parametrize("h,hkv,s,hd,scale", [
+    (16, 8, 1, 128, None),     # one row: o = v[0]
+    (16, 8, 2, 128, None),
+    (16, 8, 31, 128, None),
+    (16, 8, 33, 128, None),
+    (16, 8, 100, 128, None),
+    (32, 8, 65, 128, None),    # GQA 4 (4 heads per workgroup)
+    (8, 8, 97, 64, None),      # MHA (1 head per workgroup)
+    (24, 8, 70, 128, 0.2),     # GQA 3
+    (64, 4, 40, 128, None),    # GQA 16 (four 4-head workgroups per KV head)
+    (16, 8, 77, 256, 1.0),     # Gemma hd 256, scale 1
+    (4, 2, 50, 32, None),
+    (4, 2, 50, 16, None),
+    (4, 2, 19, 4, None),
+    (2, 1, 130, 8, 0.0),       # scale 0: causal prefix mean of V
+])
+def test_shapes(dev, h, hkv, s, hd, scale):
+    note(f"prefill h={h} hkv={hkv} s={s} hd={hd} scale={scale}")
+    sc = float(oracle.default_scale(hd)) if scale is None else scale
+    q = oracle.randn((s, h, hd), 11)
+    k = oracle.randn((s, hkv, hd), 12)
+    v = oracle.randn((s, hkv, hd), 13)
+    got = prefill(dev, q, k, v, h, hkv, s, hd, sc)
+    want = oracle.attn_prefill(q, k, v, h, hkv, s, hd, sc, threads=8)
+    assert_close(got, want, what="shape")
+    g = h // hkv
+    np.testing.assert_array_equal(got[0], np.repeat(v[0], g, axis=0))
+
+
+def _sampled_rows(T):
+    rows = [(0, 40), (T // 2 - 20, 40), (T - 40, 40)]
+    return [(a, n) for a, n in rows if a >= 0]
+
+
+@pytest.mark.parametrize("name,H,Hkv,hd,T,scale", [
+    ("qwen", 16, 8, 128, 512, None),
+    ("qwen", 16, 8, 128, 2048, None),
+    ("qwen", 16, 8, 128, 4096, None),
+    ("mistral", 32, 8, 128, 4096, None),
+])
+def test_baseline_prefill_configs(dev, name, H, Hkv, hd, T, scale):
+    """BASELINE configs 3 and 4 at full size: K/V written by kv_write into a max_seq = T
+    cache, prefill over the fresh K/V (attention.rs:78-115), compared with the oracle on
+    row samples at the start, middle and end of the sequence."""
+    note(f"prefill {name} T={T}")
+    sc = float(oracle.default_scale(hd)) if scale is None else scale
+    q = oracle.randn((T, H, hd), 1)
+    k = oracle.randn((T, Hkv, hd), 2)
+    v = oracle.randn((T, Hkv, hd), 3)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    kc = eb.Tensor.empty(dev, (T, Hkv, hd))
+    vc = eb.Tensor.empty(dev, (T, Hkv, hd))
+    ot = eb.Tensor.empty(dev, (T, H, hd))
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, kc, kt, Hkv, T, hd, T, 0)
+    eb.kv_write(rec, vc, vt, Hkv, T, hd, T, 0)
+    eb.attn_prefill(rec, qt, kc, vc, ot, H, Hkv, T, hd, sc)
+    rec.submit()
+    got = ot.to_f32().reshape(T, H, hd)
+    assert np.isfinite(got).all()
+    for row0, n in _sampled_rows(T):
+        want = oracle.attn_prefill(q, k, v, H, Hkv, T, hd, sc, rows=(row0, n), threads=16)
+        assert_close(got[row0:row0 + n], want[row0:row0 + n], what=f"{name} rows {row0}+{n}")
+    # |o| <= max |v| row-wise (a convex combination of V rows), every row
+    vmax = np.abs(v).max(axis=0).max()
+    assert np.abs(got).max() <= vmax * (1 + 1e-5)
+
+
+def test_prefill_is_deterministic_and_order_free(dev):
+    """Two launches give identical bits; a causal row only depends on its prefix: running
+    the first 100 rows alone gives the same bits as rows 0..99 of a 300-row prefill."""
+    note("prefill determinism / prefix")
+    H, Hkv, hd, T = 16, 8, 128, 300
+    q, k, v = oracle.randn((T, H, hd), 1), oracle.randn((T, Hkv, hd), 2), oracle.randn((T, Hkv, hd), 3)
+    sc = float(oracle.default_scale(hd))
+    a = prefill(dev, q, k, v, H, Hkv, T, hd, sc)
+    b = prefill(dev, q, k, v, H, Hkv, T, hd, sc)
+    assert a.tobytes() == b.tobytes()
+    c = prefill(dev, q[:100].copy(), k[:100].copy(), v[:100].copy(), H, Hkv, 100, hd, sc)
+    assert c.tobytes() == a[:100].tobytes()
+
+
+def test_raw_launch(dev):
+    note("prefill raw launch")
+    H, Hkv, hd, T = 16, 8, 128, 200
+    q, k, v = oracle.randn((T, H, hd), 4), oracle.randn((T, Hkv, hd), 5), oracle.randn((T, Hkv, hd), 6)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    ot = eb.Tensor.empty(dev, (T, H, hd))
+    eb.launch_attn_prefill(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(),
+                           vt.data_ptr, vt.numel(), ot.data_ptr, ot.numel(), H, Hkv, T, hd, 0.1)
+    dev.synchronize()
+    want = oracle.attn_prefill(q, k, v, H, Hkv, T, hd, 0.1, threads=8)
+    assert_close(ot.to_f32().reshape(T, H, hd), want, what="raw")

@@ -1,0 +1,322 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is compared against it.
+
+Each oracle function is checked against something that does not share its code:
+float64 textbook attention / RMSNorm / RoPE (tests/_textbook.py), torch's own CPU
+scaled_dot_product_attention in float64, closed forms and invariants, and the
+reference's own known-answer cases (same ramp inputs and shapes as
+crates/eyebrowse-kernels/src/attention.rs:175-233, ops.rs:271-292, rope.rs:92-111,
+rmsnorm.rs:72-90, crates/eyebrowse-nn/src/rope.rs:82-104, nn/src/tests.rs:152-177).
+A mutation test builds deliberately wrong oracles and shows the checks reject them.
+"""
+import os
+import subprocess
+import tempfile
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._textbook import attention_f64, ramp, rel_l2_f64, rmsnorm_f64, rope_f64
+
+# The oracle is f32 arithmetic; against float64 the residual is f32 rounding only.
+F32_VS_F64 = 2e-6
+
+
+# ---------------------------------------------------------------- attention -------------
+
+@pytest.mark.parametrize("h,hkv,s,hd,scale", [
+    (2, 1, 5, 8, None),        # reference prefill known-answer shape (attention.rs:177)
+    (4, 2, 9, 16, None),
+    (16, 8, 33, 128, None),    # Qwen3 shape, short
+    (32, 8, 17, 128, None),    # Mistral GQA ratio 4
+    (4, 4, 7, 32, 0.3),        # MHA, explicit scale
+    (16, 8, 12, 256, 1.0),     # Gemma hd=256, scale 1.0
+])
+def test_prefill_matches_f64_textbook(h, hkv, s, hd, scale):
+    q = oracle.randn((s, h, hd), 11)
+    k = oracle.randn((s, hkv, hd), 12)
+    v = oracle.randn((s, hkv, hd), 13)
+    sc = oracle.default_scale(hd) if scale is None else scale
+    got = oracle.attn_prefill(q, k, v, h, hkv, s, hd, sc)
+    want = attention_f64(q, k, v, sc)
+    assert rel_l2_f64(got, want) < F32_VS_F64 * (4 if scale == 1.0 else 1)
+
+
+def test_prefill_matches_torch_sdpa_f64():
+    torch = pytest.importorskip("torch")
+    import torch.nn.functional as F
+    h, hkv, s, hd = 8, 2, 21, 64
+    q = oracle.randn((s, h, hd), 1)
+    k = oracle.randn((s, hkv, hd), 2)
+    v = oracle.randn((s, hkv, hd), 3)
+    got = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    tq = torch.from_numpy(q).double().permute(1, 0, 2)[None]
+    tk = torch.from_numpy(k).double().permute(1, 0, 2)[None]
+    tv = torch.from_numpy(v).double().permute(1, 0, 2)[None]
+    ref = F.scaled_dot_product_attention(tq, tk, tv, is_causal=True,
+                                         scale=float(oracle.default_scale(hd)), enable_gqa=True)
+    want = ref[0].permute(1, 0, 2).numpy()
+    assert rel_l2_f64(got, want) < F32_VS_F64
+
+
+def test_reference_prefill_ramp_case():
+    """attention.rs:175-202: h=2, hkv=1, s=5, hd=8 with ramp inputs."""
+    h, hkv, s, hd = 2, 1, 5, 8
+    q = ramp(h * s * hd, -0.5, 0.011).reshape(s, h, hd)
+    k = ramp(hkv * s * hd, -0.3, 0.007).reshape(s, hkv, hd)
+    v = ramp(hkv * s * hd, 0.2, 0.013).reshape(s, hkv, hd)
+    got = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    assert rel_l2_f64(got, attention_f64(q, k, v, 1 / np.sqrt(8))) < F32_VS_F64
+
+
+def test_reference_decode_ramp_case():
+    """attention.rs:205-233: h=4, hkv=2, hd=8, max_seq=16, pos=5 over ramp caches."""
+    h, hkv, hd, max_seq, pos = 4, 2, 8, 16, 5
+    q = ramp(h * hd, -0.4, 0.02)
+    kc = ramp(hkv * max_seq * hd, -0.2, 0.005)
+    vc = ramp(hkv * max_seq * hd, 0.1, 0.009)
+    got = oracle.attn_decode(q, kc, vc, h, hkv, pos, hd, max_seq)
+    k = kc.reshape(max_seq, hkv, hd)[: pos + 1]
+    v = vc.reshape(max_seq, hkv, hd)[: pos + 1]
+    want = attention_f64(q.reshape(1, h, hd), k, v, 1 / np.sqrt(8), causal=False)[0]
+    assert rel_l2_f64(got, want) < F32_VS_F64
+
+
+@pytest.mark.parametrize("h,hkv,hd,max_seq,pos", [(16, 8, 128, 300, 257), (32, 8, 128, 64, 0),
+                                                  (16, 8, 256, 40, 39)])
+def test_decode_matches_f64_textbook(h, hkv, hd, max_seq, pos):
+    q = oracle.randn((h, hd), 1)
+    kc = oracle.randn((max_seq, hkv, hd), 2)
+    vc = oracle.randn((max_seq, hkv, hd), 3)
+    got = oracle.attn_decode(q, kc, vc, h, hkv, pos, hd, max_seq)
+    want = attention_f64(q[None], kc[: pos + 1], vc[: pos + 1], 1 / np.sqrt(hd),
+                         causal=False)[0]
+    assert rel_l2_f64(got, want) < F32_VS_F64
+
+
+def test_first_row_is_v0_exactly():
+    """T=1 (and row 0 of any prefill) attends one key with weight exp(0)/exp(0) = 1."""
+    h, hkv, s, hd = 4, 2, 6, 16
+    q, k, v = (oracle.randn(sh, sd) for sh, sd in [((s, h, hd), 1), ((s, hkv, hd), 2),
+                                                   ((s, hkv, hd), 3)])
+    o = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    for hh in range(h):
+        np.testing.assert_array_equal(o[0, hh], v[0, hh // (h // hkv)])
+    od = oracle.attn_decode(q[0], k, v, h, hkv, 0, hd, s)
+    np.testing.assert_array_equal(od, o[0])
+
+
+def test_scale_zero_is_causal_prefix_mean():
+    h, hkv, s, hd = 2, 1, 9, 8
+    q, k, v = (oracle.randn(sh, sd) for sh, sd in [((s, h, hd), 1), ((s, hkv, hd), 2),
+                                                   ((s, hkv, hd), 3)])
+    o = oracle.attn_prefill(q, k, v, h, hkv, s, hd, 0.0)
+    want = np.cumsum(v.astype(np.float64), axis=0) / np.arange(1, s + 1)[:, None, None]
+    np.testing.assert_allclose(o, np.repeat(want, h, axis=1), rtol=0, atol=1e-6)
+
+
+def test_equal_keys_give_uniform_weights():
+    h, hkv, s, hd = 2, 2, 7, 8
+    q = oracle.randn((s, h, hd), 1)
+    k = np.tile(oracle.randn((1, hkv, hd), 2), (s, 1, 1))
+    v = oracle.randn((s, hkv, hd), 3)
+    o = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    want = np.cumsum(v.astype(np.float64), axis=0) / np.arange(1, s + 1)[:, None, None]
+    np.testing.assert_allclose(o, want, rtol=0, atol=2e-6)
+
+
+def test_gqa_equals_mha_with_repeated_kv():
+    h, hkv, s, hd = 8, 2, 11, 16
+    q, k, v = (oracle.randn(sh, sd) for sh, sd in [((s, h, hd), 1), ((s, hkv, hd), 2),
+                                                   ((s, hkv, hd), 3)])
+    a = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    b = oracle.attn_prefill(q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), h, h, s, hd)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_decode_equals_prefill_row_bitwise():
+    """decode(pos) over the first pos+1 cache rows is prefill row pos: the same
+    per-row arithmetic (nn/src/tests.rs:181-244 is this invariant end to end)."""
+    h, hkv, s, hd = 16, 8, 40, 128
+    q, k, v = (oracle.randn(sh, sd) for sh, sd in [((s, h, hd), 4), ((s, hkv, hd), 5),
+                                                   ((s, hkv, hd), 6)])
+    o = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    for pos in (0, 1, 17, s - 1):
+        od = oracle.attn_decode(q[pos], k, v, h, hkv, pos, hd, s)
+        np.testing.assert_array_equal(od, o[pos])
+
+
+def test_row_subset_matches_full_and_threads_do_not_change_bits():
+    h, hkv, s, hd = 16, 8, 50, 128
+    q, k, v = (oracle.randn(sh, sd) for sh, sd in [((s, h, hd), 7), ((s, hkv, hd), 8),
+                                                   ((s, hkv, hd), 9)])
+    full = oracle.attn_prefill(q, k, v, h, hkv, s, hd)
+    part = oracle.attn_prefill(q, k, v, h, hkv, s, hd, rows=(20, 13), threads=4)
+    np.testing.assert_array_equal(part[20:33], full[20:33])
+    assert np.isnan(part[:20]).all() and np.isnan(part[33:]).all()
+    par = oracle.attn_prefill(q, k, v, h, hkv, s, hd, threads=4)
+    np.testing.assert_array_equal(par, full)
+
+
+def test_default_scale_is_reference_value():
+    for hd in (4, 8, 64, 128, 256):
+        assert np.float32(oracle.default_scale(hd)) == np.float32(1.0) / np.sqrt(np.float32(hd))
+
+
+# ------------------------------------------------------------------ kv_write -------------
+
+def test_kv_write_reference_known_answer():
+    """ops.rs:271-292: hkv=2, hd=4, max_seq=8, src[i]=i+1 written at dst=3."""
+    hkv, hd, max_seq = 2, 4, 8
+    cache = np.zeros(max_seq * hkv * hd, np.float32)
+    src = np.arange(hkv * hd, dtype=np.float32) + 1
+    got = oracle.kv_write(cache, src, hkv, 1, hd, 3)
+    for head in range(hkv):
+        for d in range(hd):
+            assert got[(3 * hkv + head) * hd + d] == src[head * hd + d]
+    assert got[0] == 0.0
+    # closed form: a contiguous copy to element offset dst * hkv * hd
+    want = cache.copy()
+    want[3 * hkv * hd: 4 * hkv * hd] = src
+    np.testing.assert_array_equal(got, want)
+
+
+def test_kv_write_is_contiguous_block_copy():
+    hkv, hd, max_seq, count, dst = 8, 128, 64, 13, 40
+    cache = oracle.randn((max_seq * hkv * hd,), 1)
+    src = oracle.randn((count * hkv * hd,), 2)
+    got = oracle.kv_write(cache, src, hkv, count, hd, dst)
+    want = cache.copy()
+    want[dst * hkv * hd:(dst + count) * hkv * hd] = src
+    assert got.tobytes() == want.tobytes()
+
+
+# ------------------------------------------------------------------ RMSNorm / RoPE -------
+
+def test_rmsnorm_reference_case_and_f64():
+    """rmsnorm.rs:72-90 inputs (rows 3, dim 320), checked against float64."""
+    rows, dim, eps = 3, 320, 1e-6
+    x = (np.arange(rows * dim) % 17).astype(np.float32) * np.float32(0.05) - np.float32(0.4)
+    w = np.float32(1.0) + np.arange(dim, dtype=np.float32) * np.float32(0.001)
+    got = oracle.rmsnorm(x, w, rows, dim, eps)
+    assert rel_l2_f64(got, rmsnorm_f64(x, w, dim, eps)) < 1e-6
+    x2 = oracle.randn((40 * 256,), 3)
+    w2 = (1 + 0.1 * oracle.randn((256,), 4)).astype(np.float32)
+    got2 = oracle.rmsnorm(x2, w2, 40, 256, 1e-6)
+    assert rel_l2_f64(got2, rmsnorm_f64(x2, w2, 256, 1e-6)) < 1e-6
+
+
+def test_rmsnorm_unit_weight_gives_unit_rms():
+    x = oracle.randn((10 * 128,), 5) * 3
+    y = oracle.rmsnorm(x, np.ones(128, np.float32), 10, 128, 0.0).reshape(10, 128)
+    np.testing.assert_allclose(np.sqrt((y.astype(np.float64) ** 2).mean(axis=1)), 1.0, atol=1e-6)
+
+
+def test_rope_tables_reference_cases():
+    """nn/src/tests.rs:152-177 (row 0 is (1, 0); row 3 matches f64) and the partial-table
+    test nn/src/rope.rs:82-104 (first rope_angles pairs equal the full table, rest 1/0)."""
+    c, s = oracle.rope_tables(8, 4, 10000.0)
+    np.testing.assert_array_equal(c[0], 1.0)
+    np.testing.assert_array_equal(s[0], 0.0)
+    k = np.arange(2)
+    ang = 3 * np.power(10000.0, -2.0 * k / 4)
+    np.testing.assert_allclose(c[3], np.cos(ang), atol=1e-7)
+    np.testing.assert_allclose(s[3], np.sin(ang), atol=1e-7)
+    fc, fs = oracle.rope_tables(5, 8, 10000.0)
+    pc, ps = oracle.rope_tables(5, 8, 10000.0, rope_angles=2)
+    np.testing.assert_array_equal(pc[:, :2], fc[:, :2])
+    np.testing.assert_array_equal(ps[:, :2], fs[:, :2])
+    np.testing.assert_array_equal(pc[:, 2:], 1.0)
+    np.testing.assert_array_equal(ps[:, 2:], 0.0)
+
+
+def test_gemma_partial_rope_tables():
+    """Gemma global layers: rope_angles = floor(0.25 * 256 / 2) = 32, theta 1e6
+    (models/gemma4.rs:157-165). Pairs >= 32 are exactly (1, 0)."""
+    c, s = oracle.rope_tables(300, 256, 1e6, rope_angles=32)
+    p = np.arange(128)
+    ang = np.arange(300)[:, None] * np.power(1e6, -2.0 * p / 256)[None, :]
+    np.testing.assert_allclose(c[:, :32], np.cos(ang[:, :32]), atol=2e-7)
+    np.testing.assert_allclose(s[:, :32], np.sin(ang[:, :32]), atol=2e-7)
+    assert (c[:, 32:] == 1.0).all() and (s[:, 32:] == 0.0).all()
+
+
+def test_rope_reference_case_and_f64():
+    """rope.rs:92-111: seq 4, 2 heads, hd 8, theta 1e4, x = i*0.03 - 0.5; plus base_pos."""
+    seq, nh, hd = 4, 2, 8
+    x = np.arange(seq * nh * hd, dtype=np.float32) * np.float32(0.03) - np.float32(0.5)
+    c, s = oracle.rope_tables(16, hd, 10000.0)
+    got = oracle.rope(x, c, s, seq, nh, hd)
+    assert rel_l2_f64(got, rope_f64(x, seq, nh, hd, 10000.0)) < 1e-6
+    got5 = oracle.rope(x, c, s, seq, nh, hd, base_pos=5)
+    assert rel_l2_f64(got5, rope_f64(x, seq, nh, hd, 10000.0, base_pos=5)) < 1e-6
+    # partial rotary leaves pass-through dims bit-identical
+    x2 = oracle.randn((6 * 2 * 256,), 8)
+    c2, s2 = oracle.rope_tables(10, 256, 1e6, rope_angles=32)
+    y2 = oracle.rope(x2, c2, s2, 6, 2, 256, base_pos=3).reshape(6, 2, 256)
+    x2r = x2.reshape(6, 2, 256)
+    np.testing.assert_array_equal(y2[..., 32:128], x2r[..., 32:128])
+    np.testing.assert_array_equal(y2[..., 160:], x2r[..., 160:])
+    assert rel_l2_f64(y2, rope_f64(x2, 6, 2, 256, 1e6, rope_angles=32, base_pos=3)) < 1e-6
+
+
+def test_rope_preserves_pair_norms():
+    x = oracle.randn((5 * 3 * 64,), 9)
+    c, s = oracle.rope_tables(5, 64, 10000.0)
+    y = oracle.rope(x, c, s, 5, 3, 64).reshape(5, 3, 64).astype(np.float64)
+    xr = x.reshape(5, 3, 64).astype(np.float64)
+    n_in = xr[..., :32] ** 2 + xr[..., 32:] ** 2
+    n_out = y[..., :32] ** 2 + y[..., 32:] ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------ helpers ----------------
+
+def test_rel_l2_closed_form():
+    a = np.array([1.0, 2.0, 3.0], np.float32)
+    b = np.array([1.0, 2.0, 5.0], np.float32)
+    assert abs(oracle.rel_l2(a, b) - 2.0 / (np.sqrt(30.0) + 1e-12)) < 1e-7
+    assert oracle.rel_l2(b, b) == 0.0
+
+
+def test_prng_range_and_moments():
+    x = oracle.prng(1 << 20, 0).astype(np.float64)
+    assert x.min() >= -1.0 and x.max() < 1.0
+    assert abs(x.mean()) < 3e-3 and abs(x.var() - 1 / 3) < 3e-3
+    assert not np.array_equal(oracle.prng(16, 1), oracle.prng(16, 2))
+    np.testing.assert_array_equal(oracle.prng(16, 7), oracle.prng(32, 7)[:16])
+
+
+def test_randn_is_standard_normal():
+    scipy_stats = pytest.importorskip("scipy.stats")
+    z = oracle.randn((1 << 18,), 3).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
+    assert scipy_stats.kstest(z, "norm").pvalue > 1e-3
+    assert np.isfinite(z).all()
+
+
+# ------------------------------------------------------------------ mutation test ----------
+
+@pytest.mark.parametrize("plant", [1, 2, 3, 4])
+def test_checks_reject_planted_oracle_mistakes(plant):
+    """Build the oracle with a planted mistake (GQA grouping, causal diagonal, scale,
+    V read from K) and show the float64 textbook check above rejects it."""
+    src = os.path.join(os.path.dirname(oracle.__file__), "oracle.c")
+    with tempfile.TemporaryDirectory() as td:
+        so = os.path.join(td, f"planted{plant}.so")
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fPIC", "-shared", "-fopenmp",
+                        f"-DEBO_PLANT={plant}", "-o", so, src, "-lm"], check=True)
+        lib = ctypes.CDLL(so)
+        f32p = ctypes.POINTER(ctypes.c_float)
+        sz = ctypes.c_size_t
+        lib.ebo_attn_prefill_rows.argtypes = [f32p, f32p, f32p, f32p, sz, sz, sz, sz,
+                                              ctypes.c_float, sz, sz, ctypes.c_int]
+        h, hkv, s, hd = 4, 2, 9, 16
+        q, k, v = (oracle.randn(sh, sd) for sh, sd in [((s, h, hd), 1), ((s, hkv, hd), 2),
+                                                       ((s, hkv, hd), 3)])
+        o = np.empty((s, h, hd), np.float32)
+        sc = 0.25
+        p = lambda a: a.ctypes.data_as(f32p)  # noqa: E731
+        lib.ebo_attn_prefill_rows(p(q), p(k), p(v), p(o), h, hkv, s, hd, sc, 0, s, 1)
+        assert rel_l2_f64(o, attention_f64(q, k, v, sc)) > 1e-3
