@@ -11,15 +11,16 @@ reference's Rust interface:
 from ._lib import LIB_PATH, lib
 from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, OutOfMemory,
                   Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
-from .kernels import (attn_decode, attn_decode_workspace_floats, attn_prefill, kv_write,
-                      launch_attn_decode, launch_attn_prefill, launch_kv_write, launch_rmsnorm,
-                      launch_rope, rmsnorm, rope)
+from .kernels import (attn_decode, attn_decode_step, attn_decode_workspace_floats, attn_prefill,
+                      kv_write, launch_attn_decode, launch_attn_decode_step,
+                      launch_attn_prefill, launch_kv_write, launch_rmsnorm, launch_rope, rmsnorm,
+                      rope)
 from .nn import Attention, KvCache, Rope
 
 __all__ = [
     "LIB_PATH", "lib", "DType", "Device", "DeviceUnavailable", "EyebrowseError", "LoadError",
     "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
-    "attn_decode_workspace_floats", "attn_prefill", "kv_write", "launch_attn_decode",
+    "attn_decode_step", "launch_attn_decode_step", "attn_decode_workspace_floats", "attn_prefill", "kv_write", "launch_attn_decode",
     "launch_attn_prefill", "launch_kv_write", "launch_rmsnorm", "launch_rope", "rmsnorm", "rope",
     "Attention", "KvCache", "Rope",
 ]

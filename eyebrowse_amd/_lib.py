@@ -67,6 +67,8 @@ SIGNATURES = {
                                c_float]),
     "eb_attn_decode": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size,
                               c_size, c_float]),
+    "eb_attn_decode_step": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size,
+                                   c_size, c_size, c_size, c_float]),
     "eb_kv_write": (c_st, [c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size, c_size]),
     "eb_rmsnorm": (c_st, [c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_float]),
     "eb_rope": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size]),
@@ -78,6 +80,9 @@ SIGNATURES = {
     "eb_launch_attn_decode": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
                                      c_size, c_size, c_size, c_size, c_size, c_size, c_float,
                                      c_vp, c_size, c_int]),
+    "eb_launch_attn_decode_step": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size,
+                                          c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
+                                          c_size, c_size, c_float, c_vp, c_size, c_int]),
     "eb_launch_rmsnorm": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
                                  c_size, c_float]),
     "eb_launch_rope": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size, c_size,

@@ -2,24 +2,32 @@
 // cache [max_seq, Hkv, HD], then a log-sum-exp merge.
 //
 // Replaces attn_decode (crates/eyebrowse-kernels/src/attention.rs:52-90,124-162), which
-// runs one thread per query head and streams the whole cache serially. Here the keys
-// 0..=pos are cut into chunks; one 256-thread workgroup reduces one chunk for one KV head
-// and the G query heads that share it (GQA: every K/V row is read once for all of them).
+// runs one thread per query head and streams the whole cache serially, and optionally
+// folds in the two kv_write calls that precede it in Attention::decode
+// (crates/eyebrowse-nn/src/attention.rs:149-183).
 //
-// Pass 1 (decode_split_kernel), per workgroup:
+// Pass 1, grid (Hkv * nsub) x nsplit, 256 threads per workgroup. Workgroup (col, split)
+// reduces keys [split*chunk, min((split+1)*chunk, pos+1)) for KV head col/nsub and the G
+// query heads that share it (GQA: every K/V row is read once for all of them):
 //  - a key row of HD floats is spread over LPK = HD/DPL lanes (DPL = 16 dims per lane),
-//    so a wave covers KPW = 64/LPK keys per step; the loads are 128-bit and each
-//    instruction's lanes cover contiguous 64-byte..1-KiB spans of the row;
+//    so a wave covers KPW = 64/LPK keys per step; loads are 128-bit and each instruction's
+//    lanes cover contiguous spans of the row;
 //  - scores are lane-partial dot products summed across the LPK lanes with DPP;
-//  - every lane group keeps an online softmax (running max m, sum l, acc[DPL]) in the
-//    log2 domain (scores pre-multiplied by scale*log2(e), exponentials via v_exp_f32),
-//    updating once per U keys;
-//  - at the end the groups of a wave merge with lane shuffles, the 4 waves merge through
-//    LDS, and the workgroup writes either the final row (one split) or its partial
-//    (m, l, acc[HD]) per query head to the workspace.
-// Pass 2 (decode_merge_kernel): o[h] = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+//  - each lane group keeps an online softmax (running max m, sum l, acc[DPL]) in the log2
+//    domain (scores times scale*log2(e), exponentials on v_exp_f32), updated once per U
+//    keys;
+//  - the wave's lane groups merge with shuffles, the 4 waves merge through LDS;
+//  - with one split the workgroup writes o directly; otherwise it writes its partial
+//    (m, l, acc[HD]) per head and pass 2 (decode_merge_kernel) computes
+//    o = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M). A second launch is cheaper here
+//    than merging in the last-arriving workgroup: on the 8-XCD part that needs an L2
+//    write-back fence in every workgroup.
+// Fused new-token write: when knew/vnew are given, key `pos` is read from them instead of
+// the cache, and the workgroup whose chunk holds `pos` (first head-subgroup) copies them
+// into cache row `pos`; nothing else touches that row in the launch, so the copy is exact
+// and race free.
 //
-// The result equals softmax(scale * q K^T) V over keys 0..=pos; it differs from the
+// The result is softmax(scale * q K^T) V over keys 0..=pos; it differs from the
 // reference's 3-pass f32 softmax only by rounding (summation order, exp2 vs expf).
 #include "eb_common.h"
 #include "eb_internal.h"
@@ -27,19 +35,26 @@
 #include <algorithm>
 #include <cstdlib>
 
+// Wave steps per softmax update: 4 when at most 2 query heads share a workgroup, else 2
+// (register budget: the q fragment and accumulators grow with the head count). A
+// positive EB_DECODE_U forces one value for all shapes.
+#ifndef EB_DECODE_U
+#define EB_DECODE_U 0
+#endif
+
 namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kMaxSplits = 1024;
+constexpr int kMaxSplits = 256;  // per column; bounds the merge's LDS weights
 
-template <int HD>
+template <int HD, int G>
 struct DecodeShape {
     static constexpr int DPL = HD >= 16 ? 16 : HD;  // dims per lane
     static constexpr int LPK = HD / DPL;            // lanes per key row
     static constexpr int KPW = 64 / LPK;            // keys per wave step
     static constexpr int NV4 = DPL / 4;             // float4 loads per lane per row
-    static constexpr int U = 2;                     // wave steps per softmax update
+    static constexpr int U = EB_DECODE_U > 0 ? EB_DECODE_U : (G <= 2 ? 4 : 2);
     static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
     static_assert(DPL % 4 == 0 && LPK <= 16, "head_dim must be a multiple of 4, at most 256");
 };
@@ -47,34 +62,61 @@ struct DecodeShape {
 // Element offset (within a row) of float4 number i held by dim slice `ls`.
 template <int HD>
 __device__ __forceinline__ int dim_of(int i, int ls) {
-    return (i * DecodeShape<HD>::LPK + ls) * 4;
+    return (i * DecodeShape<HD, 1>::LPK + ls) * 4;
 }
 
+struct DecodeArgs {
+    const float *q;
+    const float *kc;   // cache rows read (and row `pos` written when knew != null)
+    const float *vc;
+    float *kc_w;       // same as kc, writable
+    float *vc_w;
+    const float *knew; // [Hkv, HD] new token K (or null)
+    const float *vnew;
+    float *o;
+    float *part_acc;   // [nsplit, h, HD]
+    float *part_ml;    // [nsplit, h, 2]
+    int h, hkv, g, keys, chunk, nsplit;
+    float scale_log2;
+};
+
 template <int HD, int G>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(
-    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
-    float *__restrict__ o, float *__restrict__ part_acc, float *__restrict__ part_ml, int h,
-    int hkv, int g, int keys, int chunk, int nsplit, float scale_log2) {
-    using S = DecodeShape<HD>;
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+    using S = DecodeShape<HD, G>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int nsub = g / G;
-    const int kvh = blockIdx.x / nsub;
-    const int head0 = kvh * g + (blockIdx.x % nsub) * G;
+    const int nsub = a.g / G;
+    const int col = blockIdx.x;
+    const int kvh = col / nsub;
+    const int head0 = kvh * a.g + (col % nsub) * G;
     const int split = blockIdx.y;
-    const int c0 = split * chunk;
-    const int c1 = min(c0 + chunk, keys);
+    const int c0 = split * a.chunk;
+    const int c1 = min(c0 + a.chunk, a.keys);
     const int kg = lane / S::LPK;
     const int ls = lane % S::LPK;
+    const int pos = a.keys - 1;
+    const bool has_new = a.knew != nullptr;
+    const size_t row_stride = (size_t)a.hkv * HD;
+
+    // New-token write: one workgroup per KV head copies the row into the cache.
+    if (has_new && (col % nsub) == 0 && pos >= c0 && pos < c1) {
+        for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
+            const size_t dst = (size_t)pos * row_stride + (size_t)kvh * HD + 4 * i;
+            *reinterpret_cast<float4 *>(a.kc_w + dst) =
+                *reinterpret_cast<const float4 *>(a.knew + (size_t)kvh * HD + 4 * i);
+            *reinterpret_cast<float4 *>(a.vc_w + dst) =
+                *reinterpret_cast<const float4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
+        }
+    }
 
     float qr[G][S::DPL];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
         for (int i = 0; i < NV4; ++i) {
-            float4 t = *reinterpret_cast<const float4 *>(q + (size_t)(head0 + gi) * HD +
+            float4 t = *reinterpret_cast<const float4 *>(a.q + (size_t)(head0 + gi) * HD +
                                                          dim_of<HD>(i, ls));
             qr[gi][4 * i + 0] = t.x;
             qr[gi][4 * i + 1] = t.y;
@@ -91,20 +133,23 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
         for (int d = 0; d < S::DPL; ++d) acc[gi][d] = 0.0f;
     }
 
-    const size_t row_stride = (size_t)hkv * HD;
-    const float *kbase = kc + (size_t)kvh * HD;
-    const float *vbase = vc + (size_t)kvh * HD;
+    const float *kbase = a.kc + (size_t)kvh * HD;
+    const float *vbase = a.vc + (size_t)kvh * HD;
 
     for (int base = c0; base < c1; base += S::KEYS_PER_ITER) {
         float4 kv[U][NV4], vv[U][NV4];
         bool valid[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            int key = base + (u * kWaves + wave) * S::KPW + kg;
+            const int key = base + (u * kWaves + wave) * S::KPW + kg;
             valid[u] = key < c1;
-            int kk = valid[u] ? key : c1 - 1;
+            const int kk = valid[u] ? key : c1 - 1;
             const float *kp = kbase + (size_t)kk * row_stride;
             const float *vp = vbase + (size_t)kk * row_stride;
+            if (has_new && kk == pos) {
+                kp = a.knew + (size_t)kvh * HD;
+                vp = a.vnew + (size_t)kvh * HD;
+            }
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
                 kv[u][i] = *reinterpret_cast<const float4 *>(kp + dim_of<HD>(i, ls));
@@ -125,14 +170,14 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
                     s += qr[gi][4 * i + 3] * kv[u][i].w;
                 }
                 s = eb::group_sum<S::LPK>(s);
-                sc[u] = valid[u] ? s * scale_log2 : -INFINITY;
+                sc[u] = valid[u] ? s * a.scale_log2 : -INFINITY;
             }
             float mloc = sc[0];
 #pragma unroll
             for (int u = 1; u < U; ++u) mloc = fmaxf(mloc, sc[u]);
-            float mnew = fmaxf(m[gi], mloc);
-            float mref = (mnew == -INFINITY) ? 0.0f : mnew;
-            float corr = eb::fast_exp2(m[gi] - mref);
+            const float mnew = fmaxf(m[gi], mloc);
+            const float mref = (mnew == -INFINITY) ? 0.0f : mnew;
+            const float corr = eb::fast_exp2(m[gi] - mref);
             float p[U];
             float psum = 0.0f;
 #pragma unroll
@@ -167,8 +212,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
         float M = m[gi];
 #pragma unroll
         for (int off = S::LPK; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
-        float mref = (M == -INFINITY) ? 0.0f : M;
-        float sc = eb::fast_exp2(m[gi] - mref);
+        const float mref = (M == -INFINITY) ? 0.0f : M;
+        const float sc = eb::fast_exp2(m[gi] - mref);
         float L = l[gi] * sc;
 #pragma unroll
         for (int off = S::LPK; off < 64; off <<= 1) L += __shfl_xor(L, off);
@@ -176,10 +221,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
         m[gi] = M;
 #pragma unroll
         for (int d = 0; d < S::DPL; ++d) {
-            float a = acc[gi][d] * sc;
+            float x = acc[gi][d] * sc;
 #pragma unroll
-            for (int off = S::LPK; off < 64; off <<= 1) a += __shfl_xor(a, off);
-            acc[gi][d] = a;
+            for (int off = S::LPK; off < 64; off <<= 1) x += __shfl_xor(x, off);
+            acc[gi][d] = x;
         }
     }
 
@@ -207,85 +252,118 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(
         float M = s_m[0][gi];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][gi]);
-        float mref = (M == -INFINITY) ? 0.0f : M;
+        const float mref = (M == -INFINITY) ? 0.0f : M;
         float L = 0.0f, A = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            float sc = eb::fast_exp2(s_m[w][gi] - mref);
+            const float sc = eb::fast_exp2(s_m[w][gi] - mref);
             L += s_l[w][gi] * sc;
             A += s_acc[w][gi][d] * sc;
         }
         const int hh = head0 + gi;
-        if (nsplit == 1) {
-            o[(size_t)hh * HD + d] = A / L;
+        if (a.nsplit == 1) {
+            a.o[(size_t)hh * HD + d] = A / L;
         } else {
-            part_acc[((size_t)split * h + hh) * HD + d] = A;
+            a.part_acc[((size_t)split * a.h + hh) * HD + d] = A;
             if (d == 0) {
-                part_ml[((size_t)split * h + hh) * 2 + 0] = M;
-                part_ml[((size_t)split * h + hh) * 2 + 1] = L;
+                a.part_ml[((size_t)split * a.h + hh) * 2 + 0] = M;
+                a.part_ml[((size_t)split * a.h + hh) * 2 + 1] = L;
             }
         }
     }
 }
 
-// One block per query head: log-sum-exp merge of the split partials.
+// Log-sum-exp merge of the split partials (a second launch, so the partials written by
+// every XCD are visible without in-kernel fences): one 256-thread block per query head.
+// Phase A: the split maxima and weights w_s = 2^(m_s - M), L = sum_s w_s l_s; phase B:
+// 256/HD groups of HD threads sum disjoint split subsets of acc_s[d] * w_s, combined
+// through LDS; o[h][d] = A / L.
 template <int HD>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float *__restrict__ part_acc,
-                                                           const float *__restrict__ part_ml,
-                                                           float *__restrict__ o, int h,
-                                                           int nsplit) {
+__global__ __launch_bounds__(kThreads) void decode_merge_kernel(const float *__restrict__ part_acc,
+                                                                const float *__restrict__ part_ml,
+                                                                float *__restrict__ o, int h,
+                                                                int nsplit) {
+    constexpr int GROUPS = HD >= kThreads ? 1 : kThreads / HD;
     __shared__ float s_w[kMaxSplits];
-    __shared__ float s_red[256];
+    __shared__ float s_red[kWaves];
+    __shared__ float s_part[GROUPS][HD];
     const int hh = blockIdx.x;
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
 
-    float M = -INFINITY;
-    for (int s = tid; s < nsplit; s += 256) M = fmaxf(M, part_ml[((size_t)s * h + hh) * 2]);
-    s_red[tid] = M;
+    const bool has = tid < nsplit;
+    const float m = has ? part_ml[((size_t)tid * h + hh) * 2] : -INFINITY;
+    const float lv = has ? part_ml[((size_t)tid * h + hh) * 2 + 1] : 0.0f;
+    float M = m;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (lane == 0) s_red[wave] = M;
     __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
-        if (tid < stride) s_red[tid] = fmaxf(s_red[tid], s_red[tid + stride]);
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float mref = (M == -INFINITY) ? 0.0f : M;
+    const float w = has ? eb::fast_exp2(m - mref) : 0.0f;
+    if (tid < kMaxSplits) s_w[tid] = w;
+    float L = w * lv;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
+    __syncthreads();
+    if (lane == 0) s_red[wave] = L;
+    __syncthreads();
+    L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+
+    for (int d0 = 0; d0 < HD; d0 += kThreads) {
+        const int d = d0 + tid % HD;
+        const int grp = tid / HD;
+        float A0 = 0.0f, A1 = 0.0f;
+        if (grp < GROUPS && d < HD) {
+            const float *pa = part_acc + (size_t)hh * HD + d;
+            const size_t stride = (size_t)h * HD;
+            int s = grp;
+            for (; s + GROUPS < nsplit; s += 2 * GROUPS) {
+                A0 += pa[(size_t)s * stride] * s_w[s];
+                A1 += pa[(size_t)(s + GROUPS) * stride] * s_w[s + GROUPS];
+            }
+            if (s < nsplit) A0 += pa[(size_t)s * stride] * s_w[s];
+            s_part[grp][tid % HD] = A0 + A1;
+        }
         __syncthreads();
-    }
-    M = s_red[0];
-    __syncthreads();
-    float mref = (M == -INFINITY) ? 0.0f : M;
-    float L = 0.0f;
-    for (int s = tid; s < nsplit; s += 256) {
-        float w = eb::fast_exp2(part_ml[((size_t)s * h + hh) * 2] - mref);
-        s_w[s] = w;
-        L += w * part_ml[((size_t)s * h + hh) * 2 + 1];
-    }
-    s_red[tid] = L;
-    __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
-        if (tid < stride) s_red[tid] += s_red[tid + stride];
+        if (tid < HD && d0 + tid < HD) {
+            float A = 0.0f;
+#pragma unroll
+            for (int g2 = 0; g2 < GROUPS; ++g2) A += s_part[g2][tid];
+            o[(size_t)hh * HD + d0 + tid] = A / L;
+        }
         __syncthreads();
-    }
-    L = s_red[0];
-    for (int d = tid; d < HD; d += 256) {
-        float A = 0.0f;
-        for (int s = 0; s < nsplit; ++s) A += part_acc[((size_t)s * h + hh) * HD + d] * s_w[s];
-        o[(size_t)hh * HD + d] = A / L;
     }
 }
 
 struct DecodePlan {
-    int G = 1;       // query heads per workgroup (a power of two dividing h/hkv)
+    int G = 1;       // query heads per workgroup (a power of two dividing h/hkv, <= 8)
     int nsub = 1;    // workgroups per KV head along the head axis
     int chunk = 0;   // keys per split
     int nsplit = 1;  // splits along the key axis
 };
 
-int keys_per_iter(size_t hd) {
+template <int G>
+int keys_per_iter_g(size_t hd) {
     switch (hd) {
-        case 4: return DecodeShape<4>::KEYS_PER_ITER;
-        case 8: return DecodeShape<8>::KEYS_PER_ITER;
-        case 16: return DecodeShape<16>::KEYS_PER_ITER;
-        case 32: return DecodeShape<32>::KEYS_PER_ITER;
-        case 64: return DecodeShape<64>::KEYS_PER_ITER;
-        case 128: return DecodeShape<128>::KEYS_PER_ITER;
-        default: return DecodeShape<256>::KEYS_PER_ITER;
+        case 4: return DecodeShape<4, G>::KEYS_PER_ITER;
+        case 8: return DecodeShape<8, G>::KEYS_PER_ITER;
+        case 16: return DecodeShape<16, G>::KEYS_PER_ITER;
+        case 32: return DecodeShape<32, G>::KEYS_PER_ITER;
+        case 64: return DecodeShape<64, G>::KEYS_PER_ITER;
+        case 128: return DecodeShape<128, G>::KEYS_PER_ITER;
+        default: return DecodeShape<256, G>::KEYS_PER_ITER;
+    }
+}
+
+int keys_per_iter(size_t hd, int G) {
+    switch (G) {
+        case 8: return keys_per_iter_g<8>(hd);
+        case 4: return keys_per_iter_g<4>(hd);
+        case 2: return keys_per_iter_g<2>(hd);
+        default: return keys_per_iter_g<1>(hd);
     }
 }
 
@@ -293,8 +371,8 @@ int keys_per_iter(size_t hd) {
 int wgs_per_cu() {
     static int v = [] {
         const char *e = std::getenv("EB_DECODE_WGS_PER_CU");
-        int x = e ? std::atoi(e) : 2;
-        return (x >= 1 && x <= 64) ? x : 2;
+        int x = e ? std::atoi(e) : 1;
+        return (x >= 1 && x <= 64) ? x : 1;
     }();
     return v;
 }
@@ -306,9 +384,9 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     p.nsub = (int)(g / p.G);
     const size_t keys = pos + 1;
     const size_t cols = hkv * (size_t)p.nsub;
-    const size_t kpi = (size_t)keys_per_iter(hd);
-    size_t target = (size_t)cu_count * (size_t)wgs_per_cu();
-    size_t want = std::max<size_t>(1, target / cols);
+    const size_t kpi = (size_t)keys_per_iter(hd, p.G);
+    const size_t target = (size_t)cu_count * (size_t)wgs_per_cu();
+    const size_t want = std::max<size_t>(1, target / cols);
     size_t chunk = (keys + want - 1) / want;
     chunk = std::max(kpi, (chunk + kpi - 1) / kpi * kpi);
     size_t nsplit = (keys + chunk - 1) / chunk;
@@ -323,34 +401,30 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
 }
 
 template <int HD, int G>
-void launch_split(hipStream_t st, const DecodePlan &p, const float *q, const float *kc,
-                  const float *vc, float *o, float *pacc, float *pml, int h, int hkv, int g,
-                  int keys, float scale_log2) {
-    dim3 grid((unsigned)(hkv * p.nsub), (unsigned)p.nsplit);
-    decode_split_kernel<HD, G><<<grid, kThreads, 0, st>>>(q, kc, vc, o, pacc, pml, h, hkv, g, keys,
-                                                          p.chunk, p.nsplit, scale_log2);
+void launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+    dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
+    decode_kernel<HD, G><<<grid, kThreads, 0, st>>>(a);
 }
 
 template <int HD>
-void launch_hd(hipStream_t st, const DecodePlan &p, const float *q, const float *kc,
-               const float *vc, float *o, float *ws, int h, int hkv, int keys, float scale_log2) {
-    const int g = h / hkv;
-    float *pacc = ws;
-    float *pml = ws ? ws + (size_t)p.nsplit * h * HD : nullptr;
+void launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     switch (p.G) {
-        case 8: launch_split<HD, 8>(st, p, q, kc, vc, o, pacc, pml, h, hkv, g, keys, scale_log2); break;
-        case 4: launch_split<HD, 4>(st, p, q, kc, vc, o, pacc, pml, h, hkv, g, keys, scale_log2); break;
-        case 2: launch_split<HD, 2>(st, p, q, kc, vc, o, pacc, pml, h, hkv, g, keys, scale_log2); break;
-        default: launch_split<HD, 1>(st, p, q, kc, vc, o, pacc, pml, h, hkv, g, keys, scale_log2); break;
+        case 8: launch_g<HD, 8>(st, p, a); break;
+        case 4: launch_g<HD, 4>(st, p, a); break;
+        case 2: launch_g<HD, 2>(st, p, a); break;
+        default: launch_g<HD, 1>(st, p, a); break;
     }
     if (p.nsplit > 1)
-        decode_merge_kernel<HD><<<(unsigned)h, 256, 0, st>>>(pacc, pml, o, h, p.nsplit);
+        decode_merge_kernel<HD><<<(unsigned)a.h, kThreads, 0, st>>>(a.part_acc, a.part_ml, a.o,
+                                                                    a.h, p.nsplit);
 }
 
 }  // namespace
 
 namespace eb {
 
+// Workspace layout (floats): part_acc [nsplit*h*hd] | part_ml [nsplit*h*2]. Every split
+// writes its whole partial before the merge reads it, so no initialisation is needed.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count) {
     DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count);
     if (p.nsplit <= 1) return 0;
@@ -358,21 +432,45 @@ size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int 
 }
 
 eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
+                             float *kc_w, float *vc_w, const float *knew, const float *vnew,
                              float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                              float scale, float *ws, size_t ws_floats, int cu_count) {
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
+         reinterpret_cast<uintptr_t>(vc) | reinterpret_cast<uintptr_t>(knew) |
+         reinterpret_cast<uintptr_t>(vnew)) & 15)
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: q/caches/new rows must be 16-byte aligned");
     DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count);
-    if (p.nsplit > 1 && (ws == nullptr || ws_floats < (size_t)p.nsplit * h * (hd + 2)))
+    const size_t need = decode_workspace_floats(h, hkv, pos, hd, cu_count);
+    if (need > 0 && (ws == nullptr || ws_floats < need))
         return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace too small");
-    const float sl2 = scale * kLog2e;
-    const int hi = (int)h, hk = (int)hkv, keys = (int)(pos + 1);
+    DecodeArgs a{};
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.kc_w = kc_w;
+    a.vc_w = vc_w;
+    a.knew = knew;
+    a.vnew = vnew;
+    a.o = o;
+    if (ws) {
+        a.part_acc = ws;
+        a.part_ml = ws + (size_t)p.nsplit * h * hd;
+    }
+    a.h = (int)h;
+    a.hkv = (int)hkv;
+    a.g = (int)(h / hkv);
+    a.keys = (int)(pos + 1);
+    a.chunk = p.chunk;
+    a.nsplit = p.nsplit;
+    a.scale_log2 = scale * kLog2e;
     switch (hd) {
-        case 4: launch_hd<4>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
-        case 8: launch_hd<8>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
-        case 16: launch_hd<16>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
-        case 32: launch_hd<32>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
-        case 64: launch_hd<64>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
-        case 128: launch_hd<128>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
-        case 256: launch_hd<256>(st, p, q, kc, vc, o, ws, hi, hk, keys, sl2); break;
+        case 4: launch_hd<4>(st, p, a); break;
+        case 8: launch_hd<8>(st, p, a); break;
+        case 16: launch_hd<16>(st, p, a); break;
+        case 32: launch_hd<32>(st, p, a); break;
+        case 64: launch_hd<64>(st, p, a); break;
+        case 128: launch_hd<128>(st, p, a); break;
+        case 256: launch_hd<256>(st, p, a); break;
         default: return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);
     }
     return check_launch("attn_decode");

@@ -50,8 +50,12 @@ eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale);
+// Decode workspace: part_acc [nsplit*h*hd] | part_ml [nsplit*h*2], no initialisation.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count);
+// knew/vnew null: plain attention over keys 0..=pos. Otherwise key `pos` comes from
+// knew/vnew ([hkv, hd]) and is also written to cache row `pos` through kc_w/vc_w.
 eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
+                             float *kc_w, float *vc_w, const float *knew, const float *vnew,
                              float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                              float scale, float *ws, size_t ws_floats, int cu_count);
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,

@@ -242,19 +242,20 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
     EB_TRY(eb_rope_apply(rope, rec, kn, rows, Hkv, base_pos, &kr_t));
     Owned kr(kr_t);
 
-    EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
-    EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
-
     const size_t oshape[2] = {rows, H * hd};
     eb_tensor *o_t = nullptr;
     EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape, 2, EB_F32, &o_t));
     Owned o(o_t);
     if (prefill) {
-        // attention.rs:104-115 attends the fresh kr / v, not the cache.
+        // attention.rs:78-97 writes the prompt's K (post-RoPE) and V into the cache, and
+        // :104-115 attends the fresh kr / v, not the cache.
+        EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, 0));
+        EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, 0));
         EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
     } else {
-        EB_TRY(eb_attn_decode(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, hd, kv->max_seq,
-                              d.scale));
+        // attention.rs:149-183: kv_write K and V at pos, then attn_decode, as one launch.
+        EB_TRY(eb_attn_decode_step(rec, qr.t, kr.t, vn, kc, vc, o.t, H, Hkv, base_pos, hd,
+                                   kv->max_seq, d.scale));
     }
     *out = o.release();
     return eb::ok();

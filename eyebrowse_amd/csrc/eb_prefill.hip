@@ -30,7 +30,16 @@
 #include "eb_common.h"
 #include "eb_internal.h"
 
+#include <cstdlib>
 #include <mutex>
+#include <string>
+
+// Workgroups the compiler must fit per CU for head_dim <= 128 (bounds registers per wave:
+// 2 four-wave workgroups = 2 waves per SIMD). head_dim 256 keeps one: its Q fragment and
+// O^T accumulators alone take 256 registers per lane.
+#ifndef EB_PREFILL_MIN_BLOCKS
+#define EB_PREFILL_MIN_BLOCKS 2
+#endif
 
 namespace {
 
@@ -53,13 +62,25 @@ struct PrefillShape {
     static constexpr size_t LDS_BYTES = (size_t)(2 * kTile * KS + 2 * kTile * HD) * sizeof(float);
 };
 
+// Query block processed by workgroup `flat`. Rank r = flat / ngroups runs over the query
+// blocks of every KV group; ranks are dealt in passes of `pass` ranks (one workgroup per
+// CU per pass). Even passes go heaviest first; odd passes run in reverse, so the two
+// workgroups a CU holds at once (from passes 0 and 1) add up to the same causal work.
+__device__ __forceinline__ int prefill_block_of(int flat, int ngroups, int nqb, int pass) {
+    const int rank = flat / ngroups;
+    if (pass <= 0) return nqb - 1 - rank;
+    const int round = rank / pass;
+    const int first = round * pass;
+    const int count = min(pass, nqb - first);
+    const int order = (round & 1) ? first + (count - 1 - (rank - first)) : rank;
+    return nqb - 1 - order;
+}
+
 template <int HD, int HPW>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(const float *__restrict__ q,
-                                                           const float *__restrict__ k,
-                                                           const float *__restrict__ v,
-                                                           float *__restrict__ o, int H, int Hkv,
-                                                           int T, float scale_log2, int nqb,
-                                                           int ngroups) {
+__global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) void prefill_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    float *__restrict__ o, int H, int Hkv, int T, float scale_log2, int nqb, int ngroups,
+    int pass) {
     using S = PrefillShape<HD>;
     constexpr int WPH = 4 / HPW;    // waves per head
     constexpr int QB = kTile * WPH; // query rows per workgroup
@@ -80,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const float *__restri
     const int gsub = g / HPW;
     const int flat = blockIdx.x;
     const int grp = flat % ngroups;
-    const int qb = nqb - 1 - flat / ngroups;
+    const int qb = prefill_block_of(flat, ngroups, nqb, pass);
     const int kvh = grp / gsub;
     const int head = kvh * g + (grp % gsub) * HPW + wave / WPH;
     const int q0 = qb * QB + (wave % WPH) * kTile;
@@ -275,6 +296,18 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const float *__restri
     }
 }
 
+// Ranks per pass of the snake order: one workgroup per CU per pass. EB_PREFILL_ORDER=heavy
+// turns the snake off (plain heaviest-first order).
+int prefill_pass(int ngroups) {
+    static const bool snake = [] {
+        const char *e = std::getenv("EB_PREFILL_ORDER");
+        return !(e && std::string(e) == "heavy");
+    }();
+    if (!snake) return 0;
+    const int cus = eb::current_cu_count();
+    return cus >= ngroups ? cus / ngroups : 1;
+}
+
 template <int HD, int HPW>
 eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const float *v,
                            float *o, int H, int Hkv, int T, float scale_log2) {
@@ -292,7 +325,7 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const
     const int nqb = (T + QB - 1) / QB;
     const unsigned blocks = (unsigned)(nqb * ngroups);
     prefill_kernel<HD, HPW><<<blocks, kThreads, lds, st>>>(q, k, v, o, H, Hkv, T, scale_log2, nqb,
-                                                          ngroups);
+                                                          ngroups, prefill_pass(ngroups));
     return eb::check_launch("attn_prefill");
 }
 

@@ -502,7 +502,17 @@ static eb_status rope_checked(hipStream_t st, const float *x, size_t xn, const f
     return eb::ok();
 }
 
-// Grows the device's decode workspace (stream ordered: hipFree waits for the device).
+// Checks the new-token rows of a fused decode step ([hkv, hd] each).
+static eb_status step_rows_checked(const float *knew, const float *vnew, size_t new_n,
+                                   size_t hkv, size_t hd) {
+    EB_TRY(eb::check_numel(new_n, hkv * hd, "knew/vnew"));
+    EB_TRY(eb::check_ptr(knew, "knew"));
+    EB_TRY(eb::check_ptr(vnew, "vnew"));
+    return EB_OK;
+}
+
+// Grows the device's decode workspace. Stream ordered: the old buffer is freed only after
+// the stream drains.
 static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
     std::lock_guard<std::mutex> lk(dev->ws_mu);
     if (floats > dev->ws_floats) {
@@ -517,6 +527,19 @@ static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
     }
     *out = dev->ws;
     return EB_OK;
+}
+
+// Shared by eb_attn_decode / eb_attn_decode_step: device workspace, then one launch.
+static eb_status device_decode(eb_device *dev, const float *q, const float *kc, const float *vc,
+                               float *kc_w, float *vc_w, const float *knew, const float *vnew,
+                               float *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                               float scale) {
+    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
+    float *ws = nullptr;
+    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
+    EB_TRY(eb::launch_attn_decode(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv, pos,
+                                  hd, scale, ws, wsn, dev->cu_count));
+    return eb::ok();
 }
 
 extern "C" {
@@ -558,15 +581,34 @@ eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *
                                 (const float *)vcache->ptr, eb_tensor_numel(vcache),
                                 (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
                                 max_seq));
-    eb_device *dev = rec->dev;
-    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
-    float *ws = nullptr;
-    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
-    EB_TRY(eb::launch_attn_decode(dev->stream, (const float *)q->ptr,
-                                  (const float *)kcache->ptr, (const float *)vcache->ptr,
-                                  (float *)o->ptr, h, hkv, pos, hd, scale, ws, wsn,
-                                  dev->cu_count));
-    return eb::ok();
+    return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
+                         (const float *)vcache->ptr, nullptr, nullptr, nullptr, nullptr,
+                         (float *)o->ptr, h, hkv, pos, hd, scale);
+}
+
+eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
+                              const eb_tensor *vnew, eb_tensor *kcache, eb_tensor *vcache,
+                              eb_tensor *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                              size_t max_seq, float scale) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(knew, "knew", rec->dev));
+    EB_TRY(tensor_f32(vnew, "vnew", rec->dev));
+    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
+    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q),
+                                (const float *)kcache->ptr, eb_tensor_numel(kcache),
+                                (const float *)vcache->ptr, eb_tensor_numel(vcache),
+                                (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
+                                max_seq));
+    size_t nn = eb_tensor_numel(knew) < eb_tensor_numel(vnew) ? eb_tensor_numel(knew)
+                                                              : eb_tensor_numel(vnew);
+    EB_TRY(step_rows_checked((const float *)knew->ptr, (const float *)vnew->ptr, nn, hkv, hd));
+    return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
+                         (const float *)vcache->ptr, (float *)kcache->ptr, (float *)vcache->ptr,
+                         (const float *)knew->ptr, (const float *)vnew->ptr, (float *)o->ptr, h,
+                         hkv, pos, hd, scale);
 }
 
 eb_status eb_rmsnorm(eb_recorder *rec, const eb_tensor *x, const eb_tensor *weight,
@@ -631,8 +673,29 @@ eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel, co
         return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
                     workspace_floats, need);
     if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
-    EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, o, h, hkv, pos, hd, scale,
-                                  workspace, workspace_floats, cus));
+    EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, nullptr, nullptr, nullptr,
+                                  nullptr, o, h, hkv, pos, hd, scale, workspace,
+                                  workspace_floats, cus));
+    return eb::ok();
+}
+
+eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_numel,
+                                     const float *knew, const float *vnew, size_t new_numel,
+                                     float *kc, size_t kc_numel, float *vc, size_t vc_numel,
+                                     float *o, size_t o_numel, size_t h, size_t hkv, size_t pos,
+                                     size_t hd, size_t max_seq, float scale, float *workspace,
+                                     size_t workspace_floats, int cu_count) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq));
+    EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, kc, vc, knew, vnew, o, h, hkv,
+                                  pos, hd, scale, workspace, workspace_floats, cus));
     return eb::ok();
 }
 

@@ -22,6 +22,16 @@ def attn_decode(rec: Recorder, q: Tensor, kcache: Tensor, vcache: Tensor, o: Ten
                                hkv, pos, hd, max_seq, scale))
 
 
+def attn_decode_step(rec: Recorder, q: Tensor, knew: Tensor, vnew: Tensor, kcache: Tensor,
+                     vcache: Tensor, o: Tensor, h: int, hkv: int, pos: int, hd: int,
+                     max_seq: int, scale: float) -> None:
+    """kv_write(K), kv_write(V), attn_decode of Attention::decode
+    (crates/eyebrowse-nn/src/attention.rs:149-183) in one launch."""
+    check(lib().eb_attn_decode_step(rec.handle, q.handle, knew.handle, vnew.handle,
+                                    kcache.handle, vcache.handle, o.handle, h, hkv, pos, hd,
+                                    max_seq, scale))
+
+
 def kv_write(rec: Recorder, cache: Tensor, src: Tensor, hkv: int, count: int, hd: int,
              max_seq: int, dst_start: int) -> None:
     """ops.rs:150-179: copy src [count,hkv,hd] into cache rows dst_start.."""
@@ -68,6 +78,17 @@ def launch_attn_decode(stream: int, q: int, q_numel: int, kc: int, kc_numel: int
     check(lib().eb_launch_attn_decode(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
                                       o_numel, h, hkv, pos, hd, max_seq, scale, workspace,
                                       workspace_floats, cu_count))
+
+
+def launch_attn_decode_step(stream: int, q: int, q_numel: int, knew: int, vnew: int,
+                            new_numel: int, kc: int, kc_numel: int, vc: int, vc_numel: int,
+                            o: int, o_numel: int, h: int, hkv: int, pos: int, hd: int,
+                            max_seq: int, scale: float, workspace: int, workspace_floats: int,
+                            cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode_step(stream, q, q_numel, knew, vnew, new_numel, kc,
+                                           kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos, hd,
+                                           max_seq, scale, workspace, workspace_floats,
+                                           cu_count))
 
 
 def launch_rmsnorm(stream: int, x: int, x_numel: int, w: int, w_numel: int, out: int,

@@ -127,6 +127,14 @@ eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor 
 eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
                          const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
                          size_t pos, size_t hd, size_t max_seq, float scale);
+/* The kv_write(K), kv_write(V), attn_decode sequence of Attention::decode
+ * (crates/eyebrowse-nn/src/attention.rs:149-183) in one launch: knew/vnew [hkv, hd] are
+ * copied bit-exactly into cache row pos and q attends keys 0..=pos (key pos taken from
+ * knew/vnew). Same result as the three calls. */
+eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
+                              const eb_tensor *vnew, eb_tensor *kcache, eb_tensor *vcache,
+                              eb_tensor *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                              size_t max_seq, float scale);
 /* kv_write (ops.rs:150-179): copy src [count,hkv,hd] into cache rows
  * [dst_start, dst_start+count) of [max_seq,hkv,hd]; bit-exact. Unlike the reference,
  * dst_start + count > max_seq is rejected (EB_SHAPE_MISMATCH). */
@@ -150,8 +158,9 @@ eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel,
                                  const float *k, size_t k_numel, const float *v,
                                  size_t v_numel, float *o, size_t o_numel, size_t h,
                                  size_t hkv, size_t s, size_t hd, float scale);
-/* Floats of workspace eb_launch_attn_decode needs for this shape on this many CUs
- * (0 when the split count is 1 and no workspace is used). */
+/* Floats of workspace eb_launch_attn_decode(_step) needs for this shape on this many CUs
+ * (0 when the split count is 1 and no workspace is used). Its contents need no
+ * initialisation. Launches that share a workspace must not overlap (use one stream). */
 size_t eb_attn_decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd,
                                        int cu_count);
 eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel,
@@ -160,6 +169,13 @@ eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel,
                                 size_t hkv, size_t pos, size_t hd, size_t max_seq,
                                 float scale, float *workspace, size_t workspace_floats,
                                 int cu_count);
+/* eb_attn_decode_step on caller memory; knew/vnew each hold new_numel >= hkv*hd floats. */
+eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_numel,
+                                     const float *knew, const float *vnew, size_t new_numel,
+                                     float *kc, size_t kc_numel, float *vc, size_t vc_numel,
+                                     float *o, size_t o_numel, size_t h, size_t hkv, size_t pos,
+                                     size_t hd, size_t max_seq, float scale, float *workspace,
+                                     size_t workspace_floats, int cu_count);
 eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel,
                             const float *weight, size_t w_numel, float *out,
                             size_t out_numel, size_t rows, size_t dim, float eps);

@@ -34,6 +34,15 @@ def assert_close(got, want, rel=F32_REL_L2, abs_=F32_MAX_ABS, what=""):
     return r, m
 
 
+def assert_bitwise(got, want, what=""):
+    """Bit-for-bit equality of two f32 arrays (reports the mismatch count, not a diff)."""
+    g = np.ascontiguousarray(got, np.float32).view(np.uint32).ravel()
+    w = np.ascontiguousarray(want, np.float32).view(np.uint32).ravel()
+    assert g.size == w.size, f"{what}: {g.size} vs {w.size} elements"
+    bad = int(np.count_nonzero(g != w))
+    assert bad == 0, f"{what}: {bad} of {g.size} elements differ bitwise"
+
+
 def upload(dev, a):
     a = np.ascontiguousarray(a, np.float32)
     return eb.Tensor.from_f32(dev, a.shape, a)

@@ -6,7 +6,7 @@ import pytest
 
 import eyebrowse_amd as eb
 import oracle
-from tests._gpu import assert_close, decode, note, upload
+from tests._gpu import assert_bitwise, assert_close, decode, note, upload
 from tests._textbook import ramp, rel_l2_f64
 
 pytestmark = pytest.mark.gpu
@@ -54,7 +54,7 @@ def _decode_step(dev, h, hkv, hd, max_seq, pos, scale, seed=1):
     rec.submit()
     kc2 = oracle.kv_write(kc, knew, hkv, 1, hd, pos)
     vc2 = oracle.kv_write(vc, vnew, hkv, 1, hd, pos)
-    assert kt.to_f32().tobytes() == kc2.tobytes()
+    assert_bitwise(kt.to_f32(), kc2, "cache after kv_write")
     want = oracle.attn_decode(q, kc2, vc2, h, hkv, pos, hd, max_seq, scale, threads=8)
     return ot.to_f32().reshape(h, hd), want
 
@@ -112,13 +112,94 @@ def test_raw_launch_with_caller_workspace(dev):
     cus = dev.cu_count
     wsn = eb.attn_decode_workspace_floats(h, hkv, pos, hd, cus)
     assert wsn > 0
-    ws = eb.Tensor.empty(dev, (wsn,))
-    eb.launch_attn_decode(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(),
-                          vt.data_ptr, vt.numel(), ot.data_ptr, ot.numel(), h, hkv, pos, hd, ms,
-                          float(oracle.default_scale(hd)), ws.data_ptr, wsn, cus)
-    dev.synchronize()
+    # the workspace needs no initialisation: fill it with NaN first
+    ws = upload(dev, np.full(wsn, np.nan, np.float32))
     want = oracle.attn_decode(q, kc, vc, h, hkv, pos, hd, ms, threads=8)
-    assert_close(ot.to_f32().reshape(h, hd), want, what="raw")
+    for _ in range(2):
+        eb.launch_attn_decode(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(),
+                              vt.data_ptr, vt.numel(), ot.data_ptr, ot.numel(), h, hkv, pos, hd,
+                              ms, float(oracle.default_scale(hd)), ws.data_ptr, wsn, cus)
+        dev.synchronize()
+        assert_close(ot.to_f32().reshape(h, hd), want, what="raw")
+
+
+def test_shrinking_shapes_share_the_device_workspace(dev):
+    """Decode calls of decreasing size on one device reuse its grow-only workspace: a
+    smaller shape must not pick up a larger shape's leftovers."""
+    note("decode shrinking shapes")
+    for h, hkv, hd, ms, pos in [(32, 8, 128, 32768, 32767), (16, 8, 256, 9000, 8999),
+                                (16, 8, 128, 4096, 4095), (8, 8, 64, 3000, 2999),
+                                (24, 8, 128, 700, 650), (4, 2, 8, 600, 599)]:
+        q, kc, vc = oracle.randn((h, hd), 1), oracle.randn((ms, hkv, hd), 2), oracle.randn((ms, hkv, hd), 3)
+        got = decode(dev, q, kc, vc, h, hkv, pos, hd, ms, 0.1)
+        want = oracle.attn_decode(q, kc, vc, h, hkv, pos, hd, ms, 0.1, threads=8)
+        assert_close(got, want, what=f"h={h} hd={hd} pos={pos}")
+
+
+@pytest.mark.parametrize("h,hkv,hd,max_seq,pos", [
+    (16, 8, 128, 8192, 8191),
+    (32, 8, 128, 32768, 20000),
+    (16, 8, 256, 16384, 16383),
+    (4, 2, 8, 16, 5),
+    (4, 2, 8, 16, 0),
+])
+def test_fused_step_equals_kv_write_then_decode(dev, h, hkv, hd, max_seq, pos):
+    """eb_attn_decode_step == kv_write(K), kv_write(V), attn_decode (attention.rs:149-183):
+    same cache bytes, same output bits."""
+    note(f"decode step h={h} hd={hd} pos={pos}")
+    sc = float(oracle.default_scale(hd))
+    kc = oracle.randn((max_seq, hkv, hd), 2)
+    vc = oracle.randn((max_seq, hkv, hd), 3)
+    knew, vnew = oracle.randn((1, hkv, hd), 4), oracle.randn((1, hkv, hd), 5)
+    q = oracle.randn((h, hd), 1)
+    qt, knt, vnt = upload(dev, q), upload(dev, knew), upload(dev, vnew)
+    k1, v1, k2, v2 = upload(dev, kc), upload(dev, vc), upload(dev, kc), upload(dev, vc)
+    o1, o2 = eb.Tensor.empty(dev, (h, hd)), eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, k1, knt, hkv, 1, hd, max_seq, pos)
+    eb.kv_write(rec, v1, vnt, hkv, 1, hd, max_seq, pos)
+    eb.attn_decode(rec, qt, k1, v1, o1, h, hkv, pos, hd, max_seq, sc)
+    eb.attn_decode_step(rec, qt, knt, vnt, k2, v2, o2, h, hkv, pos, hd, max_seq, sc)
+    rec.submit()
+    assert_bitwise(k2.to_f32(), k1.to_f32(), "K cache")
+    assert_bitwise(v2.to_f32(), v1.to_f32(), "V cache")
+    assert_bitwise(o2.to_f32(), o1.to_f32(), "output")
+    want = oracle.attn_decode(q, oracle.kv_write(kc, knew, hkv, 1, hd, pos),
+                              oracle.kv_write(vc, vnew, hkv, 1, hd, pos), h, hkv, pos, hd,
+                              max_seq, sc, threads=8)
+    assert_close(o2.to_f32().reshape(h, hd), want, what="step")
+
+
+def test_sequence_of_steps_reuses_the_workspace(dev):
+    """A decode loop (positions 0..N-1 through the fused step) on one device workspace;
+    each step matches the oracle, so the split counters reset correctly every launch."""
+    note("decode loop")
+    h, hkv, hd, max_seq = 16, 8, 128, 4096
+    kc = eb.Tensor.empty(dev, (max_seq, hkv, hd))
+    vc = eb.Tensor.empty(dev, (max_seq, hkv, hd))
+    kall = oracle.randn((max_seq, hkv, hd), 7)
+    vall = oracle.randn((max_seq, hkv, hd), 8)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, kc, upload(dev, kall), hkv, 3000, hd, max_seq, 0)
+    eb.kv_write(rec, vc, upload(dev, vall), hkv, 3000, hd, max_seq, 0)
+    rec.submit()
+    for pos in (3000, 3001, 3002, 3500, 4095):
+        q = oracle.randn((h, hd), pos)
+        o = eb.Tensor.empty(dev, (h, hd))
+        rec = eb.Recorder(dev)
+        eb.attn_decode_step(rec, upload(dev, q), upload(dev, kall[pos:pos + 1]),
+                            upload(dev, vall[pos:pos + 1]), kc, vc, o, h, hkv, pos, hd, max_seq, 0.09)
+        rec.submit()
+        # decode at pos reads rows 0..pos only, all of which the cache holds by now
+        want = oracle.attn_decode(q, kall, vall, h, hkv, pos, hd, max_seq, 0.09, threads=8)
+        assert_close(o.to_f32().reshape(h, hd), want, what=f"pos {pos}")
+        gap = {3002: (3003, 3500), 3500: (3501, 4095)}.get(pos)
+        if gap:  # fill the rows the loop skips
+            a, b = gap
+            rec = eb.Recorder(dev)
+            eb.kv_write(rec, kc, upload(dev, kall[a:b]), hkv, b - a, hd, max_seq, a)
+            eb.kv_write(rec, vc, upload(dev, vall[a:b]), hkv, b - a, hd, max_seq, a)
+            rec.submit()
 
 
 def test_repeated_calls_are_deterministic(dev):
@@ -127,5 +208,5 @@ def test_repeated_calls_are_deterministic(dev):
     q, kc, vc = oracle.randn((h, hd), 1), oracle.randn((ms, hkv, hd), 2), oracle.randn((ms, hkv, hd), 3)
     a = decode(dev, q, kc, vc, h, hkv, pos, hd, ms, 0.1)
     b = decode(dev, q, kc, vc, h, hkv, pos, hd, ms, 0.1)
-    assert a.tobytes() == b.tobytes()
+    assert_bitwise(a, b, "repeat")
     assert rel_l2_f64(a, oracle.attn_decode(q, kc, vc, h, hkv, pos, hd, ms, 0.1)) < 2e-5

@@ -5,7 +5,7 @@ import pytest
 
 import eyebrowse_amd as eb
 import oracle
-from tests._gpu import note, upload
+from tests._gpu import assert_bitwise, note, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -26,7 +26,7 @@ def test_reference_known_answer(dev):
             assert got[(3 * hkv + head) * hd + d] == src[head * hd + d]
     assert got[0] == 0.0
     want = oracle.kv_write(np.zeros(max_seq * hkv * hd, np.float32), src, hkv, 1, hd, 3)
-    assert got.tobytes() == want.tobytes()
+    assert_bitwise(got, want, "kv_write")
 
 
 @pytest.mark.parametrize("hkv,hd,max_seq,count,dst", [
@@ -48,7 +48,7 @@ def test_bit_exact_against_oracle(dev, hkv, hd, max_seq, count, dst):
     eb.kv_write(rec, ct, st, hkv, count, hd, max_seq, dst)
     rec.submit()
     want = oracle.kv_write(cache, src, hkv, count, hd, dst)
-    assert ct.to_f32().tobytes() == want.tobytes()
+    assert_bitwise(ct.to_f32(), want, "kv_write")
 
 
 def test_special_float_payloads_are_copied_bitwise(dev):
