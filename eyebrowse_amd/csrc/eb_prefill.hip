@@ -4,11 +4,14 @@
 // runs one thread per (query row, head) and re-reads K/V from memory for every row.
 //
 // Layout of the work
-//  - A workgroup is 4 waves; each wave owns 32 query rows of one head. The workgroup covers
-//    HPW heads of one KV group (GQA: the K/V tiles it stages are shared by all of them)
-//    and 32 * 4/HPW consecutive query rows.
-//  - K and V tiles of 32 keys are staged in LDS (double buffered: the next tile is
-//    fetched into registers while the current one is in use).
+//  - Every wave owns 32 query rows of one head. A workgroup covers HPW heads of one KV
+//    group (GQA: the K/V tiles it stages serve all of them), WPH consecutive 32-row query
+//    sub-blocks per head (QB = 32*WPH rows), and splits the key range KSPLIT ways: wave
+//    set ks takes key tiles t with t % KSPLIT == ks, and the KSPLIT partial softmax states
+//    are merged through LDS at the end. Splitting the keys halves the longest per-wave
+//    chain, so the causal triangle's big query blocks no longer set the kernel's length.
+//  - Each step stages KSPLIT tiles of 32 keys (K and V) in LDS, double buffered: the next
+//    step is fetched into registers while the current one is in use.
 //  - Everything is computed transposed so that the query index sits on the lane:
 //      S^T[key][query] = K Q^T         (v_mfma_f32_32x32x2_f32, contraction over head_dim)
 //      O^T[d][query]  += V^T P^T       (same instruction, contraction over the 32 keys)
@@ -21,93 +24,76 @@
 //  - Softmax runs in the log2 domain: scores are multiplied by scale*log2(e) and
 //    exponentiated with v_exp_f32. Only the diagonal tile of each wave is masked; tiles
 //    past the wave's last query are skipped.
-//  - Workgroups are numbered so the longest query blocks start first and so consecutive
-//    workgroup ids (which the dispatcher spreads over the 8 XCDs) walk across KV groups:
-//    with 8 groups each XCD keeps one group's K/V in its own L2.
+//  - Workgroups are numbered heaviest query block first, and consecutive workgroup ids
+//    (which the dispatcher spreads over the 8 XCDs) walk across KV groups: with 8 groups
+//    each XCD keeps one group's K/V in its own L2.
 //
 // FLOPs per launch: 2*H*HD*T*(T+1) algorithmic (QK^T and PV over the causal pairs); the
 // kernel issues MFMA work for whole 32x32 tiles, i.e. slightly more on the diagonal.
 #include "eb_common.h"
 #include "eb_internal.h"
 
-#include <cstdlib>
 #include <mutex>
-#include <string>
-
-// Workgroups the compiler must fit per CU for head_dim <= 128 (bounds registers per wave:
-// 2 four-wave workgroups = 2 waves per SIMD). head_dim 256 keeps one: its Q fragment and
-// O^T accumulators alone take 256 registers per lane.
-#ifndef EB_PREFILL_MIN_BLOCKS
-#define EB_PREFILL_MIN_BLOCKS 2
-#endif
 
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
 constexpr int kTile = 32;  // keys per tile, queries per wave
 
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-template <int HD>
-struct PrefillShape {
-    static constexpr int KS = HD + 4;          // K row stride in LDS (floats), bank spread
-    static constexpr int HALF = HD / 2;        // QK^T contraction steps per lane half
+template <int HD, int HPW, int WPH, int KSPLIT>
+struct PrefillCfg {
+    static constexpr int NW = HPW * WPH * KSPLIT;  // waves per workgroup
+    static constexpr int THREADS = NW * 64;
+    static constexpr int QB = kTile * WPH;         // query rows per workgroup
+    static constexpr int KS = HD + 4;              // K row stride in LDS (floats), bank spread
+    static constexpr int HALF = HD / 2;            // QK^T contraction steps per lane half
     static constexpr int NB = HD >= 32 ? HD / 32 : 1;  // 32-row blocks of O^T
-    static constexpr int TILE_F4 = kTile * HD / 4;     // float4 per K (or V) tile
-    static constexpr int NLD = (TILE_F4 + kThreads - 1) / kThreads;
-    static constexpr size_t LDS_BYTES = (size_t)(2 * kTile * KS + 2 * kTile * HD) * sizeof(float);
+    static constexpr int STEP_KEYS = kTile * KSPLIT;   // keys staged per step
+    static constexpr int STEP_F4 = STEP_KEYS * HD / 4;  // float4 per K (or V) step
+    static constexpr int NLD = (STEP_F4 + THREADS - 1) / THREADS;
+    static constexpr int BUF = STEP_KEYS * (KS + HD);  // floats per buffer: K rows, V rows
+    static constexpr int REC = 2 + 16 * NB;            // merged fields per lane: m, l, O^T
+    static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
+    static constexpr size_t LDS_BYTES =
+        (size_t)(2 * BUF > MERGE ? 2 * BUF : MERGE) * sizeof(float);
 };
 
-// Query block processed by workgroup `flat`. Rank r = flat / ngroups runs over the query
-// blocks of every KV group; ranks are dealt in passes of `pass` ranks (one workgroup per
-// CU per pass). Even passes go heaviest first; odd passes run in reverse, so the two
-// workgroups a CU holds at once (from passes 0 and 1) add up to the same causal work.
-__device__ __forceinline__ int prefill_block_of(int flat, int ngroups, int nqb, int pass) {
-    const int rank = flat / ngroups;
-    if (pass <= 0) return nqb - 1 - rank;
-    const int round = rank / pass;
-    const int first = round * pass;
-    const int count = min(pass, nqb - first);
-    const int order = (round & 1) ? first + (count - 1 - (rank - first)) : rank;
-    return nqb - 1 - order;
-}
-
-template <int HD, int HPW>
-__global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) void prefill_kernel(
+template <int HD, int HPW, int WPH, int KSPLIT>
+__global__ __launch_bounds__(HPW * WPH * KSPLIT * 64) void prefill_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-    float *__restrict__ o, int H, int Hkv, int T, float scale_log2, int nqb, int ngroups,
-    int pass) {
-    using S = PrefillShape<HD>;
-    constexpr int WPH = 4 / HPW;    // waves per head
-    constexpr int QB = kTile * WPH; // query rows per workgroup
-    constexpr int HALF = S::HALF;
-    constexpr int NB = S::NB;
-    constexpr int KS = S::KS;
+    float *__restrict__ o, int H, int Hkv, int T, float scale_log2, int nqb, int ngroups) {
+    using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
+    constexpr int QB = C::QB;
+    constexpr int HALF = C::HALF;
+    constexpr int NB = C::NB;
+    constexpr int KS = C::KS;
+    constexpr int THREADS = C::THREADS;
 
-    extern __shared__ float smem[];
-    float *Ks = smem;                    // [2][32][KS]
-    float *Vs = smem + 2 * kTile * KS;   // [2][32][HD]
+    extern __shared__ float smem[];  // [2][BUF]: K rows [STEP_KEYS][KS], V rows [STEP_KEYS][HD]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int hf = lane >> 5;
     const int col = lane & 31;
+    const int ks = wave / (HPW * WPH);     // key split this wave takes
+    const int slot = wave % (HPW * WPH);   // (head, query sub-block) of this wave
     const int g = H / Hkv;
     const int gsub = g / HPW;
     const int flat = blockIdx.x;
     const int grp = flat % ngroups;
-    const int qb = prefill_block_of(flat, ngroups, nqb, pass);
+    const int qb = nqb - 1 - flat / ngroups;  // heaviest query blocks first
     const int kvh = grp / gsub;
-    const int head = kvh * g + (grp % gsub) * HPW + wave / WPH;
-    const int q0 = qb * QB + (wave % WPH) * kTile;
+    const int head = kvh * g + (grp % gsub) * HPW + slot / WPH;
+    const int q0 = qb * QB + (slot % WPH) * kTile;
     const int wg_last = min(qb * QB + QB, T) - 1;
-    const int ntiles = wg_last / kTile + 1;
-    const int my_tiles = q0 < T ? q0 / kTile + 1 : 0;
+    const int nsteps = (wg_last / kTile) / KSPLIT + 1;
+    const int my_tiles = q0 < T ? q0 / kTile + 1 : 0;  // tiles 0..q0/32 hold its keys
     const int qi = q0 + col;
 
     // Q fragment: query qi, head dims [HALF*hf, HALF*hf + HALF).
@@ -139,12 +125,12 @@ __global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) 
     float m = -INFINITY;
     float l = 0.0f;
 
-    float4 rk[S::NLD], rv[S::NLD];
-    auto load_tile = [&](int kb) {
+    float4 rk[C::NLD], rv[C::NLD];
+    auto load_step = [&](int kb) {
 #pragma unroll
-        for (int r = 0; r < S::NLD; ++r) {
-            const int idx = tid + r * kThreads;
-            if (idx < S::TILE_F4) {
+        for (int r = 0; r < C::NLD; ++r) {
+            const int idx = tid + r * THREADS;
+            if (idx < C::STEP_F4) {
                 const int row = idx / (HD / 4);
                 const int c4 = idx % (HD / 4);
                 const int key = kb + row;
@@ -159,34 +145,39 @@ __global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) 
             }
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_step = [&](int buf) {
+        float *Kb = smem + buf * C::BUF;
+        float *Vb = Kb + C::STEP_KEYS * KS;
 #pragma unroll
-        for (int r = 0; r < S::NLD; ++r) {
-            const int idx = tid + r * kThreads;
-            if (idx < S::TILE_F4) {
+        for (int r = 0; r < C::NLD; ++r) {
+            const int idx = tid + r * THREADS;
+            if (idx < C::STEP_F4) {
                 const int row = idx / (HD / 4);
                 const int c4 = idx % (HD / 4);
-                *reinterpret_cast<float4 *>(Ks + (buf * kTile + row) * KS + c4 * 4) = rk[r];
-                *reinterpret_cast<float4 *>(Vs + (buf * kTile + row) * HD + c4 * 4) = rv[r];
+                *reinterpret_cast<float4 *>(Kb + row * KS + c4 * 4) = rk[r];
+                *reinterpret_cast<float4 *>(Vb + row * HD + c4 * 4) = rv[r];
             }
         }
     };
 
-    load_tile(0);
-    store_tile(0);
+    load_step(0);
+    store_step(0);
     __syncthreads();
 
-    for (int it = 0; it < ntiles; ++it) {
+    for (int it = 0; it < nsteps; ++it) {
         const int buf = it & 1;
-        const int kb = it * kTile;
-        if (it + 1 < ntiles) load_tile(kb + kTile);
+        const int tile = it * KSPLIT + ks;
+        const int kb = tile * kTile;
+        if (it + 1 < nsteps) load_step((it + 1) * C::STEP_KEYS);
 
-        if (it < my_tiles) {
+        if (tile < my_tiles) {
+            const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
+            const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS + ks * kTile * HD;
             // S^T = K Q^T for this tile: 16 keys x 1 query per lane.
             floatx16 sacc;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
-            const float *kr = Ks + (buf * kTile + col) * KS + HALF * hf;
+            const float *kr = Kb + col * KS + HALF * hf;
             if constexpr (HALF % 4 == 0) {
 #pragma unroll
                 for (int i = 0; i < HALF / 4; ++i) {
@@ -230,11 +221,10 @@ __global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) 
                 for (int r = 0; r < 16; ++r) oacc[mb][r] *= corr;
 
             // O^T += V^T P^T: step t pairs key 8*(t/4) + 4*hf + t%4 with p[t].
-            const float *vt = Vs + buf * kTile * HD;
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
                 const int kl = 8 * (t >> 2) + 4 * hf + (t & 3);
-                const float *vp = vt + kl * HD;
+                const float *vp = Vb + kl * HD;
                 if constexpr (NB == 8) {
                     float4 a0 = *reinterpret_cast<const float4 *>(vp + 8 * col);
                     float4 a1 = *reinterpret_cast<const float4 *>(vp + 8 * col + 4);
@@ -265,13 +255,47 @@ __global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) 
             }
         }
 
-        if (it + 1 < ntiles) store_tile(buf ^ 1);
+        if (it + 1 < nsteps) store_step(buf ^ 1);
         __syncthreads();
+    }
+
+    // Merge the key splits: waves ks >= 1 hand (m, l, O^T) to wave ks = 0 of their slot
+    // through LDS (reusing the tile buffers, free after the loop's last barrier). Fields are
+    // stored [record][field][lane] so every access is a contiguous 64-lane row.
+    if constexpr (KSPLIT > 1) {
+        if (ks > 0) {
+            float *rec = smem + ((ks - 1) * (HPW * WPH) + slot) * C::REC * 64;
+            rec[0 * 64 + lane] = m;
+            rec[1 * 64 + lane] = l;
+#pragma unroll
+            for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) rec[(2 + mb * 16 + r) * 64 + lane] = oacc[mb][r];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int j = 1; j < KSPLIT; ++j) {
+                const float *rec = smem + ((j - 1) * (HPW * WPH) + slot) * C::REC * 64;
+                const float m2 = rec[lane];
+                const float l2 = rec[64 + lane];
+                const float M = fmaxf(m, m2);
+                const float a1 = eb::fast_exp2(m - M);   // m is finite: ks 0 ran tile 0
+                const float a2 = eb::fast_exp2(m2 - M);  // 0 when split j saw no keys
+                l = l * a1 + l2 * a2;
+                m = M;
+#pragma unroll
+                for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        oacc[mb][r] = oacc[mb][r] * a1 + rec[(2 + mb * 16 + r) * 64 + lane] * a2;
+            }
+        }
     }
 
     // Normalise and store: lane holds O[qi][NB*c + mb] for c = 8*(r/4) + 4*hf + r%4.
     const float lt = l + __shfl_xor(l, 32);
-    if (my_tiles > 0 && qi < T) {
+    if (ks == 0 && my_tiles > 0 && qi < T) {
         const float inv = 1.0f / lt;
         float *op = o + ((size_t)qi * H + head) * HD;
 #pragma unroll
@@ -296,46 +320,38 @@ __global__ __launch_bounds__(kThreads, (HD <= 128 ? EB_PREFILL_MIN_BLOCKS : 1)) 
     }
 }
 
-// Ranks per pass of the snake order: one workgroup per CU per pass. EB_PREFILL_ORDER=heavy
-// turns the snake off (plain heaviest-first order).
-int prefill_pass(int ngroups) {
-    static const bool snake = [] {
-        const char *e = std::getenv("EB_PREFILL_ORDER");
-        return !(e && std::string(e) == "heavy");
-    }();
-    if (!snake) return 0;
-    const int cus = eb::current_cu_count();
-    return cus >= ngroups ? cus / ngroups : 1;
-}
-
-template <int HD, int HPW>
+template <int HD, int HPW, int WPH, int KSPLIT>
 eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const float *v,
                            float *o, int H, int Hkv, int T, float scale_log2) {
-    constexpr int QB = kTile * (4 / HPW);
-    const size_t lds = PrefillShape<HD>::LDS_BYTES;
+    using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [&] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_kernel<HD, HPW>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        attr_err = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&prefill_kernel<HD, HPW, WPH, KSPLIT>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
     const int g = H / Hkv;
     const int ngroups = Hkv * (g / HPW);
-    const int nqb = (T + QB - 1) / QB;
+    const int nqb = (T + C::QB - 1) / C::QB;
     const unsigned blocks = (unsigned)(nqb * ngroups);
-    prefill_kernel<HD, HPW><<<blocks, kThreads, lds, st>>>(q, k, v, o, H, Hkv, T, scale_log2, nqb,
-                                                          ngroups, prefill_pass(ngroups));
+    prefill_kernel<HD, HPW, WPH, KSPLIT><<<blocks, C::THREADS, C::LDS_BYTES, st>>>(
+        q, k, v, o, H, Hkv, T, scale_log2, nqb, ngroups);
     return eb::check_launch("attn_prefill");
 }
 
+// head_dim <= 128: 8 waves (2 per SIMD) = 4 (head, 32-row) slots x 2 key splits.
+// head_dim 256: the Q fragment and O^T accumulators take ~400 registers per lane, so one
+// wave per SIMD: 4 waves, no key split.
 template <int HD>
 eb_status launch_prefill_hd(hipStream_t st, const float *q, const float *k, const float *v,
                             float *o, int H, int Hkv, int T, float scale_log2) {
     const int g = H / Hkv;
-    if (g % 4 == 0) return launch_prefill_t<HD, 4>(st, q, k, v, o, H, Hkv, T, scale_log2);
-    if (g % 2 == 0) return launch_prefill_t<HD, 2>(st, q, k, v, o, H, Hkv, T, scale_log2);
-    return launch_prefill_t<HD, 1>(st, q, k, v, o, H, Hkv, T, scale_log2);
+    constexpr int KSPLIT = HD <= 128 ? 2 : 1;
+    if (g % 4 == 0) return launch_prefill_t<HD, 4, 1, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
+    if (g % 2 == 0) return launch_prefill_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
+    return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
 }
 
 }  // namespace
