@@ -232,6 +232,34 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+def traffic_run(eb, hip, dev, sc128):
+    """Dispatches for the HBM-traffic counter passes, each kernel launched directly (no
+    graph) so that every dispatch is counted on its own:
+      1. kv_write copying 256 MiB (a plain copy of known size: FETCH_SIZE and WRITE_SIZE
+         of it calibrate the counters), 3 times;
+      2. the headline decode step (Qwen L=8191) over 7 rotated caches, 14 times;
+      3. Qwen T=4096 prefill, 3 times."""
+    rows, hkv, hd = 65536, 8, 128
+    src = eb.Tensor.empty(dev, (rows, hkv, hd))
+    dst = eb.Tensor.empty(dev, (rows, hkv, hd))
+    for _ in range(3):
+        eb.launch_kv_write(dev.stream, dst.data_ptr, dst.numel(), src.data_ptr, src.numel(), hkv,
+                           rows, hd, rows, 0)
+    dev.synchronize()
+    del src, dst
+    w = DecodeWorkload(eb, hip, dev, 16, 8, 128, 8192, 8191, sc128, per_graph=1)
+    for i in range(14):
+        w._step(w.caches[i % w.n_caches])
+    dev.synchronize()
+    w.close()
+    del w
+    p = PrefillWorkload(eb, dev, 16, 8, 128, 4096, sc128)
+    for _ in range(3):
+        p.launch()
+    dev.synchronize()
+    print(json.dumps({"traffic_run": "done", "copy_bytes": rows * hkv * hd * 4}), flush=True)
+
+
 # ------------------------------------------------------------------ main
 
 def main():
@@ -240,7 +268,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["headline", "all"], default="all")
+    ap.add_argument("--only", choices=["headline", "all", "traffic"], default="all",
+                    help="traffic: a short run for rocprofv3 --pmc passes (see profiles/)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the eyebrowse attention path is a single-device "
@@ -252,6 +281,9 @@ def main():
     hip = Hip()
     dev = eb.Device.new(0)
     sc128 = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    if args.only == "traffic":
+        traffic_run(eb, hip, dev, sc128)
+        return
 
     # Headline: Qwen decode L=8191. A step is one kernel (kv_write + split-KV attention +
     # merge), so the step time is also the dominant kernel's average launch duration.

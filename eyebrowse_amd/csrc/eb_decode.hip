@@ -81,7 +81,7 @@ struct DecodeArgs {
 };
 
 template <int HD, int G>
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void decode_kernel(DecodeArgs a) {
     using S = DecodeShape<HD, G>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
@@ -136,9 +136,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     const float *kbase = a.kc + (size_t)kvh * HD;
     const float *vbase = a.vc + (size_t)kvh * HD;
 
-    for (int base = c0; base < c1; base += S::KEYS_PER_ITER) {
-        float4 kv[U][NV4], vv[U][NV4];
-        bool valid[U];
+    // One iteration = U wave steps of KPW keys. Two register buffers: the next
+    // iteration's K/V loads are issued before the current one is consumed, so the wave
+    // keeps a full iteration of loads in flight while it computes.
+    auto load_iter = [&](int base, float4 (&kv)[U][NV4], float4 (&vv)[U][NV4],
+                         bool (&valid)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int key = base + (u * kWaves + wave) * S::KPW + kg;
@@ -156,6 +158,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
                 vv[u][i] = *reinterpret_cast<const float4 *>(vp + dim_of<HD>(i, ls));
             }
         }
+    };
+    auto consume_iter = [&](const float4 (&kv)[U][NV4], const float4 (&vv)[U][NV4],
+                            const bool (&valid)[U]) {
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             float sc[U];
@@ -203,6 +208,25 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
                 acc[gi][4 * i + 3] = a3;
             }
             m[gi] = mnew;
+        }
+    };
+
+    {
+        float4 kA[U][NV4], vA[U][NV4], kB[U][NV4], vB[U][NV4];
+        bool okA[U], okB[U];
+        int base = c0;
+        load_iter(base, kA, vA, okA);
+        while (true) {
+            base += S::KEYS_PER_ITER;
+            const bool moreB = base < c1;
+            if (moreB) load_iter(base, kB, vB, okB);
+            consume_iter(kA, vA, okA);
+            if (!moreB) break;
+            base += S::KEYS_PER_ITER;
+            const bool moreA = base < c1;
+            if (moreA) load_iter(base, kA, vA, okA);
+            consume_iter(kB, vB, okB);
+            if (!moreA) break;
         }
     }
 
@@ -275,64 +299,77 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 
 // Log-sum-exp merge of the split partials (a second launch, so the partials written by
 // every XCD are visible without in-kernel fences): one 256-thread block per query head.
-// Phase A: the split maxima and weights w_s = 2^(m_s - M), L = sum_s w_s l_s; phase B:
-// 256/HD groups of HD threads sum disjoint split subsets of acc_s[d] * w_s, combined
-// through LDS; o[h][d] = A / L.
+// Thread (grp, d), GROUPS = 256/HD groups, folds splits s = grp, grp + GROUPS, ... into a
+// running (M, L, A) in batches of kBatch splits whose loads are all issued before any is
+// used, so a merge costs about ceil(nsplit / (GROUPS * kBatch)) memory round trips. The
+// groups then combine through LDS: o[h][d] = A / L.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(const float *__restrict__ part_acc,
                                                                 const float *__restrict__ part_ml,
                                                                 float *__restrict__ o, int h,
                                                                 int nsplit) {
     constexpr int GROUPS = HD >= kThreads ? 1 : kThreads / HD;
-    __shared__ float s_w[kMaxSplits];
-    __shared__ float s_red[kWaves];
-    __shared__ float s_part[GROUPS][HD];
+    constexpr int kBatch = 8;
+    __shared__ float s_m[GROUPS][HD < kThreads ? HD : kThreads];
+    __shared__ float s_l[GROUPS][HD < kThreads ? HD : kThreads];
+    __shared__ float s_a[GROUPS][HD < kThreads ? HD : kThreads];
     const int hh = blockIdx.x;
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    const bool has = tid < nsplit;
-    const float m = has ? part_ml[((size_t)tid * h + hh) * 2] : -INFINITY;
-    const float lv = has ? part_ml[((size_t)tid * h + hh) * 2 + 1] : 0.0f;
-    float M = m;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (lane == 0) s_red[wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float mref = (M == -INFINITY) ? 0.0f : M;
-    const float w = has ? eb::fast_exp2(m - mref) : 0.0f;
-    if (tid < kMaxSplits) s_w[tid] = w;
-    float L = w * lv;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off);
-    __syncthreads();
-    if (lane == 0) s_red[wave] = L;
-    __syncthreads();
-    L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const size_t stride_acc = (size_t)h * HD;
+    const size_t stride_ml = (size_t)h * 2;
 
     for (int d0 = 0; d0 < HD; d0 += kThreads) {
-        const int d = d0 + tid % HD;
-        const int grp = tid / HD;
-        float A0 = 0.0f, A1 = 0.0f;
+        const int dl = tid % (HD < kThreads ? HD : kThreads);
+        const int d = d0 + dl;
+        const int grp = tid / (HD < kThreads ? HD : kThreads);
+        float M = -INFINITY, L = 0.0f, A = 0.0f;
         if (grp < GROUPS && d < HD) {
             const float *pa = part_acc + (size_t)hh * HD + d;
-            const size_t stride = (size_t)h * HD;
-            int s = grp;
-            for (; s + GROUPS < nsplit; s += 2 * GROUPS) {
-                A0 += pa[(size_t)s * stride] * s_w[s];
-                A1 += pa[(size_t)(s + GROUPS) * stride] * s_w[s + GROUPS];
+            const float *pm = part_ml + (size_t)hh * 2;
+            for (int s0 = grp; s0 < nsplit; s0 += GROUPS * kBatch) {
+                float bm[kBatch], bl[kBatch], ba[kBatch];
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    const int s = s0 + j * GROUPS;
+                    const bool ok = s < nsplit;
+                    bm[j] = ok ? pm[(size_t)s * stride_ml] : -INFINITY;
+                    bl[j] = ok ? pm[(size_t)s * stride_ml + 1] : 0.0f;
+                    ba[j] = ok ? pa[(size_t)s * stride_acc] : 0.0f;
+                }
+                float bM = bm[0];
+#pragma unroll
+                for (int j = 1; j < kBatch; ++j) bM = fmaxf(bM, bm[j]);
+                const float Mn = fmaxf(M, bM);
+                const float mref = (Mn == -INFINITY) ? 0.0f : Mn;
+                const float c = eb::fast_exp2(M - mref);
+                L *= c;
+                A *= c;
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    const float w = eb::fast_exp2(bm[j] - mref);
+                    L += w * bl[j];
+                    A += w * ba[j];
+                }
+                M = Mn;
             }
-            if (s < nsplit) A0 += pa[(size_t)s * stride] * s_w[s];
-            s_part[grp][tid % HD] = A0 + A1;
+            s_m[grp][dl] = M;
+            s_l[grp][dl] = L;
+            s_a[grp][dl] = A;
         }
         __syncthreads();
-        if (tid < HD && d0 + tid < HD) {
-            float A = 0.0f;
+        if (tid < (HD < kThreads ? HD : kThreads) && d < HD) {
+            float Mt = s_m[0][tid];
 #pragma unroll
-            for (int g2 = 0; g2 < GROUPS; ++g2) A += s_part[g2][tid];
-            o[(size_t)hh * HD + d0 + tid] = A / L;
+            for (int g2 = 1; g2 < GROUPS; ++g2) Mt = fmaxf(Mt, s_m[g2][tid]);
+            const float mref = (Mt == -INFINITY) ? 0.0f : Mt;
+            float Lt = 0.0f, At = 0.0f;
+#pragma unroll
+            for (int g2 = 0; g2 < GROUPS; ++g2) {
+                const float w = eb::fast_exp2(s_m[g2][tid] - mref);
+                Lt += w * s_l[g2][tid];
+                At += w * s_a[g2][tid];
+            }
+            o[(size_t)hh * HD + d] = At / Lt;
         }
         __syncthreads();
     }

@@ -64,7 +64,9 @@ struct PrefillCfg {
 };
 
 template <int HD, int HPW, int WPH, int KSPLIT>
-__global__ __launch_bounds__(HPW * WPH * KSPLIT * 64) void prefill_kernel(
+// Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
+__global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
+                             (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     float *__restrict__ o, int H, int Hkv, int T, float scale_log2, int nqb, int ngroups) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
@@ -341,15 +343,20 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const
     return eb::check_launch("attn_prefill");
 }
 
-// head_dim <= 128: 8 waves (2 per SIMD) = 4 (head, 32-row) slots x 2 key splits.
-// head_dim 256: the Q fragment and O^T accumulators take ~400 registers per lane, so one
+// head_dim <= 128:
+//  - 4 query heads per KV head or more: 4 waves = 4 heads x 32 rows, no key split, two
+//    workgroups per CU. 32-row blocks already give 4x more workgroups than CU slots, so
+//    the dispatcher balances the causal triangle.
+//  - otherwise: 8 waves (2 per SIMD) = 4 (head, 32-row) slots x 2 key splits, which
+//    halves the longest per-wave chain where the blocks are 64 or 128 rows tall.
+// head_dim 256: the Q fragment and O^T accumulators take ~450 registers per lane, so one
 // wave per SIMD: 4 waves, no key split.
 template <int HD>
 eb_status launch_prefill_hd(hipStream_t st, const float *q, const float *k, const float *v,
                             float *o, int H, int Hkv, int T, float scale_log2) {
     const int g = H / Hkv;
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
-    if (g % 4 == 0) return launch_prefill_t<HD, 4, 1, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
+    if (g % 4 == 0) return launch_prefill_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, T, scale_log2);
     if (g % 2 == 0) return launch_prefill_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
     return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
 }
