@@ -41,6 +41,15 @@
 #ifndef EB_DECODE_U
 #define EB_DECODE_U 0
 #endif
+// 1: two register buffers per wave (next iteration's loads issued before the current one
+// is consumed); 0: one buffer, latency hidden by other waves.
+#ifndef EB_DECODE_PIPELINE
+#define EB_DECODE_PIPELINE 1
+#endif
+// Workgroups per CU the register allocation must allow (launch-bounds minimum).
+#ifndef EB_DECODE_MINB
+#define EB_DECODE_MINB 1
+#endif
 
 namespace {
 
@@ -81,7 +90,7 @@ struct DecodeArgs {
 };
 
 template <int HD, int G>
-__global__ __launch_bounds__(kThreads, 1) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads, EB_DECODE_MINB) void decode_kernel(DecodeArgs a) {
     using S = DecodeShape<HD, G>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
@@ -211,22 +220,29 @@ __global__ __launch_bounds__(kThreads, 1) void decode_kernel(DecodeArgs a) {
         }
     };
 
-    {
+    if constexpr (!EB_DECODE_PIPELINE) {
+        for (int base = c0; base < c1; base += S::KEYS_PER_ITER) {
+            float4 kv[U][NV4], vv[U][NV4];
+            bool ok[U];
+            load_iter(base, kv, vv, ok);
+            consume_iter(kv, vv, ok);
+        }
+    } else {
         float4 kA[U][NV4], vA[U][NV4], kB[U][NV4], vB[U][NV4];
         bool okA[U], okB[U];
-        int base = c0;
-        load_iter(base, kA, vA, okA);
-        while (true) {
-            base += S::KEYS_PER_ITER;
-            const bool moreB = base < c1;
-            if (moreB) load_iter(base, kB, vB, okB);
+        // Counted loop over pairs of iterations with unconditional loads: a load issued
+        // under a branch would be sunk by the compiler next to its use, draining the queue.
+        // Iterations past c1 load clamped rows and are fully masked (valid = false), which
+        // leaves the softmax state unchanged.
+        const int n_iter = (c1 - c0 + S::KEYS_PER_ITER - 1) / S::KEYS_PER_ITER;
+        load_iter(c0, kA, vA, okA);
+        for (int it = 0; it < n_iter; it += 2) {
+            load_iter(c0 + (it + 1) * S::KEYS_PER_ITER, kB, vB, okB);
+            __builtin_amdgcn_sched_barrier(0);
             consume_iter(kA, vA, okA);
-            if (!moreB) break;
-            base += S::KEYS_PER_ITER;
-            const bool moreA = base < c1;
-            if (moreA) load_iter(base, kA, vA, okA);
+            load_iter(c0 + (it + 2) * S::KEYS_PER_ITER, kA, vA, okA);
+            __builtin_amdgcn_sched_barrier(0);
             consume_iter(kB, vB, okB);
-            if (!moreA) break;
         }
     }
 
