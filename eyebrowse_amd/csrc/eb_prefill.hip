@@ -38,6 +38,9 @@
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Native 4-wide vector for staged K/V values. HIP's float4 is a class type: a conditional
+// on it is lowered through a stack copy (scratch memory); this one stays in registers.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
 
@@ -47,6 +50,7 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
 
 template <int HD, int HPW, int WPH, int KSPLIT>
 struct PrefillCfg {
+    static constexpr int HD_ = HD;
     static constexpr int NW = HPW * WPH * KSPLIT;  // waves per workgroup
     static constexpr int THREADS = NW * 64;
     static constexpr int QB = kTile * WPH;         // query rows per workgroup
@@ -59,12 +63,60 @@ struct PrefillCfg {
     static constexpr int BUF = STEP_KEYS * (KS + HD);  // floats per buffer: K rows, V rows
     static constexpr int REC = 2 + 16 * NB;            // merged fields per lane: m, l, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
-    static constexpr size_t LDS_BYTES =
-        (size_t)(2 * BUF > MERGE ? 2 * BUF : MERGE) * sizeof(float);
+    static constexpr int OS = HD + 4;                  // output staging row stride (floats)
+    static constexpr int OUT = HPW * WPH * kTile * OS; // output staging, one tile per slot
+    static constexpr int LDS_FLOATS =
+        (2 * BUF > MERGE ? 2 * BUF : MERGE) > OUT ? (2 * BUF > MERGE ? 2 * BUF : MERGE) : OUT;
+    static constexpr size_t LDS_BYTES = (size_t)LDS_FLOATS * sizeof(float);
 };
 
-template <int HD, int HPW, int WPH, int KSPLIT>
+// Fetch the K and V rows [kb, kb + STEP_KEYS) of KV head kvh into registers; rows past
+// T read as zero. Every element is assigned on every call (clamped addresses, selected
+// values): conditionally written register arrays end up in scratch memory.
+template <class C>
+__device__ __forceinline__ void prefill_load_step(const float *__restrict__ k,
+                                                  const float *__restrict__ v,
+                                                  f32x4 (&rk)[C::NLD], f32x4 (&rv)[C::NLD],
+                                                  int kb, int T, int Hkv, int kvh, int tid) {
+    constexpr int HD = C::HD_;
+#pragma unroll
+    for (int r = 0; r < C::NLD; ++r) {
+        const int idx = min(tid + r * C::THREADS, C::STEP_F4 - 1);
+        const int row = idx / (HD / 4);
+        const int c4 = idx % (HD / 4);
+        const int key = kb + row;
+        const size_t off = ((size_t)min(key, T - 1) * Hkv + kvh) * HD + c4 * 4;
+        const f32x4 kx = *reinterpret_cast<const f32x4 *>(k + off);
+        const f32x4 vx = *reinterpret_cast<const f32x4 *>(v + off);
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        rk[r] = key < T ? kx : z;
+        rv[r] = key < T ? vx : z;
+    }
+}
+
+// Write the staged rows into LDS buffer `buf`: K rows [STEP_KEYS][KS], then V rows
+// [STEP_KEYS][HD].
+template <class C>
+__device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk)[C::NLD],
+                                                   const f32x4 (&rv)[C::NLD], int buf,
+                                                   int tid) {
+    constexpr int HD = C::HD_;
+    float *Kb = smem + buf * C::BUF;
+    float *Vb = Kb + C::STEP_KEYS * C::KS;
+#pragma unroll
+    for (int r = 0; r < C::NLD; ++r) {
+        const int idx = tid + r * C::THREADS;
+        if (idx < C::STEP_F4) {
+            const int row = idx / (HD / 4);
+            const int c4 = idx % (HD / 4);
+            *reinterpret_cast<f32x4 *>(Kb + row * C::KS + c4 * 4) = rk[r];
+            *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
+        }
+    }
+}
+
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
+template <int HD, int HPW, int WPH, int KSPLIT>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -127,50 +179,18 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     float m = -INFINITY;
     float l = 0.0f;
 
-    float4 rk[C::NLD], rv[C::NLD];
-    auto load_step = [&](int kb) {
-#pragma unroll
-        for (int r = 0; r < C::NLD; ++r) {
-            const int idx = tid + r * THREADS;
-            if (idx < C::STEP_F4) {
-                const int row = idx / (HD / 4);
-                const int c4 = idx % (HD / 4);
-                const int key = kb + row;
-                if (key < T) {
-                    const size_t off = ((size_t)key * Hkv + kvh) * HD + c4 * 4;
-                    rk[r] = *reinterpret_cast<const float4 *>(k + off);
-                    rv[r] = *reinterpret_cast<const float4 *>(v + off);
-                } else {
-                    rk[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    rv[r] = rk[r];
-                }
-            }
-        }
-    };
-    auto store_step = [&](int buf) {
-        float *Kb = smem + buf * C::BUF;
-        float *Vb = Kb + C::STEP_KEYS * KS;
-#pragma unroll
-        for (int r = 0; r < C::NLD; ++r) {
-            const int idx = tid + r * THREADS;
-            if (idx < C::STEP_F4) {
-                const int row = idx / (HD / 4);
-                const int c4 = idx % (HD / 4);
-                *reinterpret_cast<float4 *>(Kb + row * KS + c4 * 4) = rk[r];
-                *reinterpret_cast<float4 *>(Vb + row * HD + c4 * 4) = rv[r];
-            }
-        }
-    };
-
-    load_step(0);
-    store_step(0);
+    f32x4 rk[C::NLD], rv[C::NLD];
+    prefill_load_step<C>(k, v, rk, rv, 0, T, Hkv, kvh, tid);
+    prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
 
     for (int it = 0; it < nsteps; ++it) {
         const int buf = it & 1;
         const int tile = it * KSPLIT + ks;
         const int kb = tile * kTile;
-        if (it + 1 < nsteps) load_step((it + 1) * C::STEP_KEYS);
+        // Prefetch the next step (past the last step this re-reads clamped rows; the
+        // buffer written from them is never read).
+        prefill_load_step<C>(k, v, rk, rv, (it + 1) * C::STEP_KEYS, T, Hkv, kvh, tid);
 
         if (tile < my_tiles) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
@@ -257,7 +277,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             }
         }
 
-        if (it + 1 < nsteps) store_step(buf ^ 1);
+        prefill_store_step<C>(smem, rk, rv, buf ^ 1, tid);
         __syncthreads();
     }
 
@@ -295,28 +315,48 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         }
     }
 
-    // Normalise and store: lane holds O[qi][NB*c + mb] for c = 8*(r/4) + 4*hf + r%4.
+    // Normalise, then store through LDS: lane (col, hf) holds O[q0 + col][NB*c + mb] for
+    // c = 8*(r/4) + 4*hf + r%4, i.e. 16-byte pieces of 32 different output rows. Each
+    // slot's 32 x HD tile is transposed through LDS so the global stores are whole rows
+    // (HD contiguous floats per (query, head)).
     const float lt = l + __shfl_xor(l, 32);
-    if (ks == 0 && my_tiles > 0 && qi < T) {
+    if constexpr (KSPLIT > 1) __syncthreads();  // the merge records are read; reuse LDS
+    float *ot = smem + slot * kTile * C::OS;    // this slot's staging tile [32][OS]
+    if (ks == 0 && my_tiles > 0) {
         const float inv = 1.0f / lt;
-        float *op = o + ((size_t)qi * H + head) * HD;
+        float *orow = ot + col * C::OS;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int c = 8 * (r >> 2) + 4 * hf + (r & 3);
             if constexpr (NB == 8) {
-                *reinterpret_cast<float4 *>(op + 8 * c) =
+                *reinterpret_cast<float4 *>(orow + 8 * c) =
                     make_float4(oacc[0][r] * inv, oacc[1][r] * inv, oacc[2][r] * inv, oacc[3][r] * inv);
-                *reinterpret_cast<float4 *>(op + 8 * c + 4) =
+                *reinterpret_cast<float4 *>(orow + 8 * c + 4) =
                     make_float4(oacc[4][r] * inv, oacc[5][r] * inv, oacc[6][r] * inv, oacc[7][r] * inv);
             } else if constexpr (NB == 4) {
-                *reinterpret_cast<float4 *>(op + 4 * c) =
+                *reinterpret_cast<float4 *>(orow + 4 * c) =
                     make_float4(oacc[0][r] * inv, oacc[1][r] * inv, oacc[2][r] * inv, oacc[3][r] * inv);
             } else if constexpr (NB == 2) {
-                *reinterpret_cast<float2 *>(op + 2 * c) = make_float2(oacc[0][r] * inv, oacc[1][r] * inv);
+                *reinterpret_cast<float2 *>(orow + 2 * c) = make_float2(oacc[0][r] * inv, oacc[1][r] * inv);
             } else if constexpr (HD >= 32) {
-                op[c] = oacc[0][r] * inv;
+                orow[c] = oacc[0][r] * inv;
             } else {
-                if (c < HD) op[c] = oacc[0][r] * inv;
+                if (c < HD) orow[c] = oacc[0][r] * inv;
+            }
+        }
+    }
+    __syncthreads();
+    if (ks == 0 && my_tiles > 0) {
+        constexpr int ROW4 = HD / 4;  // float4 per output row
+#pragma unroll
+        for (int j = 0; j < (kTile * ROW4 + 63) / 64; ++j) {
+            const int idx = j * 64 + lane;
+            if (kTile * ROW4 % 64 == 0 || idx < kTile * ROW4) {
+                const int row = idx / ROW4;
+                const int c4 = idx % ROW4;
+                if (q0 + row < T)
+                    *reinterpret_cast<float4 *>(o + ((size_t)(q0 + row) * H + head) * HD + 4 * c4) =
+                        *reinterpret_cast<const float4 *>(ot + row * C::OS + 4 * c4);
             }
         }
     }
