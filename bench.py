@@ -232,6 +232,55 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+def decode_extras(eb, hip, dev, sc128) -> dict:
+    """Decode step GB/s at every BASELINE decode config (kv_write + attention, graph-launched,
+    caches rotated past the Infinity Cache)."""
+    out = {}
+    cfgs = [("qwen_L512", 16, 8, 128, 8192, 512, sc128),
+            ("qwen_L2048", 16, 8, 128, 8192, 2048, sc128),
+            ("qwen_L4096", 16, 8, 128, 8192, 4096, sc128),
+            ("mistral_keys8193", 32, 8, 128, 32768, 8192, sc128),
+            ("mistral_keys32768", 32, 8, 128, 32768, 32767, sc128),
+            ("gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0)]
+    for name, H, Hkv, hd, ms, pos, sc in cfgs:
+        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc)
+        w.run_steps(20)
+        t_step, _ = w.run_steps(500)
+        out[f"decode_{name}"] = {
+            "keys": pos + 1, "kv_bytes": w.kv_bytes, "ms_step": round(t_step, 5),
+            "GBs": round(w.kv_bytes / t_step / 1e6, 1),
+            "frac_hbm": round(w.kv_bytes / t_step / 1e6 / HBM_PEAK_GBS, 4)}
+        w.close()
+        del w
+        dev.synchronize()
+    return out
+
+
+def prefill_extras(eb, hip, dev, sc128) -> dict:
+    """Causal prefill TFLOP/s (2*H*hd*T*(T+1) algorithmic FLOPs) for the BASELINE prefill
+    configs, HIP events around back-to-back launches."""
+    out = {}
+    cfgs = [("qwen_T512", 16, 8, 128, 512, sc128),
+            ("qwen_T2048", 16, 8, 128, 2048, sc128),
+            ("qwen_T4096", 16, 8, 128, 4096, sc128),
+            ("mistral_T4096", 32, 8, 128, 4096, sc128),
+            ("gemma_T4096", 16, 8, 256, 4096, 1.0)]
+    for name, H, Hkv, hd, T, sc in cfgs:
+        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc)
+        for _ in range(3):
+            p.launch()
+        reps = 20 if T >= 2048 else 100
+        t = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+        tf_s = p.flops / (t * 1e-3) / 1e12
+        out[f"prefill_{name}"] = {
+            "gflop": round(p.flops / 1e9, 3), "ms": round(t, 4), "TFLOPs": round(tf_s, 2),
+            "mfma": "fp32 (v_mfma_f32_32x32x2_f32)",
+            "frac_fp32_mfma_peak": round(tf_s / FP32_MFMA_PEAK_TFLOPS, 4)}
+        del p
+        dev.synchronize()
+    return out
+
+
 def traffic_run(eb, hip, dev, sc128):
     """Dispatches for the HBM-traffic counter passes, each kernel launched directly (no
     graph) so that every dispatch is counted on its own:
@@ -260,6 +309,42 @@ def traffic_run(eb, hip, dev, sc128):
     print(json.dumps({"traffic_run": "done", "copy_bytes": rows * hkv * hd * 4}), flush=True)
 
 
+def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
+    """Per-kernel HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, KiB
+    per dispatch) over `bench.py --only traffic`. Each counter is scaled by what it reads
+    for the 256 MiB kv_write copy in that run (bytes copied / counter bytes), so that
+    traffic is in the same bytes as the algorithmic figures."""
+    import csv
+    import re
+
+    def load(path):
+        per = {}
+        for r in csv.DictReader(open(path)):
+            name = re.sub(r"\(anonymous namespace\)::", "", r["Kernel_Name"]).split("(")[0]
+            name = name.replace("void ", "").strip()
+            per.setdefault(name, []).append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in per.items()}
+
+    fetch, write = load(fetch_csv), load(write_csv)
+    copy_bytes = 65536 * 8 * 128 * 4
+    copy = "kv_write_vec4_kernel"
+    fs = copy_bytes / (fetch[copy] * 1024)
+    ws = copy_bytes / (write[copy] * 1024)
+    kernels = {k: {"fetch_bytes": round(fetch[k] * 1024 * fs), "write_bytes": round(write.get(k, 0) * 1024 * ws),
+                   "FETCH_SIZE_KiB": round(fetch[k], 1), "WRITE_SIZE_KiB": round(write.get(k, 0), 1)}
+               for k in fetch}
+    out = {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": kernels}
+    dk = next((k for k in kernels if k.startswith("decode_kernel<128, 2>")), None)
+    mk = next((k for k in kernels if k.startswith("decode_merge_kernel<128>")), None)
+    if dk:
+        t = kernels[dk]["fetch_bytes"] + kernels[dk]["write_bytes"]
+        if mk:
+            t += kernels[mk]["fetch_bytes"] + kernels[mk]["write_bytes"]
+        out["decode_qwen_L8191"] = t
+    json.dump(out, open(out_json, "w"), indent=1)
+    print(json.dumps(out, indent=1))
+
+
 # ------------------------------------------------------------------ main
 
 def main():
@@ -268,9 +353,17 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["headline", "all", "traffic"], default="all",
-                    help="traffic: a short run for rocprofv3 --pmc passes (see profiles/)")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
+                    help="no GPU: turn the counter_collection.csv files of the FETCH_SIZE and "
+                         "WRITE_SIZE passes over `--only traffic` into per-kernel HBM bytes")
+    ap.add_argument("--only", choices=["headline", "all", "prefill", "traffic"], default="all",
+                    help="headline: the decode line only; prefill: the prefill configs only "
+                         "(prints their timings, not the contract line); traffic: a short run "
+                         "for rocprofv3 --pmc passes")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the eyebrowse attention path is a single-device "
               "workload and this build has no multi-GPU path (run with --gpus 1).",
@@ -283,6 +376,9 @@ def main():
     sc128 = float(np.float32(1.0) / np.sqrt(np.float32(128)))
     if args.only == "traffic":
         traffic_run(eb, hip, dev, sc128)
+        return
+    if args.only == "prefill":
+        print(json.dumps(prefill_extras(eb, hip, dev, sc128)), flush=True)
         return
 
     # Headline: Qwen decode L=8191. A step is one kernel (kv_write + split-KV attention +
@@ -301,41 +397,8 @@ def main():
 
     extra = {}
     if args.only == "all":
-        dec_cfgs = [("qwen_L512", 16, 8, 128, 8192, 512, sc128),
-                    ("qwen_L2048", 16, 8, 128, 8192, 2048, sc128),
-                    ("qwen_L4096", 16, 8, 128, 8192, 4096, sc128),
-                    ("mistral_keys8193", 32, 8, 128, 32768, 8192, sc128),
-                    ("mistral_keys32768", 32, 8, 128, 32768, 32767, sc128),
-                    ("gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0)]
-        for name, H, Hkv, hd, ms, pos, sc in dec_cfgs:
-            w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc)
-            w.run_steps(20)
-            t_step, _ = w.run_steps(500)
-            extra[f"decode_{name}"] = {
-                "keys": pos + 1, "kv_bytes": w.kv_bytes, "ms_step": round(t_step, 5),
-                "GBs": round(w.kv_bytes / t_step / 1e6, 1),
-                "frac_hbm": round(w.kv_bytes / t_step / 1e6 / HBM_PEAK_GBS, 4)}
-            w.close()
-            del w
-            dev.synchronize()
-        pre_cfgs = [("qwen_T512", 16, 8, 128, 512, sc128),
-                    ("qwen_T2048", 16, 8, 128, 2048, sc128),
-                    ("qwen_T4096", 16, 8, 128, 4096, sc128),
-                    ("mistral_T4096", 32, 8, 128, 4096, sc128),
-                    ("gemma_T4096", 16, 8, 256, 4096, 1.0)]
-        for name, H, Hkv, hd, T, sc in pre_cfgs:
-            p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc)
-            for _ in range(3):
-                p.launch()
-            reps = 20 if T >= 2048 else 100
-            t = hip.time_loop(dev.stream, reps, lambda i: p.launch())
-            tf_s = p.flops / (t * 1e-3) / 1e12
-            extra[f"prefill_{name}"] = {
-                "gflop": round(p.flops / 1e9, 3), "ms": round(t, 4), "TFLOPs": round(tf_s, 2),
-                "mfma": "fp32 (v_mfma_f32_32x32x2_f32)",
-                "frac_fp32_mfma_peak": round(tf_s / FP32_MFMA_PEAK_TFLOPS, 4)}
-            del p
-            dev.synchronize()
+        extra.update(decode_extras(eb, hip, dev, sc128))
+        extra.update(prefill_extras(eb, hip, dev, sc128))
 
     line = {
         "metric": METRIC,

@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(const float *__r
                                                                 float *__restrict__ o, int h,
                                                                 int nsplit) {
     constexpr int GROUPS = HD >= kThreads ? 1 : kThreads / HD;
-    constexpr int kBatch = 8;
+    constexpr int kBatch = 16;  // 32 splits (one workgroup per CU) merge in one round trip
     __shared__ float s_m[GROUPS][HD < kThreads ? HD : kThreads];
     __shared__ float s_l[GROUPS][HD < kThreads ? HD : kThreads];
     __shared__ float s_a[GROUPS][HD < kThreads ? HD : kThreads];
