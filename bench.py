@@ -333,7 +333,16 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
     kernels = {k: {"fetch_bytes": round(fetch[k] * 1024 * fs), "write_bytes": round(write.get(k, 0) * 1024 * ws),
                    "FETCH_SIZE_KiB": round(fetch[k], 1), "WRITE_SIZE_KiB": round(write.get(k, 0), 1)}
                for k in fetch}
-    out = {"fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": kernels}
+    out = {"commands": [
+        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE --kernel-trace -f csv "
+        "-d $R/gpurun_out/pmc_fetch -o run -- python3 $R/bench.py --only traffic",
+        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc WRITE_SIZE --kernel-trace -f csv "
+        "-d $R/gpurun_out/pmc_write -o run -- python3 $R/bench.py --only traffic",
+        "python bench.py --pmc-summary gpurun_out/pmc_fetch/run_counter_collection.csv "
+        "gpurun_out/pmc_write/run_counter_collection.csv profiles/traffic.json"],
+        "calibration": "kv_write_vec4_kernel copying 256 MiB (65536 rows x 8 heads x 128 f32): "
+                       "scale = 268435456 / (counter KiB * 1024)",
+        "fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": kernels}
     dk = next((k for k in kernels if k.startswith("decode_kernel<128, 2>")), None)
     mk = next((k for k in kernels if k.startswith("decode_merge_kernel<128>")), None)
     if dk:
