@@ -85,8 +85,9 @@ size_t eb_pool_max_bytes(void);
  * buffer of the exact byte size exists (sizes <= eb_pool_max_bytes()). */
 eb_status eb_tensor_empty(eb_device *dev, const size_t *shape, size_t ndim, eb_dtype dt,
                           eb_tensor **out);
-/* Tensor::from_f32 / from_u32 (tensor.rs:241-267): a fresh, never-pooled buffer
- * initialised from host memory (n elements must equal the shape's element count). */
+/* Tensor::from_f32 / from_u32 (tensor.rs:241-267): a fresh buffer (never drawn from the
+ * pool) initialised from host memory (n elements must equal the shape's element count).
+ * Like every tensor it is recycled into the pool on release when small enough. */
 eb_status eb_tensor_from_f32(eb_device *dev, const size_t *shape, size_t ndim,
                              const float *data, size_t n, eb_tensor **out);
 eb_status eb_tensor_from_u32(eb_device *dev, const size_t *shape, size_t ndim,
