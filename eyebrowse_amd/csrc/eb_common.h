@@ -31,6 +31,43 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
+// The value held by lane i ^ 16 (v_permlane16_swap exchanges the odd 16-lane rows of one
+// operand with the even rows of the other; with both operands x, the first result holds
+// the lower neighbour's row on odd rows, the second the upper neighbour's on even rows).
+__device__ __forceinline__ float lane_xor16(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const bool odd_row = (__lane_id() >> 4) & 1;
+    return __builtin_bit_cast(float, odd_row ? r[0] : r[1]);
+}
+
+// The value held by lane i ^ 32 (v_permlane32_swap exchanges the wave's two halves).
+__device__ __forceinline__ float lane_xor32(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const bool upper = __lane_id() >= 32;
+    return __builtin_bit_cast(float, upper ? r[0] : r[1]);
+}
+
+// Reduce (sum or max) over the lanes that share lane bits [0, log2(FROM)): every lane
+// ends with the reduction over its class {i' : i' % FROM == i % FROM}. VALU lane
+// permutes only (DPP row rotations within 16 lanes, then the 16- and 32-lane swaps): a
+// rotation by 8 within a row pairs lane i with i ^ 8, and the rotations by 1, 2, 4 fold
+// a class's members within a row in any order, which a sum or max does not notice.
+template <int FROM, bool MAX>
+__device__ __forceinline__ float class_reduce(float x) {
+    static_assert(FROM == 1 || FROM == 2 || FROM == 4 || FROM == 8 || FROM == 16 ||
+                      FROM == 32 || FROM == 64, "power of two");
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    if constexpr (FROM <= 1) x = op(x, dpp<0x121>(x));  // row_ror:1
+    if constexpr (FROM <= 2) x = op(x, dpp<0x122>(x));  // row_ror:2
+    if constexpr (FROM <= 4) x = op(x, dpp<0x124>(x));  // row_ror:4
+    if constexpr (FROM <= 8) x = op(x, dpp<0x128>(x));  // row_ror:8
+    if constexpr (FROM <= 16) x = op(x, lane_xor16(x));
+    if constexpr (FROM <= 32) x = op(x, lane_xor32(x));
+    return x;
+}
+
 // 2^x on the hardware transcendental unit (v_exp_f32); exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -7,25 +7,28 @@
 // (crates/eyebrowse-nn/src/attention.rs:149-183).
 //
 // Pass 1, grid (Hkv * nsub) x nsplit, 256 threads per workgroup. Workgroup (col, split)
-// reduces keys [split*chunk, min((split+1)*chunk, pos+1)) for KV head col/nsub and the G
-// query heads that share it (GQA: every K/V row is read once for all of them):
+// reduces a 1/nsplit share of the keys for KV head col/nsub and the G query heads that
+// share it (GQA: every K/V row is read once for all of them):
 //  - a key row of HD floats is spread over LPK = HD/DPL lanes (DPL = 16 dims per lane),
-//    so a wave covers KPW = 64/LPK keys per step; loads are 128-bit and each instruction's
-//    lanes cover contiguous spans of the row;
+//    so a wave covers KPW = 64/LPK keys per step; the keys are dealt to the splits in
+//    blocks of KPW rows (split s owns blocks s, s + nsplit, ...), so that all workgroups
+//    together stream one contiguous stretch of the cache at a time;
+//  - loads are 128-bit raw buffer loads whose range check turns rows past the end into
+//    zeros (no clamping, no branches); two register buffers per wave keep the next
+//    iteration's loads in flight while the current one is consumed;
 //  - scores are lane-partial dot products summed across the LPK lanes with DPP;
 //  - each lane group keeps an online softmax (running max m, sum l, acc[DPL]) in the log2
-//    domain (scores times scale*log2(e), exponentials on v_exp_f32), updated once per U
-//    keys;
-//  - the wave's lane groups merge with shuffles, the 4 waves merge through LDS;
+//    domain (scores times scale*log2(e), exponentials on v_exp_f32);
+//  - the lane groups' states meet in LDS, where the workgroup combines them per head;
 //  - with one split the workgroup writes o directly; otherwise it writes its partial
 //    (m, l, acc[HD]) per head and pass 2 (decode_merge_kernel) computes
 //    o = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M). A second launch is cheaper here
 //    than merging in the last-arriving workgroup: on the 8-XCD part that needs an L2
 //    write-back fence in every workgroup.
-// Fused new-token write: when knew/vnew are given, key `pos` is read from them instead of
-// the cache, and the workgroup whose chunk holds `pos` (first head-subgroup) copies them
-// into cache row `pos`; nothing else touches that row in the launch, so the copy is exact
-// and race free.
+// Fused new-token write: when knew/vnew are given, rows 0..pos-1 come from the cache and
+// key `pos` from knew/vnew, folded in after the loop by the split that owns its block;
+// that split's first head-subgroup workgroup also copies knew/vnew into cache row `pos`.
+// Nothing else touches that row in the launch, so the copy is exact and race free.
 //
 // The result is softmax(scale * q K^T) V over keys 0..=pos; it differs from the
 // reference's 3-pass f32 softmax only by rounding (summation order, exp2 vs expf).
@@ -34,44 +37,69 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
-// Wave steps per softmax update: 4 when at most 2 query heads share a workgroup, else 2
-// (register budget: the q fragment and accumulators grow with the head count). A
-// positive EB_DECODE_U forces one value for all shapes.
+// Wave steps per iteration (and per softmax update); a positive EB_DECODE_U overrides
+// the default of one.
 #ifndef EB_DECODE_U
 #define EB_DECODE_U 0
 #endif
-// 1: two register buffers per wave (next iteration's loads issued before the current one
-// is consumed); 0: one buffer, latency hidden by other waves.
-#ifndef EB_DECODE_PIPELINE
-#define EB_DECODE_PIPELINE 1
-#endif
-// Workgroups per CU the register allocation must allow (launch-bounds minimum).
+// Workgroups per CU the register allocation must allow (launch-bounds minimum); 0 picks
+// 2 when at most 2 query heads share a workgroup (then everything fits 256 VGPRs), else 1.
 #ifndef EB_DECODE_MINB
-#define EB_DECODE_MINB 1
+#define EB_DECODE_MINB 0
 #endif
 
 namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kMaxSplits = 256;  // per column; bounds the merge's LDS weights
+constexpr int kMaxSplits = 256;  // per column
+constexpr int kRawBufferFlags = 0x00020000;  // gfx9 raw buffer: 32-bit data, range checked
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int HD, int G>
 struct DecodeShape {
     static constexpr int DPL = HD >= 16 ? 16 : HD;  // dims per lane
     static constexpr int LPK = HD / DPL;            // lanes per key row
     static constexpr int KPW = 64 / LPK;            // keys per wave step
-    static constexpr int NV4 = DPL / 4;             // float4 loads per lane per row
-    static constexpr int U = EB_DECODE_U > 0 ? EB_DECODE_U : (G <= 2 ? 4 : 2);
+    static constexpr int NV4 = DPL / 4;             // 16-byte loads per lane per row
+    // Wave steps per iteration: each of the two register buffers holds U*NV4*2 16-byte
+    // loads per lane. One step per buffer keeps everything in VGPRs; with the workgroups
+    // of a CU that is as much in flight as the HBM rewards.
+    static constexpr int U = EB_DECODE_U > 0 ? EB_DECODE_U : 1;
     static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
+    // Epilogue LDS: NS lane-group states of SS floats (G heads of HD, padded by 4 floats
+    // so that the lane groups' 16-byte writes fall in different banks), plus m, l, the
+    // weights, the weighted sums and the per-head reference max.
+    static constexpr int NS = kWaves * KPW;
+    static constexpr int SS = G * HD + 4;
+    static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)NS * SS + 4 * G * NS + G);
     static_assert(DPL % 4 == 0 && LPK <= 16, "head_dim must be a multiple of 4, at most 256");
 };
 
-// Element offset (within a row) of float4 number i held by dim slice `ls`.
+// Byte offset (within a row) of 16-byte load number i of dim slice `ls`.
 template <int HD>
-__device__ __forceinline__ int dim_of(int i, int ls) {
-    return (i * DecodeShape<HD, 1>::LPK + ls) * 4;
+__device__ __forceinline__ int dim_byte(int i, int ls) {
+    return (i * DecodeShape<HD, 1>::LPK + ls) * 16;
+}
+
+// Raw buffer resource over [p, p + nbytes). The operands are made wave-uniform explicitly
+// so that the descriptor lives in SGPRs (a per-lane descriptor costs a loop per load).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *p, int nbytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    void *u = reinterpret_cast<void *>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(nbytes),
+                                             kRawBufferFlags);
+}
+
+__device__ __forceinline__ f32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset,
+                                               int soffset = 0) {
+    return __builtin_bit_cast(f32x4,
+                              __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
 }
 
 struct DecodeArgs {
@@ -85,12 +113,12 @@ struct DecodeArgs {
     float *o;
     float *part_acc;   // [nsplit, h, HD]
     float *part_ml;    // [nsplit, h, 2]
-    int h, hkv, g, keys, chunk, nsplit;
+    int h, hkv, g, keys, nsplit;
     float scale_log2;
 };
 
 template <int HD, int G>
-__global__ __launch_bounds__(kThreads, EB_DECODE_MINB) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G <= 2 ? 2 : 1))) void decode_kernel(DecodeArgs a) {
     using S = DecodeShape<HD, G>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
@@ -101,90 +129,101 @@ __global__ __launch_bounds__(kThreads, EB_DECODE_MINB) void decode_kernel(Decode
     const int kvh = col / nsub;
     const int head0 = kvh * a.g + (col % nsub) * G;
     const int split = blockIdx.y;
-    const int c0 = split * a.chunk;
-    const int c1 = min(c0 + a.chunk, a.keys);
     const int kg = lane / S::LPK;
     const int ls = lane % S::LPK;
     const int pos = a.keys - 1;
-    const bool has_new = a.knew != nullptr;
-    const size_t row_stride = (size_t)a.hkv * HD;
+    // Keys are dealt to the splits in blocks of KPW rows (one wave step): split s owns
+    // blocks s, s + nsplit, s + 2*nsplit, ... At any moment the workgroups of all splits
+    // and KV heads together stream one contiguous stretch of the cache, which the HBM
+    // serves faster than nsplit separate chunks, and every split gets the same share.
+    // With a new token, rows [0, pos) come from the cache and key `pos` from knew/vnew,
+    // folded in by the split that owns its block.
+    const int ce = a.knew != nullptr ? pos : a.keys;
+    const bool tail_new = a.knew != nullptr && split == (pos / S::KPW) % a.nsplit;
+    const int nblk = (ce + S::KPW - 1) / S::KPW;
+    const int my_blk = nblk > split ? (nblk - split + a.nsplit - 1) / a.nsplit : 0;
+    const int row_bytes = a.hkv * HD * 4;
 
-    // New-token write: one workgroup per KV head copies the row into the cache.
-    if (has_new && (col % nsub) == 0 && pos >= c0 && pos < c1) {
+    // New-token write: one workgroup per KV head copies the row into the cache. No
+    // workgroup reads cache row `pos` in this launch.
+    if (tail_new && (col % nsub) == 0) {
+        const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
         for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
-            const size_t dst = (size_t)pos * row_stride + (size_t)kvh * HD + 4 * i;
-            *reinterpret_cast<float4 *>(a.kc_w + dst) =
-                *reinterpret_cast<const float4 *>(a.knew + (size_t)kvh * HD + 4 * i);
-            *reinterpret_cast<float4 *>(a.vc_w + dst) =
-                *reinterpret_cast<const float4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
+            *reinterpret_cast<f32x4 *>(a.kc_w + dst + 4 * i) =
+                *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
+            *reinterpret_cast<f32x4 *>(a.vc_w + dst + 4 * i) =
+                *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
         }
     }
 
-    float qr[G][S::DPL];
+    f32x4 qr[G][NV4];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-        for (int i = 0; i < NV4; ++i) {
-            float4 t = *reinterpret_cast<const float4 *>(a.q + (size_t)(head0 + gi) * HD +
-                                                         dim_of<HD>(i, ls));
-            qr[gi][4 * i + 0] = t.x;
-            qr[gi][4 * i + 1] = t.y;
-            qr[gi][4 * i + 2] = t.z;
-            qr[gi][4 * i + 3] = t.w;
-        }
+        for (int i = 0; i < NV4; ++i)
+            qr[gi][i] = *reinterpret_cast<const f32x4 *>(
+                reinterpret_cast<const char *>(a.q + (size_t)(head0 + gi) * HD) + dim_byte<HD>(i, ls));
 
-    float m[G], l[G], acc[G][S::DPL];
+    float m[G], l[G];
+    f32x4 acc[G][NV4];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
         m[gi] = -INFINITY;
         l[gi] = 0.0f;
 #pragma unroll
-        for (int d = 0; d < S::DPL; ++d) acc[gi][d] = 0.0f;
+        for (int i = 0; i < NV4; ++i) acc[gi][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
+    // Iteration `it` covers the split's local blocks it*U*kWaves .. +U*kWaves; wave step
+    // (u, wave) reads local block it*U*kWaves + u*kWaves + wave, i.e. global rows
+    // ((that)*nsplit + split)*KPW + kg. Each iteration gets buffer resources based at its
+    // first global row (64-bit pointer arithmetic on the scalar unit), so the per-lane
+    // offsets are the same for every iteration and stay far below 2^31; rows at or past
+    // `ce` are out of range and read as zeros without touching memory.
+    const int blk_stride = U * kWaves * a.nsplit;  // global blocks per iteration
+    int rowof[U], voff[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        rowof[u] = ((u * kWaves + wave) * a.nsplit + split) * S::KPW + kg;  // minus it0
+        voff[u] = rowof[u] * row_bytes + dim_byte<HD>(0, ls);
+    }
     const float *kbase = a.kc + (size_t)kvh * HD;
     const float *vbase = a.vc + (size_t)kvh * HD;
-
-    // One iteration = U wave steps of KPW keys. Two register buffers: the next
-    // iteration's K/V loads are issued before the current one is consumed, so the wave
-    // keeps a full iteration of loads in flight while it computes.
-    auto load_iter = [&](int base, float4 (&kv)[U][NV4], float4 (&vv)[U][NV4],
-                         bool (&valid)[U]) {
+    auto rows_from = [&](int it) { return it * blk_stride * S::KPW; };
+    auto load_iter = [&](int it, f32x4 (&kv)[U][NV4], f32x4 (&vv)[U][NV4]) {
+        const int r0 = rows_from(it);
+        const int left = min(ce - r0, blk_stride * S::KPW);  // rows in range, window-capped
+        const int nbytes = left > 0 ? (left - 1) * row_bytes + HD * 4 : 0;
+        const size_t off = (size_t)r0 * a.hkv * HD;
+        const __amdgpu_buffer_rsrc_t kres = make_rsrc(kbase + off, nbytes);
+        const __amdgpu_buffer_rsrc_t vres = make_rsrc(vbase + off, nbytes);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int key = base + (u * kWaves + wave) * S::KPW + kg;
-            valid[u] = key < c1;
-            const int kk = valid[u] ? key : c1 - 1;
-            const float *kp = kbase + (size_t)kk * row_stride;
-            const float *vp = vbase + (size_t)kk * row_stride;
-            if (has_new && kk == pos) {
-                kp = a.knew + (size_t)kvh * HD;
-                vp = a.vnew + (size_t)kvh * HD;
-            }
+        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
-                kv[u][i] = *reinterpret_cast<const float4 *>(kp + dim_of<HD>(i, ls));
-                vv[u][i] = *reinterpret_cast<const float4 *>(vp + dim_of<HD>(i, ls));
+                // The dim offset goes in the scalar offset: the row offsets stay the only
+                // per-lane values (a hoisted per-load address would cost a VGPR each).
+                // Range checks decide by row either way, since a row's dims end within
+                // its HD*4 bytes.
+                kv[u][i] = buffer_load16(kres, voff[u], i * S::LPK * 16);
+                vv[u][i] = buffer_load16(vres, voff[u], i * S::LPK * 16);
             }
-        }
     };
-    auto consume_iter = [&](const float4 (&kv)[U][NV4], const float4 (&vv)[U][NV4],
-                            const bool (&valid)[U]) {
+    // Online-softmax update of every head with the U rows of one iteration (rows at or
+    // past `ce` are masked out).
+    auto consume_iter = [&](int it, const f32x4 (&kv)[U][NV4], const f32x4 (&vv)[U][NV4]) {
+        const int r0 = rows_from(it);
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             float sc[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                float s = 0.0f;
+                f32x4 t = qr[gi][0] * kv[u][0];
 #pragma unroll
-                for (int i = 0; i < NV4; ++i) {
-                    s += qr[gi][4 * i + 0] * kv[u][i].x;
-                    s += qr[gi][4 * i + 1] * kv[u][i].y;
-                    s += qr[gi][4 * i + 2] * kv[u][i].z;
-                    s += qr[gi][4 * i + 3] * kv[u][i].w;
-                }
-                s = eb::group_sum<S::LPK>(s);
-                sc[u] = valid[u] ? s * a.scale_log2 : -INFINITY;
+                for (int i = 1; i < NV4; ++i) t += qr[gi][i] * kv[u][i];
+                float sv = (t.x + t.y) + (t.z + t.w);
+                sv = eb::group_sum<S::LPK>(sv);
+                sc[u] = (r0 + rowof[u] < ce) ? sv * a.scale_log2 : -INFINITY;
             }
             float mloc = sc[0];
 #pragma unroll
@@ -202,103 +241,119 @@ __global__ __launch_bounds__(kThreads, EB_DECODE_MINB) void decode_kernel(Decode
             l[gi] = l[gi] * corr + psum;
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
-                float a0 = acc[gi][4 * i + 0] * corr, a1 = acc[gi][4 * i + 1] * corr;
-                float a2 = acc[gi][4 * i + 2] * corr, a3 = acc[gi][4 * i + 3] * corr;
+                f32x4 t = acc[gi][i] * corr;
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    a0 += p[u] * vv[u][i].x;
-                    a1 += p[u] * vv[u][i].y;
-                    a2 += p[u] * vv[u][i].z;
-                    a3 += p[u] * vv[u][i].w;
-                }
-                acc[gi][4 * i + 0] = a0;
-                acc[gi][4 * i + 1] = a1;
-                acc[gi][4 * i + 2] = a2;
-                acc[gi][4 * i + 3] = a3;
+                for (int u = 0; u < U; ++u) t += p[u] * vv[u][i];
+                acc[gi][i] = t;
             }
             m[gi] = mnew;
         }
     };
 
-    if constexpr (!EB_DECODE_PIPELINE) {
-        for (int base = c0; base < c1; base += S::KEYS_PER_ITER) {
-            float4 kv[U][NV4], vv[U][NV4];
-            bool ok[U];
-            load_iter(base, kv, vv, ok);
-            consume_iter(kv, vv, ok);
-        }
-    } else {
-        float4 kA[U][NV4], vA[U][NV4], kB[U][NV4], vB[U][NV4];
-        bool okA[U], okB[U];
-        // Counted loop over pairs of iterations with unconditional loads: a load issued
-        // under a branch would be sunk by the compiler next to its use, draining the queue.
-        // Iterations past c1 load clamped rows and are fully masked (valid = false), which
-        // leaves the softmax state unchanged.
-        const int n_iter = (c1 - c0 + S::KEYS_PER_ITER - 1) / S::KEYS_PER_ITER;
-        load_iter(c0, kA, vA, okA);
-        for (int it = 0; it < n_iter; it += 2) {
-            load_iter(c0 + (it + 1) * S::KEYS_PER_ITER, kB, vB, okB);
+    // Iterations run in pairs (A, B): both buffers are loaded before the first is used
+    // and each is refilled right after it is consumed. The loop is counted and its loads
+    // unconditional (a load under a branch is sunk next to its use by the compiler,
+    // draining the queue); an iteration past the split's blocks reads zeros and is masked.
+    const int n_iter = (my_blk + U * kWaves - 1) / (U * kWaves);
+    const int n_pairs = (n_iter + 1) / 2;
+    if (n_pairs > 0) {
+        f32x4 kA[U][NV4], vA[U][NV4], kB[U][NV4], vB[U][NV4];
+        load_iter(0, kA, vA);
+        load_iter(1, kB, vB);
+        for (int pr = 1; pr < n_pairs; ++pr) {
             __builtin_amdgcn_sched_barrier(0);
-            consume_iter(kA, vA, okA);
-            load_iter(c0 + (it + 2) * S::KEYS_PER_ITER, kA, vA, okA);
+            consume_iter(2 * pr - 2, kA, vA);
+            load_iter(2 * pr, kA, vA);
             __builtin_amdgcn_sched_barrier(0);
-            consume_iter(kB, vB, okB);
+            consume_iter(2 * pr - 1, kB, vB);
+            load_iter(2 * pr + 1, kB, vB);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        consume_iter(2 * n_pairs - 2, kA, vA);
+        consume_iter(2 * n_pairs - 1, kB, vB);
     }
 
-    // Merge the KPW lane groups of this wave (lanes with equal `ls`).
+    // Key `pos` from knew/vnew, folded into the first lane group of wave 0.
+    if (tail_new && wave == 0) {
+        f32x4 kn[NV4], vn[NV4];
 #pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        float M = m[gi];
-#pragma unroll
-        for (int off = S::LPK; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
-        const float mref = (M == -INFINITY) ? 0.0f : M;
-        const float sc = eb::fast_exp2(m[gi] - mref);
-        float L = l[gi] * sc;
-#pragma unroll
-        for (int off = S::LPK; off < 64; off <<= 1) L += __shfl_xor(L, off);
-        l[gi] = L;
-        m[gi] = M;
-#pragma unroll
-        for (int d = 0; d < S::DPL; ++d) {
-            float x = acc[gi][d] * sc;
-#pragma unroll
-            for (int off = S::LPK; off < 64; off <<= 1) x += __shfl_xor(x, off);
-            acc[gi][d] = x;
+        for (int i = 0; i < NV4; ++i) {
+            kn[i] = *reinterpret_cast<const f32x4 *>(
+                reinterpret_cast<const char *>(a.knew + (size_t)kvh * HD) + dim_byte<HD>(i, ls));
+            vn[i] = *reinterpret_cast<const f32x4 *>(
+                reinterpret_cast<const char *>(a.vnew + (size_t)kvh * HD) + dim_byte<HD>(i, ls));
         }
-    }
-
-    __shared__ float s_acc[kWaves][G][HD];
-    __shared__ float s_m[kWaves][G];
-    __shared__ float s_l[kWaves][G];
-    if (kg == 0) {
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
+            f32x4 t = qr[gi][0] * kn[0];
 #pragma unroll
-            for (int i = 0; i < NV4; ++i)
+            for (int i = 1; i < NV4; ++i) t += qr[gi][i] * kn[i];
+            const float s = eb::group_sum<S::LPK>((t.x + t.y) + (t.z + t.w)) * a.scale_log2;
+            if (kg == 0) {
+                const float mnew = fmaxf(m[gi], s);
+                const float corr = eb::fast_exp2(m[gi] - mnew);
+                const float p = eb::fast_exp2(s - mnew);
+                l[gi] = l[gi] * corr + p;
 #pragma unroll
-                for (int c = 0; c < 4; ++c) s_acc[wave][gi][dim_of<HD>(i, ls) + c] = acc[gi][4 * i + c];
-            if (ls == 0) {
-                s_m[wave][gi] = m[gi];
-                s_l[wave][gi] = l[gi];
+                for (int i = 0; i < NV4; ++i) acc[gi][i] = acc[gi][i] * corr + p * vn[i];
+                m[gi] = mnew;
             }
         }
     }
-    __syncthreads();
 
+    // Epilogue: every lane group's state (m, l, acc) goes to LDS, then the workgroup
+    // combines the NS states of each head with one weight per state, 2^(m_s - M): a few
+    // LDS reads and FMAs per output instead of cross-lane reductions.
+    constexpr int NS = S::NS;
+    constexpr int SS = S::SS;
+    extern __shared__ float smem[];
+    float *s_acc = smem;              // [NS][SS]: state s, then head gi, then dim
+    float *s_m = s_acc + NS * SS;     // [G][NS]
+    float *s_l = s_m + G * NS;        // [G][NS]
+    float *s_w = s_l + G * NS;        // [G][NS] weights
+    float *s_lw = s_w + G * NS;       // [G][NS] weighted sums
+    float *s_M = s_lw + G * NS;       // [G] reference max per head
+    const int st = wave * S::KPW + kg;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+#pragma unroll
+        for (int i = 0; i < NV4; ++i)
+            *reinterpret_cast<f32x4 *>(s_acc + st * SS + gi * HD + dim_byte<HD>(i, ls) / 4) =
+                acc[gi][i];
+        if (ls == 0) {
+            s_m[gi * NS + st] = m[gi];
+            s_l[gi * NS + st] = l[gi];
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * NS; idx += kThreads) {
+        const int gi = idx / NS;
+        float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NS; j += 4) {
+            const f32x4 mm = *reinterpret_cast<const f32x4 *>(s_m + gi * NS + j);
+            M = fmaxf(M, fmaxf(fmaxf(mm.x, mm.y), fmaxf(mm.z, mm.w)));
+        }
+        const float mref = (M == -INFINITY) ? 0.0f : M;
+        const float w = eb::fast_exp2(s_m[idx] - mref);
+        s_w[idx] = w;
+        s_lw[idx] = w * s_l[idx];
+        if (idx % NS == 0) s_M[gi] = M;
+    }
+    __syncthreads();
     for (int idx = threadIdx.x; idx < G * HD; idx += kThreads) {
         const int gi = idx / HD;
         const int d = idx % HD;
-        float M = s_m[0][gi];
+        float A = 0.0f, L = 0.0f;
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][gi]);
-        const float mref = (M == -INFINITY) ? 0.0f : M;
-        float L = 0.0f, A = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float sc = eb::fast_exp2(s_m[w][gi] - mref);
-            L += s_l[w][gi] * sc;
-            A += s_acc[w][gi][d] * sc;
+        for (int j = 0; j < NS; j += 4) {
+            const f32x4 w4 = *reinterpret_cast<const f32x4 *>(s_w + gi * NS + j);
+            const f32x4 lw4 = *reinterpret_cast<const f32x4 *>(s_lw + gi * NS + j);
+            A += w4.x * s_acc[(j + 0) * SS + gi * HD + d];
+            A += w4.y * s_acc[(j + 1) * SS + gi * HD + d];
+            A += w4.z * s_acc[(j + 2) * SS + gi * HD + d];
+            A += w4.w * s_acc[(j + 3) * SS + gi * HD + d];
+            L += (lw4.x + lw4.y) + (lw4.z + lw4.w);
         }
         const int hh = head0 + gi;
         if (a.nsplit == 1) {
@@ -306,7 +361,7 @@ __global__ __launch_bounds__(kThreads, EB_DECODE_MINB) void decode_kernel(Decode
         } else {
             a.part_acc[((size_t)split * a.h + hh) * HD + d] = A;
             if (d == 0) {
-                a.part_ml[((size_t)split * a.h + hh) * 2 + 0] = M;
+                a.part_ml[((size_t)split * a.h + hh) * 2 + 0] = s_M[gi];
                 a.part_ml[((size_t)split * a.h + hh) * 2 + 1] = L;
             }
         }
@@ -314,87 +369,89 @@ __global__ __launch_bounds__(kThreads, EB_DECODE_MINB) void decode_kernel(Decode
 }
 
 // Log-sum-exp merge of the split partials (a second launch, so the partials written by
-// every XCD are visible without in-kernel fences): one 256-thread block per query head.
-// Thread (grp, d), GROUPS = 256/HD groups, folds splits s = grp, grp + GROUPS, ... into a
-// running (M, L, A) in batches of kBatch splits whose loads are all issued before any is
-// used, so a merge costs about ceil(nsplit / (GROUPS * kBatch)) memory round trips. The
+// every XCD are visible without in-kernel fences). Grid (h, HD / DS): a workgroup owns DS
+// dims of one head; thread (grp, d) of GROUPS = 256/DS groups folds splits grp,
+// grp + GROUPS, ... into a running (M, L, A), issuing a batch of kBatch splits' loads
+// before using any, so up to GROUPS*kBatch splits merge in one memory round trip. The
 // groups then combine through LDS: o[h][d] = A / L.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(const float *__restrict__ part_acc,
                                                                 const float *__restrict__ part_ml,
                                                                 float *__restrict__ o, int h,
                                                                 int nsplit) {
-    constexpr int GROUPS = HD >= kThreads ? 1 : kThreads / HD;
-    constexpr int kBatch = 16;  // 32 splits (one workgroup per CU) merge in one round trip
-    __shared__ float s_m[GROUPS][HD < kThreads ? HD : kThreads];
-    __shared__ float s_l[GROUPS][HD < kThreads ? HD : kThreads];
-    __shared__ float s_a[GROUPS][HD < kThreads ? HD : kThreads];
+    constexpr int DS = HD < 64 ? HD : 64;
+    constexpr int GROUPS = kThreads / DS;
+    constexpr int kBatch = 16;
+    __shared__ float s_m[GROUPS][DS];
+    __shared__ float s_l[GROUPS][DS];
+    __shared__ float s_a[GROUPS][DS];
     const int hh = blockIdx.x;
-    const int tid = threadIdx.x;
-    const size_t stride_acc = (size_t)h * HD;
-    const size_t stride_ml = (size_t)h * 2;
-
-    for (int d0 = 0; d0 < HD; d0 += kThreads) {
-        const int dl = tid % (HD < kThreads ? HD : kThreads);
-        const int d = d0 + dl;
-        const int grp = tid / (HD < kThreads ? HD : kThreads);
-        float M = -INFINITY, L = 0.0f, A = 0.0f;
-        if (grp < GROUPS && d < HD) {
-            const float *pa = part_acc + (size_t)hh * HD + d;
-            const float *pm = part_ml + (size_t)hh * 2;
-            for (int s0 = grp; s0 < nsplit; s0 += GROUPS * kBatch) {
-                float bm[kBatch], bl[kBatch], ba[kBatch];
+    const int dl = threadIdx.x % DS;
+    const int grp = threadIdx.x / DS;
+    const int d = blockIdx.y * DS + dl;
+    // Buffer resources over the partials: a split past nsplit is out of range and reads
+    // zeros (masked below), so the batch needs no clamping and its offsets are affine.
+    const __amdgpu_buffer_rsrc_t racc = make_rsrc(part_acc, nsplit * h * HD * 4);
+    const __amdgpu_buffer_rsrc_t rml = make_rsrc(part_ml, nsplit * h * 2 * 4);
+    const int acc_step = GROUPS * h * HD * 4, ml_step = GROUPS * h * 2 * 4;
+    float M = -INFINITY, L = 0.0f, A = 0.0f;
+    for (int s0 = grp; s0 < nsplit; s0 += GROUPS * kBatch) {
+        float2 bml[kBatch];
+        float ba[kBatch];
+        const int acc0 = ((s0 * h + hh) * HD + d) * 4, ml0 = (s0 * h + hh) * 2 * 4;
 #pragma unroll
-                for (int j = 0; j < kBatch; ++j) {
-                    const int s = s0 + j * GROUPS;
-                    const bool ok = s < nsplit;
-                    bm[j] = ok ? pm[(size_t)s * stride_ml] : -INFINITY;
-                    bl[j] = ok ? pm[(size_t)s * stride_ml + 1] : 0.0f;
-                    ba[j] = ok ? pa[(size_t)s * stride_acc] : 0.0f;
-                }
-                float bM = bm[0];
-#pragma unroll
-                for (int j = 1; j < kBatch; ++j) bM = fmaxf(bM, bm[j]);
-                const float Mn = fmaxf(M, bM);
-                const float mref = (Mn == -INFINITY) ? 0.0f : Mn;
-                const float c = eb::fast_exp2(M - mref);
-                L *= c;
-                A *= c;
-#pragma unroll
-                for (int j = 0; j < kBatch; ++j) {
-                    const float w = eb::fast_exp2(bm[j] - mref);
-                    L += w * bl[j];
-                    A += w * ba[j];
-                }
-                M = Mn;
-            }
-            s_m[grp][dl] = M;
-            s_l[grp][dl] = L;
-            s_a[grp][dl] = A;
+        for (int j = 0; j < kBatch; ++j) {
+            bml[j] = __builtin_bit_cast(
+                float2, __builtin_amdgcn_raw_buffer_load_b64(rml, ml0 + j * ml_step, 0, 0));
+            ba[j] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(racc, acc0 + j * acc_step, 0, 0));
         }
-        __syncthreads();
-        if (tid < (HD < kThreads ? HD : kThreads) && d < HD) {
-            float Mt = s_m[0][tid];
+        // Every load of the batch is issued before the first result is used (otherwise the
+        // running max below is scheduled between the loads, one round trip each); splits
+        // past nsplit are masked here, after the loads.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int g2 = 1; g2 < GROUPS; ++g2) Mt = fmaxf(Mt, s_m[g2][tid]);
-            const float mref = (Mt == -INFINITY) ? 0.0f : Mt;
-            float Lt = 0.0f, At = 0.0f;
+        for (int j = 0; j < kBatch; ++j)
+            if (s0 + j * GROUPS >= nsplit) bml[j].x = -INFINITY;
+        float bM = bml[0].x;
 #pragma unroll
-            for (int g2 = 0; g2 < GROUPS; ++g2) {
-                const float w = eb::fast_exp2(s_m[g2][tid] - mref);
-                Lt += w * s_l[g2][tid];
-                At += w * s_a[g2][tid];
-            }
-            o[(size_t)hh * HD + d] = At / Lt;
+        for (int j = 1; j < kBatch; ++j) bM = fmaxf(bM, bml[j].x);
+        const float Mn = fmaxf(M, bM);
+        const float mref = (Mn == -INFINITY) ? 0.0f : Mn;
+        const float c = eb::fast_exp2(M - mref);
+        L *= c;
+        A *= c;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const float w = eb::fast_exp2(bml[j].x - mref);
+            L += w * bml[j].y;
+            A += w * ba[j];
         }
-        __syncthreads();
+        M = Mn;
+    }
+    s_m[grp][dl] = M;
+    s_l[grp][dl] = L;
+    s_a[grp][dl] = A;
+    __syncthreads();
+    if (grp == 0) {
+        float Mt = s_m[0][dl];
+#pragma unroll
+        for (int g2 = 1; g2 < GROUPS; ++g2) Mt = fmaxf(Mt, s_m[g2][dl]);
+        const float mref = (Mt == -INFINITY) ? 0.0f : Mt;
+        float Lt = 0.0f, At = 0.0f;
+#pragma unroll
+        for (int g2 = 0; g2 < GROUPS; ++g2) {
+            const float w = eb::fast_exp2(s_m[g2][dl] - mref);
+            Lt += w * s_l[g2][dl];
+            At += w * s_a[g2][dl];
+        }
+        o[(size_t)hh * HD + d] = At / Lt;
     }
 }
 
 struct DecodePlan {
-    int G = 1;       // query heads per workgroup (a power of two dividing h/hkv, <= 8)
+    int G = 1;       // query heads per workgroup (1, 2 or 4, dividing h/hkv)
     int nsub = 1;    // workgroups per KV head along the head axis
-    int chunk = 0;   // keys per split
     int nsplit = 1;  // splits along the key axis
 };
 
@@ -413,14 +470,13 @@ int keys_per_iter_g(size_t hd) {
 
 int keys_per_iter(size_t hd, int G) {
     switch (G) {
-        case 8: return keys_per_iter_g<8>(hd);
         case 4: return keys_per_iter_g<4>(hd);
         case 2: return keys_per_iter_g<2>(hd);
         default: return keys_per_iter_g<1>(hd);
     }
 }
 
-// Workgroups to aim for per CU: enough waves in flight to cover HBM latency.
+// Workgroups to aim for per CU.
 int wgs_per_cu() {
     static int v = [] {
         const char *e = std::getenv("EB_DECODE_WGS_PER_CU");
@@ -433,43 +489,59 @@ int wgs_per_cu() {
 DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count) {
     DecodePlan p;
     const size_t g = h / hkv;
-    p.G = (g % 8 == 0) ? 8 : (g % 4 == 0) ? 4 : (g % 2 == 0) ? 2 : 1;
+    // At most 4 query heads per workgroup: their q fragments and accumulators, plus two
+    // K/V register buffers, must fit the register file without spilling.
+    p.G = (g % 4 == 0) ? 4 : (g % 2 == 0) ? 2 : 1;
     p.nsub = (int)(g / p.G);
     const size_t keys = pos + 1;
     const size_t cols = hkv * (size_t)p.nsub;
-    const size_t kpi = (size_t)keys_per_iter(hd, p.G);
+    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G);
+    // Enough workgroups to cover the CUs, but at least one pair of iterations per split.
     const size_t target = (size_t)cu_count * (size_t)wgs_per_cu();
-    const size_t want = std::max<size_t>(1, target / cols);
-    size_t chunk = (keys + want - 1) / want;
-    chunk = std::max(kpi, (chunk + kpi - 1) / kpi * kpi);
-    size_t nsplit = (keys + chunk - 1) / chunk;
-    if (nsplit > (size_t)kMaxSplits) {
-        chunk = (keys + kMaxSplits - 1) / kMaxSplits;
-        chunk = (chunk + kpi - 1) / kpi * kpi;
-        nsplit = (keys + chunk - 1) / chunk;
-    }
-    p.chunk = (int)chunk;
+    size_t nsplit = std::max<size_t>(1, target / cols);
+    nsplit = std::min(nsplit, std::max<size_t>(1, keys / (2 * iter_rows)));
+    nsplit = std::min(nsplit, (size_t)kMaxSplits);
+    // An iteration's loads address a window of iter_rows * nsplit cache rows from one
+    // base with 32-bit offsets: keep the window under 2^30 bytes.
+    const size_t row_bytes = hkv * hd * sizeof(float);
+    while (nsplit > 1 && iter_rows * nsplit * row_bytes > ((size_t)1 << 30)) nsplit /= 2;
     p.nsplit = (int)nsplit;
     return p;
 }
 
 template <int HD, int G>
-void launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+    using S = DecodeShape<HD, G>;
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    if (S::LDS_BYTES > 64 * 1024)
+        std::call_once(once, [&] {
+            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_kernel<HD, G>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)S::LDS_BYTES);
+        });
+    if (attr_err != hipSuccess) return attr_err;
     dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
-    decode_kernel<HD, G><<<grid, kThreads, 0, st>>>(a);
+    decode_kernel<HD, G><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
+    return hipSuccess;
 }
 
 template <int HD>
-void launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+    hipError_t e;
     switch (p.G) {
-        case 8: launch_g<HD, 8>(st, p, a); break;
-        case 4: launch_g<HD, 4>(st, p, a); break;
-        case 2: launch_g<HD, 2>(st, p, a); break;
-        default: launch_g<HD, 1>(st, p, a); break;
+        case 4: e = launch_g<HD, 4>(st, p, a); break;
+        case 2: e = launch_g<HD, 2>(st, p, a); break;
+        default: e = launch_g<HD, 1>(st, p, a); break;
     }
-    if (p.nsplit > 1)
-        decode_merge_kernel<HD><<<(unsigned)a.h, kThreads, 0, st>>>(a.part_acc, a.part_ml, a.o,
-                                                                    a.h, p.nsplit);
+    if (e != hipSuccess) return e;
+    if (p.nsplit > 1) {
+        constexpr int DS = HD < 64 ? HD : 64;
+        dim3 grid((unsigned)a.h, (unsigned)(HD / DS));
+        decode_merge_kernel<HD><<<grid, kThreads, 0, st>>>(a.part_acc, a.part_ml, a.o, a.h,
+                                                          p.nsplit);
+    }
+    return hipSuccess;
 }
 
 }  // namespace
@@ -490,8 +562,10 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              float scale, float *ws, size_t ws_floats, int cu_count) {
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
          reinterpret_cast<uintptr_t>(vc) | reinterpret_cast<uintptr_t>(knew) |
-         reinterpret_cast<uintptr_t>(vnew)) & 15)
-        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: q/caches/new rows must be 16-byte aligned");
+         reinterpret_cast<uintptr_t>(vnew) | reinterpret_cast<uintptr_t>(o) |
+         reinterpret_cast<uintptr_t>(ws)) & 15)
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_decode: q/caches/new rows/o/workspace must be 16-byte aligned");
     DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count);
     const size_t need = decode_workspace_floats(h, hkv, pos, hd, cu_count);
     if (need > 0 && (ws == nullptr || ws_floats < need))
@@ -513,19 +587,20 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
     a.hkv = (int)hkv;
     a.g = (int)(h / hkv);
     a.keys = (int)(pos + 1);
-    a.chunk = p.chunk;
     a.nsplit = p.nsplit;
     a.scale_log2 = scale * kLog2e;
+    hipError_t e;
     switch (hd) {
-        case 4: launch_hd<4>(st, p, a); break;
-        case 8: launch_hd<8>(st, p, a); break;
-        case 16: launch_hd<16>(st, p, a); break;
-        case 32: launch_hd<32>(st, p, a); break;
-        case 64: launch_hd<64>(st, p, a); break;
-        case 128: launch_hd<128>(st, p, a); break;
-        case 256: launch_hd<256>(st, p, a); break;
+        case 4: e = launch_hd<4>(st, p, a); break;
+        case 8: e = launch_hd<8>(st, p, a); break;
+        case 16: e = launch_hd<16>(st, p, a); break;
+        case 32: e = launch_hd<32>(st, p, a); break;
+        case 64: e = launch_hd<64>(st, p, a); break;
+        case 128: e = launch_hd<128>(st, p, a); break;
+        case 256: e = launch_hd<256>(st, p, a); break;
         default: return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);
     }
+    if (e != hipSuccess) return eb::hip_fail(e, "hipFuncSetAttribute(attn_decode)");
     return check_launch("attn_decode");
 }
 

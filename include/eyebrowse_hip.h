@@ -131,7 +131,8 @@ eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *
 /* The kv_write(K), kv_write(V), attn_decode sequence of Attention::decode
  * (crates/eyebrowse-nn/src/attention.rs:149-183) in one launch: knew/vnew [hkv, hd] are
  * copied bit-exactly into cache row pos and q attends keys 0..=pos (key pos taken from
- * knew/vnew). Same result as the three calls. */
+ * knew/vnew). Same cache contents as the three calls, bit for bit; the same output up
+ * to f32 rounding (key pos is folded into the softmax after the cached keys). */
 eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
                               const eb_tensor *vnew, eb_tensor *kcache, eb_tensor *vcache,
                               eb_tensor *o, size_t h, size_t hkv, size_t pos, size_t hd,

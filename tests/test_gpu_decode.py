@@ -80,7 +80,7 @@ def test_mistral_decode_config(dev, pos):
     (16, 8, 128, 100, 63, None),
     (16, 16, 64, 1000, 999, None),  # MHA
     (24, 8, 128, 700, 650, None),   # g = 3 (three single-head workgroups per KV head)
-    (64, 4, 128, 3000, 2999, None), # g = 16 (two 8-head workgroups per KV head)
+    (64, 4, 128, 3000, 2999, None), # g = 16 (four 4-head workgroups per KV head)
     (8, 1, 256, 5000, 4321, 1.0),   # scale 1.0, hd 256
     (8, 8, 32, 300, 255, 0.0),      # scale 0: mean of V
     (2, 1, 4, 70, 69, None),
@@ -145,7 +145,8 @@ def test_shrinking_shapes_share_the_device_workspace(dev):
 ])
 def test_fused_step_equals_kv_write_then_decode(dev, h, hkv, hd, max_seq, pos):
     """eb_attn_decode_step == kv_write(K), kv_write(V), attn_decode (attention.rs:149-183):
-    same cache bytes, same output bits."""
+    same cache bytes; the same output up to f32 rounding (the fused step folds key `pos`
+    in after the cached keys, the separate calls fold it in with its chunk)."""
     note(f"decode step h={h} hd={hd} pos={pos}")
     sc = float(oracle.default_scale(hd))
     kc = oracle.randn((max_seq, hkv, hd), 2)
@@ -163,7 +164,7 @@ def test_fused_step_equals_kv_write_then_decode(dev, h, hkv, hd, max_seq, pos):
     rec.submit()
     assert_bitwise(k2.to_f32(), k1.to_f32(), "K cache")
     assert_bitwise(v2.to_f32(), v1.to_f32(), "V cache")
-    assert_bitwise(o2.to_f32(), o1.to_f32(), "output")
+    assert_close(o2.to_f32(), o1.to_f32(), what="step vs separate calls")
     want = oracle.attn_decode(q, oracle.kv_write(kc, knew, hkv, 1, hd, pos),
                               oracle.kv_write(vc, vnew, hkv, 1, hd, pos), h, hkv, pos, hd,
                               max_seq, sc, threads=8)
