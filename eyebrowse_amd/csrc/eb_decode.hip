@@ -18,7 +18,8 @@
 //    iteration's loads in flight while the current one is consumed;
 //  - scores are lane-partial dot products summed across the LPK lanes with DPP;
 //  - each lane group keeps an online softmax (running max m, sum l, acc[DPL]) in the log2
-//    domain (scores times scale*log2(e), exponentials on v_exp_f32);
+//    domain (scores times scale*log2(e), exponentials on v_exp_f32), with the rescale of
+//    l and acc skipped until a score exceeds the running max by a slack;
 //  - the lane groups' states meet in LDS, where the workgroup combines them per head;
 //  - with one split the workgroup writes o directly; otherwise it writes its partial
 //    (m, l, acc[HD]) per head and pass 2 (decode_merge_kernel) computes
@@ -56,6 +57,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxSplits = 256;  // per column
 constexpr int kRawBufferFlags = 0x00020000;  // gfx9 raw buffer: 32-bit data, range checked
+constexpr float kSlack = 8.0f;  // log2-units a score may exceed the reference max by
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -213,9 +215,10 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     // past `ce` are masked out).
     auto consume_iter = [&](int it, const f32x4 (&kv)[U][NV4], const f32x4 (&vv)[U][NV4]) {
         const int r0 = rows_from(it);
+        // Scores of every head first (their DPP chains interleave).
+        float sc[G][U];
 #pragma unroll
-        for (int gi = 0; gi < G; ++gi) {
-            float sc[U];
+        for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 f32x4 t = qr[gi][0] * kv[u][0];
@@ -223,30 +226,52 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
                 for (int i = 1; i < NV4; ++i) t += qr[gi][i] * kv[u][i];
                 float sv = (t.x + t.y) + (t.z + t.w);
                 sv = eb::group_sum<S::LPK>(sv);
-                sc[u] = (r0 + rowof[u] < ce) ? sv * a.scale_log2 : -INFINITY;
+                sc[gi][u] = (r0 + rowof[u] < ce) ? sv * a.scale_log2 : -INFINITY;
             }
-            float mloc = sc[0];
+        // Lazy rescale: a head's reference max m moves only when a score exceeds it by more
+        // than kSlack (log2 units), and the rescale of l and acc is skipped for the whole
+        // wave when no lane group needs it. Terms 2^(s - m) then stay below 2^kSlack; the
+        // result is the same up to rounding, since l and acc always share the reference.
+        float mloc[G];
+        bool grow[G];
+        bool any = false;
 #pragma unroll
-            for (int u = 1; u < U; ++u) mloc = fmaxf(mloc, sc[u]);
-            const float mnew = fmaxf(m[gi], mloc);
-            const float mref = (mnew == -INFINITY) ? 0.0f : mnew;
-            const float corr = eb::fast_exp2(m[gi] - mref);
+        for (int gi = 0; gi < G; ++gi) {
+            mloc[gi] = sc[gi][0];
+#pragma unroll
+            for (int u = 1; u < U; ++u) mloc[gi] = fmaxf(mloc[gi], sc[gi][u]);
+            grow[gi] = mloc[gi] > m[gi] + kSlack;
+            any = any || grow[gi];
+        }
+        if (__builtin_amdgcn_ballot_w64(any) != 0) {
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                // 0 when m was -inf; exactly 1 for the lane groups that keep their max
+                const float corr = grow[gi] ? eb::fast_exp2(m[gi] - mloc[gi]) : 1.0f;
+                l[gi] *= corr;
+#pragma unroll
+                for (int i = 0; i < NV4; ++i) acc[gi][i] *= corr;
+                m[gi] = grow[gi] ? mloc[gi] : m[gi];
+            }
+        }
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const float mref = (m[gi] == -INFINITY) ? 0.0f : m[gi];
             float p[U];
             float psum = 0.0f;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                p[u] = eb::fast_exp2(sc[u] - mref);
+                p[u] = eb::fast_exp2(sc[gi][u] - mref);
                 psum += p[u];
             }
-            l[gi] = l[gi] * corr + psum;
+            l[gi] += psum;
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
-                f32x4 t = acc[gi][i] * corr;
+                f32x4 t = acc[gi][i];
 #pragma unroll
                 for (int u = 0; u < U; ++u) t += p[u] * vv[u][i];
                 acc[gi][i] = t;
             }
-            m[gi] = mnew;
         }
     };
 
