@@ -5,22 +5,26 @@ ABI in ``include/eyebrowse_hip.h``); this package is a thin ctypes mirror of the
 reference's Rust interface:
 
 - ``gpu``: DType, EyebrowseError, Device, Tensor, Recorder (crates/eyebrowse-gpu);
-- ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels);
+- ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels),
+  plus chunked / windowed attention and the fused decode step;
 - ``nn``: Rope, KvCache, Attention (crates/eyebrowse-nn).
 """
 from ._lib import LIB_PATH, lib
 from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, OutOfMemory,
                   Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
-from .kernels import (attn_decode, attn_decode_step, attn_decode_workspace_floats, attn_prefill,
-                      kv_write, launch_attn_decode, launch_attn_decode_step,
-                      launch_attn_prefill, launch_kv_write, launch_rmsnorm, launch_rope, rmsnorm,
-                      rope)
+from .kernels import (attn_decode, attn_decode_step, attn_decode_step_window,
+                      attn_decode_window, attn_decode_workspace_floats, attn_prefill,
+                      attn_prefill_chunk, kv_write, launch_attn_decode, launch_attn_decode_step,
+                      launch_attn_decode_window, launch_attn_prefill, launch_attn_prefill_chunk,
+                      launch_kv_write, launch_rmsnorm, launch_rope, rmsnorm, rope)
 from .nn import Attention, KvCache, Rope
 
 __all__ = [
     "LIB_PATH", "lib", "DType", "Device", "DeviceUnavailable", "EyebrowseError", "LoadError",
     "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
-    "attn_decode_step", "launch_attn_decode_step", "attn_decode_workspace_floats", "attn_prefill", "kv_write", "launch_attn_decode",
-    "launch_attn_prefill", "launch_kv_write", "launch_rmsnorm", "launch_rope", "rmsnorm", "rope",
-    "Attention", "KvCache", "Rope",
+    "attn_decode_step", "attn_decode_step_window", "attn_decode_window",
+    "attn_decode_workspace_floats", "attn_prefill", "attn_prefill_chunk", "kv_write",
+    "launch_attn_decode", "launch_attn_decode_step", "launch_attn_decode_window",
+    "launch_attn_prefill", "launch_attn_prefill_chunk", "launch_kv_write", "launch_rmsnorm",
+    "launch_rope", "rmsnorm", "rope", "Attention", "KvCache", "Rope",
 ]

@@ -30,6 +30,7 @@ class AttentionDesc(ctypes.Structure):
         ("q_norm", c_vp),
         ("k_norm", c_vp),
         ("v_norm", c_vp),
+        ("window", c_size),
     ]
 
 
@@ -69,6 +70,12 @@ SIGNATURES = {
                               c_size, c_float]),
     "eb_attn_decode_step": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size,
                                    c_size, c_size, c_size, c_float]),
+    "eb_attn_decode_window": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size,
+                                     c_size, c_size, c_float, c_size]),
+    "eb_attn_decode_step_window": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size,
+                                          c_size, c_size, c_size, c_size, c_float, c_size]),
+    "eb_attn_prefill_chunk": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size,
+                                     c_size, c_size, c_size, c_float, c_size]),
     "eb_kv_write": (c_st, [c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size, c_size]),
     "eb_rmsnorm": (c_st, [c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_float]),
     "eb_rope": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size]),
@@ -76,10 +83,16 @@ SIGNATURES = {
                                   c_size, c_size]),
     "eb_launch_attn_prefill": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
                                       c_size, c_size, c_size, c_size, c_size, c_float]),
+    "eb_launch_attn_prefill_chunk": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,
+                                            c_vp, c_size, c_size, c_size, c_size, c_size,
+                                            c_size, c_size, c_float, c_size]),
     "eb_attn_decode_workspace_floats": (c_size, [c_size, c_size, c_size, c_size, c_int]),
     "eb_launch_attn_decode": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
                                      c_size, c_size, c_size, c_size, c_size, c_size, c_float,
                                      c_vp, c_size, c_int]),
+    "eb_launch_attn_decode_window": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,
+                                            c_vp, c_size, c_size, c_size, c_size, c_size,
+                                            c_size, c_float, c_size, c_vp, c_size, c_int]),
     "eb_launch_attn_decode_step": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size,
                                           c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
                                           c_size, c_size, c_float, c_vp, c_size, c_int]),

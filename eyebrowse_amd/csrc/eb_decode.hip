@@ -584,7 +584,19 @@ size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int 
 eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
                              float *kc_w, float *vc_w, const float *knew, const float *vnew,
                              float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                             float scale, float *ws, size_t ws_floats, int cu_count) {
+                             float scale, float *ws, size_t ws_floats, int cu_count,
+                             size_t window) {
+    // A window is a shift of the cache view: keys first..=pos become keys 0..=pos-first of
+    // caches based at row `first` (the fused write then lands on the same absolute row).
+    if (window > 0 && pos + 1 > window) {
+        const size_t first = pos + 1 - window;
+        const size_t shift = first * hkv * hd;
+        kc += shift;
+        vc += shift;
+        if (kc_w) kc_w += shift;
+        if (vc_w) vc_w += shift;
+        pos -= first;
+    }
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
          reinterpret_cast<uintptr_t>(vc) | reinterpret_cast<uintptr_t>(knew) |
          reinterpret_cast<uintptr_t>(vnew) | reinterpret_cast<uintptr_t>(o) |

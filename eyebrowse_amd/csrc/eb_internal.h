@@ -50,14 +50,23 @@ eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale);
+// Chunked causal prefill: q rows at positions pos0..pos0+rows-1 attend cache keys
+// max(0, p - window + 1)..p (window 0: 0..p); kc/vc are the cache bases.
+eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
+                                    const float *vc, float *o, size_t h, size_t hkv,
+                                    size_t pos0, size_t rows, size_t hd, float scale,
+                                    size_t window);
 // Decode workspace: part_acc [nsplit*h*hd] | part_ml [nsplit*h*2], no initialisation.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count);
 // knew/vnew null: plain attention over keys 0..=pos. Otherwise key `pos` comes from
 // knew/vnew ([hkv, hd]) and is also written to cache row `pos` through kc_w/vc_w.
+// window > 0 limits the keys to pos - window + 1..=pos. A workspace sized for
+// decode_workspace_floats(h, hkv, pos, ...) is enough for any window.
 eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
                              float *kc_w, float *vc_w, const float *knew, const float *vnew,
                              float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                             float scale, float *ws, size_t ws_floats, int cu_count);
+                             float scale, float *ws, size_t ws_floats, int cu_count,
+                             size_t window = 0);
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
                          size_t rows, size_t dim, float eps);
 eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,

@@ -219,13 +219,9 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
         return fail(EB_SHAPE_MISMATCH, "attention_forward: cache layer is not [max_seq, %zu, %zu]",
                     Hkv, hd);
     if (rows == 0) return fail(EB_SHAPE_MISMATCH, "attention_forward: rows must be > 0");
-    // Routing rule of attention.rs:40.
-    const bool prefill = base_pos == 0 && rows > 1;
-    if (!prefill && rows != 1)
-        return fail(EB_UNSUPPORTED_CONFIG,
-                    "attention_forward: %zu rows at base_pos %zu (chunked prefill is not part "
-                    "of the reference path)",
-                    rows, base_pos);
+    if (base_pos > kv->max_seq || rows > kv->max_seq - base_pos)
+        return fail(EB_SHAPE_MISMATCH, "attention_forward: rows [%zu, %zu) exceed max_seq %zu",
+                    base_pos, base_pos + rows, kv->max_seq);
     if (eb_tensor_numel(q) != rows * H * hd || eb_tensor_numel(k) != rows * Hkv * hd ||
         eb_tensor_numel(v) != rows * Hkv * hd)
         return fail(EB_SHAPE_MISMATCH, "attention_forward: q/k/v are not [rows, heads*head_dim]");
@@ -246,16 +242,22 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
     eb_tensor *o_t = nullptr;
     EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape, 2, EB_F32, &o_t));
     Owned o(o_t);
-    if (prefill) {
-        // attention.rs:78-97 writes the prompt's K (post-RoPE) and V into the cache, and
-        // :104-115 attends the fresh kr / v, not the cache.
-        EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, 0));
-        EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, 0));
-        EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
-    } else {
+    if (rows == 1) {
         // attention.rs:149-183: kv_write K and V at pos, then attn_decode, as one launch.
-        EB_TRY(eb_attn_decode_step(rec, qr.t, kr.t, vn, kc, vc, o.t, H, Hkv, base_pos, hd,
-                                   kv->max_seq, d.scale));
+        EB_TRY(eb_attn_decode_step_window(rec, qr.t, kr.t, vn, kc, vc, o.t, H, Hkv, base_pos, hd,
+                                          kv->max_seq, d.scale, d.window));
+    } else {
+        // attention.rs:78-97 writes the new rows' K (post-RoPE) and V into the cache.
+        EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
+        EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
+        if (base_pos == 0 && d.window == 0) {
+            // attention.rs:104-115 (routing rule :40): a prompt attends its fresh kr / v.
+            EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
+        } else {
+            // A continuation chunk (or a windowed prompt) attends the cache rows it needs.
+            EB_TRY(eb_attn_prefill_chunk(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, rows, hd,
+                                         kv->max_seq, d.scale, d.window));
+        }
     }
     *out = o.release();
     return eb::ok();

@@ -116,11 +116,14 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
 }
 
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
-template <int HD, int HPW, int WPH, int KSPLIT>
+// RANGE: queries start at position qbase and may have a sliding window; without it the
+// kernel is specialised to a prompt from position 0 (no window), whose masks are simpler.
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-    float *__restrict__ o, int H, int Hkv, int T, float scale_log2, int nqb, int ngroups) {
+    float *__restrict__ o, int H, int Hkv, int rows, int nkeys, int qbase, int window,
+    float scale_log2, int nqb, int ngroups) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     constexpr int QB = C::QB;
     constexpr int HALF = C::HALF;
@@ -144,16 +147,30 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     const int qb = nqb - 1 - flat / ngroups;  // heaviest query blocks first
     const int kvh = grp / gsub;
     const int head = kvh * g + (grp % gsub) * HPW + slot / WPH;
+    // Query rows are local (0..rows-1) and sit at positions qbase + row. Key tiles of 32
+    // cover keys [32 t, 32 t + 32); a query at p sees keys max(0, p - window + 1)..p
+    // (0..p without a window).
+    if constexpr (!RANGE) {
+        qbase = 0;
+        window = 0;
+    }
     const int q0 = qb * QB + (slot % WPH) * kTile;
-    const int wg_last = min(qb * QB + QB, T) - 1;
-    const int nsteps = (wg_last / kTile) / KSPLIT + 1;
-    const int my_tiles = q0 < T ? q0 / kTile + 1 : 0;  // tiles 0..q0/32 hold its keys
+    const int p_first = qbase + qb * QB;
+    const int p_last = qbase + min(qb * QB + QB, rows) - 1;
+    const int t0 = window > 0 ? max(0, p_first - window + 1) / kTile : 0;
+    const int nsteps = (p_last / kTile - t0) / KSPLIT + 1;
+    const bool live = q0 < rows;
+    const int wp0 = qbase + q0;                         // this wave's first position
+    const int wp1 = qbase + min(q0 + kTile, rows) - 1;  // and last
+    const int my_t0 = window > 0 ? max(0, wp0 - window + 1) / kTile : 0;
+    const int my_t1 = wp1 / kTile;
     const int qi = q0 + col;
+    const int pi = qbase + qi;
 
     // Q fragment: query qi, head dims [HALF*hf, HALF*hf + HALF).
     float qreg[HALF];
     {
-        const bool qv = qi < T;
+        const bool qv = qi < rows;
         const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * HD + HALF * hf;
         if constexpr (HALF % 4 == 0) {
 #pragma unroll
@@ -180,19 +197,20 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     float l = 0.0f;
 
     f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C>(k, v, rk, rv, 0, T, Hkv, kvh, tid);
+    prefill_load_step<C>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
 
     for (int it = 0; it < nsteps; ++it) {
         const int buf = it & 1;
-        const int tile = it * KSPLIT + ks;
+        const int tile = t0 + it * KSPLIT + ks;
         const int kb = tile * kTile;
         // Prefetch the next step (past the last step this re-reads clamped rows; the
         // buffer written from them is never read).
-        prefill_load_step<C>(k, v, rk, rv, (it + 1) * C::STEP_KEYS, T, Hkv, kvh, tid);
+        prefill_load_step<C>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys, Hkv, kvh,
+                             tid);
 
-        if (tile < my_tiles) {
+        if (live && tile >= my_t0 && tile <= my_t1) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
             const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS + ks * kTile * HD;
             // S^T = K Q^T for this tile: 16 keys x 1 query per lane.
@@ -214,25 +232,32 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 for (int s = 0; s < HALF; ++s) sacc = mfma32(kr[s], qreg[s], sacc);
             }
 
-            // Online softmax over this tile's keys (log2 domain).
-            const bool diag = (kb == q0);
+            // Online softmax over this tile's keys (log2 domain). Only tiles that reach
+            // past the wave's first position, or (window) below its last position's
+            // window, need the per-key mask.
+            const bool edge =
+                RANGE ? (kb + kTile - 1 > wp0 || (window > 0 && kb <= wp1 - window)) : kb == q0;
             float p[16];
             float mt = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
                 float x = sacc[r] * scale_log2;
-                if (diag && key > qi) x = -INFINITY;
+                if (edge && (key > pi || (RANGE && window > 0 && key <= pi - window)))
+                    x = -INFINITY;
                 p[r] = x;
                 mt = fmaxf(mt, x);
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32));
             const float mnew = fmaxf(m, mt);
-            const float corr = eb::fast_exp2(m - mnew);
+            // A query can meet a tile with all of its keys masked before its first visible
+            // key (unaligned chunk starts, windows): keep exp2 away from -inf - -inf.
+            const float mref = (RANGE && mnew == -INFINITY) ? 0.0f : mnew;
+            const float corr = eb::fast_exp2(m - mref);
             float ps = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                p[r] = eb::fast_exp2(p[r] - mnew);
+                p[r] = eb::fast_exp2(p[r] - mref);
                 ps += p[r];
             }
             l = l * corr + ps;
@@ -302,8 +327,9 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 const float m2 = rec[lane];
                 const float l2 = rec[64 + lane];
                 const float M = fmaxf(m, m2);
-                const float a1 = eb::fast_exp2(m - M);   // m is finite: ks 0 ran tile 0
-                const float a2 = eb::fast_exp2(m2 - M);  // 0 when split j saw no keys
+                const float Mr = (M == -INFINITY) ? 0.0f : M;
+                const float a1 = eb::fast_exp2(m - Mr);   // 0 when this wave saw no keys
+                const float a2 = eb::fast_exp2(m2 - Mr);  // 0 when split j saw no keys
                 l = l * a1 + l2 * a2;
                 m = M;
 #pragma unroll
@@ -322,7 +348,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     const float lt = l + __shfl_xor(l, 32);
     if constexpr (KSPLIT > 1) __syncthreads();  // the merge records are read; reuse LDS
     float *ot = smem + slot * kTile * C::OS;    // this slot's staging tile [32][OS]
-    if (ks == 0 && my_tiles > 0) {
+    if (ks == 0 && live) {
         const float inv = 1.0f / lt;
         float *orow = ot + col * C::OS;
 #pragma unroll
@@ -346,7 +372,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         }
     }
     __syncthreads();
-    if (ks == 0 && my_tiles > 0) {
+    if (ks == 0 && live) {
         constexpr int ROW4 = HD / 4;  // float4 per output row
 #pragma unroll
         for (int j = 0; j < (kTile * ROW4 + 63) / 64; ++j) {
@@ -354,7 +380,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             if (kTile * ROW4 % 64 == 0 || idx < kTile * ROW4) {
                 const int row = idx / ROW4;
                 const int c4 = idx % ROW4;
-                if (q0 + row < T)
+                if (q0 + row < rows)
                     *reinterpret_cast<float4 *>(o + ((size_t)(q0 + row) * H + head) * HD + 4 * c4) =
                         *reinterpret_cast<const float4 *>(ot + row * C::OS + 4 * c4);
             }
@@ -362,25 +388,41 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     }
 }
 
-template <int HD, int HPW, int WPH, int KSPLIT>
-eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const float *v,
-                           float *o, int H, int Hkv, int T, float scale_log2) {
+struct PrefillRange {
+    int rows;    // query rows
+    int nkeys;   // key rows available in k/v
+    int qbase;   // position of query row 0
+    int window;  // sliding window (0: none)
+};
+
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE>
+eb_status launch_prefill_r(hipStream_t st, const float *q, const float *k, const float *v,
+                           float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&prefill_kernel<HD, HPW, WPH, KSPLIT>),
+            reinterpret_cast<const void *>(&prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
     const int g = H / Hkv;
     const int ngroups = Hkv * (g / HPW);
-    const int nqb = (T + C::QB - 1) / C::QB;
+    const int nqb = (r.rows + C::QB - 1) / C::QB;
     const unsigned blocks = (unsigned)(nqb * ngroups);
-    prefill_kernel<HD, HPW, WPH, KSPLIT><<<blocks, C::THREADS, C::LDS_BYTES, st>>>(
-        q, k, v, o, H, Hkv, T, scale_log2, nqb, ngroups);
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE><<<blocks, C::THREADS, C::LDS_BYTES, st>>>(
+        q, k, v, o, H, Hkv, r.rows, r.nkeys, r.qbase, r.window, scale_log2, nqb, ngroups);
     return eb::check_launch("attn_prefill");
+}
+
+template <int HD, int HPW, int WPH, int KSPLIT>
+eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const float *v,
+                           float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
+    if (r.qbase == 0 && r.window == 0)
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false>(st, q, k, v, o, H, Hkv, r,
+                                                             scale_log2);
+    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true>(st, q, k, v, o, H, Hkv, r, scale_log2);
 }
 
 // head_dim <= 128:
@@ -393,12 +435,34 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const
 // wave per SIMD: 4 waves, no key split.
 template <int HD>
 eb_status launch_prefill_hd(hipStream_t st, const float *q, const float *k, const float *v,
-                            float *o, int H, int Hkv, int T, float scale_log2) {
+                            float *o, int H, int Hkv, const PrefillRange &r,
+                            float scale_log2) {
     const int g = H / Hkv;
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
-    if (g % 4 == 0) return launch_prefill_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, T, scale_log2);
-    if (g % 2 == 0) return launch_prefill_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
-    return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, T, scale_log2);
+    if (g % 4 == 0) return launch_prefill_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, scale_log2);
+    if (g % 2 == 0)
+        return launch_prefill_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
+    return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
+}
+
+eb_status launch_prefill_range(hipStream_t st, const float *q, const float *k, const float *v,
+                               float *o, size_t h, size_t hkv, size_t hd, float scale,
+                               const PrefillRange &r) {
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15)
+        return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: q/k/v/o must be 16-byte aligned");
+    const float sl2 = scale * eb::kLog2e;
+    const int H = (int)h, Hk = (int)hkv;
+    switch (hd) {
+        case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, r, sl2);
+        case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, r, sl2);
+        case 16: return launch_prefill_hd<16>(st, q, k, v, o, H, Hk, r, sl2);
+        case 32: return launch_prefill_hd<32>(st, q, k, v, o, H, Hk, r, sl2);
+        case 64: return launch_prefill_hd<64>(st, q, k, v, o, H, Hk, r, sl2);
+        case 128: return launch_prefill_hd<128>(st, q, k, v, o, H, Hk, r, sl2);
+        case 256: return launch_prefill_hd<256>(st, q, k, v, o, H, Hk, r, sl2);
+        default: return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: head_dim %zu", hd);
+    }
 }
 
 }  // namespace
@@ -408,21 +472,17 @@ namespace eb {
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale) {
-    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
-         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15)
-        return fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: q/k/v/o must be 16-byte aligned");
-    const float sl2 = scale * kLog2e;
-    const int H = (int)h, Hk = (int)hkv, T = (int)s;
-    switch (hd) {
-        case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, T, sl2);
-        case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, T, sl2);
-        case 16: return launch_prefill_hd<16>(st, q, k, v, o, H, Hk, T, sl2);
-        case 32: return launch_prefill_hd<32>(st, q, k, v, o, H, Hk, T, sl2);
-        case 64: return launch_prefill_hd<64>(st, q, k, v, o, H, Hk, T, sl2);
-        case 128: return launch_prefill_hd<128>(st, q, k, v, o, H, Hk, T, sl2);
-        case 256: return launch_prefill_hd<256>(st, q, k, v, o, H, Hk, T, sl2);
-        default: return fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: head_dim %zu", hd);
-    }
+    return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
+                                PrefillRange{(int)s, (int)s, 0, 0});
+}
+
+eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
+                                    const float *vc, float *o, size_t h, size_t hkv,
+                                    size_t pos0, size_t rows, size_t hd, float scale,
+                                    size_t window) {
+    return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
+                                PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
+                                             (int)window});
 }
 
 }  // namespace eb

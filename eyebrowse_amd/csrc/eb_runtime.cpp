@@ -450,6 +450,32 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     return eb::ok();
 }
 
+static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn,
+                                       const float *kc, size_t kcn, const float *vc, size_t vcn,
+                                       float *o, size_t on, size_t h, size_t hkv, size_t pos0,
+                                       size_t rows, size_t hd, size_t max_seq, float scale,
+                                       size_t window) {
+    EB_TRY(eb::check_heads(h, hkv));
+    if (!eb::attn_head_dim_supported(hd))
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_prefill_chunk: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)",
+                    hd);
+    if (pos0 > max_seq || rows > max_seq - pos0)
+        return fail(EB_SHAPE_MISMATCH, "attn_prefill_chunk: rows [%zu, %zu) exceed max_seq %zu",
+                    pos0, pos0 + rows, max_seq);
+    EB_TRY(eb::check_numel(qn, rows * h * hd, "q"));
+    EB_TRY(eb::check_numel(kcn, max_seq * hkv * hd, "kcache"));
+    EB_TRY(eb::check_numel(vcn, max_seq * hkv * hd, "vcache"));
+    EB_TRY(eb::check_numel(on, rows * h * hd, "o"));
+    if (rows == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(q, "q"));
+    EB_TRY(eb::check_ptr(kc, "kcache"));
+    EB_TRY(eb::check_ptr(vc, "vcache"));
+    EB_TRY(eb::check_ptr(o, "o"));
+    EB_TRY(eb::launch_attn_prefill_chunk(st, q, kc, vc, o, h, hkv, pos0, rows, hd, scale, window));
+    return eb::ok();
+}
+
 static eb_status decode_shape_checked(const float *q, size_t qn, const float *kc, size_t kcn,
                                       const float *vc, size_t vcn, const float *o, size_t on,
                                       size_t h, size_t hkv, size_t pos, size_t hd,
@@ -533,14 +559,15 @@ static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
 static eb_status device_decode(eb_device *dev, const float *q, const float *kc, const float *vc,
                                float *kc_w, float *vc_w, const float *knew, const float *vnew,
                                float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                               float scale) {
+                               float scale, size_t window = 0) {
     size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
     float *ws = nullptr;
     if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
     EB_TRY(eb::launch_attn_decode(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv, pos,
-                                  hd, scale, ws, wsn, dev->cu_count));
+                                  hd, scale, ws, wsn, dev->cu_count, window));
     return eb::ok();
 }
+
 
 extern "C" {
 
@@ -586,10 +613,54 @@ eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *
                          (float *)o->ptr, h, hkv, pos, hd, scale);
 }
 
+eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
+                                const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                                size_t pos0, size_t rows, size_t hd, size_t max_seq,
+                                float scale, size_t window) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
+    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    return prefill_chunk_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
+                                 (const float *)kcache->ptr, eb_tensor_numel(kcache),
+                                 (const float *)vcache->ptr, eb_tensor_numel(vcache),
+                                 (float *)o->ptr, eb_tensor_numel(o), h, hkv, pos0, rows, hd,
+                                 max_seq, scale, window);
+}
+
+eb_status eb_attn_decode_window(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
+                                const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                                size_t pos, size_t hd, size_t max_seq, float scale,
+                                size_t window) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
+    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q),
+                                (const float *)kcache->ptr, eb_tensor_numel(kcache),
+                                (const float *)vcache->ptr, eb_tensor_numel(vcache),
+                                (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
+                                max_seq));
+    return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
+                         (const float *)vcache->ptr, nullptr, nullptr, nullptr, nullptr,
+                         (float *)o->ptr, h, hkv, pos, hd, scale, window);
+}
+
 eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
                               const eb_tensor *vnew, eb_tensor *kcache, eb_tensor *vcache,
                               eb_tensor *o, size_t h, size_t hkv, size_t pos, size_t hd,
                               size_t max_seq, float scale) {
+    return eb_attn_decode_step_window(rec, q, knew, vnew, kcache, vcache, o, h, hkv, pos, hd,
+                                      max_seq, scale, 0);
+}
+
+eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
+                                     const eb_tensor *vnew, eb_tensor *kcache,
+                                     eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                                     size_t pos, size_t hd, size_t max_seq, float scale,
+                                     size_t window) {
     EB_TRY(rec_ready(rec));
     EB_TRY(tensor_f32(q, "q", rec->dev));
     EB_TRY(tensor_f32(knew, "knew", rec->dev));
@@ -608,7 +679,7 @@ eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_ten
     return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
                          (const float *)vcache->ptr, (float *)kcache->ptr, (float *)vcache->ptr,
                          (const float *)knew->ptr, (const float *)vnew->ptr, (float *)o->ptr, h,
-                         hkv, pos, hd, scale);
+                         hkv, pos, hd, scale, window);
 }
 
 eb_status eb_rmsnorm(eb_recorder *rec, const eb_tensor *x, const eb_tensor *weight,
@@ -654,6 +725,15 @@ eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel, c
                            h, hkv, s, hd, scale);
 }
 
+eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_numel,
+                                       const float *kc, size_t kc_numel, const float *vc,
+                                       size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                       size_t hkv, size_t pos0, size_t rows, size_t hd,
+                                       size_t max_seq, float scale, size_t window) {
+    return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window);
+}
+
 size_t eb_attn_decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd,
                                        int cu_count) {
     if (h == 0 || hkv == 0 || h % hkv != 0 || !eb::attn_head_dim_supported(hd)) return 0;
@@ -676,6 +756,26 @@ eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel, co
     EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, nullptr, nullptr, nullptr,
                                   nullptr, o, h, hkv, pos, hd, scale, workspace,
                                   workspace_floats, cus));
+    return eb::ok();
+}
+
+eb_status eb_launch_attn_decode_window(void *stream, const float *q, size_t q_numel,
+                                       const float *kc, size_t kc_numel, const float *vc,
+                                       size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                       size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                       float scale, size_t window, float *workspace,
+                                       size_t workspace_floats, int cu_count) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, nullptr, nullptr, nullptr,
+                                  nullptr, o, h, hkv, pos, hd, scale, workspace,
+                                  workspace_floats, cus, window));
     return eb::ok();
 }
 

@@ -32,6 +32,32 @@ def attn_decode_step(rec: Recorder, q: Tensor, knew: Tensor, vnew: Tensor, kcach
                                     max_seq, scale))
 
 
+def attn_decode_window(rec: Recorder, q: Tensor, kcache: Tensor, vcache: Tensor, o: Tensor,
+                       h: int, hkv: int, pos: int, hd: int, max_seq: int, scale: float,
+                       window: int) -> None:
+    """attn_decode over keys pos - window + 1..=pos only (window 0: all keys)."""
+    check(lib().eb_attn_decode_window(rec.handle, q.handle, kcache.handle, vcache.handle,
+                                      o.handle, h, hkv, pos, hd, max_seq, scale, window))
+
+
+def attn_decode_step_window(rec: Recorder, q: Tensor, knew: Tensor, vnew: Tensor,
+                            kcache: Tensor, vcache: Tensor, o: Tensor, h: int, hkv: int,
+                            pos: int, hd: int, max_seq: int, scale: float, window: int) -> None:
+    """attn_decode_step over keys pos - window + 1..=pos only (window 0: all keys)."""
+    check(lib().eb_attn_decode_step_window(rec.handle, q.handle, knew.handle, vnew.handle,
+                                           kcache.handle, vcache.handle, o.handle, h, hkv, pos,
+                                           hd, max_seq, scale, window))
+
+
+def attn_prefill_chunk(rec: Recorder, q: Tensor, kcache: Tensor, vcache: Tensor, o: Tensor,
+                       h: int, hkv: int, pos0: int, rows: int, hd: int, max_seq: int,
+                       scale: float, window: int = 0) -> None:
+    """Chunked causal prefill: q [rows,h,hd] at positions pos0.. attends the cache keys
+    0..=pos0+r (or the last `window`) of [max_seq,hkv,hd] caches that already hold them."""
+    check(lib().eb_attn_prefill_chunk(rec.handle, q.handle, kcache.handle, vcache.handle,
+                                      o.handle, h, hkv, pos0, rows, hd, max_seq, scale, window))
+
+
 def kv_write(rec: Recorder, cache: Tensor, src: Tensor, hkv: int, count: int, hd: int,
              max_seq: int, dst_start: int) -> None:
     """ops.rs:150-179: copy src [count,hkv,hd] into cache rows dst_start.."""
@@ -67,6 +93,15 @@ def launch_attn_prefill(stream: int, q: int, q_numel: int, k: int, k_numel: int,
                                        h, hkv, s, hd, scale))
 
 
+def launch_attn_prefill_chunk(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
+                              vc: int, vc_numel: int, o: int, o_numel: int, h: int, hkv: int,
+                              pos0: int, rows: int, hd: int, max_seq: int, scale: float,
+                              window: int = 0) -> None:
+    check(lib().eb_launch_attn_prefill_chunk(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                             o_numel, h, hkv, pos0, rows, hd, max_seq, scale,
+                                             window))
+
+
 def attn_decode_workspace_floats(h: int, hkv: int, pos: int, hd: int, cu_count: int) -> int:
     return int(lib().eb_attn_decode_workspace_floats(h, hkv, pos, hd, cu_count))
 
@@ -78,6 +113,15 @@ def launch_attn_decode(stream: int, q: int, q_numel: int, kc: int, kc_numel: int
     check(lib().eb_launch_attn_decode(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
                                       o_numel, h, hkv, pos, hd, max_seq, scale, workspace,
                                       workspace_floats, cu_count))
+
+
+def launch_attn_decode_window(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
+                              vc: int, vc_numel: int, o: int, o_numel: int, h: int, hkv: int,
+                              pos: int, hd: int, max_seq: int, scale: float, window: int,
+                              workspace: int, workspace_floats: int, cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode_window(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                             o_numel, h, hkv, pos, hd, max_seq, scale, window,
+                                             workspace, workspace_floats, cu_count))
 
 
 def launch_attn_decode_step(stream: int, q: int, q_numel: int, knew: int, vnew: int,

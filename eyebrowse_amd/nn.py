@@ -119,12 +119,14 @@ class Attention:
     k_norm: Optional[Tensor] = None
     v_norm: Optional[Tensor] = None
     norm_eps: float = 1e-6
+    window: int = 0  # sliding window of a local layer (0: global attention)
 
     def __post_init__(self):
         d = AttentionDesc(self.n_heads, self.n_kv_heads, self.head_dim, self.scale, self.norm_eps,
                           self.q_norm.handle if self.q_norm is not None else None,
                           self.k_norm.handle if self.k_norm is not None else None,
-                          self.v_norm.handle if self.v_norm is not None else None)
+                          self.v_norm.handle if self.v_norm is not None else None,
+                          self.window)
         out = c_vp()
         check(lib().eb_attention_new(ctypes.byref(d), ctypes.byref(out)))
         self._h = out
@@ -133,7 +135,8 @@ class Attention:
                     kv: KvCache, layer: int, rows: int, base_pos: int) -> Tensor:
         """Attention::forward (attention.rs:30-185) from the projected q [rows, H*hd],
         k/v [rows, Hkv*hd]: norms, RoPE, kv_write, then prefill (base_pos == 0 and
-        rows > 1) or decode. Returns [rows, H*hd], the o_proj input."""
+        rows > 1), chunked prefill over the cache (base_pos > 0 and rows > 1) or the fused
+        decode step (rows == 1). Returns [rows, H*hd], the o_proj input."""
         out = c_vp()
         check(lib().eb_attention_forward_qkv(self._h, rec.handle, q.handle, k.handle, v.handle,
                                              rope.handle, kv.handle, layer, rows, base_pos,

@@ -137,6 +137,28 @@ eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_ten
                               const eb_tensor *vnew, eb_tensor *kcache, eb_tensor *vcache,
                               eb_tensor *o, size_t h, size_t hkv, size_t pos, size_t hd,
                               size_t max_seq, float scale);
+/* Windowed variants (no counterpart in the reference, whose attention is always global):
+ * with window > 0 a query at position p attends only keys p - window + 1 ..= p (all of
+ * 0..=p when window == 0), as sliding-window (local) layers do. */
+eb_status eb_attn_decode_window(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
+                                const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                                size_t pos, size_t hd, size_t max_seq, float scale,
+                                size_t window);
+eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
+                                     const eb_tensor *vnew, eb_tensor *kcache,
+                                     eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                                     size_t pos, size_t hd, size_t max_seq, float scale,
+                                     size_t window);
+/* Chunked causal prefill: q [rows,h,hd] holds the queries at positions pos0..pos0+rows-1,
+ * whose K/V are already in the caches [max_seq,hkv,hd]; row r attends cache keys
+ * 0..=pos0+r (or the last `window` of them). With pos0 == 0 and no window this is
+ * attn_prefill over the cache; with rows == 1 it is attn_decode at pos0. The reference
+ * routes such calls (rows > 1 at base_pos > 0, attention.rs:40) to attn_prefill over the
+ * fresh rows only and defers chunked prefill; this is the attention that call intends. */
+eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
+                                const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
+                                size_t pos0, size_t rows, size_t hd, size_t max_seq,
+                                float scale, size_t window);
 /* kv_write (ops.rs:150-179): copy src [count,hkv,hd] into cache rows
  * [dst_start, dst_start+count) of [max_seq,hkv,hd]; bit-exact. Unlike the reference,
  * dst_start + count > max_seq is rejected (EB_SHAPE_MISMATCH). */
@@ -160,6 +182,11 @@ eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel,
                                  const float *k, size_t k_numel, const float *v,
                                  size_t v_numel, float *o, size_t o_numel, size_t h,
                                  size_t hkv, size_t s, size_t hd, float scale);
+eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_numel,
+                                       const float *kc, size_t kc_numel, const float *vc,
+                                       size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                       size_t hkv, size_t pos0, size_t rows, size_t hd,
+                                       size_t max_seq, float scale, size_t window);
 /* Floats of workspace eb_launch_attn_decode(_step) needs for this shape on this many CUs
  * (0 when the split count is 1 and no workspace is used). Its contents need no
  * initialisation. Launches that share a workspace must not overlap (use one stream). */
@@ -171,6 +198,13 @@ eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel,
                                 size_t hkv, size_t pos, size_t hd, size_t max_seq,
                                 float scale, float *workspace, size_t workspace_floats,
                                 int cu_count);
+/* eb_attn_decode_window on caller memory (a workspace sized for pos fits any window). */
+eb_status eb_launch_attn_decode_window(void *stream, const float *q, size_t q_numel,
+                                       const float *kc, size_t kc_numel, const float *vc,
+                                       size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                       size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                       float scale, size_t window, float *workspace,
+                                       size_t workspace_floats, int cu_count);
 /* eb_attn_decode_step on caller memory; knew/vnew each hold new_numel >= hkv*hd floats. */
 eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_numel,
                                      const float *knew, const float *vnew, size_t new_numel,
@@ -219,6 +253,7 @@ typedef struct eb_attention_desc {
     const eb_tensor *q_norm; /* may be NULL */
     const eb_tensor *k_norm; /* may be NULL */
     const eb_tensor *v_norm; /* may be NULL */
+    size_t window;           /* sliding window of a local layer; 0 = global attention */
 } eb_attention_desc;
 
 eb_status eb_attention_new(const eb_attention_desc *desc, eb_attention **out);
@@ -226,8 +261,9 @@ void eb_attention_release(eb_attention *attn);
 /* Attention::forward (attention.rs:30-45, 49-117, 120-185) from the projected
  * q [rows, n_heads*hd], k/v [rows, n_kv_heads*hd] on: optional q/k/v RMSNorm, RoPE at
  * base_pos, kv_write of K and V at base_pos, then attn_prefill (base_pos == 0 and
- * rows > 1) or attn_decode. *out is a new tensor [rows, n_heads*hd] (the input of
- * o_proj). */
+ * rows > 1), chunked prefill over the cache (base_pos > 0 and rows > 1), or the fused
+ * decode step (rows == 1); desc.window > 0 restricts every query to its last `window`
+ * keys. *out is a new tensor [rows, n_heads*hd] (the input of o_proj). */
 eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recorder *rec,
                                    const eb_tensor *q, const eb_tensor *k, const eb_tensor *v,
                                    const eb_rope_tables *rope, eb_kv_cache *kv, size_t layer,

@@ -55,6 +55,9 @@ def _load():
     lib.ebo_attn_prefill_rows.restype = ctypes.c_int
     lib.ebo_attn_prefill_rows.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz,
                                           ctypes.c_float, _sz, _sz, ctypes.c_int]
+    lib.ebo_attn_chunk.restype = ctypes.c_int
+    lib.ebo_attn_chunk.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
+                                   ctypes.c_float, _sz, ctypes.c_int]
     lib.ebo_attn_decode.restype = ctypes.c_int
     lib.ebo_attn_decode.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
                                     ctypes.c_float, ctypes.c_int]
@@ -175,3 +178,22 @@ def attn_decode(q, kc, vc, h: int, hkv: int, pos: int, hd: int, max_seq: int,
     if rc != 0:
         raise ValueError("oracle attn_decode: bad shape")
     return o.reshape(h, hd)
+
+
+def attn_chunk(q, k, v, h: int, hkv: int, pos0: int, rows: int, hd: int,
+               scale: float | None = None, window: int = 0, threads: int = 1) -> np.ndarray:
+    """Chunked causal attention with an optional sliding window: row r of q [rows, h, hd]
+    at position pos0 + r attends keys max(0, p - window + 1)..=p (window 0: all of 0..=p)
+    of k/v [>= pos0 + rows, hkv, hd]. Same per-row arithmetic as attn_prefill /
+    attn_decode (testutil.rs:142-169); the reference has no chunked or windowed attention.
+    Returns o [rows, h, hd]."""
+    q, k, v = _f32(q).ravel(), _f32(k).ravel(), _f32(v).ravel()
+    assert q.size == rows * h * hd and k.size >= (pos0 + rows) * hkv * hd and v.size == k.size
+    if scale is None:
+        scale = default_scale(hd)
+    o = np.empty(rows * h * hd, np.float32)
+    rc = _load().ebo_attn_chunk(_p(q), _p(k), _p(v), _p(o), h, hkv, pos0, rows, hd, scale,
+                                window, threads)
+    if rc != 0:
+        raise ValueError("oracle attn_chunk: bad shape")
+    return o.reshape(rows, h, hd)

@@ -150,14 +150,15 @@ void ebo_kv_write(float *cache, const float *src, size_t hkv, size_t count, size
                 cache[((dst_start + c) * hkv + head) * hd + d] = src[(c * hkv + head) * hd + d];
 }
 
-/* One query row of the reference CPU attention: 3-pass softmax over keys 0..=last.
+/* One query row of the reference CPU attention: 3-pass softmax over keys first..=last.
  * Scores: f32 dot with d ascending, then * scale; max; sum of expf(sc - mx); then per
  * key j: w = expf(sc - mx) / sum, o[d] += w * v[d].
  * Follows crates/eyebrowse-kernels/src/testutil.rs:142-169 (prefill) and :190-216
- * (decode), which share this body. `scores` is caller scratch of last+1 floats. */
+ * (decode), which share this body with first = 0. `scores` is caller scratch of last+1
+ * floats. */
 static void ebo_attn_row(const float *qrow, const float *k, const float *v, float *orow,
-                         size_t hkv, size_t kvh, size_t last, size_t hd, float scale,
-                         float *scores) {
+                         size_t hkv, size_t kvh, size_t first, size_t last, size_t hd,
+                         float scale, float *scores) {
 #if EBO_PLANT == 2 /* planted mistake: causal mask drops the diagonal */
     if (last > 0) last -= 1;
 #endif
@@ -165,7 +166,7 @@ static void ebo_attn_row(const float *qrow, const float *k, const float *v, floa
     scale = 1.0f;
 #endif
     float mx = -INFINITY;
-    for (size_t j = 0; j <= last; ++j) {
+    for (size_t j = first; j <= last; ++j) {
         const float *kr = k + (j * hkv + kvh) * hd;
         float dot = 0.0f;
         for (size_t d = 0; d < hd; ++d) dot += qrow[d] * kr[d];
@@ -174,9 +175,9 @@ static void ebo_attn_row(const float *qrow, const float *k, const float *v, floa
         mx = fmaxf(mx, dot);
     }
     float sum = 0.0f;
-    for (size_t j = 0; j <= last; ++j) sum += expf(scores[j] - mx);
+    for (size_t j = first; j <= last; ++j) sum += expf(scores[j] - mx);
     for (size_t d = 0; d < hd; ++d) orow[d] = 0.0f;
-    for (size_t j = 0; j <= last; ++j) {
+    for (size_t j = first; j <= last; ++j) {
         float w = expf(scores[j] - mx) / sum;
 #if EBO_PLANT == 4 /* planted mistake: values read from the key tensor */
         const float *vr = k + (j * hkv + kvh) * hd;
@@ -223,7 +224,7 @@ int ebo_attn_prefill_rows(const float *q, const float *k, const float *v, float 
             size_t kvh = hh / group;
 #endif
             size_t qbase = (i * h + hh) * hd;
-            ebo_attn_row(q + qbase, k, v, o + qbase, hkv, kvh, i, hd, scale, scores);
+            ebo_attn_row(q + qbase, k, v, o + qbase, hkv, kvh, 0, i, hd, scale, scores);
         }
         free(scores);
     }
@@ -255,8 +256,44 @@ int ebo_attn_decode(const float *q, const float *kc, const float *vc, float *o, 
 #endif
         for (long long hh = 0; hh < (long long)h; ++hh) {
             size_t kvh = (size_t)hh / group;
-            ebo_attn_row(q + (size_t)hh * hd, kc, vc, o + (size_t)hh * hd, hkv, kvh, pos, hd,
+            ebo_attn_row(q + (size_t)hh * hd, kc, vc, o + (size_t)hh * hd, hkv, kvh, 0, pos, hd,
                          scale, scores);
+        }
+        free(scores);
+    }
+    (void)threads;
+    return 0;
+}
+
+/* Chunked causal attention with an optional sliding window: query row r < rows of
+ * q [rows, h, hd] sits at position p = pos0 + r and attends keys
+ * max(0, p - window + 1) ..= p (all of 0..=p when window == 0) of the seq-major k/v
+ * [>= pos0 + rows, hkv, hd]; o [rows, h, hd]. The per-row arithmetic is the reference's
+ * (testutil.rs:142-169) over that key range: with pos0 = 0 and no window it is
+ * ebo_attn_prefill, with rows = 1 and no window ebo_attn_decode at pos0. The reference
+ * itself has neither chunked nor windowed attention. */
+int ebo_attn_chunk(const float *q, const float *k, const float *v, float *o, size_t h,
+                   size_t hkv, size_t pos0, size_t rows, size_t hd, float scale, size_t window,
+                   int threads) {
+    if (hkv == 0 || h % hkv != 0) return -1;
+    size_t group = h / hkv;
+    long long total = (long long)(rows * h);
+#ifdef _OPENMP
+    int nt = threads > 0 ? threads : 1;
+#pragma omp parallel num_threads(nt)
+#endif
+    {
+        float *scores = (float *)malloc((pos0 + rows > 0 ? pos0 + rows : 1) * sizeof(float));
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (long long t = 0; t < total; ++t) {
+            size_t r = (size_t)t / h;
+            size_t hh = (size_t)t % h;
+            size_t p = pos0 + r;
+            size_t first = (window > 0 && p + 1 > window) ? p + 1 - window : 0;
+            size_t qoff = (r * h + hh) * hd;
+            ebo_attn_row(q + qoff, k, v, o + qoff, hkv, hh / group, first, p, hd, scale, scores);
         }
         free(scores);
     }

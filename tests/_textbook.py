@@ -7,11 +7,11 @@ h // (H / Hkv)); they share no code with oracle/oracle.c.
 import numpy as np
 
 
-def attention_f64(q, k, v, scale, causal=True, q_offset=0):
+def attention_f64(q, k, v, scale, causal=True, q_offset=0, window=0):
     """q [T, H, D], k/v [S, Hkv, D] -> o [T, H, D] in float64.
 
-    Query row t sits at absolute position q_offset + t and may attend keys 0..=that
-    position when causal."""
+    Query row t sits at absolute position p = q_offset + t and may attend keys 0..=p when
+    causal; with window > 0 only the keys p - window < j <= p."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -24,6 +24,8 @@ def attention_f64(q, k, v, scale, causal=True, q_offset=0):
     if causal:
         pos = q_offset + np.arange(T)[:, None]
         mask = np.arange(S)[None, :] > pos
+        if window > 0:
+            mask = mask | (np.arange(S)[None, :] <= pos - window)
         s = np.where(mask[None], -np.inf, s)
     s = s - s.max(axis=-1, keepdims=True)
     p = np.exp(s)

@@ -127,6 +127,25 @@ def test_decode_validation_and_workspace():
     assert l.eb_attn_decode_workspace_floats(6, 4, 5, 8, 256) == 0  # bad heads -> 0
 
 
+def test_chunk_and_window_validation():
+    l = eb.lib()
+    # rows [60, 76) past max_seq 70
+    st, msg = _err(l.eb_launch_attn_prefill_chunk, None, None, 16 * 4 * 8, None, 1 << 20, None,
+                   1 << 20, None, 16 * 4 * 8, 4, 2, 60, 16, 8, 70, 0.3, 0)
+    assert st == 4 and "max_seq" in msg
+    # unsupported head_dim
+    st, msg = _err(l.eb_launch_attn_prefill_chunk, None, None, 1, None, 1, None, 1, None, 1, 4,
+                   2, 0, 1, 6, 8, 0.3, 0)
+    assert st == 3 and "head_dim" in msg
+    # zero rows is a no-op
+    assert l.eb_launch_attn_prefill_chunk(None, None, 0, None, 64, None, 64, None, 0, 4, 2, 3,
+                                          0, 8, 4, 0.3, 0) == 0
+    # windowed decode checks like decode
+    st, msg = _err(l.eb_launch_attn_decode_window, None, None, 16 * 128, None, 16 * 8 * 128,
+                   None, 16 * 8 * 128, None, 16 * 128, 16, 8, 16, 128, 16, 0.1, 4, None, 0, 256)
+    assert st == 4 and "pos" in msg
+
+
 def test_rmsnorm_rope_validation():
     l = eb.lib()
     st, msg = _err(l.eb_launch_rmsnorm, None, None, 30, None, 9, None, 30, 3, 10, 1e-6)

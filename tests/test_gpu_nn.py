@@ -255,8 +255,8 @@ def test_forward_routing_and_errors(dev):
     q = upload(dev, oracle.randn((2, H * hd), 1))
     k = upload(dev, oracle.randn((2, Hkv * hd), 2))
     rec = eb.Recorder(dev)
-    with pytest.raises(eb.UnsupportedConfig):       # 2 rows at base_pos 5: chunked prefill
-        attn.forward_qkv(rec, q, k, k, rope, kv, 0, 2, 5)
+    with pytest.raises(eb.ShapeMismatch):           # rows [15, 17) past max_seq 16
+        attn.forward_qkv(rec, q, k, k, rope, kv, 0, 2, 15)
     with pytest.raises(eb.ShapeMismatch):           # layer out of range
         attn.forward_qkv(rec, q, k, k, rope, kv, 1, 2, 0)
     rec.submit()

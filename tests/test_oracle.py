@@ -296,6 +296,46 @@ def test_randn_is_standard_normal():
     assert np.isfinite(z).all()
 
 
+# ------------------------------------------------------ chunked / windowed attention ----
+
+@pytest.mark.parametrize("h,hkv,pos0,rows,hd,window", [
+    (4, 2, 0, 9, 16, 0),
+    (4, 2, 7, 5, 16, 0),       # continuation chunk
+    (16, 8, 40, 9, 128, 0),
+    (8, 2, 13, 11, 32, 6),     # window shorter than the chunk
+    (4, 1, 0, 20, 8, 4),
+    (16, 8, 30, 4, 256, 1000), # window longer than the context: no effect
+])
+def test_chunk_matches_f64_textbook(h, hkv, pos0, rows, hd, window):
+    S = pos0 + rows
+    q, k, v = oracle.randn((rows, h, hd), 1), oracle.randn((S, hkv, hd), 2), oracle.randn((S, hkv, hd), 3)
+    got = oracle.attn_chunk(q, k, v, h, hkv, pos0, rows, hd, 0.3, window)
+    want = attention_f64(q, k, v, 0.3, q_offset=pos0, window=window)
+    assert rel_l2_f64(got, want) < F32_VS_F64
+
+
+def test_chunk_reduces_to_prefill_and_decode_bitwise():
+    h, hkv, hd, S = 8, 2, 32, 23
+    q, k, v = oracle.randn((S, h, hd), 1), oracle.randn((S, hkv, hd), 2), oracle.randn((S, hkv, hd), 3)
+    full = oracle.attn_prefill(q, k, v, h, hkv, S, hd)
+    assert np.array_equal(oracle.attn_chunk(q, k, v, h, hkv, 0, S, hd), full)
+    # a continuation chunk computes exactly the rows the full prefill computes there
+    assert np.array_equal(oracle.attn_chunk(q[10:], k, v, h, hkv, 10, S - 10, hd), full[10:])
+    # one row at position p is a decode step at p
+    p = 17
+    assert np.array_equal(oracle.attn_chunk(q[p:p + 1], k, v, h, hkv, p, 1, hd)[0],
+                          oracle.attn_decode(q[p], k, v, h, hkv, p, hd, S))
+    # a window covering the whole context changes nothing
+    assert np.array_equal(oracle.attn_chunk(q, k, v, h, hkv, 0, S, hd, window=S), full)
+
+
+def test_window_of_one_returns_the_current_value_row():
+    h, hkv, hd, S = 4, 2, 8, 12
+    q, k, v = oracle.randn((S, h, hd), 1), oracle.randn((S, hkv, hd), 2), oracle.randn((S, hkv, hd), 3)
+    got = oracle.attn_chunk(q, k, v, h, hkv, 0, S, hd, window=1)
+    assert np.array_equal(got, np.repeat(v, h // hkv, axis=1))
+
+
 # ------------------------------------------------------------------ mutation test ----------
 
 @pytest.mark.parametrize("plant", [1, 2, 3, 4])
