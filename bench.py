@@ -122,20 +122,34 @@ class DecodeWorkload:
     pos+1 keys, one kernel. `per_graph` consecutive steps (cycling through the caches) are
     captured in one HIP graph so the host launch cost is paid once per graph."""
 
-    def __init__(self, eb, hip, dev, H, Hkv, hd, max_seq, pos, scale, seed=0, per_graph=64):
+    def __init__(self, eb, hip, dev, H, Hkv, hd, max_seq, pos, scale, seed=0, per_graph=64,
+                 f16=False):
         self.eb, self.hip, self.dev = eb, hip, dev
         self.H, self.Hkv, self.hd, self.max_seq, self.pos, self.scale = H, Hkv, hd, max_seq, pos, scale
+        self.f16 = f16
+        esize = 2 if f16 else 4
         self.keys = pos + 1
-        self.kv_bytes = 2 * self.keys * Hkv * hd * 4
-        cache_bytes = 2 * max_seq * Hkv * hd * 4
+        self.kv_bytes = 2 * self.keys * Hkv * hd * esize
+        cache_bytes = 2 * max_seq * Hkv * hd * esize
         self.n_caches = max(3, int(np.ceil(1.5 * MALL_BYTES / cache_bytes)) + 1)
         rng = np.random.default_rng(seed)
-        kfill = randn(rng, (max_seq, Hkv, hd))
-        vfill = randn(rng, (max_seq, Hkv, hd))
+        kfill = eb.Tensor.from_f32(dev, (max_seq, Hkv, hd), randn(rng, (max_seq, Hkv, hd)))
+        vfill = eb.Tensor.from_f32(dev, (max_seq, Hkv, hd), randn(rng, (max_seq, Hkv, hd)))
         self.caches = []
         for _ in range(self.n_caches):
-            self.caches.append((eb.Tensor.from_f32(dev, kfill.shape, kfill),
-                                eb.Tensor.from_f32(dev, vfill.shape, vfill)))
+            pair = []
+            for fill in (kfill, vfill):
+                if f16:
+                    t = eb.Tensor.empty(dev, fill.shape, eb.DType.F16)
+                    eb.launch_kv_write_f16(dev.stream, t.data_ptr, t.numel(), fill.data_ptr,
+                                           fill.numel(), Hkv, max_seq, hd, max_seq, 0)
+                else:
+                    t = eb.Tensor.empty(dev, fill.shape)
+                    eb.launch_kv_write(dev.stream, t.data_ptr, t.numel(), fill.data_ptr,
+                                       fill.numel(), Hkv, max_seq, hd, max_seq, 0)
+                pair.append(t)
+            self.caches.append(tuple(pair))
+        dev.synchronize()
         del kfill, vfill
         self.q = eb.Tensor.from_f32(dev, (H, hd), randn(rng, (H, hd)))
         self.knew = eb.Tensor.from_f32(dev, (1, Hkv, hd), randn(rng, (1, Hkv, hd)))
@@ -150,6 +164,13 @@ class DecodeWorkload:
 
     def _step(self, cache):
         kc, vc = cache
+        if self.f16:
+            self.eb.launch_attn_decode_step_f16(
+                self.dev.stream, self.q.data_ptr, self.q.numel(), self.knew.data_ptr,
+                self.vnew.data_ptr, self.knew.numel(), kc.data_ptr, kc.numel(), vc.data_ptr,
+                vc.numel(), self.o.data_ptr, self.o.numel(), self.H, self.Hkv, self.pos,
+                self.hd, self.max_seq, self.scale, 0, self.ws.data_ptr, self.wsn, self.cus)
+            return
         self.eb.launch_attn_decode_step(
             self.dev.stream, self.q.data_ptr, self.q.numel(), self.knew.data_ptr,
             self.vnew.data_ptr, self.knew.numel(), kc.data_ptr, kc.numel(), vc.data_ptr,
@@ -242,8 +263,12 @@ def decode_extras(eb, hip, dev, sc128) -> dict:
             ("mistral_keys8193", 32, 8, 128, 32768, 8192, sc128),
             ("mistral_keys32768", 32, 8, 128, 32768, 32767, sc128),
             ("gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0)]
-    for name, H, Hkv, hd, ms, pos, sc in cfgs:
-        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc)
+    # IEEE-half caches (no counterpart in the reference): half the bytes per key.
+    cfgs += [("f16_qwen_L8191", 16, 8, 128, 8192, 8191, sc128, True),
+             ("f16_mistral_keys32768", 32, 8, 128, 32768, 32767, sc128, True),
+             ("f16_gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0, True)]
+    for name, H, Hkv, hd, ms, pos, sc, *f16 in cfgs:
+        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc, f16=bool(f16))
         w.run_steps(20)
         t_step, _ = w.run_steps(500)
         out[f"decode_{name}"] = {

@@ -6,7 +6,7 @@ reference's Rust interface:
 
 - ``gpu``: DType, EyebrowseError, Device, Tensor, Recorder (crates/eyebrowse-gpu);
 - ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels),
-  plus chunked / windowed attention and the fused decode step;
+  plus chunked / windowed attention, the fused decode step and IEEE-half caches;
 - ``nn``: Rope, KvCache, Attention (crates/eyebrowse-nn).
 """
 from ._lib import LIB_PATH, lib
@@ -14,9 +14,11 @@ from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, O
                   Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
 from .kernels import (attn_decode, attn_decode_step, attn_decode_step_window,
                       attn_decode_window, attn_decode_workspace_floats, attn_prefill,
-                      attn_prefill_chunk, kv_write, launch_attn_decode, launch_attn_decode_step,
+                      attn_prefill_chunk, kv_write, launch_attn_decode, launch_attn_decode_f16,
+                      launch_attn_decode_step, launch_attn_decode_step_f16,
                       launch_attn_decode_window, launch_attn_prefill, launch_attn_prefill_chunk,
-                      launch_kv_write, launch_rmsnorm, launch_rope, rmsnorm, rope)
+                      launch_attn_prefill_chunk_f16, launch_kv_write, launch_kv_write_f16,
+                      launch_rmsnorm, launch_rope, rmsnorm, rope)
 from .nn import Attention, KvCache, Rope
 
 __all__ = [
@@ -24,7 +26,9 @@ __all__ = [
     "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
     "attn_decode_step", "attn_decode_step_window", "attn_decode_window",
     "attn_decode_workspace_floats", "attn_prefill", "attn_prefill_chunk", "kv_write",
-    "launch_attn_decode", "launch_attn_decode_step", "launch_attn_decode_window",
-    "launch_attn_prefill", "launch_attn_prefill_chunk", "launch_kv_write", "launch_rmsnorm",
+    "launch_attn_decode", "launch_attn_decode_f16", "launch_attn_decode_step",
+    "launch_attn_decode_step_f16", "launch_attn_decode_window", "launch_attn_prefill",
+    "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_kv_write",
+    "launch_kv_write_f16", "launch_rmsnorm",
     "launch_rope", "rmsnorm", "rope", "Attention", "KvCache", "Rope",
 ]

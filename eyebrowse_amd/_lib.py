@@ -96,6 +96,18 @@ SIGNATURES = {
     "eb_launch_attn_decode_step": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size,
                                           c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
                                           c_size, c_size, c_float, c_vp, c_size, c_int]),
+    "eb_launch_kv_write_f16": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
+                                      c_size, c_size]),
+    "eb_launch_attn_prefill_chunk_f16": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,
+                                                c_vp, c_size, c_size, c_size, c_size, c_size,
+                                                c_size, c_size, c_float, c_size]),
+    "eb_launch_attn_decode_f16": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
+                                         c_size, c_size, c_size, c_size, c_size, c_size, c_float,
+                                         c_size, c_vp, c_size, c_int]),
+    "eb_launch_attn_decode_step_f16": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp,
+                                              c_size, c_vp, c_size, c_vp, c_size, c_size, c_size,
+                                              c_size, c_size, c_size, c_float, c_size, c_vp,
+                                              c_size, c_int]),
     "eb_launch_rmsnorm": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
                                  c_size, c_float]),
     "eb_launch_rope": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size, c_size,
@@ -108,6 +120,8 @@ SIGNATURES = {
     "eb_rope_apply": (c_st, [c_vp, c_vp, c_vp, c_size, c_size, c_size, ctypes.POINTER(c_vp)]),
     "eb_kv_cache_new_per_layer": (c_st, [c_vp, ctypes.POINTER(c_size), c_size, c_size, c_size,
                                          ctypes.POINTER(c_vp)]),
+    "eb_kv_cache_new_per_layer_dtype": (c_st, [c_vp, ctypes.POINTER(c_size), c_size, c_size,
+                                               c_size, c_int, ctypes.POINTER(c_vp)]),
     "eb_kv_cache_release": (None, [c_vp]),
     "eb_kv_cache_k": (c_vp, [c_vp, c_size]),
     "eb_kv_cache_v": (c_vp, [c_vp, c_size]),

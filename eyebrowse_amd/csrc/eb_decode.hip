@@ -45,6 +45,12 @@
 #ifndef EB_DECODE_U
 #define EB_DECODE_U 0
 #endif
+// Wave steps per iteration over IEEE-half caches. Two would keep the bytes in flight of
+// one f32 step, but measured 4 % slower than one at 32k keys: per byte the f16 kernel
+// does twice the f32 arithmetic (v_fma_mix per dim and head), which then dominates.
+#ifndef EB_DECODE_U16
+#define EB_DECODE_U16 1
+#endif
 // Workgroups per CU the register allocation must allow (launch-bounds minimum); 0 picks
 // 2 when at most 2 query heads share a workgroup (then everything fits 256 VGPRs), else 1.
 #ifndef EB_DECODE_MINB
@@ -61,16 +67,16 @@ constexpr float kSlack = 8.0f;  // log2-units a score may exceed the reference m
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int HD, int G>
+template <int HD, int G, int UDEF = 1>
 struct DecodeShape {
     static constexpr int DPL = HD >= 16 ? 16 : HD;  // dims per lane
     static constexpr int LPK = HD / DPL;            // lanes per key row
     static constexpr int KPW = 64 / LPK;            // keys per wave step
     static constexpr int NV4 = DPL / 4;             // 16-byte loads per lane per row
     // Wave steps per iteration: each of the two register buffers holds U*NV4*2 16-byte
-    // loads per lane. One step per buffer keeps everything in VGPRs; with the workgroups
-    // of a CU that is as much in flight as the HBM rewards.
-    static constexpr int U = EB_DECODE_U > 0 ? EB_DECODE_U : 1;
+    // loads per lane (half that over f16 caches). One f32 step per buffer keeps everything
+    // in VGPRs; with the workgroups of a CU that is as much in flight as the HBM rewards.
+    static constexpr int U = EB_DECODE_U > 0 ? EB_DECODE_U : UDEF;
     static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
     // Epilogue LDS: NS lane-group states of SS floats (G heads of HD, padded by 4 floats
     // so that the lane groups' 16-byte writes fall in different banks), plus m, l, the
@@ -81,15 +87,45 @@ struct DecodeShape {
     static_assert(DPL % 4 == 0 && LPK <= 16, "head_dim must be a multiple of 4, at most 256");
 };
 
-// Byte offset (within a row) of 16-byte load number i of dim slice `ls`.
+// Byte offset (within a row) of 16-byte load number j of dim slice `ls`.
 template <int HD>
-__device__ __forceinline__ int dim_byte(int i, int ls) {
-    return (i * DecodeShape<HD, 1>::LPK + ls) * 16;
+__device__ __forceinline__ int dim_byte(int j, int ls) {
+    return (j * DecodeShape<HD, 1>::LPK + ls) * 16;
+}
+
+// First dim of the lane's f32x4 unit i: a 16-byte load holds 4 dims of an f32 cache row
+// and 8 of an f16 one, so unit i of an f16 lane is half of load i/2.
+template <int HD, bool H16>
+__device__ __forceinline__ int dim_of(int i, int ls) {
+    if constexpr (H16)
+        return dim_byte<HD>(i / 2, ls) / 2 + (i % 2) * 4;
+    else
+        return dim_byte<HD>(i, ls) / 4;
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// Unit i (4 dims, as f32) of a lane's raw 16-byte loads of one row.
+template <bool H16>
+__device__ __forceinline__ f32x4 unit_f32(const f32x4 *raw, int i) {
+    if constexpr (H16) {
+        const f16x8 h = __builtin_bit_cast(f16x8, raw[i / 2]);
+        return (i % 2) ? f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]}
+                       : f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    } else {
+        return raw[i];
+    }
+}
+
+// f32 -> IEEE half -> f32: the value an f16 cache holds for x (round to nearest even).
+__device__ __forceinline__ f32x4 through_f16(f32x4 x) {
+    return __builtin_convertvector(__builtin_convertvector(x, f16x4), f32x4);
 }
 
 // Raw buffer resource over [p, p + nbytes). The operands are made wave-uniform explicitly
 // so that the descriptor lives in SGPRs (a per-lane descriptor costs a loop per load).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *p, int nbytes) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int nbytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
@@ -106,10 +142,10 @@ __device__ __forceinline__ f32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int vof
 
 struct DecodeArgs {
     const float *q;
-    const float *kc;   // cache rows read (and row `pos` written when knew != null)
-    const float *vc;
-    float *kc_w;       // same as kc, writable
-    float *vc_w;
+    const void *kc;    // cache rows read (and row `pos` written when knew != null),
+    const void *vc;    // f32 or IEEE half elements
+    void *kc_w;        // same as kc, writable
+    void *vc_w;
     const float *knew; // [Hkv, HD] new token K (or null)
     const float *vnew;
     float *o;
@@ -119,11 +155,18 @@ struct DecodeArgs {
     float scale_log2;
 };
 
-template <int HD, int G>
+// H16: the caches hold IEEE half elements (converted to f32 as they are loaded).
+template <int HD, int G, bool H16>
+using DecodeShapeOf = DecodeShape<HD, G, H16 ? EB_DECODE_U16 : 1>;
+
+template <int HD, int G, bool H16>
 __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G <= 2 ? 2 : 1))) void decode_kernel(DecodeArgs a) {
-    using S = DecodeShape<HD, G>;
+    using S = DecodeShapeOf<HD, G, H16>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
+    constexpr int EB = H16 ? 2 : 4;           // bytes per cache element
+    constexpr int NL = H16 ? NV4 / 2 : NV4;   // 16-byte loads per lane per row
+    static_assert(!H16 || NV4 % 2 == 0, "f16 caches need head_dim >= 8");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nsub = a.g / G;
@@ -144,17 +187,24 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     const bool tail_new = a.knew != nullptr && split == (pos / S::KPW) % a.nsplit;
     const int nblk = (ce + S::KPW - 1) / S::KPW;
     const int my_blk = nblk > split ? (nblk - split + a.nsplit - 1) / a.nsplit : 0;
-    const int row_bytes = a.hkv * HD * 4;
+    const int row_bytes = a.hkv * HD * EB;
 
     // New-token write: one workgroup per KV head copies the row into the cache. No
     // workgroup reads cache row `pos` in this launch.
     if (tail_new && (col % nsub) == 0) {
         const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
         for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
-            *reinterpret_cast<f32x4 *>(a.kc_w + dst + 4 * i) =
-                *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
-            *reinterpret_cast<f32x4 *>(a.vc_w + dst + 4 * i) =
-                *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
+            const f32x4 kx = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
+            const f32x4 vx = *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
+            if constexpr (H16) {
+                *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.kc_w) + dst + 4 * i) =
+                    __builtin_convertvector(kx, f16x4);
+                *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.vc_w) + dst + 4 * i) =
+                    __builtin_convertvector(vx, f16x4);
+            } else {
+                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.kc_w) + dst + 4 * i) = kx;
+                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.vc_w) + dst + 4 * i) = vx;
+            }
         }
     }
 
@@ -163,8 +213,8 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
         for (int i = 0; i < NV4; ++i)
-            qr[gi][i] = *reinterpret_cast<const f32x4 *>(
-                reinterpret_cast<const char *>(a.q + (size_t)(head0 + gi) * HD) + dim_byte<HD>(i, ls));
+            qr[gi][i] = *reinterpret_cast<const f32x4 *>(a.q + (size_t)(head0 + gi) * HD +
+                                                         dim_of<HD, H16>(i, ls));
 
     float m[G], l[G];
     f32x4 acc[G][NV4];
@@ -189,31 +239,31 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         rowof[u] = ((u * kWaves + wave) * a.nsplit + split) * S::KPW + kg;  // minus it0
         voff[u] = rowof[u] * row_bytes + dim_byte<HD>(0, ls);
     }
-    const float *kbase = a.kc + (size_t)kvh * HD;
-    const float *vbase = a.vc + (size_t)kvh * HD;
+    const char *kbase = static_cast<const char *>(a.kc) + (size_t)kvh * HD * EB;
+    const char *vbase = static_cast<const char *>(a.vc) + (size_t)kvh * HD * EB;
     auto rows_from = [&](int it) { return it * blk_stride * S::KPW; };
-    auto load_iter = [&](int it, f32x4 (&kv)[U][NV4], f32x4 (&vv)[U][NV4]) {
+    auto load_iter = [&](int it, f32x4 (&kv)[U][NL], f32x4 (&vv)[U][NL]) {
         const int r0 = rows_from(it);
         const int left = min(ce - r0, blk_stride * S::KPW);  // rows in range, window-capped
-        const int nbytes = left > 0 ? (left - 1) * row_bytes + HD * 4 : 0;
-        const size_t off = (size_t)r0 * a.hkv * HD;
+        const int nbytes = left > 0 ? (left - 1) * row_bytes + HD * EB : 0;
+        const size_t off = (size_t)r0 * row_bytes;
         const __amdgpu_buffer_rsrc_t kres = make_rsrc(kbase + off, nbytes);
         const __amdgpu_buffer_rsrc_t vres = make_rsrc(vbase + off, nbytes);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int i = 0; i < NV4; ++i) {
+            for (int j = 0; j < NL; ++j) {
                 // The dim offset goes in the scalar offset: the row offsets stay the only
                 // per-lane values (a hoisted per-load address would cost a VGPR each).
                 // Range checks decide by row either way, since a row's dims end within
-                // its HD*4 bytes.
-                kv[u][i] = buffer_load16(kres, voff[u], i * S::LPK * 16);
-                vv[u][i] = buffer_load16(vres, voff[u], i * S::LPK * 16);
+                // its HD*EB bytes.
+                kv[u][j] = buffer_load16(kres, voff[u], j * S::LPK * 16);
+                vv[u][j] = buffer_load16(vres, voff[u], j * S::LPK * 16);
             }
     };
     // Online-softmax update of every head with the U rows of one iteration (rows at or
     // past `ce` are masked out).
-    auto consume_iter = [&](int it, const f32x4 (&kv)[U][NV4], const f32x4 (&vv)[U][NV4]) {
+    auto consume_iter = [&](int it, const f32x4 (&kv)[U][NL], const f32x4 (&vv)[U][NL]) {
         const int r0 = rows_from(it);
         // Scores of every head first (their DPP chains interleave).
         float sc[G][U];
@@ -221,9 +271,9 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                f32x4 t = qr[gi][0] * kv[u][0];
+                f32x4 t = qr[gi][0] * unit_f32<H16>(kv[u], 0);
 #pragma unroll
-                for (int i = 1; i < NV4; ++i) t += qr[gi][i] * kv[u][i];
+                for (int i = 1; i < NV4; ++i) t += qr[gi][i] * unit_f32<H16>(kv[u], i);
                 float sv = (t.x + t.y) + (t.z + t.w);
                 sv = eb::group_sum<S::LPK>(sv);
                 sc[gi][u] = (r0 + rowof[u] < ce) ? sv * a.scale_log2 : -INFINITY;
@@ -269,7 +319,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             for (int i = 0; i < NV4; ++i) {
                 f32x4 t = acc[gi][i];
 #pragma unroll
-                for (int u = 0; u < U; ++u) t += p[u] * vv[u][i];
+                for (int u = 0; u < U; ++u) t += p[u] * unit_f32<H16>(vv[u], i);
                 acc[gi][i] = t;
             }
         }
@@ -282,7 +332,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     const int n_iter = (my_blk + U * kWaves - 1) / (U * kWaves);
     const int n_pairs = (n_iter + 1) / 2;
     if (n_pairs > 0) {
-        f32x4 kA[U][NV4], vA[U][NV4], kB[U][NV4], vB[U][NV4];
+        f32x4 kA[U][NL], vA[U][NL], kB[U][NL], vB[U][NL];
         load_iter(0, kA, vA);
         load_iter(1, kB, vB);
         for (int pr = 1; pr < n_pairs; ++pr) {
@@ -303,10 +353,14 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         f32x4 kn[NV4], vn[NV4];
 #pragma unroll
         for (int i = 0; i < NV4; ++i) {
-            kn[i] = *reinterpret_cast<const f32x4 *>(
-                reinterpret_cast<const char *>(a.knew + (size_t)kvh * HD) + dim_byte<HD>(i, ls));
-            vn[i] = *reinterpret_cast<const f32x4 *>(
-                reinterpret_cast<const char *>(a.vnew + (size_t)kvh * HD) + dim_byte<HD>(i, ls));
+            kn[i] = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD +
+                                                     dim_of<HD, H16>(i, ls));
+            vn[i] = *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD +
+                                                     dim_of<HD, H16>(i, ls));
+            if constexpr (H16) {  // the value the cache row now holds
+                kn[i] = through_f16(kn[i]);
+                vn[i] = through_f16(vn[i]);
+            }
         }
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
@@ -343,7 +397,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     for (int gi = 0; gi < G; ++gi) {
 #pragma unroll
         for (int i = 0; i < NV4; ++i)
-            *reinterpret_cast<f32x4 *>(s_acc + st * SS + gi * HD + dim_byte<HD>(i, ls) / 4) =
+            *reinterpret_cast<f32x4 *>(s_acc + st * SS + gi * HD + dim_of<HD, H16>(i, ls)) =
                 acc[gi][i];
         if (ls == 0) {
             s_m[gi * NS + st] = m[gi];
@@ -480,24 +534,31 @@ struct DecodePlan {
     int nsplit = 1;  // splits along the key axis
 };
 
-template <int G>
+template <int G, bool H16>
 int keys_per_iter_g(size_t hd) {
     switch (hd) {
-        case 4: return DecodeShape<4, G>::KEYS_PER_ITER;
-        case 8: return DecodeShape<8, G>::KEYS_PER_ITER;
-        case 16: return DecodeShape<16, G>::KEYS_PER_ITER;
-        case 32: return DecodeShape<32, G>::KEYS_PER_ITER;
-        case 64: return DecodeShape<64, G>::KEYS_PER_ITER;
-        case 128: return DecodeShape<128, G>::KEYS_PER_ITER;
-        default: return DecodeShape<256, G>::KEYS_PER_ITER;
+        case 4: return DecodeShapeOf<4, G, H16>::KEYS_PER_ITER;
+        case 8: return DecodeShapeOf<8, G, H16>::KEYS_PER_ITER;
+        case 16: return DecodeShapeOf<16, G, H16>::KEYS_PER_ITER;
+        case 32: return DecodeShapeOf<32, G, H16>::KEYS_PER_ITER;
+        case 64: return DecodeShapeOf<64, G, H16>::KEYS_PER_ITER;
+        case 128: return DecodeShapeOf<128, G, H16>::KEYS_PER_ITER;
+        default: return DecodeShapeOf<256, G, H16>::KEYS_PER_ITER;
     }
 }
 
-int keys_per_iter(size_t hd, int G) {
+int keys_per_iter(size_t hd, int G, bool h16) {
+    if (h16) {
+        switch (G) {
+            case 4: return keys_per_iter_g<4, true>(hd);
+            case 2: return keys_per_iter_g<2, true>(hd);
+            default: return keys_per_iter_g<1, true>(hd);
+        }
+    }
     switch (G) {
-        case 4: return keys_per_iter_g<4>(hd);
-        case 2: return keys_per_iter_g<2>(hd);
-        default: return keys_per_iter_g<1>(hd);
+        case 4: return keys_per_iter_g<4, false>(hd);
+        case 2: return keys_per_iter_g<2, false>(hd);
+        default: return keys_per_iter_g<1, false>(hd);
     }
 }
 
@@ -511,7 +572,7 @@ int wgs_per_cu() {
     return v;
 }
 
-DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count) {
+DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count, bool h16) {
     DecodePlan p;
     const size_t g = h / hkv;
     // At most 4 query heads per workgroup: their q fragments and accumulators, plus two
@@ -520,7 +581,7 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     p.nsub = (int)(g / p.G);
     const size_t keys = pos + 1;
     const size_t cols = hkv * (size_t)p.nsub;
-    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G);
+    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G, h16);
     // Enough workgroups to cover the CUs, but at least one pair of iterations per split.
     const size_t target = (size_t)cu_count * (size_t)wgs_per_cu();
     size_t nsplit = std::max<size_t>(1, target / cols);
@@ -534,30 +595,30 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     return p;
 }
 
-template <int HD, int G>
+template <int HD, int G, bool H16>
 hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
-    using S = DecodeShape<HD, G>;
+    using S = DecodeShapeOf<HD, G, H16>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     if (S::LDS_BYTES > 64 * 1024)
         std::call_once(once, [&] {
-            attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&decode_kernel<HD, G>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)S::LDS_BYTES);
+            attr_err = hipFuncSetAttribute(
+                reinterpret_cast<const void *>(&decode_kernel<HD, G, H16>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS_BYTES);
         });
     if (attr_err != hipSuccess) return attr_err;
     dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
-    decode_kernel<HD, G><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
+    decode_kernel<HD, G, H16><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
     return hipSuccess;
 }
 
-template <int HD>
+template <int HD, bool H16>
 hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     hipError_t e;
     switch (p.G) {
-        case 4: e = launch_g<HD, 4>(st, p, a); break;
-        case 2: e = launch_g<HD, 2>(st, p, a); break;
-        default: e = launch_g<HD, 1>(st, p, a); break;
+        case 4: e = launch_g<HD, 4, H16>(st, p, a); break;
+        case 2: e = launch_g<HD, 2, H16>(st, p, a); break;
+        default: e = launch_g<HD, 1, H16>(st, p, a); break;
     }
     if (e != hipSuccess) return e;
     if (p.nsplit > 1) {
@@ -569,32 +630,52 @@ hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     return hipSuccess;
 }
 
+template <bool H16>
+hipError_t launch_elem(hipStream_t st, size_t hd, const DecodePlan &p, const DecodeArgs &a) {
+    switch (hd) {
+        case 8: return launch_hd<8, H16>(st, p, a);
+        case 16: return launch_hd<16, H16>(st, p, a);
+        case 32: return launch_hd<32, H16>(st, p, a);
+        case 64: return launch_hd<64, H16>(st, p, a);
+        case 128: return launch_hd<128, H16>(st, p, a);
+        case 256: return launch_hd<256, H16>(st, p, a);
+        default:
+            if constexpr (!H16) return launch_hd<4, false>(st, p, a);  // hd 4 (f32 only)
+            return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
 
 namespace eb {
 
 // Workspace layout (floats): part_acc [nsplit*h*hd] | part_ml [nsplit*h*2]. Every split
 // writes its whole partial before the merge reads it, so no initialisation is needed.
-size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count) {
-    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count);
+// The f32 plan's split count bounds the f16 one (more rows per iteration, never more
+// splits), so the f32 figure serves both cache types.
+size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
+                               bool h16) {
+    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, h16);
     if (p.nsplit <= 1) return 0;
     return (size_t)p.nsplit * h * (hd + 2);
 }
 
-eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
-                             float *kc_w, float *vc_w, const float *knew, const float *vnew,
-                             float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                             float scale, float *ws, size_t ws_floats, int cu_count,
-                             size_t window) {
+eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc, const void *vc,
+                                 void *kc_w, void *vc_w, const float *knew, const float *vnew,
+                                 float *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                                 float scale, float *ws, size_t ws_floats, int cu_count,
+                                 size_t window, bool h16) {
+    if (h16 && hd < 8)
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
     // A window is a shift of the cache view: keys first..=pos become keys 0..=pos-first of
     // caches based at row `first` (the fused write then lands on the same absolute row).
     if (window > 0 && pos + 1 > window) {
         const size_t first = pos + 1 - window;
-        const size_t shift = first * hkv * hd;
-        kc += shift;
-        vc += shift;
-        if (kc_w) kc_w += shift;
-        if (vc_w) vc_w += shift;
+        const size_t shift = first * hkv * hd * (h16 ? 2 : 4);  // bytes
+        kc = static_cast<const char *>(kc) + shift;
+        vc = static_cast<const char *>(vc) + shift;
+        if (kc_w) kc_w = static_cast<char *>(kc_w) + shift;
+        if (vc_w) vc_w = static_cast<char *>(vc_w) + shift;
         pos -= first;
     }
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
@@ -603,8 +684,8 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
          reinterpret_cast<uintptr_t>(ws)) & 15)
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_decode: q/caches/new rows/o/workspace must be 16-byte aligned");
-    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count);
-    const size_t need = decode_workspace_floats(h, hkv, pos, hd, cu_count);
+    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, h16);
+    const size_t need = decode_workspace_floats(h, hkv, pos, hd, cu_count, h16);
     if (need > 0 && (ws == nullptr || ws_floats < need))
         return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace too small");
     DecodeArgs a{};
@@ -626,19 +707,20 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
     a.keys = (int)(pos + 1);
     a.nsplit = p.nsplit;
     a.scale_log2 = scale * kLog2e;
-    hipError_t e;
-    switch (hd) {
-        case 4: e = launch_hd<4>(st, p, a); break;
-        case 8: e = launch_hd<8>(st, p, a); break;
-        case 16: e = launch_hd<16>(st, p, a); break;
-        case 32: e = launch_hd<32>(st, p, a); break;
-        case 64: e = launch_hd<64>(st, p, a); break;
-        case 128: e = launch_hd<128>(st, p, a); break;
-        case 256: e = launch_hd<256>(st, p, a); break;
-        default: return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);
-    }
-    if (e != hipSuccess) return eb::hip_fail(e, "hipFuncSetAttribute(attn_decode)");
+    if (!attn_head_dim_supported(hd))
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);
+    const hipError_t e = h16 ? launch_elem<true>(st, hd, p, a) : launch_elem<false>(st, hd, p, a);
+    if (e != hipSuccess) return eb::hip_fail(e, "attn_decode launch set-up");
     return check_launch("attn_decode");
+}
+
+eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, const float *vc,
+                             float *kc_w, float *vc_w, const float *knew, const float *vnew,
+                             float *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                             float scale, float *ws, size_t ws_floats, int cu_count,
+                             size_t window) {
+    return launch_attn_decode_any(st, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv, pos, hd,
+                                  scale, ws, ws_floats, cu_count, window, false);
 }
 
 }  // namespace eb

@@ -16,16 +16,29 @@ constexpr int kBlock = 256;
 
 __global__ __launch_bounds__(kBlock) void kv_write_vec4_kernel(float4 *__restrict__ dst,
                                                                const float4 *__restrict__ src,
-                                                               unsigned n4) {
-    unsigned stride = gridDim.x * kBlock;
-    for (unsigned i = blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) dst[i] = src[i];
+                                                               size_t n4) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) dst[i] = src[i];
 }
 
 __global__ __launch_bounds__(kBlock) void kv_write_scalar_kernel(float *__restrict__ dst,
                                                                  const float *__restrict__ src,
-                                                                 unsigned n) {
-    unsigned stride = gridDim.x * kBlock;
-    for (unsigned i = blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+                                                                 size_t n) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// f32 rows into an IEEE-half cache: round to nearest even (v_cvt_f16_f32), four
+// elements per thread (16 bytes read, 8 written); n4 = elements / 4.
+__global__ __launch_bounds__(kBlock) void kv_write_f16_kernel(f16x4 *__restrict__ dst,
+                                                              const f32x4 *__restrict__ src,
+                                                              size_t n4) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride)
+        dst[i] = __builtin_convertvector(src[i], f16x4);
 }
 
 unsigned copy_grid(size_t n) {
@@ -87,11 +100,23 @@ eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t
     if (aligned && n % 4 == 0) {
         size_t n4 = n / 4;
         kv_write_vec4_kernel<<<copy_grid(n4), kBlock, 0, st>>>(
-            reinterpret_cast<float4 *>(dst), reinterpret_cast<const float4 *>(src), (unsigned)n4);
+            reinterpret_cast<float4 *>(dst), reinterpret_cast<const float4 *>(src), n4);
     } else {
-        kv_write_scalar_kernel<<<copy_grid(n), kBlock, 0, st>>>(dst, src, (unsigned)n);
+        kv_write_scalar_kernel<<<copy_grid(n), kBlock, 0, st>>>(dst, src, n);
     }
     return check_launch("kv_write");
+}
+
+eb_status launch_kv_write_f16(hipStream_t st, uint16_t *cache, const float *src, size_t hkv,
+                              size_t count, size_t hd, size_t dst_start) {
+    const size_t n = count * hkv * hd;  // hd is a multiple of 4
+    uint16_t *dst = cache + dst_start * hkv * hd;
+    if (((reinterpret_cast<uintptr_t>(dst) & 7) | (reinterpret_cast<uintptr_t>(src) & 15)) != 0)
+        return fail(EB_UNSUPPORTED_CONFIG, "kv_write: f16 cache / src must be 8 / 16-byte aligned");
+    const size_t n4 = n / 4;
+    kv_write_f16_kernel<<<copy_grid(n4), kBlock, 0, st>>>(
+        reinterpret_cast<f16x4 *>(dst), reinterpret_cast<const f32x4 *>(src), n4);
+    return check_launch("kv_write_f16");
 }
 
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,

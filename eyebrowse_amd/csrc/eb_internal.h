@@ -57,7 +57,8 @@ eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float 
                                     size_t pos0, size_t rows, size_t hd, float scale,
                                     size_t window);
 // Decode workspace: part_acc [nsplit*h*hd] | part_ml [nsplit*h*2], no initialisation.
-size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count);
+size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
+                               bool h16 = false);
 // knew/vnew null: plain attention over keys 0..=pos. Otherwise key `pos` comes from
 // knew/vnew ([hkv, hd]) and is also written to cache row `pos` through kc_w/vc_w.
 // window > 0 limits the keys to pos - window + 1..=pos. A workspace sized for
@@ -67,6 +68,21 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                              float scale, float *ws, size_t ws_floats, int cu_count,
                              size_t window = 0);
+// The same over caches of f32 (h16 false) or IEEE half (h16 true) elements; f16 caches
+// need head_dim >= 8.
+eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc, const void *vc,
+                                 void *kc_w, void *vc_w, const float *knew, const float *vnew,
+                                 float *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                                 float scale, float *ws, size_t ws_floats, int cu_count,
+                                 size_t window, bool h16);
+// kv_write into an IEEE-half cache: src f32 rows rounded to nearest even.
+eb_status launch_kv_write_f16(hipStream_t st, uint16_t *cache, const float *src, size_t hkv,
+                              size_t count, size_t hd, size_t dst_start);
+// Chunked prefill over IEEE-half caches (rows converted to f32 as they are staged).
+eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
+                                        const uint16_t *vc, float *o, size_t h, size_t hkv,
+                                        size_t pos0, size_t rows, size_t hd, float scale,
+                                        size_t window);
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
                          size_t rows, size_t dim, float eps);
 eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,

@@ -119,8 +119,17 @@ eb_status eb_rope_apply(const eb_rope_tables *rope, eb_recorder *rec, const eb_t
 
 eb_status eb_kv_cache_new_per_layer(eb_device *dev, const size_t *head_dims, size_t n_layers,
                                     size_t max_seq, size_t n_kv_heads, eb_kv_cache **out) {
+    return eb_kv_cache_new_per_layer_dtype(dev, head_dims, n_layers, max_seq, n_kv_heads, EB_F32,
+                                           out);
+}
+
+eb_status eb_kv_cache_new_per_layer_dtype(eb_device *dev, const size_t *head_dims,
+                                          size_t n_layers, size_t max_seq, size_t n_kv_heads,
+                                          eb_dtype dtype, eb_kv_cache **out) {
     if (!dev || !out || (n_layers > 0 && !head_dims))
         return fail(EB_OTHER, "kv_cache: null argument");
+    if (dtype != EB_F32 && dtype != EB_F16)
+        return fail(EB_UNSUPPORTED_CONFIG, "kv_cache: element type must be f32 or f16");
     *out = nullptr;
     auto kv = std::make_unique<eb_kv_cache>();
     kv->max_seq = max_seq;
@@ -128,8 +137,8 @@ eb_status eb_kv_cache_new_per_layer(eb_device *dev, const size_t *head_dims, siz
     for (size_t l = 0; l < n_layers; ++l) {
         const size_t shape[3] = {max_seq, n_kv_heads, head_dims[l]};
         eb_tensor *kt = nullptr, *vt = nullptr;
-        eb_status st = eb_tensor_empty(dev, shape, 3, EB_F32, &kt);
-        if (st == EB_OK) st = eb_tensor_empty(dev, shape, 3, EB_F32, &vt);
+        eb_status st = eb_tensor_empty(dev, shape, 3, dtype, &kt);
+        if (st == EB_OK) st = eb_tensor_empty(dev, shape, 3, dtype, &vt);
         if (st != EB_OK) {
             eb_tensor_release(kt);
             eb_kv_cache_release(kv.release());
@@ -250,11 +259,12 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
         // attention.rs:78-97 writes the new rows' K (post-RoPE) and V into the cache.
         EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
         EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
-        if (base_pos == 0 && d.window == 0) {
+        if (base_pos == 0 && d.window == 0 && eb_tensor_dtype(kc) == EB_F32) {
             // attention.rs:104-115 (routing rule :40): a prompt attends its fresh kr / v.
             EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
         } else {
-            // A continuation chunk (or a windowed prompt) attends the cache rows it needs.
+            // A continuation chunk, a windowed prompt, or any prompt over an f16 cache
+            // (so that prompt and decode read the same rounded K/V) attends the cache.
             EB_TRY(eb_attn_prefill_chunk(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, rows, hd,
                                          kv->max_seq, d.scale, d.window));
         }

@@ -41,6 +41,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // Native 4-wide vector for staged K/V values. HIP's float4 is a class type: a conditional
 // on it is lowered through a stack copy (scratch memory); this one stays in registers.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
 
@@ -73,9 +74,10 @@ struct PrefillCfg {
 // Fetch the K and V rows [kb, kb + STEP_KEYS) of KV head kvh into registers; rows past
 // T read as zero. Every element is assigned on every call (clamped addresses, selected
 // values): conditionally written register arrays end up in scratch memory.
-template <class C>
-__device__ __forceinline__ void prefill_load_step(const float *__restrict__ k,
-                                                  const float *__restrict__ v,
+// H16: k/v hold IEEE half elements, converted to f32 here.
+template <class C, bool H16>
+__device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
+                                                  const void *__restrict__ v,
                                                   f32x4 (&rk)[C::NLD], f32x4 (&rv)[C::NLD],
                                                   int kb, int T, int Hkv, int kvh, int tid) {
     constexpr int HD = C::HD_;
@@ -86,8 +88,16 @@ __device__ __forceinline__ void prefill_load_step(const float *__restrict__ k,
         const int c4 = idx % (HD / 4);
         const int key = kb + row;
         const size_t off = ((size_t)min(key, T - 1) * Hkv + kvh) * HD + c4 * 4;
-        const f32x4 kx = *reinterpret_cast<const f32x4 *>(k + off);
-        const f32x4 vx = *reinterpret_cast<const f32x4 *>(v + off);
+        f32x4 kx, vx;
+        if constexpr (H16) {
+            kx = __builtin_convertvector(
+                *reinterpret_cast<const f16x4 *>(static_cast<const _Float16 *>(k) + off), f32x4);
+            vx = __builtin_convertvector(
+                *reinterpret_cast<const f16x4 *>(static_cast<const _Float16 *>(v) + off), f32x4);
+        } else {
+            kx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(k) + off);
+            vx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(v) + off);
+        }
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         rk[r] = key < T ? kx : z;
         rv[r] = key < T ? vx : z;
@@ -118,10 +128,11 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
 // RANGE: queries start at position qbase and may have a sliding window; without it the
 // kernel is specialised to a prompt from position 0 (no window), whose masks are simpler.
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE>
+// H16: the K/V rows are IEEE half (an f16 KV cache), converted to f32 as they are staged.
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     float *__restrict__ o, int H, int Hkv, int rows, int nkeys, int qbase, int window,
     float scale_log2, int nqb, int ngroups) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
@@ -197,7 +208,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     float l = 0.0f;
 
     f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
+    prefill_load_step<C, H16>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
 
@@ -207,8 +218,8 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         const int kb = tile * kTile;
         // Prefetch the next step (past the last step this re-reads clamped rows; the
         // buffer written from them is never read).
-        prefill_load_step<C>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys, Hkv, kvh,
-                             tid);
+        prefill_load_step<C, H16>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys, Hkv,
+                                  kvh, tid);
 
         if (live && tile >= my_t0 && tile <= my_t1) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
@@ -393,17 +404,18 @@ struct PrefillRange {
     int nkeys;   // key rows available in k/v
     int qbase;   // position of query row 0
     int window;  // sliding window (0: none)
+    bool h16;    // k/v hold IEEE half elements
 };
 
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE>
-eb_status launch_prefill_r(hipStream_t st, const float *q, const float *k, const float *v,
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16>
+eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
                            float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE>),
+            reinterpret_cast<const void *>(&prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
@@ -411,18 +423,22 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const float *k, const
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const unsigned blocks = (unsigned)(nqb * ngroups);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE><<<blocks, C::THREADS, C::LDS_BYTES, st>>>(
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16><<<blocks, C::THREADS, C::LDS_BYTES, st>>>(
         q, k, v, o, H, Hkv, r.rows, r.nkeys, r.qbase, r.window, scale_log2, nqb, ngroups);
     return eb::check_launch("attn_prefill");
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT>
-eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const float *v,
+eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const void *v,
                            float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
+    if (r.h16)
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, true>(st, q, k, v, o, H, Hkv, r,
+                                                                  scale_log2);
     if (r.qbase == 0 && r.window == 0)
-        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false>(st, q, k, v, o, H, Hkv, r,
-                                                             scale_log2);
-    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true>(st, q, k, v, o, H, Hkv, r, scale_log2);
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false>(st, q, k, v, o, H, Hkv, r,
+                                                                    scale_log2);
+    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false>(st, q, k, v, o, H, Hkv, r,
+                                                               scale_log2);
 }
 
 // head_dim <= 128:
@@ -434,7 +450,7 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const float *k, const
 // head_dim 256: the Q fragment and O^T accumulators take ~450 registers per lane, so one
 // wave per SIMD: 4 waves, no key split.
 template <int HD>
-eb_status launch_prefill_hd(hipStream_t st, const float *q, const float *k, const float *v,
+eb_status launch_prefill_hd(hipStream_t st, const float *q, const void *k, const void *v,
                             float *o, int H, int Hkv, const PrefillRange &r,
                             float scale_log2) {
     const int g = H / Hkv;
@@ -445,7 +461,7 @@ eb_status launch_prefill_hd(hipStream_t st, const float *q, const float *k, cons
     return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
 }
 
-eb_status launch_prefill_range(hipStream_t st, const float *q, const float *k, const float *v,
+eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, const void *v,
                                float *o, size_t h, size_t hkv, size_t hd, float scale,
                                const PrefillRange &r) {
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
@@ -473,7 +489,7 @@ eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, co
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale) {
     return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
-                                PrefillRange{(int)s, (int)s, 0, 0});
+                                PrefillRange{(int)s, (int)s, 0, 0, false});
 }
 
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
@@ -482,7 +498,16 @@ eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float 
                                     size_t window) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window});
+                                             (int)window, false});
+}
+
+eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
+                                        const uint16_t *vc, float *o, size_t h, size_t hkv,
+                                        size_t pos0, size_t rows, size_t hd, float scale,
+                                        size_t window) {
+    return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
+                                PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
+                                             (int)window, true});
 }
 
 }  // namespace eb

@@ -407,6 +407,16 @@ static eb_status tensor_f32(const eb_tensor *t, const char *name, eb_device *dev
     return EB_OK;
 }
 
+// A KV cache: f32 or IEEE-half elements. `h16` reports which.
+static eb_status tensor_cache(const eb_tensor *t, const char *name, eb_device *dev, bool *h16) {
+    if (!t) return fail(EB_SHAPE_MISMATCH, "%s is null", name);
+    if (t->dtype != EB_F32 && t->dtype != EB_F16)
+        return fail(EB_SHAPE_MISMATCH, "%s must be f32 or f16", name);
+    if (t->dev != dev) return fail(EB_OTHER, "%s lives on another device", name);
+    *h16 = t->dtype == EB_F16;
+    return EB_OK;
+}
+
 #define EB_TRY(expr)                     \
     do {                                 \
         eb_status eb_s_ = (expr);        \
@@ -414,9 +424,9 @@ static eb_status tensor_f32(const eb_tensor *t, const char *name, eb_device *dev
     } while (0)
 
 // Float-buffer views with element counts, shared by the handle and raw entry points.
-static eb_status kv_write_checked(hipStream_t st, float *cache, size_t cache_n,
+static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
                                   const float *src, size_t src_n, size_t hkv, size_t count,
-                                  size_t hd, size_t max_seq, size_t dst) {
+                                  size_t hd, size_t max_seq, size_t dst, bool h16 = false) {
     if (hkv == 0 || hd == 0) return fail(EB_SHAPE_MISMATCH, "kv_write: hkv and hd must be > 0");
     if (dst > max_seq || count > max_seq - dst)
         return fail(EB_SHAPE_MISMATCH, "kv_write: rows [%zu, %zu) exceed max_seq %zu", dst,
@@ -426,7 +436,13 @@ static eb_status kv_write_checked(hipStream_t st, float *cache, size_t cache_n,
     if (count == 0) return eb::ok();
     EB_TRY(eb::check_ptr(cache, "cache"));
     EB_TRY(eb::check_ptr(src, "src"));
-    EB_TRY(eb::launch_kv_write(st, cache, src, hkv, count, hd, dst));
+    if (h16) {
+        if (hd % 4 != 0) return fail(EB_UNSUPPORTED_CONFIG, "kv_write: f16 caches need hd % 4 == 0");
+        EB_TRY(eb::launch_kv_write_f16(st, static_cast<uint16_t *>(cache), src, hkv, count, hd,
+                                       dst));
+    } else {
+        EB_TRY(eb::launch_kv_write(st, static_cast<float *>(cache), src, hkv, count, hd, dst));
+    }
     return eb::ok();
 }
 
@@ -451,15 +467,17 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
 }
 
 static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn,
-                                       const float *kc, size_t kcn, const float *vc, size_t vcn,
+                                       const void *kc, size_t kcn, const void *vc, size_t vcn,
                                        float *o, size_t on, size_t h, size_t hkv, size_t pos0,
                                        size_t rows, size_t hd, size_t max_seq, float scale,
-                                       size_t window) {
+                                       size_t window, bool h16 = false) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_prefill_chunk: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)",
                     hd);
+    if (h16 && hd < 8)
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_prefill_chunk: f16 caches need head_dim >= 8");
     if (pos0 > max_seq || rows > max_seq - pos0)
         return fail(EB_SHAPE_MISMATCH, "attn_prefill_chunk: rows [%zu, %zu) exceed max_seq %zu",
                     pos0, pos0 + rows, max_seq);
@@ -472,18 +490,27 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     EB_TRY(eb::check_ptr(kc, "kcache"));
     EB_TRY(eb::check_ptr(vc, "vcache"));
     EB_TRY(eb::check_ptr(o, "o"));
-    EB_TRY(eb::launch_attn_prefill_chunk(st, q, kc, vc, o, h, hkv, pos0, rows, hd, scale, window));
+    if (h16)
+        EB_TRY(eb::launch_attn_prefill_chunk_f16(st, q, static_cast<const uint16_t *>(kc),
+                                                 static_cast<const uint16_t *>(vc), o, h, hkv,
+                                                 pos0, rows, hd, scale, window));
+    else
+        EB_TRY(eb::launch_attn_prefill_chunk(st, q, static_cast<const float *>(kc),
+                                             static_cast<const float *>(vc), o, h, hkv, pos0,
+                                             rows, hd, scale, window));
     return eb::ok();
 }
 
-static eb_status decode_shape_checked(const float *q, size_t qn, const float *kc, size_t kcn,
-                                      const float *vc, size_t vcn, const float *o, size_t on,
+static eb_status decode_shape_checked(const float *q, size_t qn, const void *kc, size_t kcn,
+                                      const void *vc, size_t vcn, const float *o, size_t on,
                                       size_t h, size_t hkv, size_t pos, size_t hd,
-                                      size_t max_seq) {
+                                      size_t max_seq, bool h16 = false) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_decode: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)", hd);
+    if (h16 && hd < 8)
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
     if (pos >= max_seq)
         return fail(EB_SHAPE_MISMATCH, "attn_decode: pos %zu >= max_seq %zu", pos, max_seq);
     EB_TRY(eb::check_numel(qn, h * hd, "q"));
@@ -556,16 +583,27 @@ static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
 }
 
 // Shared by eb_attn_decode / eb_attn_decode_step: device workspace, then one launch.
-static eb_status device_decode(eb_device *dev, const float *q, const float *kc, const float *vc,
-                               float *kc_w, float *vc_w, const float *knew, const float *vnew,
+static eb_status device_decode(eb_device *dev, const float *q, const void *kc, const void *vc,
+                               void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                               float scale, size_t window = 0) {
+                               float scale, size_t window = 0, bool h16 = false) {
     size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
     float *ws = nullptr;
     if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
-    EB_TRY(eb::launch_attn_decode(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv, pos,
-                                  hd, scale, ws, wsn, dev->cu_count, window));
+    EB_TRY(eb::launch_attn_decode_any(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv,
+                                      pos, hd, scale, ws, wsn, dev->cu_count, window, h16));
     return eb::ok();
+}
+
+// Both caches of one layer share a dtype.
+static eb_status cache_pair(const eb_tensor *kc, const eb_tensor *vc, eb_device *dev,
+                            bool *h16) {
+    bool hk = false, hv = false;
+    EB_TRY(tensor_cache(kc, "kcache", dev, &hk));
+    EB_TRY(tensor_cache(vc, "vcache", dev, &hv));
+    if (hk != hv) return fail(EB_SHAPE_MISMATCH, "kcache and vcache dtypes differ");
+    *h16 = hk;
+    return EB_OK;
 }
 
 
@@ -574,11 +612,12 @@ extern "C" {
 eb_status eb_kv_write(eb_recorder *rec, eb_tensor *cache, const eb_tensor *src, size_t hkv,
                       size_t count, size_t hd, size_t max_seq, size_t dst_start) {
     EB_TRY(rec_ready(rec));
-    EB_TRY(tensor_f32(cache, "cache", rec->dev));
+    bool h16 = false;
+    EB_TRY(tensor_cache(cache, "cache", rec->dev, &h16));
     EB_TRY(tensor_f32(src, "src", rec->dev));
-    return kv_write_checked(rec->dev->stream, (float *)cache->ptr, eb_tensor_numel(cache),
+    return kv_write_checked(rec->dev->stream, cache->ptr, eb_tensor_numel(cache),
                             (const float *)src->ptr, eb_tensor_numel(src), hkv, count, hd,
-                            max_seq, dst_start);
+                            max_seq, dst_start, h16);
 }
 
 eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
@@ -598,19 +637,7 @@ eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor 
 eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
                          const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
                          size_t pos, size_t hd, size_t max_seq, float scale) {
-    EB_TRY(rec_ready(rec));
-    EB_TRY(tensor_f32(q, "q", rec->dev));
-    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
-    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
-    EB_TRY(tensor_f32(o, "o", rec->dev));
-    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q),
-                                (const float *)kcache->ptr, eb_tensor_numel(kcache),
-                                (const float *)vcache->ptr, eb_tensor_numel(vcache),
-                                (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
-                                max_seq));
-    return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
-                         (const float *)vcache->ptr, nullptr, nullptr, nullptr, nullptr,
-                         (float *)o->ptr, h, hkv, pos, hd, scale);
+    return eb_attn_decode_window(rec, q, kcache, vcache, o, h, hkv, pos, hd, max_seq, scale, 0);
 }
 
 eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
@@ -619,14 +646,13 @@ eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_t
                                 float scale, size_t window) {
     EB_TRY(rec_ready(rec));
     EB_TRY(tensor_f32(q, "q", rec->dev));
-    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
-    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    bool h16 = false;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
     EB_TRY(tensor_f32(o, "o", rec->dev));
     return prefill_chunk_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
-                                 (const float *)kcache->ptr, eb_tensor_numel(kcache),
-                                 (const float *)vcache->ptr, eb_tensor_numel(vcache),
-                                 (float *)o->ptr, eb_tensor_numel(o), h, hkv, pos0, rows, hd,
-                                 max_seq, scale, window);
+                                 kcache->ptr, eb_tensor_numel(kcache), vcache->ptr,
+                                 eb_tensor_numel(vcache), (float *)o->ptr, eb_tensor_numel(o), h,
+                                 hkv, pos0, rows, hd, max_seq, scale, window, h16);
 }
 
 eb_status eb_attn_decode_window(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
@@ -635,17 +661,16 @@ eb_status eb_attn_decode_window(eb_recorder *rec, const eb_tensor *q, const eb_t
                                 size_t window) {
     EB_TRY(rec_ready(rec));
     EB_TRY(tensor_f32(q, "q", rec->dev));
-    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
-    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    bool h16 = false;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
     EB_TRY(tensor_f32(o, "o", rec->dev));
-    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q),
-                                (const float *)kcache->ptr, eb_tensor_numel(kcache),
-                                (const float *)vcache->ptr, eb_tensor_numel(vcache),
+    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q), kcache->ptr,
+                                eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache),
                                 (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
-                                max_seq));
-    return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
-                         (const float *)vcache->ptr, nullptr, nullptr, nullptr, nullptr,
-                         (float *)o->ptr, h, hkv, pos, hd, scale, window);
+                                max_seq, h16));
+    return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, nullptr,
+                         nullptr, nullptr, nullptr, (float *)o->ptr, h, hkv, pos, hd, scale,
+                         window, h16);
 }
 
 eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
@@ -665,21 +690,19 @@ eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const
     EB_TRY(tensor_f32(q, "q", rec->dev));
     EB_TRY(tensor_f32(knew, "knew", rec->dev));
     EB_TRY(tensor_f32(vnew, "vnew", rec->dev));
-    EB_TRY(tensor_f32(kcache, "kcache", rec->dev));
-    EB_TRY(tensor_f32(vcache, "vcache", rec->dev));
+    bool h16 = false;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
     EB_TRY(tensor_f32(o, "o", rec->dev));
-    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q),
-                                (const float *)kcache->ptr, eb_tensor_numel(kcache),
-                                (const float *)vcache->ptr, eb_tensor_numel(vcache),
+    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q), kcache->ptr,
+                                eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache),
                                 (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
-                                max_seq));
+                                max_seq, h16));
     size_t nn = eb_tensor_numel(knew) < eb_tensor_numel(vnew) ? eb_tensor_numel(knew)
                                                               : eb_tensor_numel(vnew);
     EB_TRY(step_rows_checked((const float *)knew->ptr, (const float *)vnew->ptr, nn, hkv, hd));
-    return device_decode(rec->dev, (const float *)q->ptr, (const float *)kcache->ptr,
-                         (const float *)vcache->ptr, (float *)kcache->ptr, (float *)vcache->ptr,
-                         (const float *)knew->ptr, (const float *)vnew->ptr, (float *)o->ptr, h,
-                         hkv, pos, hd, scale, window);
+    return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, kcache->ptr,
+                         vcache->ptr, (const float *)knew->ptr, (const float *)vnew->ptr,
+                         (float *)o->ptr, h, hkv, pos, hd, scale, window, h16);
 }
 
 eb_status eb_rmsnorm(eb_recorder *rec, const eb_tensor *x, const eb_tensor *weight,
@@ -796,6 +819,67 @@ eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_nume
     if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
     EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, kc, vc, knew, vnew, o, h, hkv,
                                   pos, hd, scale, workspace, workspace_floats, cus));
+    return eb::ok();
+}
+
+// ---- raw launches over IEEE-half KV caches ------------------------------------------
+
+eb_status eb_launch_kv_write_f16(void *stream, uint16_t *cache, size_t cache_numel,
+                                 const float *src, size_t src_numel, size_t hkv, size_t count,
+                                 size_t hd, size_t max_seq, size_t dst_start) {
+    return kv_write_checked((hipStream_t)stream, cache, cache_numel, src, src_numel, hkv, count,
+                            hd, max_seq, dst_start, true);
+}
+
+eb_status eb_launch_attn_prefill_chunk_f16(void *stream, const float *q, size_t q_numel,
+                                           const uint16_t *kc, size_t kc_numel,
+                                           const uint16_t *vc, size_t vc_numel, float *o,
+                                           size_t o_numel, size_t h, size_t hkv, size_t pos0,
+                                           size_t rows, size_t hd, size_t max_seq, float scale,
+                                           size_t window) {
+    return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window, true);
+}
+
+eb_status eb_launch_attn_decode_f16(void *stream, const float *q, size_t q_numel,
+                                    const uint16_t *kc, size_t kc_numel, const uint16_t *vc,
+                                    size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                    size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                    float scale, size_t window, float *workspace,
+                                    size_t workspace_floats, int cu_count) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq, true));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode_any((hipStream_t)stream, q, kc, vc, nullptr, nullptr, nullptr,
+                                      nullptr, o, h, hkv, pos, hd, scale, workspace,
+                                      workspace_floats, cus, window, true));
+    return eb::ok();
+}
+
+eb_status eb_launch_attn_decode_step_f16(void *stream, const float *q, size_t q_numel,
+                                         const float *knew, const float *vnew, size_t new_numel,
+                                         uint16_t *kc, size_t kc_numel, uint16_t *vc,
+                                         size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                         size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                         float scale, size_t window, float *workspace,
+                                         size_t workspace_floats, int cu_count) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq, true));
+    EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode_any((hipStream_t)stream, q, kc, vc, kc, vc, knew, vnew, o, h,
+                                      hkv, pos, hd, scale, workspace, workspace_floats, cus,
+                                      window, true));
     return eb::ok();
 }
 

@@ -135,6 +135,44 @@ def launch_attn_decode_step(stream: int, q: int, q_numel: int, knew: int, vnew: 
                                            cu_count))
 
 
+# ---- raw launches over IEEE-half caches (no counterpart in the reference) --------------
+
+def launch_kv_write_f16(stream: int, cache: int, cache_numel: int, src: int, src_numel: int,
+                        hkv: int, count: int, hd: int, max_seq: int, dst_start: int) -> None:
+    """kv_write into a uint16 (IEEE half) cache; f32 rows round to nearest even."""
+    check(lib().eb_launch_kv_write_f16(stream, cache, cache_numel, src, src_numel, hkv, count,
+                                       hd, max_seq, dst_start))
+
+
+def launch_attn_prefill_chunk_f16(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
+                                  vc: int, vc_numel: int, o: int, o_numel: int, h: int,
+                                  hkv: int, pos0: int, rows: int, hd: int, max_seq: int,
+                                  scale: float, window: int = 0) -> None:
+    check(lib().eb_launch_attn_prefill_chunk_f16(stream, q, q_numel, kc, kc_numel, vc, vc_numel,
+                                                 o, o_numel, h, hkv, pos0, rows, hd, max_seq,
+                                                 scale, window))
+
+
+def launch_attn_decode_f16(stream: int, q: int, q_numel: int, kc: int, kc_numel: int, vc: int,
+                           vc_numel: int, o: int, o_numel: int, h: int, hkv: int, pos: int,
+                           hd: int, max_seq: int, scale: float, window: int, workspace: int,
+                           workspace_floats: int, cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode_f16(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                          o_numel, h, hkv, pos, hd, max_seq, scale, window,
+                                          workspace, workspace_floats, cu_count))
+
+
+def launch_attn_decode_step_f16(stream: int, q: int, q_numel: int, knew: int, vnew: int,
+                                new_numel: int, kc: int, kc_numel: int, vc: int, vc_numel: int,
+                                o: int, o_numel: int, h: int, hkv: int, pos: int, hd: int,
+                                max_seq: int, scale: float, window: int, workspace: int,
+                                workspace_floats: int, cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode_step_f16(stream, q, q_numel, knew, vnew, new_numel, kc,
+                                               kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos,
+                                               hd, max_seq, scale, window, workspace,
+                                               workspace_floats, cu_count))
+
+
 def launch_rmsnorm(stream: int, x: int, x_numel: int, w: int, w_numel: int, out: int,
                    out_numel: int, rows: int, dim: int, eps: float) -> None:
     check(lib().eb_launch_rmsnorm(stream, x, x_numel, w, w_numel, out, out_numel, rows, dim,

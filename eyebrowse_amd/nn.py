@@ -11,7 +11,7 @@ from dataclasses import dataclass
 from typing import Optional
 
 from ._lib import AttentionDesc, c_size, c_vp, lib
-from .gpu import Device, Recorder, Tensor, check
+from .gpu import DType, Device, Recorder, Tensor, check
 
 
 class _Borrowed(Tensor):
@@ -75,26 +75,31 @@ class KvCache:
     """KvCache (crates/eyebrowse-nn/src/kv_cache.rs:9-50): per-layer K/V tensors
     [max_seq, n_kv_heads, head_dims[l]]."""
 
-    def __init__(self, handle: int, dev: Device, n_layers: int, max_seq: int, n_kv_heads: int):
+    def __init__(self, handle: int, dev: Device, n_layers: int, max_seq: int, n_kv_heads: int,
+                 dtype: DType = DType.F32):
         self._h = c_vp(handle)
         self.dev = dev
         self.max_seq = max_seq
         self.n_kv_heads = n_kv_heads
+        self.dtype = dtype
         self.k = [_Borrowed(lib().eb_kv_cache_k(self._h, l), dev, self) for l in range(n_layers)]
         self.v = [_Borrowed(lib().eb_kv_cache_v(self._h, l), dev, self) for l in range(n_layers)]
 
     @classmethod
     def new(cls, dev: Device, n_layers: int, max_seq: int, n_kv_heads: int,
-            head_dim: int) -> "KvCache":
-        return cls.new_per_layer(dev, [head_dim] * n_layers, max_seq, n_kv_heads)
+            head_dim: int, dtype: DType = DType.F32) -> "KvCache":
+        return cls.new_per_layer(dev, [head_dim] * n_layers, max_seq, n_kv_heads, dtype)
 
     @classmethod
-    def new_per_layer(cls, dev: Device, head_dims, max_seq: int, n_kv_heads: int) -> "KvCache":
+    def new_per_layer(cls, dev: Device, head_dims, max_seq: int, n_kv_heads: int,
+                      dtype: DType = DType.F32) -> "KvCache":
+        """dtype F32 is the reference's cache; F16 (IEEE half, no counterpart in the
+        reference) halves the cache bytes that decode streams."""
         arr = (c_size * max(1, len(head_dims)))(*head_dims)
         out = c_vp()
-        check(lib().eb_kv_cache_new_per_layer(dev.handle, arr, len(head_dims), max_seq,
-                                              n_kv_heads, ctypes.byref(out)))
-        return cls(out.value, dev, len(head_dims), max_seq, n_kv_heads)
+        check(lib().eb_kv_cache_new_per_layer_dtype(dev.handle, arr, len(head_dims), max_seq,
+                                                    n_kv_heads, int(dtype), ctypes.byref(out)))
+        return cls(out.value, dev, len(head_dims), max_seq, n_kv_heads, DType(dtype))
 
     @property
     def handle(self):

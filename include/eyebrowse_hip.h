@@ -219,6 +219,37 @@ eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const flo
                          const float *sin, size_t table_numel, float *out, size_t out_numel,
                          size_t seq, size_t n_heads, size_t head_dim, size_t base_pos);
 
+/* ---- raw launches over IEEE-half (f16) KV caches ----------------------------------
+ * Caches hold uint16_t IEEE half bit patterns, [max_seq, hkv, hd], numel in elements.
+ * kv_write rounds the f32 rows to nearest even; attention loads the halves, converts
+ * them to f32 and computes as the f32 entry points do (the fused step's key pos uses the
+ * rounded new row, the value the cache then holds). Head dims 8..256 (f16 rows of 8
+ * halves per 16-byte load). No counterpart in the reference (its caches are f32). The
+ * handle entry points (eb_kv_write, eb_attn_decode*, eb_attn_prefill_chunk) take f16
+ * caches too, dispatching on the cache tensors' dtype. */
+eb_status eb_launch_kv_write_f16(void *stream, uint16_t *cache, size_t cache_numel,
+                                 const float *src, size_t src_numel, size_t hkv, size_t count,
+                                 size_t hd, size_t max_seq, size_t dst_start);
+eb_status eb_launch_attn_prefill_chunk_f16(void *stream, const float *q, size_t q_numel,
+                                           const uint16_t *kc, size_t kc_numel,
+                                           const uint16_t *vc, size_t vc_numel, float *o,
+                                           size_t o_numel, size_t h, size_t hkv, size_t pos0,
+                                           size_t rows, size_t hd, size_t max_seq, float scale,
+                                           size_t window);
+eb_status eb_launch_attn_decode_f16(void *stream, const float *q, size_t q_numel,
+                                    const uint16_t *kc, size_t kc_numel, const uint16_t *vc,
+                                    size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                    size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                    float scale, size_t window, float *workspace,
+                                    size_t workspace_floats, int cu_count);
+eb_status eb_launch_attn_decode_step_f16(void *stream, const float *q, size_t q_numel,
+                                         const float *knew, const float *vnew, size_t new_numel,
+                                         uint16_t *kc, size_t kc_numel, uint16_t *vc,
+                                         size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                         size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                         float scale, size_t window, float *workspace,
+                                         size_t workspace_floats, int cu_count);
+
 /* ---- nn (crates/eyebrowse-nn/src) -------------------------------------------------- */
 
 /* Rope::build_partial (rope.rs:24-50): host f64 tables -> f32 device tensors
@@ -236,6 +267,13 @@ eb_status eb_rope_apply(const eb_rope_tables *rope, eb_recorder *rec, const eb_t
  * [max_seq, n_kv_heads, head_dims[l]] from Tensor::empty. */
 eb_status eb_kv_cache_new_per_layer(eb_device *dev, const size_t *head_dims, size_t n_layers,
                                     size_t max_seq, size_t n_kv_heads, eb_kv_cache **out);
+/* The same with the caches' element type: EB_F32 (the reference's) or EB_F16 (IEEE half:
+ * half the cache bytes; kv_write rounds to nearest even, attention computes in f32 on
+ * the rounded values). No counterpart in the reference, whose caches are f32
+ * (kv_cache.rs:37,41). */
+eb_status eb_kv_cache_new_per_layer_dtype(eb_device *dev, const size_t *head_dims,
+                                          size_t n_layers, size_t max_seq, size_t n_kv_heads,
+                                          eb_dtype dtype, eb_kv_cache **out);
 void eb_kv_cache_release(eb_kv_cache *kv);
 eb_tensor *eb_kv_cache_k(eb_kv_cache *kv, size_t layer);
 eb_tensor *eb_kv_cache_v(eb_kv_cache *kv, size_t layer);

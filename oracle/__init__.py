@@ -197,3 +197,27 @@ def attn_chunk(q, k, v, h: int, hkv: int, pos0: int, rows: int, hd: int,
     if rc != 0:
         raise ValueError("oracle attn_chunk: bad shape")
     return o.reshape(rows, h, hd)
+
+
+def f16_bits(x) -> np.ndarray:
+    """IEEE 754 binary16 bit patterns of f32 values, rounded to nearest even (overflow to
+    +-inf, gradual underflow to subnormals, NaN stays NaN): numpy's float32 -> float16
+    conversion. The f16 KV cache stores these; the reference's caches are f32 only."""
+    with np.errstate(over="ignore"):
+        return np.ascontiguousarray(_f32(x)).astype(np.float16).view(np.uint16)
+
+
+def f16_values(bits) -> np.ndarray:
+    """f32 values of binary16 bit patterns (exact: every half is an f32)."""
+    return np.ascontiguousarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def kv_write_f16(cache_bits, src, hkv: int, count: int, hd: int, dst_start: int) -> np.ndarray:
+    """kv_write (ops.rs:70-87 row placement) into a binary16 cache: rows dst_start..
+    dst_start+count of cache_bits [uint16] take f16_bits of src. Returns a new array."""
+    cache = np.ascontiguousarray(cache_bits, np.uint16).ravel().copy()
+    src = _f32(src).ravel()
+    n = count * hkv * hd
+    assert src.size >= n and cache.size >= (dst_start + count) * hkv * hd
+    cache[dst_start * hkv * hd:dst_start * hkv * hd + n] = f16_bits(src[:n])
+    return cache

@@ -336,6 +336,66 @@ def test_window_of_one_returns_the_current_value_row():
     assert np.array_equal(got, np.repeat(v, h // hkv, axis=1))
 
 
+# ------------------------------------------------------------------ IEEE-half caches ------
+
+def _half_to_f64(bits):
+    """binary16 decoded from its fields (sign, 5-bit exponent bias 15, 10-bit fraction)."""
+    b = np.asarray(bits, np.int64)
+    sign = np.where(b >> 15, -1.0, 1.0)
+    e = (b >> 10) & 31
+    f = (b & 1023).astype(np.float64)
+    val = np.where(e == 0, f * 2.0 ** -24, (1024 + f) * 2.0 ** (e - 25))
+    val = np.where(e == 31, np.where(f == 0, np.inf, np.nan), val)
+    return sign * val
+
+
+def test_f16_bits_known_answers():
+    """Hand-derived binary16 patterns: ties to even at 1 + 2^-11 and 2^-25, the largest
+    finite half, the overflow threshold 65520, signed zero, the smallest subnormal."""
+    cases = {1.0: 0x3C00, 1 + 2 ** -11: 0x3C00, 1 + 3 * 2 ** -11: 0x3C02, -2.0: 0xC000,
+             65504.0: 0x7BFF, 65519.0: 0x7BFF, 65520.0: 0x7C00, 1e6: 0x7C00, -1e6: 0xFC00,
+             -0.0: 0x8000, 2 ** -24: 0x0001, 2 ** -25: 0x0000, 1.5 * 2 ** -25: 0x0001,
+             2 ** -14: 0x0400, float("inf"): 0x7C00, float("-inf"): 0xFC00, 0.1: 0x2E66}
+    got = oracle.f16_bits(np.array(list(cases), np.float32))
+    assert [int(g) for g in got] == list(cases.values())
+    nan = oracle.f16_bits(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def test_f16_bits_round_to_nearest_even():
+    """Every finite half-range f32 lands on a nearest binary16 (the error is at most half
+    the gap to the neighbouring half; on a tie the fraction is even), decoded from the
+    bit fields independently of numpy's float16."""
+    x = np.concatenate([oracle.randn((20000,), 5) * 3.0,
+                        oracle.randn((5000,), 6) * 1e-5,
+                        oracle.randn((5000,), 7) * 3e4]).astype(np.float32)
+    x = x[np.abs(x) < 65504]
+    bits = oracle.f16_bits(x).astype(np.int64)
+    val = _half_to_f64(bits)
+    assert np.array_equal(bits >> 15, (x < 0).astype(np.int64))   # sign kept, also at -0
+    m = bits & 0x7FFF                                         # magnitude pattern
+    mag = np.abs(val)
+    up = _half_to_f64(m + 1)                                  # next half away from zero
+    dn = np.where(m > 0, _half_to_f64(np.maximum(m - 1, 0)), -_half_to_f64(np.ones_like(m)))
+    ax = np.abs(x.astype(np.float64))
+    assert np.all(ax - mag <= (up - mag) / 2) and np.all(mag - ax <= (mag - dn) / 2)
+    tie = ((ax - mag == (up - mag) / 2) | (mag - ax == (mag - dn) / 2)) & (ax != mag)
+    assert np.all((bits[tie] & 1) == 0)
+    assert np.array_equal(oracle.f16_values(bits.astype(np.uint16)), val.astype(np.float32))
+
+
+def test_kv_write_f16_places_rounded_rows():
+    hkv, hd, count, start, max_seq = 2, 8, 3, 4, 9
+    cache = np.arange(max_seq * hkv * hd, dtype=np.uint16)
+    src = oracle.randn((count, hkv, hd), 8)
+    got = oracle.kv_write_f16(cache, src, hkv, count, hd, start)
+    a, b = start * hkv * hd, (start + count) * hkv * hd
+    assert np.array_equal(got[:a], cache[:a]) and np.array_equal(got[b:], cache[b:])
+    assert np.array_equal(_half_to_f64(got[a:b]),
+                          _half_to_f64(oracle.f16_bits(src.ravel())))
+    assert np.max(np.abs(oracle.f16_values(got[a:b]) - src.ravel())) <= 2.0 ** -11 * 4
+
+
 # ------------------------------------------------------------------ mutation test ----------
 
 @pytest.mark.parametrize("plant", [1, 2, 3, 4])
