@@ -6,7 +6,8 @@ reference's Rust interface:
 
 - ``gpu``: DType, EyebrowseError, Device, Tensor, Recorder (crates/eyebrowse-gpu);
 - ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels),
-  plus chunked / windowed attention, the fused decode step and IEEE-half caches;
+  linear_f16w (the projections around attention), plus chunked / windowed attention, the
+  fused decode step and IEEE-half caches;
 - ``nn``: Rope, KvCache, Attention (crates/eyebrowse-nn).
 """
 from ._lib import LIB_PATH, lib
@@ -15,6 +16,7 @@ from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, O
 from .kernels import (attn_decode, attn_decode_step, attn_decode_step_window,
                       attn_decode_window, attn_decode_workspace_floats, attn_prefill,
                       attn_prefill_chunk, kv_write, launch_attn_decode, launch_attn_decode_f16,
+                      launch_linear_f16w, linear_f16w, linear_f16w_multi, linear_workspace_floats,
                       launch_attn_decode_step, launch_attn_decode_step_f16,
                       launch_attn_decode_window, launch_attn_prefill, launch_attn_prefill_chunk,
                       launch_attn_prefill_chunk_f16, launch_kv_write, launch_kv_write_f16,
@@ -29,6 +31,7 @@ __all__ = [
     "launch_attn_decode", "launch_attn_decode_f16", "launch_attn_decode_step",
     "launch_attn_decode_step_f16", "launch_attn_decode_window", "launch_attn_prefill",
     "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_kv_write",
-    "launch_kv_write_f16", "launch_rmsnorm",
+    "launch_kv_write_f16", "launch_linear_f16w", "linear_f16w", "linear_f16w_multi",
+    "linear_workspace_floats", "launch_rmsnorm",
     "launch_rope", "rmsnorm", "rope", "Attention", "KvCache", "Rope",
 ]

@@ -96,6 +96,13 @@ SIGNATURES = {
     "eb_launch_attn_decode_step": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size,
                                           c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
                                           c_size, c_size, c_float, c_vp, c_size, c_int]),
+    "eb_linear_f16w": (c_st, [c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size]),
+    "eb_linear_f16w_multi": (c_st, [c_vp, c_vp, c_size, ctypes.POINTER(c_vp),
+                                    ctypes.POINTER(c_vp), ctypes.POINTER(c_size), c_size,
+                                    c_size]),
+    "eb_linear_workspace_floats": (c_size, [c_size, c_size]),
+    "eb_launch_linear_f16w": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
+                                     c_size, c_size, c_vp, c_size]),
     "eb_launch_kv_write_f16": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
                                       c_size, c_size]),
     "eb_launch_attn_prefill_chunk_f16": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,

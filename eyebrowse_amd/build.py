@@ -41,6 +41,7 @@ SOURCES = [
     "eb_elementwise.hip",
     "eb_decode.hip",
     "eb_prefill.hip",
+    "eb_linear.hip",
 ]
 
 

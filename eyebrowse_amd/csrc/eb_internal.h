@@ -83,6 +83,16 @@ eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const ui
                                         const uint16_t *vc, float *o, size_t h, size_t hkv,
                                         size_t pos0, size_t rows, size_t hd, float scale,
                                         size_t window);
+// linear_f16w: y[i][m, o] = sum_k x[m, k] * w[i][o, k] for nseg (1..kLinearMaxSegs)
+// weight/output pairs sharing x; w IEEE half [out_f[i], in_f]. m <= kLinearGemvRows runs
+// the weight-streaming kernel; more rows run the split-f16 matrix-core GEMM, which needs
+// linear_workspace_floats(m, in_f) floats of workspace (row exponents).
+constexpr int kLinearMaxSegs = 3;
+constexpr size_t kLinearGemvRows = 8;
+size_t linear_workspace_floats(size_t m, size_t in_f);
+eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_t *const *w,
+                                   float *const *y, const size_t *out_f, int nseg, size_t m,
+                                   size_t in_f, float *ws, size_t ws_floats);
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
                          size_t rows, size_t dim, float eps);
 eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,

@@ -595,6 +595,73 @@ static eb_status device_decode(eb_device *dev, const float *q, const void *kc, c
     return eb::ok();
 }
 
+// A packed-f16 weight: EB_U32 words holding two halves each, low half first (the
+// reference's from_f16_packed, crates/eyebrowse-gpu/src/tensor.rs:108-116), or EB_F16
+// elements. *halves = how many halves it holds.
+static eb_status tensor_weight(const eb_tensor *t, const char *name, eb_device *dev,
+                               size_t *halves) {
+    if (!t) return fail(EB_SHAPE_MISMATCH, "%s is null", name);
+    if (t->dev != dev) return fail(EB_OTHER, "%s lives on another device", name);
+    if (t->dtype == EB_U32)
+        *halves = 2 * eb_tensor_numel(t);
+    else if (t->dtype == EB_F16)
+        *halves = eb_tensor_numel(t);
+    else
+        return fail(EB_SHAPE_MISMATCH, "%s must be packed f16 (u32 words) or f16", name);
+    return EB_OK;
+}
+
+// linear_f16w over nseg weight/output pairs that share x.
+static eb_status linear_checked(hipStream_t st, const float *x, size_t xn,
+                                const uint16_t *const *w, const size_t *w_halves,
+                                float *const *y, const size_t *yn, const size_t *out_f, int nseg,
+                                size_t m, size_t in_f, float *ws, size_t wsn) {
+    if (nseg < 1 || nseg > eb::kLinearMaxSegs)
+        return fail(EB_OTHER, "linear_f16w: 1 to %d weights per launch", eb::kLinearMaxSegs);
+    EB_TRY(eb::check_numel(xn, m * in_f, "a"));
+    for (int i = 0; i < nseg; ++i) {
+        EB_TRY(eb::check_numel(w_halves[i], out_f[i] * in_f, "w"));
+        EB_TRY(eb::check_numel(yn[i], m * out_f[i], "c"));
+    }
+    if (m == 0) return eb::ok();
+    if (in_f > 0) EB_TRY(eb::check_ptr(x, "a"));
+    for (int i = 0; i < nseg; ++i) {
+        if (out_f[i] == 0) continue;
+        if (in_f > 0) EB_TRY(eb::check_ptr(w[i], "w"));
+        EB_TRY(eb::check_ptr(y[i], "c"));
+    }
+    const size_t need = eb::linear_workspace_floats(m, in_f);
+    if (wsn < need)
+        return fail(EB_SHAPE_MISMATCH, "linear_f16w: workspace holds %zu floats, needs %zu", wsn,
+                    need);
+    if (need > 0) EB_TRY(eb::check_ptr(ws, "workspace"));
+    EB_TRY(eb::launch_linear_f16w_multi(st, x, w, y, out_f, nseg, m, in_f, ws, wsn));
+    return eb::ok();
+}
+
+static eb_status device_linear(eb_device *dev, const eb_tensor *a,
+                               const eb_tensor *const *w, eb_tensor *const *c,
+                               const size_t *out_f, int nseg, size_t m, size_t in_f) {
+    EB_TRY(tensor_f32(a, "a", dev));
+    if (nseg < 1 || nseg > eb::kLinearMaxSegs || !w || !c || !out_f)
+        return fail(EB_OTHER, "linear_f16w: 1 to %d weights per launch", eb::kLinearMaxSegs);
+    const uint16_t *wp[eb::kLinearMaxSegs];
+    float *yp[eb::kLinearMaxSegs];
+    size_t wh[eb::kLinearMaxSegs], yn[eb::kLinearMaxSegs];
+    for (int i = 0; i < nseg; ++i) {
+        EB_TRY(tensor_weight(w[i], "w", dev, &wh[i]));
+        EB_TRY(tensor_f32(c[i], "c", dev));
+        wp[i] = static_cast<const uint16_t *>(w[i]->ptr);
+        yp[i] = static_cast<float *>(c[i]->ptr);
+        yn[i] = eb_tensor_numel(c[i]);
+    }
+    const size_t wsn = eb::linear_workspace_floats(m, in_f);
+    float *ws = nullptr;
+    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
+    return linear_checked(dev->stream, static_cast<const float *>(a->ptr), eb_tensor_numel(a),
+                          wp, wh, yp, yn, out_f, nseg, m, in_f, ws, wsn);
+}
+
 // Both caches of one layer share a dtype.
 static eb_status cache_pair(const eb_tensor *kc, const eb_tensor *vc, eb_device *dev,
                             bool *h16) {
@@ -895,6 +962,32 @@ eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const flo
                          size_t seq, size_t n_heads, size_t head_dim, size_t base_pos) {
     return rope_checked((hipStream_t)stream, x, x_numel, cos, sin, table_numel, out, out_numel,
                         seq, n_heads, head_dim, base_pos);
+}
+
+eb_status eb_linear_f16w(eb_recorder *rec, const eb_tensor *a, const eb_tensor *w, eb_tensor *c,
+                         size_t m, size_t in_f, size_t out_f) {
+    EB_TRY(rec_ready(rec));
+    return device_linear(rec->dev, a, &w, &c, &out_f, 1, m, in_f);
+}
+
+eb_status eb_linear_f16w_multi(eb_recorder *rec, const eb_tensor *a, size_t n,
+                               const eb_tensor *const *w, eb_tensor *const *c,
+                               const size_t *out_f, size_t m, size_t in_f) {
+    EB_TRY(rec_ready(rec));
+    if (n < 1 || n > (size_t)eb::kLinearMaxSegs)
+        return fail(EB_OTHER, "linear_f16w: 1 to %d weights per launch", eb::kLinearMaxSegs);
+    return device_linear(rec->dev, a, w, c, out_f, (int)n, m, in_f);
+}
+
+size_t eb_linear_workspace_floats(size_t m, size_t in_f) {
+    return eb::linear_workspace_floats(m, in_f);
+}
+
+eb_status eb_launch_linear_f16w(void *stream, const float *a, size_t a_numel, const uint16_t *w,
+                                size_t w_halves, float *c, size_t c_numel, size_t m, size_t in_f,
+                                size_t out_f, float *workspace, size_t workspace_floats) {
+    return linear_checked((hipStream_t)stream, a, a_numel, &w, &w_halves, &c, &c_numel, &out_f,
+                          1, m, in_f, workspace, workspace_floats);
 }
 
 }  // extern "C"

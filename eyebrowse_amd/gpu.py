@@ -141,6 +141,20 @@ class Tensor:
                                        ctypes.byref(out)))
         return cls(out.value, dev)
 
+    @classmethod
+    def from_f16_packed(cls, dev: Device, logical_shape, data) -> "Tensor":
+        """Tensor::from_f16_packed (crates/eyebrowse-gpu/src/tensor.rs:108-116): f32 data
+        rounded to IEEE half (nearest even) and packed two per u32 word, low half first,
+        odd tail zero-padded; a U32 tensor of ceil(n/2) words."""
+        a = np.ascontiguousarray(np.asarray(data, dtype=np.float32)).ravel()
+        assert a.size == int(np.prod(logical_shape)), "from_f16_packed: data len != shape numel"
+        with np.errstate(over="ignore"):
+            h = a.astype(np.float16).view(np.uint16)
+        if h.size % 2:
+            h = np.concatenate([h, np.zeros(1, np.uint16)])
+        words = h[0::2].astype(np.uint32) | (h[1::2].astype(np.uint32) << 16)
+        return cls.from_u32(dev, (words.size,), words)
+
     @property
     def handle(self):
         return self._h

@@ -4,7 +4,7 @@ caller-owned device memory.
 """
 from __future__ import annotations
 
-from ._lib import lib
+from ._lib import c_size, c_vp, lib
 from .gpu import Recorder, Tensor, check
 
 
@@ -78,7 +78,37 @@ def rope(rec: Recorder, x: Tensor, cos: Tensor, sin: Tensor, out: Tensor, seq: i
                         head_dim, base_pos))
 
 
+def linear_f16w(rec: Recorder, a: Tensor, w: Tensor, c: Tensor, m: int, in_f: int,
+                out_f: int) -> None:
+    """linear_f16w (crates/eyebrowse-kernels/src/matmul.rs:120-140): c = a . w^T, w the
+    packed-f16 [out_f, in_f] weight (a U32 tensor of packed words, or an F16 tensor)."""
+    check(lib().eb_linear_f16w(rec.handle, a.handle, w.handle, c.handle, m, in_f, out_f))
+
+
+def linear_f16w_multi(rec: Recorder, a: Tensor, ws, cs, out_fs, m: int, in_f: int) -> None:
+    """Up to three projections of the same a in one launch (no counterpart in the
+    reference): cs[i] = a . ws[i]^T."""
+    n = len(ws)
+    assert len(cs) == n and len(out_fs) == n
+    warr = (c_vp * max(n, 1))(*[t.handle for t in ws])
+    carr = (c_vp * max(n, 1))(*[t.handle for t in cs])
+    oarr = (c_size * max(n, 1))(*out_fs)
+    check(lib().eb_linear_f16w_multi(rec.handle, a.handle, n, warr, carr, oarr, m, in_f))
+
+
+def linear_workspace_floats(m: int, in_f: int) -> int:
+    return int(lib().eb_linear_workspace_floats(m, in_f))
+
+
 # ---- raw launches on caller memory (stream and pointers as ints) ------------------------
+
+def launch_linear_f16w(stream: int, a: int, a_numel: int, w: int, w_halves: int, c: int,
+                       c_numel: int, m: int, in_f: int, out_f: int, workspace: int,
+                       workspace_floats: int) -> None:
+    check(lib().eb_launch_linear_f16w(stream, a, a_numel, w, w_halves, c, c_numel, m, in_f,
+                                      out_f, workspace, workspace_floats))
+
+
 
 def launch_kv_write(stream: int, cache: int, cache_numel: int, src: int, src_numel: int,
                     hkv: int, count: int, hd: int, max_seq: int, dst_start: int) -> None:

@@ -219,6 +219,30 @@ eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const flo
                          const float *sin, size_t table_numel, float *out, size_t out_numel,
                          size_t seq, size_t n_heads, size_t head_dim, size_t base_pos);
 
+/* ---- projections: linear_f16w (crates/eyebrowse-kernels/src/matmul.rs:84-144) -------
+ * c [m, out_f] = a [m, in_f] . w^T, a and c f32, w the packed-f16 weight of logical shape
+ * [out_f, in_f] (HF Linear layout, crates/eyebrowse-nn/src/linear.rs:5-23): an EB_U32
+ * tensor of ceil(out_f*in_f/2) words, two halves per word, low half first (the
+ * reference's Tensor::from_f16_packed, crates/eyebrowse-gpu/src/tensor.rs:108-116), or
+ * an EB_F16 tensor of out_f*in_f elements. Accumulation is f32 (m <= 8: f32 multiply-adds
+ * on the halves; more rows: matrix cores on an exact f16 split of a, to about f32
+ * accuracy; the two differ from the reference only in summation order). */
+eb_status eb_linear_f16w(eb_recorder *rec, const eb_tensor *a, const eb_tensor *w, eb_tensor *c,
+                         size_t m, size_t in_f, size_t out_f);
+/* n (1..3) projections of the same a in one launch, e.g. a layer's q/k/v
+ * (crates/eyebrowse-nn/src/attention.rs:58-60,129-131): c[i] = a . w[i]^T, c[i]
+ * [m, out_f[i]]. No counterpart in the reference (three linear_f16w calls there). */
+eb_status eb_linear_f16w_multi(eb_recorder *rec, const eb_tensor *a, size_t n,
+                               const eb_tensor *const *w, eb_tensor *const *c,
+                               const size_t *out_f, size_t m, size_t in_f);
+/* Raw form: w holds w_halves IEEE halves (the packed words read as uint16_t). Rows m > 8
+ * need eb_linear_workspace_floats(m, in_f) floats of workspace (row exponents; no
+ * initialisation needed). */
+size_t eb_linear_workspace_floats(size_t m, size_t in_f);
+eb_status eb_launch_linear_f16w(void *stream, const float *a, size_t a_numel, const uint16_t *w,
+                                size_t w_halves, float *c, size_t c_numel, size_t m, size_t in_f,
+                                size_t out_f, float *workspace, size_t workspace_floats);
+
 /* ---- raw launches over IEEE-half (f16) KV caches ----------------------------------
  * Caches hold uint16_t IEEE half bit patterns, [max_seq, hkv, hd], numel in elements.
  * kv_write rounds the f32 rows to nearest even; attention loads the halves, converts

@@ -61,6 +61,13 @@ def _load():
     lib.ebo_attn_decode.restype = ctypes.c_int
     lib.ebo_attn_decode.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz, _sz,
                                     ctypes.c_float, ctypes.c_int]
+    lib.ebo_linear_f16w.restype = None
+    lib.ebo_linear_f16w.argtypes = [_f32p, ctypes.POINTER(ctypes.c_uint16), _f32p, _sz, _sz, _sz,
+                                    ctypes.c_int]
+    lib.ebo_f16_to_f32.restype = ctypes.c_float
+    lib.ebo_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.ebo_argmax.restype = ctypes.c_uint32
+    lib.ebo_argmax.argtypes = [_f32p, _sz]
     lib.ebo_default_scale.restype = ctypes.c_float
     lib.ebo_default_scale.argtypes = [_sz]
     lib.ebo_max_threads.restype = ctypes.c_int
@@ -221,3 +228,31 @@ def kv_write_f16(cache_bits, src, hkv: int, count: int, hd: int, dst_start: int)
     assert src.size >= n and cache.size >= (dst_start + count) * hkv * hd
     cache[dst_start * hkv * hd:dst_start * hkv * hd + n] = f16_bits(src[:n])
     return cache
+
+
+def linear_f16w(x, w_bits, m: int, in_f: int, out_f: int, threads: int = 1) -> np.ndarray:
+    """linear_f16w (testutil.rs:68-80 on f16-rounded weights): y [m, out_f] = x [m, in_f]
+    times w^T, w the f16 bit patterns of [out_f, in_f] (flat)."""
+    x = _f32(x).ravel()
+    w = np.ascontiguousarray(w_bits, np.uint16).ravel()
+    assert x.size == m * in_f and w.size >= out_f * in_f
+    y = np.empty(m * out_f, np.float32)
+    _load().ebo_linear_f16w(_p(x), w.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), _p(y), m,
+                            in_f, out_f, threads)
+    return y.reshape(m, out_f)
+
+
+def pack_f16(x) -> np.ndarray:
+    """The reference's packed-u32 weight format (crates/eyebrowse-gpu/src/tensor.rs:7-23):
+    u32[w] = bits(f16(x[2w])) | bits(f16(x[2w+1])) << 16, odd tail zero-padded."""
+    b = f16_bits(np.ravel(x))
+    if b.size % 2:
+        b = np.concatenate([b, np.zeros(1, np.uint16)])
+    return b[0::2].astype(np.uint32) | (b[1::2].astype(np.uint32) << 16)
+
+
+def argmax(x) -> int:
+    """argmax (sampling.rs:6-38): first index of the maximum; NaN and values <= -3e38
+    never win."""
+    x = _f32(x).ravel()
+    return int(_load().ebo_argmax(_p(x), x.size))

@@ -301,6 +301,57 @@ int ebo_attn_chunk(const float *q, const float *k, const float *v, float *o, siz
     return 0;
 }
 
+/* IEEE binary16 bit pattern -> f32 (exact), from its fields: sign, 5-bit exponent with
+ * bias 15, 10-bit fraction; exponent 0 is subnormal (fraction * 2^-24), 31 is inf/NaN. */
+float ebo_f16_to_f32(uint16_t h) {
+    const int sign = h >> 15, e = (h >> 10) & 31, f = h & 1023;
+    float v;
+    if (e == 0)
+        v = ldexpf((float)f, -24);
+    else if (e == 31)
+        v = f ? NAN : INFINITY;
+    else
+        v = ldexpf((float)(1024 + f), e - 25);
+    return sign ? -v : v;
+}
+
+/* linear_f16w's CPU reference (crates/eyebrowse-kernels/src/testutil.rs:68-80, the
+ * weight rounded to f16 as the kernel reads it, matmul.rs:246-247,266-267):
+ * y[i, o] = sum_k x[i, k] * w[o, k], f32 accumulation with k ascending. w holds the
+ * f16 bit patterns of the logical [out_f, in_f] weight in flat order: the reference's
+ * packed-u32 layout (tensor.rs:7-23, low half first) read as little-endian u16. */
+void ebo_linear_f16w(const float *x, const uint16_t *w, float *y, size_t m, size_t in_f,
+                     size_t out_f, int threads) {
+    if (threads < 1) threads = 1;
+#pragma omp parallel for num_threads(threads) schedule(static) collapse(2)
+    for (size_t i = 0; i < m; ++i)
+        for (size_t o = 0; o < out_f; ++o) {
+            float acc = 0.0f;
+            for (size_t k = 0; k < in_f; ++k) {
+#if EBO_PLANT == 5 /* planted mistake: weight read transposed ([in, out]) */
+                acc += x[i * in_f + k] * ebo_f16_to_f32(w[k * out_f + o]);
+#else
+                acc += x[i * in_f + k] * ebo_f16_to_f32(w[o * in_f + k]);
+#endif
+            }
+            y[i * out_f + o] = acc;
+        }
+}
+
+/* argmax's semantics (crates/eyebrowse-kernels/src/sampling.rs:6-38): the index of the
+ * largest value, the lowest such index on ties; values not above -3e38 (and NaN) never
+ * win, so an all -inf/NaN vector gives 0. */
+uint32_t ebo_argmax(const float *x, size_t n) {
+    float bv = -3.0e38f;
+    uint32_t bi = 0;
+    for (size_t i = 0; i < n; ++i)
+        if (x[i] > bv) {
+            bv = x[i];
+            bi = (uint32_t)i;
+        }
+    return bi;
+}
+
 /* The reference's hard-coded scale: 1.0 / (hd as f32).sqrt()
  * (crates/eyebrowse-kernels/src/testutil.rs:140,188). */
 float ebo_default_scale(size_t hd) { return 1.0f / sqrtf((float)hd); }

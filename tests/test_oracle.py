@@ -396,7 +396,104 @@ def test_kv_write_f16_places_rounded_rows():
     assert np.max(np.abs(oracle.f16_values(got[a:b]) - src.ravel())) <= 2.0 ** -11 * 4
 
 
+# ------------------------------------------------------------------ linear_f16w / argmax --
+
+def test_f16_decode_matches_numpy_for_every_pattern():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    lib = oracle._load()
+    got = np.array([lib.ebo_f16_to_f32(int(b)) for b in bits], np.float32)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_pack_f16_reference_layout():
+    """tensor.rs:7-23: low half first, odd tail zero-padded."""
+    assert [int(v) for v in oracle.pack_f16(np.array([1.0, -2.0, 0.5], np.float32))] == \
+        [0xC0003C00, 0x00003800]
+
+
+def test_linear_reference_ramp_case():
+    """matmul.rs:255-272: m=5, in=33, out=7 ramps; the reference asserts rel-L2 < 2e-3
+    against its CPU linear on f16-rounded weights. Here against float64."""
+    m, in_f, out_f = 5, 33, 7
+    x = (np.arange(m * in_f) * 0.01 - 0.2).astype(np.float32).reshape(m, in_f)
+    w = (np.arange(out_f * in_f) * 0.005 - 0.3).astype(np.float32).reshape(out_f, in_f)
+    wb = oracle.f16_bits(w)
+    got = oracle.linear_f16w(x, wb, m, in_f, out_f)
+    want = x.astype(np.float64) @ oracle.f16_values(wb).reshape(out_f, in_f).astype(np.float64).T
+    assert rel_l2_f64(got, want) < 1e-6
+
+
+@pytest.mark.parametrize("m,in_f,out_f", [(1, 1024, 64), (7, 96, 130), (33, 256, 48),
+                                          (2, 4096, 16)])
+def test_linear_matches_f64(m, in_f, out_f):
+    x = oracle.randn((m, in_f), 1)
+    wb = oracle.f16_bits(oracle.randn((out_f, in_f), 2) * 0.05)
+    got = oracle.linear_f16w(x, wb, m, in_f, out_f, threads=8)
+    w64 = oracle.f16_values(wb).reshape(out_f, in_f).astype(np.float64)
+    want = x.astype(np.float64) @ w64.T
+    # sequential f32 accumulation: error within in_f unit roundoffs of the row's scale
+    bound = in_f * 2.0 ** -24
+    assert rel_l2_f64(got, want) < bound
+    assert np.max(np.abs(got - want)) <= bound * np.max(np.abs(want))
+
+
+def test_linear_identity_and_single_column_exact():
+    """w = I gives x back exactly; a one-hot row picks one column of x exactly."""
+    n = 40
+    x = oracle.randn((3, n), 3)
+    y = oracle.linear_f16w(x, oracle.f16_bits(np.eye(n, dtype=np.float32)), 3, n, n)
+    assert np.array_equal(y, x)
+    w = np.zeros((2, n), np.float32)
+    w[0, 5] = 1.0
+    w[1, 7] = -2.0
+    y = oracle.linear_f16w(x, oracle.f16_bits(w), 3, n, 2)
+    assert np.array_equal(y[:, 0], x[:, 5]) and np.array_equal(y[:, 1], -2 * x[:, 7])
+
+
+def test_argmax_reference_case_and_ties():
+    """sampling.rs:62-80 (vocab 1000, sin ramp, unique max at 731); ties go to the first
+    index; NaN never wins; an all -inf vector gives 0."""
+    v = np.sin(np.arange(1000, dtype=np.float32) * np.float32(0.001)).astype(np.float32)
+    v[731] = 5.0
+    assert oracle.argmax(v) == 731
+    assert oracle.argmax(np.array([1, 7, 3, 7], np.float32)) == 1
+    assert oracle.argmax(np.array([np.nan, 2, np.nan, 1], np.float32)) == 1
+    assert oracle.argmax(np.full(5, -np.inf, np.float32)) == 0
+    r = oracle.randn((100000,), 4)
+    assert oracle.argmax(r) == int(np.argmax(r))
+
+
 # ------------------------------------------------------------------ mutation test ----------
+
+def _planted(plant, td):
+    src = os.path.join(os.path.dirname(oracle.__file__), "oracle.c")
+    so = os.path.join(td, f"planted{plant}.so")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fPIC", "-shared", "-fopenmp",
+                    f"-DEBO_PLANT={plant}", "-o", so, src, "-lm"], check=True)
+    return ctypes.CDLL(so)
+
+
+def test_linear_check_rejects_transposed_weight():
+    """EBO_PLANT=5 reads the weight as [in, out]; the float64 check above rejects it."""
+    with tempfile.TemporaryDirectory() as td:
+        lib = _planted(5, td)
+        f32p = ctypes.POINTER(ctypes.c_float)
+        lib.ebo_linear_f16w.argtypes = [f32p, ctypes.POINTER(ctypes.c_uint16), f32p,
+                                        ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                        ctypes.c_int]
+        m, in_f, out_f = 3, 24, 24
+        x = oracle.randn((m, in_f), 1)
+        wb = oracle.f16_bits(oracle.randn((out_f, in_f), 2))
+        y = np.empty((m, out_f), np.float32)
+        lib.ebo_linear_f16w(x.ctypes.data_as(f32p),
+                            wb.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)),
+                            y.ctypes.data_as(f32p), m, in_f, out_f, 1)
+        want = x.astype(np.float64) @ oracle.f16_values(wb).reshape(out_f, in_f).T
+        assert rel_l2_f64(y, want) > 1e-3
+
 
 @pytest.mark.parametrize("plant", [1, 2, 3, 4])
 def test_checks_reject_planted_oracle_mistakes(plant):
