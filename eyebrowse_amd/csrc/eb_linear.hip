@@ -191,7 +191,10 @@ __global__ __launch_bounds__(kThreads) void linear_row_scale_kernel(const float 
 
 constexpr int kBM = 128;  // x rows per workgroup tile
 constexpr int kBN = 128;  // output features per workgroup tile
-constexpr int kBK = 32;   // contraction per LDS stage
+#ifndef EB_LINEAR_BK
+#define EB_LINEAR_BK 32
+#endif
+constexpr int kBK = EB_LINEAR_BK;  // contraction per LDS stage
 constexpr int kLdsRow = kBK + 8;  // halves per LDS row (16-byte pad against bank conflicts)
 constexpr int kTileHalves = kBM * kLdsRow;
 constexpr size_t kGemmLdsBytes = 2 /*buffers*/ * 3 /*hi, lo, w*/ * kTileHalves * 2;
@@ -219,24 +222,26 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
     const int n0 = (nu - s.first[sg]) * kBN;
     const _Float16 *w = s.w[sg];
 
-    // Staging assignment: x tile 128 x 32 f32 = 1024 f32x4, 4 per thread; w tile
-    // 128 x 32 halves = 512 f16x8, 2 per thread.
-    f32x4 rx[4];
-    f16x8 rw[2];
+    // Staging assignment: x tile 128 x kBK f32 (NX f32x4 per thread); w tile 128 x kBK
+    // halves (NW f16x8 per thread).
+    constexpr int X4 = kBK / 4, W8 = kBK / 8;  // vectors per tile row
+    constexpr int NX = kBM * X4 / kThreads, NW = kBN * W8 / kThreads;
+    f32x4 rx[NX];
+    f16x8 rw[NW];
     __shared__ int s_ex[kBM];  // row exponents of the tile (read by the epilogue)
     if (tid < kBM) s_ex[tid] = (int)ex[min(m0 + tid, M - 1)];
-    int rs[4];  // -e of the row each staged f32x4 belongs to
+    int rs[NX];  // -e of the row each staged f32x4 belongs to
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NX; ++j) {
         const int idx = tid + j * kThreads;
-        const int row = min(m0 + idx / 8, M - 1);
+        const int row = min(m0 + idx / X4, M - 1);
         rs[j] = -(int)ex[row];
     }
     auto load_stage = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NX; ++j) {
             const int idx = tid + j * kThreads;
-            const int r = idx / 8, c4 = idx % 8;
+            const int r = idx / X4, c4 = idx % X4;
             const int row = m0 + r, k = k0 + c4 * 4;
             const bool ok = row < M && k < K;
             const f32x4 v = *reinterpret_cast<const f32x4 *>(
@@ -244,9 +249,9 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
             rx[j] = ok ? v : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NW; ++j) {
             const int idx = tid + j * kThreads;
-            const int r = idx / 4, c8 = idx % 4;
+            const int r = idx / W8, c8 = idx % W8;
             const int o = n0 + r, k = k0 + c8 * 8;
             const bool ok = o < N && k < K;
             const f16x8 v = *reinterpret_cast<const f16x8 *>(
@@ -259,9 +264,9 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
         _Float16 *lo = hi + kTileHalves;
         _Float16 *wt = lo + kTileHalves;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NX; ++j) {
             const int idx = tid + j * kThreads;
-            const int r = idx / 8, c4 = idx % 8;
+            const int r = idx / X4, c4 = idx % X4;
             const f32x4 v = {ldexpf(rx[j].x, rs[j]), ldexpf(rx[j].y, rs[j]),
                              ldexpf(rx[j].z, rs[j]), ldexpf(rx[j].w, rs[j])};
             const f16x4 h = __builtin_convertvector(v, f16x4);
@@ -270,9 +275,9 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
             *reinterpret_cast<f16x4 *>(lo + r * kLdsRow + c4 * 4) = l;
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NW; ++j) {
             const int idx = tid + j * kThreads;
-            const int r = idx / 4, c8 = idx % 4;
+            const int r = idx / W8, c8 = idx % W8;
             *reinterpret_cast<f16x8 *>(wt + r * kLdsRow + c8 * 8) = rw[j];
         }
     };
