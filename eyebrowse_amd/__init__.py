@@ -8,7 +8,7 @@ reference's Rust interface:
 - ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels),
   linear_f16w (the projections around attention), plus chunked / windowed attention, the
   fused decode step and IEEE-half caches;
-- ``nn``: Rope, KvCache, Attention (crates/eyebrowse-nn).
+- ``nn``: Linear, Rope, KvCache, Attention (crates/eyebrowse-nn).
 """
 from ._lib import LIB_PATH, lib
 from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, OutOfMemory,
@@ -21,7 +21,7 @@ from .kernels import (attn_decode, attn_decode_step, attn_decode_step_window,
                       launch_attn_decode_window, launch_attn_prefill, launch_attn_prefill_chunk,
                       launch_attn_prefill_chunk_f16, launch_kv_write, launch_kv_write_f16,
                       launch_rmsnorm, launch_rope, rmsnorm, rope)
-from .nn import Attention, KvCache, Rope
+from .nn import Attention, KvCache, Linear, Rope
 
 __all__ = [
     "LIB_PATH", "lib", "DType", "Device", "DeviceUnavailable", "EyebrowseError", "LoadError",
@@ -33,5 +33,5 @@ __all__ = [
     "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_kv_write",
     "launch_kv_write_f16", "launch_linear_f16w", "linear_f16w", "linear_f16w_multi",
     "linear_workspace_floats", "launch_rmsnorm",
-    "launch_rope", "rmsnorm", "rope", "Attention", "KvCache", "Rope",
+    "launch_rope", "rmsnorm", "rope", "Attention", "KvCache", "Linear", "Rope",
 ]

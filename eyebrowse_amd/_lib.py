@@ -31,6 +31,11 @@ class AttentionDesc(ctypes.Structure):
         ("k_norm", c_vp),
         ("v_norm", c_vp),
         ("window", c_size),
+        ("q_proj", c_vp),
+        ("k_proj", c_vp),
+        ("v_proj", c_vp),
+        ("o_proj", c_vp),
+        ("hidden", c_size),
     ]
 
 
@@ -135,6 +140,8 @@ SIGNATURES = {
     "eb_kv_cache_max_seq": (c_size, [c_vp]),
     "eb_attention_new": (c_st, [ctypes.POINTER(AttentionDesc), ctypes.POINTER(c_vp)]),
     "eb_attention_release": (None, [c_vp]),
+    "eb_attention_forward": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size,
+                                    ctypes.POINTER(c_vp)]),
     "eb_attention_forward_qkv": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size,
                                         c_size, c_size, ctypes.POINTER(c_vp)]),
 }

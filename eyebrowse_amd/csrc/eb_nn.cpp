@@ -166,6 +166,14 @@ eb_tensor *eb_kv_cache_v(eb_kv_cache *kv, size_t layer) {
 }
 size_t eb_kv_cache_max_seq(const eb_kv_cache *kv) { return kv ? kv->max_seq : 0; }
 
+// A packed-f16 weight of n halves: EB_U32 words (two halves each, odd tail padded) or
+// EB_F16 elements.
+static bool weight_holds(const eb_tensor *w, size_t n) {
+    if (eb_tensor_dtype(w) == EB_U32) return eb_tensor_numel(w) == (n + 1) / 2;
+    if (eb_tensor_dtype(w) == EB_F16) return eb_tensor_numel(w) == n;
+    return false;
+}
+
 eb_status eb_attention_new(const eb_attention_desc *desc, eb_attention **out) {
     if (!desc || !out) return fail(EB_OTHER, "attention_new: null argument");
     *out = nullptr;
@@ -177,6 +185,22 @@ eb_status eb_attention_new(const eb_attention_desc *desc, eb_attention **out) {
     for (const eb_tensor *n : norms)
         if (n && (eb_tensor_dtype(n) != EB_F32 || eb_tensor_numel(n) != desc->head_dim))
             return fail(EB_SHAPE_MISMATCH, "attention: norm weights must be [head_dim] f32");
+    const eb_tensor *proj[4] = {desc->q_proj, desc->k_proj, desc->v_proj, desc->o_proj};
+    const size_t qd = desc->n_heads * desc->head_dim, kd = desc->n_kv_heads * desc->head_dim;
+    const size_t outs[4] = {qd, kd, kd, desc->hidden};
+    const size_t ins[4] = {desc->hidden, desc->hidden, desc->hidden, qd};
+    const int given = (proj[0] != nullptr) + (proj[1] != nullptr) + (proj[2] != nullptr) +
+                      (proj[3] != nullptr);
+    if (given != 0 && given != 4)
+        return fail(EB_SHAPE_MISMATCH, "attention: give all four projections or none");
+    if (given == 4) {
+        if (desc->hidden == 0) return fail(EB_SHAPE_MISMATCH, "attention: hidden must be > 0");
+        for (int i = 0; i < 4; ++i)
+            if (!weight_holds(proj[i], outs[i] * ins[i]))
+                return fail(EB_SHAPE_MISMATCH,
+                            "attention: projection %d must be packed f16 [%zu, %zu]", i, outs[i],
+                            ins[i]);
+    }
     auto a = std::make_unique<eb_attention>();
     a->d = *desc;
     *out = a.release();
@@ -270,5 +294,44 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
         }
     }
     *out = o.release();
+    return eb::ok();
+}
+
+// Attention::forward with the projections (attention.rs:30-45; prefill :49-117, decode
+// :120-185): q/k/v = x . W^T in one launch, the post-projection part above, then o_proj.
+extern "C" eb_status eb_attention_forward(const eb_attention *attn, eb_recorder *rec,
+                                          const eb_tensor *x, const eb_rope_tables *rope,
+                                          eb_kv_cache *kv, size_t layer, size_t rows,
+                                          size_t base_pos, eb_tensor **out) {
+    if (!attn || !rec || !x || !out) return fail(EB_OTHER, "attention_forward: null argument");
+    *out = nullptr;
+    const eb_attention_desc &d = attn->d;
+    if (!d.q_proj) return fail(EB_SHAPE_MISMATCH, "attention_forward: no projection weights");
+    const size_t qd = d.n_heads * d.head_dim, kd = d.n_kv_heads * d.head_dim;
+    if (eb_tensor_dtype(x) != EB_F32 || eb_tensor_numel(x) != rows * d.hidden)
+        return fail(EB_SHAPE_MISMATCH, "attention_forward: x is not [rows, hidden] f32");
+    eb_device *dev = tensor_device_of(x);
+    const size_t qs[2] = {rows, qd}, ks[2] = {rows, kd};
+    eb_tensor *qt = nullptr, *kt = nullptr, *vt = nullptr;
+    EB_TRY(eb_tensor_empty(dev, qs, 2, EB_F32, &qt));
+    Owned q(qt);
+    EB_TRY(eb_tensor_empty(dev, ks, 2, EB_F32, &kt));
+    Owned k(kt);
+    EB_TRY(eb_tensor_empty(dev, ks, 2, EB_F32, &vt));
+    Owned v(vt);
+    const eb_tensor *w[3] = {d.q_proj, d.k_proj, d.v_proj};
+    eb_tensor *c[3] = {q.t, k.t, v.t};
+    const size_t of[3] = {qd, kd, kd};
+    EB_TRY(eb_linear_f16w_multi(rec, x, 3, w, c, of, rows, d.hidden));
+    eb_tensor *ot = nullptr;
+    EB_TRY(eb_attention_forward_qkv(attn, rec, q.t, k.t, v.t, rope, kv, layer, rows, base_pos,
+                                    &ot));
+    Owned o(ot);
+    const size_t ys[2] = {rows, d.hidden};
+    eb_tensor *yt = nullptr;
+    EB_TRY(eb_tensor_empty(dev, ys, 2, EB_F32, &yt));
+    Owned y(yt);
+    EB_TRY(eb_linear_f16w(rec, o.t, d.o_proj, y.t, rows, qd, d.hidden));
+    *out = y.release();
     return eb::ok();
 }

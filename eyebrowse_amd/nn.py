@@ -12,6 +12,7 @@ from typing import Optional
 
 from ._lib import AttentionDesc, c_size, c_vp, lib
 from .gpu import DType, Device, Recorder, Tensor, check
+from .kernels import linear_f16w
 
 
 class _Borrowed(Tensor):
@@ -71,6 +72,19 @@ class Rope:
             self._h = c_vp()
 
 
+class Linear:
+    """Linear (crates/eyebrowse-nn/src/linear.rs:5-23): bias-free, packed-f16 weight
+    [out_f, in_f] (HF layout)."""
+
+    def __init__(self, w: Tensor, in_f: int, out_f: int):
+        self.w, self.in_f, self.out_f = w, in_f, out_f
+
+    def forward(self, rec: Recorder, x: Tensor, rows: int) -> Tensor:
+        out = Tensor.empty(rec.dev, (rows, self.out_f))
+        linear_f16w(rec, x, self.w, out, rows, self.in_f, self.out_f)
+        return out
+
+
 class KvCache:
     """KvCache (crates/eyebrowse-nn/src/kv_cache.rs:9-50): per-layer K/V tensors
     [max_seq, n_kv_heads, head_dims[l]]."""
@@ -114,8 +128,9 @@ class KvCache:
 
 @dataclass
 class Attention:
-    """Attention (crates/eyebrowse-nn/src/attention.rs:10-23) without the projections:
-    optional per-head q/k/v RMSNorm weights ([head_dim] f32 tensors), head counts, scale."""
+    """Attention (crates/eyebrowse-nn/src/attention.rs:10-23): head counts, scale, optional
+    per-head q/k/v RMSNorm weights ([head_dim] f32 tensors) and, optionally, the four
+    packed-f16 projections (all or none) with the model width `hidden`."""
     n_heads: int
     n_kv_heads: int
     head_dim: int
@@ -125,13 +140,18 @@ class Attention:
     v_norm: Optional[Tensor] = None
     norm_eps: float = 1e-6
     window: int = 0  # sliding window of a local layer (0: global attention)
+    q_proj: Optional[Tensor] = None  # [n_heads*head_dim, hidden]
+    k_proj: Optional[Tensor] = None  # [n_kv_heads*head_dim, hidden]
+    v_proj: Optional[Tensor] = None
+    o_proj: Optional[Tensor] = None  # [hidden, n_heads*head_dim]
+    hidden: int = 0
 
     def __post_init__(self):
+        h = lambda t: t.handle if t is not None else None  # noqa: E731
         d = AttentionDesc(self.n_heads, self.n_kv_heads, self.head_dim, self.scale, self.norm_eps,
-                          self.q_norm.handle if self.q_norm is not None else None,
-                          self.k_norm.handle if self.k_norm is not None else None,
-                          self.v_norm.handle if self.v_norm is not None else None,
-                          self.window)
+                          h(self.q_norm), h(self.k_norm), h(self.v_norm), self.window,
+                          h(self.q_proj), h(self.k_proj), h(self.v_proj), h(self.o_proj),
+                          self.hidden)
         out = c_vp()
         check(lib().eb_attention_new(ctypes.byref(d), ctypes.byref(out)))
         self._h = out
@@ -146,6 +166,15 @@ class Attention:
         check(lib().eb_attention_forward_qkv(self._h, rec.handle, q.handle, k.handle, v.handle,
                                              rope.handle, kv.handle, layer, rows, base_pos,
                                              ctypes.byref(out)))
+        return Tensor(out.value, rec.dev)
+
+    def forward(self, rec: Recorder, x: Tensor, rope: Rope, kv: KvCache, layer: int, rows: int,
+                base_pos: int) -> Tensor:
+        """Attention::forward (attention.rs:30-45) whole: x [rows, hidden] -> [rows, hidden]
+        (q/k/v projections in one launch, forward_qkv, o_proj)."""
+        out = c_vp()
+        check(lib().eb_attention_forward(self._h, rec.handle, x.handle, rope.handle, kv.handle,
+                                         layer, rows, base_pos, ctypes.byref(out)))
         return Tensor(out.value, rec.dev)
 
     def __del__(self):

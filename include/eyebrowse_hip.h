@@ -303,9 +303,12 @@ eb_tensor *eb_kv_cache_k(eb_kv_cache *kv, size_t layer);
 eb_tensor *eb_kv_cache_v(eb_kv_cache *kv, size_t layer);
 size_t eb_kv_cache_max_seq(const eb_kv_cache *kv);
 
-/* The Attention fields that matter between the projections
- * (crates/eyebrowse-nn/src/attention.rs:10-23). Norm weights are [head_dim] f32
- * tensors or NULL (None); the module keeps its own references. */
+/* The Attention fields (crates/eyebrowse-nn/src/attention.rs:10-23). Norm weights are
+ * [head_dim] f32 tensors or NULL (None). Projections are packed-f16 weights in the
+ * linear_f16w format: q_proj [n_heads*head_dim, hidden], k_proj and v_proj
+ * [n_kv_heads*head_dim, hidden], o_proj [hidden, n_heads*head_dim]; all four or none
+ * (none: only eb_attention_forward_qkv is available). The module borrows every tensor:
+ * they must outlive it, as the reference's Attention owns them. */
 typedef struct eb_attention_desc {
     size_t n_heads;
     size_t n_kv_heads;
@@ -316,6 +319,11 @@ typedef struct eb_attention_desc {
     const eb_tensor *k_norm; /* may be NULL */
     const eb_tensor *v_norm; /* may be NULL */
     size_t window;           /* sliding window of a local layer; 0 = global attention */
+    const eb_tensor *q_proj; /* may be NULL (then all four are) */
+    const eb_tensor *k_proj;
+    const eb_tensor *v_proj;
+    const eb_tensor *o_proj;
+    size_t hidden;           /* model width (the projections' in / out features) */
 } eb_attention_desc;
 
 eb_status eb_attention_new(const eb_attention_desc *desc, eb_attention **out);
@@ -330,6 +338,12 @@ eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recorder *rec,
                                    const eb_tensor *q, const eb_tensor *k, const eb_tensor *v,
                                    const eb_rope_tables *rope, eb_kv_cache *kv, size_t layer,
                                    size_t rows, size_t base_pos, eb_tensor **out);
+/* Attention::forward (attention.rs:30-45) whole: x [rows, hidden] f32; q/k/v projections
+ * in one launch, then eb_attention_forward_qkv, then o_proj. *out is a new tensor
+ * [rows, hidden]. Needs the projection weights in the descriptor. */
+eb_status eb_attention_forward(const eb_attention *attn, eb_recorder *rec, const eb_tensor *x,
+                               const eb_rope_tables *rope, eb_kv_cache *kv, size_t layer,
+                               size_t rows, size_t base_pos, eb_tensor **out);
 
 #ifdef __cplusplus
 }

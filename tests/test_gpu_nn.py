@@ -262,3 +262,87 @@ def test_forward_routing_and_errors(dev):
     rec.submit()
     with pytest.raises(eb.UnsupportedConfig):
         eb.Attention(H, Hkv, 6, 0.3)
+
+
+# ---------------------------------------------------------------- with projections ------
+
+def _proj(dev, out_f, in_f, seed, scale=0.03):
+    w = oracle.randn((out_f, in_f), seed) * np.float32(scale)
+    return w, eb.Tensor.from_f16_packed(dev, w.shape, w)
+
+
+@pytest.mark.parametrize("cfg", ["qwen", "gemma"])
+def test_attention_forward_with_projections(dev, cfg):
+    """Attention.forward whole (attention.rs:30-45): q/k/v projections, norms, RoPE,
+    kv_write, attention, o_proj; a prompt, a continuation chunk and two decode steps,
+    each against the oracle chain (linear_f16w, rmsnorm, rope, attention over the cache
+    contents the oracle builds itself)."""
+    if cfg == "qwen":   # Qwen3-0.6B widths: QK-norm, full RoPE theta 1e6, scale 1/sqrt(hd)
+        H, Hkv, hd, hidden, ra, theta = 16, 8, 128, 1024, None, 1e6
+        sc = float(oracle.default_scale(hd))
+        vgain = None
+    else:               # Gemma-4-shaped: QK-norm + weightless V-norm, partial RoPE, scale 1
+        H, Hkv, hd, hidden, ra, theta = 8, 4, 256, 640, 32, 1e6
+        sc = 1.0
+        vgain = np.ones(hd, np.float32)
+    eps, max_seq = 1e-6, 512
+    note(f"attention forward with projections {cfg}")
+    gq = (1 + 0.1 * oracle.randn((hd,), 4)).astype(np.float32)
+    gk = (1 + 0.1 * oracle.randn((hd,), 5)).astype(np.float32)
+    wq, tq = _proj(dev, H * hd, hidden, 11)
+    wk, tk = _proj(dev, Hkv * hd, hidden, 12)
+    wv, tv = _proj(dev, Hkv * hd, hidden, 13)
+    wo, to = _proj(dev, hidden, H * hd, 14)
+    attn = eb.Attention(H, Hkv, hd, sc, q_norm=upload(dev, gq), k_norm=upload(dev, gk),
+                        v_norm=upload(dev, vgain) if vgain is not None else None, norm_eps=eps,
+                        q_proj=tq, k_proj=tk, v_proj=tv, o_proj=to, hidden=hidden)
+    if ra is None:
+        rope = eb.Rope.build(dev, max_seq, hd, theta)
+        cos, sin = oracle.rope_tables(max_seq, hd, theta)
+    else:
+        rope = eb.Rope.build_partial(dev, max_seq, hd, ra, theta)
+        cos, sin = oracle.rope_tables(max_seq, hd, theta, rope_angles=ra)
+    kv = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    kc = np.zeros((max_seq, Hkv, hd), np.float32)
+    vc = np.zeros((max_seq, Hkv, hd), np.float32)
+    bits = {n: oracle.f16_bits(w) for n, w in (("q", wq), ("k", wk), ("v", wv), ("o", wo))}
+    for a, b in ((0, 40), (40, 60), (60, 61), (61, 62)):
+        rows = b - a
+        x = oracle.randn((rows, hidden), 100 + a)
+        rec = eb.Recorder(dev)
+        y = attn.forward(rec, upload(dev, x), rope, kv, 0, rows, a)
+        rec.submit()
+        q = oracle.linear_f16w(x, bits["q"], rows, hidden, H * hd, threads=16)
+        k = oracle.linear_f16w(x, bits["k"], rows, hidden, Hkv * hd, threads=16)
+        v = oracle.linear_f16w(x, bits["v"], rows, hidden, Hkv * hd, threads=16)
+        qn = oracle.rmsnorm(q, gq, rows * H, hd, eps)
+        kn = oracle.rmsnorm(k, gk, rows * Hkv, hd, eps)
+        vn = oracle.rmsnorm(v, vgain, rows * Hkv, hd, eps) if vgain is not None else v
+        qr = oracle.rope(qn, cos, sin, rows, H, hd, a)
+        kr = oracle.rope(kn, cos, sin, rows, Hkv, hd, a)
+        kc[a:b] = kr.reshape(rows, Hkv, hd)
+        vc[a:b] = np.asarray(vn).reshape(rows, Hkv, hd)
+        o = oracle.attn_chunk(qr.reshape(rows, H, hd), kc, vc, H, Hkv, a, rows, hd, sc,
+                              threads=16)
+        want = oracle.linear_f16w(o.reshape(rows, H * hd), bits["o"], rows, H * hd, hidden,
+                                  threads=16)
+        assert_close(y.to_f32().reshape(rows, hidden), want, what=f"{cfg} rows {a}..{b}")
+
+
+def test_attention_projection_validation(dev):
+    note("attention projection validation")
+    H, Hkv, hd, hidden = 4, 2, 64, 128
+    _, tq = _proj(dev, H * hd, hidden, 1)
+    _, tk = _proj(dev, Hkv * hd, hidden, 2)
+    _, to = _proj(dev, hidden, H * hd, 3)
+    with pytest.raises(eb.ShapeMismatch):  # three of four
+        eb.Attention(H, Hkv, hd, 0.1, q_proj=tq, k_proj=tk, v_proj=tk, hidden=hidden)
+    with pytest.raises(eb.ShapeMismatch):  # wrong shape (k_proj as q_proj)
+        eb.Attention(H, Hkv, hd, 0.1, q_proj=tk, k_proj=tk, v_proj=tk, o_proj=to, hidden=hidden)
+    bare = eb.Attention(H, Hkv, hd, 0.1)
+    rope = eb.Rope.build(dev, 16, hd, 1e4)
+    kv = eb.KvCache.new(dev, 1, 16, Hkv, hd)
+    rec = eb.Recorder(dev)
+    with pytest.raises(eb.ShapeMismatch):  # no projections: forward_qkv only
+        bare.forward(rec, upload(dev, np.zeros((1, hidden), np.float32)), rope, kv, 0, 1, 0)
+    rec.submit()
