@@ -11,20 +11,22 @@ reference's Rust interface:
 - ``nn``: Linear, Rope, KvCache, Attention (crates/eyebrowse-nn).
 """
 from ._lib import LIB_PATH, lib
-from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, LoadError, OutOfMemory,
-                  Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
-from .kernels import (attn_decode, attn_decode_step, attn_decode_step_window,
-                      attn_decode_window, attn_decode_workspace_floats, attn_prefill,
-                      attn_prefill_chunk, kv_write, launch_attn_decode, launch_attn_decode_f16,
-                      launch_linear_f16w, linear_f16w, linear_f16w_multi, linear_workspace_floats,
-                      launch_attn_decode_step, launch_attn_decode_step_f16,
-                      launch_attn_decode_window, launch_attn_prefill, launch_attn_prefill_chunk,
+from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, Graph, LoadError,
+                  OutOfMemory, Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
+from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_step,
+                      attn_decode_step_window, attn_decode_window, attn_decode_workspace_floats,
+                      attn_prefill, attn_prefill_chunk, kv_write, launch_argmax,
+                      launch_attn_decode, launch_attn_decode_f16, launch_attn_decode_step,
+                      launch_attn_decode_step_f16, launch_attn_decode_window,
+                      launch_attn_prefill, launch_attn_prefill_chunk,
                       launch_attn_prefill_chunk_f16, launch_kv_write, launch_kv_write_f16,
-                      launch_rmsnorm, launch_rope, rmsnorm, rope)
+                      launch_linear_f16w, launch_rmsnorm, launch_rope, linear_f16w,
+                      linear_f16w_multi, linear_workspace_floats, rmsnorm, rope)
 from .nn import Attention, KvCache, Linear, Rope
 
 __all__ = [
-    "LIB_PATH", "lib", "DType", "Device", "DeviceUnavailable", "EyebrowseError", "LoadError",
+    "LIB_PATH", "lib", "DType", "Device", "DeviceUnavailable", "EyebrowseError", "Graph",
+    "LoadError", "argmax", "argmax_workspace_floats", "launch_argmax",
     "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
     "attn_decode_step", "attn_decode_step_window", "attn_decode_window",
     "attn_decode_workspace_floats", "attn_prefill", "attn_prefill_chunk", "kv_write",

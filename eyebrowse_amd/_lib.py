@@ -101,6 +101,14 @@ SIGNATURES = {
     "eb_launch_attn_decode_step": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size,
                                           c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
                                           c_size, c_size, c_float, c_vp, c_size, c_int]),
+    "eb_device_begin_capture": (c_st, [c_vp]),
+    "eb_device_end_capture": (c_st, [c_vp, ctypes.POINTER(c_vp)]),
+    "eb_graph_launch": (c_st, [c_vp]),
+    "eb_graph_release": (None, [c_vp]),
+    "eb_tensor_write": (c_st, [c_vp, c_vp, c_size]),
+    "eb_argmax": (c_st, [c_vp, c_vp, c_vp, c_size]),
+    "eb_argmax_workspace_floats": (c_size, [c_size]),
+    "eb_launch_argmax": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size]),
     "eb_linear_f16w": (c_st, [c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size]),
     "eb_linear_f16w_multi": (c_st, [c_vp, c_vp, c_size, ctypes.POINTER(c_vp),
                                     ctypes.POINTER(c_vp), ctypes.POINTER(c_size), c_size,

@@ -42,6 +42,7 @@ SOURCES = [
     "eb_decode.hip",
     "eb_prefill.hip",
     "eb_linear.hip",
+    "eb_argmax.hip",
 ]
 
 

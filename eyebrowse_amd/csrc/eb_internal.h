@@ -93,6 +93,11 @@ size_t linear_workspace_floats(size_t m, size_t in_f);
 eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_t *const *w,
                                    float *const *y, const size_t *out_f, int nseg, size_t m,
                                    size_t in_f, float *ws, size_t ws_floats);
+// argmax (sampling.rs:6-53 semantics): out[0] = winning index of x[0..n); workspace of
+// argmax_workspace_floats(n) floats, 8-byte aligned.
+size_t argmax_workspace_floats(size_t n);
+eb_status launch_argmax(hipStream_t st, const float *x, size_t n, uint32_t *out, float *ws,
+                        size_t ws_floats);
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
                          size_t rows, size_t dim, float eps);
 eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,

@@ -103,11 +103,25 @@ int current_cu_count() {
 
 using eb::fail;
 
+#define EB_TRY(expr)                     \
+    do {                                 \
+        eb_status eb_s_ = (expr);        \
+        if (eb_s_ != EB_OK) return eb_s_; \
+    } while (0)
+
 // ------------------------------------------------------------------ handles --------------
 
 // Buffers at or below this size are recycled; larger ones are freed on release
 // (MAX_POOLED_BYTES, crates/eyebrowse-gpu/src/device.rs:12-14).
 static constexpr size_t kMaxPooledBytes = (size_t)64 << 20;
+
+// A device buffer handed back while a graph capture was running: it stays out of the
+// pool for as long as the graph that may write it exists.
+struct Parked {
+    void *p;
+    size_t bytes;
+    bool poolable;
+};
 
 struct eb_device {
     int ordinal = 0;
@@ -119,6 +133,14 @@ struct eb_device {
     std::mutex ws_mu;
     float *ws = nullptr;  // decode split workspace, grow-only, stream ordered
     size_t ws_floats = 0;
+    std::atomic<bool> capturing{false};  // the stream is being captured into a graph
+    std::vector<Parked> parked;          // buffers released during the capture (pool_mu)
+};
+
+struct eb_graph {
+    eb_device *dev = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<Parked> held;  // intermediates the graph's kernels read and write
 };
 
 struct eb_tensor {
@@ -133,6 +155,12 @@ struct eb_tensor {
 struct eb_recorder {
     eb_device *dev = nullptr;
 };
+
+static eb_status not_capturing(const eb_device *d, const char *what) {
+    if (d && d->capturing.load())
+        return fail(EB_OTHER, "%s: not allowed while the device's stream is being captured", what);
+    return EB_OK;
+}
 
 static void device_retain(eb_device *d) { d->refs.fetch_add(1); }
 
@@ -221,6 +249,7 @@ void eb_device_release(eb_device *dev) { device_unref(dev); }
 
 eb_status eb_device_synchronize(eb_device *dev) {
     if (!dev) return fail(EB_OTHER, "device is null");
+    EB_TRY(not_capturing(dev, "synchronize"));
     EB_HIP_TRY(hipSetDevice(dev->ordinal));
     EB_HIP_TRY(hipStreamSynchronize(dev->stream));
     return eb::ok();
@@ -285,6 +314,7 @@ eb_status eb_tensor_empty(eb_device *dev, const size_t *shape, size_t ndim, eb_d
 
 static eb_status tensor_from_host(eb_device *dev, const size_t *shape, size_t ndim,
                                   eb_dtype dt, const void *data, size_t n, eb_tensor **out) {
+    EB_TRY(not_capturing(dev, "from_host"));
     if (n != shape_numel(shape, ndim))
         return fail(EB_SHAPE_MISMATCH, "from_host: data len %zu != shape numel %zu", n,
                     shape_numel(shape, ndim));
@@ -317,6 +347,7 @@ eb_status eb_tensor_from_u32(eb_device *dev, const size_t *shape, size_t ndim,
 
 eb_status eb_tensor_read_bytes(const eb_tensor *t, void *host, size_t nbytes) {
     if (!t) return fail(EB_OTHER, "tensor is null");
+    EB_TRY(not_capturing(t->dev, "read_bytes"));
     size_t want = shape_numel(t->shape.data(), t->shape.size()) * eb_dtype_size(t->dtype);
     if (nbytes != want)
         return fail(EB_SHAPE_MISMATCH, "read_bytes: asked for %zu bytes, tensor has %zu", nbytes,
@@ -338,7 +369,11 @@ eb_status eb_tensor_to_f32(const eb_tensor *t, float *host, size_t n) {
 void eb_tensor_release(eb_tensor *t) {
     if (!t) return;
     eb_device *d = t->dev;
-    if (t->poolable) {
+    if (d->capturing.load()) {
+        // A captured kernel may still use this buffer on every replay of the graph.
+        std::lock_guard<std::mutex> lk(d->pool_mu);
+        d->parked.push_back(Parked{t->ptr, t->bytes, t->poolable});
+    } else if (t->poolable) {
         // Stream-ordered reuse: every kernel runs on the device's single stream, so a
         // later user of this buffer is queued after every earlier one.
         std::lock_guard<std::mutex> lk(d->pool_mu);
@@ -390,6 +425,130 @@ void eb_recorder_release(eb_recorder *rec) {
     delete rec;
 }
 
+
+eb_status eb_tensor_write(eb_tensor *t, const void *host, size_t nbytes) {
+    if (!t) return fail(EB_OTHER, "tensor is null");
+    EB_TRY(not_capturing(t->dev, "tensor_write"));
+    size_t want = shape_numel(t->shape.data(), t->shape.size()) * eb_dtype_size(t->dtype);
+    if (nbytes != want)
+        return fail(EB_SHAPE_MISMATCH, "tensor_write: %zu bytes given, tensor has %zu", nbytes,
+                    want);
+    if (nbytes == 0) return eb::ok();
+    if (!host) return fail(EB_SHAPE_MISMATCH, "tensor_write: host buffer is null");
+    EB_HIP_TRY(hipSetDevice(t->dev->ordinal));
+    EB_HIP_TRY(hipMemcpyAsync(t->ptr, host, nbytes, hipMemcpyHostToDevice, t->dev->stream));
+    EB_HIP_TRY(hipStreamSynchronize(t->dev->stream));
+    return eb::ok();
+}
+
+// ---- graphs ---------------------------------------------------------------------------
+
+// Hands parked buffers back: pooled sizes to the pool (stream-ordered reuse, like any
+// release), larger ones freed once the stream has drained.
+static void return_buffers(eb_device *d, std::vector<Parked> &v) {
+    bool synced = false;
+    for (const Parked &b : v) {
+        if (b.poolable) {
+            std::lock_guard<std::mutex> lk(d->pool_mu);
+            d->pool[b.bytes].push_back(b.p);
+        } else {
+            if (!synced) (void)hipStreamSynchronize(d->stream);
+            synced = true;
+            (void)hipFree(b.p);
+        }
+    }
+    v.clear();
+}
+
+eb_status eb_device_begin_capture(eb_device *dev) {
+    if (!dev) return fail(EB_OTHER, "device is null");
+    EB_TRY(not_capturing(dev, "begin_capture"));
+    EB_HIP_TRY(hipSetDevice(dev->ordinal));
+    EB_HIP_TRY(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeRelaxed));
+    dev->capturing.store(true);
+    return eb::ok();
+}
+
+eb_status eb_device_end_capture(eb_device *dev, eb_graph **inout) {
+    if (!dev || !inout) return fail(EB_OTHER, "device/graph is null");
+    if (!dev->capturing.load()) return fail(EB_OTHER, "end_capture: no capture is running");
+    EB_HIP_TRY(hipSetDevice(dev->ordinal));
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(dev->stream, &g);
+    std::vector<Parked> held;
+    {
+        std::lock_guard<std::mutex> lk(dev->pool_mu);
+        held.swap(dev->parked);
+    }
+    dev->capturing.store(false);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return_buffers(dev, held);
+        return eb::hip_fail(e, "hipStreamEndCapture (a call during the capture failed?)");
+    }
+    eb_graph *gr = *inout;
+    if (gr && gr->dev != dev) {
+        (void)hipGraphDestroy(g);
+        return_buffers(dev, held);
+        return fail(EB_OTHER, "end_capture: the graph belongs to another device");
+    }
+    if (gr) {
+        // Same topology: update the executable in place; otherwise instantiate anew. The
+        // stream is drained first so that no launch of the old version still runs.
+        e = hipStreamSynchronize(dev->stream);
+        if (e == hipSuccess) {
+            hipGraphNode_t err_node = nullptr;
+            hipGraphExecUpdateResult res;
+            if (hipGraphExecUpdate(gr->exec, g, &err_node, &res) != hipSuccess) {
+                (void)hipGetLastError();
+                (void)hipGraphExecDestroy(gr->exec);
+                gr->exec = nullptr;
+                e = hipGraphInstantiate(&gr->exec, g, nullptr, nullptr, 0);
+            }
+        }
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) {
+            return_buffers(dev, held);
+            return eb::hip_fail(e, "graph update");
+        }
+        return_buffers(dev, gr->held);
+        gr->held.swap(held);
+        return eb::ok();
+    }
+    auto *ng = new eb_graph();
+    ng->dev = dev;
+    e = hipGraphInstantiate(&ng->exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        delete ng;
+        return_buffers(dev, held);
+        return eb::hip_fail(e, "hipGraphInstantiate");
+    }
+    device_retain(dev);
+    ng->held.swap(held);
+    *inout = ng;
+    return eb::ok();
+}
+
+eb_status eb_graph_launch(eb_graph *g) {
+    if (!g || !g->exec) return fail(EB_OTHER, "graph is null");
+    EB_TRY(not_capturing(g->dev, "graph_launch"));
+    EB_HIP_TRY(hipSetDevice(g->dev->ordinal));
+    EB_HIP_TRY(hipGraphLaunch(g->exec, g->dev->stream));
+    return eb::ok();
+}
+
+void eb_graph_release(eb_graph *g) {
+    if (!g) return;
+    eb_device *d = g->dev;
+    (void)hipSetDevice(d->ordinal);
+    (void)hipStreamSynchronize(d->stream);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    return_buffers(d, g->held);
+    delete g;
+    device_unref(d);
+}
+
 }  // extern "C"
 
 // ------------------------------------------------------------------ kernel entry points -
@@ -417,11 +576,6 @@ static eb_status tensor_cache(const eb_tensor *t, const char *name, eb_device *d
     return EB_OK;
 }
 
-#define EB_TRY(expr)                     \
-    do {                                 \
-        eb_status eb_s_ = (expr);        \
-        if (eb_s_ != EB_OK) return eb_s_; \
-    } while (0)
 
 // Float-buffer views with element counts, shared by the handle and raw entry points.
 static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
@@ -569,6 +723,10 @@ static eb_status step_rows_checked(const float *knew, const float *vnew, size_t 
 static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
     std::lock_guard<std::mutex> lk(dev->ws_mu);
     if (floats > dev->ws_floats) {
+        if (dev->capturing.load())
+            return fail(EB_OTHER,
+                        "the device workspace would have to grow during a graph capture "
+                        "(run the captured step once outside the capture first)");
         if (dev->ws) {
             EB_HIP_TRY(hipStreamSynchronize(dev->stream));
             EB_HIP_TRY(hipFree(dev->ws));
@@ -988,6 +1146,45 @@ eb_status eb_launch_linear_f16w(void *stream, const float *a, size_t a_numel, co
                                 size_t out_f, float *workspace, size_t workspace_floats) {
     return linear_checked((hipStream_t)stream, a, a_numel, &w, &w_halves, &c, &c_numel, &out_f,
                           1, m, in_f, workspace, workspace_floats);
+}
+
+
+static eb_status argmax_checked(hipStream_t st, const float *x, size_t xn, uint32_t *out,
+                                size_t out_n, size_t vocab, float *ws, size_t wsn) {
+    EB_TRY(eb::check_numel(xn, vocab, "logits"));
+    EB_TRY(eb::check_numel(out_n, 1, "out_idx"));
+    EB_TRY(eb::check_ptr(out, "out_idx"));
+    if (vocab > 0) EB_TRY(eb::check_ptr(x, "logits"));
+    const size_t need = eb::argmax_workspace_floats(vocab);
+    if (wsn < need)
+        return fail(EB_SHAPE_MISMATCH, "argmax: workspace holds %zu floats, needs %zu", wsn, need);
+    EB_TRY(eb::check_ptr(ws, "workspace"));
+    EB_TRY(eb::launch_argmax(st, x, vocab, out, ws, wsn));
+    return eb::ok();
+}
+
+eb_status eb_argmax(eb_recorder *rec, const eb_tensor *logits, eb_tensor *out_idx,
+                    size_t vocab) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(logits, "logits", rec->dev));
+    if (!out_idx || (out_idx->dtype != EB_U32 && out_idx->dtype != EB_I32))
+        return fail(EB_SHAPE_MISMATCH, "argmax: out_idx must be a u32 tensor");
+    if (out_idx->dev != rec->dev) return fail(EB_OTHER, "out_idx lives on another device");
+    const size_t wsn = eb::argmax_workspace_floats(vocab);
+    float *ws = nullptr;
+    EB_TRY(device_workspace(rec->dev, wsn, &ws));
+    return argmax_checked(rec->dev->stream, static_cast<const float *>(logits->ptr),
+                          eb_tensor_numel(logits), static_cast<uint32_t *>(out_idx->ptr),
+                          eb_tensor_numel(out_idx), vocab, ws, wsn);
+}
+
+size_t eb_argmax_workspace_floats(size_t vocab) { return eb::argmax_workspace_floats(vocab); }
+
+eb_status eb_launch_argmax(void *stream, const float *logits, size_t logits_numel,
+                           uint32_t *out_idx, size_t vocab, float *workspace,
+                           size_t workspace_floats) {
+    return argmax_checked((hipStream_t)stream, logits, logits_numel, out_idx, 1, vocab,
+                          workspace, workspace_floats);
 }
 
 }  // extern "C"

@@ -99,6 +99,19 @@ class Device:
         """Free pooled buffers of exactly ``nbytes`` (device.rs:63-70)."""
         return int(lib().eb_device_pooled(self._h, nbytes))
 
+    def begin_capture(self) -> None:
+        """Start capturing the device stream into a HIP graph (no counterpart in the
+        reference): kernels recorded until end_capture are captured, not run."""
+        check(lib().eb_device_begin_capture(self._h))
+
+    def end_capture(self, graph: "Graph | None" = None) -> "Graph":
+        """End the capture: a new Graph, or `graph` updated in place."""
+        h = c_vp(graph._h.value if graph is not None else None)
+        check(lib().eb_device_end_capture(self._h, ctypes.byref(h)))
+        if graph is not None:
+            return graph
+        return Graph(h.value, self)
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
@@ -184,6 +197,17 @@ class Tensor:
                                      out.size))
         return out
 
+    def write(self, data) -> None:
+        """Copy host data (same byte size as the tensor) into it, synchronously."""
+        if isinstance(data, (bytes, bytearray)):
+            buf = bytes(data)
+        else:
+            a = np.ascontiguousarray(data)
+            if a.dtype == np.float64:
+                a = a.astype(np.float32)
+            buf = a.tobytes()
+        check(lib().eb_tensor_write(self._h, buf, len(buf)))
+
     def read_bytes(self) -> bytes:
         buf = ctypes.create_string_buffer(self.byte_len())
         check(lib().eb_tensor_read_bytes(self._h, buf, self.byte_len()))
@@ -227,3 +251,24 @@ class Recorder:
         if h is not None and h.value:
             lib().eb_recorder_release(h)
             self._h = c_vp()
+
+
+class Graph:
+    """A captured step (Device.begin_capture / end_capture): one hipGraphLaunch replays
+    every captured kernel on the device stream."""
+
+    def __init__(self, handle: int, dev: Device):
+        self._h = c_vp(handle)
+        self.dev = dev
+
+    def launch(self) -> None:
+        check(lib().eb_graph_launch(self._h))
+
+    def release(self) -> None:
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().eb_graph_release(h)
+            self._h = c_vp()
+
+    def __del__(self):
+        self.release()

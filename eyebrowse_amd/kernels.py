@@ -100,7 +100,23 @@ def linear_workspace_floats(m: int, in_f: int) -> int:
     return int(lib().eb_linear_workspace_floats(m, in_f))
 
 
+def argmax(rec: Recorder, logits: Tensor, out_idx: Tensor, vocab: int) -> None:
+    """argmax (crates/eyebrowse-kernels/src/sampling.rs:42-53): out_idx[0] = index of the
+    largest logit, with the reference's tie order."""
+    check(lib().eb_argmax(rec.handle, logits.handle, out_idx.handle, vocab))
+
+
+def argmax_workspace_floats(vocab: int) -> int:
+    return int(lib().eb_argmax_workspace_floats(vocab))
+
+
 # ---- raw launches on caller memory (stream and pointers as ints) ------------------------
+
+def launch_argmax(stream: int, logits: int, logits_numel: int, out_idx: int, vocab: int,
+                  workspace: int, workspace_floats: int) -> None:
+    check(lib().eb_launch_argmax(stream, logits, logits_numel, out_idx, vocab, workspace,
+                                 workspace_floats))
+
 
 def launch_linear_f16w(stream: int, a: int, a_numel: int, w: int, w_halves: int, c: int,
                        c_numel: int, m: int, in_f: int, out_f: int, workspace: int,

@@ -115,6 +115,30 @@ eb_status eb_recorder_submit(eb_recorder *rec);
 /* Drop a recorder without submitting (work already enqueued still runs). */
 void eb_recorder_release(eb_recorder *rec);
 
+/* ---- graphs: a whole step as one HIP graph ----------------------------------------
+ * No counterpart in the reference, whose answer to per-dispatch overhead is one command
+ * buffer per step (README.md:43-45, models/src/model.rs:108-175); this is the HIP form:
+ * the step's launches are captured once and replayed with one hipGraphLaunch.
+ * eb_device_begin_capture starts capturing the device's stream: every kernel recorded on
+ * the device until eb_device_end_capture becomes part of the graph instead of running.
+ * While capturing: no host copies (eb_tensor_from_*, to_f32, read_bytes, eb_tensor_write)
+ * and no synchronize; a device workspace that would have to grow fails the call (run the
+ * step once eagerly first, which also fills the buffer pool). Buffers released during the
+ * capture stay reserved until the graph is released or updated. Kernels take their
+ * shapes and positions as launch arguments, so a decode step at a new position is a new
+ * capture: pass the previous graph to eb_device_end_capture to update it in place. */
+typedef struct eb_graph eb_graph;
+eb_status eb_device_begin_capture(eb_device *dev);
+/* *inout NULL: a new graph. *inout a graph of this device: updated in place (its old
+ * intermediates are released). */
+eb_status eb_device_end_capture(eb_device *dev, eb_graph **inout);
+/* Enqueue one replay on the device stream. */
+eb_status eb_graph_launch(eb_graph *g);
+void eb_graph_release(eb_graph *g);
+/* Host -> device copy into an existing tensor (nbytes = its size), synchronous: how a
+ * captured step gets new inputs between replays. */
+eb_status eb_tensor_write(eb_tensor *t, const void *host, size_t nbytes);
+
 /* ---- kernels (crates/eyebrowse-kernels/src) --------------------------------------- */
 
 /* attn_prefill (attention.rs:94-120): causal GQA attention over q [s,h,hd],
@@ -242,6 +266,18 @@ size_t eb_linear_workspace_floats(size_t m, size_t in_f);
 eb_status eb_launch_linear_f16w(void *stream, const float *a, size_t a_numel, const uint16_t *w,
                                 size_t w_halves, float *c, size_t c_numel, size_t m, size_t in_f,
                                 size_t out_f, float *workspace, size_t workspace_floats);
+
+/* ---- greedy sampling: argmax (crates/eyebrowse-kernels/src/sampling.rs:6-53) -------
+ * out_idx[0] = the index of the largest of logits[0..vocab), with the reference's choice
+ * on ties (its 256-lane scan then tree: the lane i mod 256 first in bit-reversed order,
+ * then the smallest i); NaN and values <= -3e38 never win; 0 if nothing does. out_idx is
+ * a [1] u32 tensor. Two launches over many workgroups (the reference uses one). */
+eb_status eb_argmax(eb_recorder *rec, const eb_tensor *logits, eb_tensor *out_idx,
+                    size_t vocab);
+size_t eb_argmax_workspace_floats(size_t vocab);
+eb_status eb_launch_argmax(void *stream, const float *logits, size_t logits_numel,
+                           uint32_t *out_idx, size_t vocab, float *workspace,
+                           size_t workspace_floats);
 
 /* ---- raw launches over IEEE-half (f16) KV caches ----------------------------------
  * Caches hold uint16_t IEEE half bit patterns, [max_seq, hkv, hd], numel in elements.

@@ -252,7 +252,8 @@ def pack_f16(x) -> np.ndarray:
 
 
 def argmax(x) -> int:
-    """argmax (sampling.rs:6-38): first index of the maximum; NaN and values <= -3e38
-    never win."""
+    """argmax (sampling.rs:6-38), the reference's 256-lane scan and tree: the maximum;
+    ties to the lane (index mod 256) first in bit-reversed order, then the smallest index;
+    NaN and values <= -3e38 never win (0 if nothing does)."""
     x = _f32(x).ravel()
     return int(_load().ebo_argmax(_p(x), x.size))

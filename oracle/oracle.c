@@ -338,18 +338,31 @@ void ebo_linear_f16w(const float *x, const uint16_t *w, float *y, size_t m, size
         }
 }
 
-/* argmax's semantics (crates/eyebrowse-kernels/src/sampling.rs:6-38): the index of the
- * largest value, the lowest such index on ties; values not above -3e38 (and NaN) never
- * win, so an all -inf/NaN vector gives 0. */
+/* argmax (crates/eyebrowse-kernels/src/sampling.rs:6-38) restated step by step: 256
+ * lanes, lane t scans i = t, t+256, ... keeping the first strictly larger value (start
+ * -3e38, so NaN and values <= -3e38 never win, index 0 if nothing does); then a tree
+ * over the lanes, strides 128..1, where the right lane replaces the left only if its
+ * value is strictly larger. Ties therefore go to the lane (i mod 256) that comes first
+ * in bit-reversed order, then to the smallest i. */
 uint32_t ebo_argmax(const float *x, size_t n) {
-    float bv = -3.0e38f;
-    uint32_t bi = 0;
-    for (size_t i = 0; i < n; ++i)
-        if (x[i] > bv) {
-            bv = x[i];
-            bi = (uint32_t)i;
-        }
-    return bi;
+    float bv[256];
+    uint32_t bi[256];
+    for (size_t t = 0; t < 256; ++t) {
+        bv[t] = -3.0e38f;
+        bi[t] = 0;
+        for (size_t i = t; i < n; i += 256)
+            if (x[i] > bv[t]) {
+                bv[t] = x[i];
+                bi[t] = (uint32_t)i;
+            }
+    }
+    for (size_t stride = 128; stride > 0; stride >>= 1)
+        for (size_t t = 0; t < stride; ++t)
+            if (bv[t + stride] > bv[t]) {
+                bv[t] = bv[t + stride];
+                bi[t] = bi[t + stride];
+            }
+    return bi[0];
 }
 
 /* The reference's hard-coded scale: 1.0 / (hd as f32).sqrt()

@@ -453,20 +453,52 @@ def test_linear_identity_and_single_column_exact():
     assert np.array_equal(y[:, 0], x[:, 5]) and np.array_equal(y[:, 1], -2 * x[:, 7])
 
 
+def _bitrev8(t):
+    return int(f"{t:08b}"[::-1], 2)
+
+
+def _argmax_rule(x):
+    """The reference's argmax in closed form: among the indices holding the largest value
+    above -3e38 (NaN excluded), the one whose lane i mod 256 comes first in bit-reversed
+    order, then the smallest i; 0 if there is none. (Each lane keeps its first maximum.
+    In the tree, lane t sits at position t mod s before stride s; two lanes first meet at
+    the stride of their lowest differing bit, and the one with that bit clear is on the
+    left, which keeps ties.)"""
+    x = np.asarray(x, np.float32)
+    ok = (x > np.float32(-3e38)) & ~np.isnan(x)
+    if not ok.any():
+        return 0
+    m = x[ok].max()
+    idx = np.nonzero(ok & (x == m))[0]
+    return int(min(idx, key=lambda i: (_bitrev8(i % 256), i)))
+
+
 def test_argmax_reference_case_and_ties():
-    """sampling.rs:62-80 (vocab 1000, sin ramp, unique max at 731); ties go to the first
-    index; NaN never wins; an all -inf vector gives 0."""
+    """sampling.rs:62-80 (vocab 1000, sin ramp, unique max at 731); ties across lanes go
+    by the tree (index 256, lane 0, beats index 1; lane 116 beats lane 44); NaN and -inf
+    never win."""
     v = np.sin(np.arange(1000, dtype=np.float32) * np.float32(0.001)).astype(np.float32)
     v[731] = 5.0
     assert oracle.argmax(v) == 731
     assert oracle.argmax(np.array([1, 7, 3, 7], np.float32)) == 1
+    t = np.zeros(600, np.float32)
+    t[1] = t[256] = t[513] = 2.0
+    assert oracle.argmax(t) == 256
+    t = np.zeros(300, np.float32)
+    t[44] = t[116] = 1.0
+    assert oracle.argmax(t) == 116
     assert oracle.argmax(np.array([np.nan, 2, np.nan, 1], np.float32)) == 1
     assert oracle.argmax(np.full(5, -np.inf, np.float32)) == 0
-    r = oracle.randn((100000,), 4)
+    assert oracle.argmax(np.array([-3.1e38, -3.3e38], np.float32)) == 0
+    for seed in range(20):
+        r = oracle.randn((3000,), seed)
+        r = np.round(r * 2) / 2  # many ties
+        if seed % 3 == 0:
+            r[seed::7] = np.nan
+        assert oracle.argmax(r) == _argmax_rule(r)
+    r = oracle.randn((151936,), 99)
     assert oracle.argmax(r) == int(np.argmax(r))
 
-
-# ------------------------------------------------------------------ mutation test ----------
 
 def _planted(plant, td):
     src = os.path.join(os.path.dirname(oracle.__file__), "oracle.c")
