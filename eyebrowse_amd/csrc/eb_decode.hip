@@ -153,7 +153,56 @@ struct DecodeArgs {
     float *part_ml;    // [nsplit, h, 2]
     int h, hkv, g, keys, nsplit;
     float scale_log2;
+    // Optional prologue (the step of Attention::decode between the projections and the
+    // attention, attention.rs:133-168): per-head RMSNorm of q / knew / vnew with these
+    // gains (null: no norm), then RoPE of q and knew at table row rope_row (null tables:
+    // no RoPE). With it, the new row is written from the processed knew / vnew.
+    bool prologue;
+    const float *qn_w, *kn_w, *vn_w;
+    float eps;
+    const float *rcos, *rsin;  // [max_seq, HD/2]
+    int rope_row;
 };
+
+// RMSNorm of one head held in a lane group's units (attention.rs:62-73 via
+// kernels/src/rmsnorm.rs:6-38): y = x * (1/sqrt(sum x^2 / HD + eps)) * w.
+template <int HD, bool H16, int NV4, int LPK>
+__device__ __forceinline__ void norm_units(f32x4 (&u)[NV4], const float *__restrict__ w,
+                                           float eps, int ls) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) ss += (u[i].x * u[i].x + u[i].y * u[i].y) +
+                                       (u[i].z * u[i].z + u[i].w * u[i].w);
+    ss = eb::group_sum<LPK>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int i = 0; i < NV4; ++i)
+        u[i] = u[i] * inv * *reinterpret_cast<const f32x4 *>(w + dim_of<HD, H16>(i, ls));
+}
+
+// RoPE of one head (kernels/src/rope.rs:6-32): dims p and p + HD/2 rotate by the table
+// row's angle p. In the lane layout, unit i + NV4/2 holds the partners of unit i's dims
+// (both cache layouts), so each lane rotates its own units.
+template <int HD, bool H16, int NV4>
+__device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restrict__ cs,
+                                           const float *__restrict__ sn, int ls) {
+    if constexpr (NV4 == 1) {  // HD 4: pairs (0, 2) and (1, 3) inside the unit
+        const float c0 = cs[0], c1 = cs[1], s0 = sn[0], s1 = sn[1];
+        const f32x4 x = u[0];
+        u[0] = f32x4{x.x * c0 - x.z * s0, x.y * c1 - x.w * s1, x.z * c0 + x.x * s0,
+                     x.w * c1 + x.y * s1};
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV4 / 2; ++i) {
+            const int d = dim_of<HD, H16>(i, ls);
+            const f32x4 c = *reinterpret_cast<const f32x4 *>(cs + d);
+            const f32x4 sv = *reinterpret_cast<const f32x4 *>(sn + d);
+            const f32x4 x1 = u[i], x2 = u[i + NV4 / 2];
+            u[i] = x1 * c - x2 * sv;
+            u[i + NV4 / 2] = x2 * c + x1 * sv;
+        }
+    }
+}
 
 // H16: the caches hold IEEE half elements (converted to f32 as they are loaded).
 template <int HD, int G, bool H16>
@@ -190,8 +239,9 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     const int row_bytes = a.hkv * HD * EB;
 
     // New-token write: one workgroup per KV head copies the row into the cache. No
-    // workgroup reads cache row `pos` in this launch.
-    if (tail_new && (col % nsub) == 0) {
+    // workgroup reads cache row `pos` in this launch. (With the prologue the row is
+    // written after its norm and RoPE, from the tail fold below.)
+    if (tail_new && (col % nsub) == 0 && !a.prologue) {
         const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
         for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
             const f32x4 kx = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
@@ -215,6 +265,16 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         for (int i = 0; i < NV4; ++i)
             qr[gi][i] = *reinterpret_cast<const f32x4 *>(a.q + (size_t)(head0 + gi) * HD +
                                                          dim_of<HD, H16>(i, ls));
+
+    if (a.prologue) {
+        const float *cs = a.rcos ? a.rcos + (size_t)a.rope_row * (HD / 2) : nullptr;
+        const float *sn = a.rsin ? a.rsin + (size_t)a.rope_row * (HD / 2) : nullptr;
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            if (a.qn_w) norm_units<HD, H16, NV4, S::LPK>(qr[gi], a.qn_w, a.eps, ls);
+            if (cs) rope_units<HD, H16, NV4>(qr[gi], cs, sn, ls);
+        }
+    }
 
     float m[G], l[G];
     f32x4 acc[G][NV4];
@@ -357,7 +417,33 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
                                                      dim_of<HD, H16>(i, ls));
             vn[i] = *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD +
                                                      dim_of<HD, H16>(i, ls));
-            if constexpr (H16) {  // the value the cache row now holds
+        }
+        if (a.prologue) {
+            if (a.kn_w) norm_units<HD, H16, NV4, S::LPK>(kn, a.kn_w, a.eps, ls);
+            if (a.vn_w) norm_units<HD, H16, NV4, S::LPK>(vn, a.vn_w, a.eps, ls);
+            if (a.rcos)
+                rope_units<HD, H16, NV4>(kn, a.rcos + (size_t)a.rope_row * (HD / 2),
+                                         a.rsin + (size_t)a.rope_row * (HD / 2), ls);
+            if ((col % nsub) == 0 && kg == 0) {  // the new cache row, one lane group
+                const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
+#pragma unroll
+                for (int i = 0; i < NV4; ++i) {
+                    const int d = dim_of<HD, H16>(i, ls);
+                    if constexpr (H16) {
+                        *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.kc_w) + dst + d) =
+                            __builtin_convertvector(kn[i], f16x4);
+                        *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.vc_w) + dst + d) =
+                            __builtin_convertvector(vn[i], f16x4);
+                    } else {
+                        *reinterpret_cast<f32x4 *>(static_cast<float *>(a.kc_w) + dst + d) = kn[i];
+                        *reinterpret_cast<f32x4 *>(static_cast<float *>(a.vc_w) + dst + d) = vn[i];
+                    }
+                }
+            }
+        }
+        if constexpr (H16) {  // the value the cache row now holds
+#pragma unroll
+            for (int i = 0; i < NV4; ++i) {
                 kn[i] = through_f16(kn[i]);
                 vn[i] = through_f16(vn[i]);
             }
@@ -664,9 +750,11 @@ eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc,
                                  void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                  float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                                  float scale, float *ws, size_t ws_floats, int cu_count,
-                                 size_t window, bool h16) {
+                                 size_t window, bool h16, const DecodePrologue *pro) {
     if (h16 && hd < 8)
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
+    if (pro && !knew) return fail(EB_OTHER, "attn_decode: the prologue needs the new rows");
+    const size_t rope_row = pos;  // absolute position, before any window shift
     // A window is a shift of the cache view: keys first..=pos become keys 0..=pos-first of
     // caches based at row `first` (the fused write then lands on the same absolute row).
     if (window > 0 && pos + 1 > window) {
@@ -707,6 +795,24 @@ eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc,
     a.keys = (int)(pos + 1);
     a.nsplit = p.nsplit;
     a.scale_log2 = scale * kLog2e;
+    if (pro) {
+        a.prologue = true;
+        a.qn_w = pro->q_norm;
+        a.kn_w = pro->k_norm;
+        a.vn_w = pro->v_norm;
+        a.eps = pro->eps;
+        a.rcos = pro->rope_cos;
+        a.rsin = pro->rope_sin;
+        a.rope_row = (int)rope_row;
+        const float *ptrs[5] = {pro->q_norm, pro->k_norm, pro->v_norm, pro->rope_cos,
+                                pro->rope_sin};
+        for (const float *pp : ptrs)
+            if (reinterpret_cast<uintptr_t>(pp) & 15)
+                return fail(EB_UNSUPPORTED_CONFIG,
+                            "attn_decode: norm gains and RoPE tables must be 16-byte aligned");
+        if ((pro->rope_cos == nullptr) != (pro->rope_sin == nullptr))
+            return fail(EB_OTHER, "attn_decode: RoPE needs both tables");
+    }
     if (!attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);
     const hipError_t e = h16 ? launch_elem<true>(st, hd, p, a) : launch_elem<false>(st, hd, p, a);
@@ -720,7 +826,7 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              float scale, float *ws, size_t ws_floats, int cu_count,
                              size_t window) {
     return launch_attn_decode_any(st, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv, pos, hd,
-                                  scale, ws, ws_floats, cu_count, window, false);
+                                  scale, ws, ws_floats, cu_count, window, false, nullptr);
 }
 
 }  // namespace eb

@@ -70,11 +70,20 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              size_t window = 0);
 // The same over caches of f32 (h16 false) or IEEE half (h16 true) elements; f16 caches
 // need head_dim >= 8.
+// The part of Attention::decode between the projections and the attention, done inside
+// the fused step: per-head RMSNorm of q, knew, vnew (null gains: none) and RoPE of q and
+// knew at the step's absolute position (null tables: none). Gains [hd], tables
+// [max_seq, hd/2], 16-byte aligned.
+struct DecodePrologue {
+    const float *q_norm, *k_norm, *v_norm;
+    float eps;
+    const float *rope_cos, *rope_sin;
+};
 eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc, const void *vc,
                                  void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                  float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                                  float scale, float *ws, size_t ws_floats, int cu_count,
-                                 size_t window, bool h16);
+                                 size_t window, bool h16, const DecodePrologue *pro = nullptr);
 // kv_write into an IEEE-half cache: src f32 rows rounded to nearest even.
 eb_status launch_kv_write_f16(hipStream_t st, uint16_t *cache, const float *src, size_t hkv,
                               size_t count, size_t hd, size_t dst_start);
@@ -83,6 +92,16 @@ eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const ui
                                         const uint16_t *vc, float *o, size_t h, size_t hkv,
                                         size_t pos0, size_t rows, size_t hd, float scale,
                                         size_t window);
+// Attention::decode after the projections as one fused step: RMSNorm (null gains: none)
+// and RoPE (null tables: none) of q and the new K row, RMSNorm of the new V row, the
+// cache-row write and the attention. Handle-level, used by eb_attention_forward_qkv.
+eb_status attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
+                                 const eb_tensor *vnew, eb_tensor *kcache, eb_tensor *vcache,
+                                 eb_tensor *o, size_t h, size_t hkv, size_t pos, size_t hd,
+                                 size_t max_seq, float scale, size_t window,
+                                 const eb_tensor *q_norm, const eb_tensor *k_norm,
+                                 const eb_tensor *v_norm, float eps, const eb_tensor *rope_cos,
+                                 const eb_tensor *rope_sin);
 // linear_f16w: y[i][m, o] = sum_k x[m, k] * w[i][o, k] for nseg (1..kLinearMaxSegs)
 // weight/output pairs sharing x; w IEEE half [out_f[i], in_f]. m <= kLinearGemvRows runs
 // the weight-streaming kernel; more rows run the split-f16 matrix-core GEMM, which needs

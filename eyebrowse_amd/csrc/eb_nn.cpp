@@ -259,6 +259,20 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
         eb_tensor_numel(v) != rows * Hkv * hd)
         return fail(EB_SHAPE_MISMATCH, "attention_forward: q/k/v are not [rows, heads*head_dim]");
 
+    if (rows == 1) {
+        // attention.rs:133-183 after the projections: q/k/v norms, RoPE at pos, kv_write
+        // of K and V, attn_decode; all of it inside the fused decode step.
+        const size_t oshape1[2] = {1, H * hd};
+        eb_tensor *o1 = nullptr;
+        EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape1, 2, EB_F32, &o1));
+        Owned o(o1);
+        EB_TRY(eb::attn_decode_step_fused(rec, q, k, v, kc, vc, o.t, H, Hkv, base_pos, hd,
+                                          kv->max_seq, d.scale, d.window, d.q_norm, d.k_norm,
+                                          d.v_norm, d.norm_eps, rope->cos, rope->sin));
+        *out = o.release();
+        return eb::ok();
+    }
+
     Owned qn_h, kn_h, vn_h;
     const eb_tensor *qn = nullptr, *kn = nullptr, *vn = nullptr;
     EB_TRY(maybe_norm(rec, d.q_norm, q, rows * H, hd, d.norm_eps, qn_h, &qn));
@@ -275,23 +289,17 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
     eb_tensor *o_t = nullptr;
     EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape, 2, EB_F32, &o_t));
     Owned o(o_t);
-    if (rows == 1) {
-        // attention.rs:149-183: kv_write K and V at pos, then attn_decode, as one launch.
-        EB_TRY(eb_attn_decode_step_window(rec, qr.t, kr.t, vn, kc, vc, o.t, H, Hkv, base_pos, hd,
-                                          kv->max_seq, d.scale, d.window));
+    // attention.rs:78-97 writes the new rows' K (post-RoPE) and V into the cache.
+    EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
+    EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
+    if (base_pos == 0 && d.window == 0 && eb_tensor_dtype(kc) == EB_F32) {
+        // attention.rs:104-115 (routing rule :40): a prompt attends its fresh kr / v.
+        EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
     } else {
-        // attention.rs:78-97 writes the new rows' K (post-RoPE) and V into the cache.
-        EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
-        EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
-        if (base_pos == 0 && d.window == 0 && eb_tensor_dtype(kc) == EB_F32) {
-            // attention.rs:104-115 (routing rule :40): a prompt attends its fresh kr / v.
-            EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
-        } else {
-            // A continuation chunk, a windowed prompt, or any prompt over an f16 cache
-            // (so that prompt and decode read the same rounded K/V) attends the cache.
-            EB_TRY(eb_attn_prefill_chunk(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, rows, hd,
-                                         kv->max_seq, d.scale, d.window));
-        }
+        // A continuation chunk, a windowed prompt, or any prompt over an f16 cache
+        // (so that prompt and decode read the same rounded K/V) attends the cache.
+        EB_TRY(eb_attn_prefill_chunk(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, rows, hd,
+                                     kv->max_seq, d.scale, d.window));
     }
     *out = o.release();
     return eb::ok();

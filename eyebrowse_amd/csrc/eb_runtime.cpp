@@ -744,12 +744,13 @@ static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
 static eb_status device_decode(eb_device *dev, const float *q, const void *kc, const void *vc,
                                void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                               float scale, size_t window = 0, bool h16 = false) {
+                               float scale, size_t window = 0, bool h16 = false,
+                               const eb::DecodePrologue *pro = nullptr) {
     size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
     float *ws = nullptr;
     if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
     EB_TRY(eb::launch_attn_decode_any(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv,
-                                      pos, hd, scale, ws, wsn, dev->cu_count, window, h16));
+                                      pos, hd, scale, ws, wsn, dev->cu_count, window, h16, pro));
     return eb::ok();
 }
 
@@ -929,6 +930,61 @@ eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const
                          vcache->ptr, (const float *)knew->ptr, (const float *)vnew->ptr,
                          (float *)o->ptr, h, hkv, pos, hd, scale, window, h16);
 }
+
+}  // extern "C"
+
+// Attention::decode's post-projection part in one fused step (see DecodePrologue):
+// q [h, hd], knew / vnew [hkv, hd] straight from the projections.
+eb_status eb::attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q,
+                                     const eb_tensor *knew, const eb_tensor *vnew,
+                                     eb_tensor *kcache, eb_tensor *vcache, eb_tensor *o,
+                                     size_t h, size_t hkv, size_t pos, size_t hd,
+                                     size_t max_seq, float scale, size_t window,
+                                     const eb_tensor *q_norm, const eb_tensor *k_norm,
+                                     const eb_tensor *v_norm, float eps,
+                                     const eb_tensor *rope_cos, const eb_tensor *rope_sin) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(knew, "knew", rec->dev));
+    EB_TRY(tensor_f32(vnew, "vnew", rec->dev));
+    bool h16 = false;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q), kcache->ptr,
+                                eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache),
+                                (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
+                                max_seq, h16));
+    size_t nn = eb_tensor_numel(knew) < eb_tensor_numel(vnew) ? eb_tensor_numel(knew)
+                                                              : eb_tensor_numel(vnew);
+    EB_TRY(step_rows_checked((const float *)knew->ptr, (const float *)vnew->ptr, nn, hkv, hd));
+    eb::DecodePrologue pro{};
+    pro.eps = eps;
+    const eb_tensor *norms[3] = {q_norm, k_norm, v_norm};
+    const float **slots[3] = {&pro.q_norm, &pro.k_norm, &pro.v_norm};
+    for (int i = 0; i < 3; ++i) {
+        if (!norms[i]) continue;
+        EB_TRY(tensor_f32(norms[i], "norm gain", rec->dev));
+        if (eb_tensor_numel(norms[i]) != hd)
+            return fail(EB_SHAPE_MISMATCH, "norm gain holds %zu, head_dim is %zu",
+                        eb_tensor_numel(norms[i]), hd);
+        *slots[i] = (const float *)norms[i]->ptr;
+    }
+    if ((rope_cos == nullptr) != (rope_sin == nullptr))
+        return fail(EB_OTHER, "RoPE needs both tables");
+    if (rope_cos) {
+        EB_TRY(tensor_f32(rope_cos, "rope cos", rec->dev));
+        EB_TRY(tensor_f32(rope_sin, "rope sin", rec->dev));
+        EB_TRY(eb::check_numel(eb_tensor_numel(rope_cos), (pos + 1) * (hd / 2), "rope cos"));
+        EB_TRY(eb::check_numel(eb_tensor_numel(rope_sin), (pos + 1) * (hd / 2), "rope sin"));
+        pro.rope_cos = (const float *)rope_cos->ptr;
+        pro.rope_sin = (const float *)rope_sin->ptr;
+    }
+    return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, kcache->ptr,
+                         vcache->ptr, (const float *)knew->ptr, (const float *)vnew->ptr,
+                         (float *)o->ptr, h, hkv, pos, hd, scale, window, h16, &pro);
+}
+
+extern "C" {
 
 eb_status eb_rmsnorm(eb_recorder *rec, const eb_tensor *x, const eb_tensor *weight,
                      eb_tensor *out, size_t rows, size_t dim, float eps) {

@@ -181,10 +181,11 @@ def test_prefill_decode_consistency(dev):
         rec.submit()
         last = out.to_f32()
     assert rel_l2_f64(last, pre_out[seq - 1]) < 2e-5
-    # both caches hold the same rows 0..seq-1
-    # (same per-element RoPE arithmetic at the same positions, so bit-identical)
-    assert_bitwise(kv_p.k[0].to_f32()[: seq * Hkv * hd], kv_d.k[0].to_f32()[: seq * Hkv * hd],
-                   "prefill vs decode cache rows")
+    # both caches hold the same rows 0..seq-1 up to the norm's summation order (the decode
+    # step folds RMSNorm and RoPE into its own kernel)
+    n = seq * Hkv * hd
+    assert rel_l2_f64(kv_d.k[0].to_f32()[:n], kv_p.k[0].to_f32()[:n]) < 1e-6
+    assert_bitwise(kv_d.v[0].to_f32()[:n], kv_p.v[0].to_f32()[:n], "V rows (no norm here)")
 
 
 def test_gemma_attention_forward(dev):
