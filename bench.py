@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 METRIC = "prefill attn TFLOP/s + decode KV-read GB/s, as % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix
+F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix
 MALL_BYTES = 256 << 20
 
 
@@ -306,6 +307,102 @@ def prefill_extras(eb, hip, dev, sc128) -> dict:
     return out
 
 
+def projection_extras(eb, hip, dev) -> dict:
+    """linear_f16w (the projections around attention): the weight-streaming kernel on the
+    Qwen3 LM head (151936 x 1024 halves, 311 MB, beyond the Infinity Cache: GB/s of
+    weight), and the split-f16 matrix-core GEMM on prompt-sized projections (TFLOP/s of
+    2*m*in*out algorithmic FLOPs)."""
+    rng = np.random.default_rng(3)
+    out = {}
+
+    def bench_one(name, m, k, outs, reps):
+        x = eb.Tensor.from_f32(dev, (m, k), randn(rng, (m, k)))
+        ws = [eb.Tensor.from_f16_packed(dev, (o, k), randn(rng, (o, k)) * 0.05) for o in outs]
+        cs = [eb.Tensor.empty(dev, (m, o)) for o in outs]
+        need = eb.linear_workspace_floats(m, k)
+        wsp = eb.Tensor.empty(dev, (max(need, 1),))
+
+        def launch(_i):
+            if len(outs) == 1:
+                eb.launch_linear_f16w(dev.stream, x.data_ptr, x.numel(), ws[0].data_ptr,
+                                      2 * ws[0].numel(), cs[0].data_ptr, cs[0].numel(), m, k,
+                                      outs[0], wsp.data_ptr, need)
+            else:
+                rec = eb.Recorder(dev)
+                eb.linear_f16w_multi(rec, x, ws, cs, outs, m, k)
+                rec.submit()
+        for _ in range(3):
+            launch(0)
+        t = hip.time_loop(dev.stream, reps, launch)
+        flops = 2.0 * m * k * sum(outs)
+        wbytes = 2.0 * k * sum(outs)
+        r = {"m": m, "in": k, "out": list(outs), "ms": round(t, 5)}
+        if m <= 8:
+            r["GBs_weight"] = round(wbytes / t / 1e6, 1)
+            r["frac_hbm"] = round(wbytes / t / 1e6 / HBM_PEAK_GBS, 4)
+        else:
+            r["TFLOPs"] = round(flops / t / 1e9, 1)
+            # two f16 MFMAs (x_hi*w, x_lo*w) per algorithmic multiply-add
+            r["frac_f16_mfma_peak_of_mfma_work"] = round(2 * flops / t / 1e9 / F16_MFMA_PEAK_TFLOPS, 4)
+        out[f"linear_{name}"] = r
+        dev.synchronize()
+
+    bench_one("qwen_lm_head_m1", 1, 1024, (151936,), 50)
+    bench_one("qwen_qkv_T4096", 4096, 1024, (2048, 1024, 1024), 10)
+    bench_one("qwen_o_T4096", 4096, 2048, (1024,), 10)
+    bench_one("mistral_qkv_T4096", 4096, 4096, (4096, 1024, 1024), 5)
+    return out
+
+
+def layer_step_extras(eb, hip, dev) -> dict:
+    """One Qwen3-width attention layer decode step at pos 100 (fused q/k/v projection,
+    decode step with QK-norm and RoPE folded in, o_proj, a 4096-row LM head, argmax):
+    microseconds per step, recorded eagerly and replayed as a captured HIP graph."""
+    H, Hkv, hd, hidden, vocab, max_seq, pos = 16, 8, 128, 1024, 4096, 256, 100
+    rng = np.random.default_rng(4)
+    w = {n: eb.Tensor.from_f16_packed(dev, sh, randn(rng, sh) * 0.03)
+         for n, sh in (("q", (H * hd, hidden)), ("k", (Hkv * hd, hidden)),
+                       ("v", (Hkv * hd, hidden)), ("o", (hidden, H * hd)), ("lm", (vocab, hidden)))}
+    gq = eb.Tensor.from_f32(dev, (hd,), 1 + 0.1 * randn(rng, (hd,)))
+    gk = eb.Tensor.from_f32(dev, (hd,), 1 + 0.1 * randn(rng, (hd,)))
+    attn = eb.Attention(H, Hkv, hd, float(hd ** -0.5), q_norm=gq, k_norm=gk, q_proj=w["q"],
+                        k_proj=w["k"], v_proj=w["v"], o_proj=w["o"], hidden=hidden)
+    rope = eb.Rope.build(dev, max_seq, hd, 1e6)
+    kv = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    rec = eb.Recorder(dev)
+    attn.forward(rec, eb.Tensor.from_f32(dev, (pos, hidden), randn(rng, (pos, hidden))), rope,
+                 kv, 0, pos, 0)
+    rec.submit()
+    x = eb.Tensor.from_f32(dev, (1, hidden), randn(rng, (1, hidden)))
+
+    def step():
+        r = eb.Recorder(dev)
+        y = attn.forward(r, x, rope, kv, 0, 1, pos)
+        logits = eb.Tensor.empty(dev, (1, vocab))
+        eb.linear_f16w(r, y, w["lm"], logits, 1, hidden, vocab)
+        idx = eb.Tensor.empty(dev, (1,), eb.DType.U32)
+        eb.argmax(r, logits, idx, vocab)
+        r.submit()
+        return y, logits, idx
+
+    for _ in range(5):
+        step()
+    eager = hip.time_loop(dev.stream, 200, lambda i: step())
+    dev.begin_capture()
+    try:
+        keep = step()
+    finally:
+        g = dev.end_capture()
+    for _ in range(5):
+        g.launch()
+    graph = hip.time_loop(dev.stream, 200, lambda i: g.launch())
+    dev.synchronize()
+    g.release()
+    del keep
+    return {"layer_decode_step_qwen_pos100": {
+        "kernels": 7, "eager_us": round(eager * 1e3, 2), "graph_us": round(graph * 1e3, 2)}}
+
+
 def traffic_run(eb, hip, dev, sc128):
     """Dispatches for the HBM-traffic counter passes, each kernel launched directly (no
     graph) so that every dispatch is counted on its own:
@@ -433,6 +530,8 @@ def main():
     if args.only == "all":
         extra.update(decode_extras(eb, hip, dev, sc128))
         extra.update(prefill_extras(eb, hip, dev, sc128))
+        extra.update(projection_extras(eb, hip, dev))
+        extra.update(layer_step_extras(eb, hip, dev))
 
     line = {
         "metric": METRIC,

@@ -190,46 +190,64 @@ __global__ __launch_bounds__(kThreads) void linear_row_scale_kernel(const float 
 }
 
 constexpr int kBM = 128;  // x rows per workgroup tile
-constexpr int kBN = 128;  // output features per workgroup tile
 #ifndef EB_LINEAR_BK
 #define EB_LINEAR_BK 32
 #endif
 constexpr int kBK = EB_LINEAR_BK;  // contraction per LDS stage
 constexpr int kLdsRow = kBK + 8;  // halves per LDS row (16-byte pad against bank conflicts)
-constexpr int kTileHalves = kBM * kLdsRow;
-constexpr size_t kGemmLdsBytes = 2 /*buffers*/ * 3 /*hi, lo, w*/ * kTileHalves * 2;
-static_assert(kBM == kBN, "one LDS tile shape for x and w");
+constexpr int kXcds = 8;  // MI355X: workgroup ids are dealt round-robin to 8 XCDs
+
+template <int WNB>
+struct GemmShape {
+    static constexpr int BN = 64 * WNB;  // features per workgroup tile
+    static constexpr int BUF = (2 * kBM + BN) * kLdsRow;  // halves: x_hi, x_lo, w
+};
+template <int WNB, int NBUF>
+constexpr size_t gemm_lds_bytes() {
+    return (size_t)NBUF * GemmShape<WNB>::BUF * 2;
+}
 
 __device__ __forceinline__ floatx16 mfma16(f16x8 a, f16x8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Requires in % 8 == 0 and 16-byte aligned x and w. Tile t of the grid: m-tile t / ntn,
-// n-unit t % ntn (n-units numbered pair by pair).
-__global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__restrict__ x,
+// Requires in % 8 == 0 and 16-byte aligned x and w. Tile t: m-tile t / ntn, n-unit
+// t % ntn (n-units numbered pair by pair). Workgroup ids are remapped so that each XCD
+// works on a contiguous range of tiles (the same x rows), which its own L2 then keeps.
+// WNB: 32-feature blocks per wave (the workgroup tile is 128 rows x 64*WNB features);
+// NBUF: LDS buffers per stage (2: double buffered, one barrier per stage; 1: two
+// barriers, half the LDS); MINB: workgroups per CU the registers must allow.
+template <int WNB, int NBUF, int MINB>
+__global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float *__restrict__ x,
                                                                const float *__restrict__ ex,
                                                                LinearSegs s, int M, int K) {
+    using Sh = GemmShape<WNB>;
+    constexpr int BN = Sh::BN;
     extern __shared__ _Float16 lds[];
+    __shared__ int s_ex[kBM];  // row exponents of the tile (read by the epilogue)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int nt = gridDim.x;
+    const int bid = blockIdx.x;
+    const int full = (nt / kXcds) * kXcds;
+    const int t = bid < full ? (bid % kXcds) * (nt / kXcds) + bid / kXcds : bid;
     const int ntn = s.first[s.nseg];
-    const int mt = blockIdx.x / ntn;
-    const int nu = blockIdx.x % ntn;
+    const int mt = t / ntn;
+    const int nu = t % ntn;
     const int sg = seg_of(s, nu);
     const int N = s.n[sg];
     const int m0 = mt * kBM;
-    const int n0 = (nu - s.first[sg]) * kBN;
+    const int n0 = (nu - s.first[sg]) * BN;
     const _Float16 *w = s.w[sg];
+    if (tid < kBM) s_ex[tid] = (int)ex[min(m0 + tid, M - 1)];
 
-    // Staging assignment: x tile 128 x kBK f32 (NX f32x4 per thread); w tile 128 x kBK
+    // Staging assignment: x tile kBM x kBK f32 (NX f32x4 per thread); w tile BN x kBK
     // halves (NW f16x8 per thread).
     constexpr int X4 = kBK / 4, W8 = kBK / 8;  // vectors per tile row
-    constexpr int NX = kBM * X4 / kThreads, NW = kBN * W8 / kThreads;
+    constexpr int NX = kBM * X4 / kThreads, NW = BN * W8 / kThreads;
     f32x4 rx[NX];
     f16x8 rw[NW];
-    __shared__ int s_ex[kBM];  // row exponents of the tile (read by the epilogue)
-    if (tid < kBM) s_ex[tid] = (int)ex[min(m0 + tid, M - 1)];
     int rs[NX];  // -e of the row each staged f32x4 belongs to
 #pragma unroll
     for (int j = 0; j < NX; ++j) {
@@ -260,9 +278,9 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
         }
     };
     auto store_stage = [&](int buf) {
-        _Float16 *hi = lds + buf * 3 * kTileHalves;
-        _Float16 *lo = hi + kTileHalves;
-        _Float16 *wt = lo + kTileHalves;
+        _Float16 *hi = lds + buf * Sh::BUF;
+        _Float16 *lo = hi + kBM * kLdsRow;
+        _Float16 *wt = lo + kBM * kLdsRow;
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
             const int idx = tid + j * kThreads;
@@ -282,29 +300,23 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
         }
     };
 
-    // Wave (wm, wn) computes rows wm*64..+64 and features wn*64..+64 of the tile: 2 x 2
-    // blocks of 32 x 32.
+    // Wave (wm, wn) computes rows wm*64..+64 and features wn*32*WNB..+32*WNB of the tile:
+    // 2 x WNB blocks of 32 x 32.
     const int wm = wave >> 1, wn = wave & 1;
-    floatx16 acc[2][2];
+    floatx16 acc[2][WNB];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = floatx16{};
+        for (int b = 0; b < WNB; ++b) acc[a][b] = floatx16{};
 
-    const int nst = (K + kBK - 1) / kBK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int st = 0; st < nst; ++st) {
-        const int buf = st & 1;
-        if (st + 1 < nst) load_stage((st + 1) * kBK);
-        const _Float16 *hi = lds + buf * 3 * kTileHalves;
-        const _Float16 *lo = hi + kTileHalves;
-        const _Float16 *wt = lo + kTileHalves;
+    auto compute = [&](int buf) {
+        const _Float16 *hi = lds + buf * Sh::BUF;
+        const _Float16 *lo = hi + kBM * kLdsRow;
+        const _Float16 *wt = lo + kBM * kLdsRow;
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
             const int kof = kk * 16 + (lane >> 5) * 8;
-            f16x8 ah[2], al[2], bw[2];
+            f16x8 ah[2], al[2], bw[WNB];
 #pragma unroll
             for (int a = 0; a < 2; ++a) {
                 const int r = wm * 64 + a * 32 + (lane & 31);
@@ -312,20 +324,38 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
                 al[a] = *reinterpret_cast<const f16x8 *>(lo + r * kLdsRow + kof);
             }
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                const int r = wn * 64 + b * 32 + (lane & 31);
+            for (int b = 0; b < WNB; ++b) {
+                const int r = wn * 32 * WNB + b * 32 + (lane & 31);
                 bw[b] = *reinterpret_cast<const f16x8 *>(wt + r * kLdsRow + kof);
             }
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
+                for (int b = 0; b < WNB; ++b) {
                     acc[a][b] = mfma16(ah[a], bw[b], acc[a][b]);
                     acc[a][b] = mfma16(al[a], bw[b], acc[a][b]);
                 }
         }
-        if (st + 1 < nst) store_stage(buf ^ 1);
-        __syncthreads();
+    };
+
+    const int nst = (K + kBK - 1) / kBK;
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int st = 0; st < nst; ++st) {
+        if (st + 1 < nst) load_stage((st + 1) * kBK);
+        if constexpr (NBUF == 2) {
+            compute(st & 1);
+            if (st + 1 < nst) store_stage((st & 1) ^ 1);
+            __syncthreads();
+        } else {
+            compute(0);
+            if (st + 1 < nst) {
+                __syncthreads();  // every wave is done reading the buffer
+                store_stage(0);
+                __syncthreads();
+            }
+        }
     }
 
     // Epilogue: lane holds feature j = lane % 32 of each block, rows
@@ -334,8 +364,8 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int o = n0 + wn * 64 + b * 32 + (lane & 31);
+        for (int b = 0; b < WNB; ++b) {
+            const int o = n0 + wn * 32 * WNB + b * 32 + (lane & 31);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int rt = wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -343,6 +373,45 @@ __global__ __launch_bounds__(kThreads) void linear_gemm_kernel(const float *__re
                 if (row < M && o < N) y[(size_t)row * N + o] = ldexpf(acc[a][b][r], s_ex[rt]);
             }
         }
+}
+
+// CUs of the current device (cached per device ordinal).
+int current_cu_count() {
+    static std::mutex mu;
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    if (cache[dev] == 0) {
+        int n = 0;
+        cache[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                          hipSuccess && n > 0)
+                         ? n
+                         : 256;
+    }
+    return cache[dev];
+}
+
+template <int WNB, int NBUF, int MINB>
+eb_status launch_gemm(hipStream_t st, const float *x, const float *ex, LinearSegs s,
+                      const size_t *out_f, int nseg, size_t m, size_t in_f) {
+    constexpr int BN = GemmShape<WNB>::BN;
+    constexpr size_t lds_bytes = gemm_lds_bytes<WNB, NBUF>();
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(once, [] {
+        attr_err = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&linear_gemm_kernel<WNB, NBUF, MINB>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+    });
+    if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(linear)");
+    s.first[0] = 0;
+    for (int i = 0; i < nseg; ++i)
+        s.first[i + 1] = s.first[i] + (int)((out_f[i] + BN - 1) / BN);
+    const size_t tiles = (size_t)((m + kBM - 1) / kBM) * (size_t)s.first[nseg];
+    linear_gemm_kernel<WNB, NBUF, MINB><<<(unsigned)tiles, kThreads, lds_bytes, st>>>(
+        x, ex, s, (int)m, (int)in_f);
+    return eb::check_launch("linear_f16w");
 }
 
 __global__ __launch_bounds__(kThreads) void zero_fill_kernel(float *__restrict__ y, size_t n) {
@@ -411,23 +480,17 @@ eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_
         return check_launch("linear_f16w");
     }
     if (ws == nullptr || ws_floats < m) return fail(EB_SHAPE_MISMATCH, "linear: workspace too small");
-    static std::once_flag once;
-    static hipError_t attr_err = hipSuccess;
-    std::call_once(once, [] {
-        attr_err = hipFuncSetAttribute(reinterpret_cast<const void *>(&linear_gemm_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kGemmLdsBytes);
-    });
-    if (attr_err != hipSuccess) return hip_fail(attr_err, "hipFuncSetAttribute(linear)");
     linear_row_scale_kernel<<<(unsigned)((m + kWaves - 1) / kWaves), kThreads, 0, st>>>(
         x, ws, (int)m, (int)in_f);
-    s.first[0] = 0;
-    for (int i = 0; i < nseg; ++i)
-        s.first[i + 1] = s.first[i] + (int)((out_f[i] + kBN - 1) / kBN);
-    const size_t tiles = (size_t)((m + kBM - 1) / kBM) * (size_t)s.first[nseg];
-    linear_gemm_kernel<<<(unsigned)tiles, kThreads, kGemmLdsBytes, st>>>(x, ws, s, (int)m,
-                                                                         (int)in_f);
-    return check_launch("linear_f16w");
+    // Wide tiles (64 x 128 per wave: 0.5 LDS fragment reads per MFMA instead of 0.75) when
+    // they still give every CU two workgroups; otherwise 128 x 128 tiles, whose twice as
+    // many workgroups keep more of the chip busy.
+    const size_t mtiles = (m + kBM - 1) / kBM;
+    size_t wide_units = 0;
+    for (int i = 0; i < nseg; ++i) wide_units += (out_f[i] + GemmShape<4>::BN - 1) / GemmShape<4>::BN;
+    if (mtiles * wide_units >= 2 * (size_t)current_cu_count())
+        return launch_gemm<4, 1, 2>(st, x, ws, s, out_f, nseg, m, in_f);
+    return launch_gemm<2, 2, 1>(st, x, ws, s, out_f, nseg, m, in_f);
 }
 
 }  // namespace eb

@@ -197,3 +197,27 @@ def test_empty_and_invalid(dev):
     eb.linear_f16w(rec, x, w0, c2, 3, 0, 5)
     rec.submit()
     assert np.array_equal(c2.to_f32(), np.zeros(15, np.float32))
+
+
+@pytest.mark.parametrize("m,outs", [
+    (4096, (2048, 1024, 1024)),  # Qwen3 q/k/v at T=4096: wide 128 x 256 tiles
+    (2000, (4096, 2000, 4000)),  # ragged rows and features on the wide tiles
+])
+def test_wide_tile_gemm_sampled_rows(dev, m, outs):
+    """Grids with at least two wide tiles per CU take the 64 x 128-per-wave kernel; rows
+    sampled across the tiles (first, last, tile edges) against the oracle."""
+    note(f"linear wide gemm m={m} outs={outs}")
+    in_f = 1024
+    x = oracle.randn((m, in_f), 60)
+    ws = [oracle.randn((o, in_f), 61 + i) * 0.03 for i, o in enumerate(outs)]
+    xt = upload(dev, x)
+    wts = [eb.Tensor.from_f16_packed(dev, w.shape, w) for w in ws]
+    cs = [eb.Tensor.empty(dev, (m, o)) for o in outs]
+    rec = eb.Recorder(dev)
+    eb.linear_f16w_multi(rec, xt, wts, cs, outs, m, in_f)
+    rec.submit()
+    rows = sorted({0, 1, 127, 128, 129, m // 2, m - 129, m - 2, m - 1})
+    for i, o in enumerate(outs):
+        got = cs[i].to_f32().reshape(m, o)[rows]
+        want = oracle.linear_f16w(x[rows], oracle.f16_bits(ws[i]), len(rows), in_f, o, threads=16)
+        assert_close(got, want, what=f"projection {i}")
