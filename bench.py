@@ -243,6 +243,17 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     oracle.attn_prefill(pq, pk, pv, H, Hkv, T, hd, sc, rows=(T - rows, rows), threads=1)
     pdt = time.perf_counter() - t1
     pflops = sum(2.0 * 2 * H * hd * (i + 1) for i in range(T - rows, T))
+
+    # secondary: the same decode with the oracle's heads spread over the host's cores
+    # (16 at most: the GPU box's CPU share)
+    mt = max(1, min(16, os.cpu_count() or 1))
+    m, t2 = 0, time.perf_counter()
+    while True:
+        oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc, threads=mt)
+        m += 1
+        mdt = time.perf_counter() - t2
+        if mdt >= budget_s / 4:
+            break
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": f"oracle attn_decode, Qwen3 shape 16/8 heads hd128, 8192 keys, {n} calls "
@@ -251,6 +262,10 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
         "prefill_sample": f"oracle attn_prefill, Qwen3 T=4096, last {rows} rows, 1 thread, "
                           f"{pdt:.1f} s",
         "host_cpus": os.cpu_count(),
+        "all_cores_value": round(kv_bytes * m / mdt / 1e9, 3),
+        "all_cores": mt,
+        "all_cores_sample": f"the same decode, heads over {mt} OpenMP threads, {m} calls in "
+                            f"{mdt:.1f} s",
     }
 
 
@@ -439,17 +454,27 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
     import csv
     import re
 
+    copy = "kv_write_vec4_kernel"
+
     def load(path):
-        per = {}
-        for r in csv.DictReader(open(path)):
+        # The first three kv_write dispatches are the calibration copies; later ones (the
+        # decode workload filling its caches) are left out of every average.
+        per, calib = {}, []
+        rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
+        for r in rows:
             name = re.sub(r"\(anonymous namespace\)::", "", r["Kernel_Name"]).split("(")[0]
             name = name.replace("void ", "").strip()
+            if name == copy:
+                if len(calib) < 3:
+                    calib.append(float(r["Counter_Value"]))
+                continue
             per.setdefault(name, []).append(float(r["Counter_Value"]))
-        return {k: sum(v) / len(v) for k, v in per.items()}
+        avg = {k: sum(v) / len(v) for k, v in per.items()}
+        avg[copy] = sum(calib) / len(calib)
+        return avg
 
     fetch, write = load(fetch_csv), load(write_csv)
     copy_bytes = 65536 * 8 * 128 * 4
-    copy = "kv_write_vec4_kernel"
     fs = copy_bytes / (fetch[copy] * 1024)
     ws = copy_bytes / (write[copy] * 1024)
     kernels = {k: {"fetch_bytes": round(fetch[k] * 1024 * fs), "write_bytes": round(write.get(k, 0) * 1024 * ws),
@@ -462,10 +487,11 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
         "-d $R/gpurun_out/pmc_write -o run -- python3 $R/bench.py --only traffic",
         "python bench.py --pmc-summary gpurun_out/pmc_fetch/run_counter_collection.csv "
         "gpurun_out/pmc_write/run_counter_collection.csv profiles/traffic.json"],
-        "calibration": "kv_write_vec4_kernel copying 256 MiB (65536 rows x 8 heads x 128 f32): "
-                       "scale = 268435456 / (counter KiB * 1024)",
+        "calibration": "the run's first three kv_write_vec4_kernel dispatches, each copying "
+                       "256 MiB (65536 rows x 8 heads x 128 f32): scale = 268435456 / "
+                       "(counter KiB * 1024)",
         "fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": kernels}
-    dk = next((k for k in kernels if k.startswith("decode_kernel<128, 2>")), None)
+    dk = next((k for k in kernels if re.match(r"decode_kernel<128, 2\b", k)), None)
     mk = next((k for k in kernels if k.startswith("decode_merge_kernel<128>")), None)
     if dk:
         t = kernels[dk]["fetch_bytes"] + kernels[dk]["write_bytes"]
@@ -487,10 +513,11 @@ def main():
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
                     help="no GPU: turn the counter_collection.csv files of the FETCH_SIZE and "
                          "WRITE_SIZE passes over `--only traffic` into per-kernel HBM bytes")
-    ap.add_argument("--only", choices=["headline", "all", "prefill", "traffic"], default="all",
-                    help="headline: the decode line only; prefill: the prefill configs only "
-                         "(prints their timings, not the contract line); traffic: a short run "
-                         "for rocprofv3 --pmc passes")
+    ap.add_argument("--only", choices=["headline", "all", "prefill", "projections", "layer",
+                                       "traffic"], default="all",
+                    help="headline: the decode line only; prefill / projections / layer: "
+                         "only those extras (prints their timings, not the contract line); "
+                         "traffic: a short run for rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
@@ -510,6 +537,12 @@ def main():
         return
     if args.only == "prefill":
         print(json.dumps(prefill_extras(eb, hip, dev, sc128)), flush=True)
+        return
+    if args.only == "projections":
+        print(json.dumps(projection_extras(eb, hip, dev)), flush=True)
+        return
+    if args.only == "layer":
+        print(json.dumps(layer_step_extras(eb, hip, dev)), flush=True)
         return
 
     # Headline: Qwen decode L=8191. A step is one kernel (kv_write + split-KV attention +
@@ -555,7 +588,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<128,2> (new-token write + split-KV pass) + decode_merge_kernel<128>",
+            "kernel": "decode_kernel<128,2,false> (new-token write + split-KV pass) + decode_merge_kernel<128>",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": head.kv_bytes, "avg_launch_ms": round(ms_step, 6),
