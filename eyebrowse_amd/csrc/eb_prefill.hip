@@ -1,4 +1,4 @@
-// Causal GQA flash-attention prefill for gfx950 on FP32 matrix cores.
+// Causal GQA flash-attention prefill for gfx950 on the matrix cores.
 //
 // Replaces attn_prefill (crates/eyebrowse-kernels/src/attention.rs:10-50,94-120), which
 // runs one thread per (query row, head) and re-reads K/V from memory for every row.
@@ -13,8 +13,15 @@
 //  - Each step stages KSPLIT tiles of 32 keys (K and V) in LDS, double buffered: the next
 //    step is fetched into registers while the current one is in use.
 //  - Everything is computed transposed so that the query index sits on the lane:
-//      S^T[key][query] = K Q^T         (v_mfma_f32_32x32x2_f32, contraction over head_dim)
-//      O^T[d][query]  += V^T P^T       (same instruction, contraction over the 32 keys)
+//      S^T[key][query] = K Q^T         (contraction over head_dim)
+//      O^T[d][query]  += V^T P^T       (v_mfma_f32_32x32x2_f32, contraction over 32 keys)
+//  - S^T for head_dim >= 32 runs on the f16 matrix cores (v_mfma_f32_32x32x16_f16) at
+//    about f32 accuracy: every K row and every Q row is scaled by a power of two (its
+//    largest magnitude lands in [2^14, 2^15)) and split exactly into hi = f16(x') and
+//    lo = f16(x' - hi); K Q^T = hi*hi + hi*lo + lo*hi (lo*lo is below 2^-22 of the
+//    product), accumulated in f32, and each score is scaled back with ldexp by the
+//    key's and the query's exponents. Rows holding inf or NaN keep exponent 0 and pass
+//    them on. Smaller head dims use the FP32 instruction for S^T as well.
 //    The S^T accumulator holds, per lane, 16 keys of one query, which is exactly the B
 //    operand layout the PV product needs, so P never leaves registers, and the online
 //    softmax state (running max m, partial sum l) is a per-lane scalar.
@@ -42,11 +49,16 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // on it is lowered through a stack copy (scratch memory); this one stays in registers.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
 
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16 mfma16(f16x8 a, f16x8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT>
@@ -61,7 +73,10 @@ struct PrefillCfg {
     static constexpr int STEP_KEYS = kTile * KSPLIT;   // keys staged per step
     static constexpr int STEP_F4 = STEP_KEYS * HD / 4;  // float4 per K (or V) step
     static constexpr int NLD = (STEP_F4 + THREADS - 1) / THREADS;
-    static constexpr int BUF = STEP_KEYS * (KS + HD);  // floats per buffer: K rows, V rows
+    // head_dim >= 32: Q K^T on the f16 matrix cores with an exact hi/lo split (K rows and
+    // Q rows scaled by powers of two first); smaller head dims keep FP32 MFMA throughout.
+    static constexpr bool SQK = HD >= 32;
+    static constexpr int BUF = STEP_KEYS * (KS + HD + 1);  // floats: K rows, V rows, K exps
     static constexpr int REC = 2 + 16 * NB;            // merged fields per lane: m, l, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
     static constexpr int OS = HD + 4;                  // output staging row stride (floats)
@@ -106,6 +121,34 @@ __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
 
 // Write the staged rows into LDS buffer `buf`: K rows [STEP_KEYS][KS], then V rows
 // [STEP_KEYS][HD].
+// Largest value over aligned groups of N consecutive lanes (N a power of two, up to 64).
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+    if constexpr (N >= 2) x = fmaxf(x, eb::dpp<eb::kDppQuadXor1>(x));
+    if constexpr (N >= 4) x = fmaxf(x, eb::dpp<eb::kDppQuadXor2>(x));
+    if constexpr (N >= 8) x = fmaxf(x, eb::dpp<eb::kDppRowHalfMirror>(x));
+    if constexpr (N >= 16) x = fmaxf(x, eb::dpp<eb::kDppRowMirror>(x));
+    if constexpr (N >= 32) x = fmaxf(x, eb::lane_xor16(x));
+    if constexpr (N >= 64) x = fmaxf(x, eb::lane_xor32(x));
+    return x;
+}
+
+// The exponent e that brings a row whose largest magnitude is mx into [2^14, 2^15)
+// (0 for zero or non-finite rows, which then keep their inf / NaN).
+__device__ __forceinline__ int split_exponent(float mx) {
+    return (mx > 0.0f && mx <= 3.4028235e38f) ? ilogbf(mx) - 14 : 0;
+}
+
+// x' = x * 2^-e (exact), hi = f16(x'), lo = f16(x' - hi): x' = hi + lo to about 2^-22.
+__device__ __forceinline__ void split_f16(f32x4 x, int e, f16x4 &hi, f16x4 &lo) {
+    const f32x4 v = {ldexpf(x.x, -e), ldexpf(x.y, -e), ldexpf(x.z, -e), ldexpf(x.w, -e)};
+    hi = __builtin_convertvector(v, f16x4);
+    lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x4), f16x4);
+}
+
+// Write the staged rows into LDS buffer `buf`: K rows [STEP_KEYS][KS], then V rows
+// [STEP_KEYS][HD], then (SQK) the K rows' exponents [STEP_KEYS]. With SQK a K row holds
+// its HD halves of hi, then HD halves of lo (the same KS floats).
 template <class C>
 __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk)[C::NLD],
                                                    const f32x4 (&rv)[C::NLD], int buf,
@@ -113,12 +156,28 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
     constexpr int HD = C::HD_;
     float *Kb = smem + buf * C::BUF;
     float *Vb = Kb + C::STEP_KEYS * C::KS;
+    int *Eb = reinterpret_cast<int *>(Vb + C::STEP_KEYS * HD);
 #pragma unroll
     for (int r = 0; r < C::NLD; ++r) {
         const int idx = tid + r * C::THREADS;
-        if (idx < C::STEP_F4) {
-            const int row = idx / (HD / 4);
-            const int c4 = idx % (HD / 4);
+        const int row = idx / (HD / 4);
+        const int c4 = idx % (HD / 4);
+        if constexpr (C::SQK) {
+            // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32)
+            const f32x4 x = rk[r];
+            const bool fin = isfinite(x.x) && isfinite(x.y) && isfinite(x.z) && isfinite(x.w);
+            const float m4 = fin ? fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)))
+                                 : INFINITY;
+            const float mx = group_max<HD / 4>(m4);
+            const int e = split_exponent(mx);
+            f16x4 hi, lo;
+            split_f16(x, e, hi, lo);
+            _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * C::KS);
+            *reinterpret_cast<f16x4 *>(kr + c4 * 4) = hi;
+            *reinterpret_cast<f16x4 *>(kr + HD + c4 * 4) = lo;
+            if (c4 == 0) Eb[row] = e;
+            *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
+        } else if (idx < C::STEP_F4) {
             *reinterpret_cast<f32x4 *>(Kb + row * C::KS + c4 * 4) = rk[r];
             *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
         }
@@ -178,9 +237,44 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     const int qi = q0 + col;
     const int pi = qbase + qi;
 
-    // Q fragment: query qi, head dims [HALF*hf, HALF*hf + HALF).
-    float qreg[HALF];
-    {
+    // Q fragment. SQK: query qi scaled by 2^-eq (its largest magnitude in [2^14, 2^15))
+    // and split into f16 hi/lo, dims ks*16 + hf*8 .. +8 for every 16-dim step ks; else
+    // f32, head dims [HALF*hf, HALF*hf + HALF).
+    constexpr int NKS = HD / 16;
+    f16x8 qh[C::SQK ? NKS : 1], ql[C::SQK ? NKS : 1];
+    int eq = 0;
+    if constexpr (C::SQK) {
+        const bool qv = qi < rows;
+        const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * HD + 8 * hf;
+        f32x4 qa[NKS], qb[NKS];
+        float mx = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < NKS; ++k2) {
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            qa[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) : z;
+            qb[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) : z;
+            const bool fin = isfinite(qa[k2].x) && isfinite(qa[k2].y) && isfinite(qa[k2].z) &&
+                             isfinite(qa[k2].w) && isfinite(qb[k2].x) && isfinite(qb[k2].y) &&
+                             isfinite(qb[k2].z) && isfinite(qb[k2].w);
+            const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
+                                         fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
+                                   fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
+                                         fmaxf(fabsf(qb[k2].z), fabsf(qb[k2].w))));
+            mx = fmaxf(mx, fin ? m8 : INFINITY);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));  // the other half of the row
+        eq = split_exponent(mx);
+#pragma unroll
+        for (int k2 = 0; k2 < NKS; ++k2) {
+            f16x4 h0, l0, h1, l1;
+            split_f16(qa[k2], eq, h0, l0);
+            split_f16(qb[k2], eq, h1, l1);
+            qh[k2] = f16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+            ql[k2] = f16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+        }
+    }
+    float qreg[C::SQK ? 1 : HALF];
+    if constexpr (!C::SQK) {
         const bool qv = qi < rows;
         const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * HD + HALF * hf;
         if constexpr (HALF % 4 == 0) {
@@ -229,7 +323,30 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
             const float *kr = Kb + col * KS + HALF * hf;
-            if constexpr (HALF % 4 == 0) {
+            int ek[16];  // SQK: exponent of each of this lane's keys
+            if constexpr (C::SQK) {
+                // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
+                const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KS);
+#pragma unroll
+                for (int k2 = 0; k2 < NKS; ++k2) {
+                    const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
+                    const f16x8 al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                    sacc = mfma16(ah, qh[k2], sacc);
+                    sacc = mfma16(ah, ql[k2], sacc);
+                    sacc = mfma16(al, qh[k2], sacc);
+                }
+                const int *Eb = reinterpret_cast<const int *>(smem + buf * C::BUF +
+                                                              C::STEP_KEYS * (KS + HD)) +
+                                ks * kTile;
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4) {
+                    const int4 e4 = *reinterpret_cast<const int4 *>(Eb + 8 * s4 + 4 * hf);
+                    ek[4 * s4 + 0] = e4.x;
+                    ek[4 * s4 + 1] = e4.y;
+                    ek[4 * s4 + 2] = e4.z;
+                    ek[4 * s4 + 3] = e4.w;
+                }
+            } else if constexpr (HALF % 4 == 0) {
 #pragma unroll
                 for (int i = 0; i < HALF / 4; ++i) {
                     float4 a = *reinterpret_cast<const float4 *>(kr + 4 * i);
@@ -253,7 +370,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-                float x = sacc[r] * scale_log2;
+                float x = (C::SQK ? ldexpf(sacc[r], eq + ek[r]) : sacc[r]) * scale_log2;
                 if (edge && (key > pi || (RANGE && window > 0 && key <= pi - window)))
                     x = -INFINITY;
                 p[r] = x;
