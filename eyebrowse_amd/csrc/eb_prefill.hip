@@ -14,14 +14,23 @@
 //    step is fetched into registers while the current one is in use.
 //  - Everything is computed transposed so that the query index sits on the lane:
 //      S^T[key][query] = K Q^T         (contraction over head_dim)
-//      O^T[d][query]  += V^T P^T       (v_mfma_f32_32x32x2_f32, contraction over 32 keys)
-//  - S^T for head_dim >= 32 runs on the f16 matrix cores (v_mfma_f32_32x32x16_f16) at
-//    about f32 accuracy: every K row and every Q row is scaled by a power of two (its
-//    largest magnitude lands in [2^14, 2^15)) and split exactly into hi = f16(x') and
-//    lo = f16(x' - hi); K Q^T = hi*hi + hi*lo + lo*hi (lo*lo is below 2^-22 of the
-//    product), accumulated in f32, and each score is scaled back with ldexp by the
-//    key's and the query's exponents. Rows holding inf or NaN keep exponent 0 and pass
-//    them on. Smaller head dims use the FP32 instruction for S^T as well.
+//      O^T[d][query]  += V^T P^T       (contraction over the 32 keys of a tile)
+//  - For head_dim >= 32 both run on the f16 matrix cores (v_mfma_f32_32x32x16_f16) at
+//    about f32 accuracy (head_dim 256 keeps V^T P^T on v_mfma_f32_32x32x2_f32, whose
+//    register budget the split would exceed; head_dim < 32 uses it for both):
+//      - every K, Q and V row is scaled by a power of two (its largest magnitude lands in
+//        [2^14, 2^15)) and split exactly into hi = f16(x') and lo = f16(x' - hi), so
+//        x' = hi + lo to about 2^-22; all-zero rows get an exponent below every real one;
+//        rows holding inf or NaN keep exponent 0 and pass them on;
+//      - K Q^T = hi*hi + hi*lo + lo*hi (lo*lo is below 2^-22 of the product), in f32;
+//        each score is scaled back with ldexp by its key's and query's exponents;
+//      - V is staged transposed ([head_dim][keys] halves) so that each lane's 8 keys of an
+//        MFMA step are contiguous; P is scaled per key by 2^(ev_key - E) and split, where
+//        E, the largest V exponent seen so far, only grows: O^T accumulates in units of
+//        2^E (rescaled with the softmax correction when E grows), so p' <= 2^kSlack;
+//      - the reference max of the online softmax moves only when a score exceeds it by
+//        more than kSlack, and the rescale of l and O^T is skipped for the whole wave
+//        when no lane needs it.
 //    The S^T accumulator holds, per lane, 16 keys of one query, which is exactly the B
 //    operand layout the PV product needs, so P never leaves registers, and the online
 //    softmax state (running max m, partial sum l) is a per-lane scalar.
@@ -52,6 +61,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
+constexpr float kSlack = 8.0f;  // log2 units the reference max may lag a score (SPV)
 
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -76,8 +86,13 @@ struct PrefillCfg {
     // head_dim >= 32: Q K^T on the f16 matrix cores with an exact hi/lo split (K rows and
     // Q rows scaled by powers of two first); smaller head dims keep FP32 MFMA throughout.
     static constexpr bool SQK = HD >= 32;
-    static constexpr int BUF = STEP_KEYS * (KS + HD + 1);  // floats: K rows, V rows, K exps
-    static constexpr int REC = 2 + 16 * NB;            // merged fields per lane: m, l, O^T
+    // V^T P^T the same way (V rows scaled and split at staging, stored transposed as
+    // [HD][VROW] halves, hi then lo; P scaled per key and split in registers).
+    static constexpr bool SPV = HD >= 32 && HD <= 128;  // (256: registers would spill)
+    static constexpr int VROW = STEP_KEYS + 4;  // halves per V^T row (8-byte reads, banks)
+    static constexpr int VFL = SPV ? HD * VROW : STEP_KEYS * HD;  // floats of V per buffer
+    static constexpr int BUF = STEP_KEYS * KS + VFL + 2 * STEP_KEYS;  // + K and V exponents
+    static constexpr int REC = 3 + 16 * NB;  // merged fields per lane: m, l, V unit, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
     static constexpr int OS = HD + 4;                  // output staging row stride (floats)
     static constexpr int OUT = HPW * WPH * kTile * OS; // output staging, one tile per slot
@@ -133,10 +148,14 @@ __device__ __forceinline__ float group_max(float x) {
     return x;
 }
 
-// The exponent e that brings a row whose largest magnitude is mx into [2^14, 2^15)
-// (0 for zero or non-finite rows, which then keep their inf / NaN).
+// The exponent e that brings a row whose largest magnitude is mx into [2^14, 2^15); 0 for
+// non-finite rows (which then keep their inf / NaN), and kZeroRowExp for all-zero rows
+// (masked or padding rows), below every real exponent so that a tile's largest exponent
+// ignores them.
+constexpr int kZeroRowExp = -1000;
 __device__ __forceinline__ int split_exponent(float mx) {
-    return (mx > 0.0f && mx <= 3.4028235e38f) ? ilogbf(mx) - 14 : 0;
+    if (mx > 3.4028235e38f) return 0;
+    return mx > 0.0f ? ilogbf(mx) - 14 : kZeroRowExp;
 }
 
 // x' = x * 2^-e (exact), hi = f16(x'), lo = f16(x' - hi): x' = hi + lo to about 2^-22.
@@ -156,7 +175,8 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
     constexpr int HD = C::HD_;
     float *Kb = smem + buf * C::BUF;
     float *Vb = Kb + C::STEP_KEYS * C::KS;
-    int *Eb = reinterpret_cast<int *>(Vb + C::STEP_KEYS * HD);
+    int *Eb = reinterpret_cast<int *>(Vb + C::VFL);
+    int *Ev = Eb + C::STEP_KEYS;
 #pragma unroll
     for (int r = 0; r < C::NLD; ++r) {
         const int idx = tid + r * C::THREADS;
@@ -176,7 +196,27 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
             *reinterpret_cast<f16x4 *>(kr + c4 * 4) = hi;
             *reinterpret_cast<f16x4 *>(kr + HD + c4 * 4) = lo;
             if (c4 == 0) Eb[row] = e;
-            *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
+            if constexpr (C::SPV) {
+                const f32x4 y = rv[r];
+                const bool vfin =
+                    isfinite(y.x) && isfinite(y.y) && isfinite(y.z) && isfinite(y.w);
+                const float vm4 = vfin ? fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)),
+                                               fmaxf(fabsf(y.z), fabsf(y.w)))
+                                       : INFINITY;
+                const int ev = split_exponent(group_max<HD / 4>(vm4));
+                f16x4 vh, vl;
+                split_f16(y, ev, vh, vl);
+                _Float16 *vth = reinterpret_cast<_Float16 *>(Vb);  // [HD][VROW] hi
+                _Float16 *vtl = vth + HD * C::VROW;                 // then lo
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    vth[(c4 * 4 + i) * C::VROW + row] = vh[i];
+                    vtl[(c4 * 4 + i) * C::VROW + row] = vl[i];
+                }
+                if (c4 == 0) Ev[row] = ev;
+            } else {
+                *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
+            }
         } else if (idx < C::STEP_F4) {
             *reinterpret_cast<f32x4 *>(Kb + row * C::KS + c4 * 4) = rk[r];
             *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
@@ -300,6 +340,9 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         for (int r = 0; r < 16; ++r) oacc[mb][r] = 0.0f;
     float m = -INFINITY;
     float l = 0.0f;
+    // SPV: O^T is accumulated in units of 2^E, E the largest V exponent seen so far (the
+    // same for every lane of the wave: all lanes see the same keys).
+    int E = kZeroRowExp;
 
     f32x4 rk[C::NLD], rv[C::NLD];
     prefill_load_step<C, H16>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
@@ -317,7 +360,8 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 
         if (live && tile >= my_t0 && tile <= my_t1) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
-            const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS + ks * kTile * HD;
+            const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS +
+                              (C::SPV ? 0 : ks * kTile * HD);
             // S^T = K Q^T for this tile: 16 keys x 1 query per lane.
             floatx16 sacc;
 #pragma unroll
@@ -336,7 +380,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     sacc = mfma16(al, qh[k2], sacc);
                 }
                 const int *Eb = reinterpret_cast<const int *>(smem + buf * C::BUF +
-                                                              C::STEP_KEYS * (KS + HD)) +
+                                                              C::STEP_KEYS * KS + C::VFL) +
                                 ks * kTile;
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4) {
@@ -377,11 +421,15 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 mt = fmaxf(mt, x);
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float mnew = fmaxf(m, mt);
+            // SPV: lazy reference max. m moves only when a score exceeds it by more than
+            // kSlack (log2 units), so most tiles need no rescale of l and O^T; terms
+            // 2^(s - m) then stay below 2^kSlack, which the f16 split holds exactly.
+            const bool grow = C::SPV ? (mt > m + kSlack) : true;
+            const float mnew = grow ? fmaxf(m, mt) : m;
             // A query can meet a tile with all of its keys masked before its first visible
             // key (unaligned chunk starts, windows): keep exp2 away from -inf - -inf.
-            const float mref = (RANGE && mnew == -INFINITY) ? 0.0f : mnew;
-            const float corr = eb::fast_exp2(m - mref);
+            const float mref = ((RANGE || C::SPV) && mnew == -INFINITY) ? 0.0f : mnew;
+            const float corr = grow ? eb::fast_exp2(m - mref) : 1.0f;
             float ps = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -390,6 +438,65 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             }
             l = l * corr + ps;
             m = mnew;
+            if constexpr (C::SPV) {
+                // The tile's V exponents; the unit E only grows, so p' = p * 2^(ev - E) <= 1.
+                const int *Ev = reinterpret_cast<const int *>(smem + buf * C::BUF +
+                                                              C::STEP_KEYS * KS + C::VFL) +
+                                C::STEP_KEYS + ks * kTile;
+                int ev[16];
+                int et = kZeroRowExp;
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4) {
+                    const int4 e4 = *reinterpret_cast<const int4 *>(Ev + 8 * s4 + 4 * hf);
+                    ev[4 * s4 + 0] = e4.x;
+                    ev[4 * s4 + 1] = e4.y;
+                    ev[4 * s4 + 2] = e4.z;
+                    ev[4 * s4 + 3] = e4.w;
+                    et = max(et, max(max(e4.x, e4.y), max(e4.z, e4.w)));
+                }
+                et = max(et, __shfl_xor(et, 32));
+                const int En = max(E, et);
+                if (En != E || __builtin_amdgcn_ballot_w64(grow) != 0) {
+                    const float f = ldexpf(corr, E - En);
+#pragma unroll
+                    for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) oacc[mb][r] *= f;
+                }
+                E = En;
+                // P^T operands: k-step u takes this lane's keys r = 8u .. 8u+7.
+                f16x8 ph[2], pl[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const float pp = ldexpf(p[8 * u + c], ev[8 * u + c] - E);
+                        const _Float16 hh = (_Float16)pp;
+                        ph[u][c] = hh;
+                        pl[u][c] = (_Float16)(pp - (float)hh);
+                    }
+                // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the
+                // output stage expects); keys 16u + 4hf + 0..3 and 16u + 8 + 4hf + 0..3 of
+                // this wave's tile (the order of ph / pl).
+                const _Float16 *vth = reinterpret_cast<const _Float16 *>(Vb);
+                const _Float16 *vtl = vth + HD * C::VROW;
+#pragma unroll
+                for (int mb = 0; mb < NB; ++mb) {
+                    const int roff = (NB * col + mb) * C::VROW + ks * kTile + 4 * hf;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const f16x4 h0 = *reinterpret_cast<const f16x4 *>(vth + roff + 16 * u);
+                        const f16x4 h1 = *reinterpret_cast<const f16x4 *>(vth + roff + 16 * u + 8);
+                        const f16x4 l0 = *reinterpret_cast<const f16x4 *>(vtl + roff + 16 * u);
+                        const f16x4 l1 = *reinterpret_cast<const f16x4 *>(vtl + roff + 16 * u + 8);
+                        const f16x8 vh = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                        const f16x8 vl = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+                        oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
+                        oacc[mb] = mfma16(vh, pl[u], oacc[mb]);
+                        oacc[mb] = mfma16(vl, ph[u], oacc[mb]);
+                    }
+                }
+            } else {
 #pragma unroll
             for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
@@ -428,6 +535,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     oacc[0] = mfma32(a, p[t], oacc[0]);
                 }
             }
+            }
         }
 
         prefill_store_step<C>(smem, rk, rv, buf ^ 1, tid);
@@ -442,10 +550,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             float *rec = smem + ((ks - 1) * (HPW * WPH) + slot) * C::REC * 64;
             rec[0 * 64 + lane] = m;
             rec[1 * 64 + lane] = l;
+            rec[2 * 64 + lane] = __int_as_float(E);
 #pragma unroll
             for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) rec[(2 + mb * 16 + r) * 64 + lane] = oacc[mb][r];
+                for (int r = 0; r < 16; ++r) rec[(3 + mb * 16 + r) * 64 + lane] = oacc[mb][r];
         }
         __syncthreads();
         if (ks == 0) {
@@ -454,17 +563,23 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 const float *rec = smem + ((j - 1) * (HPW * WPH) + slot) * C::REC * 64;
                 const float m2 = rec[lane];
                 const float l2 = rec[64 + lane];
+                const int E2 = __float_as_int(rec[128 + lane]);
                 const float M = fmaxf(m, m2);
                 const float Mr = (M == -INFINITY) ? 0.0f : M;
                 const float a1 = eb::fast_exp2(m - Mr);   // 0 when this wave saw no keys
                 const float a2 = eb::fast_exp2(m2 - Mr);  // 0 when split j saw no keys
                 l = l * a1 + l2 * a2;
                 m = M;
+                // both O^T partials to the larger unit 2^En (SPV; E stays unused otherwise)
+                const int En = max(E, E2);
+                const float b1 = C::SPV ? ldexpf(a1, E - En) : a1;
+                const float b2 = C::SPV ? ldexpf(a2, E2 - En) : a2;
+                E = En;
 #pragma unroll
                 for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        oacc[mb][r] = oacc[mb][r] * a1 + rec[(2 + mb * 16 + r) * 64 + lane] * a2;
+                        oacc[mb][r] = oacc[mb][r] * b1 + rec[(3 + mb * 16 + r) * 64 + lane] * b2;
             }
         }
     }
@@ -478,24 +593,32 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     float *ot = smem + slot * kTile * C::OS;    // this slot's staging tile [32][OS]
     if (ks == 0 && live) {
         const float inv = 1.0f / lt;
+        // SPV: O^T is in units of 2^E; ldexp each normalised value back (exact)
+        if constexpr (C::SPV) {
+#pragma unroll
+            for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[mb][r] = ldexpf(oacc[mb][r] * inv, E);
+        }
+        const float sc_o = C::SPV ? 1.0f : inv;
         float *orow = ot + col * C::OS;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int c = 8 * (r >> 2) + 4 * hf + (r & 3);
             if constexpr (NB == 8) {
                 *reinterpret_cast<float4 *>(orow + 8 * c) =
-                    make_float4(oacc[0][r] * inv, oacc[1][r] * inv, oacc[2][r] * inv, oacc[3][r] * inv);
+                    make_float4(oacc[0][r] * sc_o, oacc[1][r] * sc_o, oacc[2][r] * sc_o, oacc[3][r] * sc_o);
                 *reinterpret_cast<float4 *>(orow + 8 * c + 4) =
-                    make_float4(oacc[4][r] * inv, oacc[5][r] * inv, oacc[6][r] * inv, oacc[7][r] * inv);
+                    make_float4(oacc[4][r] * sc_o, oacc[5][r] * sc_o, oacc[6][r] * sc_o, oacc[7][r] * sc_o);
             } else if constexpr (NB == 4) {
                 *reinterpret_cast<float4 *>(orow + 4 * c) =
-                    make_float4(oacc[0][r] * inv, oacc[1][r] * inv, oacc[2][r] * inv, oacc[3][r] * inv);
+                    make_float4(oacc[0][r] * sc_o, oacc[1][r] * sc_o, oacc[2][r] * sc_o, oacc[3][r] * sc_o);
             } else if constexpr (NB == 2) {
-                *reinterpret_cast<float2 *>(orow + 2 * c) = make_float2(oacc[0][r] * inv, oacc[1][r] * inv);
+                *reinterpret_cast<float2 *>(orow + 2 * c) = make_float2(oacc[0][r] * sc_o, oacc[1][r] * sc_o);
             } else if constexpr (HD >= 32) {
-                orow[c] = oacc[0][r] * inv;
+                orow[c] = oacc[0][r] * sc_o;
             } else {
-                if (c < HD) orow[c] = oacc[0][r] * inv;
+                if (c < HD) orow[c] = oacc[0][r] * sc_o;
             }
         }
     }

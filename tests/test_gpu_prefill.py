@@ -60,7 +60,10 @@ def test_shapes(dev, h, hkv, s, hd, scale):
     want = oracle.attn_prefill(q, k, v, h, hkv, s, hd, sc, threads=8)
     assert_close(got, want, what="shape")
     g = h // hkv
-    np.testing.assert_array_equal(got[0], np.repeat(v[0], g, axis=0))
+    # row 0 attends key 0 only: o = v[0] (head_dim >= 32 holds V as an f16 hi + lo pair,
+    # i.e. to 2^-22 relative; smaller head dims keep it exactly)
+    tol = 2.0 ** -21 if hd >= 32 else 0.0
+    np.testing.assert_allclose(got[0], np.repeat(v[0], g, axis=0), rtol=tol, atol=0)
 
 
 def _sampled_rows(T):
