@@ -149,13 +149,24 @@ __device__ __forceinline__ float group_max(float x) {
 }
 
 // The exponent e that brings a row whose largest magnitude is mx into [2^14, 2^15); 0 for
-// non-finite rows (which then keep their inf / NaN), and kZeroRowExp for all-zero rows
-// (masked or padding rows), below every real exponent so that a tile's largest exponent
-// ignores them.
+// rows holding inf (which then keep it), and kZeroRowExp for all-zero rows (masked or
+// padding rows), below every real exponent so that a tile's largest exponent ignores
+// them. (fmaxf drops NaN, so a NaN row gets the exponent of its other elements and still
+// passes its NaN on.) frexp gives m * 2^k with m in [0.5, 1): the exponent is k - 1.
 constexpr int kZeroRowExp = -1000;
 __device__ __forceinline__ int split_exponent(float mx) {
     if (mx > 3.4028235e38f) return 0;
-    return mx > 0.0f ? ilogbf(mx) - 14 : kZeroRowExp;
+    return mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 15 : kZeroRowExp;
+}
+
+// The value held by lane i ^ N (N = 8, 16 or 32).
+template <int N>
+__device__ __forceinline__ unsigned lane_xor_u(unsigned x) {
+    static_assert(N == 8 || N == 16 || N == 32, "8, 16 or 32");
+    const float f = __builtin_bit_cast(float, x);
+    if constexpr (N == 32) return __builtin_bit_cast(unsigned, eb::lane_xor32(f));
+    else if constexpr (N == 16) return __builtin_bit_cast(unsigned, eb::lane_xor16(f));
+    else return __builtin_bit_cast(unsigned, eb::dpp<0x128>(f));  // row_ror:8 = i ^ 8 in a row
 }
 
 // x' = x * 2^-e (exact), hi = f16(x'), lo = f16(x' - hi): x' = hi + lo to about 2^-22.
@@ -185,9 +196,7 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
         if constexpr (C::SQK) {
             // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32)
             const f32x4 x = rk[r];
-            const bool fin = isfinite(x.x) && isfinite(x.y) && isfinite(x.z) && isfinite(x.w);
-            const float m4 = fin ? fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)))
-                                 : INFINITY;
+            const float m4 = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
             const float mx = group_max<HD / 4>(m4);
             const int e = split_exponent(mx);
             f16x4 hi, lo;
@@ -198,20 +207,33 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
             if (c4 == 0) Eb[row] = e;
             if constexpr (C::SPV) {
                 const f32x4 y = rv[r];
-                const bool vfin =
-                    isfinite(y.x) && isfinite(y.y) && isfinite(y.z) && isfinite(y.w);
-                const float vm4 = vfin ? fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)),
-                                               fmaxf(fabsf(y.z), fabsf(y.w)))
-                                       : INFINITY;
+                const float vm4 = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
                 const int ev = split_exponent(group_max<HD / 4>(vm4));
                 f16x4 vh, vl;
                 split_f16(y, ev, vh, vl);
-                _Float16 *vth = reinterpret_cast<_Float16 *>(Vb);  // [HD][VROW] hi
-                _Float16 *vtl = vth + HD * C::VROW;                 // then lo
+                // V^T row of dim d sits at p(d) = (d % NB) * 32 + d / NB (the MFMA reader
+                // then walks consecutive rows). Rows j and j + 1 (lanes i and i ^ HD/4) pair
+                // their halves: the even row's lane writes dims 0, 1 of its four, the odd
+                // row's lane dims 2, 3, each as one 32-bit (key j, key j + 1) word.
+                using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
+                const u32x2 ho = __builtin_bit_cast(u32x2, vh), lw = __builtin_bit_cast(u32x2, vl);
+                const u32x2 hp = {lane_xor_u<HD / 4>(ho.x), lane_xor_u<HD / 4>(ho.y)};
+                const u32x2 lp = {lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
+                const f16x4 vh2 = __builtin_bit_cast(f16x4, hp), vl2 = __builtin_bit_cast(f16x4, lp);
+                const bool odd = row & 1;
+                const int j0 = row & ~1;
+                unsigned *vth = reinterpret_cast<unsigned *>(Vb);  // [HD][VROW/2] words, hi
+                unsigned *vtl = vth + HD * (C::VROW / 2);           // then lo
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    vth[(c4 * 4 + i) * C::VROW + row] = vh[i];
-                    vtl[(c4 * 4 + i) * C::VROW + row] = vl[i];
+                for (int t = 0; t < 2; ++t) {
+                    const int i = odd ? 2 + t : t;  // which of the four dims
+                    const int d = c4 * 4 + i;
+                    const int pr = (d % C::NB) * 32 + d / C::NB;
+                    const _Float16 he = odd ? vh2[i] : vh[i], ho2 = odd ? vh[i] : vh2[i];
+                    const _Float16 le = odd ? vl2[i] : vl[i], lo2 = odd ? vl[i] : vl2[i];
+                    using h2 = __attribute__((ext_vector_type(2))) _Float16;
+                    vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
+                    vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
                 }
                 if (c4 == 0) Ev[row] = ev;
             } else {
@@ -293,14 +315,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
             qa[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) : z;
             qb[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) : z;
-            const bool fin = isfinite(qa[k2].x) && isfinite(qa[k2].y) && isfinite(qa[k2].z) &&
-                             isfinite(qa[k2].w) && isfinite(qb[k2].x) && isfinite(qb[k2].y) &&
-                             isfinite(qb[k2].z) && isfinite(qb[k2].w);
             const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
                                          fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
                                    fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
                                          fmaxf(fabsf(qb[k2].z), fabsf(qb[k2].w))));
-            mx = fmaxf(mx, fin ? m8 : INFINITY);
+            mx = fmaxf(mx, m8);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));  // the other half of the row
         eq = split_exponent(mx);
@@ -476,13 +495,13 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                         pl[u][c] = (_Float16)(pp - (float)hh);
                     }
                 // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the
-                // output stage expects); keys 16u + 4hf + 0..3 and 16u + 8 + 4hf + 0..3 of
-                // this wave's tile (the order of ph / pl).
+                // output stage expects), stored at V^T row 32*mb + col; keys 16u + 4hf +
+                // 0..3 and 16u + 8 + 4hf + 0..3 of this wave's tile (the order of ph / pl).
                 const _Float16 *vth = reinterpret_cast<const _Float16 *>(Vb);
                 const _Float16 *vtl = vth + HD * C::VROW;
 #pragma unroll
                 for (int mb = 0; mb < NB; ++mb) {
-                    const int roff = (NB * col + mb) * C::VROW + ks * kTile + 4 * hf;
+                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 4 * hf;
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
                         const f16x4 h0 = *reinterpret_cast<const f16x4 *>(vth + roff + 16 * u);
