@@ -89,7 +89,8 @@ struct PrefillCfg {
     // V^T P^T the same way (V rows scaled and split at staging, stored transposed as
     // [HD][VROW] halves, hi then lo; P scaled per key and split in registers).
     static constexpr bool SPV = HD >= 32 && HD <= 128;  // (256: registers would spill)
-    static constexpr int VROW = STEP_KEYS + 4;  // halves per V^T row (8-byte reads, banks)
+    static constexpr int VROW = STEP_KEYS + 8;  // halves per V^T row (16-byte aligned reads
+                                                // of consecutive rows spread over the banks)
     static constexpr int VFL = SPV ? HD * VROW : STEP_KEYS * HD;  // floats of V per buffer
     static constexpr int BUF = STEP_KEYS * KS + VFL + 2 * STEP_KEYS;  // + K and V exponents
     static constexpr int REC = 3 + 16 * NB;  // merged fields per lane: m, l, V unit, O^T
@@ -221,7 +222,11 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                 const u32x2 lp = {lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
                 const f16x4 vh2 = __builtin_bit_cast(f16x4, hp), vl2 = __builtin_bit_cast(f16x4, lp);
                 const bool odd = row & 1;
-                const int j0 = row & ~1;
+                // Keys are stored permuted within each 16: groups of four in the order
+                // 0, 2, 1, 3, so that the 8 keys one lane half feeds an MFMA step (keys
+                // 16u + 4hf + 0..3 and 16u + 8 + 4hf + 0..3) are contiguous.
+                const int g4 = (row >> 2) & 3;
+                const int j0 = (row & ~15) | (((g4 & 1) << 1 | (g4 >> 1)) << 2) | (row & 2);
                 unsigned *vth = reinterpret_cast<unsigned *>(Vb);  // [HD][VROW/2] words, hi
                 unsigned *vtl = vth + HD * (C::VROW / 2);           // then lo
 #pragma unroll
@@ -501,15 +506,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 const _Float16 *vtl = vth + HD * C::VROW;
 #pragma unroll
                 for (int mb = 0; mb < NB; ++mb) {
-                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 4 * hf;
+                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 8 * hf;
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
-                        const f16x4 h0 = *reinterpret_cast<const f16x4 *>(vth + roff + 16 * u);
-                        const f16x4 h1 = *reinterpret_cast<const f16x4 *>(vth + roff + 16 * u + 8);
-                        const f16x4 l0 = *reinterpret_cast<const f16x4 *>(vtl + roff + 16 * u);
-                        const f16x4 l1 = *reinterpret_cast<const f16x4 *>(vtl + roff + 16 * u + 8);
-                        const f16x8 vh = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-                        const f16x8 vl = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+                        const f16x8 vh = *reinterpret_cast<const f16x8 *>(vth + roff + 16 * u);
+                        const f16x8 vl = *reinterpret_cast<const f16x8 *>(vtl + roff + 16 * u);
                         oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
                         oacc[mb] = mfma16(vh, pl[u], oacc[mb]);
                         oacc[mb] = mfma16(vl, ph[u], oacc[mb]);
