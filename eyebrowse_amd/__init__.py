@@ -15,11 +15,13 @@ from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, Graph, LoadE
                   OutOfMemory, Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
 from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_step,
                       attn_decode_step_window, attn_decode_window, attn_decode_workspace_floats,
-                      attn_prefill, attn_prefill_chunk, kv_write, launch_argmax,
+                      attn_prefill, attn_prefill_chunk, attn_prefill_workspace_floats,
+                      kv_write, launch_argmax,
                       launch_attn_decode, launch_attn_decode_f16, launch_attn_decode_step,
                       launch_attn_decode_step_f16, launch_attn_decode_window,
                       launch_attn_prefill, launch_attn_prefill_chunk,
-                      launch_attn_prefill_chunk_f16, launch_kv_write, launch_kv_write_f16,
+                      launch_attn_prefill_chunk_f16, launch_attn_prefill_chunk_ws,
+                      launch_attn_prefill_ws, launch_kv_write, launch_kv_write_f16,
                       launch_linear_f16w, launch_rmsnorm, launch_rope, linear_f16w,
                       linear_f16w_multi, linear_workspace_floats, rmsnorm, rope)
 from .nn import Attention, KvCache, Linear, Rope
@@ -32,7 +34,8 @@ __all__ = [
     "attn_decode_workspace_floats", "attn_prefill", "attn_prefill_chunk", "kv_write",
     "launch_attn_decode", "launch_attn_decode_f16", "launch_attn_decode_step",
     "launch_attn_decode_step_f16", "launch_attn_decode_window", "launch_attn_prefill",
-    "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_kv_write",
+    "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_attn_prefill_chunk_ws",
+    "launch_attn_prefill_ws", "attn_prefill_workspace_floats", "launch_kv_write",
     "launch_kv_write_f16", "launch_linear_f16w", "linear_f16w", "linear_f16w_multi",
     "linear_workspace_floats", "launch_rmsnorm",
     "launch_rope", "rmsnorm", "rope", "Attention", "KvCache", "Linear", "Rope",

@@ -47,15 +47,20 @@ int current_cu_count();
 // ---- kernel launchers (validated arguments, caller's stream) -------------------------
 eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t hkv,
                           size_t count, size_t hd, size_t dst_start);
+// Prefill workspace: floats of the pre-split K/V records for this shape (0: the prefill
+// splits K/V while staging). Launches given at least that much (16-byte aligned) run the
+// pre-split pass first; with less they stage as without. No initialisation needed.
+size_t prefill_workspace_floats(size_t hkv, size_t hd, size_t rows, size_t nkeys, size_t qbase,
+                                size_t window);
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
-                              float scale);
+                              float scale, float *ws = nullptr, size_t ws_floats = 0);
 // Chunked causal prefill: q rows at positions pos0..pos0+rows-1 attend cache keys
 // max(0, p - window + 1)..p (window 0: 0..p); kc/vc are the cache bases.
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
                                     const float *vc, float *o, size_t h, size_t hkv,
                                     size_t pos0, size_t rows, size_t hd, float scale,
-                                    size_t window);
+                                    size_t window, float *ws = nullptr, size_t ws_floats = 0);
 // Decode workspace: part_acc [nsplit*h*hd] | part_ml [nsplit*h*2], no initialisation.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
                                bool h16 = false);
@@ -91,7 +96,8 @@ eb_status launch_kv_write_f16(hipStream_t st, uint16_t *cache, const float *src,
 eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
                                         const uint16_t *vc, float *o, size_t h, size_t hkv,
                                         size_t pos0, size_t rows, size_t hd, float scale,
-                                        size_t window);
+                                        size_t window, float *ws = nullptr,
+                                        size_t ws_floats = 0);
 // Attention::decode after the projections as one fused step: RMSNorm (null gains: none)
 // and RoPE (null tables: none) of q and the new K row, RMSNorm of the new V row, the
 // cache-row write and the attention. Handle-level, used by eb_attention_forward_qkv.

@@ -26,8 +26,9 @@
 //        each score is scaled back with ldexp by its key's and query's exponents;
 //      - V is staged transposed ([head_dim][keys] halves) so that each lane's 8 keys of an
 //        MFMA step are contiguous; P is scaled per key by 2^(ev_key - E) and split, where
-//        E, the largest V exponent seen so far, only grows: O^T accumulates in units of
-//        2^E (rescaled with the softmax correction when E grows), so p' <= 2^kSlack;
+//        E, per query, is the exponent of its largest term p * 2^ev_key: O^T accumulates
+//        in units of 2^E (rescaled when E moves, with the softmax correction), so p' <= 1
+//        and the largest terms keep the split's full precision;
 //      - the reference max of the online softmax moves only when a score exceeds it by
 //        more than kSlack, and the rescale of l and O^T is skipped for the whole wave
 //        when no lane needs it.
@@ -93,6 +94,12 @@ struct PrefillCfg {
                                                 // of consecutive rows spread over the banks)
     static constexpr int VFL = SPV ? HD * VROW : STEP_KEYS * HD;  // floats of V per buffer
     static constexpr int BUF = STEP_KEYS * KS + VFL + 2 * STEP_KEYS;  // + K and V exponents
+    // Pre-split K/V (SPV): one record per (KV head, 32-key tile) of 16-byte chunks: K rows
+    // [32][HD floats of hi then lo halves], V^T hi [HD][32 halves], V^T lo, K exponents
+    // [32], V exponents [32]. A step copies KSPLIT records into LDS.
+    static constexpr int PS_CH = 16 * HD + 16;          // chunks per record
+    static constexpr int PS_KV = KSPLIT * 16 * HD;      // K/V chunks per step
+    static constexpr int PSN = (PS_KV + THREADS - 1) / THREADS + 1;  // + one exponent chunk
     static constexpr int REC = 3 + 16 * NB;  // merged fields per lane: m, l, V unit, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
     static constexpr int OS = HD + 4;                  // output staging row stride (floats)
@@ -154,7 +161,7 @@ __device__ __forceinline__ float group_max(float x) {
 // padding rows), below every real exponent so that a tile's largest exponent ignores
 // them. (fmaxf drops NaN, so a NaN row gets the exponent of its other elements and still
 // passes its NaN on.) frexp gives m * 2^k with m in [0.5, 1): the exponent is k - 1.
-constexpr int kZeroRowExp = -1000;
+constexpr int kZeroRowExp = -200;  // (ev << 23 of every exponent fits an int)
 __device__ __forceinline__ int split_exponent(float mx) {
     if (mx > 3.4028235e38f) return 0;
     return mx > 0.0f ? __builtin_amdgcn_frexp_expf(mx) - 15 : kZeroRowExp;
@@ -251,16 +258,93 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
     }
 }
 
+// Float offset, inside one LDS buffer of C, of chunk w of tile kt's pre-split record (the
+// image prefill_store_step writes for that tile, less its row padding).
+template <class C>
+__device__ __forceinline__ int ps_lds_offset(int kt, int w) {
+    constexpr int HD = C::HD_;
+    if (w < 8 * HD) return (kt * kTile + w / (HD / 4)) * C::KS + 4 * (w % (HD / 4));
+    if (w < 16 * HD) {
+        const int w2 = w - 8 * HD;
+        const int lo = w2 >= 4 * HD;
+        const int w3 = w2 - (lo ? 4 * HD : 0);
+        return C::STEP_KEYS * C::KS + lo * HD * (C::VROW / 2) + (w3 / 4) * (C::VROW / 2) +
+               kt * (kTile / 2) + 4 * (w3 % 4);
+    }
+    const int e = w - 16 * HD;  // exponents: K chunks 0..7, V chunks 8..15
+    return C::STEP_KEYS * C::KS + C::VFL + (e >= 8 ? C::STEP_KEYS : 0) + kt * kTile + 4 * (e % 8);
+}
+
+// Fetch the pre-split records of tiles tile0 .. tile0 + KSPLIT - 1 (clamped to the last
+// record, nt - 1; a clamped buffer is never read) of one KV head (recs).
+template <class C>
+__device__ __forceinline__ void ps_load_step(const f32x4 *__restrict__ recs,
+                                             f32x4 (&r)[C::PSN], int tile0, int nt, int tid) {
+    constexpr int HD = C::HD_;
+#pragma unroll
+    for (int i = 0; i < C::PSN - 1; ++i) {
+        const int c = min(tid + i * C::THREADS, C::PS_KV - 1);
+        const int t = min(tile0 + c / (16 * HD), nt - 1);
+        r[i] = recs[(size_t)t * C::PS_CH + c % (16 * HD)];
+    }
+    const int kt = min(tid / 16, C::STEP_KEYS / kTile - 1);
+    const int t = min(tile0 + kt, nt - 1);
+    r[C::PSN - 1] = recs[(size_t)t * C::PS_CH + 16 * HD + tid % 16];
+}
+
+template <class C>
+__device__ __forceinline__ void ps_store_step(float *smem, const f32x4 (&r)[C::PSN], int buf,
+                                              int tid) {
+    constexpr int HD = C::HD_;
+    float *B = smem + buf * C::BUF;
+#pragma unroll
+    for (int i = 0; i < C::PSN - 1; ++i) {
+        const int c = tid + i * C::THREADS;
+        if (C::PS_KV % C::THREADS == 0 || c < C::PS_KV)
+            *reinterpret_cast<f32x4 *>(B + ps_lds_offset<C>(c / (16 * HD), c % (16 * HD))) = r[i];
+    }
+    if (tid < 16 * (C::STEP_KEYS / kTile))
+        *reinterpret_cast<f32x4 *>(B + ps_lds_offset<C>(tid / 16, 16 * HD + tid % 16)) =
+            r[C::PSN - 1];
+}
+
+// Pre-split pass: workgroup (t, kvh) splits keys [(tlo + t) * 32, +32) of KV head kvh
+// (rows past nkeys as zeros) exactly as the prefill's own staging does, and writes the
+// tile's record. The prefill then only copies records into LDS: the split is done once
+// per key instead of once per workgroup that reads the key.
+template <int HD, bool H16>
+__global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ k,
+                                                       const void *__restrict__ v,
+                                                       f32x4 *__restrict__ ps, int nkeys,
+                                                       int Hkv, int tlo, int nt) {
+    using C = PrefillCfg<HD, 4, 1, 1>;  // 256 threads, one 32-key tile per step
+    static_assert(C::SPV, "pre-split needs the split V path");
+    __shared__ float smem[C::BUF];
+    const int t = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x;
+    f32x4 rk[C::NLD], rv[C::NLD];
+    prefill_load_step<C, H16>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid);
+    prefill_store_step<C>(smem, rk, rv, 0, tid);
+    __syncthreads();
+    f32x4 *rec = ps + ((size_t)kvh * nt + t) * C::PS_CH;
+    for (int c = tid; c < C::PS_CH; c += C::THREADS)
+        rec[c] = *reinterpret_cast<const f32x4 *>(smem + ps_lds_offset<C>(0, c));
+}
+
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
 // RANGE: queries start at position qbase and may have a sliding window; without it the
 // kernel is specialised to a prompt from position 0 (no window), whose masks are simpler.
 // H16: the K/V rows are IEEE half (an f16 KV cache), converted to f32 as they are staged.
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16>
+// PS: K/V come as pre-split records (ps: ps_nt records per KV head, record 0 = tile
+// ps_tlo) instead of k/v.
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
-    float *__restrict__ o, int H, int Hkv, int rows, int nkeys, int qbase, int window,
-    float scale_log2, int nqb, int ngroups) {
+    const f32x4 *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
+    int Hkv, int rows, int nkeys, int qbase, int window, float scale_log2, int nqb,
+    int ngroups) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     constexpr int QB = C::QB;
     constexpr int HALF = C::HALF;
@@ -364,13 +448,21 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         for (int r = 0; r < 16; ++r) oacc[mb][r] = 0.0f;
     float m = -INFINITY;
     float l = 0.0f;
-    // SPV: O^T is accumulated in units of 2^E, E the largest V exponent seen so far (the
-    // same for every lane of the wave: all lanes see the same keys).
+    // SPV: O^T is accumulated in units of 2^E (per query; both lane halves of a query hold
+    // the same E).
     int E = kZeroRowExp;
 
-    f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C, H16>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
-    prefill_store_step<C>(smem, rk, rv, 0, tid);
+    static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
+    f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
+    f32x4 rs[PS ? C::PSN : 1];
+    const f32x4 *recs = PS ? ps + (size_t)kvh * ps_nt * C::PS_CH : nullptr;
+    if constexpr (PS) {
+        ps_load_step<C>(recs, rs, t0 - ps_tlo, ps_nt, tid);
+        ps_store_step<C>(smem, rs, 0, tid);
+    } else {
+        prefill_load_step<C, H16>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
+        prefill_store_step<C>(smem, rk, rv, 0, tid);
+    }
     __syncthreads();
 
     for (int it = 0; it < nsteps; ++it) {
@@ -379,8 +471,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         const int kb = tile * kTile;
         // Prefetch the next step (past the last step this re-reads clamped rows; the
         // buffer written from them is never read).
-        prefill_load_step<C, H16>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys, Hkv,
-                                  kvh, tid);
+        if constexpr (PS)
+            ps_load_step<C>(recs, rs, t0 + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
+        else
+            prefill_load_step<C, H16>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys,
+                                      Hkv, kvh, tid);
 
         if (live && tile >= my_t0 && tile <= my_t1) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
@@ -461,14 +556,14 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 ps += p[r];
             }
             l = l * corr + ps;
+            const float mold = m;
             m = mnew;
             if constexpr (C::SPV) {
-                // The tile's V exponents; the unit E only grows, so p' = p * 2^(ev - E) <= 1.
+                // The tile's V exponents ev (V row = 2^ev * v').
                 const int *Ev = reinterpret_cast<const int *>(smem + buf * C::BUF +
                                                               C::STEP_KEYS * KS + C::VFL) +
                                 C::STEP_KEYS + ks * kTile;
                 int ev[16];
-                int et = kZeroRowExp;
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4) {
                     const int4 e4 = *reinterpret_cast<const int4 *>(Ev + 8 * s4 + 4 * hf);
@@ -476,12 +571,29 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     ev[4 * s4 + 1] = e4.y;
                     ev[4 * s4 + 2] = e4.z;
                     ev[4 * s4 + 3] = e4.w;
-                    et = max(et, max(max(e4.x, e4.y), max(e4.z, e4.w)));
                 }
-                et = max(et, __shfl_xor(et, 32));
-                const int En = max(E, et);
-                if (En != E || __builtin_amdgcn_ballot_w64(grow) != 0) {
-                    const float f = ldexpf(corr, E - En);
+                // This query's unit: O^T is held in units of 2^E, E the exponent of its
+                // largest term p * 2^ev, so that p' = p * 2^(ev - E) <= 1 and the largest
+                // terms keep full f16 hi/lo precision (a wave-wide unit would push the p'
+                // of a query's small-V keys below f16 range whenever another query, or a
+                // key of negligible weight, brings a large V row). p * 2^ev has the float
+                // bits of p plus ev in the exponent field (an upper bound for p = 0 or
+                // subnormal), so the tile's largest term comes from an integer max.
+                unsigned tb = 0x80000000u;  // the smallest int
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const unsigned t = __builtin_bit_cast(unsigned, p[r]) + ((unsigned)ev[r] << 23);
+                    tb = (int)t > (int)tb ? t : tb;
+                }
+                int tx = ((int)tb >> 23) - 126;
+                tx = max(tx, __shfl_xor(tx, 32));
+                // The softmax correction 2^-(mref - mold) moves the accumulated terms down:
+                // the unit follows by whole bits, the fraction goes into the rescale factor.
+                const float dm = mref - mold;
+                const int Eb = !grow ? E : (dm < 1000.0f ? max(E - (int)dm, kZeroRowExp) : kZeroRowExp);
+                const int En = max(Eb, tx);
+                if (__builtin_amdgcn_ballot_w64(grow || En != E) != 0) {
+                    const float f = ldexpf(corr, E - En);  // <= 1
 #pragma unroll
                     for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
@@ -558,7 +670,10 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             }
         }
 
-        prefill_store_step<C>(smem, rk, rv, buf ^ 1, tid);
+        if constexpr (PS)
+            ps_store_step<C>(smem, rs, buf ^ 1, tid);
+        else
+            prefill_store_step<C>(smem, rk, rv, buf ^ 1, tid);
         __syncthreads();
     }
 
@@ -665,17 +780,37 @@ struct PrefillRange {
     int qbase;   // position of query row 0
     int window;  // sliding window (0: none)
     bool h16;    // k/v hold IEEE half elements
+    float *ws;   // pre-split workspace (null: split while staging)
+    size_t ws_floats;
 };
 
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16>
+// The pre-split pass pays one read and one write of the keys in range; it is used when at
+// least this many query rows (each workgroup of them re-staging every key) share them.
+constexpr int kPresplitMinRows = 256;
+
+// First tile and number of tiles the pre-split records cover: every key some query of the
+// launch can see.
+int presplit_tlo(const PrefillRange &r) {
+    return r.window > 0 ? (r.qbase - r.window + 1 > 0 ? r.qbase - r.window + 1 : 0) / kTile : 0;
+}
+int presplit_nt(const PrefillRange &r) { return (r.nkeys + kTile - 1) / kTile - presplit_tlo(r); }
+
+size_t presplit_floats(size_t hd, size_t hkv, const PrefillRange &r) {
+    if (hd < 32 || hd > 128 || r.rows < kPresplitMinRows || r.nkeys <= 0) return 0;
+    return hkv * (size_t)presplit_nt(r) * (16 * hd + 16) * 4;
+}
+
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
 eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
-                           float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
+                           const f32x4 *ps, float *o, int H, int Hkv, const PrefillRange &r,
+                           float scale_log2) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16>),
+            reinterpret_cast<const void *>(
+                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
@@ -683,22 +818,45 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const unsigned blocks = (unsigned)(nqb * ngroups);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16><<<blocks, C::THREADS, C::LDS_BYTES, st>>>(
-        q, k, v, o, H, Hkv, r.rows, r.nkeys, r.qbase, r.window, scale_log2, nqb, ngroups);
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS>
+        <<<blocks, C::THREADS, C::LDS_BYTES, st>>>(q, k, v, ps, presplit_tlo(r),
+                                                   presplit_nt(r), o, H, Hkv, r.rows, r.nkeys,
+                                                   r.qbase, r.window, scale_log2, nqb, ngroups);
     return eb::check_launch("attn_prefill");
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT>
 eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const void *v,
                            float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
+    const bool plain = r.qbase == 0 && r.window == 0;
+    if constexpr (PrefillCfg<HD, HPW, WPH, KSPLIT>::SPV) {
+        if (r.ws) {
+            const int nt = presplit_nt(r);
+            f32x4 *ps = reinterpret_cast<f32x4 *>(r.ws);
+            const dim3 grid((unsigned)nt, (unsigned)Hkv);
+            if (r.h16)
+                presplit_kernel<HD, true><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
+                                                               presplit_tlo(r), nt);
+            else
+                presplit_kernel<HD, false><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
+                                                                presplit_tlo(r), nt);
+            const eb_status err = eb::check_launch("attn_prefill (pre-split)");
+            if (err != EB_OK) return err;
+            if (plain && !r.h16)
+                return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, true>(
+                    st, q, k, v, ps, o, H, Hkv, r, scale_log2);
+            return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false, true>(
+                st, q, k, v, ps, o, H, Hkv, r, scale_log2);
+        }
+    }
     if (r.h16)
-        return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, true>(st, q, k, v, o, H, Hkv, r,
-                                                                  scale_log2);
-    if (r.qbase == 0 && r.window == 0)
-        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false>(st, q, k, v, o, H, Hkv, r,
-                                                                    scale_log2);
-    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false>(st, q, k, v, o, H, Hkv, r,
-                                                               scale_log2);
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, true, false>(
+            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2);
+    if (plain)
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, false>(
+            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2);
+    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false, false>(
+        st, q, k, v, nullptr, o, H, Hkv, r, scale_log2);
 }
 
 // head_dim <= 128:
@@ -729,14 +887,18 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
         return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: q/k/v/o must be 16-byte aligned");
     const float sl2 = scale * eb::kLog2e;
     const int H = (int)h, Hk = (int)hkv;
+    PrefillRange rr = r;
+    const size_t need = presplit_floats(hd, hkv, r);
+    if (need == 0 || !r.ws || r.ws_floats < need || (reinterpret_cast<uintptr_t>(r.ws) & 15))
+        rr.ws = nullptr;  // stage with the split in the prefill itself
     switch (hd) {
-        case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, r, sl2);
-        case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, r, sl2);
-        case 16: return launch_prefill_hd<16>(st, q, k, v, o, H, Hk, r, sl2);
-        case 32: return launch_prefill_hd<32>(st, q, k, v, o, H, Hk, r, sl2);
-        case 64: return launch_prefill_hd<64>(st, q, k, v, o, H, Hk, r, sl2);
-        case 128: return launch_prefill_hd<128>(st, q, k, v, o, H, Hk, r, sl2);
-        case 256: return launch_prefill_hd<256>(st, q, k, v, o, H, Hk, r, sl2);
+        case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, rr, sl2);
+        case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, rr, sl2);
+        case 16: return launch_prefill_hd<16>(st, q, k, v, o, H, Hk, rr, sl2);
+        case 32: return launch_prefill_hd<32>(st, q, k, v, o, H, Hk, rr, sl2);
+        case 64: return launch_prefill_hd<64>(st, q, k, v, o, H, Hk, rr, sl2);
+        case 128: return launch_prefill_hd<128>(st, q, k, v, o, H, Hk, rr, sl2);
+        case 256: return launch_prefill_hd<256>(st, q, k, v, o, H, Hk, rr, sl2);
         default: return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: head_dim %zu", hd);
     }
 }
@@ -745,29 +907,36 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
 
 namespace eb {
 
+size_t prefill_workspace_floats(size_t hkv, size_t hd, size_t rows, size_t nkeys, size_t qbase,
+                                size_t window) {
+    return presplit_floats(hd, hkv,
+                           PrefillRange{(int)rows, (int)nkeys, (int)qbase, (int)window, false,
+                                        nullptr, 0});
+}
+
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
-                              float *o, size_t h, size_t hkv, size_t s, size_t hd,
-                              float scale) {
+                              float *o, size_t h, size_t hkv, size_t s, size_t hd, float scale,
+                              float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
-                                PrefillRange{(int)s, (int)s, 0, 0, false});
+                                PrefillRange{(int)s, (int)s, 0, 0, false, ws, ws_floats});
 }
 
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
                                     const float *vc, float *o, size_t h, size_t hkv,
                                     size_t pos0, size_t rows, size_t hd, float scale,
-                                    size_t window) {
+                                    size_t window, float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window, false});
+                                             (int)window, false, ws, ws_floats});
 }
 
 eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
                                         const uint16_t *vc, float *o, size_t h, size_t hkv,
                                         size_t pos0, size_t rows, size_t hd, float scale,
-                                        size_t window) {
+                                        size_t window, float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window, true});
+                                             (int)window, true, ws, ws_floats});
 }
 
 }  // namespace eb

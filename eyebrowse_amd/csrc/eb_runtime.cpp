@@ -591,7 +591,7 @@ static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
     EB_TRY(eb::check_ptr(cache, "cache"));
     EB_TRY(eb::check_ptr(src, "src"));
     if (h16) {
-        if (hd % 4 != 0) return fail(EB_UNSUPPORTED_CONFIG, "kv_write: f16 caches need hd % 4 == 0");
+        if (hd % 4 != 0) return fail(EB_UNSUPPORTED_CONFIG, "kv_write: f16 caches need hd %% 4 == 0");
         EB_TRY(eb::launch_kv_write_f16(st, static_cast<uint16_t *>(cache), src, hkv, count, hd,
                                        dst));
     } else {
@@ -600,9 +600,45 @@ static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
     return eb::ok();
 }
 
+static eb_status device_workspace(eb_device *dev, size_t floats, float **out);
+
+// Where a prefill's pre-split workspace comes from: the device's grow-only workspace
+// (recorder launches), the caller's buffer (raw _ws launches; null with 0 floats is allowed
+// only where the shape needs none), or nowhere (raw launches without one: the prefill
+// splits K/V while staging).
+struct PrefillWs {
+    eb_device *dev = nullptr;
+    bool caller = false;
+    float *ptr = nullptr;
+    size_t floats = 0;
+};
+
+static eb_status prefill_ws(const PrefillWs &src, size_t hkv, size_t hd, size_t rows,
+                            size_t nkeys, size_t qbase, size_t window, float **ws, size_t *wsn) {
+    *ws = nullptr;
+    *wsn = 0;
+    if (!src.dev && !src.caller) return EB_OK;
+    const size_t need = eb::prefill_workspace_floats(hkv, hd, rows, nkeys, qbase, window);
+    if (need == 0) return EB_OK;
+    if (src.dev) {
+        EB_TRY(device_workspace(src.dev, need, ws));
+    } else {
+        if (src.floats < need)
+            return fail(EB_SHAPE_MISMATCH, "attn_prefill: workspace holds %zu floats, needs %zu",
+                        src.floats, need);
+        EB_TRY(eb::check_ptr(src.ptr, "workspace"));
+        if (reinterpret_cast<uintptr_t>(src.ptr) & 15)
+            return fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: workspace must be 16-byte aligned");
+        *ws = src.ptr;
+    }
+    *wsn = need;
+    return EB_OK;
+}
+
 static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, const float *k,
                                  size_t kn, const float *v, size_t vn, float *o, size_t on,
-                                 size_t h, size_t hkv, size_t s, size_t hd, float scale) {
+                                 size_t h, size_t hkv, size_t s, size_t hd, float scale,
+                                 const PrefillWs &wsrc = PrefillWs()) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
@@ -616,7 +652,10 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     EB_TRY(eb::check_ptr(k, "k"));
     EB_TRY(eb::check_ptr(v, "v"));
     EB_TRY(eb::check_ptr(o, "o"));
-    EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale));
+    float *ws;
+    size_t wsn;
+    EB_TRY(prefill_ws(wsrc, hkv, hd, s, s, 0, 0, &ws, &wsn));
+    EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
     return eb::ok();
 }
 
@@ -624,7 +663,8 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
                                        const void *kc, size_t kcn, const void *vc, size_t vcn,
                                        float *o, size_t on, size_t h, size_t hkv, size_t pos0,
                                        size_t rows, size_t hd, size_t max_seq, float scale,
-                                       size_t window, bool h16 = false) {
+                                       size_t window, bool h16 = false,
+                                       const PrefillWs &wsrc = PrefillWs()) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
@@ -644,14 +684,17 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     EB_TRY(eb::check_ptr(kc, "kcache"));
     EB_TRY(eb::check_ptr(vc, "vcache"));
     EB_TRY(eb::check_ptr(o, "o"));
+    float *ws;
+    size_t wsn;
+    EB_TRY(prefill_ws(wsrc, hkv, hd, rows, pos0 + rows, pos0, window, &ws, &wsn));
     if (h16)
         EB_TRY(eb::launch_attn_prefill_chunk_f16(st, q, static_cast<const uint16_t *>(kc),
                                                  static_cast<const uint16_t *>(vc), o, h, hkv,
-                                                 pos0, rows, hd, scale, window));
+                                                 pos0, rows, hd, scale, window, ws, wsn));
     else
         EB_TRY(eb::launch_attn_prefill_chunk(st, q, static_cast<const float *>(kc),
                                              static_cast<const float *>(vc), o, h, hkv, pos0,
-                                             rows, hd, scale, window));
+                                             rows, hd, scale, window, ws, wsn));
     return eb::ok();
 }
 
@@ -857,7 +900,7 @@ eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor 
     return prefill_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
                            (const float *)k->ptr, eb_tensor_numel(k), (const float *)v->ptr,
                            eb_tensor_numel(v), (float *)o->ptr, eb_tensor_numel(o), h, hkv, s,
-                           hd, scale);
+                           hd, scale, PrefillWs{rec->dev});
 }
 
 eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
@@ -878,7 +921,8 @@ eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_t
     return prefill_chunk_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
                                  kcache->ptr, eb_tensor_numel(kcache), vcache->ptr,
                                  eb_tensor_numel(vcache), (float *)o->ptr, eb_tensor_numel(o), h,
-                                 hkv, pos0, rows, hd, max_seq, scale, window, h16);
+                                 hkv, pos0, rows, hd, max_seq, scale, window, h16,
+                                 PrefillWs{rec->dev});
 }
 
 eb_status eb_attn_decode_window(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
@@ -1036,6 +1080,44 @@ eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_nu
                                        size_t max_seq, float scale, size_t window) {
     return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
                                  o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window);
+}
+
+size_t eb_attn_prefill_workspace_floats(size_t hkv, size_t hd, size_t pos0, size_t rows,
+                                        size_t window) {
+    if (hkv == 0 || !eb::attn_head_dim_supported(hd)) return 0;
+    return eb::prefill_workspace_floats(hkv, hd, rows, pos0 + rows, pos0, window);
+}
+
+eb_status eb_launch_attn_prefill_ws(void *stream, const float *q, size_t q_numel, const float *k,
+                                    size_t k_numel, const float *v, size_t v_numel, float *o,
+                                    size_t o_numel, size_t h, size_t hkv, size_t s, size_t hd,
+                                    float scale, float *workspace, size_t workspace_floats) {
+    return prefill_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
+                           h, hkv, s, hd, scale,
+                           PrefillWs{nullptr, true, workspace, workspace_floats});
+}
+
+eb_status eb_launch_attn_prefill_chunk_ws(void *stream, const float *q, size_t q_numel,
+                                          const float *kc, size_t kc_numel, const float *vc,
+                                          size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                          size_t hkv, size_t pos0, size_t rows, size_t hd,
+                                          size_t max_seq, float scale, size_t window,
+                                          float *workspace, size_t workspace_floats) {
+    return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window, false,
+                                 PrefillWs{nullptr, true, workspace, workspace_floats});
+}
+
+eb_status eb_launch_attn_prefill_chunk_f16_ws(void *stream, const float *q, size_t q_numel,
+                                              const uint16_t *kc, size_t kc_numel,
+                                              const uint16_t *vc, size_t vc_numel, float *o,
+                                              size_t o_numel, size_t h, size_t hkv, size_t pos0,
+                                              size_t rows, size_t hd, size_t max_seq,
+                                              float scale, size_t window, float *workspace,
+                                              size_t workspace_floats) {
+    return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window, true,
+                                 PrefillWs{nullptr, true, workspace, workspace_floats});
 }
 
 size_t eb_attn_decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd,

@@ -139,6 +139,27 @@ def launch_attn_prefill(stream: int, q: int, q_numel: int, k: int, k_numel: int,
                                        h, hkv, s, hd, scale))
 
 
+def attn_prefill_workspace_floats(hkv: int, hd: int, pos0: int, rows: int, window: int = 0) -> int:
+    """Floats of workspace the _ws prefill launches need for this shape (0: no pre-split)."""
+    return int(lib().eb_attn_prefill_workspace_floats(hkv, hd, pos0, rows, window))
+
+
+def launch_attn_prefill_ws(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                           v_numel: int, o: int, o_numel: int, h: int, hkv: int, s: int, hd: int,
+                           scale: float, ws: int, ws_floats: int) -> None:
+    check(lib().eb_launch_attn_prefill_ws(stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                          o_numel, h, hkv, s, hd, scale, ws, ws_floats))
+
+
+def launch_attn_prefill_chunk_ws(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
+                                 vc: int, vc_numel: int, o: int, o_numel: int, h: int, hkv: int,
+                                 pos0: int, rows: int, hd: int, max_seq: int, scale: float,
+                                 window: int, ws: int, ws_floats: int, f16: bool = False) -> None:
+    fn = lib().eb_launch_attn_prefill_chunk_f16_ws if f16 else lib().eb_launch_attn_prefill_chunk_ws
+    check(fn(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos0, rows, hd,
+             max_seq, scale, window, ws, ws_floats))
+
+
 def launch_attn_prefill_chunk(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
                               vc: int, vc_numel: int, o: int, o_numel: int, h: int, hkv: int,
                               pos0: int, rows: int, hd: int, max_seq: int, scale: float,
