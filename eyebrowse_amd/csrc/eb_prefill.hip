@@ -60,9 +60,26 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// x - f32(h), h the low (sub_f16_lo) or high (sub_f16_hi) half of a packed pair, in one
+// mixed-precision fma (exact here: x - h fits f32 when h = f16(x)).
+__device__ __forceinline__ float sub_f16_lo(unsigned h2, float x) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h2), "v"(x));
+    return d;
+}
+__device__ __forceinline__ float sub_f16_hi(unsigned h2, float x) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h2), "v"(x));
+    return d;
+}
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
 constexpr float kSlack = 8.0f;  // log2 units the reference max may lag a score (SPV)
+constexpr int kUnitSlack = 8;   // bits a P V term may exceed its query's O^T unit (SPV)
 
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -350,7 +367,6 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     constexpr int HALF = C::HALF;
     constexpr int NB = C::NB;
     constexpr int KS = C::KS;
-    constexpr int THREADS = C::THREADS;
 
     extern __shared__ float smem[];  // [2][BUF]: K rows [STEP_KEYS][KS], V rows [STEP_KEYS][HD]
 
@@ -402,8 +418,10 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
         for (int k2 = 0; k2 < NKS; ++k2) {
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            qa[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) : z;
-            qb[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) : z;
+            // The softmax scale (log2 units) is applied to q before its split, so the
+            // product needs no multiply per score.
+            qa[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) * scale_log2 : z;
+            qb[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) * scale_log2 : z;
             const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
                                          fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
                                    fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
@@ -529,16 +547,19 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             const bool edge =
                 RANGE ? (kb + kTile - 1 > wp0 || (window > 0 && kb <= wp1 - window)) : kb == q0;
             float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                p[r] = C::SQK ? ldexpf(sacc[r], eq + ek[r]) : sacc[r] * scale_log2;
+            if (edge) {  // wave-uniform: most tiles skip the per-key mask
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (key > pi || (RANGE && window > 0 && key <= pi - window)) p[r] = -INFINITY;
+                }
+            }
             float mt = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-                float x = (C::SQK ? ldexpf(sacc[r], eq + ek[r]) : sacc[r]) * scale_log2;
-                if (edge && (key > pi || (RANGE && window > 0 && key <= pi - window)))
-                    x = -INFINITY;
-                p[r] = x;
-                mt = fmaxf(mt, x);
-            }
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
             mt = fmaxf(mt, __shfl_xor(mt, 32));
             // SPV: lazy reference max. m moves only when a score exceeds it by more than
             // kSlack (log2 units), so most tiles need no rescale of l and O^T; terms
@@ -589,11 +610,14 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 tx = max(tx, __shfl_xor(tx, 32));
                 // The softmax correction 2^-(mref - mold) moves the accumulated terms down:
                 // the unit follows by whole bits, the fraction goes into the rescale factor.
+                // The unit moves up only for a term more than 2^kUnitSlack above it (then
+                // to that term): p' <= 2^kUnitSlack, which f16 holds, and most tiles keep
+                // the unit, so the wave skips the rescale.
                 const float dm = mref - mold;
                 const int Eb = !grow ? E : (dm < 1000.0f ? max(E - (int)dm, kZeroRowExp) : kZeroRowExp);
-                const int En = max(Eb, tx);
+                const int En = tx > Eb + kUnitSlack ? tx : Eb;
                 if (__builtin_amdgcn_ballot_w64(grow || En != E) != 0) {
-                    const float f = ldexpf(corr, E - En);  // <= 1
+                    const float f = ldexpf(corr, E - En);  // <= 1 (grow) or 2^(E - En) <= 1
 #pragma unroll
                     for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
@@ -603,14 +627,19 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 // P^T operands: k-step u takes this lane's keys r = 8u .. 8u+7.
                 f16x8 ph[2], pl[2];
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < 2; ++u) {
+                    unsigned hw[4], lw[4];
 #pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        const float pp = ldexpf(p[8 * u + c], ev[8 * u + c] - E);
-                        const _Float16 hh = (_Float16)pp;
-                        ph[u][c] = hh;
-                        pl[u][c] = (_Float16)(pp - (float)hh);
+                    for (int c2 = 0; c2 < 4; ++c2) {
+                        const int r = 8 * u + 2 * c2;
+                        const f32x2 pp = {ldexpf(p[r], ev[r] - E), ldexpf(p[r + 1], ev[r + 1] - E)};
+                        hw[c2] = __builtin_bit_cast(unsigned, __builtin_convertvector(pp, f16x2));
+                        const f32x2 rem = {sub_f16_lo(hw[c2], pp.x), sub_f16_hi(hw[c2], pp.y)};
+                        lw[c2] = __builtin_bit_cast(unsigned, __builtin_convertvector(rem, f16x2));
                     }
+                    ph[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+                    pl[u] = __builtin_bit_cast(f16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+                }
                 // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the
                 // output stage expects), stored at V^T row 32*mb + col; keys 16u + 4hf +
                 // 0..3 and 16u + 8 + 4hf + 0..3 of this wave's tile (the order of ph / pl).
