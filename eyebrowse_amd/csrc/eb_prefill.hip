@@ -414,14 +414,16 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         const bool qv = qi < rows;
         const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * HD + 8 * hf;
         f32x4 qa[NKS], qb[NKS];
+        const float qs = qv ? scale_log2 : 0.0f;
         float mx = 0.0f;
 #pragma unroll
         for (int k2 = 0; k2 < NKS; ++k2) {
-            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
             // The softmax scale (log2 units) is applied to q before its split, so the
-            // product needs no multiply per score.
-            qa[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) * scale_log2 : z;
-            qb[k2] = qv ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) * scale_log2 : z;
+            // product needs no multiply per score. Every lane loads (rows past the end
+            // from the clamped row 0) and scales by qs, 0 past the end, so that the loads
+            // issue back to back; such a lane's query column never reaches the output.
+            qa[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2) * qs;
+            qb[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) * qs;
             const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
                                          fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
                                    fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
