@@ -205,8 +205,11 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
 }
 
 // H16: the caches hold IEEE half elements (converted to f32 as they are loaded).
+// Two wave steps per iteration for f32 head_dim 256 (4 rows per wave step there): measured
+// +4 % at 16k keys; head_dim 128 measured slower with two (its query heads per workgroup
+// then fill the register file).
 template <int HD, int G, bool H16>
-using DecodeShapeOf = DecodeShape<HD, G, H16 ? EB_DECODE_U16 : 1>;
+using DecodeShapeOf = DecodeShape<HD, G, H16 ? EB_DECODE_U16 : (HD == 256 ? 2 : 1)>;
 
 template <int HD, int G, bool H16>
 __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G <= 2 ? 2 : 1))) void decode_kernel(DecodeArgs a) {
