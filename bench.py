@@ -307,9 +307,9 @@ def decode_extras(eb, hip, dev, sc128) -> dict:
 
 def prefill_extras(eb, hip, dev, sc128) -> dict:
     """Causal prefill TFLOP/s (2*H*hd*T*(T+1) algorithmic FLOPs) for the BASELINE prefill
-    configs, HIP events around back-to-back launches. head_dim 128: each step is the
-    pre-split pass plus the attention kernel (eb_launch_attn_prefill_ws); the plain raw
-    launch, which splits K/V while staging them, is reported beside it."""
+    configs, HIP events around back-to-back launches. Each step is the pre-split pass plus
+    the attention kernel (eb_launch_attn_prefill_ws); the plain raw launch, which splits K/V
+    while staging them, is reported beside it."""
     out = {}
     cfgs = [("qwen_T512", 16, 8, 128, 512, sc128),
             ("qwen_T2048", 16, 8, 128, 2048, sc128),
@@ -323,9 +323,8 @@ def prefill_extras(eb, hip, dev, sc128) -> dict:
         reps = 20 if T >= 2048 else 100
         t = hip.time_loop(dev.stream, reps, lambda i: p.launch())
         tf_s = p.flops / (t * 1e-3) / 1e12
-        # head_dim 128: both products on the f16 matrix cores as three split products each
-        # (f32 accuracy); head_dim 256: Q K^T split, V^T P^T on the FP32 instruction
-        f16_work = 3 * tf_s if hd <= 128 else 1.5 * tf_s
+        # both products on the f16 matrix cores as three split products each (f32 accuracy)
+        f16_work = 3 * tf_s
         staged = {}
         if p.ws is not None:
             ps = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc, presplit=False)
@@ -337,9 +336,7 @@ def prefill_extras(eb, hip, dev, sc128) -> dict:
             "gflop": round(p.flops / 1e9, 3), "ms": round(t, 4), "TFLOPs": round(tf_s, 2),
             "path": "pre-split pass + attention" if p.ws is not None else "attention",
             **staged,
-            "mfma": ("f16 split x3 (v_mfma_f32_32x32x16_f16) for Q K^T and V^T P^T"
-                     if hd <= 128 else
-                     "f16 split x3 for Q K^T, fp32 (v_mfma_f32_32x32x2_f32) for V^T P^T"),
+            "mfma": "f16 split x3 (v_mfma_f32_32x32x16_f16) for Q K^T and V^T P^T",
             "frac_fp32_mfma_peak": round(tf_s / FP32_MFMA_PEAK_TFLOPS, 4),
             "f16_mfma_work_TFLOPs": round(f16_work, 1),
             "frac_f16_mfma_peak_of_mfma_work": round(f16_work / F16_MFMA_PEAK_TFLOPS, 4)}

@@ -16,8 +16,8 @@
 //      S^T[key][query] = K Q^T         (contraction over head_dim)
 //      O^T[d][query]  += V^T P^T       (contraction over the 32 keys of a tile)
 //  - For head_dim >= 32 both run on the f16 matrix cores (v_mfma_f32_32x32x16_f16) at
-//    about f32 accuracy (head_dim 256 keeps V^T P^T on v_mfma_f32_32x32x2_f32, whose
-//    register budget the split would exceed; head_dim < 32 uses it for both):
+//    about f32 accuracy (head_dim < 32 uses v_mfma_f32_32x32x2_f32 for both; at head_dim
+//    256 the split fills 256 VGPRs and about 200 AGPRs, one wave per SIMD):
 //      - every K, Q and V row is scaled by a power of two (its largest magnitude lands in
 //        [2^14, 2^15)) and split exactly into hi = f16(x') and lo = f16(x' - hi), so
 //        x' = hi + lo to about 2^-22; all-zero rows get an exponent below every real one;
@@ -106,17 +106,24 @@ struct PrefillCfg {
     static constexpr bool SQK = HD >= 32;
     // V^T P^T the same way (V rows scaled and split at staging, stored transposed as
     // [HD][VROW] halves, hi then lo; P scaled per key and split in registers).
-    static constexpr bool SPV = HD >= 32 && HD <= 128;  // (256: registers would spill)
+    static constexpr bool SPV = HD >= 32;
     static constexpr int VROW = STEP_KEYS + 8;  // halves per V^T row (16-byte aligned reads
                                                 // of consecutive rows spread over the banks)
     static constexpr int VFL = SPV ? HD * VROW : STEP_KEYS * HD;  // floats of V per buffer
-    static constexpr int BUF = STEP_KEYS * KS + VFL + 2 * STEP_KEYS;  // + K and V exponents
-    // Pre-split K/V (SPV): one record per (KV head, 32-key tile) of 16-byte chunks: K rows
-    // [32][HD floats of hi then lo halves], V^T hi [HD][32 halves], V^T lo, K exponents
-    // [32], V exponents [32]. A step copies KSPLIT records into LDS.
+    // + K and V exponents; whole KiB, so that a buffer takes memory-to-LDS copies exactly
+    static constexpr int BUF = (STEP_KEYS * KS + VFL + 2 * STEP_KEYS + 255) / 256 * 256;
+    // Pre-split K/V (SPV): one record per (KV head, 32-key tile).
+    //  - head_dim <= 128: 16-byte chunks K rows [32][HD floats of hi then lo halves], V^T hi
+    //    [HD][32 halves], V^T lo, K exponents [32], V exponents [32]; a step copies KSPLIT
+    //    records into LDS through registers.
+    //  - head_dim 256 (one key split, so a step's buffer is one tile): the buffer's LDS
+    //    image itself, copied with memory-to-LDS loads (the register copy would hold 68
+    //    VGPRs where the split already fills the register file).
+    static constexpr bool PS_IMAGE = HD > 128;
     static constexpr int PS_CH = 16 * HD + 16;          // chunks per record
+    static constexpr int PS_FLOATS = PS_IMAGE ? BUF : 4 * PS_CH;  // floats per record
     static constexpr int PS_KV = KSPLIT * 16 * HD;      // K/V chunks per step
-    static constexpr int PSN = (PS_KV + THREADS - 1) / THREADS + 1;  // + one exponent chunk
+    static constexpr int PSN = PS_IMAGE ? 1 : (PS_KV + THREADS - 1) / THREADS + 1;  // + exps
     static constexpr int REC = 3 + 16 * NB;  // merged fields per lane: m, l, V unit, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
     static constexpr int OS = HD + 4;                  // output staging row stride (floats)
@@ -240,6 +247,21 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                 // then walks consecutive rows). Rows j and j + 1 (lanes i and i ^ HD/4) pair
                 // their halves: the even row's lane writes dims 0, 1 of its four, the odd
                 // row's lane dims 2, 3, each as one 32-bit (key j, key j + 1) word.
+                if constexpr (HD / 4 > 32) {
+                    // A row spans the whole wave (no partner row in it): halves one by one,
+                    // at the same permuted key position as below.
+                    const int g4s = (row >> 2) & 3;
+                    const int js = (row & ~15) | (((g4s & 1) << 1 | (g4s >> 1)) << 2) | (row & 3);
+                    _Float16 *vth16 = reinterpret_cast<_Float16 *>(Vb);
+                    _Float16 *vtl16 = vth16 + HD * C::VROW;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int d = c4 * 4 + i;
+                        const int pr = (d % C::NB) * 32 + d / C::NB;
+                        vth16[pr * C::VROW + js] = vh[i];
+                        vtl16[pr * C::VROW + js] = vl[i];
+                    }
+                } else {
                 using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
                 const u32x2 ho = __builtin_bit_cast(u32x2, vh), lw = __builtin_bit_cast(u32x2, vl);
                 const u32x2 hp = {lane_xor_u<HD / 4>(ho.x), lane_xor_u<HD / 4>(ho.y)};
@@ -263,6 +285,7 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     using h2 = __attribute__((ext_vector_type(2))) _Float16;
                     vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
                     vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
+                }
                 }
                 if (c4 == 0) Ev[row] = ev;
             } else {
@@ -332,7 +355,7 @@ __device__ __forceinline__ void ps_store_step(float *smem, const f32x4 (&r)[C::P
 template <int HD, bool H16>
 __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ k,
                                                        const void *__restrict__ v,
-                                                       f32x4 *__restrict__ ps, int nkeys,
+                                                       float *__restrict__ ps, int nkeys,
                                                        int Hkv, int tlo, int nt) {
     using C = PrefillCfg<HD, 4, 1, 1>;  // 256 threads, one 32-key tile per step
     static_assert(C::SPV, "pre-split needs the split V path");
@@ -340,13 +363,49 @@ __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ 
     const int t = blockIdx.x;
     const int kvh = blockIdx.y;
     const int tid = threadIdx.x;
+    if constexpr (C::PS_IMAGE) {  // the image's padding: zeros
+        for (int i = tid; i < C::BUF; i += C::THREADS) smem[i] = 0.0f;
+        __syncthreads();
+    }
     f32x4 rk[C::NLD], rv[C::NLD];
     prefill_load_step<C, H16>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
-    f32x4 *rec = ps + ((size_t)kvh * nt + t) * C::PS_CH;
-    for (int c = tid; c < C::PS_CH; c += C::THREADS)
-        rec[c] = *reinterpret_cast<const f32x4 *>(smem + ps_lds_offset<C>(0, c));
+    f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::PS_FLOATS);
+    if constexpr (C::PS_IMAGE) {
+        for (int c = tid; c < C::BUF / 4; c += C::THREADS)
+            rec[c] = reinterpret_cast<const f32x4 *>(smem)[c];
+    } else {
+        for (int c = tid; c < C::PS_CH; c += C::THREADS)
+            rec[c] = *reinterpret_cast<const f32x4 *>(smem + ps_lds_offset<C>(0, c));
+    }
+}
+
+// Copy the image record of tile `tile` (clamped to the last record, nt - 1: a clamped
+// buffer is never read) of one KV head (recs) into LDS buffer `buf` with memory-to-LDS
+// loads: each wave instruction moves 1 KiB, lane i writing bytes 16i .. 16i + 15 of it.
+// Issued as inline assembly, which the compiler's wait counting does not see (it would
+// otherwise wait for these loads before every read of the other buffer); the loads are
+// complete after wait_vm_all().
+template <class C>
+__device__ __forceinline__ void ps_copy_image(const float *__restrict__ recs, float *smem,
+                                              int buf, int tile, int nt, int wave, int lane) {
+    static_assert(C::PS_IMAGE && C::STEP_KEYS == kTile, "one image record per step");
+    const int t = min(tile, nt - 1);
+    for (int j = wave; j < C::BUF / 256; j += C::NW) {
+        const float *src = recs + (size_t)t * C::PS_FLOATS + j * 256 + lane * 4;
+        const unsigned dst =
+            (unsigned)(uintptr_t)(__attribute__((address_space(3))) float *)(smem + buf * C::BUF +
+                                                                              j * 256);
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                     :
+                     : "s"(__builtin_amdgcn_readfirstlane(dst)), "v"(src)
+                     : "memory", "m0");
+    }
+}
+
+__device__ __forceinline__ void wait_vm_all() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
@@ -359,7 +418,7 @@ template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
-    const f32x4 *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
+    const float *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
     int Hkv, int rows, int nkeys, int qbase, int window, float scale_log2, int nqb,
     int ngroups) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
@@ -475,9 +534,12 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
     f32x4 rs[PS ? C::PSN : 1];
-    const f32x4 *recs = PS ? ps + (size_t)kvh * ps_nt * C::PS_CH : nullptr;
-    if constexpr (PS) {
-        ps_load_step<C>(recs, rs, t0 - ps_tlo, ps_nt, tid);
+    const float *recs = PS ? ps + (size_t)kvh * ps_nt * C::PS_FLOATS : nullptr;
+    if constexpr (PS && C::PS_IMAGE) {
+        ps_copy_image<C>(recs, smem, 0, t0 - ps_tlo, ps_nt, wave, lane);
+        wait_vm_all();
+    } else if constexpr (PS) {
+        ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, t0 - ps_tlo, ps_nt, tid);
         ps_store_step<C>(smem, rs, 0, tid);
     } else {
         prefill_load_step<C, H16>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
@@ -491,8 +553,14 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         const int kb = tile * kTile;
         // Prefetch the next step (past the last step this re-reads clamped rows; the
         // buffer written from them is never read).
-        if constexpr (PS)
-            ps_load_step<C>(recs, rs, t0 + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
+        // PS image records go straight into the other buffer, which every wave finished
+        // reading before the last barrier.
+        if constexpr (PS && C::PS_IMAGE)
+            ps_copy_image<C>(recs, smem, buf ^ 1, t0 + (it + 1) * KSPLIT - ps_tlo, ps_nt, wave,
+                             lane);
+        else if constexpr (PS)
+            ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
+                            t0 + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
         else
             prefill_load_step<C, H16>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys,
                                       Hkv, kvh, tid);
@@ -701,7 +769,9 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             }
         }
 
-        if constexpr (PS)
+        if constexpr (PS && C::PS_IMAGE)
+            wait_vm_all();
+        else if constexpr (PS)
             ps_store_step<C>(smem, rs, buf ^ 1, tid);
         else
             prefill_store_step<C>(smem, rk, rv, buf ^ 1, tid);
@@ -827,13 +897,17 @@ int presplit_tlo(const PrefillRange &r) {
 int presplit_nt(const PrefillRange &r) { return (r.nkeys + kTile - 1) / kTile - presplit_tlo(r); }
 
 size_t presplit_floats(size_t hd, size_t hkv, const PrefillRange &r) {
-    if (hd < 32 || hd > 128 || r.rows < kPresplitMinRows || r.nkeys <= 0) return 0;
-    return hkv * (size_t)presplit_nt(r) * (16 * hd + 16) * 4;
+    if (hd < 32 || r.rows < kPresplitMinRows || r.nkeys <= 0) return 0;
+    const size_t rec = hd == 32    ? PrefillCfg<32, 4, 1, 1>::PS_FLOATS
+                       : hd == 64  ? PrefillCfg<64, 4, 1, 1>::PS_FLOATS
+                       : hd == 128 ? PrefillCfg<128, 4, 1, 1>::PS_FLOATS
+                                   : PrefillCfg<256, 4, 1, 1>::PS_FLOATS;
+    return hkv * (size_t)presplit_nt(r) * rec;
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
 eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
-                           const f32x4 *ps, float *o, int H, int Hkv, const PrefillRange &r,
+                           const float *ps, float *o, int H, int Hkv, const PrefillRange &r,
                            float scale_log2) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     static std::once_flag once;
@@ -863,7 +937,7 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
     if constexpr (PrefillCfg<HD, HPW, WPH, KSPLIT>::SPV) {
         if (r.ws) {
             const int nt = presplit_nt(r);
-            f32x4 *ps = reinterpret_cast<f32x4 *>(r.ws);
+            float *ps = r.ws;
             const dim3 grid((unsigned)nt, (unsigned)Hkv);
             if (r.h16)
                 presplit_kernel<HD, true><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,

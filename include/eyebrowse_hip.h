@@ -211,7 +211,7 @@ eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_nu
                                        size_t vc_numel, float *o, size_t o_numel, size_t h,
                                        size_t hkv, size_t pos0, size_t rows, size_t hd,
                                        size_t max_seq, float scale, size_t window);
-/* Prefill with a pre-split pass (no counterpart in the reference): with head_dim 32..128
+/* Prefill with a pre-split pass (no counterpart in the reference): with head_dim 32..256
  * and at least 256 query rows, the _ws launches first split every key they can see once
  * into workspace records (K and V rows scaled by powers of two into f16 hi/lo halves, V
  * transposed), so that the attention kernel only copies them into LDS; the plain raw

@@ -76,9 +76,10 @@ def _sampled_rows(T):
     ("qwen", 16, 8, 128, 2048, None),
     ("qwen", 16, 8, 128, 4096, None),
     ("mistral", 32, 8, 128, 4096, None),
+    ("gemma", 16, 8, 256, 4096, 1.0),   # BASELINE config 5 (the global layer: hd 256, scale 1)
 ])
 def test_baseline_prefill_configs(dev, name, H, Hkv, hd, T, scale):
-    """BASELINE configs 3 and 4 at full size: K/V written by kv_write into a max_seq = T
+    """BASELINE configs 3, 4 and 5 at full size: K/V written by kv_write into a max_seq = T
     cache, prefill over the fresh K/V (attention.rs:78-115), compared with the oracle on
     row samples at the start, middle and end of the sequence."""
     note(f"prefill {name} T={T}")

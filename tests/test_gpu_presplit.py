@@ -37,6 +37,9 @@ def recorder_and_raw_prefill(dev, q, k, v, h, hkv, s, hd, sc):
     (8, 8, 297, 64),
     (4, 2, 300, 32),
     (16, 8, 256, 128),   # exactly the threshold, whole tiles
+    (16, 8, 300, 256),   # head_dim 256: image records copied memory-to-LDS, 2 heads x 2 blocks
+    (32, 8, 257, 256),   # head_dim 256, 4 heads per workgroup
+    (8, 8, 290, 256),    # head_dim 256, MHA: 4 query blocks per workgroup
 ])
 def test_prefill_presplit_equals_staged_split(dev, h, hkv, s, hd):
     note(f"presplit prefill h={h} hkv={hkv} s={s} hd={hd}")
@@ -49,12 +52,13 @@ def test_prefill_presplit_equals_staged_split(dev, h, hkv, s, hd):
     assert_close(a[rows[0]:rows[0] + rows[1]], want[rows[0]:rows[0] + rows[1]], what="pre-split")
 
 
-def test_prefill_presplit_special_rows(dev):
+@pytest.mark.parametrize("hd", [128, 256])
+def test_prefill_presplit_special_rows(dev, hd):
     """Zero K/V rows (kept below every real exponent), rows of very different magnitudes,
     and an inf in one V row at key 224 (the first key of a tile, so no earlier query's wave
     reads it)."""
-    note("presplit special rows")
-    h, hkv, s, hd = 16, 8, 320, 128
+    note(f"presplit special rows hd={hd}")
+    h, hkv, s = 16, 8, 320
     sc = float(oracle.default_scale(hd))
     q, k, v = oracle.randn((s, h, hd), 41), oracle.randn((s, hkv, hd), 42), oracle.randn((s, hkv, hd), 43)
     k[5], v[7] = 0.0, 0.0
@@ -102,6 +106,8 @@ def chunk_pair(dev, q, kc, vc, h, hkv, pos0, rows, hd, max_seq, sc, window, f16)
     (16, 8, 128, 300, 260, 100, False),  # windowed continuation: records start past tile 0
     (16, 8, 128, 70, 280, 0, True),      # f16 cache
     (24, 8, 128, 500, 300, 77, True),    # f16 cache, GQA 3, window
+    (16, 8, 256, 100, 300, 0, False),    # head_dim 256 continuation
+    (16, 8, 256, 300, 260, 100, True),   # head_dim 256, f16 cache, window
 ])
 def test_chunk_presplit_equals_staged_split(dev, h, hkv, hd, pos0, rows, window, f16):
     note(f"presplit chunk h={h} hd={hd} pos0={pos0} rows={rows} window={window} f16={f16}")
