@@ -204,7 +204,7 @@ class PrefillWorkload:
         self.o = eb.Tensor.empty(dev, (T, H, hd))
         # The pre-split workspace (head_dim 32..128, T >= 256): K/V split once per key, then
         # the attention kernel; both launches are inside every timed step.
-        self.ws_floats = eb.attn_prefill_workspace_floats(Hkv, hd, 0, T) if presplit else 0
+        self.ws_floats = eb.attn_prefill_workspace_floats(H, Hkv, hd, 0, T) if presplit else 0
         self.ws = eb.Tensor.empty(dev, (self.ws_floats,)) if self.ws_floats else None
 
     def launch(self):
@@ -341,6 +341,41 @@ def prefill_extras(eb, hip, dev, sc128) -> dict:
             "f16_mfma_work_TFLOPs": round(f16_work, 1),
             "frac_f16_mfma_peak_of_mfma_work": round(f16_work / F16_MFMA_PEAK_TFLOPS, 4)}
         del p
+        dev.synchronize()
+    out.update(chunk_extras(eb, hip, dev))
+    return out
+
+
+def chunk_extras(eb, hip, dev) -> dict:
+    """Chunked prefill (a prompt continuation attending a filled cache): `rows` new query
+    rows at positions pos0.. over [max_seq, hkv, hd] f32 caches, through
+    eb_launch_attn_prefill_chunk_ws (pre-split pass where rows >= 256, key chunks merged by
+    a second launch). FLOPs 4*H*hd*sum_r(pos0 + r + 1)."""
+    rng = np.random.default_rng(5)
+    out = {}
+    for name, H, Hkv, hd, pos0, rows in (("qwen_128_over_8k", 16, 8, 128, 8064, 128),
+                                         ("mistral_256_over_32k", 32, 8, 128, 32512, 256)):
+        ms = pos0 + rows
+        q = eb.Tensor.from_f32(dev, (rows, H, hd), randn(rng, (rows, H, hd)))
+        kc = eb.Tensor.from_f32(dev, (ms, Hkv, hd), randn(rng, (ms, Hkv, hd)))
+        vc = eb.Tensor.from_f32(dev, (ms, Hkv, hd), randn(rng, (ms, Hkv, hd)))
+        o = eb.Tensor.empty(dev, (rows, H, hd))
+        need = eb.attn_prefill_workspace_floats(H, Hkv, hd, pos0, rows)
+        ws = eb.Tensor.empty(dev, (max(need, 1),))
+        sc = float(1.0 / np.sqrt(hd))
+
+        def launch(_i):
+            eb.launch_attn_prefill_chunk_ws(dev.stream, q.data_ptr, q.numel(), kc.data_ptr,
+                                            kc.numel(), vc.data_ptr, vc.numel(), o.data_ptr,
+                                            o.numel(), H, Hkv, pos0, rows, hd, ms, sc, 0,
+                                            ws.data_ptr, need)
+        for _ in range(2):
+            launch(0)
+        t = hip.time_loop(dev.stream, 10, launch)
+        flops = 4.0 * H * hd * (rows * (pos0 + 1) + rows * (rows - 1) / 2)
+        out[f"prefill_chunk_{name}"] = {"gflop": round(flops / 1e9, 3), "ms": round(t, 4),
+                                        "TFLOPs": round(flops / (t * 1e-3) / 1e12, 2)}
+        del q, kc, vc, o, ws
         dev.synchronize()
     return out
 

@@ -91,7 +91,8 @@ SIGNATURES = {
     "eb_launch_attn_prefill_chunk": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,
                                             c_vp, c_size, c_size, c_size, c_size, c_size,
                                             c_size, c_size, c_float, c_size]),
-    "eb_attn_prefill_workspace_floats": (c_size, [c_size, c_size, c_size, c_size, c_size]),
+    "eb_attn_prefill_workspace_floats": (c_size, [c_size, c_size, c_size, c_size, c_size,
+                                                  c_size]),
     "eb_launch_attn_prefill_ws": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
                                          c_size, c_size, c_size, c_size, c_size, c_float, c_vp,
                                          c_size]),

@@ -47,11 +47,12 @@ int current_cu_count();
 // ---- kernel launchers (validated arguments, caller's stream) -------------------------
 eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t hkv,
                           size_t count, size_t hd, size_t dst_start);
-// Prefill workspace: floats of the pre-split K/V records for this shape (0: the prefill
-// splits K/V while staging). Launches given at least that much (16-byte aligned) run the
-// pre-split pass first; with less they stage as without. No initialisation needed.
-size_t prefill_workspace_floats(size_t hkv, size_t hd, size_t rows, size_t nkeys, size_t qbase,
-                                size_t window);
+// Prefill workspace: floats of the pre-split K/V records and of the key-chunk partials for
+// this shape (0: neither is used). Launches given at least that much (16-byte aligned)
+// run the pre-split pass and split the keys into chunks where that pays; with less they
+// do neither. No initialisation needed.
+size_t prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t rows, size_t nkeys,
+                                size_t qbase, size_t window);
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale, float *ws = nullptr, size_t ws_floats = 0);

@@ -50,6 +50,7 @@
 #include "eb_common.h"
 #include "eb_internal.h"
 
+#include <algorithm>
 #include <mutex>
 
 namespace {
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     const float *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
     int Hkv, int rows, int nkeys, int qbase, int window, float scale_log2, int nqb,
-    int ngroups) {
+    int ngroups, int ctiles, float *__restrict__ part_acc, float *__restrict__ part_ml) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     constexpr int QB = C::QB;
     constexpr int HALF = C::HALF;
@@ -454,7 +455,15 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     const int p_first = qbase + qb * QB;
     const int p_last = qbase + min(qb * QB + QB, rows) - 1;
     const int t0 = window > 0 ? max(0, p_first - window + 1) / kTile : 0;
-    const int nsteps = (p_last / kTile - t0) / KSPLIT + 1;
+    // Key chunk blockIdx.y of the block's tiles t0..tE (ctiles tiles each): a block with
+    // more than one chunk writes partial states, which prefill_merge_kernel combines.
+    const int tE = p_last / kTile;
+    const int nch = (tE - t0) / ctiles + 1;
+    const int chunk = blockIdx.y;
+    if (chunk >= nch) return;  // (workgroup-uniform)
+    const int c_lo = t0 + chunk * ctiles;
+    const int c_hi = min(tE, c_lo + ctiles - 1);
+    const int nsteps = (c_hi - c_lo) / KSPLIT + 1;
     const bool live = q0 < rows;
     const int wp0 = qbase + q0;                         // this wave's first position
     const int wp1 = qbase + min(q0 + kTile, rows) - 1;  // and last
@@ -536,36 +545,36 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     f32x4 rs[PS ? C::PSN : 1];
     const float *recs = PS ? ps + (size_t)kvh * ps_nt * C::PS_FLOATS : nullptr;
     if constexpr (PS && C::PS_IMAGE) {
-        ps_copy_image<C>(recs, smem, 0, t0 - ps_tlo, ps_nt, wave, lane);
+        ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
         wait_vm_all();
     } else if constexpr (PS) {
-        ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, t0 - ps_tlo, ps_nt, tid);
+        ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
         ps_store_step<C>(smem, rs, 0, tid);
     } else {
-        prefill_load_step<C, H16>(k, v, rk, rv, t0 * kTile, nkeys, Hkv, kvh, tid);
+        prefill_load_step<C, H16>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid);
         prefill_store_step<C>(smem, rk, rv, 0, tid);
     }
     __syncthreads();
 
     for (int it = 0; it < nsteps; ++it) {
         const int buf = it & 1;
-        const int tile = t0 + it * KSPLIT + ks;
+        const int tile = c_lo + it * KSPLIT + ks;
         const int kb = tile * kTile;
         // Prefetch the next step (past the last step this re-reads clamped rows; the
         // buffer written from them is never read).
         // PS image records go straight into the other buffer, which every wave finished
         // reading before the last barrier.
         if constexpr (PS && C::PS_IMAGE)
-            ps_copy_image<C>(recs, smem, buf ^ 1, t0 + (it + 1) * KSPLIT - ps_tlo, ps_nt, wave,
+            ps_copy_image<C>(recs, smem, buf ^ 1, c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, wave,
                              lane);
         else if constexpr (PS)
             ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
-                            t0 + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
+                            c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
         else
-            prefill_load_step<C, H16>(k, v, rk, rv, (t0 + (it + 1) * KSPLIT) * kTile, nkeys,
+            prefill_load_step<C, H16>(k, v, rk, rv, (c_lo + (it + 1) * KSPLIT) * kTile, nkeys,
                                       Hkv, kvh, tid);
 
-        if (live && tile >= my_t0 && tile <= my_t1) {
+        if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
             const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS +
                               (C::SPV ? 0 : ks * kTile * HD);
@@ -824,18 +833,26 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     // c = 8*(r/4) + 4*hf + r%4, i.e. 16-byte pieces of 32 different output rows. Each
     // slot's 32 x HD tile is transposed through LDS so the global stores are whole rows
     // (HD contiguous floats per (query, head)).
+    // A block split into key chunks writes its raw state instead: O^T (in units of 2^E for
+    // SPV) and (m, l, E) per query, for prefill_merge_kernel.
     const float lt = l + __shfl_xor(l, 32);
+    const bool partial = nch > 1;
     if constexpr (KSPLIT > 1) __syncthreads();  // the merge records are read; reuse LDS
     float *ot = smem + slot * kTile * C::OS;    // this slot's staging tile [32][OS]
     if (ks == 0 && live) {
-        const float inv = 1.0f / lt;
+        const float inv = partial ? 1.0f : 1.0f / lt;
         // SPV: O^T is in units of 2^E; ldexp each normalised value back (exact)
         if constexpr (C::SPV) {
+            if (!partial) {
 #pragma unroll
-            for (int mb = 0; mb < NB; ++mb)
+                for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[mb][r] = ldexpf(oacc[mb][r] * inv, E);
+                    for (int r = 0; r < 16; ++r) oacc[mb][r] = ldexpf(oacc[mb][r] * inv, E);
+            }
         }
+        if (partial && hf == 0 && qi < rows)
+            *reinterpret_cast<float4 *>(part_ml + (((size_t)chunk * rows + qi) * H + head) * 4) =
+                make_float4(m, lt, __int_as_float(C::SPV ? E : 0), 0.0f);
         const float sc_o = C::SPV ? 1.0f : inv;
         float *orow = ot + col * C::OS;
 #pragma unroll
@@ -860,6 +877,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     }
     __syncthreads();
     if (ks == 0 && live) {
+        float *dst = partial ? part_acc + (size_t)chunk * rows * H * HD : o;
         constexpr int ROW4 = HD / 4;  // float4 per output row
 #pragma unroll
         for (int j = 0; j < (kTile * ROW4 + 63) / 64; ++j) {
@@ -868,11 +886,81 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 const int row = idx / ROW4;
                 const int c4 = idx % ROW4;
                 if (q0 + row < rows)
-                    *reinterpret_cast<float4 *>(o + ((size_t)(q0 + row) * H + head) * HD + 4 * c4) =
+                    *reinterpret_cast<float4 *>(dst + ((size_t)(q0 + row) * H + head) * HD + 4 * c4) =
                         *reinterpret_cast<const float4 *>(ot + row * C::OS + 4 * c4);
             }
         }
     }
+}
+
+// Combines the key chunks of the query blocks that were split: o = sum_c w_c O_c /
+// sum_c w_c l_c with w_c = 2^(m_c - M), M the largest m_c, and O_c in units of 2^E_c
+// (brought to the largest E first, so nothing overflows). A chunk that saw no key of a
+// query has m = -inf and weight 0. Blocks of one chunk were written by the prefill itself.
+// Thread (pair, d4): four output dims of one (row, head) pair; the chunks' states are read
+// kMergeBatch at a time, all loads of a batch issued before any is used.
+constexpr int kMergeBatch = 8;
+template <int HD>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(
+    const float *__restrict__ part_acc, const float *__restrict__ part_ml, float *__restrict__ o,
+    int rows, int H, int QB, int qbase, int window, int ctiles) {
+    constexpr int TP = HD >= 4 ? HD / 4 : 1;  // threads per (row, head) pair
+    constexpr int PER = 256 / TP;
+    const int pair = blockIdx.x * PER + threadIdx.x / TP;
+    const int d = 4 * (threadIdx.x % TP);
+    if (pair >= rows * H) return;
+    const int row = pair / H;
+    const int head = pair % H;
+    const int qb = row / QB;
+    const int p_first = qbase + qb * QB;
+    const int p_last = qbase + min(qb * QB + QB, rows) - 1;
+    const int t0 = window > 0 ? max(0, p_first - window + 1) / kTile : 0;
+    const int nch = (p_last / kTile - t0) / ctiles + 1;
+    if (nch <= 1) return;
+    const size_t cstride = (size_t)rows * H;  // (row, head) pairs per chunk
+    const size_t at0 = (size_t)row * H + head;
+    float M = -INFINITY;
+    int EM = kZeroRowExp;
+    for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
+        float4 ml[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j)
+            ml[j] = *reinterpret_cast<const float4 *>(
+                part_ml + (at0 + (size_t)min(c0 + j, nch - 1) * cstride) * 4);
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            M = fmaxf(M, ml[j].x);
+            EM = max(EM, __float_as_int(ml[j].z));
+        }
+    }
+    const float Mr = (M == -INFINITY) ? 0.0f : M;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
+        float4 ml[kMergeBatch], acc[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            const size_t at = at0 + (size_t)min(c0 + j, nch - 1) * cstride;
+            ml[j] = *reinterpret_cast<const float4 *>(part_ml + at * 4);
+            acc[j] = *reinterpret_cast<const float4 *>(part_acc + at * HD + d);
+        }
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            if (c0 + j < nch) {
+                const float w = eb::fast_exp2(ml[j].x - Mr);
+                const int sh = __float_as_int(ml[j].z) - EM;
+                L += w * ml[j].y;
+                A.x += w * ldexpf(acc[j].x, sh);
+                A.y += w * ldexpf(acc[j].y, sh);
+                A.z += w * ldexpf(acc[j].z, sh);
+                A.w += w * ldexpf(acc[j].w, sh);
+            }
+        }
+    }
+    const float inv = 1.0f / L;
+    *reinterpret_cast<float4 *>(o + at0 * HD + d) =
+        make_float4(ldexpf(A.x * inv, EM), ldexpf(A.y * inv, EM), ldexpf(A.z * inv, EM),
+                    ldexpf(A.w * inv, EM));
 }
 
 struct PrefillRange {
@@ -881,7 +969,7 @@ struct PrefillRange {
     int qbase;   // position of query row 0
     int window;  // sliding window (0: none)
     bool h16;    // k/v hold IEEE half elements
-    float *ws;   // pre-split workspace (null: split while staging)
+    float *ws;   // workspace (null: no pre-split pass, no key chunks)
     size_t ws_floats;
 };
 
@@ -905,10 +993,74 @@ size_t presplit_floats(size_t hd, size_t hkv, const PrefillRange &r) {
     return hkv * (size_t)presplit_nt(r) * rec;
 }
 
+// The workgroup shape launch_prefill_hd picks for head_dim hd and g query heads per KV head:
+// HPW heads x WPH 32-row blocks x KSPLIT key splits.
+struct PrefillShape {
+    int hpw, wph, ksplit;
+};
+PrefillShape prefill_shape(size_t hd, int g) {
+    const int hpw = g % 4 == 0 ? 4 : g % 2 == 0 ? 2 : 1;
+    return {hpw, 4 / hpw, (hpw == 4 || hd > 128) ? 1 : 2};
+}
+
+// Key chunks: when the query blocks alone would leave most of the CUs idle (fewer than
+// kPrefillFewUnits workgroups: short prompts, a short chunk over a long cache), each
+// block's key tiles are cut into chunks of ctiles tiles, one workgroup each, merged
+// afterwards. The chunk is halved (in steps of KSPLIT tiles) until there are
+// kPrefillUnits workgroups (two rounds on 256 CUs) or it is kPrefillMinSteps steps long.
+// Each chunk pays the q fragment, one unhidden staging step and an epilogue, which at
+// 256 block workgroups (a 2048-token prompt) cost what the better balance gains.
+constexpr int kPrefillFewUnits = 128;
+constexpr int kPrefillUnits = 512;
+constexpr int kPrefillMinSteps = 2;
+struct PrefillChunks {
+    int ctiles = 1 << 30;  // tiles per chunk (one chunk per block: no merge)
+    int nchmax = 1;        // most chunks of one block
+};
+PrefillChunks prefill_chunks(size_t hd, int H, int Hkv, const PrefillRange &r) {
+    const PrefillShape sh = prefill_shape(hd, H / Hkv);
+    const int QB = kTile * sh.wph;
+    const int ngroups = Hkv * (H / Hkv / sh.hpw);
+    const int nqb = (r.rows + QB - 1) / QB;
+    auto span = [&](int qb) {  // tiles t0..tE of block qb: tE - t0
+        const int p_first = r.qbase + qb * QB;
+        const int p_last = r.qbase + std::min(qb * QB + QB, r.rows) - 1;
+        const int t0 = r.window > 0 ? std::max(0, p_first - r.window + 1) / kTile : 0;
+        return p_last / kTile - t0;
+    };
+    int smax = 1;
+    for (int qb = 0; qb < nqb; ++qb) smax = std::max(smax, span(qb) / sh.ksplit + 1);
+    auto units = [&](int cs) {
+        long u = 0;
+        for (int qb = 0; qb < nqb; ++qb) u += span(qb) / (cs * sh.ksplit) + 1;
+        return u * ngroups;
+    };
+    PrefillChunks ch;
+    if ((long)nqb * ngroups >= kPrefillFewUnits) return ch;
+    int cs = smax;
+    while (cs > kPrefillMinSteps && units(cs) < kPrefillUnits) cs = (cs + 1) / 2;
+    if (cs >= smax) return ch;
+    ch.ctiles = cs * sh.ksplit;
+    int nmax = 1;
+    for (int qb = 0; qb < nqb; ++qb) nmax = std::max(nmax, span(qb) / ch.ctiles + 1);
+    ch.nchmax = nmax;
+    return ch;
+}
+
+// Workspace: [pre-split records | partial O^T: nchmax x rows x H x hd | partial (m, l, E):
+// nchmax x rows x H x 4].
+size_t chunk_floats(size_t hd, int H, const PrefillChunks &ch, const PrefillRange &r) {
+    return ch.nchmax > 1 ? (size_t)ch.nchmax * r.rows * H * (hd + 4) : 0;
+}
+size_t workspace_floats(size_t hd, int H, int Hkv, const PrefillRange &r) {
+    return presplit_floats(hd, Hkv, r) + chunk_floats(hd, H, prefill_chunks(hd, H, Hkv, r), r);
+}
+
 template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
 eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
                            const float *ps, float *o, int H, int Hkv, const PrefillRange &r,
-                           float scale_log2) {
+                           float scale_log2, const PrefillChunks &ch, float *part_acc,
+                           float *part_ml) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
@@ -922,20 +1074,30 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     const int g = H / Hkv;
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
-    const unsigned blocks = (unsigned)(nqb * ngroups);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS>
-        <<<blocks, C::THREADS, C::LDS_BYTES, st>>>(q, k, v, ps, presplit_tlo(r),
-                                                   presplit_nt(r), o, H, Hkv, r.rows, r.nkeys,
-                                                   r.qbase, r.window, scale_log2, nqb, ngroups);
-    return eb::check_launch("attn_prefill");
+    const dim3 grid((unsigned)(nqb * ngroups), (unsigned)ch.nchmax);
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+        q, k, v, ps, presplit_tlo(r), presplit_nt(r), o, H, Hkv, r.rows, r.nkeys, r.qbase,
+        r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml);
+    eb_status err = eb::check_launch("attn_prefill");
+    if (err != EB_OK || ch.nchmax <= 1) return err;
+    constexpr int PER = 256 / (HD >= 4 ? HD / 4 : 1);
+    const unsigned mblocks = (unsigned)(((size_t)r.rows * H + PER - 1) / PER);
+    prefill_merge_kernel<HD><<<mblocks, 256, 0, st>>>(part_acc, part_ml, o, r.rows, H, C::QB,
+                                                      r.qbase, r.window, ch.ctiles);
+    return eb::check_launch("attn_prefill (chunk merge)");
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT>
 eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const void *v,
                            float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
     const bool plain = r.qbase == 0 && r.window == 0;
+    // r.ws non-null: sized for workspace_floats (pre-split records, then key-chunk partials)
+    const size_t ps_floats = r.ws ? presplit_floats(HD, Hkv, r) : 0;
+    const PrefillChunks ch = r.ws ? prefill_chunks(HD, H, Hkv, r) : PrefillChunks{};
+    float *part_acc = ch.nchmax > 1 ? r.ws + ps_floats : nullptr;
+    float *part_ml = part_acc ? part_acc + (size_t)ch.nchmax * r.rows * H * HD : nullptr;
     if constexpr (PrefillCfg<HD, HPW, WPH, KSPLIT>::SPV) {
-        if (r.ws) {
+        if (ps_floats > 0) {
             const int nt = presplit_nt(r);
             float *ps = r.ws;
             const dim3 grid((unsigned)nt, (unsigned)Hkv);
@@ -949,19 +1111,19 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
             if (err != EB_OK) return err;
             if (plain && !r.h16)
                 return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, true>(
-                    st, q, k, v, ps, o, H, Hkv, r, scale_log2);
+                    st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
             return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false, true>(
-                st, q, k, v, ps, o, H, Hkv, r, scale_log2);
+                st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
         }
     }
     if (r.h16)
         return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, true, false>(
-            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2);
+            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
     if (plain)
         return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, false>(
-            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2);
+            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
     return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false, false>(
-        st, q, k, v, nullptr, o, H, Hkv, r, scale_log2);
+        st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
 }
 
 // head_dim <= 128:
@@ -971,7 +1133,7 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
 //  - otherwise: 8 waves (2 per SIMD) = 4 (head, 32-row) slots x 2 key splits, which
 //    halves the longest per-wave chain where the blocks are 64 or 128 rows tall.
 // head_dim 256: the Q fragment and O^T accumulators take ~450 registers per lane, so one
-// wave per SIMD: 4 waves, no key split.
+// wave per SIMD: 4 waves, no key split. (prefill_shape restates this choice.)
 template <int HD>
 eb_status launch_prefill_hd(hipStream_t st, const float *q, const void *k, const void *v,
                             float *o, int H, int Hkv, const PrefillRange &r,
@@ -993,9 +1155,9 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
     const float sl2 = scale * eb::kLog2e;
     const int H = (int)h, Hk = (int)hkv;
     PrefillRange rr = r;
-    const size_t need = presplit_floats(hd, hkv, r);
+    const size_t need = workspace_floats(hd, H, Hk, r);
     if (need == 0 || !r.ws || r.ws_floats < need || (reinterpret_cast<uintptr_t>(r.ws) & 15))
-        rr.ws = nullptr;  // stage with the split in the prefill itself
+        rr.ws = nullptr;  // no pre-split pass (split while staging), no key chunks
     switch (hd) {
         case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, rr, sl2);
         case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, rr, sl2);
@@ -1012,11 +1174,12 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
 
 namespace eb {
 
-size_t prefill_workspace_floats(size_t hkv, size_t hd, size_t rows, size_t nkeys, size_t qbase,
-                                size_t window) {
-    return presplit_floats(hd, hkv,
-                           PrefillRange{(int)rows, (int)nkeys, (int)qbase, (int)window, false,
-                                        nullptr, 0});
+size_t prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t rows, size_t nkeys,
+                                size_t qbase, size_t window) {
+    if (rows == 0 || hkv == 0 || h % hkv != 0) return 0;
+    return workspace_floats(hd, (int)h, (int)hkv,
+                            PrefillRange{(int)rows, (int)nkeys, (int)qbase, (int)window, false,
+                                         nullptr, 0});
 }
 
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,

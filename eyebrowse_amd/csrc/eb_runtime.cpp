@@ -613,12 +613,12 @@ struct PrefillWs {
     size_t floats = 0;
 };
 
-static eb_status prefill_ws(const PrefillWs &src, size_t hkv, size_t hd, size_t rows,
+static eb_status prefill_ws(const PrefillWs &src, size_t h, size_t hkv, size_t hd, size_t rows,
                             size_t nkeys, size_t qbase, size_t window, float **ws, size_t *wsn) {
     *ws = nullptr;
     *wsn = 0;
     if (!src.dev && !src.caller) return EB_OK;
-    const size_t need = eb::prefill_workspace_floats(hkv, hd, rows, nkeys, qbase, window);
+    const size_t need = eb::prefill_workspace_floats(h, hkv, hd, rows, nkeys, qbase, window);
     if (need == 0) return EB_OK;
     if (src.dev) {
         EB_TRY(device_workspace(src.dev, need, ws));
@@ -654,7 +654,7 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     EB_TRY(eb::check_ptr(o, "o"));
     float *ws;
     size_t wsn;
-    EB_TRY(prefill_ws(wsrc, hkv, hd, s, s, 0, 0, &ws, &wsn));
+    EB_TRY(prefill_ws(wsrc, h, hkv, hd, s, s, 0, 0, &ws, &wsn));
     EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
     return eb::ok();
 }
@@ -686,7 +686,7 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     EB_TRY(eb::check_ptr(o, "o"));
     float *ws;
     size_t wsn;
-    EB_TRY(prefill_ws(wsrc, hkv, hd, rows, pos0 + rows, pos0, window, &ws, &wsn));
+    EB_TRY(prefill_ws(wsrc, h, hkv, hd, rows, pos0 + rows, pos0, window, &ws, &wsn));
     if (h16)
         EB_TRY(eb::launch_attn_prefill_chunk_f16(st, q, static_cast<const uint16_t *>(kc),
                                                  static_cast<const uint16_t *>(vc), o, h, hkv,
@@ -1082,10 +1082,10 @@ eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_nu
                                  o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window);
 }
 
-size_t eb_attn_prefill_workspace_floats(size_t hkv, size_t hd, size_t pos0, size_t rows,
+size_t eb_attn_prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t pos0, size_t rows,
                                         size_t window) {
-    if (hkv == 0 || !eb::attn_head_dim_supported(hd)) return 0;
-    return eb::prefill_workspace_floats(hkv, hd, rows, pos0 + rows, pos0, window);
+    if (h == 0 || hkv == 0 || h % hkv != 0 || !eb::attn_head_dim_supported(hd)) return 0;
+    return eb::prefill_workspace_floats(h, hkv, hd, rows, pos0 + rows, pos0, window);
 }
 
 eb_status eb_launch_attn_prefill_ws(void *stream, const float *q, size_t q_numel, const float *k,

@@ -139,9 +139,10 @@ def launch_attn_prefill(stream: int, q: int, q_numel: int, k: int, k_numel: int,
                                        h, hkv, s, hd, scale))
 
 
-def attn_prefill_workspace_floats(hkv: int, hd: int, pos0: int, rows: int, window: int = 0) -> int:
-    """Floats of workspace the _ws prefill launches need for this shape (0: no pre-split)."""
-    return int(lib().eb_attn_prefill_workspace_floats(hkv, hd, pos0, rows, window))
+def attn_prefill_workspace_floats(h: int, hkv: int, hd: int, pos0: int, rows: int,
+                                  window: int = 0) -> int:
+    """Floats of workspace the _ws prefill launches need for this shape (0: none)."""
+    return int(lib().eb_attn_prefill_workspace_floats(h, hkv, hd, pos0, rows, window))
 
 
 def launch_attn_prefill_ws(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,

@@ -211,17 +211,21 @@ eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_nu
                                        size_t vc_numel, float *o, size_t o_numel, size_t h,
                                        size_t hkv, size_t pos0, size_t rows, size_t hd,
                                        size_t max_seq, float scale, size_t window);
-/* Prefill with a pre-split pass (no counterpart in the reference): with head_dim 32..256
- * and at least 256 query rows, the _ws launches first split every key they can see once
- * into workspace records (K and V rows scaled by powers of two into f16 hi/lo halves, V
+/* Prefill with a workspace (no counterpart in the reference). With head_dim 32..256 and
+ * at least 256 query rows, the _ws launches first split every key they can see once into
+ * workspace records (K and V rows scaled by powers of two into f16 hi/lo halves, V
  * transposed), so that the attention kernel only copies them into LDS; the plain raw
- * launches split the keys again in every workgroup that stages them. Same bits either way.
- * Floats of workspace for q rows pos0..pos0+rows-1 (pos0 0 for eb_launch_attn_prefill_ws)
- * with this window; 0 when no pre-split is done (the workspace may then be null). No
+ * launches split the keys again in every workgroup that stages them (same bits). When
+ * the query blocks alone give fewer than 128 workgroups, the keys of each block are also
+ * cut into chunks, one workgroup each, whose partial states (in the workspace) a second
+ * launch merges: the sums are then taken in another order than the plain launch's.
+ * Floats of workspace for h query heads over hkv KV heads and q rows pos0..pos0+rows-1
+ * (pos0 0 for eb_launch_attn_prefill_ws) with this window; 0 when neither is done (the
+ * workspace may then be null). No
  * initialisation needed; launches sharing a workspace must not overlap. The recorder
  * entry points (eb_attn_prefill, eb_attn_prefill_chunk) use the device's workspace. */
-size_t eb_attn_prefill_workspace_floats(size_t hkv, size_t hd, size_t pos0, size_t rows,
-                                        size_t window);
+size_t eb_attn_prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t pos0,
+                                        size_t rows, size_t window);
 eb_status eb_launch_attn_prefill_ws(void *stream, const float *q, size_t q_numel,
                                     const float *k, size_t k_numel, const float *v,
                                     size_t v_numel, float *o, size_t o_numel, size_t h,
