@@ -364,10 +364,8 @@ __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ 
     const int t = blockIdx.x;
     const int kvh = blockIdx.y;
     const int tid = threadIdx.x;
-    if constexpr (C::PS_IMAGE) {  // the image's padding: zeros
-        for (int i = tid; i < C::BUF; i += C::THREADS) smem[i] = 0.0f;
-        __syncthreads();
-    }
+    // (An image record's padding is left as it is: K rows are read within their HD floats,
+    // V^T rows within their 32 keys, and the exponents where written.)
     f32x4 rk[C::NLD], rv[C::NLD];
     prefill_load_step<C, H16>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
