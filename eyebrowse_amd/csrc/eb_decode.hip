@@ -749,6 +749,12 @@ size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int 
     return (size_t)p.nsplit * h * (hd + 2);
 }
 
+size_t decode_workspace_floats_any(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count) {
+    const size_t a = decode_workspace_floats(h, hkv, pos, hd, cu_count, false);
+    const size_t b = hd >= 8 ? decode_workspace_floats(h, hkv, pos, hd, cu_count, true) : 0;
+    return a > b ? a : b;
+}
+
 eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc, const void *vc,
                                  void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                  float *o, size_t h, size_t hkv, size_t pos, size_t hd,

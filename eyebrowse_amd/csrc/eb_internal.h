@@ -65,6 +65,9 @@ eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float 
 // Decode workspace: part_acc [nsplit*h*hd] | part_ml [nsplit*h*2], no initialisation.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
                                bool h16 = false);
+// The larger of the f32 and IEEE-half plans' workspaces (the plans split the keys
+// differently: their iterations hold different numbers of rows).
+size_t decode_workspace_floats_any(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count);
 // knew/vnew null: plain attention over keys 0..=pos. Otherwise key `pos` comes from
 // knew/vnew ([hkv, hd]) and is also written to cache row `pos` through kc_w/vc_w.
 // window > 0 limits the keys to pos - window + 1..=pos. A workspace sized for

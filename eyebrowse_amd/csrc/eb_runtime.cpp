@@ -789,7 +789,7 @@ static eb_status device_decode(eb_device *dev, const float *q, const void *kc, c
                                float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                                float scale, size_t window = 0, bool h16 = false,
                                const eb::DecodePrologue *pro = nullptr) {
-    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count);
+    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count, h16);
     float *ws = nullptr;
     if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
     EB_TRY(eb::launch_attn_decode_any(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv,
@@ -1123,7 +1123,7 @@ eb_status eb_launch_attn_prefill_chunk_f16_ws(void *stream, const float *q, size
 size_t eb_attn_decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd,
                                        int cu_count) {
     if (h == 0 || hkv == 0 || h % hkv != 0 || !eb::attn_head_dim_supported(hd)) return 0;
-    return eb::decode_workspace_floats(h, hkv, pos, hd, cu_count > 0 ? cu_count : 256);
+    return eb::decode_workspace_floats_any(h, hkv, pos, hd, cu_count > 0 ? cu_count : 256);
 }
 
 eb_status eb_launch_attn_decode(void *stream, const float *q, size_t q_numel, const float *kc,
@@ -1213,7 +1213,7 @@ eb_status eb_launch_attn_decode_f16(void *stream, const float *q, size_t q_numel
     EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
                                 pos, hd, max_seq, true));
     int cus = cu_count > 0 ? cu_count : 256;
-    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus, true);
     if (workspace_floats < need)
         return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
                     workspace_floats, need);
@@ -1235,7 +1235,7 @@ eb_status eb_launch_attn_decode_step_f16(void *stream, const float *q, size_t q_
                                 pos, hd, max_seq, true));
     EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
     int cus = cu_count > 0 ? cu_count : 256;
-    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus, true);
     if (workspace_floats < need)
         return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
                     workspace_floats, need);

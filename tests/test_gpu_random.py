@@ -1,0 +1,120 @@
+"""Seeded random shapes through every attention entry point on the GPU, against the oracle.
+
+Each case draws head_dim, GQA ratio, lengths, positions, window, scale and cache dtype
+from a fixed seed, so the sweep crosses the paths the fixed cases take one at a time
+(pre-split pass on or off, key chunks, sliding windows, IEEE-half caches, split-KV decode
+with the fused new-token step) at shapes none of them uses. The oracle is the reference's
+CPU attention restated in oracle/oracle.c (testutil.rs:130-218) with the chunk/window
+extension (attn_chunk); outputs are held to the FP32 bar of tests/_gpu.py on the rows
+each case samples.
+"""
+import numpy as np
+import pytest
+
+import eyebrowse_amd as eb
+import oracle
+from tests._gpu import assert_bitwise, assert_close, note, upload
+
+pytestmark = pytest.mark.gpu
+
+HDS = (4, 8, 16, 32, 64, 128, 256)
+
+
+def draw(seed):
+    r = np.random.default_rng(1000 + seed)
+    hd = int(r.choice(HDS))
+    hkv = int(r.choice((1, 2, 4, 8)))
+    g = int(r.choice((1, 2, 3, 4, 8)))
+    scale = float(r.choice((0.0, 1.0, 0.05, 0.3))) if seed % 4 == 0 else float(oracle.default_scale(hd))
+    return r, hd, hkv * g, hkv, scale
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_prefill(dev, seed):
+    r, hd, h, hkv, sc = draw(seed)
+    s = int(r.integers(1, 700))
+    note(f"random prefill seed={seed} h={h} hkv={hkv} hd={hd} s={s} scale={sc}")
+    q = oracle.randn((s, h, hd), 3 * seed)
+    k, v = oracle.randn((s, hkv, hd), 3 * seed + 1), oracle.randn((s, hkv, hd), 3 * seed + 2)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    ot = eb.Tensor.empty(dev, (s, h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_prefill(rec, qt, kt, vt, ot, h, hkv, s, hd, sc)
+    rec.submit()
+    got = ot.to_f32().reshape(s, h, hd)
+    for r0 in sorted({0, max(0, s // 2 - 8), max(0, s - 16)}):
+        n = min(16, s - r0)
+        want = oracle.attn_prefill(q, k, v, h, hkv, s, hd, sc, rows=(r0, n), threads=16)
+        assert_close(got[r0:r0 + n], want[r0:r0 + n], what=f"rows {r0}+{n}")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_chunk(dev, seed):
+    r, hd, h, hkv, sc = draw(100 + seed)
+    pos0 = int(r.integers(0, 1500))
+    rows = int(r.integers(1, 400))
+    window = int(r.choice((0, 0, 1, 17, 200, 5000)))
+    f16 = hd >= 8 and bool(r.integers(0, 2))
+    max_seq = pos0 + rows + int(r.integers(0, 9))
+    note(f"random chunk seed={seed} h={h} hkv={hkv} hd={hd} pos0={pos0} rows={rows} "
+         f"window={window} f16={f16}")
+    q = oracle.randn((rows, h, hd), 7 * seed + 1)
+    kc, vc = oracle.randn((max_seq, hkv, hd), 7 * seed + 2), oracle.randn((max_seq, hkv, hd), 7 * seed + 3)
+    if f16:
+        kt = eb.Tensor.empty(dev, kc.shape, eb.DType.F16)
+        vt = eb.Tensor.empty(dev, vc.shape, eb.DType.F16)
+        rec = eb.Recorder(dev)
+        eb.kv_write(rec, kt, upload(dev, kc), hkv, max_seq, hd, max_seq, 0)
+        eb.kv_write(rec, vt, upload(dev, vc), hkv, max_seq, hd, max_seq, 0)
+        rec.submit()
+        kc = oracle.f16_values(oracle.f16_bits(kc)).reshape(kc.shape)
+        vc = oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape)
+    else:
+        kt, vt = upload(dev, kc), upload(dev, vc)
+    ot = eb.Tensor.empty(dev, (rows, h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_prefill_chunk(rec, upload(dev, q), kt, vt, ot, h, hkv, pos0, rows, hd, max_seq, sc,
+                          window)
+    rec.submit()
+    got = ot.to_f32().reshape(rows, h, hd)
+    for rr in sorted({0, rows // 2, rows - 1}):
+        want = oracle.attn_chunk(q[rr:rr + 1], kc, vc, h, hkv, pos0 + rr, 1, hd, sc, window,
+                                 threads=16)
+        assert_close(got[rr:rr + 1], want, what=f"row {rr}")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_decode_step(dev, seed):
+    """The fused step (new row written at pos, attention over 0..=pos, optional window)
+    against kv_write + the oracle; the cache row must be the new row's bits (f32) or its
+    binary16 rounding (f16)."""
+    r, hd, h, hkv, sc = draw(200 + seed)
+    max_seq = int(r.integers(2, 20000))
+    pos = int(r.integers(0, max_seq))
+    window = int(r.choice((0, 0, 1, 33, 4096)))
+    f16 = hd >= 8 and bool(r.integers(0, 2))
+    note(f"random decode seed={seed} h={h} hkv={hkv} hd={hd} pos={pos} max_seq={max_seq} "
+         f"window={window} f16={f16}")
+    kc, vc = oracle.randn((max_seq, hkv, hd), 11 * seed + 1), oracle.randn((max_seq, hkv, hd), 11 * seed + 2)
+    q = oracle.randn((h, hd), 11 * seed + 3)
+    kn, vn = oracle.randn((hkv, hd), 11 * seed + 4), oracle.randn((hkv, hd), 11 * seed + 5)
+    dt = eb.DType.F16 if f16 else eb.DType.F32
+    kt, vt = eb.Tensor.empty(dev, kc.shape, dt), eb.Tensor.empty(dev, vc.shape, dt)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, kt, upload(dev, kc), hkv, max_seq, hd, max_seq, 0)
+    eb.kv_write(rec, vt, upload(dev, vc), hkv, max_seq, hd, max_seq, 0)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    eb.attn_decode_step_window(rec, upload(dev, q), upload(dev, kn), upload(dev, vn), kt, vt, ot,
+                               h, hkv, pos, hd, max_seq, sc, window)
+    rec.submit()
+    kc[pos], vc[pos] = kn, vn
+    if f16:
+        kc = oracle.f16_values(oracle.f16_bits(kc)).reshape(kc.shape)
+        vc = oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape)
+        row = np.frombuffer(kt.read_bytes(), np.uint16).reshape(max_seq, hkv, hd)[pos]
+        assert np.array_equal(row, oracle.f16_bits(kn))
+    else:
+        assert_bitwise(kt.to_f32().reshape(max_seq, hkv, hd)[pos], kn, "new K row")
+    want = oracle.attn_chunk(q.reshape(1, h, hd), kc, vc, h, hkv, pos, 1, hd, sc, window,
+                             threads=16)
+    assert_close(ot.to_f32().reshape(1, h, hd), want, what="decode step")
