@@ -49,13 +49,33 @@ __device__ __forceinline__ float lane_xor32(float x) {
     return __builtin_bit_cast(float, upper ? r[0] : r[1]);
 }
 
+// Reduce-scatter halves with the swaps: a + b over lane pairs i, i ^ 32 (swap_sum32) or
+// i, i ^ 16 (swap_sum16), where lanes 0-31 (even 16-lane rows) end with the pair's sum of
+// a and lanes 32-63 (odd rows) with the pair's sum of b. The empty asm keeps the second
+// result opaque: the ROCm 7.2 compiler folds the f32 add of a swap's two results into
+// an add of the first result to itself.
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, a),
+                                                    __builtin_bit_cast(unsigned, b), false, false);
+    unsigned r1 = r[1];
+    asm volatile("" : "+v"(r1));
+    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a),
+                                                    __builtin_bit_cast(unsigned, b), false, false);
+    unsigned r1 = r[1];
+    asm volatile("" : "+v"(r1));
+    return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r1);
+}
+
 // Reduce (sum or max) over the lanes that share lane bits [0, log2(FROM)): every lane
 // ends with the reduction over its class {i' : i' % FROM == i % FROM}. VALU lane
 // permutes only (DPP row rotations within 16 lanes, then the 16- and 32-lane swaps): a
 // rotation by 8 within a row pairs lane i with i ^ 8, and the rotations by 1, 2, 4 fold
 // a class's members within a row in any order, which a sum or max does not notice.
 template <int FROM, bool MAX>
-__device__ __forceinline__ float class_reduce(float x) {
+__device__ __forceinline__ float row_class_reduce(float x) {
     static_assert(FROM == 1 || FROM == 2 || FROM == 4 || FROM == 8 || FROM == 16 ||
                       FROM == 32 || FROM == 64, "power of two");
     auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
@@ -63,6 +83,13 @@ __device__ __forceinline__ float class_reduce(float x) {
     if constexpr (FROM <= 2) x = op(x, dpp<0x122>(x));  // row_ror:2
     if constexpr (FROM <= 4) x = op(x, dpp<0x124>(x));  // row_ror:4
     if constexpr (FROM <= 8) x = op(x, dpp<0x128>(x));  // row_ror:8
+    return x;
+}
+
+template <int FROM, bool MAX>
+__device__ __forceinline__ float class_reduce(float x) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    x = row_class_reduce<FROM, MAX>(x);  // the members within each 16-lane row
     if constexpr (FROM <= 16) x = op(x, lane_xor16(x));
     if constexpr (FROM <= 32) x = op(x, lane_xor32(x));
     return x;

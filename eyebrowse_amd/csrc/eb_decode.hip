@@ -78,12 +78,10 @@ struct DecodeShape {
     // in VGPRs; with the workgroups of a CU that is as much in flight as the HBM rewards.
     static constexpr int U = EB_DECODE_U > 0 ? EB_DECODE_U : UDEF;
     static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
-    // Epilogue LDS: NS lane-group states of SS floats (G heads of HD, padded by 4 floats
-    // so that the lane groups' 16-byte writes fall in different banks), plus m, l, the
-    // weights, the weighted sums and the per-head reference max.
-    static constexpr int NS = kWaves * KPW;
-    static constexpr int SS = G * HD + 4;
-    static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)NS * SS + 4 * G * NS + G);
+    // Epilogue LDS: one state per wave, WS floats (G heads of HD, padded by 4 floats so
+    // that the waves' rows start in different banks), plus m and l per head and wave.
+    static constexpr int WS = G * HD + 4;
+    static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)kWaves * WS + 2 * G * kWaves);
     static_assert(DPL % 4 == 0 && LPK <= 16, "head_dim must be a multiple of 4, at most 256");
 };
 
@@ -469,67 +467,82 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         }
     }
 
-    // Epilogue: every lane group's state (m, l, acc) goes to LDS, then the workgroup
-    // combines the NS states of each head with one weight per state, 2^(m_s - M): a few
-    // LDS reads and FMAs per output instead of cross-lane reductions.
-    constexpr int NS = S::NS;
-    constexpr int SS = S::SS;
+    // Epilogue, in two levels. Within a wave the KPW lane groups' states (m, l, acc) meet
+    // through lane permutes, each weighted by 2^(m - M_wave). A 32-lane swap of two
+    // different units followed by an add leaves one unit's sum in the lower half of the
+    // wave and the other's in the upper half, so each halving of the lanes also halves the
+    // registers: after the 32- and 16-lane steps lane L holds unit (L >> 4) & 3 of its
+    // lane slot, and the row rotations finish the lane groups that share a 16-lane row.
+    // The kWaves wave states then meet in LDS, combined per output with one weight each.
+    static_assert(kWaves == 4, "the wave states are read as one f32x4");
+    constexpr int WS = S::WS;
     extern __shared__ float smem[];
-    float *s_acc = smem;              // [NS][SS]: state s, then head gi, then dim
-    float *s_m = s_acc + NS * SS;     // [G][NS]
-    float *s_l = s_m + G * NS;        // [G][NS]
-    float *s_w = s_l + G * NS;        // [G][NS] weights
-    float *s_lw = s_w + G * NS;       // [G][NS] weighted sums
-    float *s_M = s_lw + G * NS;       // [G] reference max per head
-    const int st = wave * S::KPW + kg;
+    float *s_acc = smem;                // [kWaves][WS]: wave, then head gi, then dim
+    float *s_m = s_acc + kWaves * WS;   // [G][kWaves]
+    float *s_l = s_m + G * kWaves;      // [G][kWaves]
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-#pragma unroll
-        for (int i = 0; i < NV4; ++i)
-            *reinterpret_cast<f32x4 *>(s_acc + st * SS + gi * HD + dim_of<HD, H16>(i, ls)) =
-                acc[gi][i];
-        if (ls == 0) {
-            s_m[gi * NS + st] = m[gi];
-            s_l[gi * NS + st] = l[gi];
+        const float mw = eb::class_reduce<S::LPK, true>(m[gi]);
+        const float w = eb::fast_exp2(m[gi] - (mw == -INFINITY ? 0.0f : mw));
+        const float lw = eb::class_reduce<S::LPK, false>(l[gi] * w);
+        if (lane == 0) {
+            s_m[gi * kWaves + wave] = mw;
+            s_l[gi * kWaves + wave] = lw;
         }
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < G * NS; idx += kThreads) {
-        const int gi = idx / NS;
-        float M = -INFINITY;
+        float *dst = s_acc + wave * WS + gi * HD;
+        if constexpr (NV4 == 4) {
+            float v[16];
 #pragma unroll
-        for (int j = 0; j < NS; j += 4) {
-            const f32x4 mm = *reinterpret_cast<const f32x4 *>(s_m + gi * NS + j);
-            M = fmaxf(M, fmaxf(fmaxf(mm.x, mm.y), fmaxf(mm.z, mm.w)));
+            for (int i = 0; i < 4; ++i) {
+                const f32x4 t = acc[gi][i] * w;
+                v[4 * i + 0] = t.x;
+                v[4 * i + 1] = t.y;
+                v[4 * i + 2] = t.z;
+                v[4 * i + 3] = t.w;
+            }
+            float v2[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)  // lower half: v[k] summed; upper: v[k + 8]
+                v2[k] = eb::swap_sum32(v[k], v[k + 8]);
+            f32x4 out;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)  // even rows: v2[k] summed; odd rows: v2[k + 4]
+                out[k] = eb::row_class_reduce<S::LPK, false>(eb::swap_sum16(v2[k], v2[k + 4]));
+            if ((lane & 15) < S::LPK)
+                *reinterpret_cast<f32x4 *>(dst + dim_of<HD, H16>((lane >> 4) & 3, ls)) = out;
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV4; ++i) {
+                const f32x4 t = acc[gi][i] * w;
+                f32x4 out;
+                out.x = eb::class_reduce<S::LPK, false>(t.x);
+                out.y = eb::class_reduce<S::LPK, false>(t.y);
+                out.z = eb::class_reduce<S::LPK, false>(t.z);
+                out.w = eb::class_reduce<S::LPK, false>(t.w);
+                if (kg == 0) *reinterpret_cast<f32x4 *>(dst + dim_of<HD, H16>(i, ls)) = out;
+            }
         }
-        const float mref = (M == -INFINITY) ? 0.0f : M;
-        const float w = eb::fast_exp2(s_m[idx] - mref);
-        s_w[idx] = w;
-        s_lw[idx] = w * s_l[idx];
-        if (idx % NS == 0) s_M[gi] = M;
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < G * HD; idx += kThreads) {
         const int gi = idx / HD;
         const int d = idx % HD;
-        float A = 0.0f, L = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NS; j += 4) {
-            const f32x4 w4 = *reinterpret_cast<const f32x4 *>(s_w + gi * NS + j);
-            const f32x4 lw4 = *reinterpret_cast<const f32x4 *>(s_lw + gi * NS + j);
-            A += w4.x * s_acc[(j + 0) * SS + gi * HD + d];
-            A += w4.y * s_acc[(j + 1) * SS + gi * HD + d];
-            A += w4.z * s_acc[(j + 2) * SS + gi * HD + d];
-            A += w4.w * s_acc[(j + 3) * SS + gi * HD + d];
-            L += (lw4.x + lw4.y) + (lw4.z + lw4.w);
-        }
+        const f32x4 m4 = *reinterpret_cast<const f32x4 *>(s_m + gi * kWaves);
+        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(s_l + gi * kWaves);
+        const float M = fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w));
+        const float mref = (M == -INFINITY) ? 0.0f : M;
+        const float w0 = eb::fast_exp2(m4.x - mref), w1 = eb::fast_exp2(m4.y - mref);
+        const float w2 = eb::fast_exp2(m4.z - mref), w3 = eb::fast_exp2(m4.w - mref);
+        const float A = (w0 * s_acc[idx] + w1 * s_acc[WS + idx]) +
+                        (w2 * s_acc[2 * WS + idx] + w3 * s_acc[3 * WS + idx]);
+        const float L = (w0 * l4.x + w1 * l4.y) + (w2 * l4.z + w3 * l4.w);
         const int hh = head0 + gi;
         if (a.nsplit == 1) {
             a.o[(size_t)hh * HD + d] = A / L;
         } else {
             a.part_acc[((size_t)split * a.h + hh) * HD + d] = A;
             if (d == 0) {
-                a.part_ml[((size_t)split * a.h + hh) * 2 + 0] = s_M[gi];
+                a.part_ml[((size_t)split * a.h + hh) * 2 + 0] = M;
                 a.part_ml[((size_t)split * a.h + hh) * 2 + 1] = L;
             }
         }
