@@ -118,3 +118,83 @@ def test_random_decode_step(dev, seed):
     want = oracle.attn_chunk(q.reshape(1, h, hd), kc, vc, h, hkv, pos, 1, hd, sc, window,
                              threads=16)
     assert_close(ot.to_f32().reshape(1, h, hd), want, what="decode step")
+
+
+def _caches(dev, max_seq, hkv, hd, f16, seed):
+    """Seeded K/V caches on the device (f32, or IEEE-half written by kv_write) and the
+    values they hold, as f32 for the oracle."""
+    kc = oracle.randn((max_seq, hkv, hd), seed)
+    vc = oracle.randn((max_seq, hkv, hd), seed + 1)
+    if not f16:
+        return upload(dev, kc), upload(dev, vc), kc, vc
+    kt = eb.Tensor.empty(dev, kc.shape, eb.DType.F16)
+    vt = eb.Tensor.empty(dev, vc.shape, eb.DType.F16)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, kt, upload(dev, kc), hkv, max_seq, hd, max_seq, 0)
+    eb.kv_write(rec, vt, upload(dev, vc), hkv, max_seq, hd, max_seq, 0)
+    rec.submit()
+    return (kt, vt, oracle.f16_values(oracle.f16_bits(kc)).reshape(kc.shape),
+            oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_raw_decode(dev, seed):
+    """Stream-level decode on a caller workspace of exactly the size the public sizing
+    function returns, for CU counts other than the device's (other split plans), f32 and
+    IEEE-half caches, with and without a window. The workspace starts as NaN so a partial
+    the launch forgets to write shows up in the output."""
+    r, hd, h, hkv, sc = draw(300 + seed)
+    max_seq = int(r.integers(2, 20000))
+    pos = int(r.integers(0, max_seq))
+    window = int(r.choice((0, 0, 1, 77, 3000)))
+    f16 = hd >= 8 and bool(r.integers(0, 2))
+    cus = int(r.choice((dev.cu_count, 1, 40, 304, 1000)))
+    note(f"random raw decode seed={seed} h={h} hkv={hkv} hd={hd} pos={pos} max_seq={max_seq} "
+         f"window={window} f16={f16} cus={cus}")
+    kt, vt, kc, vc = _caches(dev, max_seq, hkv, hd, f16, 13 * seed + 1)
+    q = oracle.randn((h, hd), 13 * seed + 3)
+    qt = upload(dev, q)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    need = eb.attn_decode_workspace_floats(h, hkv, pos, hd, cus)
+    ws = upload(dev, np.full(max(need, 1), np.nan, np.float32))
+    args = (dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(), vt.data_ptr,
+            vt.numel(), ot.data_ptr, ot.numel(), h, hkv, pos, hd, max_seq, sc)
+    if f16:
+        eb.launch_attn_decode_f16(*args, window, ws.data_ptr, need, cus)
+    else:
+        eb.launch_attn_decode_window(*args, window, ws.data_ptr, need, cus)
+    dev.synchronize()
+    want = oracle.attn_chunk(q.reshape(1, h, hd), kc, vc, h, hkv, pos, 1, hd, sc, window,
+                             threads=16)
+    assert_close(ot.to_f32().reshape(1, h, hd), want, what="raw decode")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_raw_prefill_ws(dev, seed):
+    """Stream-level chunked prefill on a caller workspace of exactly the size
+    eb_attn_prefill_workspace_floats returns (pre-split records and, for launches with few
+    query blocks, key-chunk partials), NaN-filled beforehand."""
+    r, hd, h, hkv, sc = draw(400 + seed)
+    pos0 = int(r.integers(0, 3000))
+    rows = int(r.integers(1, 300))
+    window = int(r.choice((0, 0, 1, 40, 1000)))
+    f16 = hd >= 8 and bool(r.integers(0, 2))
+    max_seq = pos0 + rows + int(r.integers(0, 5))
+    note(f"random raw prefill_ws seed={seed} h={h} hkv={hkv} hd={hd} pos0={pos0} rows={rows} "
+         f"window={window} f16={f16}")
+    kt, vt, kc, vc = _caches(dev, max_seq, hkv, hd, f16, 17 * seed + 1)
+    q = oracle.randn((rows, h, hd), 17 * seed + 3)
+    qt = upload(dev, q)
+    ot = eb.Tensor.empty(dev, (rows, h, hd))
+    need = eb.attn_prefill_workspace_floats(h, hkv, hd, pos0, rows, window)
+    ws = upload(dev, np.full(max(need, 1), np.nan, np.float32))
+    eb.launch_attn_prefill_chunk_ws(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr,
+                                    kt.numel(), vt.data_ptr, vt.numel(), ot.data_ptr,
+                                    ot.numel(), h, hkv, pos0, rows, hd, max_seq, sc, window,
+                                    ws.data_ptr, need, f16=f16)
+    dev.synchronize()
+    got = ot.to_f32().reshape(rows, h, hd)
+    for rr in sorted({0, rows // 3, rows - 1}):
+        want = oracle.attn_chunk(q[rr:rr + 1], kc, vc, h, hkv, pos0 + rr, 1, hd, sc, window,
+                                 threads=16)
+        assert_close(got[rr:rr + 1], want, what=f"row {rr}")
