@@ -14,6 +14,7 @@
 #include <atomic>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -57,6 +58,25 @@ eb_status check_launch(const char *kernel) {
 eb_status check_ptr(const void *p, const char *name) {
     if (p == nullptr) return fail(EB_SHAPE_MISMATCH, "%s is null", name);
     return EB_OK;
+}
+
+eb_status check_numel(size_t have, size_t need, const char *name);
+
+// The product of a shape's dims, refused when it wraps (a caller's absurd sizes must not
+// pass the element-count checks below as a small number).
+eb_status shape_numel(std::initializer_list<size_t> dims, const char *name, size_t *out) {
+    size_t n = 1;
+    for (size_t d : dims)
+        if (__builtin_mul_overflow(n, d, &n))
+            return fail(EB_UNSUPPORTED_CONFIG, "%s: shape size overflows", name);
+    *out = n;
+    return EB_OK;
+}
+
+eb_status check_numel(size_t have, std::initializer_list<size_t> dims, const char *name) {
+    size_t need = 0;
+    const eb_status st = shape_numel(dims, name, &need);
+    return st != EB_OK ? st : check_numel(have, need, name);
 }
 
 eb_status check_numel(size_t have, size_t need, const char *name) {
@@ -180,9 +200,11 @@ static void device_unref(eb_device *d) {
     if (d && d->refs.fetch_sub(1) == 1) device_destroy(d);
 }
 
+// Elements of a shape, or SIZE_MAX when the product wraps.
 static size_t shape_numel(const size_t *shape, size_t ndim) {
     size_t n = 1;
-    for (size_t i = 0; i < ndim; ++i) n *= shape[i];
+    for (size_t i = 0; i < ndim; ++i)
+        if (__builtin_mul_overflow(n, shape[i], &n)) return SIZE_MAX;
     return n;
 }
 
@@ -277,6 +299,9 @@ static eb_status tensor_alloc(eb_device *dev, const size_t *shape, size_t ndim, 
     size_t esz = eb_dtype_size(dt);
     if (esz == 0) return fail(EB_OTHER, "unknown dtype %d", (int)dt);
     size_t numel = shape_numel(shape, ndim);
+    size_t nbytes_check = 0;
+    if (numel == SIZE_MAX || __builtin_mul_overflow(numel, esz, &nbytes_check))
+        return fail(EB_OUT_OF_MEMORY, "tensor of %zu dims: size overflows", ndim);
     // (numel * size).max(size): a zero-element tensor still owns one element
     // (crates/eyebrowse-gpu/src/tensor.rs:228).
     size_t bytes = numel * esz;
@@ -585,8 +610,8 @@ static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
     if (dst > max_seq || count > max_seq - dst)
         return fail(EB_SHAPE_MISMATCH, "kv_write: rows [%zu, %zu) exceed max_seq %zu", dst,
                     dst + count, max_seq);
-    EB_TRY(eb::check_numel(cache_n, max_seq * hkv * hd, "cache"));
-    EB_TRY(eb::check_numel(src_n, count * hkv * hd, "src"));
+    EB_TRY(eb::check_numel(cache_n, {max_seq, hkv, hd}, "cache"));
+    EB_TRY(eb::check_numel(src_n, {count, hkv, hd}, "src"));
     if (count == 0) return eb::ok();
     EB_TRY(eb::check_ptr(cache, "cache"));
     EB_TRY(eb::check_ptr(src, "src"));
@@ -643,10 +668,10 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_prefill: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)", hd);
-    EB_TRY(eb::check_numel(qn, s * h * hd, "q"));
-    EB_TRY(eb::check_numel(kn, s * hkv * hd, "k"));
-    EB_TRY(eb::check_numel(vn, s * hkv * hd, "v"));
-    EB_TRY(eb::check_numel(on, s * h * hd, "o"));
+    EB_TRY(eb::check_numel(qn, {s, h, hd}, "q"));
+    EB_TRY(eb::check_numel(kn, {s, hkv, hd}, "k"));
+    EB_TRY(eb::check_numel(vn, {s, hkv, hd}, "v"));
+    EB_TRY(eb::check_numel(on, {s, h, hd}, "o"));
     if (s == 0) return eb::ok();
     EB_TRY(eb::check_ptr(q, "q"));
     EB_TRY(eb::check_ptr(k, "k"));
@@ -675,10 +700,10 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     if (pos0 > max_seq || rows > max_seq - pos0)
         return fail(EB_SHAPE_MISMATCH, "attn_prefill_chunk: rows [%zu, %zu) exceed max_seq %zu",
                     pos0, pos0 + rows, max_seq);
-    EB_TRY(eb::check_numel(qn, rows * h * hd, "q"));
-    EB_TRY(eb::check_numel(kcn, max_seq * hkv * hd, "kcache"));
-    EB_TRY(eb::check_numel(vcn, max_seq * hkv * hd, "vcache"));
-    EB_TRY(eb::check_numel(on, rows * h * hd, "o"));
+    EB_TRY(eb::check_numel(qn, {rows, h, hd}, "q"));
+    EB_TRY(eb::check_numel(kcn, {max_seq, hkv, hd}, "kcache"));
+    EB_TRY(eb::check_numel(vcn, {max_seq, hkv, hd}, "vcache"));
+    EB_TRY(eb::check_numel(on, {rows, h, hd}, "o"));
     if (rows == 0) return eb::ok();
     EB_TRY(eb::check_ptr(q, "q"));
     EB_TRY(eb::check_ptr(kc, "kcache"));
@@ -710,10 +735,10 @@ static eb_status decode_shape_checked(const float *q, size_t qn, const void *kc,
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
     if (pos >= max_seq)
         return fail(EB_SHAPE_MISMATCH, "attn_decode: pos %zu >= max_seq %zu", pos, max_seq);
-    EB_TRY(eb::check_numel(qn, h * hd, "q"));
-    EB_TRY(eb::check_numel(kcn, max_seq * hkv * hd, "kcache"));
-    EB_TRY(eb::check_numel(vcn, max_seq * hkv * hd, "vcache"));
-    EB_TRY(eb::check_numel(on, h * hd, "o"));
+    EB_TRY(eb::check_numel(qn, {h, hd}, "q"));
+    EB_TRY(eb::check_numel(kcn, {max_seq, hkv, hd}, "kcache"));
+    EB_TRY(eb::check_numel(vcn, {max_seq, hkv, hd}, "vcache"));
+    EB_TRY(eb::check_numel(on, {h, hd}, "o"));
     EB_TRY(eb::check_ptr(q, "q"));
     EB_TRY(eb::check_ptr(kc, "kcache"));
     EB_TRY(eb::check_ptr(vc, "vcache"));
@@ -725,9 +750,9 @@ static eb_status rmsnorm_checked(hipStream_t st, const float *x, size_t xn, cons
                                  size_t wn, float *out, size_t outn, size_t rows, size_t dim,
                                  float eps) {
     if (dim == 0) return fail(EB_SHAPE_MISMATCH, "rmsnorm: dim must be > 0");
-    EB_TRY(eb::check_numel(xn, rows * dim, "x"));
+    EB_TRY(eb::check_numel(xn, {rows, dim}, "x"));
     EB_TRY(eb::check_numel(wn, dim, "weight"));
-    EB_TRY(eb::check_numel(outn, rows * dim, "out"));
+    EB_TRY(eb::check_numel(outn, {rows, dim}, "out"));
     if (rows == 0) return eb::ok();
     EB_TRY(eb::check_ptr(x, "x"));
     EB_TRY(eb::check_ptr(w, "weight"));
@@ -740,9 +765,9 @@ static eb_status rope_checked(hipStream_t st, const float *x, size_t xn, const f
                               const float *s, size_t tn, float *out, size_t outn, size_t seq,
                               size_t nh, size_t hd, size_t base_pos) {
     if (hd == 0 || hd % 2 != 0) return fail(EB_SHAPE_MISMATCH, "rope: head_dim must be even");
-    EB_TRY(eb::check_numel(xn, seq * nh * hd, "x"));
-    EB_TRY(eb::check_numel(outn, seq * nh * hd, "out"));
-    EB_TRY(eb::check_numel(tn, (seq + base_pos) * (hd / 2), "cos/sin tables"));
+    EB_TRY(eb::check_numel(xn, {seq, nh, hd}, "x"));
+    EB_TRY(eb::check_numel(outn, {seq, nh, hd}, "out"));
+    EB_TRY(eb::check_numel(tn, {(seq + base_pos), (hd / 2)}, "cos/sin tables"));
     if (seq == 0 || nh == 0) return eb::ok();
     EB_TRY(eb::check_ptr(x, "x"));
     EB_TRY(eb::check_ptr(c, "cos"));
@@ -755,7 +780,7 @@ static eb_status rope_checked(hipStream_t st, const float *x, size_t xn, const f
 // Checks the new-token rows of a fused decode step ([hkv, hd] each).
 static eb_status step_rows_checked(const float *knew, const float *vnew, size_t new_n,
                                    size_t hkv, size_t hd) {
-    EB_TRY(eb::check_numel(new_n, hkv * hd, "knew/vnew"));
+    EB_TRY(eb::check_numel(new_n, {hkv, hd}, "knew/vnew"));
     EB_TRY(eb::check_ptr(knew, "knew"));
     EB_TRY(eb::check_ptr(vnew, "vnew"));
     return EB_OK;
@@ -820,10 +845,10 @@ static eb_status linear_checked(hipStream_t st, const float *x, size_t xn,
                                 size_t m, size_t in_f, float *ws, size_t wsn) {
     if (nseg < 1 || nseg > eb::kLinearMaxSegs)
         return fail(EB_OTHER, "linear_f16w: 1 to %d weights per launch", eb::kLinearMaxSegs);
-    EB_TRY(eb::check_numel(xn, m * in_f, "a"));
+    EB_TRY(eb::check_numel(xn, {m, in_f}, "a"));
     for (int i = 0; i < nseg; ++i) {
-        EB_TRY(eb::check_numel(w_halves[i], out_f[i] * in_f, "w"));
-        EB_TRY(eb::check_numel(yn[i], m * out_f[i], "c"));
+        EB_TRY(eb::check_numel(w_halves[i], {out_f[i], in_f}, "w"));
+        EB_TRY(eb::check_numel(yn[i], {m, out_f[i]}, "c"));
     }
     if (m == 0) return eb::ok();
     if (in_f > 0) EB_TRY(eb::check_ptr(x, "a"));
@@ -1018,8 +1043,8 @@ eb_status eb::attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q,
     if (rope_cos) {
         EB_TRY(tensor_f32(rope_cos, "rope cos", rec->dev));
         EB_TRY(tensor_f32(rope_sin, "rope sin", rec->dev));
-        EB_TRY(eb::check_numel(eb_tensor_numel(rope_cos), (pos + 1) * (hd / 2), "rope cos"));
-        EB_TRY(eb::check_numel(eb_tensor_numel(rope_sin), (pos + 1) * (hd / 2), "rope sin"));
+        EB_TRY(eb::check_numel(eb_tensor_numel(rope_cos), {(pos + 1), (hd / 2)}, "rope cos"));
+        EB_TRY(eb::check_numel(eb_tensor_numel(rope_sin), {(pos + 1), (hd / 2)}, "rope sin"));
         pro.rope_cos = (const float *)rope_cos->ptr;
         pro.rope_sin = (const float *)rope_sin->ptr;
     }

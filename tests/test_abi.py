@@ -77,6 +77,18 @@ def test_kv_write_validation():
     assert l.eb_launch_kv_write(None, None, 64, None, 0, 2, 0, 4, 8, 3) == 0
 
 
+def test_wrapping_shapes_are_refused():
+    """Shape products that wrap 64 bits are refused, not checked as their small remainder."""
+    l = eb.lib()
+    huge = 1 << 62
+    # cache: 4 rows x 2^62 heads x 4 dims = 2^66 elements, 0 after wrapping
+    st, msg = _err(l.eb_launch_kv_write, None, None, 64, None, 64, huge, 1, 4, 4, 0)
+    assert st == 3 and "overflows" in msg
+    st, msg = _err(l.eb_launch_attn_prefill, None, None, 64, None, 64, None, 64, None, 64, huge,
+                   huge, 4, 8, 0.3)
+    assert st == 3 and "overflows" in msg
+
+
 def test_prefill_validation():
     l = eb.lib()
     st, msg = _err(l.eb_launch_attn_prefill, None, None, 1 << 20, None, 1 << 20, None, 1 << 20,
