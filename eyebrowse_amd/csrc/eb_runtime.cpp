@@ -625,7 +625,11 @@ static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
     return eb::ok();
 }
 
-static eb_status device_workspace(eb_device *dev, size_t floats, float **out);
+// The device workspace is handed out with its mutex held (in *lk) until the caller's launch
+// is enqueued: another thread that grows it in between would free a buffer the launch is
+// about to use.
+using WsLock = std::unique_lock<std::mutex>;
+static eb_status device_workspace(eb_device *dev, size_t floats, float **out, WsLock &lk);
 
 // Where a prefill's pre-split workspace comes from: the device's grow-only workspace
 // (recorder launches), the caller's buffer (raw _ws launches; null with 0 floats is allowed
@@ -639,14 +643,15 @@ struct PrefillWs {
 };
 
 static eb_status prefill_ws(const PrefillWs &src, size_t h, size_t hkv, size_t hd, size_t rows,
-                            size_t nkeys, size_t qbase, size_t window, float **ws, size_t *wsn) {
+                            size_t nkeys, size_t qbase, size_t window, float **ws, size_t *wsn,
+                            WsLock &lk) {
     *ws = nullptr;
     *wsn = 0;
     if (!src.dev && !src.caller) return EB_OK;
     const size_t need = eb::prefill_workspace_floats(h, hkv, hd, rows, nkeys, qbase, window);
     if (need == 0) return EB_OK;
     if (src.dev) {
-        EB_TRY(device_workspace(src.dev, need, ws));
+        EB_TRY(device_workspace(src.dev, need, ws, lk));
     } else {
         if (src.floats < need)
             return fail(EB_SHAPE_MISMATCH, "attn_prefill: workspace holds %zu floats, needs %zu",
@@ -679,7 +684,8 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     EB_TRY(eb::check_ptr(o, "o"));
     float *ws;
     size_t wsn;
-    EB_TRY(prefill_ws(wsrc, h, hkv, hd, s, s, 0, 0, &ws, &wsn));
+    WsLock lk;
+    EB_TRY(prefill_ws(wsrc, h, hkv, hd, s, s, 0, 0, &ws, &wsn, lk));
     EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
     return eb::ok();
 }
@@ -711,7 +717,8 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     EB_TRY(eb::check_ptr(o, "o"));
     float *ws;
     size_t wsn;
-    EB_TRY(prefill_ws(wsrc, h, hkv, hd, rows, pos0 + rows, pos0, window, &ws, &wsn));
+    WsLock lk;
+    EB_TRY(prefill_ws(wsrc, h, hkv, hd, rows, pos0 + rows, pos0, window, &ws, &wsn, lk));
     if (h16)
         EB_TRY(eb::launch_attn_prefill_chunk_f16(st, q, static_cast<const uint16_t *>(kc),
                                                  static_cast<const uint16_t *>(vc), o, h, hkv,
@@ -786,10 +793,10 @@ static eb_status step_rows_checked(const float *knew, const float *vnew, size_t 
     return EB_OK;
 }
 
-// Grows the device's decode workspace. Stream ordered: the old buffer is freed only after
-// the stream drains.
-static eb_status device_workspace(eb_device *dev, size_t floats, float **out) {
-    std::lock_guard<std::mutex> lk(dev->ws_mu);
+// Grows the device's workspace. Stream ordered: the old buffer is freed only after the
+// stream drains. Returns with dev->ws_mu held in lk.
+static eb_status device_workspace(eb_device *dev, size_t floats, float **out, WsLock &lk) {
+    lk = WsLock(dev->ws_mu);
     if (floats > dev->ws_floats) {
         if (dev->capturing.load())
             return fail(EB_OTHER,
@@ -816,7 +823,8 @@ static eb_status device_decode(eb_device *dev, const float *q, const void *kc, c
                                const eb::DecodePrologue *pro = nullptr) {
     size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count, h16);
     float *ws = nullptr;
-    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
+    WsLock lk;
+    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws, lk));
     EB_TRY(eb::launch_attn_decode_any(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv,
                                       pos, hd, scale, ws, wsn, dev->cu_count, window, h16, pro));
     return eb::ok();
@@ -884,7 +892,8 @@ static eb_status device_linear(eb_device *dev, const eb_tensor *a,
     }
     const size_t wsn = eb::linear_workspace_floats(m, in_f);
     float *ws = nullptr;
-    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws));
+    WsLock lk;
+    if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws, lk));
     return linear_checked(dev->stream, static_cast<const float *>(a->ptr), eb_tensor_numel(a),
                           wp, wh, yp, yn, out_f, nseg, m, in_f, ws, wsn);
 }
@@ -1335,7 +1344,8 @@ eb_status eb_argmax(eb_recorder *rec, const eb_tensor *logits, eb_tensor *out_id
     if (out_idx->dev != rec->dev) return fail(EB_OTHER, "out_idx lives on another device");
     const size_t wsn = eb::argmax_workspace_floats(vocab);
     float *ws = nullptr;
-    EB_TRY(device_workspace(rec->dev, wsn, &ws));
+    WsLock lk;
+    EB_TRY(device_workspace(rec->dev, wsn, &ws, lk));
     return argmax_checked(rec->dev->stream, static_cast<const float *>(logits->ptr),
                           eb_tensor_numel(logits), static_cast<uint32_t *>(out_idx->ptr),
                           eb_tensor_numel(out_idx), vocab, ws, wsn);
