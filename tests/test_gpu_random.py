@@ -29,7 +29,7 @@ def draw(seed):
     return r, hd, hkv * g, hkv, scale
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_prefill(dev, seed):
     r, hd, h, hkv, sc = draw(seed)
     s = int(r.integers(1, 700))
@@ -48,7 +48,7 @@ def test_random_prefill(dev, seed):
         assert_close(got[r0:r0 + n], want[r0:r0 + n], what=f"rows {r0}+{n}")
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_chunk(dev, seed):
     r, hd, h, hkv, sc = draw(100 + seed)
     pos0 = int(r.integers(0, 1500))
@@ -83,7 +83,7 @@ def test_random_chunk(dev, seed):
         assert_close(got[rr:rr + 1], want, what=f"row {rr}")
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(20))
 def test_random_decode_step(dev, seed):
     """The fused step (new row written at pos, attention over 0..=pos, optional window)
     against kv_write + the oracle; the cache row must be the new row's bits (f32) or its
@@ -137,7 +137,7 @@ def _caches(dev, max_seq, hkv, hd, f16, seed):
             oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape))
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_raw_decode(dev, seed):
     """Stream-level decode on a caller workspace of exactly the size the public sizing
     function returns, for CU counts other than the device's (other split plans), f32 and
@@ -169,7 +169,7 @@ def test_random_raw_decode(dev, seed):
     assert_close(ot.to_f32().reshape(1, h, hd), want, what="raw decode")
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(20))
 def test_random_raw_prefill_ws(dev, seed):
     """Stream-level chunked prefill on a caller workspace of exactly the size
     eb_attn_prefill_workspace_floats returns (pre-split records and, for launches with few
