@@ -971,26 +971,6 @@ struct PrefillRange {
     size_t ws_floats;
 };
 
-// The pre-split pass pays one read and one write of the keys in range; it is used when at
-// least this many query rows (each workgroup of them re-staging every key) share them.
-constexpr int kPresplitMinRows = 256;
-
-// First tile and number of tiles the pre-split records cover: every key some query of the
-// launch can see.
-int presplit_tlo(const PrefillRange &r) {
-    return r.window > 0 ? (r.qbase - r.window + 1 > 0 ? r.qbase - r.window + 1 : 0) / kTile : 0;
-}
-int presplit_nt(const PrefillRange &r) { return (r.nkeys + kTile - 1) / kTile - presplit_tlo(r); }
-
-size_t presplit_floats(size_t hd, size_t hkv, const PrefillRange &r) {
-    if (hd < 32 || r.rows < kPresplitMinRows || r.nkeys <= 0) return 0;
-    const size_t rec = hd == 32    ? PrefillCfg<32, 4, 1, 1>::PS_FLOATS
-                       : hd == 64  ? PrefillCfg<64, 4, 1, 1>::PS_FLOATS
-                       : hd == 128 ? PrefillCfg<128, 4, 1, 1>::PS_FLOATS
-                                   : PrefillCfg<256, 4, 1, 1>::PS_FLOATS;
-    return hkv * (size_t)presplit_nt(r) * rec;
-}
-
 // The workgroup shape launch_prefill_hd picks for head_dim hd and g query heads per KV head:
 // HPW heads x WPH 32-row blocks x KSPLIT key splits.
 struct PrefillShape {
@@ -1000,6 +980,34 @@ PrefillShape prefill_shape(size_t hd, int g) {
     const int hpw = g % 4 == 0 ? 4 : g % 2 == 0 ? 2 : 1;
     return {hpw, 4 / hpw, (hpw == 4 || hd > 128) ? 1 : 2};
 }
+
+// The pre-split pass pays one read and one write of the keys in range; it is used when at
+// least this many query blocks (each of whose workgroups would re-stage every key) share
+// them: 3, or 2 at head_dim 256, whose split while staging is the dearer (measured on
+// chunks of 128 and 192 rows over long caches: 2 Qwen blocks -8.5 %, 3 +6 %, 4 Mistral
+// blocks +4-9 %, 2 Gemma-4 blocks +10 %).
+constexpr int kPresplitMinBlocks = 3;
+constexpr int kPresplitMinBlocks256 = 2;
+
+// First tile and number of tiles the pre-split records cover: every key some query of the
+// launch can see.
+int presplit_tlo(const PrefillRange &r) {
+    return r.window > 0 ? (r.qbase - r.window + 1 > 0 ? r.qbase - r.window + 1 : 0) / kTile : 0;
+}
+int presplit_nt(const PrefillRange &r) { return (r.nkeys + kTile - 1) / kTile - presplit_tlo(r); }
+
+size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
+    if (hd < 32 || r.rows <= 0 || r.nkeys <= 0) return 0;
+    const int qb_rows = kTile * prefill_shape(hd, (int)(h / hkv)).wph;
+    const int nqb = (r.rows + qb_rows - 1) / qb_rows;
+    if (nqb < (hd > 128 ? kPresplitMinBlocks256 : kPresplitMinBlocks)) return 0;
+    const size_t rec = hd == 32    ? PrefillCfg<32, 4, 1, 1>::PS_FLOATS
+                       : hd == 64  ? PrefillCfg<64, 4, 1, 1>::PS_FLOATS
+                       : hd == 128 ? PrefillCfg<128, 4, 1, 1>::PS_FLOATS
+                                   : PrefillCfg<256, 4, 1, 1>::PS_FLOATS;
+    return hkv * (size_t)presplit_nt(r) * rec;
+}
+
 
 // Key chunks: when the query blocks alone would leave most of the CUs idle (fewer than
 // kPrefillFewUnits workgroups: short prompts, a short chunk over a long cache), each
@@ -1051,7 +1059,7 @@ size_t chunk_floats(size_t hd, int H, const PrefillChunks &ch, const PrefillRang
     return ch.nchmax > 1 ? (size_t)ch.nchmax * r.rows * H * (hd + 4) : 0;
 }
 size_t workspace_floats(size_t hd, int H, int Hkv, const PrefillRange &r) {
-    return presplit_floats(hd, Hkv, r) + chunk_floats(hd, H, prefill_chunks(hd, H, Hkv, r), r);
+    return presplit_floats(hd, H, Hkv, r) + chunk_floats(hd, H, prefill_chunks(hd, H, Hkv, r), r);
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
@@ -1090,7 +1098,7 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
                            float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
     const bool plain = r.qbase == 0 && r.window == 0;
     // r.ws non-null: sized for workspace_floats (pre-split records, then key-chunk partials)
-    const size_t ps_floats = r.ws ? presplit_floats(HD, Hkv, r) : 0;
+    const size_t ps_floats = r.ws ? presplit_floats(HD, H, Hkv, r) : 0;
     const PrefillChunks ch = r.ws ? prefill_chunks(HD, H, Hkv, r) : PrefillChunks{};
     float *part_acc = ch.nchmax > 1 ? r.ws + ps_floats : nullptr;
     float *part_ml = part_acc ? part_acc + (size_t)ch.nchmax * r.rows * H * HD : nullptr;

@@ -212,7 +212,8 @@ eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_nu
                                        size_t hkv, size_t pos0, size_t rows, size_t hd,
                                        size_t max_seq, float scale, size_t window);
 /* Prefill with a workspace (no counterpart in the reference). With head_dim 32..256 and
- * at least 256 query rows, the _ws launches first split every key they can see once into
+ * at least 3 query blocks sharing the keys (2 at head_dim 256; a block is 32, 64 or 128
+ * rows by the GQA ratio), the _ws launches first split every key they can see once into
  * workspace records (K and V rows scaled by powers of two into f16 hi/lo halves, V
  * transposed), so that the attention kernel only copies them into LDS; the plain raw
  * launches split the keys again in every workgroup that stages them (same bits). When

@@ -2,7 +2,8 @@
 
 A prefill given a workspace (recorder launches use the device's; raw callers pass one to
 the _ws launches) may
-  - run the pre-split pass (head_dim 32..256, at least 256 query rows): every key in range
+  - run the pre-split pass (head_dim 32..256, at least 3 query blocks, 2 at head_dim 256,
+    share the keys): every key in range
     is split once into records that the attention kernel copies into LDS, where a plain
     raw launch (no workspace) splits while staging. Both hold the same values in LDS, so
     on shapes that are not cut into key chunks the outputs are equal bit for bit;
@@ -198,8 +199,9 @@ def test_workspace_sizes_and_refusal(dev):
             vt.numel(), ot.data_ptr, ot.numel(), h, hkv, s, hd, sc)
     with pytest.raises(eb.ShapeMismatch):
         eb.launch_attn_prefill_ws(*args, ws.data_ptr, need - 1)
-    # 1024 workgroups of 64-row blocks and fewer than 256 rows: no workspace at all
-    h2, hkv2, s2 = 512, 256, 200
+    # 512 workgroups of 64-row blocks, two blocks only (too few to share a pre-split pass
+    # at head_dim 128): no workspace at all
+    h2, hkv2, s2 = 512, 256, 100
     assert eb.attn_prefill_workspace_floats(h2, hkv2, hd, 0, s2) == 0
     q2 = upload(dev, oracle.randn((s2, h2, hd), 74))
     k2, v2 = upload(dev, oracle.randn((s2, hkv2, hd), 75)), upload(dev, oracle.randn((s2, hkv2, hd), 76))
