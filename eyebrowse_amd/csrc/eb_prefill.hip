@@ -1012,12 +1012,15 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
 // Key chunks: when the query blocks alone would leave most of the CUs idle (fewer than
 // kPrefillFewUnits workgroups: short prompts, a short chunk over a long cache), each
 // block's key tiles are cut into chunks of ctiles tiles, one workgroup each, merged
-// afterwards. The chunk is halved (in steps of KSPLIT tiles) until there are
-// kPrefillUnits workgroups (two rounds on 256 CUs) or it is kPrefillMinSteps steps long.
+// afterwards. The chunk length (in steps of KSPLIT tiles) is the one among smax, smax/2,
+// ... kPrefillMinSteps with the smallest estimated makespan: rounds of kPrefillSlots
+// workgroups per CU slot, each costing its steps plus kPrefillFixedSteps (a prologue and
+// an epilogue take about 8 us where a step takes 3.4 us).
 // Each chunk pays the q fragment, one unhidden staging step and an epilogue, which at
 // 256 block workgroups (a 2048-token prompt) cost what the better balance gains.
 constexpr int kPrefillFewUnits = 128;
-constexpr int kPrefillUnits = 512;
+constexpr int kPrefillSlots = 256;
+constexpr int kPrefillFixedSteps = 2;
 constexpr int kPrefillMinSteps = 2;
 struct PrefillChunks {
     int ctiles = 1 << 30;  // tiles per chunk (one chunk per block: no merge)
@@ -1043,8 +1046,23 @@ PrefillChunks prefill_chunks(size_t hd, int H, int Hkv, const PrefillRange &r) {
     };
     PrefillChunks ch;
     if ((long)nqb * ngroups >= kPrefillFewUnits) return ch;
+    // Halving candidates from smax down to kPrefillMinSteps steps, scored by the makespan
+    // of rounds of kPrefillSlots workgroups, each costing a fixed part (prologue and
+    // epilogue, about kPrefillFixedSteps steps) plus its chunk's steps.
+    // (4-wave workgroups at head_dim <= 128 run two per CU)
+    const long slots = (sh.hpw * sh.wph * sh.ksplit == 4 && hd <= 128) ? 2 * kPrefillSlots
+                                                                        : kPrefillSlots;
     int cs = smax;
-    while (cs > kPrefillMinSteps && units(cs) < kPrefillUnits) cs = (cs + 1) / 2;
+    long best = -1;
+    for (int c = smax;; c = (c + 1) / 2) {
+        const long u = units(c);
+        const long cost = (u + slots - 1) / slots * (kPrefillFixedSteps + c);
+        if (best < 0 || cost < best) {
+            best = cost;
+            cs = c;
+        }
+        if (c <= kPrefillMinSteps) break;
+    }
     if (cs >= smax) return ch;
     ch.ctiles = cs * sh.ksplit;
     int nmax = 1;
