@@ -1,21 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of the eyebrowse attention hot path on one MI355X.
 
-Headline (`value`): BASELINE config 2 at its largest point: a Qwen3-0.6B-shaped batch-1
-decode step at L = 8191 (new token's K/V written at position 8191 by kv_write, then
-attention over 8192 keys of a max_seq 8192 f32 cache, 16 query / 8 KV heads, hd 128).
-value = KV bytes read per step (2 * keys * Hkv * hd * 4) * steps / time, in GB/s.
+Headline (`value`): the largest single-GPU BASELINE configuration, configs[3]: a
+Mistral-7B-shaped batch-1 decode step at KV length 32768 (the new token's K/V written at
+position 32767, then attention over 32768 keys of a max_seq 32768 f32 cache, 32 query /
+8 KV heads, head_dim 128). value = KV bytes read per step (2 * keys * Hkv * hd * 4) *
+steps / time, in GB/s.
 
-One step = one HIP-graph launch of [kv_write K, kv_write V, attn_decode] (the kernels the
-library records for Attention::decode, crates/eyebrowse-nn/src/attention.rs:149-183).
-Steps rotate over enough distinct caches that the working set exceeds the 256 MB Infinity
-Cache, so the K/V bytes come from HBM. Inputs are resident in HBM before timing starts.
+One step = eb_launch_attn_decode_step (the kv_write(K), kv_write(V), attn_decode sequence
+of Attention::decode, crates/eyebrowse-nn/src/attention.rs:149-183, fused: the split-KV
+pass that also writes the new row, then the log-sum-exp merge). Exactly --steps steps are
+timed, as HIP graphs of consecutive steps. Steps rotate over enough distinct caches that
+the working set exceeds the 256 MB Infinity Cache, so the K/V bytes come from HBM. Inputs
+are resident in HBM before timing starts.
 
-Also reported: prefill TFLOP/s (2*H*hd*T*(T+1) algorithmic FLOPs) for the BASELINE
-prefill configs, decode GB/s at every BASELINE decode config, the roofline of the dominant
-kernel, and the CPU oracle timed on this host (cpu_baseline).
+The same line carries `roofline` (the decode step against HBM), `roofline_prefill` (the
+Mistral T=4096 causal prefill of the same config against the f16 and FP32 matrix peaks),
+`cpu_baseline` (the oracle on this host's cores, the same decode config) and, under
+`extra`, every other BASELINE decode / prefill config, the IEEE-half cache decodes,
+chunked prefill, the projections and a layer decode step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --only trace --workload NAME   (one workload, for rocprofv3)
+       python bench.py --trace-summary OUT.md TITLE CMD LABEL=CSV ...   (no GPU)
+       python bench.py --pmc-summary FETCH.csv WRITE.csv OUT.json       (no GPU)
+       python bench.py --sq-summary OUT.md CMD CSV                       (no GPU)
 """
 from __future__ import annotations
 
@@ -94,6 +103,19 @@ class Hip:
     def launch(self, ge, stream):
         self.ok(self.l.hipGraphLaunch(ge, ctypes.c_void_p(stream)), "hipGraphLaunch")
 
+    def time_region(self, stream, body):
+        """ms of body()'s work, bracketed by HIP events on `stream`."""
+        a, b = self.event(), self.event()
+        s = ctypes.c_void_p(stream)
+        self.ok(self.l.hipStreamSynchronize(s), "hipStreamSynchronize")
+        self.ok(self.l.hipEventRecord(a, s), "hipEventRecord")
+        body()
+        self.ok(self.l.hipEventRecord(b, s), "hipEventRecord")
+        ms = self.elapsed_ms(a, b)
+        self.l.hipEventDestroy(a)
+        self.l.hipEventDestroy(b)
+        return ms
+
     def time_loop(self, stream, n, body):
         """Average ms of body(i) over n iterations, bracketed by HIP events on `stream`."""
         a, b = self.event(), self.event()
@@ -160,6 +182,7 @@ class DecodeWorkload:
         self.wsn = eb.attn_decode_workspace_floats(H, Hkv, pos, hd, self.cus)
         self.ws = eb.Tensor.empty(dev, (max(self.wsn, 1),))
         self.per_graph = max(per_graph // self.n_caches, 1) * self.n_caches
+        self.rem_graphs = {}
         self.graph = hip.capture(dev.stream, lambda: [self._step(self.caches[i % self.n_caches])
                                                       for i in range(self.per_graph)])
 
@@ -185,8 +208,29 @@ class DecodeWorkload:
         ms = self.hip.time_loop(st, reps, lambda i: self.hip.launch(self.graph, st))
         return ms / self.per_graph, reps * self.per_graph
 
+    def run_exact(self, n):
+        """Average ms per step over exactly n steps: n // per_graph whole graphs, then one
+        graph of the n % per_graph remaining steps (captured once per length), all inside
+        one pair of HIP events."""
+        full, rem = divmod(n, self.per_graph)
+        if rem and rem not in self.rem_graphs:
+            self.rem_graphs[rem] = self.hip.capture(
+                self.dev.stream,
+                lambda: [self._step(self.caches[i % self.n_caches]) for i in range(rem)])
+        st = self.dev.stream
+
+        def body():
+            for _ in range(full):
+                self.hip.launch(self.graph, st)
+            if rem:
+                self.hip.launch(self.rem_graphs[rem], st)
+        return self.hip.time_region(st, body) / max(n, 1)
+
     def close(self):
         self.hip.l.hipGraphExecDestroy(self.graph)
+        for g in self.rem_graphs.values():
+            self.hip.l.hipGraphExecDestroy(g)
+        self.rem_graphs.clear()
 
 
 class PrefillWorkload:
@@ -220,41 +264,60 @@ class PrefillWorkload:
 
 # ------------------------------------------------------------------ CPU baseline
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     """The oracle (a C restatement of the reference's CPU attention,
-    crates/eyebrowse-kernels/src/testutil.rs:177-218) timed on this host's cores, single
-    thread, on the headline decode step (8192 keys, Qwen shape) repeated for ~budget_s."""
+    crates/eyebrowse-kernels/src/testutil.rs:130-218) timed on this host on the headline
+    workload: the Mistral decode at 32768 keys, one thread pinned to one core
+    (os.sched_setaffinity) for about budget_s; the prefill restatement on the last 32 query
+    rows of Mistral T=4096 (the heaviest rows) on the same core; and, as a secondary figure,
+    the same decode with the heads spread over up to 16 OpenMP threads (the GPU box's CPU
+    share)."""
     import oracle
 
-    H, Hkv, hd, max_seq, pos = 16, 8, 128, 8192, 8191
+    H, Hkv, hd, max_seq, pos = 32, 8, 128, 32768, 32767
     rng = np.random.default_rng(1)
     q = randn(rng, (H, hd))
     kc = randn(rng, (max_seq, Hkv, hd))
     vc = randn(rng, (max_seq, Hkv, hd))
     sc = float(oracle.default_scale(hd))
-    oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc)
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= budget_s:
-            break
-    kv_bytes = 2 * (pos + 1) * Hkv * hd * 4
-    gbs = kv_bytes * n / dt / 1e9
-
-    # prefill sample: the last 16 query rows of Qwen T=4096 (the heaviest rows)
     T = 4096
     pq, pk, pv = randn(rng, (T, H, hd)), randn(rng, (T, Hkv, hd)), randn(rng, (T, Hkv, hd))
-    rows = 16
-    t1 = time.perf_counter()
-    oracle.attn_prefill(pq, pk, pv, H, Hkv, T, hd, sc, rows=(T - rows, rows), threads=1)
-    pdt = time.perf_counter() - t1
+    rows = 32
+    allowed = os.sched_getaffinity(0)
+    core = min(allowed)
+    os.sched_setaffinity(0, {core})
+    try:
+        oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc)  # warm
+        n, t0 = 0, time.perf_counter()
+        while True:
+            oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= budget_s:
+                break
+        t1 = time.perf_counter()
+        oracle.attn_prefill(pq, pk, pv, H, Hkv, T, hd, sc, rows=(T - rows, rows), threads=1)
+        pdt = time.perf_counter() - t1
+    finally:
+        os.sched_setaffinity(0, allowed)
+    kv_bytes = 2 * (pos + 1) * Hkv * hd * 4
+    gbs = kv_bytes * n / dt / 1e9
     pflops = sum(2.0 * 2 * H * hd * (i + 1) for i in range(T - rows, T))
 
-    # secondary: the same decode with the oracle's heads spread over the host's cores
-    # (16 at most: the GPU box's CPU share)
-    mt = max(1, min(16, os.cpu_count() or 1))
+    mt = max(1, min(16, len(allowed)))
     m, t2 = 0, time.perf_counter()
     while True:
         oracle.attn_decode(q, kc, vc, H, Hkv, pos, hd, max_seq, sc, threads=mt)
@@ -264,12 +327,13 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
             break
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"oracle attn_decode, Qwen3 shape 16/8 heads hd128, 8192 keys, {n} calls "
-                  f"in {dt:.1f} s, 1 thread",
+        "sample": f"oracle attn_decode on the headline workload (Mistral 32/8 heads, hd 128, "
+                  f"32768 keys of a 32768-row f32 cache): {n} calls in {dt:.1f} s, 1 thread "
+                  f"pinned to core {core}",
+        "cpu_model": cpu_model(), "host_cpus": os.cpu_count(), "allowed_cpus": len(allowed),
         "prefill_gflops": round(pflops / pdt / 1e9, 3),
-        "prefill_sample": f"oracle attn_prefill, Qwen3 T=4096, last {rows} rows, 1 thread, "
-                          f"{pdt:.1f} s",
-        "host_cpus": os.cpu_count(),
+        "prefill_sample": f"oracle attn_prefill, Mistral T=4096, last {rows} query rows, "
+                          f"1 thread pinned to core {core}, {pdt:.2f} s",
         "all_cores_value": round(kv_bytes * m / mdt / 1e9, 3),
         "all_cores": mt,
         "all_cores_sample": f"the same decode, heads over {mt} OpenMP threads, {m} calls in "
@@ -284,8 +348,8 @@ def decode_extras(eb, hip, dev, sc128) -> dict:
     cfgs = [("qwen_L512", 16, 8, 128, 8192, 512, sc128),
             ("qwen_L2048", 16, 8, 128, 8192, 2048, sc128),
             ("qwen_L4096", 16, 8, 128, 8192, 4096, sc128),
+            ("qwen_L8191", 16, 8, 128, 8192, 8191, sc128),
             ("mistral_keys8193", 32, 8, 128, 32768, 8192, sc128),
-            ("mistral_keys32768", 32, 8, 128, 32768, 32767, sc128),
             ("gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0)]
     # IEEE-half caches (no counterpart in the reference): half the bytes per key.
     cfgs += [("f16_qwen_L8191", 16, 8, 128, 8192, 8191, sc128, True),
@@ -481,8 +545,12 @@ def traffic_run(eb, hip, dev, sc128):
     graph) so that every dispatch is counted on its own:
       1. kv_write copying 256 MiB (a plain copy of known size: FETCH_SIZE and WRITE_SIZE
          of it calibrate the counters), 3 times;
-      2. the headline decode step (Qwen L=8191) over 7 rotated caches, 14 times;
-      3. Qwen T=4096 prefill, 3 times."""
+      2. the headline decode step (Mistral, 32768 keys) over its rotated caches, 6 times;
+      3. Mistral T=4096 prefill (pre-split pass + attention), 3 times;
+      4. the Gemma-4 decode step at 16384 keys, 6 times, and its T=4096 prefill, 3 times.
+    The four workloads use distinct kernel instantiations, so per-kernel averages do not mix
+    them (Qwen shares the head_dim 128 merge and pre-split kernels with Mistral and is left
+    out)."""
     rows, hkv, hd = 65536, 8, 128
     src = eb.Tensor.empty(dev, (rows, hkv, hd))
     dst = eb.Tensor.empty(dev, (rows, hkv, hd))
@@ -491,24 +559,36 @@ def traffic_run(eb, hip, dev, sc128):
                            rows, hd, rows, 0)
     dev.synchronize()
     del src, dst
-    w = DecodeWorkload(eb, hip, dev, 16, 8, 128, 8192, 8191, sc128, per_graph=1)
-    for i in range(14):
-        w._step(w.caches[i % w.n_caches])
-    dev.synchronize()
-    w.close()
-    del w
-    p = PrefillWorkload(eb, dev, 16, 8, 128, 4096, sc128)
-    for _ in range(3):
-        p.launch()
-    dev.synchronize()
+    for H, Hkv, hdd, ms, pos, sc in ((32, 8, 128, 32768, 32767, sc128),
+                                     (16, 8, 256, 16384, 16383, 1.0)):
+        w = DecodeWorkload(eb, hip, dev, H, Hkv, hdd, ms, pos, sc, per_graph=1)
+        for i in range(6):
+            w._step(w.caches[i % w.n_caches])
+        dev.synchronize()
+        w.close()
+        del w
+        p = PrefillWorkload(eb, dev, H, Hkv, hdd, 4096, sc)
+        for _ in range(3):
+            p.launch()
+        dev.synchronize()
+        del p
+        print(json.dumps({"traffic_run": f"H{H} hd{hdd} done"}), flush=True)
     print(json.dumps({"traffic_run": "done", "copy_bytes": rows * hkv * hd * 4}), flush=True)
+
+
+def _kernel_name(raw: str) -> str:
+    import re
+    name = re.sub(r"\(anonymous namespace\)::", "", raw).split("(")[0]
+    return name.replace("void ", "").strip()
 
 
 def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
     """Per-kernel HBM traffic from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, KiB
     per dispatch) over `bench.py --only traffic`. Each counter is scaled by what it reads
-    for the 256 MiB kv_write copy in that run (bytes copied / counter bytes), so that
-    traffic is in the same bytes as the algorithmic figures."""
+    for the 256 MiB kv_write copies in that run (bytes copied / counter bytes), so that
+    traffic is in the same bytes as the algorithmic figures. On this part FETCH_SIZE reads
+    half of a known copy's read bytes (its factor measures about 2.0 in every run) and
+    WRITE_SIZE all of them (1.0): the factor is measured in each run, not assumed."""
     import csv
     import re
 
@@ -516,12 +596,11 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
 
     def load(path):
         # The first three kv_write dispatches are the calibration copies; later ones (the
-        # decode workload filling its caches) are left out of every average.
+        # decode workloads filling their caches) are left out of every average.
         per, calib = {}, []
         rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
         for r in rows:
-            name = re.sub(r"\(anonymous namespace\)::", "", r["Kernel_Name"]).split("(")[0]
-            name = name.replace("void ", "").strip()
+            name = _kernel_name(r["Kernel_Name"])
             if name == copy:
                 if len(calib) < 3:
                     calib.append(float(r["Counter_Value"]))
@@ -539,25 +618,193 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
                    "FETCH_SIZE_KiB": round(fetch[k], 1), "WRITE_SIZE_KiB": round(write.get(k, 0), 1)}
                for k in fetch}
     out = {"commands": [
-        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE --kernel-trace -f csv "
-        "-d $R/gpurun_out/pmc_fetch -o run -- python3 $R/bench.py --only traffic",
-        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc WRITE_SIZE --kernel-trace -f csv "
-        "-d $R/gpurun_out/pmc_write -o run -- python3 $R/bench.py --only traffic",
+        "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE "
+        "--kernel-trace -f csv -d $R/gpurun_out/pmc_fetch -o run -- python3 $R/bench.py "
+        "--only traffic",
+        "cd /tmp && export TMPDIR=/tmp && timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE "
+        "--kernel-trace -f csv -d $R/gpurun_out/pmc_write -o run -- python3 $R/bench.py "
+        "--only traffic",
         "python bench.py --pmc-summary gpurun_out/pmc_fetch/run_counter_collection.csv "
         "gpurun_out/pmc_write/run_counter_collection.csv profiles/traffic.json"],
         "calibration": "the run's first three kv_write_vec4_kernel dispatches, each copying "
                        "256 MiB (65536 rows x 8 heads x 128 f32): scale = 268435456 / "
-                       "(counter KiB * 1024)",
+                       "(counter KiB * 1024); FETCH_SIZE reads half of the copy's bytes, "
+                       "WRITE_SIZE all of them",
         "fetch_scale": round(fs, 4), "write_scale": round(ws, 4), "kernels": kernels}
-    dk = next((k for k in kernels if re.match(r"decode_kernel<128, 2\b", k)), None)
-    mk = next((k for k in kernels if k.startswith("decode_merge_kernel<128>")), None)
-    if dk:
-        t = kernels[dk]["fetch_bytes"] + kernels[dk]["write_bytes"]
-        if mk:
-            t += kernels[mk]["fetch_bytes"] + kernels[mk]["write_bytes"]
-        out["decode_qwen_L8191"] = t
+
+    def total(*patterns):
+        t = 0
+        for pat in patterns:
+            k = next((k for k in kernels if re.fullmatch(pat, k)), None)
+            if k is None:
+                return None
+            t += kernels[k]["fetch_bytes"] + kernels[k]["write_bytes"]
+        return t
+    out["decode_mistral_keys32768"] = total(r"decode_kernel<128, 4, false>",
+                                            r"decode_merge_kernel<128>")
+    out["prefill_mistral_T4096"] = total(r"presplit_kernel<128, false>",
+                                         r"prefill_kernel<128, 4, 1, 1, false, false, true>")
+    out["decode_gemma_keys16384"] = total(r"decode_kernel<256, 2, false>",
+                                          r"decode_merge_kernel<256>")
+    out["prefill_gemma_T4096"] = total(r"presplit_kernel<256, false>",
+                                       r"prefill_kernel<256, 2, 2, 1, false, false, true>")
     json.dump(out, open(out_json, "w"), indent=1)
     print(json.dumps(out, indent=1))
+
+
+def trace_summary(out_md: str, title: str, cmd: str, labelled: list) -> None:
+    """A markdown table of rocprofv3 kernel traces (one run_kernel_trace.csv per workload,
+    given as LABEL=CSV): per workload and kernel (and grid), the dispatch count and the
+    average / min / max duration, with the kernel's resources."""
+    import csv
+    lines = [f"# {title}", "", "Command (from the repository root on the GPU box, `R=$PWD`):",
+             "", "```", cmd, "```", "",
+             "| workload | kernel | workgroups | threads/WG | VGPR | AGPR | LDS B | scratch | "
+             "dispatches | avg µs | min µs | max µs |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for item in labelled:
+        label, path = item.split("=", 1)
+        groups = {}
+        for r in csv.DictReader(open(path)):
+            wg = 1
+            for ax in "XYZ":
+                wg *= int(r[f"Grid_Size_{ax}"]) // max(1, int(r[f"Workgroup_Size_{ax}"]))
+            th = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            key = (_kernel_name(r["Kernel_Name"]), wg, th, int(r.get("VGPR_Count", 0) or 0),
+                   int(r.get("Accum_VGPR_Count", 0) or 0), int(r.get("LDS_Block_Size", 0) or 0),
+                   int(r.get("Scratch_Size", 0) or 0))
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+            groups.setdefault(key, []).append(dur)
+        for (n, wg, th, v, a, lds, scr), ds in groups.items():
+            ds.sort()
+            lines.append(f"| {label} | `{n}` | {wg} | {th} | {v} | {a} | {lds} | {scr} | "
+                         f"{len(ds)} | {sum(ds) / len(ds):.2f} | {ds[0]:.2f} | {ds[-1]:.2f} |")
+    open(out_md, "w").write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def sq_summary(out_md: str, cmd: str, csv_path: str) -> None:
+    """Per-dispatch averages of the SQ / GRBM counters of one rocprofv3 --pmc run, per
+    kernel and grid (the counters are whole-chip totals per dispatch), with: VALU
+    instructions per MFMA instruction; MFMA busy cycles per MFMA instruction; the share of
+    wave cycles spent waiting on any instruction; and the matrix pipe's busy share,
+    SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8), GRBM_GUI_ACTIVE being the
+    sum of the 8 XCDs' busy cycles (so the share is of the cycles the kernel ran, at the
+    clock it ran at)."""
+    import csv
+    tot, disp = {}, {}
+    for r in csv.DictReader(open(csv_path)):
+        key = (_kernel_name(r["Kernel_Name"]), r.get("Grid_Size", ""))
+        c = tot.setdefault(key, {})
+        c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        disp.setdefault(key, set()).add(r["Dispatch_Id"])
+    names = sorted({n for c in tot.values() for n in c})
+    lines = ["# SQ counters per dispatch", "", "Command (from the repository root on the GPU "
+             "box, `R=$PWD`):", "", "```", cmd, "```", "",
+             "| kernel | grid | dispatches | " + " | ".join(names) +
+             " | VALU/MFMA | MFMA busy cyc/MFMA | wait share | MFMA pipe busy |",
+             "|---" * (3 + len(names) + 4) + "|"]
+    for key, c in tot.items():
+        n = len(disp[key])
+        avg = {k: v / n for k, v in c.items()}
+        mf = avg.get("SQ_INSTS_MFMA", 0)
+        ratio = lambda a, b: f"{a / b:.2f}" if b else "-"  # noqa: E731
+        lines.append(f"| `{key[0]}` | {key[1]} | {n} | " +
+                     " | ".join(f"{avg.get(k, 0):.0f}" for k in names) + " | " +
+                     ratio(avg.get("SQ_INSTS_VALU", 0), mf) + " | " +
+                     ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0), mf) + " | " +
+                     ratio(avg.get("SQ_WAIT_INST_ANY", 0), avg.get("SQ_WAVE_CYCLES", 0)) + " | " +
+                     ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0),
+                           1024 * avg.get("GRBM_GUI_ACTIVE", 0) / 8) + " |")
+    open(out_md, "w").write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def trace_workload(eb, hip, dev, sc128, name: str) -> None:
+    """One workload alone, for a rocprofv3 kernel trace: decode steps through HIP graphs
+    (200 steps), prefill launches (3 warm-up + 20), the layer decode step (eager and graph),
+    or a Gemma-4 prompt through Attention.forward_qkv (the fused pre-attention pass, the
+    pre-split pass and the attention)."""
+    decode = {"decode_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, False),
+              "decode_gemma_keys16384": (16, 8, 256, 16384, 16383, 1.0, False),
+              "decode_qwen_L8191": (16, 8, 128, 8192, 8191, sc128, False),
+              "decode_f16_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, True)}
+    prefill = {"prefill_qwen_T512": (16, 8, 128, 512, sc128),
+               "prefill_qwen_T2048": (16, 8, 128, 2048, sc128),
+               "prefill_qwen_T4096": (16, 8, 128, 4096, sc128),
+               "prefill_mistral_T4096": (32, 8, 128, 4096, sc128),
+               "prefill_gemma_T4096": (16, 8, 256, 4096, 1.0)}
+    if name in decode:
+        H, Hkv, hd, ms, pos, sc, f16 = decode[name]
+        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc, f16=f16)
+        w.run_exact(200)
+        dev.synchronize()
+        w.close()
+    elif name in prefill:
+        H, Hkv, hd, T, sc = prefill[name]
+        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc)
+        for _ in range(23):
+            p.launch()
+        dev.synchronize()
+    elif name == "layer_step":
+        print(json.dumps(layer_step_extras(eb, hip, dev)), flush=True)
+    elif name == "prompt_gemma_T4096":
+        H, Hkv, hd, T = 16, 8, 256, 4096
+        rng = np.random.default_rng(6)
+        gq = eb.Tensor.from_f32(dev, (hd,), 1 + 0.1 * randn(rng, (hd,)))
+        gk = eb.Tensor.from_f32(dev, (hd,), 1 + 0.1 * randn(rng, (hd,)))
+        ones = eb.Tensor.from_f32(dev, (hd,), np.ones(hd, np.float32))
+        attn = eb.Attention(H, Hkv, hd, 1.0, q_norm=gq, k_norm=gk, v_norm=ones, norm_eps=1e-6)
+        rope = eb.Rope.build_partial(dev, T, hd, 32, 1e6)
+        kv = eb.KvCache.new(dev, 1, T, Hkv, hd)
+        q = eb.Tensor.from_f32(dev, (T, H * hd), randn(rng, (T, H * hd)))
+        k = eb.Tensor.from_f32(dev, (T, Hkv * hd), randn(rng, (T, Hkv * hd)))
+        v = eb.Tensor.from_f32(dev, (T, Hkv * hd), randn(rng, (T, Hkv * hd)))
+        for _ in range(10):
+            rec = eb.Recorder(dev)
+            attn.forward_qkv(rec, q, k, v, rope, kv, 0, T, 0)
+            rec.submit()
+        dev.synchronize()
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    print(json.dumps({"trace_workload": name, "done": True}), flush=True)
+
+
+def prefill_roofline(eb, hip, dev, sc128, reps: int = 20) -> dict:
+    """The prefill half of the metric on the same config as the headline (BASELINE
+    configs[3], Mistral-7B T=4096): the pre-split pass plus the attention kernel, HIP
+    events around `reps` back-to-back launches."""
+    p = PrefillWorkload(eb, dev, 32, 8, 128, 4096, sc128)
+    for _ in range(3):
+        p.launch()
+    ms = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+    tf = p.flops / (ms * 1e-3) / 1e12
+    traffic = None
+    tfp = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tfp):
+        traffic = json.load(open(tfp)).get("prefill_mistral_T4096")
+    del p
+    dev.synchronize()
+    return {
+        "bound": "mfma",
+        "config": "mistral-7b-shaped causal prefill, T=4096, 32 q / 8 KV heads, head_dim 128, "
+                  "f32 q/k/v (BASELINE configs[3])",
+        "kernel": "presplit_kernel<128,false> + prefill_kernel<128,4,1,1,false,false,true>",
+        "mfma": "v_mfma_f32_32x32x16_f16 on exact f16 hi/lo splits of the f32 operands, "
+                "three products per product (f32-accurate), f32 accumulation",
+        "achieved": round(tf, 2), "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
+        "peak_fp32_mfma": FP32_MFMA_PEAK_TFLOPS,
+        "frac_fp32_mfma": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+        "issued_f16_mfma_TFLOPs": round(3 * tf, 1),
+        "frac_issued_f16_mfma": round(3 * tf / F16_MFMA_PEAK_TFLOPS, 4),
+        "traffic": traffic, "algorithmic_flops_per_launch": p_flops(32, 128, 4096),
+        "avg_launch_ms": round(ms, 5),
+    }
+
+
+def p_flops(H, hd, T):
+    return 2.0 * H * hd * T * (T + 1)
 
 
 # ------------------------------------------------------------------ main
@@ -571,20 +818,36 @@ def main():
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
                     help="no GPU: turn the counter_collection.csv files of the FETCH_SIZE and "
                          "WRITE_SIZE passes over `--only traffic` into per-kernel HBM bytes")
+    ap.add_argument("--trace-summary", nargs="+", metavar="ARG",
+                    help="no GPU: OUT_MD TITLE CMD LABEL=KERNEL_TRACE_CSV ...")
+    ap.add_argument("--sq-summary", nargs=3, metavar=("OUT_MD", "CMD", "CSV"),
+                    help="no GPU: per-kernel SQ counter table of a --pmc run")
     ap.add_argument("--only", choices=["headline", "all", "prefill", "projections", "layer",
-                                       "traffic"], default="all",
-                    help="headline: the decode line only; prefill / projections / layer: "
-                         "only those extras (prints their timings, not the contract line); "
-                         "traffic: a short run for rocprofv3 --pmc passes")
+                                       "traffic", "trace"], default="all",
+                    help="headline: the contract line without extras; prefill / projections / "
+                         "layer: only those extras; traffic: a short run for rocprofv3 --pmc "
+                         "passes; trace: one --workload for a rocprofv3 kernel trace")
+    ap.add_argument("--workload", default="", help="the workload of --only trace")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.trace_summary:
+        if len(args.trace_summary) < 4:
+            raise SystemExit("--trace-summary OUT_MD TITLE CMD LABEL=CSV ...")
+        out_md, title, cmd, *labelled = args.trace_summary
+        trace_summary(out_md, title, cmd, labelled)
+        return
+    if args.sq_summary:
+        sq_summary(*args.sq_summary)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the eyebrowse attention path is a single-device "
               "workload and this build has no multi-GPU path (run with --gpus 1).",
               file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        raise SystemExit("--steps must be >= 1 and --warmup >= 0")
 
     import eyebrowse_amd as eb
     hip = Hip()
@@ -592,6 +855,9 @@ def main():
     sc128 = float(np.float32(1.0) / np.sqrt(np.float32(128)))
     if args.only == "traffic":
         traffic_run(eb, hip, dev, sc128)
+        return
+    if args.only == "trace":
+        trace_workload(eb, hip, dev, sc128, args.workload)
         return
     if args.only == "prefill":
         print(json.dumps(prefill_extras(eb, hip, dev, sc128)), flush=True)
@@ -603,19 +869,29 @@ def main():
         print(json.dumps(layer_step_extras(eb, hip, dev)), flush=True)
         return
 
-    # Headline: Qwen decode L=8191. A step is one kernel (kv_write + split-KV attention +
-    # merge), so the step time is also the dominant kernel's average launch duration.
-    head = DecodeWorkload(eb, hip, dev, 16, 8, 128, 8192, 8191, sc128)
-    head.run_steps(args.warmup)
+    # Headline: Mistral decode at 32768 keys (the largest single-GPU
+    # decode). A step is the fused decode launch (new-row write + split-KV pass) and the
+    # merge, so the step time bounds the dominant kernel's launch duration from above.
+    H, Hkv, hd, max_seq, pos = 32, 8, 128, 32768, 32767
+    head = DecodeWorkload(eb, hip, dev, H, Hkv, hd, max_seq, pos, sc128)
+    if args.warmup:
+        head.run_exact(args.warmup)
     dev.synchronize()
-    ms_step, steps_run = head.run_steps(args.steps)
+    ms_step = head.run_exact(args.steps)
     dev.synchronize()
     value = head.kv_bytes / (ms_step * 1e-3) / 1e9
-    achieved = value
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tf):
-        traffic = json.load(open(tf)).get("decode_qwen_L8191")
+        traffic = json.load(open(tf)).get("decode_mistral_keys32768")
+    n_caches, per_graph, kv_bytes = head.n_caches, head.per_graph, head.kv_bytes
+    head.close()
+    del head
+    dev.synchronize()
+    print(f"[bench] headline decode {ms_step * 1e3:.2f} us/step, {value:.1f} GB/s",
+          file=sys.stderr, flush=True)
+    pf = prefill_roofline(eb, hip, dev, sc128)
+    print(f"[bench] prefill {pf['achieved']} TFLOP/s", file=sys.stderr, flush=True)
 
     extra = {}
     if args.only == "all":
@@ -623,13 +899,14 @@ def main():
         extra.update(prefill_extras(eb, hip, dev, sc128))
         extra.update(projection_extras(eb, hip, dev))
         extra.update(layer_step_extras(eb, hip, dev))
+        print("[bench] extras done", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps_run,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 6),
         "higher_is_better": True,
@@ -638,22 +915,25 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "qwen3-0.6b-shaped batch-1 decode step at L=8191: kv_write of the new "
-                        "token at pos 8191 + attention over 8192 keys (BASELINE configs[1])",
-            "n_heads": 16, "n_kv_heads": 8, "head_dim": 128, "max_seq": 8192, "pos": 8191,
-            "kv_caches_rotated": head.n_caches,
-            "launch": f"eb_launch_attn_decode_step, {head.per_graph} steps per hipGraph",
+            "workload": "mistral-7b-shaped batch-1 decode step at KV length 32768: kv_write "
+                        "of the new token at pos 32767 + attention over 32768 keys of a "
+                        "max_seq 32768 f32 cache (BASELINE configs[3])",
+            "n_heads": H, "n_kv_heads": Hkv, "head_dim": hd, "max_seq": max_seq, "pos": pos,
+            "kv_caches_rotated": n_caches,
+            "launch": f"eb_launch_attn_decode_step, HIP graphs of {per_graph} steps plus one "
+                      f"of the remainder (exactly --steps steps timed)",
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<128,2,false> (new-token write + split-KV pass) + decode_merge_kernel<128>",
-            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "algorithmic_bytes_per_launch": head.kv_bytes, "avg_launch_ms": round(ms_step, 6),
+            "kernel": "decode_kernel<128,4,false> (new-row write + split-KV pass) + "
+                      "decode_merge_kernel<128>",
+            "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": kv_bytes, "avg_launch_ms": round(ms_step, 6),
         },
+        "roofline_prefill": pf,
         "extra": extra,
     }
-    head.close()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -144,6 +144,10 @@ SIGNATURES = {
                                  c_size, c_float]),
     "eb_launch_rope": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size, c_size,
                               c_size, c_size, c_size]),
+    "eb_launch_attn_prologue": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
+                                       c_size, c_size, c_size, c_vp, c_vp, c_vp, c_float, c_vp,
+                                       c_vp, c_size, c_size, c_vp, c_size, c_vp, c_size, c_vp,
+                                       c_size, c_size, c_int]),
     "eb_rope_build_partial": (c_st, [c_vp, c_size, c_size, c_size, c_float,
                                      ctypes.POINTER(c_vp)]),
     "eb_rope_tables_release": (None, [c_vp]),

@@ -39,6 +39,7 @@ SOURCES = [
     "eb_runtime.cpp",
     "eb_nn.cpp",
     "eb_elementwise.hip",
+    "eb_rows.hip",
     "eb_decode.hip",
     "eb_prefill.hip",
     "eb_linear.hip",

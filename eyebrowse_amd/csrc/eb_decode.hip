@@ -753,8 +753,9 @@ namespace eb {
 
 // Workspace layout (floats): part_acc [nsplit*h*hd] | part_ml [nsplit*h*2]. Every split
 // writes its whole partial before the merge reads it, so no initialisation is needed.
-// The f32 plan's split count bounds the f16 one (more rows per iteration, never more
-// splits), so the f32 figure serves both cache types.
+// The figure is the cache type's own plan: the f32 and IEEE-half plans hold different
+// rows per iteration, and the half plan can take more splits (head_dim 256), so sizes
+// handed to callers come from decode_workspace_floats_any, the larger of the two.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
                                bool h16) {
     DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, h16);

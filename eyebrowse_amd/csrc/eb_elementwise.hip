@@ -1,4 +1,5 @@
-// kv_write, RMSNorm and RoPE for gfx950: the memory-bound steps around attention.
+// kv_write and RMSNorm for gfx950: memory-bound steps around attention (RoPE and the
+// per-head pre-attention pass are in eb_rows.hip).
 //
 //  kv_write  (crates/eyebrowse-kernels/src/ops.rs:70-87,150-179): both sides are
 //            seq-major, so the write is one contiguous copy of count*hkv*hd floats to
@@ -6,7 +7,6 @@
 //            so the result is bit-exact.
 //  rmsnorm   (crates/eyebrowse-kernels/src/rmsnorm.rs:6-64): one wave per row, the sum of
 //            squares reduced across the wave, y = x * (1/sqrt(ss/dim + eps)) * w.
-//  rope      (crates/eyebrowse-kernels/src/rope.rs:6-69): one thread per rotated pair.
 #include "eb_common.h"
 #include "eb_internal.h"
 
@@ -67,27 +67,6 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float *__restrict
     for (unsigned i = lane; i < dim; i += 64) orow[i] = xr[i] * inv * w[i];
 }
 
-__global__ __launch_bounds__(kBlock) void rope_kernel(const float *__restrict__ x,
-                                                      const float *__restrict__ cosb,
-                                                      const float *__restrict__ sinb,
-                                                      float *__restrict__ out, unsigned total,
-                                                      unsigned n_heads, unsigned half,
-                                                      unsigned base_pos) {
-    unsigned idx = blockIdx.x * kBlock + threadIdx.x;
-    if (idx >= total) return;
-    unsigned p = idx % half;
-    unsigned tmp = idx / half;
-    unsigned head = tmp % n_heads;
-    unsigned s = tmp / n_heads;
-    size_t base = ((size_t)s * n_heads + head) * (2 * half);
-    float c = cosb[(size_t)(s + base_pos) * half + p];
-    float sn = sinb[(size_t)(s + base_pos) * half + p];
-    float x1 = x[base + p];
-    float x2 = x[base + half + p];
-    out[base + p] = x1 * c - x2 * sn;
-    out[base + half + p] = x2 * c + x1 * sn;
-}
-
 }  // namespace
 
 namespace eb {
@@ -124,17 +103,6 @@ eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *
     unsigned blocks = (unsigned)((rows + 3) / 4);
     rmsnorm_kernel<<<blocks, kBlock, 0, st>>>(x, w, out, (unsigned)rows, (unsigned)dim, eps);
     return check_launch("rmsnorm");
-}
-
-eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,
-                      float *out, size_t seq, size_t n_heads, size_t hd, size_t base_pos) {
-    size_t total = seq * n_heads * (hd / 2);
-    if (total == 0) return EB_OK;
-    unsigned blocks = (unsigned)((total + kBlock - 1) / kBlock);
-    rope_kernel<<<blocks, kBlock, 0, st>>>(x, cosb, sinb, out, (unsigned)total,
-                                           (unsigned)n_heads, (unsigned)(hd / 2),
-                                           (unsigned)base_pos);
-    return check_launch("rope");
 }
 
 }  // namespace eb

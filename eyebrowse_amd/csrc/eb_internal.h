@@ -77,6 +77,13 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                              float scale, float *ws, size_t ws_floats, int cu_count,
                              size_t window = 0);
+// eb_launch_attn_decode_step after its arguments are resolved: shape checks, the
+// workspace size check (workspace_floats must cover decode_workspace_floats), the launch.
+eb_status decode_step_raw(hipStream_t st, const float *q, size_t q_numel, const float *knew,
+                          const float *vnew, size_t new_numel, float *kc, size_t kc_numel,
+                          float *vc, size_t vc_numel, float *o, size_t o_numel, size_t h,
+                          size_t hkv, size_t pos, size_t hd, size_t max_seq, float scale,
+                          float *workspace, size_t workspace_floats, int cu_count);
 // The same over caches of f32 (h16 false) or IEEE half (h16 true) elements; f16 caches
 // need head_dim >= 8.
 // The part of Attention::decode between the projections and the attention, done inside
@@ -112,6 +119,16 @@ eb_status attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q, const eb_
                                  const eb_tensor *q_norm, const eb_tensor *k_norm,
                                  const eb_tensor *v_norm, float eps, const eb_tensor *rope_cos,
                                  const eb_tensor *rope_sin);
+// Attention::prefill between the projections and the attention as one launch: q/k/v
+// RMSNorm (null gains: none), RoPE of q and k at base_pos (null tables: none), q into
+// q_out [rows, h, hd] and K / V into cache rows base_pos.. (f32 or IEEE-half caches).
+// Handle-level, used by eb_attention_forward_qkv.
+eb_status attn_rows_fused(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                          const eb_tensor *v, eb_tensor *q_out, eb_tensor *kcache,
+                          eb_tensor *vcache, size_t rows, size_t h, size_t hkv, size_t hd,
+                          size_t base_pos, size_t max_seq, const eb_tensor *q_norm,
+                          const eb_tensor *k_norm, const eb_tensor *v_norm, float eps,
+                          const eb_tensor *rope_cos, const eb_tensor *rope_sin);
 // linear_f16w: y[i][m, o] = sum_k x[m, k] * w[i][o, k] for nseg (1..kLinearMaxSegs)
 // weight/output pairs sharing x; w IEEE half [out_f[i], in_f]. m <= kLinearGemvRows runs
 // the weight-streaming kernel; more rows run the split-f16 matrix-core GEMM, which needs
@@ -129,6 +146,28 @@ eb_status launch_argmax(hipStream_t st, const float *x, size_t n, uint32_t *out,
                         size_t ws_floats);
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,
                          size_t rows, size_t dim, float eps);
+// Head rows for the pre-attention pass (RMSNorm, RoPE, store into caches or q) of up to
+// three segments [rows, nh, hd]; see eb_rows.hip. Arguments validated by the caller; hd
+// even; element counts below 2^31.
+struct RowSeg {
+    const float *src;   // [rows, nh, hd] f32
+    void *dst;          // [*, nh, hd], f32 or IEEE half elements
+    const float *gain;  // [hd] RMSNorm gain, or null: no norm
+    int nh;
+    int dst_row0;       // destination row of token 0
+    bool rope;          // RoPE at table row rope_row0 + token
+    bool half;          // dst holds IEEE half (round to nearest even)
+};
+struct RowsArgs {
+    RowSeg seg[3];
+    int nseg;
+    int rows, hd;
+    float eps;
+    const float *cosb, *sinb;  // [>= rope_row0 + rows, hd / 2], null without RoPE
+    int rope_row0;
+    int start[4];  // set by launch_attn_rows: first head row of each segment
+};
+eb_status launch_attn_rows(hipStream_t st, const RowsArgs &a);
 eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const float *sinb,
                       float *out, size_t seq, size_t n_heads, size_t hd, size_t base_pos);
 

@@ -3,7 +3,7 @@
 // Replaces linear_f16w (crates/eyebrowse-kernels/src/matmul.rs:84-144), a 16x16-tiled
 // scalar GEMM that unpacks two halves per u32 word. The weight layout is the reference's:
 // the logical [out, in] matrix flattened row-major, two halves per 32-bit word, low half
-// first (crates/eyebrowse-gpu/src/tensor.rs:7-23); read as little-endian 16-bit units it
+// first (crates/eyebrowse-gpu/src/tensor.rs:6-23); read as little-endian 16-bit units it
 // is a plain half array, which is how the kernels address it.
 //
 // Two regimes:

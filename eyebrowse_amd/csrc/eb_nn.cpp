@@ -211,25 +211,6 @@ void eb_attention_release(eb_attention *attn) { delete attn; }
 
 }  // extern "C"
 
-namespace {
-
-// Optional per-head RMSNorm (attention.rs:62-73): rows x head_dim, or a pass-through.
-eb_status maybe_norm(eb_recorder *rec, const eb_tensor *w, const eb_tensor *x, size_t rows,
-                     size_t hd, float eps, Owned &holder, const eb_tensor **y) {
-    if (!w) {
-        *y = x;
-        return EB_OK;
-    }
-    const size_t shape[2] = {rows, hd};
-    eb_tensor *o = nullptr;
-    EB_TRY(eb_tensor_empty(tensor_device_of(x), shape, 2, EB_F32, &o));
-    holder.t = o;
-    EB_TRY(eb_rmsnorm(rec, x, w, o, rows, hd, eps));
-    *y = o;
-    return EB_OK;
-}
-
-}  // namespace
 
 extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recorder *rec,
                                               const eb_tensor *q, const eb_tensor *k,
@@ -273,28 +254,23 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
         return eb::ok();
     }
 
-    Owned qn_h, kn_h, vn_h;
-    const eb_tensor *qn = nullptr, *kn = nullptr, *vn = nullptr;
-    EB_TRY(maybe_norm(rec, d.q_norm, q, rows * H, hd, d.norm_eps, qn_h, &qn));
-    EB_TRY(maybe_norm(rec, d.k_norm, k, rows * Hkv, hd, d.norm_eps, kn_h, &kn));
-    EB_TRY(maybe_norm(rec, d.v_norm, v, rows * Hkv, hd, d.norm_eps, vn_h, &vn));
-
-    eb_tensor *qr_t = nullptr, *kr_t = nullptr;
-    EB_TRY(eb_rope_apply(rope, rec, qn, rows, H, base_pos, &qr_t));
+    // attention.rs:62-97 in one launch: q/k/v norms, RoPE of q and k at base_pos, q into
+    // qr, the new rows' K (post-RoPE) and V (post-norm) into the cache at base_pos.
+    const size_t qshape[3] = {rows, H, hd};
+    eb_tensor *qr_t = nullptr;
+    EB_TRY(eb_tensor_empty(tensor_device_of(q), qshape, 3, EB_F32, &qr_t));
     Owned qr(qr_t);
-    EB_TRY(eb_rope_apply(rope, rec, kn, rows, Hkv, base_pos, &kr_t));
-    Owned kr(kr_t);
-
+    EB_TRY(eb::attn_rows_fused(rec, q, k, v, qr.t, kc, vc, rows, H, Hkv, hd, base_pos,
+                               kv->max_seq, d.q_norm, d.k_norm, d.v_norm, d.norm_eps, rope->cos,
+                               rope->sin));
     const size_t oshape[2] = {rows, H * hd};
     eb_tensor *o_t = nullptr;
     EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape, 2, EB_F32, &o_t));
     Owned o(o_t);
-    // attention.rs:78-97 writes the new rows' K (post-RoPE) and V into the cache.
-    EB_TRY(eb_kv_write(rec, kc, kr.t, Hkv, rows, hd, kv->max_seq, base_pos));
-    EB_TRY(eb_kv_write(rec, vc, vn, Hkv, rows, hd, kv->max_seq, base_pos));
     if (base_pos == 0 && d.window == 0 && eb_tensor_dtype(kc) == EB_F32) {
-        // attention.rs:104-115 (routing rule :40): a prompt attends its fresh kr / v.
-        EB_TRY(eb_attn_prefill(rec, qr.t, kr.t, vn, o.t, H, Hkv, rows, hd, d.scale));
+        // attention.rs:104-115 (routing rule :40): a prompt attends its fresh K / V, which
+        // are cache rows 0..rows-1 ([rows, Hkv, hd] at the start of the seq-major cache).
+        EB_TRY(eb_attn_prefill(rec, qr.t, kc, vc, o.t, H, Hkv, rows, hd, d.scale));
     } else {
         // A continuation chunk, a windowed prompt, or any prompt over an f16 cache
         // (so that prompt and decode read the same rounded K/V) attends the cache.

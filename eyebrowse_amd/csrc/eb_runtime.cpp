@@ -4,13 +4,14 @@
 //    crates/eyebrowse-gpu/src/device.rs:20-28), an exact-size buffer pool
 //    (device.rs:82-110) and the split-KV decode workspace.
 //  - eb_tensor: a typed device buffer that goes back to the pool when released
-//    (crates/eyebrowse-gpu/src/tensor.rs:195-236).
+//    (crates/eyebrowse-gpu/src/tensor.rs:34-47,62-75).
 //  - eb_recorder: recording = enqueueing on the device stream; submit reports errors
 //    (crates/eyebrowse-gpu/src/recorder.rs:10-35).
 //  - The kernel entry points validate shapes and forward to the launchers in the
 //    kernel translation units.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstring>
@@ -151,8 +152,14 @@ struct eb_device {
     std::mutex pool_mu;
     std::unordered_map<size_t, std::vector<void *>> pool;  // exact byte size -> free buffers
     std::mutex ws_mu;
-    float *ws = nullptr;  // decode split workspace, grow-only, stream ordered
+    float *ws = nullptr;  // split / pre-split / partials workspace, grow-only, stream ordered
     size_t ws_floats = 0;
+    // Graphs whose kernels were captured with a workspace buffer in their arguments keep
+    // that buffer alive: live graph references per buffer, and buffers the workspace has
+    // outgrown that a graph still references (freed with the last such graph). ws_mu.
+    std::unordered_map<float *, int> ws_graph_refs;
+    std::vector<float *> ws_retired;
+    bool ws_in_capture = false;  // the running capture handed out the current workspace
     std::atomic<bool> capturing{false};  // the stream is being captured into a graph
     std::vector<Parked> parked;          // buffers released during the capture (pool_mu)
 };
@@ -161,6 +168,7 @@ struct eb_graph {
     eb_device *dev = nullptr;
     hipGraphExec_t exec = nullptr;
     std::vector<Parked> held;  // intermediates the graph's kernels read and write
+    float *ws = nullptr;       // the device workspace its kernels use (null: none)
 };
 
 struct eb_tensor {
@@ -192,6 +200,7 @@ static void device_destroy(eb_device *d) {
     for (auto &kv : d->pool)
         for (void *p : kv.second) (void)hipFree(p);
     if (d->ws) (void)hipFree(d->ws);
+    for (float *p : d->ws_retired) (void)hipFree(p);
     (void)hipStreamDestroy(d->stream);
     delete d;
 }
@@ -303,7 +312,7 @@ static eb_status tensor_alloc(eb_device *dev, const size_t *shape, size_t ndim, 
     if (numel == SIZE_MAX || __builtin_mul_overflow(numel, esz, &nbytes_check))
         return fail(EB_OUT_OF_MEMORY, "tensor of %zu dims: size overflows", ndim);
     // (numel * size).max(size): a zero-element tensor still owns one element
-    // (crates/eyebrowse-gpu/src/tensor.rs:228).
+    // (crates/eyebrowse-gpu/src/tensor.rs:67).
     size_t bytes = numel * esz;
     if (bytes < esz) bytes = esz;
     void *p = nullptr;
@@ -344,7 +353,7 @@ static eb_status tensor_from_host(eb_device *dev, const size_t *shape, size_t nd
         return fail(EB_SHAPE_MISMATCH, "from_host: data len %zu != shape numel %zu", n,
                     shape_numel(shape, ndim));
     if (n > 0 && !data) return fail(EB_SHAPE_MISMATCH, "from_host: data is null");
-    // Host-initialised tensors never draw from the pool (tensor.rs:238-257).
+    // Host-initialised tensors never draw from the pool (tensor.rs:77-96).
     eb_status st = tensor_alloc(dev, shape, ndim, dt, false, out);
     if (st != EB_OK) return st;
     if (n > 0) {
@@ -485,6 +494,31 @@ static void return_buffers(eb_device *d, std::vector<Parked> &v) {
     v.clear();
 }
 
+// The graph reference on the workspace buffer that the finished capture handed to its
+// kernels (null when it used none).
+static float *ws_capture_ref(eb_device *d) {
+    std::lock_guard<std::mutex> lk(d->ws_mu);
+    float *p = d->ws_in_capture ? d->ws : nullptr;
+    d->ws_in_capture = false;
+    if (p) ++d->ws_graph_refs[p];
+    return p;
+}
+
+// Drops a graph's workspace reference. A buffer the workspace has outgrown is freed with
+// its last graph (the caller has drained the stream, so no replay still runs).
+static void ws_graph_unref(eb_device *d, float *p) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lk(d->ws_mu);
+    auto it = d->ws_graph_refs.find(p);
+    if (it == d->ws_graph_refs.end() || --it->second > 0) return;
+    d->ws_graph_refs.erase(it);
+    auto r = std::find(d->ws_retired.begin(), d->ws_retired.end(), p);
+    if (r != d->ws_retired.end()) {
+        d->ws_retired.erase(r);
+        (void)hipFree(p);
+    }
+}
+
 eb_status eb_device_begin_capture(eb_device *dev) {
     if (!dev) return fail(EB_OTHER, "device is null");
     EB_TRY(not_capturing(dev, "begin_capture"));
@@ -506,15 +540,18 @@ eb_status eb_device_end_capture(eb_device *dev, eb_graph **inout) {
         held.swap(dev->parked);
     }
     dev->capturing.store(false);
+    float *ws_used = ws_capture_ref(dev);
     if (e != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
         return_buffers(dev, held);
+        ws_graph_unref(dev, ws_used);
         return eb::hip_fail(e, "hipStreamEndCapture (a call during the capture failed?)");
     }
     eb_graph *gr = *inout;
     if (gr && gr->dev != dev) {
         (void)hipGraphDestroy(g);
         return_buffers(dev, held);
+        ws_graph_unref(dev, ws_used);
         return fail(EB_OTHER, "end_capture: the graph belongs to another device");
     }
     if (gr) {
@@ -534,10 +571,13 @@ eb_status eb_device_end_capture(eb_device *dev, eb_graph **inout) {
         (void)hipGraphDestroy(g);
         if (e != hipSuccess) {
             return_buffers(dev, held);
+            ws_graph_unref(dev, ws_used);
             return eb::hip_fail(e, "graph update");
         }
         return_buffers(dev, gr->held);
         gr->held.swap(held);
+        ws_graph_unref(dev, gr->ws);
+        gr->ws = ws_used;
         return eb::ok();
     }
     auto *ng = new eb_graph();
@@ -547,10 +587,12 @@ eb_status eb_device_end_capture(eb_device *dev, eb_graph **inout) {
     if (e != hipSuccess) {
         delete ng;
         return_buffers(dev, held);
+        ws_graph_unref(dev, ws_used);
         return eb::hip_fail(e, "hipGraphInstantiate");
     }
     device_retain(dev);
     ng->held.swap(held);
+    ng->ws = ws_used;
     *inout = ng;
     return eb::ok();
 }
@@ -570,6 +612,7 @@ void eb_graph_release(eb_graph *g) {
     (void)hipStreamSynchronize(d->stream);
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     return_buffers(d, g->held);
+    ws_graph_unref(d, g->ws);
     delete g;
     device_unref(d);
 }
@@ -784,6 +827,54 @@ static eb_status rope_checked(hipStream_t st, const float *x, size_t xn, const f
     return eb::ok();
 }
 
+// Attention::prefill between the projections and the attention (nn/src/attention.rs:62-97)
+// in one launch: q/k/v RMSNorm (null gains: none), RoPE of q and k at base_pos (null
+// tables: none), q into q_out [rows, h, hd], K and V into cache rows base_pos.. (f32 or
+// IEEE half).
+static eb_status prologue_checked(hipStream_t st, const float *q, size_t qn, const float *k,
+                                  size_t kn, const float *v, size_t vn, size_t rows, size_t h,
+                                  size_t hkv, size_t hd, const float *gq, const float *gk,
+                                  const float *gv, float eps, const float *rc, const float *rs,
+                                  size_t tn, size_t base_pos, float *q_out, size_t qon,
+                                  void *kc, size_t kcn, void *vc, size_t vcn, size_t max_seq,
+                                  bool h16) {
+    EB_TRY(eb::check_heads(h, hkv));
+    if (hd == 0 || hd % 2 != 0)
+        return fail(EB_SHAPE_MISMATCH, "attention prologue: head_dim must be even and > 0");
+    if (base_pos > max_seq || rows > max_seq - base_pos)
+        return fail(EB_SHAPE_MISMATCH, "attention prologue: rows [%zu, %zu) exceed max_seq %zu",
+                    base_pos, base_pos + rows, max_seq);
+    EB_TRY(eb::check_numel(qn, {rows, h, hd}, "q"));
+    EB_TRY(eb::check_numel(kn, {rows, hkv, hd}, "k"));
+    EB_TRY(eb::check_numel(vn, {rows, hkv, hd}, "v"));
+    EB_TRY(eb::check_numel(qon, {rows, h, hd}, "q_out"));
+    EB_TRY(eb::check_numel(kcn, {max_seq, hkv, hd}, "kcache"));
+    EB_TRY(eb::check_numel(vcn, {max_seq, hkv, hd}, "vcache"));
+    if ((rc == nullptr) != (rs == nullptr)) return fail(EB_OTHER, "RoPE needs both tables");
+    if (rc) EB_TRY(eb::check_numel(tn, {(base_pos + rows), (hd / 2)}, "rope tables"));
+    if (rows == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(q, "q"));
+    EB_TRY(eb::check_ptr(k, "k"));
+    EB_TRY(eb::check_ptr(v, "v"));
+    EB_TRY(eb::check_ptr(q_out, "q_out"));
+    EB_TRY(eb::check_ptr(kc, "kcache"));
+    EB_TRY(eb::check_ptr(vc, "vcache"));
+    eb::RowsArgs a{};
+    a.nseg = 3;
+    const bool rope = rc != nullptr;
+    a.seg[0] = eb::RowSeg{q, q_out, gq, (int)h, 0, rope, false};
+    a.seg[1] = eb::RowSeg{k, kc, gk, (int)hkv, (int)base_pos, rope, h16};
+    a.seg[2] = eb::RowSeg{v, vc, gv, (int)hkv, (int)base_pos, false, h16};
+    a.rows = (int)rows;
+    a.hd = (int)hd;
+    a.eps = eps;
+    a.cosb = rc;
+    a.sinb = rs;
+    a.rope_row0 = (int)base_pos;
+    EB_TRY(eb::launch_attn_rows(st, a));
+    return eb::ok();
+}
+
 // Checks the new-token rows of a fused decode step ([hkv, hd] each).
 static eb_status step_rows_checked(const float *knew, const float *vnew, size_t new_n,
                                    size_t hkv, size_t hd) {
@@ -794,7 +885,9 @@ static eb_status step_rows_checked(const float *knew, const float *vnew, size_t 
 }
 
 // Grows the device's workspace. Stream ordered: the old buffer is freed only after the
-// stream drains. Returns with dev->ws_mu held in lk.
+// stream drains, and not at all while a captured graph still has it in its kernels'
+// arguments (it is then retired, and freed with the last such graph). Returns with
+// dev->ws_mu held in lk.
 static eb_status device_workspace(eb_device *dev, size_t floats, float **out, WsLock &lk) {
     lk = WsLock(dev->ws_mu);
     if (floats > dev->ws_floats) {
@@ -803,14 +896,19 @@ static eb_status device_workspace(eb_device *dev, size_t floats, float **out, Ws
                         "the device workspace would have to grow during a graph capture "
                         "(run the captured step once outside the capture first)");
         if (dev->ws) {
-            EB_HIP_TRY(hipStreamSynchronize(dev->stream));
-            EB_HIP_TRY(hipFree(dev->ws));
+            if (dev->ws_graph_refs.count(dev->ws)) {
+                dev->ws_retired.push_back(dev->ws);
+            } else {
+                EB_HIP_TRY(hipStreamSynchronize(dev->stream));
+                EB_HIP_TRY(hipFree(dev->ws));
+            }
             dev->ws = nullptr;
             dev->ws_floats = 0;
         }
         EB_HIP_TRY(hipMalloc((void **)&dev->ws, floats * sizeof(float)));
         dev->ws_floats = floats;
     }
+    if (dev->capturing.load()) dev->ws_in_capture = true;
     *out = dev->ws;
     return EB_OK;
 }
@@ -1011,6 +1109,26 @@ eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const
 
 }  // extern "C"
 
+// eb_launch_attn_decode_step's body, shared with the no-allocation entry point.
+eb_status eb::decode_step_raw(hipStream_t st, const float *q, size_t q_numel, const float *knew,
+                              const float *vnew, size_t new_numel, float *kc, size_t kc_numel,
+                              float *vc, size_t vc_numel, float *o, size_t o_numel, size_t h,
+                              size_t hkv, size_t pos, size_t hd, size_t max_seq, float scale,
+                              float *workspace, size_t workspace_floats, int cu_count) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq));
+    EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode(st, q, kc, vc, kc, vc, knew, vnew, o, h, hkv, pos, hd, scale,
+                                  workspace, workspace_floats, cus));
+    return eb::ok();
+}
+
 // Attention::decode's post-projection part in one fused step (see DecodePrologue):
 // q [h, hd], knew / vnew [hkv, hd] straight from the projections.
 eb_status eb::attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q,
@@ -1060,6 +1178,48 @@ eb_status eb::attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q,
     return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, kcache->ptr,
                          vcache->ptr, (const float *)knew->ptr, (const float *)vnew->ptr,
                          (float *)o->ptr, h, hkv, pos, hd, scale, window, h16, &pro);
+}
+
+// The prefill counterpart of attn_decode_step_fused: the handle form of prologue_checked.
+eb_status eb::attn_rows_fused(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                              const eb_tensor *v, eb_tensor *q_out, eb_tensor *kcache,
+                              eb_tensor *vcache, size_t rows, size_t h, size_t hkv, size_t hd,
+                              size_t base_pos, size_t max_seq, const eb_tensor *q_norm,
+                              const eb_tensor *k_norm, const eb_tensor *v_norm, float eps,
+                              const eb_tensor *rope_cos, const eb_tensor *rope_sin) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(k, "k", rec->dev));
+    EB_TRY(tensor_f32(v, "v", rec->dev));
+    EB_TRY(tensor_f32(q_out, "q_out", rec->dev));
+    bool h16 = false;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    const eb_tensor *norms[3] = {q_norm, k_norm, v_norm};
+    const float *g[3] = {nullptr, nullptr, nullptr};
+    for (int i = 0; i < 3; ++i) {
+        if (!norms[i]) continue;
+        EB_TRY(tensor_f32(norms[i], "norm gain", rec->dev));
+        if (eb_tensor_numel(norms[i]) != hd)
+            return fail(EB_SHAPE_MISMATCH, "norm gain holds %zu, head_dim is %zu",
+                        eb_tensor_numel(norms[i]), hd);
+        g[i] = static_cast<const float *>(norms[i]->ptr);
+    }
+    if ((rope_cos == nullptr) != (rope_sin == nullptr))
+        return fail(EB_OTHER, "RoPE needs both tables");
+    size_t tn = 0;
+    if (rope_cos) {
+        EB_TRY(tensor_f32(rope_cos, "rope cos", rec->dev));
+        EB_TRY(tensor_f32(rope_sin, "rope sin", rec->dev));
+        tn = std::min(eb_tensor_numel(rope_cos), eb_tensor_numel(rope_sin));
+    }
+    return prologue_checked(
+        rec->dev->stream, static_cast<const float *>(q->ptr), eb_tensor_numel(q),
+        static_cast<const float *>(k->ptr), eb_tensor_numel(k), static_cast<const float *>(v->ptr),
+        eb_tensor_numel(v), rows, h, hkv, hd, g[0], g[1], g[2], eps,
+        rope_cos ? static_cast<const float *>(rope_cos->ptr) : nullptr,
+        rope_sin ? static_cast<const float *>(rope_sin->ptr) : nullptr, tn, base_pos,
+        static_cast<float *>(q_out->ptr), eb_tensor_numel(q_out), kcache->ptr,
+        eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache), max_seq, h16);
 }
 
 extern "C" {
@@ -1205,18 +1365,9 @@ eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_nume
                                      float *o, size_t o_numel, size_t h, size_t hkv, size_t pos,
                                      size_t hd, size_t max_seq, float scale, float *workspace,
                                      size_t workspace_floats, int cu_count) {
-    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
-                                pos, hd, max_seq));
-    EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
-    int cus = cu_count > 0 ? cu_count : 256;
-    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus);
-    if (workspace_floats < need)
-        return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
-                    workspace_floats, need);
-    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
-    EB_TRY(eb::launch_attn_decode((hipStream_t)stream, q, kc, vc, kc, vc, knew, vnew, o, h, hkv,
-                                  pos, hd, scale, workspace, workspace_floats, cus));
-    return eb::ok();
+    return eb::decode_step_raw((hipStream_t)stream, q, q_numel, knew, vnew, new_numel, kc,
+                               kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos, hd, max_seq,
+                               scale, workspace, workspace_floats, cu_count);
 }
 
 // ---- raw launches over IEEE-half KV caches ------------------------------------------
@@ -1285,6 +1436,23 @@ eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel, const 
                             size_t dim, float eps) {
     return rmsnorm_checked((hipStream_t)stream, x, x_numel, weight, w_numel, out, out_numel,
                            rows, dim, eps);
+}
+
+eb_status eb_launch_attn_prologue(void *stream, const float *q, size_t q_numel, const float *k,
+                                  size_t k_numel, const float *v, size_t v_numel, size_t rows,
+                                  size_t h, size_t hkv, size_t hd, const float *q_norm,
+                                  const float *k_norm, const float *v_norm, float eps,
+                                  const float *rope_cos, const float *rope_sin,
+                                  size_t table_numel, size_t base_pos, float *q_out,
+                                  size_t q_out_numel, void *kcache, size_t kc_numel,
+                                  void *vcache, size_t vc_numel, size_t max_seq,
+                                  eb_dtype cache_dtype) {
+    if (cache_dtype != EB_F32 && cache_dtype != EB_F16)
+        return fail(EB_UNSUPPORTED_CONFIG, "attention prologue: caches must be f32 or f16");
+    return prologue_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, rows, h, hkv,
+                            hd, q_norm, k_norm, v_norm, eps, rope_cos, rope_sin, table_numel,
+                            base_pos, q_out, q_out_numel, kcache, kc_numel, vcache, vc_numel,
+                            max_seq, cache_dtype == EB_F16);
 }
 
 eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const float *cos,

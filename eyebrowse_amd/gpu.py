@@ -120,7 +120,7 @@ class Device:
 
 
 class Tensor:
-    """Tensor (crates/eyebrowse-gpu/src/tensor.rs:195-319). Dropping it returns the buffer
+    """Tensor (crates/eyebrowse-gpu/src/tensor.rs:34-157). Dropping it returns the buffer
     to the pool."""
 
     def __init__(self, handle: int, dev: Device):

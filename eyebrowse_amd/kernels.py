@@ -252,3 +252,18 @@ def launch_rope(stream: int, x: int, x_numel: int, cos: int, sin: int, table_num
                 base_pos: int) -> None:
     check(lib().eb_launch_rope(stream, x, x_numel, cos, sin, table_numel, out, out_numel, seq,
                                n_heads, head_dim, base_pos))
+
+
+def launch_attn_prologue(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                         v_numel: int, rows: int, h: int, hkv: int, hd: int, q_norm: int,
+                         k_norm: int, v_norm: int, eps: float, rope_cos: int, rope_sin: int,
+                         table_numel: int, base_pos: int, q_out: int, q_out_numel: int,
+                         kcache: int, kc_numel: int, vcache: int, vc_numel: int, max_seq: int,
+                         cache_dtype: int) -> None:
+    """eb_launch_attn_prologue: Attention::prefill between the projections and the attention
+    (crates/eyebrowse-nn/src/attention.rs:62-97) in one launch. Null (0) gains: no norm;
+    null tables: no RoPE."""
+    check(lib().eb_launch_attn_prologue(stream, q, q_numel, k, k_numel, v, v_numel, rows, h, hkv,
+                                        hd, q_norm, k_norm, v_norm, eps, rope_cos, rope_sin,
+                                        table_numel, base_pos, q_out, q_out_numel, kcache,
+                                        kc_numel, vcache, vc_numel, max_seq, int(cache_dtype)))

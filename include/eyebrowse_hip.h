@@ -81,18 +81,18 @@ size_t eb_pool_max_bytes(void);
 
 /* ---- tensor (crates/eyebrowse-gpu/src/tensor.rs:34-157) --------------------------- */
 
-/* Tensor::empty (tensor.rs:226-236): uninitialised, drawn from the pool when a free
+/* Tensor::empty (tensor.rs:62-75): uninitialised, drawn from the pool when a free
  * buffer of the exact byte size exists (sizes <= eb_pool_max_bytes()). */
 eb_status eb_tensor_empty(eb_device *dev, const size_t *shape, size_t ndim, eb_dtype dt,
                           eb_tensor **out);
-/* Tensor::from_f32 / from_u32 (tensor.rs:241-267): a fresh buffer (never drawn from the
+/* Tensor::from_f32 / from_u32 (tensor.rs:77-106): a fresh buffer (never drawn from the
  * pool) initialised from host memory (n elements must equal the shape's element count).
  * Like every tensor it is recycled into the pool on release when small enough. */
 eb_status eb_tensor_from_f32(eb_device *dev, const size_t *shape, size_t ndim,
                              const float *data, size_t n, eb_tensor **out);
 eb_status eb_tensor_from_u32(eb_device *dev, const size_t *shape, size_t ndim,
                              const uint32_t *data, size_t n, eb_tensor **out);
-/* Tensor::to_f32 / read_bytes (tensor.rs:279-318): waits for the stream, then copies.
+/* Tensor::to_f32 / read_bytes (tensor.rs:118-157): waits for the stream, then copies.
  * `n`/`nbytes` must equal the tensor's element / byte count. */
 eb_status eb_tensor_to_f32(const eb_tensor *t, float *host, size_t n);
 eb_status eb_tensor_read_bytes(const eb_tensor *t, void *host, size_t nbytes);
@@ -124,7 +124,9 @@ void eb_recorder_release(eb_recorder *rec);
  * While capturing: no host copies (eb_tensor_from_*, to_f32, read_bytes, eb_tensor_write)
  * and no synchronize; a device workspace that would have to grow fails the call (run the
  * step once eagerly first, which also fills the buffer pool). Buffers released during the
- * capture stay reserved until the graph is released or updated. Kernels take their
+ * capture stay reserved until the graph is released or updated, and so does the device
+ * workspace buffer the captured kernels use, also when later work grows the device's
+ * workspace (the outgrown buffer is freed with the last graph using it). Kernels take their
  * shapes and positions as launch arguments, so a decode step at a new position is a new
  * capture: pass the previous graph to eb_device_end_capture to update it in place. */
 typedef struct eb_graph eb_graph;
@@ -176,9 +178,10 @@ eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const
 /* Chunked causal prefill: q [rows,h,hd] holds the queries at positions pos0..pos0+rows-1,
  * whose K/V are already in the caches [max_seq,hkv,hd]; row r attends cache keys
  * 0..=pos0+r (or the last `window` of them). With pos0 == 0 and no window this is
- * attn_prefill over the cache; with rows == 1 it is attn_decode at pos0. The reference
- * routes such calls (rows > 1 at base_pos > 0, attention.rs:40) to attn_prefill over the
- * fresh rows only and defers chunked prefill; this is the attention that call intends. */
+ * attn_prefill over the cache; with rows == 1 it is attn_decode at pos0. No counterpart
+ * in the reference, which defers chunked prefill (README.md:25): its Attention::forward
+ * sends a multi-row call at base_pos > 0 to decode (nn/src/attention.rs:40-44), which
+ * projects and attends only the first row (:120-185). */
 eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,
                                 const eb_tensor *vcache, eb_tensor *o, size_t h, size_t hkv,
                                 size_t pos0, size_t rows, size_t hd, size_t max_seq,
@@ -276,6 +279,26 @@ eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel,
 eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const float *cos,
                          const float *sin, size_t table_numel, float *out, size_t out_numel,
                          size_t seq, size_t n_heads, size_t head_dim, size_t base_pos);
+/* The part of Attention::prefill between the projections and the attention
+ * (crates/eyebrowse-nn/src/attention.rs:62-97: q_norm / k_norm / v_norm RMSNorm, rope.apply
+ * of q and k at base_pos, kv_write of K and V) in one launch. q [rows,h,hd] and k / v
+ * [rows,hkv,hd] from the projections; per head row: RMSNorm with the [hd] gain when one is
+ * given (NULL: none; a weightless norm passes ones), then RoPE with the [table rows, hd/2]
+ * tables at row base_pos + token for q and k (NULL tables: none). The rotated q goes to
+ * q_out [rows,h,hd]; K and V go to cache rows base_pos.. of [max_seq,hkv,hd] caches of
+ * cache_dtype (EB_F32, or EB_F16 rounded to nearest even). RoPE is computed without fused
+ * multiply-adds, as the reference's f32 arithmetic does; rows without a norm are copied
+ * bit-exactly. hd even. The reference records 6 kernels for this (3 rmsnorm, 2 rope,
+ * 2 kv_write less the norms it skips). */
+eb_status eb_launch_attn_prologue(void *stream, const float *q, size_t q_numel, const float *k,
+                                  size_t k_numel, const float *v, size_t v_numel, size_t rows,
+                                  size_t h, size_t hkv, size_t hd, const float *q_norm,
+                                  const float *k_norm, const float *v_norm, float eps,
+                                  const float *rope_cos, const float *rope_sin,
+                                  size_t table_numel, size_t base_pos, float *q_out,
+                                  size_t q_out_numel, void *kcache, size_t kc_numel,
+                                  void *vcache, size_t vc_numel, size_t max_seq,
+                                  eb_dtype cache_dtype);
 
 /* ---- projections: linear_f16w (crates/eyebrowse-kernels/src/matmul.rs:84-144) -------
  * c [m, out_f] = a [m, in_f] . w^T, a and c f32, w the packed-f16 weight of logical shape

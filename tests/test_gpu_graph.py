@@ -179,3 +179,60 @@ def test_capture_rules(dev):
     g.launch()  # an empty graph runs
     dev.synchronize()
     g.release()
+
+
+def test_graph_keeps_its_workspace_when_the_device_workspace_grows():
+    """A captured step keeps the workspace buffer its kernels were captured with: eager work
+    that grows the device workspace afterwards must neither free it (the replays would then
+    write freed memory) nor change what the replays compute. Its own device, so that the
+    workspace starts small (the session device's may already be large)."""
+    note("graph: workspace growth between replays")
+    d2 = eb.Device.new(0)
+    attn, w, _keep = _layer(d2)
+    rope = eb.Rope.build(d2, MAX_SEQ, HD, 1e6)
+    kv_e = eb.KvCache.new(d2, 1, MAX_SEQ, HKV, HD)
+    kv_g = eb.KvCache.new(d2, 1, MAX_SEQ, HKV, HD)
+    _prompt(d2, attn, rope, kv_e, 100)
+    _prompt(d2, attn, rope, kv_g, 100)
+    x1 = oracle.randn((1, HIDDEN), 52)
+    ye, le, ie = _step(d2, attn, w["lm"], rope, kv_e, upload(d2, x1), 100)
+    ye, le = ye.to_f32(), le.to_f32()
+    ie = int(np.frombuffer(ie.read_bytes(), np.uint32)[0])
+    xg = upload(d2, x1)
+    d2.begin_capture()
+    try:
+        yg, lg, ig = _step(d2, attn, w["lm"], rope, kv_g, xg, 100)
+    finally:
+        graph = d2.end_capture()
+    graph.launch()
+    assert_bitwise(lg.to_f32(), le, "replay before growth: logits")
+    # A 1024-row prefill needs far more workspace (pre-split records, key-chunk partials)
+    # than the decode step: the device workspace grows while the graph is alive.
+    T = 1024
+    q = oracle.randn((T, H, HD), 60)
+    k = oracle.randn((T, HKV, HD), 61)
+    v = oracle.randn((T, HKV, HD), 62)
+    qt, kt, vt = upload(d2, q), upload(d2, k), upload(d2, v)
+    ot = eb.Tensor.empty(d2, (T, H, HD))
+    rec = eb.Recorder(d2)
+    eb.attn_prefill(rec, qt, kt, vt, ot, H, HKV, T, HD, float(oracle.default_scale(HD)))
+    rec.submit()
+    o_first = ot.to_f32()
+    # Fresh buffers allocated after the growth, NaN-filled: the replays must not touch them.
+    sizes = (1024, 4096, 16384, 65536, 262144, 1 << 20)
+    poison = [eb.Tensor.from_f32(d2, (n,), np.full(n, np.nan, np.float32)) for n in sizes]
+    pbits = [p.read_bytes() for p in poison]
+    for rep in range(3):
+        graph.launch()
+        assert_bitwise(yg.to_f32(), ye, f"replay {rep} after growth: layer output")
+        assert_bitwise(lg.to_f32(), le, f"replay {rep} after growth: logits")
+        assert int(np.frombuffer(ig.read_bytes(), np.uint32)[0]) == ie
+        for p, b in zip(poison, pbits):
+            assert p.read_bytes() == b, f"replay {rep} wrote a buffer allocated after the growth"
+        # eager work on the grown workspace between replays still gives its own bits
+        rec = eb.Recorder(d2)
+        eb.attn_prefill(rec, qt, kt, vt, ot, H, HKV, T, HD, float(oracle.default_scale(HD)))
+        rec.submit()
+        assert_bitwise(ot.to_f32(), o_first, f"eager prefill after replay {rep}")
+    graph.release()
+    d2.synchronize()

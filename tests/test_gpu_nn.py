@@ -40,7 +40,7 @@ def test_host_initialized_tensors_do_not_draw_from_the_pool():
     assert d.pooled(16) == 1
     np.testing.assert_array_equal(t.to_f32(), [1, 2, 3, 4])
     # Drop recycles every buffer up to MAX_POOLED_BYTES, host-initialised ones included
-    # (tensor.rs:202-208 calls recycle_buffer unconditionally).
+    # (tensor.rs:41-47 calls recycle_buffer unconditionally).
     t.release()
     assert d.pooled(16) == 2
 
@@ -127,11 +127,116 @@ def test_rope_kernel(dev, seq, nh, hd, theta, ra, base):
     c, s = oracle.rope_tables(ms, hd, theta, rope_angles=ra)
     want = oracle.rope(x, c, s, seq, nh, hd, base)
     got = out.to_f32()
-    assert oracle.rel_l2(got, want) < 1e-6
+    # the kernel rotates without fused multiply-adds, as the reference's f32 code does
+    assert_bitwise(got, want, "rope vs the oracle")
     if ra is not None:  # pass-through pairs are exact
         g3, x3 = got.reshape(seq, nh, hd), x.reshape(seq, nh, hd)
         np.testing.assert_array_equal(g3[..., ra:hd // 2], x3[..., ra:hd // 2])
         np.testing.assert_array_equal(g3[..., hd // 2 + ra:], x3[..., hd // 2 + ra:])
+
+
+@pytest.mark.parametrize("rows,H,Hkv,hd,base,norm,ra,dtype", [
+    (37, 16, 8, 128, 0, True, None, "f32"),   # Qwen prompt with QK-norm
+    (19, 16, 8, 256, 5, True, 32, "f32"),     # Gemma-4: partial rotary, continuation rows
+    (33, 4, 2, 96, 0, False, None, "f32"),    # head_dim 96 (12 lanes of a 16-lane group)
+    (9, 6, 3, 6, 2, True, None, "f32"),       # head_dim 6: the wave-per-row kernel
+    (21, 8, 4, 128, 3, False, None, "f16"),   # IEEE-half caches
+    (21, 8, 4, 64, 0, True, 16, "f16"),
+])
+def test_attention_prologue(dev, rows, H, Hkv, hd, base, norm, ra, dtype):
+    """eb_launch_attn_prologue (attention.rs:62-97 in one launch) against the oracle chain
+    rmsnorm -> rope -> kv_write. Without a norm every output is bit-exact (RoPE without
+    fused multiply-adds, V copied); with one, the sum of squares is taken in another order
+    (rel-L2 <= 1e-6). Cache rows outside [base, base + rows) keep their bits."""
+    note(f"attention prologue rows={rows} H={H} Hkv={Hkv} hd={hd} base={base} {dtype}")
+    max_seq = base + rows + 3
+    eps = 1e-6
+    q = oracle.randn((rows, H, hd), 31)
+    k = oracle.randn((rows, Hkv, hd), 32)
+    v = oracle.randn((rows, Hkv, hd), 33)
+    gq = (1 + 0.1 * oracle.randn((hd,), 34)).astype(np.float32)
+    gk = (1 + 0.1 * oracle.randn((hd,), 35)).astype(np.float32)
+    ones = np.ones(hd, np.float32)
+    c, s = oracle.rope_tables(max_seq, hd, 1e6, rope_angles=ra)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    gqt, gkt, gvt = upload(dev, gq), upload(dev, gk), upload(dev, ones)
+    ct, st = upload(dev, c), upload(dev, s)
+    qo = eb.Tensor.empty(dev, (rows, H, hd))
+    fill_k = oracle.randn((max_seq, Hkv, hd), 36)
+    fill_v = oracle.randn((max_seq, Hkv, hd), 37)
+    if dtype == "f16":
+        kc = eb.Tensor.empty(dev, fill_k.shape, eb.DType.F16)
+        vc = eb.Tensor.empty(dev, fill_v.shape, eb.DType.F16)
+        rec = eb.Recorder(dev)
+        eb.kv_write(rec, kc, upload(dev, fill_k), Hkv, max_seq, hd, max_seq, 0)
+        eb.kv_write(rec, vc, upload(dev, fill_v), Hkv, max_seq, hd, max_seq, 0)
+        rec.submit()
+    else:
+        kc, vc = upload(dev, fill_k), upload(dev, fill_v)
+    eb.launch_attn_prologue(
+        dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(), vt.data_ptr, vt.numel(),
+        rows, H, Hkv, hd, gqt.data_ptr if norm else 0, gkt.data_ptr if norm else 0,
+        gvt.data_ptr if norm else 0, eps, ct.data_ptr, st.data_ptr, ct.numel(), base,
+        qo.data_ptr, qo.numel(), kc.data_ptr, kc.numel(), vc.data_ptr, vc.numel(), max_seq,
+        eb.DType.F16 if dtype == "f16" else eb.DType.F32)
+    dev.synchronize()
+    qn = oracle.rmsnorm(q, gq, rows * H, hd, eps) if norm else q.ravel()
+    kn = oracle.rmsnorm(k, gk, rows * Hkv, hd, eps) if norm else k.ravel()
+    vn = oracle.rmsnorm(v, ones, rows * Hkv, hd, eps) if norm else v.ravel()
+    qr = oracle.rope(qn, c, s, rows, H, hd, base)
+    kr = oracle.rope(kn, c, s, rows, Hkv, hd, base)
+    want_k = oracle.kv_write(fill_k, kr, Hkv, rows, hd, base).reshape(max_seq, -1)
+    want_v = oracle.kv_write(fill_v, vn, Hkv, rows, hd, base).reshape(max_seq, -1)
+    got_q = qo.to_f32()
+    if dtype == "f16":
+        got_k = np.frombuffer(kc.read_bytes(), np.uint16).reshape(max_seq, -1)
+        got_v = np.frombuffer(vc.read_bytes(), np.uint16).reshape(max_seq, -1)
+        wk, wv = oracle.f16_bits(want_k).reshape(max_seq, -1), oracle.f16_bits(want_v).reshape(max_seq, -1)
+    else:
+        got_k = kc.to_f32().reshape(max_seq, -1)
+        got_v = vc.to_f32().reshape(max_seq, -1)
+        wk, wv = want_k, want_v
+    outside = np.r_[0:base, base + rows:max_seq]
+    np.testing.assert_array_equal(got_k[outside], wk[outside])
+    np.testing.assert_array_equal(got_v[outside], wv[outside])
+    new = slice(base, base + rows)
+    if not norm:
+        assert_bitwise(got_q, qr, "q_out")
+        np.testing.assert_array_equal(got_k[new], wk[new])
+        np.testing.assert_array_equal(got_v[new], wv[new])
+        return
+    assert rel_l2_f64(got_q, qr) < 1e-6
+    if dtype == "f16":  # halves of nearly equal f32 values: at most one unit apart
+        for g, w in ((got_k[new], wk[new]), (got_v[new], wv[new])):
+            d = np.abs(g.astype(np.int32) - w.astype(np.int32))
+            assert d.max() <= 1 and (d == 0).mean() > 0.95
+    else:
+        assert rel_l2_f64(got_k[new], wk[new]) < 1e-6
+        assert rel_l2_f64(got_v[new], wv[new]) < 1e-6
+
+
+def test_attention_prologue_refusals(dev):
+    """Shapes the prologue refuses before any launch: rows past max_seq, one table only,
+    tables too short, odd head_dim."""
+    H, Hkv, hd, rows, max_seq = 4, 2, 8, 3, 8
+    q = eb.Tensor.empty(dev, (rows, H, hd))
+    k = eb.Tensor.empty(dev, (rows, Hkv, hd))
+    kc = eb.Tensor.empty(dev, (max_seq, Hkv, hd))
+    ct = eb.Tensor.empty(dev, (max_seq, hd // 2))
+
+    def call(base=0, cos=ct.data_ptr, sin=ct.data_ptr, tn=ct.numel(), hd_=hd):
+        eb.launch_attn_prologue(dev.stream, q.data_ptr, q.numel(), k.data_ptr, k.numel(),
+                                k.data_ptr, k.numel(), rows, H, Hkv, hd_, 0, 0, 0, 1e-6, cos, sin,
+                                tn, base, q.data_ptr, q.numel(), kc.data_ptr, kc.numel(),
+                                kc.data_ptr, kc.numel(), max_seq, eb.DType.F32)
+    with pytest.raises(eb.ShapeMismatch):
+        call(base=6)
+    with pytest.raises(eb.EyebrowseError):
+        call(sin=0)
+    with pytest.raises(eb.ShapeMismatch):
+        call(base=4, tn=5 * hd // 2)
+    with pytest.raises(eb.ShapeMismatch):
+        call(hd_=7)
 
 
 # ---------------------------------------------------------------- Attention -------------
