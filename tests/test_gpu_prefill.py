@@ -8,7 +8,7 @@ import pytest
 
 import eyebrowse_amd as eb
 import oracle
-from tests._gpu import assert_bitwise, assert_close, note, prefill, upload
+from tests._gpu import F32_MAX_ABS, assert_bitwise, assert_close, note, prefill, upload
 
 pytestmark = pytest.mark.gpu
 
@@ -66,11 +66,6 @@ def test_shapes(dev, h, hkv, s, hd, scale):
     np.testing.assert_allclose(got[0], np.repeat(v[0], g, axis=0), rtol=tol, atol=0)
 
 
-def _sampled_rows(T):
-    rows = [(0, 40), (T // 2 - 20, 40), (T - 40, 40)]
-    return [(a, n) for a, n in rows if a >= 0]
-
-
 @pytest.mark.parametrize("name,H,Hkv,hd,T,scale", [
     ("qwen", 16, 8, 128, 512, None),
     ("qwen", 16, 8, 128, 2048, None),
@@ -80,8 +75,8 @@ def _sampled_rows(T):
 ])
 def test_baseline_prefill_configs(dev, name, H, Hkv, hd, T, scale):
     """BASELINE configs 3, 4 and 5 at full size: K/V written by kv_write into a max_seq = T
-    cache, prefill over the fresh K/V (attention.rs:78-115), compared with the oracle on
-    row samples at the start, middle and end of the sequence."""
+    cache, prefill over the fresh K/V (attention.rs:78-115), every row compared with the
+    oracle (16 threads)."""
     note(f"prefill {name} T={T}")
     sc = float(oracle.default_scale(hd)) if scale is None else scale
     q = oracle.randn((T, H, hd), 1)
@@ -98,9 +93,17 @@ def test_baseline_prefill_configs(dev, name, H, Hkv, hd, T, scale):
     rec.submit()
     got = ot.to_f32().reshape(T, H, hd)
     assert np.isfinite(got).all()
-    for row0, n in _sampled_rows(T):
-        want = oracle.attn_prefill(q, k, v, H, Hkv, T, hd, sc, rows=(row0, n), threads=16)
-        assert_close(got[row0:row0 + n], want[row0:row0 + n], what=f"{name} rows {row0}+{n}")
+    want = oracle.attn_prefill(q, k, v, H, Hkv, T, hd, sc, threads=16)
+    # Gemma's scale 1.0 on N(0,1) head_dim-256 rows gives scores of sigma 16 (|s| up to
+    # ~80) instead of about 1: the scores' absolute rounding error (2^-22 of each product)
+    # grows with them, so the max-abs part of the f32 bar doubles there (2e-4); rel-L2 and
+    # the north-star bar are the same for every config.
+    mx = 2e-4 if sc == 1.0 and hd == 256 else F32_MAX_ABS
+    assert_close(got, want, abs_=mx, what=f"{name} T={T} all rows")
+    # and every 64-row query block on its own (a block-indexing error in one block would be
+    # diluted in the whole-tensor rel-L2)
+    for b0 in range(0, T, 64):
+        assert_close(got[b0:b0 + 64], want[b0:b0 + 64], abs_=mx, what=f"{name} rows {b0}+64")
     # |o| <= max |v| row-wise (a convex combination of V rows), every row
     vmax = np.abs(v).max(axis=0).max()
     assert np.abs(got).max() <= vmax * (1 + 1e-5)
