@@ -22,7 +22,8 @@ from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_
                       launch_attn_prefill, launch_attn_prefill_chunk,
                       launch_attn_prefill_chunk_f16, launch_attn_prefill_chunk_ws,
                       launch_attn_prefill_ws, launch_kv_write, launch_kv_write_f16,
-                      launch_attn_prologue, launch_linear_f16w, launch_rmsnorm, launch_rope, linear_f16w,
+                      launch_attn_prologue, launch_attn_decode_step_noalloc,
+                      attn_decode_noalloc_max_floats, launch_linear_f16w, launch_rmsnorm, launch_rope, linear_f16w,
                       linear_f16w_multi, linear_workspace_floats, rmsnorm, rope)
 from .nn import Attention, KvCache, Linear, Rope
 
@@ -38,5 +39,6 @@ __all__ = [
     "launch_attn_prefill_ws", "attn_prefill_workspace_floats", "launch_kv_write",
     "launch_kv_write_f16", "launch_linear_f16w", "linear_f16w", "linear_f16w_multi",
     "linear_workspace_floats", "launch_rmsnorm",
-    "launch_rope", "launch_attn_prologue", "rmsnorm", "rope", "Attention", "KvCache", "Linear", "Rope",
+    "launch_rope", "launch_attn_prologue", "launch_attn_decode_step_noalloc",
+    "attn_decode_noalloc_max_floats", "rmsnorm", "rope", "Attention", "KvCache", "Linear", "Rope",
 ]

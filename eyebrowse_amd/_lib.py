@@ -144,6 +144,11 @@ SIGNATURES = {
                                  c_size, c_float]),
     "eb_launch_rope": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size, c_size,
                               c_size, c_size, c_size]),
+    "eb_attn_decode_noalloc_max_floats": (c_size, []),
+    "eb_launch_attn_decode_step_noalloc": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp,
+                                                  c_size, c_vp, c_size, c_vp, c_size, c_size,
+                                                  c_size, c_size, c_size, c_size, c_float,
+                                                  c_int]),
     "eb_launch_attn_prologue": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
                                        c_size, c_size, c_size, c_vp, c_vp, c_vp, c_float, c_vp,
                                        c_vp, c_size, c_size, c_vp, c_size, c_vp, c_size, c_vp,

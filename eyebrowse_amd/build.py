@@ -44,6 +44,7 @@ SOURCES = [
     "eb_prefill.hip",
     "eb_linear.hip",
     "eb_argmax.hip",
+    "eb_noalloc.hip",
 ]
 
 

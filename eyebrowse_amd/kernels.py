@@ -267,3 +267,20 @@ def launch_attn_prologue(stream: int, q: int, q_numel: int, k: int, k_numel: int
                                         hd, q_norm, k_norm, v_norm, eps, rope_cos, rope_sin,
                                         table_numel, base_pos, q_out, q_out_numel, kcache,
                                         kc_numel, vcache, vc_numel, max_seq, int(cache_dtype)))
+
+
+def attn_decode_noalloc_max_floats() -> int:
+    """Floats of split partials the no-allocation decode step's static scratch holds."""
+    return int(lib().eb_attn_decode_noalloc_max_floats())
+
+
+def launch_attn_decode_step_noalloc(stream: int, q: int, q_numel: int, knew: int, vnew: int,
+                                    new_numel: int, kc: int, kc_numel: int, vc: int,
+                                    vc_numel: int, o: int, o_numel: int, h: int, hkv: int,
+                                    pos: int, hd: int, max_seq: int, scale: float,
+                                    cu_count: int) -> None:
+    """eb_launch_attn_decode_step_noalloc: the fused decode step with its split partials in
+    the library's static device scratch (no allocation, no workspace argument)."""
+    check(lib().eb_launch_attn_decode_step_noalloc(stream, q, q_numel, knew, vnew, new_numel, kc,
+                                                   kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                                   pos, hd, max_seq, scale, cu_count))

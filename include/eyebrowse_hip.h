@@ -273,6 +273,23 @@ eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_nume
                                      float *o, size_t o_numel, size_t h, size_t hkv, size_t pos,
                                      size_t hd, size_t max_seq, float scale, float *workspace,
                                      size_t workspace_floats, int cu_count);
+/* eb_launch_attn_decode_step without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. The split-KV partials live in a
+ * static device array of eb_attn_decode_noalloc_max_floats() floats (4 MiB) that every GPU
+ * the library runs on holds until the process ends; the call allocates nothing. Shapes
+ * whose partials need more (eb_attn_decode_workspace_floats above the limit) are refused
+ * with EB_UNSUPPORTED_CONFIG. All calls on one GPU share its array: calls that overlap on
+ * one GPU race, so order them (one stream). Same kernels, same bits as
+ * eb_launch_attn_decode_step with a workspace. */
+size_t eb_attn_decode_noalloc_max_floats(void);
+eb_status eb_launch_attn_decode_step_noalloc(void *stream, const float *q, size_t q_numel,
+                                             const float *knew, const float *vnew,
+                                             size_t new_numel, float *kc, size_t kc_numel,
+                                             float *vc, size_t vc_numel, float *o,
+                                             size_t o_numel, size_t h, size_t hkv, size_t pos,
+                                             size_t hd, size_t max_seq, float scale,
+                                             int cu_count);
 eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel,
                             const float *weight, size_t w_numel, float *out,
                             size_t out_numel, size_t rows, size_t dim, float eps);
