@@ -213,11 +213,14 @@ class DecodeWorkload:
         graph of the n % per_graph remaining steps (captured once per length), all inside
         one pair of HIP events."""
         full, rem = divmod(n, self.per_graph)
+        st = self.dev.stream
         if rem and rem not in self.rem_graphs:
             self.rem_graphs[rem] = self.hip.capture(
-                self.dev.stream,
-                lambda: [self._step(self.caches[i % self.n_caches]) for i in range(rem)])
-        st = self.dev.stream
+                st, lambda: [self._step(self.caches[i % self.n_caches]) for i in range(rem)])
+            # a graph's first launch uploads it: keep that out of the timed region
+            self.hip.launch(self.rem_graphs[rem], st)
+            self.hip.ok(self.hip.l.hipStreamSynchronize(ctypes.c_void_p(st)),
+                        "hipStreamSynchronize")
 
         def body():
             for _ in range(full):
@@ -237,8 +240,9 @@ class PrefillWorkload:
     """Causal prefill over T tokens: K/V written by kv_write into a [T, Hkv, hd] cache,
     attention over the fresh K/V."""
 
-    def __init__(self, eb, dev, H, Hkv, hd, T, scale, seed=0, presplit=True):
+    def __init__(self, eb, dev, H, Hkv, hd, T, scale, seed=0, presplit=True, fast=False):
         self.eb, self.dev = eb, dev
+        self.fast = fast
         self.H, self.Hkv, self.hd, self.T, self.scale = H, Hkv, hd, T, scale
         self.flops = 2.0 * H * hd * T * (T + 1)
         rng = np.random.default_rng(seed)
@@ -248,7 +252,8 @@ class PrefillWorkload:
         self.o = eb.Tensor.empty(dev, (T, H, hd))
         # The pre-split workspace (head_dim 32..128, T >= 256): K/V split once per key, then
         # the attention kernel; both launches are inside every timed step.
-        self.ws_floats = eb.attn_prefill_workspace_floats(H, Hkv, hd, 0, T) if presplit else 0
+        self.ws_floats = (eb.attn_prefill_workspace_floats(H, Hkv, hd, 0, T)
+                          if presplit and not fast else 0)
         self.ws = eb.Tensor.empty(dev, (self.ws_floats,)) if self.ws_floats else None
 
     def launch(self):
@@ -256,7 +261,9 @@ class PrefillWorkload:
         args = (self.dev.stream, self.q.data_ptr, self.q.numel(), self.k.data_ptr,
                 self.k.numel(), self.v.data_ptr, self.v.numel(), self.o.data_ptr,
                 self.o.numel(), self.H, self.Hkv, self.T, self.hd, self.scale)
-        if self.ws is not None:
+        if self.fast:
+            e.launch_attn_prefill_fast(*args)
+        elif self.ws is not None:
             e.launch_attn_prefill_ws(*args, self.ws.data_ptr, self.ws_floats)
         else:
             e.launch_attn_prefill(*args)
@@ -406,7 +413,32 @@ def prefill_extras(eb, hip, dev, sc128) -> dict:
             "frac_f16_mfma_peak_of_mfma_work": round(f16_work / F16_MFMA_PEAK_TFLOPS, 4)}
         del p
         dev.synchronize()
+    out.update(fast_prefill_extras(eb, hip, dev, sc128))
     out.update(chunk_extras(eb, hip, dev))
+    return out
+
+
+def fast_prefill_extras(eb, hip, dev, sc128) -> dict:
+    """The opt-in single-product f16 prefill (eb_launch_attn_prefill_fast: q, K, V, P rounded
+    to f16 once, one f16 MFMA per product) on the BASELINE prefill configs it accepts (scale
+    1/sqrt(hd)); TFLOP/s of the same algorithmic FLOPs, against the f16 peak."""
+    out = {}
+    for name, H, Hkv, hd, T in (("qwen_T512", 16, 8, 128, 512), ("qwen_T2048", 16, 8, 128, 2048),
+                                ("qwen_T4096", 16, 8, 128, 4096),
+                                ("mistral_T4096", 32, 8, 128, 4096)):
+        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc128, fast=True)
+        for _ in range(3):
+            p.launch()
+        reps = 20 if T >= 2048 else 100
+        t = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+        tf_s = p.flops / (t * 1e-3) / 1e12
+        out[f"prefill_f16fast_{name}"] = {
+            "gflop": round(p.flops / 1e9, 3), "ms": round(t, 4), "TFLOPs": round(tf_s, 2),
+            "mfma": "v_mfma_f32_32x32x16_f16, one product per product (f16 q, K, V, P)",
+            "tolerance": "rel-L2 <= 1e-3, max-abs <= 2e-3 vs the f32 oracle (measured ~4e-4)",
+            "frac_f16_mfma_peak": round(tf_s / F16_MFMA_PEAK_TFLOPS, 4)}
+        del p
+        dev.synchronize()
     return out
 
 
@@ -740,9 +772,9 @@ def trace_workload(eb, hip, dev, sc128, name: str) -> None:
         w.run_exact(200)
         dev.synchronize()
         w.close()
-    elif name in prefill:
-        H, Hkv, hd, T, sc = prefill[name]
-        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc)
+    elif name in prefill or name.replace("f16fast_", "") in prefill:
+        H, Hkv, hd, T, sc = prefill[name.replace("f16fast_", "")]
+        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc, fast="f16fast_" in name)
         for _ in range(23):
             p.launch()
         dev.synchronize()
@@ -770,10 +802,33 @@ def trace_workload(eb, hip, dev, sc128, name: str) -> None:
     print(json.dumps({"trace_workload": name, "done": True}), flush=True)
 
 
-def prefill_roofline(eb, hip, dev, sc128, reps: int = 20) -> dict:
+def prefill_roofline(eb, hip, dev, sc128, reps: int = 20, fast: bool = False) -> dict:
     """The prefill half of the metric on the same config as the headline (BASELINE
-    configs[3], Mistral-7B T=4096): the pre-split pass plus the attention kernel, HIP
-    events around `reps` back-to-back launches."""
+    configs[3], Mistral-7B T=4096): the pre-split pass plus the attention kernel (f32-accurate
+    default), or the opt-in single-product f16 mode (fast), HIP events around `reps`
+    back-to-back launches."""
+    if fast:
+        p = PrefillWorkload(eb, dev, 32, 8, 128, 4096, sc128, fast=True)
+        for _ in range(3):
+            p.launch()
+        ms = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+        tf = p.flops / (ms * 1e-3) / 1e12
+        del p
+        dev.synchronize()
+        return {
+            "bound": "mfma",
+            "config": "mistral-7b-shaped causal prefill, T=4096, 32 q / 8 KV heads, head_dim "
+                      "128, f32 q/k/v (BASELINE configs[3]), opt-in f16 mode",
+            "kernel": "prefill_kernel<128,4,1,1,false,false,false,true>",
+            "mfma": "v_mfma_f32_32x32x16_f16, one product per product: q, K, V, P rounded to "
+                    "f16 once, f32 softmax and accumulation",
+            "tolerance": "rel-L2 <= 1e-3 and max-abs <= 2e-3 vs the f32 oracle (measured "
+                         "about 4e-4 rel-L2)",
+            "achieved": round(tf, 2), "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
+            "algorithmic_flops_per_launch": p_flops(32, 128, 4096),
+            "avg_launch_ms": round(ms, 5),
+        }
     p = PrefillWorkload(eb, dev, 32, 8, 128, 4096, sc128)
     for _ in range(3):
         p.launch()
@@ -892,6 +947,8 @@ def main():
           file=sys.stderr, flush=True)
     pf = prefill_roofline(eb, hip, dev, sc128)
     print(f"[bench] prefill {pf['achieved']} TFLOP/s", file=sys.stderr, flush=True)
+    pff = prefill_roofline(eb, hip, dev, sc128, fast=True)
+    print(f"[bench] prefill f16 mode {pff['achieved']} TFLOP/s", file=sys.stderr, flush=True)
 
     extra = {}
     if args.only == "all":
@@ -932,6 +989,7 @@ def main():
             "algorithmic_bytes_per_launch": kv_bytes, "avg_launch_ms": round(ms_step, 6),
         },
         "roofline_prefill": pf,
+        "roofline_prefill_f16": pff,
         "extra": extra,
     }
     if not args.no_cpu:

@@ -15,7 +15,8 @@ from .gpu import (DType, Device, DeviceUnavailable, EyebrowseError, Graph, LoadE
                   OutOfMemory, Recorder, ShapeMismatch, Tensor, UnsupportedConfig)
 from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_step,
                       attn_decode_step_window, attn_decode_window, attn_decode_workspace_floats,
-                      attn_prefill, attn_prefill_chunk, attn_prefill_workspace_floats,
+                      attn_prefill, attn_prefill_chunk, attn_prefill_fast,
+                      attn_prefill_workspace_floats, launch_attn_prefill_fast,
                       kv_write, launch_argmax,
                       launch_attn_decode, launch_attn_decode_f16, launch_attn_decode_step,
                       launch_attn_decode_step_f16, launch_attn_decode_window,
@@ -33,6 +34,7 @@ __all__ = [
     "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
     "attn_decode_step", "attn_decode_step_window", "attn_decode_window",
     "attn_decode_workspace_floats", "attn_prefill", "attn_prefill_chunk", "kv_write",
+    "attn_prefill_fast", "launch_attn_prefill_fast",
     "launch_attn_decode", "launch_attn_decode_f16", "launch_attn_decode_step",
     "launch_attn_decode_step_f16", "launch_attn_decode_window", "launch_attn_prefill",
     "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_attn_prefill_chunk_ws",

@@ -71,6 +71,10 @@ SIGNATURES = {
     "eb_recorder_release": (None, [c_vp]),
     "eb_attn_prefill": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size,
                                c_float]),
+    "eb_attn_prefill_fast": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size,
+                                    c_size, c_float]),
+    "eb_launch_attn_prefill_fast": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
+                                           c_size, c_size, c_size, c_size, c_size, c_float]),
     "eb_attn_decode": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size,
                               c_size, c_float]),
     "eb_attn_decode_step": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size,

@@ -7,9 +7,10 @@
 // (crates/eyebrowse-nn/src/attention.rs:149-183).
 //
 // Pass 1, grid (Hkv * nsub) x nsplit, 256 threads per workgroup. Workgroup (col, split)
-// reduces a 1/nsplit share of the keys for KV head col/nsub and the G query heads that
+// reduces a 1/nsplit share of the keys for KV head col % Hkv and the G query heads that
 // share it (GQA: every K/V row is read once for all of them):
-//  - a key row of HD floats is spread over LPK = HD/DPL lanes (DPL = 16 dims per lane),
+//  - a key row of HD floats is spread over LPK = HD/DPL lanes (DPL = 16 dims per lane; 8 for
+//    f32 head_dim 128 with 4 query heads per workgroup),
 //    so a wave covers KPW = 64/LPK keys per step; the keys are dealt to the splits in
 //    blocks of KPW rows (split s owns blocks s, s + nsplit, ...), so that all workgroups
 //    together stream one contiguous stretch of the cache at a time;
@@ -67,11 +68,14 @@ constexpr float kSlack = 8.0f;  // log2-units a score may exceed the reference m
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int HD, int G, int UDEF = 1>
+template <int HD, int G, int UDEF = 1, int DPLDEF = 16>
 struct DecodeShape {
-    static constexpr int DPL = HD >= 16 ? 16 : HD;  // dims per lane
-    static constexpr int LPK = HD / DPL;            // lanes per key row
-    static constexpr int KPW = 64 / LPK;            // keys per wave step
+    static constexpr int DPL = HD >= DPLDEF ? DPLDEF : HD;  // dims per lane
+    static constexpr int LPK = HD / DPL;            // lanes holding a key row's dims
+    // Lanes per row group: LPK rounded up to a power of two (head dims 48, 80, 96, ...: the
+    // extra lanes hold zeros), so that a row's lanes meet by DPP and lane swaps.
+    static constexpr int LPK2 = LPK <= 1 ? 1 : LPK <= 2 ? 2 : LPK <= 4 ? 4 : LPK <= 8 ? 8 : 16;
+    static constexpr int KPW = 64 / LPK2;           // keys per wave step
     static constexpr int NV4 = DPL / 4;             // 16-byte loads per lane per row
     // Wave steps per iteration: each of the two register buffers holds U*NV4*2 16-byte
     // loads per lane (half that over f16 caches). One f32 step per buffer keeps everything
@@ -82,23 +86,24 @@ struct DecodeShape {
     // that the waves' rows start in different banks), plus m and l per head and wave.
     static constexpr int WS = G * HD + 4;
     static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)kWaves * WS + 2 * G * kWaves);
-    static_assert(DPL % 4 == 0 && LPK <= 16, "head_dim must be a multiple of 4, at most 256");
+    static_assert(DPL % 4 == 0 && HD % DPL == 0 && LPK <= 16,
+                  "head_dim: 4, 8, or a multiple of 16 up to 256");
 };
 
-// Byte offset (within a row) of 16-byte load number j of dim slice `ls`.
-template <int HD>
+// Byte offset (within a row) of 16-byte load number j of dim slice `ls` (LPK lanes per row).
+template <int LPK>
 __device__ __forceinline__ int dim_byte(int j, int ls) {
-    return (j * DecodeShape<HD, 1>::LPK + ls) * 16;
+    return (j * LPK + ls) * 16;
 }
 
 // First dim of the lane's f32x4 unit i: a 16-byte load holds 4 dims of an f32 cache row
 // and 8 of an f16 one, so unit i of an f16 lane is half of load i/2.
-template <int HD, bool H16>
+template <int LPK, bool H16>
 __device__ __forceinline__ int dim_of(int i, int ls) {
     if constexpr (H16)
-        return dim_byte<HD>(i / 2, ls) / 2 + (i % 2) * 4;
+        return dim_byte<LPK>(i / 2, ls) / 2 + (i % 2) * 4;
     else
-        return dim_byte<HD>(i, ls) / 4;
+        return dim_byte<LPK>(i, ls) / 4;
 }
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -164,24 +169,28 @@ struct DecodeArgs {
 
 // RMSNorm of one head held in a lane group's units (attention.rs:62-73 via
 // kernels/src/rmsnorm.rs:6-38): y = x * (1/sqrt(sum x^2 / HD + eps)) * w.
-template <int HD, bool H16, int NV4, int LPK>
+// LPK lanes hold the row's dims, LPK2 (a power of two) lanes form its group; lanes
+// ls >= LPK hold zeros and keep them.
+template <int HD, bool H16, int NV4, int LPK, int LPK2>
 __device__ __forceinline__ void norm_units(f32x4 (&u)[NV4], const float *__restrict__ w,
                                            float eps, int ls) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV4; ++i) ss += (u[i].x * u[i].x + u[i].y * u[i].y) +
                                        (u[i].z * u[i].z + u[i].w * u[i].w);
-    ss = eb::group_sum<LPK>(ss);
+    ss = eb::group_sum<LPK2>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+    if (LPK == LPK2 || ls < LPK) {
 #pragma unroll
-    for (int i = 0; i < NV4; ++i)
-        u[i] = u[i] * inv * *reinterpret_cast<const f32x4 *>(w + dim_of<HD, H16>(i, ls));
+        for (int i = 0; i < NV4; ++i)
+            u[i] = u[i] * inv * *reinterpret_cast<const f32x4 *>(w + dim_of<LPK, H16>(i, ls));
+    }
 }
 
 // RoPE of one head (kernels/src/rope.rs:6-32): dims p and p + HD/2 rotate by the table
 // row's angle p. In the lane layout, unit i + NV4/2 holds the partners of unit i's dims
 // (both cache layouts), so each lane rotates its own units.
-template <int HD, bool H16, int NV4>
+template <int HD, bool H16, int NV4, int LPK>
 __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restrict__ cs,
                                            const float *__restrict__ sn, int ls) {
     if constexpr (NV4 == 1) {  // HD 4: pairs (0, 2) and (1, 3) inside the unit
@@ -192,7 +201,7 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
     } else {
 #pragma unroll
         for (int i = 0; i < NV4 / 2; ++i) {
-            const int d = dim_of<HD, H16>(i, ls);
+            const int d = dim_of<LPK, H16>(i, ls);
             const f32x4 c = *reinterpret_cast<const f32x4 *>(cs + d);
             const f32x4 sv = *reinterpret_cast<const f32x4 *>(sn + d);
             const f32x4 x1 = u[i], x2 = u[i + NV4 / 2];
@@ -206,8 +215,15 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
 // Two wave steps per iteration for f32 head_dim 256 (4 rows per wave step there): measured
 // +4 % at 16k keys; head_dim 128 measured slower with two (its query heads per workgroup
 // then fill the register file).
+// f32 head_dim 128 with 4 query heads per workgroup (GQA 4, Mistral) runs 8 dims per lane
+// (a row over 16 lanes, 4 rows per wave step): at 16 dims per lane the q fragments and
+// accumulators of 4 heads leave the two load buffers no registers (256 VGPRs and spills);
+// at 8 they take half (160 VGPRs, none spilled). Measured at 32k keys: 5.48 -> 5.77 TB/s;
+// more wave steps per iteration on the freed registers measured slower (2: 5.40, 3: 5.35,
+// 4: 5.26 TB/s), and so did 8 dims per lane for 2 heads per workgroup.
 template <int HD, int G, bool H16>
-using DecodeShapeOf = DecodeShape<HD, G, H16 ? EB_DECODE_U16 : (HD == 256 ? 2 : 1)>;
+using DecodeShapeOf = DecodeShape<HD, G, H16 ? EB_DECODE_U16 : (HD == 256 ? 2 : 1),
+                                  (!H16 && HD == 128 && G == 4) ? 8 : 16>;
 
 template <int HD, int G, bool H16>
 __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G <= 2 ? 2 : 1))) void decode_kernel(DecodeArgs a) {
@@ -219,13 +235,18 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     static_assert(!H16 || NV4 % 2 == 0, "f16 caches need head_dim >= 8");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int nsub = a.g / G;
+    // Column col = sub * hkv + kvh: workgroup ids that differ by a multiple of hkv share a
+    // KV head, so with hkv a multiple of the 8 XCDs (ids dealt round robin) every column and
+    // split of one KV head lands on the same XCD, and the head subgroups that read the same
+    // rows share that XCD's L2.
     const int col = blockIdx.x;
-    const int kvh = col / nsub;
-    const int head0 = kvh * a.g + (col % nsub) * G;
+    const int kvh = col % a.hkv;
+    const int sub = col / a.hkv;
+    const int head0 = kvh * a.g + sub * G;
     const int split = blockIdx.y;
-    const int kg = lane / S::LPK;
-    const int ls = lane % S::LPK;
+    const int kg = lane / S::LPK2;
+    const int ls = lane % S::LPK2;
+    const bool dims_on = S::LPK == S::LPK2 || ls < S::LPK;  // lane holds dims of its row
     const int pos = a.keys - 1;
     // Keys are dealt to the splits in blocks of KPW rows (one wave step): split s owns
     // blocks s, s + nsplit, s + 2*nsplit, ... At any moment the workgroups of all splits
@@ -242,7 +263,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     // New-token write: one workgroup per KV head copies the row into the cache. No
     // workgroup reads cache row `pos` in this launch. (With the prologue the row is
     // written after its norm and RoPE, from the tail fold below.)
-    if (tail_new && (col % nsub) == 0 && !a.prologue) {
+    if (tail_new && sub == 0 && !a.prologue) {
         const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
         for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
             const f32x4 kx = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
@@ -264,16 +285,17 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
         for (int i = 0; i < NV4; ++i)
-            qr[gi][i] = *reinterpret_cast<const f32x4 *>(a.q + (size_t)(head0 + gi) * HD +
-                                                         dim_of<HD, H16>(i, ls));
+            qr[gi][i] = dims_on ? *reinterpret_cast<const f32x4 *>(
+                                      a.q + (size_t)(head0 + gi) * HD + dim_of<S::LPK, H16>(i, ls))
+                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     if (a.prologue) {
         const float *cs = a.rcos ? a.rcos + (size_t)a.rope_row * (HD / 2) : nullptr;
         const float *sn = a.rsin ? a.rsin + (size_t)a.rope_row * (HD / 2) : nullptr;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
-            if (a.qn_w) norm_units<HD, H16, NV4, S::LPK>(qr[gi], a.qn_w, a.eps, ls);
-            if (cs) rope_units<HD, H16, NV4>(qr[gi], cs, sn, ls);
+            if (a.qn_w) norm_units<HD, H16, NV4, S::LPK, S::LPK2>(qr[gi], a.qn_w, a.eps, ls);
+            if (cs && dims_on) rope_units<HD, H16, NV4, S::LPK>(qr[gi], cs, sn, ls);
         }
     }
 
@@ -298,7 +320,8 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         rowof[u] = ((u * kWaves + wave) * a.nsplit + split) * S::KPW + kg;  // minus it0
-        voff[u] = rowof[u] * row_bytes + dim_byte<HD>(0, ls);
+        // (lanes without dims read past every range check: zeros, no memory access)
+        voff[u] = dims_on ? rowof[u] * row_bytes + dim_byte<S::LPK>(0, ls) : 0x7FFF0000;
     }
     const char *kbase = static_cast<const char *>(a.kc) + (size_t)kvh * HD * EB;
     const char *vbase = static_cast<const char *>(a.vc) + (size_t)kvh * HD * EB;
@@ -336,7 +359,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 #pragma unroll
                 for (int i = 1; i < NV4; ++i) t += qr[gi][i] * unit_f32<H16>(kv[u], i);
                 float sv = (t.x + t.y) + (t.z + t.w);
-                sv = eb::group_sum<S::LPK>(sv);
+                sv = eb::group_sum<S::LPK2>(sv);
                 sc[gi][u] = (r0 + rowof[u] < ce) ? sv * a.scale_log2 : -INFINITY;
             }
         // Lazy rescale: a head's reference max m moves only when a score exceeds it by more
@@ -414,22 +437,25 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         f32x4 kn[NV4], vn[NV4];
 #pragma unroll
         for (int i = 0; i < NV4; ++i) {
-            kn[i] = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD +
-                                                     dim_of<HD, H16>(i, ls));
-            vn[i] = *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD +
-                                                     dim_of<HD, H16>(i, ls));
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            kn[i] = dims_on ? *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD +
+                                                               dim_of<S::LPK, H16>(i, ls))
+                            : z;
+            vn[i] = dims_on ? *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD +
+                                                               dim_of<S::LPK, H16>(i, ls))
+                            : z;
         }
         if (a.prologue) {
-            if (a.kn_w) norm_units<HD, H16, NV4, S::LPK>(kn, a.kn_w, a.eps, ls);
-            if (a.vn_w) norm_units<HD, H16, NV4, S::LPK>(vn, a.vn_w, a.eps, ls);
-            if (a.rcos)
-                rope_units<HD, H16, NV4>(kn, a.rcos + (size_t)a.rope_row * (HD / 2),
+            if (a.kn_w) norm_units<HD, H16, NV4, S::LPK, S::LPK2>(kn, a.kn_w, a.eps, ls);
+            if (a.vn_w) norm_units<HD, H16, NV4, S::LPK, S::LPK2>(vn, a.vn_w, a.eps, ls);
+            if (a.rcos && dims_on)
+                rope_units<HD, H16, NV4, S::LPK>(kn, a.rcos + (size_t)a.rope_row * (HD / 2),
                                          a.rsin + (size_t)a.rope_row * (HD / 2), ls);
-            if ((col % nsub) == 0 && kg == 0) {  // the new cache row, one lane group
+            if (sub == 0 && kg == 0 && dims_on) {  // the new cache row, one lane group
                 const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
 #pragma unroll
                 for (int i = 0; i < NV4; ++i) {
-                    const int d = dim_of<HD, H16>(i, ls);
+                    const int d = dim_of<S::LPK, H16>(i, ls);
                     if constexpr (H16) {
                         *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.kc_w) + dst + d) =
                             __builtin_convertvector(kn[i], f16x4);
@@ -454,7 +480,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             f32x4 t = qr[gi][0] * kn[0];
 #pragma unroll
             for (int i = 1; i < NV4; ++i) t += qr[gi][i] * kn[i];
-            const float s = eb::group_sum<S::LPK>((t.x + t.y) + (t.z + t.w)) * a.scale_log2;
+            const float s = eb::group_sum<S::LPK2>((t.x + t.y) + (t.z + t.w)) * a.scale_log2;
             if (kg == 0) {
                 const float mnew = fmaxf(m[gi], s);
                 const float corr = eb::fast_exp2(m[gi] - mnew);
@@ -482,9 +508,9 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     float *s_l = s_m + G * kWaves;      // [G][kWaves]
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-        const float mw = eb::class_reduce<S::LPK, true>(m[gi]);
+        const float mw = eb::class_reduce<S::LPK2, true>(m[gi]);
         const float w = eb::fast_exp2(m[gi] - (mw == -INFINITY ? 0.0f : mw));
-        const float lw = eb::class_reduce<S::LPK, false>(l[gi] * w);
+        const float lw = eb::class_reduce<S::LPK2, false>(l[gi] * w);
         if (lane == 0) {
             s_m[gi * kWaves + wave] = mw;
             s_l[gi * kWaves + wave] = lw;
@@ -507,19 +533,20 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             f32x4 out;
 #pragma unroll
             for (int k = 0; k < 4; ++k)  // even rows: v2[k] summed; odd rows: v2[k + 4]
-                out[k] = eb::row_class_reduce<S::LPK, false>(eb::swap_sum16(v2[k], v2[k + 4]));
+                out[k] = eb::row_class_reduce<S::LPK2, false>(eb::swap_sum16(v2[k], v2[k + 4]));
             if ((lane & 15) < S::LPK)
-                *reinterpret_cast<f32x4 *>(dst + dim_of<HD, H16>((lane >> 4) & 3, ls)) = out;
+                *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, H16>((lane >> 4) & 3, ls)) = out;
         } else {
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
                 const f32x4 t = acc[gi][i] * w;
                 f32x4 out;
-                out.x = eb::class_reduce<S::LPK, false>(t.x);
-                out.y = eb::class_reduce<S::LPK, false>(t.y);
-                out.z = eb::class_reduce<S::LPK, false>(t.z);
-                out.w = eb::class_reduce<S::LPK, false>(t.w);
-                if (kg == 0) *reinterpret_cast<f32x4 *>(dst + dim_of<HD, H16>(i, ls)) = out;
+                out.x = eb::class_reduce<S::LPK2, false>(t.x);
+                out.y = eb::class_reduce<S::LPK2, false>(t.y);
+                out.z = eb::class_reduce<S::LPK2, false>(t.z);
+                out.w = eb::class_reduce<S::LPK2, false>(t.w);
+                if (kg == 0 && dims_on)
+                    *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, H16>(i, ls)) = out;
             }
         }
     }
@@ -550,17 +577,21 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 }
 
 // Log-sum-exp merge of the split partials (a second launch, so the partials written by
-// every XCD are visible without in-kernel fences). Grid (h, HD / DS): a workgroup owns DS
-// dims of one head; thread (grp, d) of GROUPS = 256/DS groups folds splits grp,
+// every XCD are visible without in-kernel fences). Grid (h, ceil(HD / DS)): a workgroup owns
+// DS dims of one head (dims past HD in the last block are read as anything and not stored); thread (grp, d) of GROUPS = 256/DS groups folds splits grp,
 // grp + GROUPS, ... into a running (M, L, A), issuing a batch of kBatch splits' loads
 // before using any, so up to GROUPS*kBatch splits merge in one memory round trip. The
 // groups then combine through LDS: o[h][d] = A / L.
+constexpr int merge_dims_per_block(int hd) {
+    return hd >= 64 ? 64 : hd >= 32 ? 32 : hd >= 16 ? 16 : hd;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(const float *__restrict__ part_acc,
                                                                 const float *__restrict__ part_ml,
                                                                 float *__restrict__ o, int h,
                                                                 int nsplit) {
-    constexpr int DS = HD < 64 ? HD : 64;
+    constexpr int DS = merge_dims_per_block(HD);
     constexpr int GROUPS = kThreads / DS;
     constexpr int kBatch = 16;
     __shared__ float s_m[GROUPS][DS];
@@ -626,7 +657,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(const float *__r
             Lt += w * s_l[g2][dl];
             At += w * s_a[g2][dl];
         }
-        o[(size_t)hh * HD + d] = At / Lt;
+        if (HD % DS == 0 || d < HD) o[(size_t)hh * HD + d] = At / Lt;
     }
 }
 
@@ -638,15 +669,13 @@ struct DecodePlan {
 
 template <int G, bool H16>
 int keys_per_iter_g(size_t hd) {
+#define EB_KPI(D) \
+    case D: return DecodeShapeOf<D, G, H16>::KEYS_PER_ITER;
     switch (hd) {
-        case 4: return DecodeShapeOf<4, G, H16>::KEYS_PER_ITER;
-        case 8: return DecodeShapeOf<8, G, H16>::KEYS_PER_ITER;
-        case 16: return DecodeShapeOf<16, G, H16>::KEYS_PER_ITER;
-        case 32: return DecodeShapeOf<32, G, H16>::KEYS_PER_ITER;
-        case 64: return DecodeShapeOf<64, G, H16>::KEYS_PER_ITER;
-        case 128: return DecodeShapeOf<128, G, H16>::KEYS_PER_ITER;
+        EB_HEAD_DIMS(EB_KPI)
         default: return DecodeShapeOf<256, G, H16>::KEYS_PER_ITER;
     }
+#undef EB_KPI
 }
 
 int keys_per_iter(size_t hd, int G, bool h16) {
@@ -724,8 +753,8 @@ hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     }
     if (e != hipSuccess) return e;
     if (p.nsplit > 1) {
-        constexpr int DS = HD < 64 ? HD : 64;
-        dim3 grid((unsigned)a.h, (unsigned)(HD / DS));
+        constexpr int DS = merge_dims_per_block(HD);
+        dim3 grid((unsigned)a.h, (unsigned)((HD + DS - 1) / DS));
         decode_merge_kernel<HD><<<grid, kThreads, 0, st>>>(a.part_acc, a.part_ml, a.o, a.h,
                                                           p.nsplit);
     }
@@ -734,17 +763,19 @@ hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
 
 template <bool H16>
 hipError_t launch_elem(hipStream_t st, size_t hd, const DecodePlan &p, const DecodeArgs &a) {
-    switch (hd) {
-        case 8: return launch_hd<8, H16>(st, p, a);
-        case 16: return launch_hd<16, H16>(st, p, a);
-        case 32: return launch_hd<32, H16>(st, p, a);
-        case 64: return launch_hd<64, H16>(st, p, a);
-        case 128: return launch_hd<128, H16>(st, p, a);
-        case 256: return launch_hd<256, H16>(st, p, a);
-        default:
-            if constexpr (!H16) return launch_hd<4, false>(st, p, a);  // hd 4 (f32 only)
-            return hipErrorInvalidValue;
+    if (hd == 4) {
+        if constexpr (!H16) return launch_hd<4, false>(st, p, a);  // f32 caches only
+        return hipErrorInvalidValue;
     }
+#define EB_LAUNCH_HD(D) \
+    case D:             \
+        if constexpr (D != 4) return launch_hd<D, H16>(st, p, a);
+    switch (hd) {
+        EB_HEAD_DIMS(EB_LAUNCH_HD)
+        default: return hipErrorInvalidValue;
+    }
+#undef EB_LAUNCH_HD
+    return hipErrorInvalidValue;
 }
 
 }  // namespace

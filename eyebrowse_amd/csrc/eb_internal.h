@@ -33,8 +33,13 @@ eb_status check_launch(const char *kernel);
 eb_status check_ptr(const void *p, const char *name);
 eb_status check_numel(size_t have, size_t need, const char *name);
 eb_status check_heads(size_t h, size_t hkv);
-// Head dims the attention kernels are instantiated for.
+// Head dims the attention kernels serve: 4, 8 and every multiple of 16 up to 256. Decode is
+// instantiated for each (X-macro below); prefill runs the next power-of-two instantiation
+// with the extra dims read as zeros and never stored.
 bool attn_head_dim_supported(size_t hd);
+#define EB_HEAD_DIMS(X) \
+    X(4) X(8) X(16) X(32) X(48) X(64) X(80) X(96) X(112) X(128) X(144) X(160) X(176) X(192) \
+    X(208) X(224) X(240) X(256)
 // Largest element count a 32-bit-indexed kernel may address.
 constexpr size_t kMaxIndex = (size_t)1 << 31;
 
@@ -56,6 +61,12 @@ size_t prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t rows, si
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale, float *ws = nullptr, size_t ws_floats = 0);
+// The single-product f16 prefill (opt-in): q, K, V and P rounded to f16 once, one f16 MFMA
+// per product, f32 softmax and accumulation. Prompts from position 0, f32 q/k/v, head dims
+// 32..256 (multiples of 16); no workspace.
+eb_status launch_attn_prefill_fast(hipStream_t st, const float *q, const float *k, const float *v,
+                                   float *o, size_t h, size_t hkv, size_t s, size_t hd,
+                                   float scale);
 // Chunked causal prefill: q rows at positions pos0..pos0+rows-1 attend cache keys
 // max(0, p - window + 1)..p (window 0: 0..p); kc/vc are the cache bases.
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,

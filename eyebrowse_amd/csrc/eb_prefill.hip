@@ -142,7 +142,8 @@ template <class C, bool H16>
 __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
                                                   const void *__restrict__ v,
                                                   f32x4 (&rk)[C::NLD], f32x4 (&rv)[C::NLD],
-                                                  int kb, int T, int Hkv, int kvh, int tid) {
+                                                  int kb, int T, int Hkv, int kvh, int tid,
+                                                  int hdr) {
     constexpr int HD = C::HD_;
 #pragma unroll
     for (int r = 0; r < C::NLD; ++r) {
@@ -150,7 +151,9 @@ __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
         const int row = idx / (HD / 4);
         const int c4 = idx % (HD / 4);
         const int key = kb + row;
-        const size_t off = ((size_t)min(key, T - 1) * Hkv + kvh) * HD + c4 * 4;
+        // rows of hdr <= HD dims (head dims padded up to the instantiation read as zeros)
+        const bool in = key < T && (HD == 4 || c4 * 4 < hdr);
+        const size_t off = ((size_t)min(key, T - 1) * Hkv + kvh) * hdr + min(c4 * 4, hdr - 4);
         f32x4 kx, vx;
         if constexpr (H16) {
             kx = __builtin_convertvector(
@@ -162,8 +165,8 @@ __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
             vx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(v) + off);
         }
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        rk[r] = key < T ? kx : z;
-        rv[r] = key < T ? vx : z;
+        rk[r] = in ? kx : z;
+        rv[r] = in ? vx : z;
     }
 }
 
@@ -212,7 +215,9 @@ __device__ __forceinline__ void split_f16(f32x4 x, int e, f16x4 &hi, f16x4 &lo) 
 // Write the staged rows into LDS buffer `buf`: K rows [STEP_KEYS][KS], then V rows
 // [STEP_KEYS][HD], then (SQK) the K rows' exponents [STEP_KEYS]. With SQK a K row holds
 // its HD halves of hi, then HD halves of lo (the same KS floats).
-template <class C>
+// FAST: rows are rounded to f16 as they are (no exponent, no lo halves, no exponent
+// arrays); the single-product mode below reads only the hi halves.
+template <class C, bool FAST = false>
 __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk)[C::NLD],
                                                    const f32x4 (&rv)[C::NLD], int buf,
                                                    int tid) {
@@ -229,21 +234,33 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
         if constexpr (C::SQK) {
             // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32)
             const f32x4 x = rk[r];
-            const float m4 = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
-            const float mx = group_max<HD / 4>(m4);
-            const int e = split_exponent(mx);
-            f16x4 hi, lo;
-            split_f16(x, e, hi, lo);
             _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * C::KS);
-            *reinterpret_cast<f16x4 *>(kr + c4 * 4) = hi;
-            *reinterpret_cast<f16x4 *>(kr + HD + c4 * 4) = lo;
-            if (c4 == 0) Eb[row] = e;
+            if constexpr (FAST) {
+                *reinterpret_cast<f16x4 *>(kr + c4 * 4) = __builtin_convertvector(x, f16x4);
+            } else {
+                const float m4 =
+                    fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+                const float mx = group_max<HD / 4>(m4);
+                const int e = split_exponent(mx);
+                f16x4 hi, lo;
+                split_f16(x, e, hi, lo);
+                *reinterpret_cast<f16x4 *>(kr + c4 * 4) = hi;
+                *reinterpret_cast<f16x4 *>(kr + HD + c4 * 4) = lo;
+                if (c4 == 0) Eb[row] = e;
+            }
             if constexpr (C::SPV) {
                 const f32x4 y = rv[r];
-                const float vm4 = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
-                const int ev = split_exponent(group_max<HD / 4>(vm4));
+                int ev = 0;
                 f16x4 vh, vl;
-                split_f16(y, ev, vh, vl);
+                if constexpr (FAST) {
+                    vh = __builtin_convertvector(y, f16x4);
+                    vl = vh;
+                } else {
+                    const float vm4 =
+                        fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+                    ev = split_exponent(group_max<HD / 4>(vm4));
+                    split_f16(y, ev, vh, vl);
+                }
                 // V^T row of dim d sits at p(d) = (d % NB) * 32 + d / NB (the MFMA reader
                 // then walks consecutive rows). Rows j and j + 1 (lanes i and i ^ HD/4) pair
                 // their halves: the even row's lane writes dims 0, 1 of its four, the odd
@@ -260,13 +277,13 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                         const int d = c4 * 4 + i;
                         const int pr = (d % C::NB) * 32 + d / C::NB;
                         vth16[pr * C::VROW + js] = vh[i];
-                        vtl16[pr * C::VROW + js] = vl[i];
+                        if constexpr (!FAST) vtl16[pr * C::VROW + js] = vl[i];
                     }
                 } else {
                 using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
                 const u32x2 ho = __builtin_bit_cast(u32x2, vh), lw = __builtin_bit_cast(u32x2, vl);
                 const u32x2 hp = {lane_xor_u<HD / 4>(ho.x), lane_xor_u<HD / 4>(ho.y)};
-                const u32x2 lp = {lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
+                const u32x2 lp = FAST ? lw : u32x2{lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
                 const f16x4 vh2 = __builtin_bit_cast(f16x4, hp), vl2 = __builtin_bit_cast(f16x4, lp);
                 const bool odd = row & 1;
                 // Keys are stored permuted within each 16: groups of four in the order
@@ -285,10 +302,11 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     const _Float16 le = odd ? vl2[i] : vl[i], lo2 = odd ? vl[i] : vl2[i];
                     using h2 = __attribute__((ext_vector_type(2))) _Float16;
                     vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
-                    vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
+                    if constexpr (!FAST)
+                        vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
                 }
                 }
-                if (c4 == 0) Ev[row] = ev;
+                if (!FAST && c4 == 0) Ev[row] = ev;
             } else {
                 *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
             }
@@ -357,7 +375,7 @@ template <int HD, bool H16>
 __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ k,
                                                        const void *__restrict__ v,
                                                        float *__restrict__ ps, int nkeys,
-                                                       int Hkv, int tlo, int nt) {
+                                                       int Hkv, int tlo, int nt, int hdr) {
     using C = PrefillCfg<HD, 4, 1, 1>;  // 256 threads, one 32-key tile per step
     static_assert(C::SPV, "pre-split needs the split V path");
     __shared__ float smem[C::BUF];
@@ -367,7 +385,7 @@ __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ 
     // (An image record's padding is left as it is: K rows are read within their HD floats,
     // V^T rows within their 32 keys, and the exponents where written.)
     f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C, H16>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid);
+    prefill_load_step<C, H16>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::PS_FLOATS);
@@ -413,13 +431,16 @@ __device__ __forceinline__ void wait_vm_all() {
 // H16: the K/V rows are IEEE half (an f16 KV cache), converted to f32 as they are staged.
 // PS: K/V come as pre-split records (ps: ps_nt records per KV head, record 0 = tile
 // ps_tlo) instead of k/v.
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
+// FAST (an opt-in mode, f32 K/V without pre-split records): q, K, V and P are rounded to
+// f16 once and each product is one f16 MFMA (instead of three on exact hi/lo splits); the
+// online softmax, its rescaling and the accumulation stay f32.
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS, bool FAST = false>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     const float *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
     int Hkv, int rows, int nkeys, int qbase, int window, float scale_log2, int nqb,
-    int ngroups, int ctiles, float *__restrict__ part_acc, float *__restrict__ part_ml) {
+    int ngroups, int ctiles, float *__restrict__ part_acc, float *__restrict__ part_ml, int hdr) {
     using C = PrefillCfg<HD, HPW, WPH, KSPLIT>;
     constexpr int QB = C::QB;
     constexpr int HALF = C::HALF;
@@ -478,7 +499,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     int eq = 0;
     if constexpr (C::SQK) {
         const bool qv = qi < rows;
-        const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * HD + 8 * hf;
+        const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * hdr + 8 * hf;
         f32x4 qa[NKS], qb[NKS];
         const float qs = qv ? scale_log2 : 0.0f;
         float mx = 0.0f;
@@ -488,8 +509,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             // product needs no multiply per score. Every lane loads (rows past the end
             // from the clamped row 0) and scales by qs, 0 past the end, so that the loads
             // issue back to back; such a lane's query column never reaches the output.
-            qa[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2) * qs;
-            qb[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) * qs;
+            // Dims past hdr (a head dim padded up to this instantiation) are zeros.
+            const bool kin = 16 * k2 < hdr;
+            const float *qk = qp + (kin ? 16 * k2 : 0);
+            qa[k2] = *reinterpret_cast<const f32x4 *>(qk) * (kin ? qs : 0.0f);
+            qb[k2] = *reinterpret_cast<const f32x4 *>(qk + 4) * (kin ? qs : 0.0f);
             const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
                                          fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
                                    fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
@@ -497,12 +521,19 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             mx = fmaxf(mx, m8);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));  // the other half of the row
-        eq = split_exponent(mx);
+        eq = FAST ? 0 : split_exponent(mx);
 #pragma unroll
         for (int k2 = 0; k2 < NKS; ++k2) {
             f16x4 h0, l0, h1, l1;
-            split_f16(qa[k2], eq, h0, l0);
-            split_f16(qb[k2], eq, h1, l1);
+            if constexpr (FAST) {
+                h0 = __builtin_convertvector(qa[k2], f16x4);
+                h1 = __builtin_convertvector(qb[k2], f16x4);
+                l0 = h0;
+                l1 = h1;
+            } else {
+                split_f16(qa[k2], eq, h0, l0);
+                split_f16(qb[k2], eq, h1, l1);
+            }
             qh[k2] = f16x8{h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
             ql[k2] = f16x8{l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
         }
@@ -536,7 +567,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     float l = 0.0f;
     // SPV: O^T is accumulated in units of 2^E (per query; both lane halves of a query hold
     // the same E).
-    int E = kZeroRowExp;
+    int E = FAST ? 0 : kZeroRowExp;
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
@@ -549,8 +580,8 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
         ps_store_step<C>(smem, rs, 0, tid);
     } else {
-        prefill_load_step<C, H16>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid);
-        prefill_store_step<C>(smem, rk, rv, 0, tid);
+        prefill_load_step<C, H16>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
+        prefill_store_step<C, FAST>(smem, rk, rv, 0, tid);
     }
     __syncthreads();
 
@@ -570,7 +601,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                             c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
         else
             prefill_load_step<C, H16>(k, v, rk, rv, (c_lo + (it + 1) * KSPLIT) * kTile, nkeys,
-                                      Hkv, kvh, tid);
+                                      Hkv, kvh, tid, hdr);
 
         if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
             const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
@@ -588,11 +619,18 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
                 for (int k2 = 0; k2 < NKS; ++k2) {
                     const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
-                    const f16x8 al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
                     sacc = mfma16(ah, qh[k2], sacc);
-                    sacc = mfma16(ah, ql[k2], sacc);
-                    sacc = mfma16(al, qh[k2], sacc);
+                    if constexpr (!FAST) {
+                        const f16x8 al =
+                            *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                        sacc = mfma16(ah, ql[k2], sacc);
+                        sacc = mfma16(al, qh[k2], sacc);
+                    }
                 }
+                if constexpr (FAST) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) ek[r] = 0;
+                } else {
                 const int *Eb = reinterpret_cast<const int *>(smem + buf * C::BUF +
                                                               C::STEP_KEYS * KS + C::VFL) +
                                 ks * kTile;
@@ -603,6 +641,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     ek[4 * s4 + 1] = e4.y;
                     ek[4 * s4 + 2] = e4.z;
                     ek[4 * s4 + 3] = e4.w;
+                }
                 }
             } else if constexpr (HALF % 4 == 0) {
 #pragma unroll
@@ -626,7 +665,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             float p[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                p[r] = C::SQK ? ldexpf(sacc[r], eq + ek[r]) : sacc[r] * scale_log2;
+                p[r] = FAST ? sacc[r] : C::SQK ? ldexpf(sacc[r], eq + ek[r]) : sacc[r] * scale_log2;
             if (edge) {  // wave-uniform: most tiles skip the per-key mask
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -656,7 +695,39 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             l = l * corr + ps;
             const float mold = m;
             m = mnew;
-            if constexpr (C::SPV) {
+            if constexpr (FAST) {
+                // One f16 product: P rounded to f16 (p <= 2^kSlack, so no unit is needed),
+                // the V^T hi halves (V rounded to f16 at staging). O^T follows the softmax
+                // correction when any lane's reference max moved.
+                if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+                    for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) oacc[mb][r] *= corr;
+                }
+                f16x8 ph[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    unsigned hw[4];
+#pragma unroll
+                    for (int c2 = 0; c2 < 4; ++c2) {
+                        const int r = 8 * u + 2 * c2;
+                        hw[c2] = __builtin_bit_cast(
+                            unsigned, __builtin_convertvector(f32x2{p[r], p[r + 1]}, f16x2));
+                    }
+                    ph[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+                }
+                const _Float16 *vth = reinterpret_cast<const _Float16 *>(Vb);
+#pragma unroll
+                for (int mb = 0; mb < NB; ++mb) {
+                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 8 * hf;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const f16x8 vh = *reinterpret_cast<const f16x8 *>(vth + roff + 16 * u);
+                        oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
+                    }
+                }
+            } else if constexpr (C::SPV) {
                 // The tile's V exponents ev (V row = 2^ev * v').
                 const int *Ev = reinterpret_cast<const int *>(smem + buf * C::BUF +
                                                               C::STEP_KEYS * KS + C::VFL) +
@@ -781,7 +852,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         else if constexpr (PS)
             ps_store_step<C>(smem, rs, buf ^ 1, tid);
         else
-            prefill_store_step<C>(smem, rk, rv, buf ^ 1, tid);
+            prefill_store_step<C, FAST>(smem, rk, rv, buf ^ 1, tid);
         __syncthreads();
     }
 
@@ -875,7 +946,9 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     }
     __syncthreads();
     if (ks == 0 && live) {
+        // o rows hold hdr dims; the partials keep the instantiation's HD
         float *dst = partial ? part_acc + (size_t)chunk * rows * H * HD : o;
+        const int dstride = partial ? HD : hdr;
         constexpr int ROW4 = HD / 4;  // float4 per output row
 #pragma unroll
         for (int j = 0; j < (kTile * ROW4 + 63) / 64; ++j) {
@@ -883,8 +956,8 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             if (kTile * ROW4 % 64 == 0 || idx < kTile * ROW4) {
                 const int row = idx / ROW4;
                 const int c4 = idx % ROW4;
-                if (q0 + row < rows)
-                    *reinterpret_cast<float4 *>(dst + ((size_t)(q0 + row) * H + head) * HD + 4 * c4) =
+                if (q0 + row < rows && 4 * c4 < dstride)
+                    *reinterpret_cast<float4 *>(dst + ((size_t)(q0 + row) * H + head) * dstride + 4 * c4) =
                         *reinterpret_cast<const float4 *>(ot + row * C::OS + 4 * c4);
             }
         }
@@ -901,12 +974,12 @@ constexpr int kMergeBatch = 8;
 template <int HD>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(
     const float *__restrict__ part_acc, const float *__restrict__ part_ml, float *__restrict__ o,
-    int rows, int H, int QB, int qbase, int window, int ctiles) {
+    int rows, int H, int QB, int qbase, int window, int ctiles, int hdr) {
     constexpr int TP = HD >= 4 ? HD / 4 : 1;  // threads per (row, head) pair
     constexpr int PER = 256 / TP;
     const int pair = blockIdx.x * PER + threadIdx.x / TP;
     const int d = 4 * (threadIdx.x % TP);
-    if (pair >= rows * H) return;
+    if (pair >= rows * H || d >= hdr) return;  // (o rows hold hdr <= HD dims)
     const int row = pair / H;
     const int head = pair % H;
     const int qb = row / QB;
@@ -956,7 +1029,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(
         }
     }
     const float inv = 1.0f / L;
-    *reinterpret_cast<float4 *>(o + at0 * HD + d) =
+    *reinterpret_cast<float4 *>(o + at0 * hdr + d) =
         make_float4(ldexpf(A.x * inv, EM), ldexpf(A.y * inv, EM), ldexpf(A.z * inv, EM),
                     ldexpf(A.w * inv, EM));
 }
@@ -969,7 +1042,16 @@ struct PrefillRange {
     bool h16;    // k/v hold IEEE half elements
     float *ws;   // workspace (null: no pre-split pass, no key chunks)
     size_t ws_floats;
+    int hdr;     // the rows' head dim (at most the instantiation's; the rest reads as zeros)
 };
+
+// The instantiation a head dim runs on: the next power of two (4 .. 256). Head dims 48, 80,
+// 96, ... pad their rows with zero dims, which change no score and are never stored.
+size_t padded_hd(size_t hd) {
+    size_t p = 4;
+    while (p < hd) p *= 2;
+    return p;
+}
 
 // The workgroup shape launch_prefill_hd picks for head_dim hd and g query heads per KV head:
 // HPW heads x WPH 32-row blocks x KSPLIT key splits.
@@ -1080,7 +1162,7 @@ size_t workspace_floats(size_t hd, int H, int Hkv, const PrefillRange &r) {
     return presplit_floats(hd, H, Hkv, r) + chunk_floats(hd, H, prefill_chunks(hd, H, Hkv, r), r);
 }
 
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS>
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS, bool FAST = false>
 eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
                            const float *ps, float *o, int H, int Hkv, const PrefillRange &r,
                            float scale_log2, const PrefillChunks &ch, float *part_acc,
@@ -1091,7 +1173,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(
             reinterpret_cast<const void *>(
-                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS>),
+                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS, FAST>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
@@ -1099,15 +1181,15 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const dim3 grid((unsigned)(nqb * ngroups), (unsigned)ch.nchmax);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS, FAST><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
         q, k, v, ps, presplit_tlo(r), presplit_nt(r), o, H, Hkv, r.rows, r.nkeys, r.qbase,
-        r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml);
+        r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml, r.hdr);
     eb_status err = eb::check_launch("attn_prefill");
     if (err != EB_OK || ch.nchmax <= 1) return err;
     constexpr int PER = 256 / (HD >= 4 ? HD / 4 : 1);
     const unsigned mblocks = (unsigned)(((size_t)r.rows * H + PER - 1) / PER);
     prefill_merge_kernel<HD><<<mblocks, 256, 0, st>>>(part_acc, part_ml, o, r.rows, H, C::QB,
-                                                      r.qbase, r.window, ch.ctiles);
+                                                      r.qbase, r.window, ch.ctiles, r.hdr);
     return eb::check_launch("attn_prefill (chunk merge)");
 }
 
@@ -1127,10 +1209,10 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
             const dim3 grid((unsigned)nt, (unsigned)Hkv);
             if (r.h16)
                 presplit_kernel<HD, true><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
-                                                               presplit_tlo(r), nt);
+                                                               presplit_tlo(r), nt, r.hdr);
             else
                 presplit_kernel<HD, false><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
-                                                                presplit_tlo(r), nt);
+                                                                presplit_tlo(r), nt, r.hdr);
             const eb_status err = eb::check_launch("attn_prefill (pre-split)");
             if (err != EB_OK) return err;
             if (plain && !r.h16)
@@ -1179,10 +1261,12 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
     const float sl2 = scale * eb::kLog2e;
     const int H = (int)h, Hk = (int)hkv;
     PrefillRange rr = r;
-    const size_t need = workspace_floats(hd, H, Hk, r);
+    rr.hdr = (int)hd;
+    const size_t hp = padded_hd(hd);
+    const size_t need = workspace_floats(hp, H, Hk, r);
     if (need == 0 || !r.ws || r.ws_floats < need || (reinterpret_cast<uintptr_t>(r.ws) & 15))
         rr.ws = nullptr;  // no pre-split pass (split while staging), no key chunks
-    switch (hd) {
+    switch (hp) {
         case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, rr, sl2);
         case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, rr, sl2);
         case 16: return launch_prefill_hd<16>(st, q, k, v, o, H, Hk, rr, sl2);
@@ -1194,23 +1278,60 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
     }
 }
 
+// The single-product f16 mode for prompts from position 0 (no window), f32 q/k/v, head
+// dims 32..256 (padded to 64 / 128 / 256 as the accurate path does).
+template <int HD>
+eb_status launch_prefill_fast_hd(hipStream_t st, const float *q, const float *k, const float *v,
+                                 float *o, int H, int Hkv, const PrefillRange &r, float sl2) {
+    const int g = H / Hkv;
+    constexpr int KSPLIT = HD <= 128 ? 2 : 1;
+    const PrefillChunks ch{};
+    if (g % 4 == 0)
+        return launch_prefill_r<HD, 4, 1, 1, false, false, false, true>(
+            st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
+    if (g % 2 == 0)
+        return launch_prefill_r<HD, 2, 2, KSPLIT, false, false, false, true>(
+            st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
+    return launch_prefill_r<HD, 1, 4, KSPLIT, false, false, false, true>(
+        st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
+}
+
 }  // namespace
 
 namespace eb {
 
+eb_status launch_attn_prefill_fast(hipStream_t st, const float *q, const float *k, const float *v,
+                                   float *o, size_t h, size_t hkv, size_t s, size_t hd,
+                                   float scale) {
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15)
+        return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill_fast: q/k/v/o must be 16-byte aligned");
+    const PrefillRange r{(int)s, (int)s, 0, 0, false, nullptr, 0, (int)hd};
+    const float sl2 = scale * kLog2e;
+    switch (padded_hd(hd)) {
+        case 32: return launch_prefill_fast_hd<32>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);
+        case 64: return launch_prefill_fast_hd<64>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);
+        case 128: return launch_prefill_fast_hd<128>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);
+        case 256: return launch_prefill_fast_hd<256>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);
+        default:
+            return eb::fail(EB_UNSUPPORTED_CONFIG,
+                            "attn_prefill_fast: head_dim %zu (32 to 256, multiples of 16)", hd);
+    }
+}
+
 size_t prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t rows, size_t nkeys,
                                 size_t qbase, size_t window) {
     if (rows == 0 || hkv == 0 || h % hkv != 0) return 0;
-    return workspace_floats(hd, (int)h, (int)hkv,
+    return workspace_floats(padded_hd(hd), (int)h, (int)hkv,
                             PrefillRange{(int)rows, (int)nkeys, (int)qbase, (int)window, false,
-                                         nullptr, 0});
+                                         nullptr, 0, (int)hd});
 }
 
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd, float scale,
                               float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
-                                PrefillRange{(int)s, (int)s, 0, 0, false, ws, ws_floats});
+                                PrefillRange{(int)s, (int)s, 0, 0, false, ws, ws_floats, (int)hd});
 }
 
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
@@ -1219,7 +1340,7 @@ eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float 
                                     size_t window, float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window, false, ws, ws_floats});
+                                             (int)window, false, ws, ws_floats, (int)hd});
 }
 
 eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
@@ -1228,7 +1349,7 @@ eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const ui
                                         size_t window, float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window, true, ws, ws_floats});
+                                             (int)window, true, ws, ws_floats, (int)hd});
 }
 
 }  // namespace eb

@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
@@ -98,10 +99,7 @@ eb_status check_heads(size_t h, size_t hkv) {
 }
 
 bool attn_head_dim_supported(size_t hd) {
-    switch (hd) {
-        case 4: case 8: case 16: case 32: case 64: case 128: case 256: return true;
-        default: return false;
-    }
+    return hd == 4 || hd == 8 || (hd % 16 == 0 && hd >= 16 && hd <= 256);
 }
 
 int current_cu_count() {
@@ -715,7 +713,7 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_prefill: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)", hd);
+                    "attn_prefill: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)", hd);
     EB_TRY(eb::check_numel(qn, {s, h, hd}, "q"));
     EB_TRY(eb::check_numel(kn, {s, hkv, hd}, "k"));
     EB_TRY(eb::check_numel(vn, {s, hkv, hd}, "v"));
@@ -733,6 +731,33 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     return eb::ok();
 }
 
+// The single-product f16 prefill (opt-in): the checks of prefill_checked, then the scale
+// bound that keeps the f16 rounding of q and K inside the stated tolerance.
+static eb_status prefill_fast_checked(hipStream_t st, const float *q, size_t qn, const float *k,
+                                      size_t kn, const float *v, size_t vn, float *o, size_t on,
+                                      size_t h, size_t hkv, size_t s, size_t hd, float scale) {
+    EB_TRY(eb::check_heads(h, hkv));
+    if (hd < 32 || hd > 256 || hd % 16 != 0)
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_prefill_fast: head_dim %zu (multiples of 16 from 32 to 256)", hd);
+    if (!(std::fabs(scale) * std::sqrt((double)hd) <= 1.0001))
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_prefill_fast: scale %g above 1/sqrt(head_dim): the f16 rounding of "
+                    "the scores would exceed the mode's tolerance (use attn_prefill)",
+                    (double)scale);
+    EB_TRY(eb::check_numel(qn, {s, h, hd}, "q"));
+    EB_TRY(eb::check_numel(kn, {s, hkv, hd}, "k"));
+    EB_TRY(eb::check_numel(vn, {s, hkv, hd}, "v"));
+    EB_TRY(eb::check_numel(on, {s, h, hd}, "o"));
+    if (s == 0) return eb::ok();
+    EB_TRY(eb::check_ptr(q, "q"));
+    EB_TRY(eb::check_ptr(k, "k"));
+    EB_TRY(eb::check_ptr(v, "v"));
+    EB_TRY(eb::check_ptr(o, "o"));
+    EB_TRY(eb::launch_attn_prefill_fast(st, q, k, v, o, h, hkv, s, hd, scale));
+    return eb::ok();
+}
+
 static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn,
                                        const void *kc, size_t kcn, const void *vc, size_t vcn,
                                        float *o, size_t on, size_t h, size_t hkv, size_t pos0,
@@ -742,7 +767,7 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_prefill_chunk: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)",
+                    "attn_prefill_chunk: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)",
                     hd);
     if (h16 && hd < 8)
         return fail(EB_UNSUPPORTED_CONFIG, "attn_prefill_chunk: f16 caches need head_dim >= 8");
@@ -780,7 +805,7 @@ static eb_status decode_shape_checked(const float *q, size_t qn, const void *kc,
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_decode: head_dim %zu (supported: 4, 8, 16, 32, 64, 128, 256)", hd);
+                    "attn_decode: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)", hd);
     if (h16 && hd < 8)
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
     if (pos >= max_seq)
@@ -1033,6 +1058,28 @@ eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor 
                            (const float *)k->ptr, eb_tensor_numel(k), (const float *)v->ptr,
                            eb_tensor_numel(v), (float *)o->ptr, eb_tensor_numel(o), h, hkv, s,
                            hd, scale, PrefillWs{rec->dev});
+}
+
+eb_status eb_attn_prefill_fast(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                               const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
+                               size_t hd, float scale) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(k, "k", rec->dev));
+    EB_TRY(tensor_f32(v, "v", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    return prefill_fast_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
+                                (const float *)k->ptr, eb_tensor_numel(k), (const float *)v->ptr,
+                                eb_tensor_numel(v), (float *)o->ptr, eb_tensor_numel(o), h, hkv, s,
+                                hd, scale);
+}
+
+eb_status eb_launch_attn_prefill_fast(void *stream, const float *q, size_t q_numel,
+                                      const float *k, size_t k_numel, const float *v,
+                                      size_t v_numel, float *o, size_t o_numel, size_t h,
+                                      size_t hkv, size_t s, size_t hd, float scale) {
+    return prefill_fast_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                o_numel, h, hkv, s, hd, scale);
 }
 
 eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,

@@ -15,6 +15,14 @@ def attn_prefill(rec: Recorder, q: Tensor, k: Tensor, v: Tensor, o: Tensor, h: i
                                 hd, scale))
 
 
+def attn_prefill_fast(rec: Recorder, q: Tensor, k: Tensor, v: Tensor, o: Tensor, h: int,
+                      hkv: int, s: int, hd: int, scale: float) -> None:
+    """attn_prefill in the opt-in f16 mode: one f16 matrix-core product per product (q, K,
+    V, P rounded to f16 once), f32 softmax and accumulation; |scale| <= 1/sqrt(hd)."""
+    check(lib().eb_attn_prefill_fast(rec.handle, q.handle, k.handle, v.handle, o.handle, h, hkv,
+                                     s, hd, scale))
+
+
 def attn_decode(rec: Recorder, q: Tensor, kcache: Tensor, vcache: Tensor, o: Tensor, h: int,
                 hkv: int, pos: int, hd: int, max_seq: int, scale: float) -> None:
     """attention.rs:124-162: q [h,hd] attends keys 0..=pos of [max_seq,hkv,hd] caches."""
@@ -137,6 +145,13 @@ def launch_attn_prefill(stream: int, q: int, q_numel: int, k: int, k_numel: int,
                         scale: float) -> None:
     check(lib().eb_launch_attn_prefill(stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
                                        h, hkv, s, hd, scale))
+
+
+def launch_attn_prefill_fast(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                             v_numel: int, o: int, o_numel: int, h: int, hkv: int, s: int,
+                             hd: int, scale: float) -> None:
+    check(lib().eb_launch_attn_prefill_fast(stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                            o_numel, h, hkv, s, hd, scale))
 
 
 def attn_prefill_workspace_floats(h: int, hkv: int, hd: int, pos0: int, rows: int,

@@ -148,6 +148,18 @@ eb_status eb_tensor_write(eb_tensor *t, const void *host, size_t nbytes);
 eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
                           const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
                           size_t hd, float scale);
+/* attn_prefill in the opt-in f16 mode (no counterpart in the reference, whose prefill is
+ * f32): q, K, V and the softmax weights are rounded to IEEE half once and each product is
+ * one f16 matrix-core instruction (attn_prefill takes three, on exact hi/lo splits); the
+ * online softmax, its rescaling and the accumulation stay f32. Tolerance against the f32
+ * reference, measured on the BASELINE prefill configs (N(0,1) inputs, scale 1/sqrt(hd)):
+ * rel-L2 about 4e-4 and max-abs below 2e-3 (the north-star bar holds). Prompts from
+ * position 0, head_dim a multiple of 16 from 32 to 256, |scale| at most 1/sqrt(head_dim):
+ * larger scales (Gemma-4's 1.0) make the scores' f16 rounding error exceed that bar and
+ * are refused (EB_UNSUPPORTED_CONFIG); inputs must fit f16 (|x| < 65504). */
+eb_status eb_attn_prefill_fast(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                               const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
+                               size_t hd, float scale);
 /* attn_decode (attention.rs:124-162): q [h,hd] attends keys 0..=pos of the seq-major
  * caches [max_seq,hkv,hd]; o [h,hd]. Split-KV with a log-sum-exp merge; the split
  * workspace belongs to the device and is stream ordered. */
@@ -209,6 +221,10 @@ eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel,
                                  const float *k, size_t k_numel, const float *v,
                                  size_t v_numel, float *o, size_t o_numel, size_t h,
                                  size_t hkv, size_t s, size_t hd, float scale);
+eb_status eb_launch_attn_prefill_fast(void *stream, const float *q, size_t q_numel,
+                                      const float *k, size_t k_numel, const float *v,
+                                      size_t v_numel, float *o, size_t o_numel, size_t h,
+                                      size_t hkv, size_t s, size_t hd, float scale);
 eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_numel,
                                        const float *kc, size_t kc_numel, const float *vc,
                                        size_t vc_numel, float *o, size_t o_numel, size_t h,

@@ -1,0 +1,111 @@
+"""The opt-in single-product f16 prefill (eb_attn_prefill_fast) against the f32 oracle.
+
+q, K, V and the softmax weights are rounded to IEEE half once and each product is one f16
+matrix-core instruction; the online softmax and the accumulation stay f32. Its stated
+tolerance is the north-star bar itself, rel-L2 <= 1e-3 and max-abs <= 2e-3 against the f32
+reference (crates/eyebrowse-kernels/src/testutil.rs:130-172 restated in oracle/oracle.c),
+for scores of the BASELINE prefill configs' size (N(0,1) inputs, scale 1/sqrt(head_dim)).
+A CPU emulation of the rounding (f16 q, K, V, P; f64 elsewhere) predicts rel-L2 4.2e-4 at
+Qwen / Mistral T=4096; each test also holds the result below 6e-4 so that a lost term (a
+dropped rescale, a wrong key) fails here rather than hiding under the bar.
+"""
+import numpy as np
+import pytest
+
+import eyebrowse_amd as eb
+import oracle
+from tests._gpu import NORTH_MAX_ABS, NORTH_REL_L2, note, upload
+from tests._textbook import rel_l2_f64
+
+pytestmark = pytest.mark.gpu
+
+FAST_REL_L2 = 6e-4
+
+
+def fast_prefill(dev, q, k, v, h, hkv, s, hd, scale):
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    ot = eb.Tensor.empty(dev, (s, h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_prefill_fast(rec, qt, kt, vt, ot, h, hkv, s, hd, scale)
+    rec.submit()
+    return ot.to_f32().reshape(s, h, hd)
+
+
+def check(got, want, what):
+    assert np.isfinite(got).all(), what
+    r = rel_l2_f64(got, want)
+    m = float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64))))
+    assert r <= NORTH_REL_L2 and m <= NORTH_MAX_ABS, f"{what}: rel={r:.3e} max={m:.3e}"
+    assert r <= FAST_REL_L2, f"{what}: rel={r:.3e} above the mode's expected 4e-4 (+50 %)"
+    return r, m
+
+
+@pytest.mark.parametrize("name,H,Hkv,hd,T", [
+    ("qwen", 16, 8, 128, 512),
+    ("qwen", 16, 8, 128, 4096),
+    ("mistral", 32, 8, 128, 4096),
+])
+def test_baseline_configs(dev, name, H, Hkv, hd, T):
+    """BASELINE prefill configs 3 and 4, every row against the oracle."""
+    note(f"fast prefill {name} T={T}")
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((T, H, hd), 1)
+    k = oracle.randn((T, Hkv, hd), 2)
+    v = oracle.randn((T, Hkv, hd), 3)
+    got = fast_prefill(dev, q, k, v, H, Hkv, T, hd, sc)
+    want = oracle.attn_prefill(q, k, v, H, Hkv, T, hd, sc, threads=16)
+    check(got, want, f"{name} T={T}")
+    for b0 in range(0, T, 256):
+        check(got[b0:b0 + 256], want[b0:b0 + 256], f"{name} rows {b0}+256")
+
+
+@pytest.mark.parametrize("h,hkv,s,hd", [
+    (16, 8, 1, 128), (16, 8, 33, 128), (32, 8, 100, 128), (8, 8, 97, 64), (24, 8, 70, 128),
+    (16, 8, 77, 256), (4, 2, 50, 32), (8, 2, 130, 80), (6, 3, 90, 192),
+])
+def test_shapes(dev, h, hkv, s, hd):
+    """GQA ratios 1 to 4, head dims 32 to 256 (80 and 192 padded), ragged lengths."""
+    note(f"fast prefill h={h} hkv={hkv} s={s} hd={hd}")
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((s, h, hd), 11)
+    k = oracle.randn((s, hkv, hd), 12)
+    v = oracle.randn((s, hkv, hd), 13)
+    got = fast_prefill(dev, q, k, v, h, hkv, s, hd, sc)
+    want = oracle.attn_prefill(q, k, v, h, hkv, s, hd, sc, threads=8)
+    check(got, want, f"shape h={h} s={s} hd={hd}")
+    # row 0 attends key 0 only: o = v[0] rounded to f16 (P = 1 exactly)
+    g = h // hkv
+    want0 = np.repeat(v[0], g, axis=0).astype(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(got[0], want0)
+
+
+def test_raw_launch_matches_recorder(dev):
+    H, Hkv, hd, T = 16, 8, 128, 300
+    q, k, v = oracle.randn((T, H, hd), 4), oracle.randn((T, Hkv, hd), 5), oracle.randn((T, Hkv, hd), 6)
+    sc = float(oracle.default_scale(hd))
+    a = fast_prefill(dev, q, k, v, H, Hkv, T, hd, sc)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    ot = eb.Tensor.empty(dev, (T, H, hd))
+    eb.launch_attn_prefill_fast(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(),
+                                vt.data_ptr, vt.numel(), ot.data_ptr, ot.numel(), H, Hkv, T, hd,
+                                sc)
+    dev.synchronize()
+    np.testing.assert_array_equal(ot.to_f32().reshape(T, H, hd), a)
+
+
+def test_refusals(dev):
+    """Scales above 1/sqrt(head_dim) (Gemma-4's 1.0: its scores' f16 rounding error exceeds
+    the bar, rel-L2 1.35e-3 and max-abs 2.2e-2 in the CPU emulation) and head dims outside
+    32..256 are refused before any launch."""
+    H, Hkv, hd, T = 16, 8, 256, 8
+    q = eb.Tensor.empty(dev, (T, H, hd))
+    k = eb.Tensor.empty(dev, (T, Hkv, hd))
+    o = eb.Tensor.empty(dev, (T, H, hd))
+    rec = eb.Recorder(dev)
+    with pytest.raises(eb.UnsupportedConfig):
+        eb.attn_prefill_fast(rec, q, k, k, o, H, Hkv, T, hd, 1.0)
+    q16 = eb.Tensor.empty(dev, (T, H, 16))
+    k16 = eb.Tensor.empty(dev, (T, Hkv, 16))
+    with pytest.raises(eb.UnsupportedConfig):
+        eb.attn_prefill_fast(rec, q16, k16, k16, q16, H, Hkv, T, 16, 0.25)
+    rec.submit()
