@@ -17,6 +17,7 @@ from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_
                       attn_decode_step_window, attn_decode_window, attn_decode_workspace_floats,
                       attn_prefill, attn_prefill_chunk, attn_prefill_fast,
                       attn_prefill_workspace_floats, launch_attn_prefill_fast,
+                      attn_prefill_fast_workspace_floats, launch_attn_prefill_fast_ws,
                       kv_write, launch_argmax,
                       launch_attn_decode, launch_attn_decode_f16, launch_attn_decode_step,
                       launch_attn_decode_step_f16, launch_attn_decode_window,
@@ -34,7 +35,8 @@ __all__ = [
     "OutOfMemory", "Recorder", "ShapeMismatch", "Tensor", "UnsupportedConfig", "attn_decode",
     "attn_decode_step", "attn_decode_step_window", "attn_decode_window",
     "attn_decode_workspace_floats", "attn_prefill", "attn_prefill_chunk", "kv_write",
-    "attn_prefill_fast", "launch_attn_prefill_fast",
+    "attn_prefill_fast", "launch_attn_prefill_fast", "attn_prefill_fast_workspace_floats",
+    "launch_attn_prefill_fast_ws",
     "launch_attn_decode", "launch_attn_decode_f16", "launch_attn_decode_step",
     "launch_attn_decode_step_f16", "launch_attn_decode_window", "launch_attn_prefill",
     "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_attn_prefill_chunk_ws",

@@ -64,9 +64,13 @@ eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, co
 // The single-product f16 prefill (opt-in): q, K, V and P rounded to f16 once, one f16 MFMA
 // per product, f32 softmax and accumulation. Prompts from position 0, f32 q/k/v, head dims
 // 32..256 (multiples of 16); no workspace.
+// With a workspace of prefill_fast_workspace_floats (16-byte aligned), a pre-convert pass
+// rounds K/V to f16 once into records that the attention kernel copies (head_dim <= 128,
+// at least 3 query blocks); otherwise every workgroup converts the f32 rows it stages.
+size_t prefill_fast_workspace_floats(size_t h, size_t hkv, size_t hd, size_t s);
 eb_status launch_attn_prefill_fast(hipStream_t st, const float *q, const float *k, const float *v,
                                    float *o, size_t h, size_t hkv, size_t s, size_t hd,
-                                   float scale);
+                                   float scale, float *ws = nullptr, size_t ws_floats = 0);
 // Chunked causal prefill: q rows at positions pos0..pos0+rows-1 attend cache keys
 // max(0, p - window + 1)..p (window 0: 0..p); kc/vc are the cache bases.
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,

@@ -125,6 +125,12 @@ struct PrefillCfg {
     static constexpr int PS_FLOATS = PS_IMAGE ? BUF : 4 * PS_CH;  // floats per record
     static constexpr int PS_KV = KSPLIT * 16 * HD;      // K/V chunks per step
     static constexpr int PSN = PS_IMAGE ? 1 : (PS_KV + THREADS - 1) / THREADS + 1;  // + exps
+    // f16-mode records (head_dim <= 128): K rows [32][HD halves] then V^T [HD][32 halves],
+    // rounded once by the pre-convert pass; a step copies KSPLIT records through registers.
+    static constexpr int FPS_CH = 8 * HD;                // chunks per record
+    static constexpr int FPS_FLOATS = 4 * FPS_CH;
+    static constexpr int FPS_KV = KSPLIT * FPS_CH;       // chunks per step
+    static constexpr int FPSN = (FPS_KV + THREADS - 1) / THREADS;
     static constexpr int REC = 3 + 16 * NB;  // merged fields per lane: m, l, V unit, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
     static constexpr int OS = HD + 4;                  // output staging row stride (floats)
@@ -367,6 +373,63 @@ __device__ __forceinline__ void ps_store_step(float *smem, const f32x4 (&r)[C::P
             r[C::PSN - 1];
 }
 
+// Float offset, inside one LDS buffer of C, of chunk w of tile kt's f16-mode record: the
+// hi halves prefill_store_step<C, true> writes for that tile (K rows, then V^T rows).
+template <class C>
+__device__ __forceinline__ int fps_lds_offset(int kt, int w) {
+    constexpr int HD = C::HD_;
+    if (w < 4 * HD) return (kt * kTile + w / (HD / 8)) * C::KS + 4 * (w % (HD / 8));
+    const int w2 = w - 4 * HD;
+    return C::STEP_KEYS * C::KS + (w2 / 4) * (C::VROW / 2) + kt * (kTile / 2) + 4 * (w2 % 4);
+}
+
+template <class C>
+__device__ __forceinline__ void fps_load_step(const f32x4 *__restrict__ recs,
+                                              f32x4 (&r)[C::FPSN], int tile0, int nt, int tid) {
+    constexpr int HD = C::HD_;
+#pragma unroll
+    for (int i = 0; i < C::FPSN; ++i) {
+        const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
+        const int t = min(tile0 + c / (8 * HD), nt - 1);
+        r[i] = recs[(size_t)t * C::FPS_CH + c % (8 * HD)];
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void fps_store_step(float *smem, const f32x4 (&r)[C::FPSN], int buf,
+                                               int tid) {
+    constexpr int HD = C::HD_;
+    float *B = smem + buf * C::BUF;
+#pragma unroll
+    for (int i = 0; i < C::FPSN; ++i) {
+        const int c = tid + i * C::THREADS;
+        if (C::FPS_KV % C::THREADS == 0 || c < C::FPS_KV)
+            *reinterpret_cast<f32x4 *>(B + fps_lds_offset<C>(c / (8 * HD), c % (8 * HD))) = r[i];
+    }
+}
+
+// Pre-convert pass of the f16 mode: workgroup (t, kvh) rounds keys [(tlo + t) * 32, +32) of KV
+// head kvh to f16 as the f16 mode's staging does, and writes the tile's record.
+template <int HD>
+__global__ __launch_bounds__(256) void preconvert_kernel(const float *__restrict__ k,
+                                                         const float *__restrict__ v,
+                                                         float *__restrict__ ps, int nkeys,
+                                                         int Hkv, int nt, int hdr) {
+    using C = PrefillCfg<HD, 4, 1, 1>;
+    static_assert(HD <= 128, "f16-mode records for head_dim <= 128");
+    __shared__ float smem[C::BUF];
+    const int t = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int tid = threadIdx.x;
+    f32x4 rk[C::NLD], rv[C::NLD];
+    prefill_load_step<C, false>(k, v, rk, rv, t * kTile, nkeys, Hkv, kvh, tid, hdr);
+    prefill_store_step<C, true>(smem, rk, rv, 0, tid);
+    __syncthreads();
+    f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::FPS_FLOATS);
+    for (int c = tid; c < C::FPS_CH; c += C::THREADS)
+        rec[c] = *reinterpret_cast<const f32x4 *>(smem + fps_lds_offset<C>(0, c));
+}
+
 // Pre-split pass: workgroup (t, kvh) splits keys [(tlo + t) * 32, +32) of KV head kvh
 // (rows past nkeys as zeros) exactly as the prefill's own staging does, and writes the
 // tile's record. The prefill then only copies records into LDS: the split is done once
@@ -510,10 +573,13 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             // from the clamped row 0) and scales by qs, 0 past the end, so that the loads
             // issue back to back; such a lane's query column never reaches the output.
             // Dims past hdr (a head dim padded up to this instantiation) are zeros.
-            const bool kin = 16 * k2 < hdr;
-            const float *qk = qp + (kin ? 16 * k2 : 0);
-            qa[k2] = *reinterpret_cast<const f32x4 *>(qk) * (kin ? qs : 0.0f);
-            qb[k2] = *reinterpret_cast<const f32x4 *>(qk + 4) * (kin ? qs : 0.0f);
+            if (16 * k2 < hdr) {  // (uniform)
+                qa[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2) * qs;
+                qb[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) * qs;
+            } else {
+                qa[k2] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                qb[k2] = qa[k2];
+            }
             const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
                                          fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
                                    fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
@@ -571,9 +637,14 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
-    f32x4 rs[PS ? C::PSN : 1];
-    const float *recs = PS ? ps + (size_t)kvh * ps_nt * C::PS_FLOATS : nullptr;
-    if constexpr (PS && C::PS_IMAGE) {
+    static_assert(!(PS && FAST && C::PS_IMAGE), "f16-mode records for head_dim <= 128");
+    f32x4 rs[PS ? (FAST ? C::FPSN : C::PSN) : 1];
+    const float *recs =
+        PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
+    if constexpr (PS && FAST) {
+        fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+        fps_store_step<C>(smem, rs, 0, tid);
+    } else if constexpr (PS && C::PS_IMAGE) {
         ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
         wait_vm_all();
     } else if constexpr (PS) {
@@ -593,7 +664,10 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         // buffer written from them is never read).
         // PS image records go straight into the other buffer, which every wave finished
         // reading before the last barrier.
-        if constexpr (PS && C::PS_IMAGE)
+        if constexpr (PS && FAST)
+            fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
+                             c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
+        else if constexpr (PS && C::PS_IMAGE)
             ps_copy_image<C>(recs, smem, buf ^ 1, c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, wave,
                              lane);
         else if constexpr (PS)
@@ -847,7 +921,9 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             }
         }
 
-        if constexpr (PS && C::PS_IMAGE)
+        if constexpr (PS && FAST)
+            fps_store_step<C>(smem, rs, buf ^ 1, tid);
+        else if constexpr (PS && C::PS_IMAGE)
             wait_vm_all();
         else if constexpr (PS)
             ps_store_step<C>(smem, rs, buf ^ 1, tid);
@@ -1280,33 +1356,68 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
 
 // The single-product f16 mode for prompts from position 0 (no window), f32 q/k/v, head
 // dims 32..256 (padded to 64 / 128 / 256 as the accurate path does).
+// f16-mode records: floats of workspace for this shape (0: the mode stages f32 K/V itself).
+// Like the pre-split pass, the pre-convert pass pays where at least 3 query blocks share the
+// keys; head dims above 128 stage directly.
+size_t fast_workspace_floats(size_t hp, int H, int Hkv, int s) {
+    if (hp < 32 || hp > 128 || s <= 0) return 0;
+    const int qb_rows = kTile * prefill_shape(hp, H / Hkv).wph;
+    if ((s + qb_rows - 1) / qb_rows < kPresplitMinBlocks) return 0;
+    const size_t rec = hp == 32 ? PrefillCfg<32, 4, 1, 1>::FPS_FLOATS
+                       : hp == 64 ? PrefillCfg<64, 4, 1, 1>::FPS_FLOATS
+                                  : PrefillCfg<128, 4, 1, 1>::FPS_FLOATS;
+    return (size_t)Hkv * (size_t)((s + kTile - 1) / kTile) * rec;
+}
+
+template <int HD, int HPW, int WPH, int KSPLIT>
+eb_status launch_prefill_fast_t(hipStream_t st, const float *q, const float *k, const float *v,
+                                float *o, int H, int Hkv, const PrefillRange &r, float sl2) {
+    const PrefillChunks ch{};
+    if constexpr (HD <= 128) {
+        if (r.ws) {
+            const int nt = presplit_nt(r);
+            preconvert_kernel<HD><<<dim3((unsigned)nt, (unsigned)Hkv), 256, 0, st>>>(
+                k, v, r.ws, r.nkeys, Hkv, nt, r.hdr);
+            const eb_status err = eb::check_launch("attn_prefill_fast (pre-convert)");
+            if (err != EB_OK) return err;
+            return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, true, true>(
+                st, q, k, v, r.ws, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
+        }
+    }
+    return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, false, true>(
+        st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
+}
+
 template <int HD>
 eb_status launch_prefill_fast_hd(hipStream_t st, const float *q, const float *k, const float *v,
                                  float *o, int H, int Hkv, const PrefillRange &r, float sl2) {
     const int g = H / Hkv;
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
-    const PrefillChunks ch{};
-    if (g % 4 == 0)
-        return launch_prefill_r<HD, 4, 1, 1, false, false, false, true>(
-            st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
-    if (g % 2 == 0)
-        return launch_prefill_r<HD, 2, 2, KSPLIT, false, false, false, true>(
-            st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
-    return launch_prefill_r<HD, 1, 4, KSPLIT, false, false, false, true>(
-        st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
+    if (g % 4 == 0) return launch_prefill_fast_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, sl2);
+    if (g % 2 == 0) return launch_prefill_fast_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, r, sl2);
+    return launch_prefill_fast_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, r, sl2);
 }
 
 }  // namespace
 
 namespace eb {
 
+size_t prefill_fast_workspace_floats(size_t h, size_t hkv, size_t hd, size_t s) {
+    if (hkv == 0 || h % hkv != 0 || s == 0) return 0;
+    return fast_workspace_floats(padded_hd(hd), (int)h, (int)hkv, (int)s);
+}
+
 eb_status launch_attn_prefill_fast(hipStream_t st, const float *q, const float *k, const float *v,
                                    float *o, size_t h, size_t hkv, size_t s, size_t hd,
-                                   float scale) {
+                                   float scale, float *ws, size_t ws_floats) {
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
-         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15)
-        return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill_fast: q/k/v/o must be 16-byte aligned");
-    const PrefillRange r{(int)s, (int)s, 0, 0, false, nullptr, 0, (int)hd};
+         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o) |
+         reinterpret_cast<uintptr_t>(ws)) & 15)
+        return eb::fail(EB_UNSUPPORTED_CONFIG,
+                        "attn_prefill_fast: q/k/v/o/workspace must be 16-byte aligned");
+    const size_t need = prefill_fast_workspace_floats(h, hkv, hd, s);
+    if (need == 0 || ws_floats < need) ws = nullptr;  // stage f32 K/V in every workgroup
+    const PrefillRange r{(int)s, (int)s, 0, 0, false, ws, ws_floats, (int)hd};
     const float sl2 = scale * kLog2e;
     switch (padded_hd(hd)) {
         case 32: return launch_prefill_fast_hd<32>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);

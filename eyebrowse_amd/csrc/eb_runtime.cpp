@@ -735,7 +735,8 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
 // bound that keeps the f16 rounding of q and K inside the stated tolerance.
 static eb_status prefill_fast_checked(hipStream_t st, const float *q, size_t qn, const float *k,
                                       size_t kn, const float *v, size_t vn, float *o, size_t on,
-                                      size_t h, size_t hkv, size_t s, size_t hd, float scale) {
+                                      size_t h, size_t hkv, size_t s, size_t hd, float scale,
+                                      const PrefillWs &wsrc = PrefillWs()) {
     EB_TRY(eb::check_heads(h, hkv));
     if (hd < 32 || hd > 256 || hd % 16 != 0)
         return fail(EB_UNSUPPORTED_CONFIG,
@@ -754,7 +755,23 @@ static eb_status prefill_fast_checked(hipStream_t st, const float *q, size_t qn,
     EB_TRY(eb::check_ptr(k, "k"));
     EB_TRY(eb::check_ptr(v, "v"));
     EB_TRY(eb::check_ptr(o, "o"));
-    EB_TRY(eb::launch_attn_prefill_fast(st, q, k, v, o, h, hkv, s, hd, scale));
+    float *ws = nullptr;
+    size_t wsn = 0;
+    WsLock lk;
+    const size_t need = eb::prefill_fast_workspace_floats(h, hkv, hd, s);
+    if (need > 0 && wsrc.dev) {
+        EB_TRY(device_workspace(wsrc.dev, need, &ws, lk));
+        wsn = need;
+    } else if (need > 0 && wsrc.caller) {
+        if (wsrc.floats < need)
+            return fail(EB_SHAPE_MISMATCH,
+                        "attn_prefill_fast: workspace holds %zu floats, needs %zu", wsrc.floats,
+                        need);
+        EB_TRY(eb::check_ptr(wsrc.ptr, "workspace"));
+        ws = wsrc.ptr;
+        wsn = need;
+    }
+    EB_TRY(eb::launch_attn_prefill_fast(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
     return eb::ok();
 }
 
@@ -1071,7 +1088,7 @@ eb_status eb_attn_prefill_fast(eb_recorder *rec, const eb_tensor *q, const eb_te
     return prefill_fast_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
                                 (const float *)k->ptr, eb_tensor_numel(k), (const float *)v->ptr,
                                 eb_tensor_numel(v), (float *)o->ptr, eb_tensor_numel(o), h, hkv, s,
-                                hd, scale);
+                                hd, scale, PrefillWs{rec->dev});
 }
 
 eb_status eb_launch_attn_prefill_fast(void *stream, const float *q, size_t q_numel,
@@ -1080,6 +1097,20 @@ eb_status eb_launch_attn_prefill_fast(void *stream, const float *q, size_t q_num
                                       size_t hkv, size_t s, size_t hd, float scale) {
     return prefill_fast_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o,
                                 o_numel, h, hkv, s, hd, scale);
+}
+
+size_t eb_attn_prefill_fast_workspace_floats(size_t h, size_t hkv, size_t hd, size_t s) {
+    return eb::prefill_fast_workspace_floats(h, hkv, hd, s);
+}
+
+eb_status eb_launch_attn_prefill_fast_ws(void *stream, const float *q, size_t q_numel,
+                                         const float *k, size_t k_numel, const float *v,
+                                         size_t v_numel, float *o, size_t o_numel, size_t h,
+                                         size_t hkv, size_t s, size_t hd, float scale,
+                                         float *workspace, size_t workspace_floats) {
+    return prefill_fast_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                o_numel, h, hkv, s, hd, scale,
+                                PrefillWs{nullptr, true, workspace, workspace_floats});
 }
 
 eb_status eb_attn_decode(eb_recorder *rec, const eb_tensor *q, const eb_tensor *kcache,

@@ -154,6 +154,19 @@ def launch_attn_prefill_fast(stream: int, q: int, q_numel: int, k: int, k_numel:
                                             o_numel, h, hkv, s, hd, scale))
 
 
+def attn_prefill_fast_workspace_floats(h: int, hkv: int, hd: int, s: int) -> int:
+    return int(lib().eb_attn_prefill_fast_workspace_floats(h, hkv, hd, s))
+
+
+def launch_attn_prefill_fast_ws(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                                v_numel: int, o: int, o_numel: int, h: int, hkv: int, s: int,
+                                hd: int, scale: float, workspace: int,
+                                workspace_floats: int) -> None:
+    check(lib().eb_launch_attn_prefill_fast_ws(stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                               o_numel, h, hkv, s, hd, scale, workspace,
+                                               workspace_floats))
+
+
 def attn_prefill_workspace_floats(h: int, hkv: int, hd: int, pos0: int, rows: int,
                                   window: int = 0) -> int:
     """Floats of workspace the _ws prefill launches need for this shape (0: none)."""

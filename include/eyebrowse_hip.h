@@ -225,6 +225,16 @@ eb_status eb_launch_attn_prefill_fast(void *stream, const float *q, size_t q_num
                                       const float *k, size_t k_numel, const float *v,
                                       size_t v_numel, float *o, size_t o_numel, size_t h,
                                       size_t hkv, size_t s, size_t hd, float scale);
+/* The f16 mode with a workspace: at head_dim <= 128 with at least 3 query blocks sharing
+ * the keys, a pre-convert pass rounds every key to f16 once into records that the
+ * attention kernel only copies into LDS (same bits as without; eb_attn_prefill_fast uses
+ * the device's workspace). Floats needed (0: none used); no initialisation. */
+size_t eb_attn_prefill_fast_workspace_floats(size_t h, size_t hkv, size_t hd, size_t s);
+eb_status eb_launch_attn_prefill_fast_ws(void *stream, const float *q, size_t q_numel,
+                                         const float *k, size_t k_numel, const float *v,
+                                         size_t v_numel, float *o, size_t o_numel, size_t h,
+                                         size_t hkv, size_t s, size_t hd, float scale,
+                                         float *workspace, size_t workspace_floats);
 eb_status eb_launch_attn_prefill_chunk(void *stream, const float *q, size_t q_numel,
                                        const float *kc, size_t kc_numel, const float *vc,
                                        size_t vc_numel, float *o, size_t o_numel, size_t h,

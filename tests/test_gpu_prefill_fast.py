@@ -93,6 +93,36 @@ def test_raw_launch_matches_recorder(dev):
     np.testing.assert_array_equal(ot.to_f32().reshape(T, H, hd), a)
 
 
+@pytest.mark.parametrize("h,hkv,T,hd", [(16, 8, 700, 128), (32, 8, 300, 128), (8, 8, 500, 64),
+                                        (8, 2, 400, 80)])
+def test_preconvert_records_give_the_same_bits(dev, h, hkv, T, hd):
+    """With a workspace the f16 mode rounds each key once (pre-convert pass) and copies the
+    records; without one every workgroup converts what it stages. Same LDS contents, so the
+    same bits; both against the oracle."""
+    note(f"fast prefill records h={h} hkv={hkv} T={T} hd={hd}")
+    sc = float(oracle.default_scale(hd))
+    q, k, v = oracle.randn((T, h, hd), 7), oracle.randn((T, hkv, hd), 8), oracle.randn((T, hkv, hd), 9)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    o1 = eb.Tensor.empty(dev, (T, h, hd))
+    o2 = eb.Tensor.empty(dev, (T, h, hd))
+    need = eb.attn_prefill_fast_workspace_floats(h, hkv, hd, T)
+    assert need > 0
+    ws = eb.Tensor.empty(dev, (need,))
+    ws.write(np.full(need, np.nan, np.float32).tobytes())  # no read before a write
+    args = (dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(), vt.data_ptr,
+            vt.numel())
+    eb.launch_attn_prefill_fast(*args, o1.data_ptr, o1.numel(), h, hkv, T, hd, sc)
+    eb.launch_attn_prefill_fast_ws(*args, o2.data_ptr, o2.numel(), h, hkv, T, hd, sc,
+                                   ws.data_ptr, need)
+    dev.synchronize()
+    np.testing.assert_array_equal(o2.to_f32(), o1.to_f32())
+    want = oracle.attn_prefill(q, k, v, h, hkv, T, hd, sc, threads=16)
+    check(o2.to_f32().reshape(T, h, hd), want, f"records h={h} T={T}")
+    with pytest.raises(eb.ShapeMismatch):
+        eb.launch_attn_prefill_fast_ws(*args, o2.data_ptr, o2.numel(), h, hkv, T, hd, sc,
+                                       ws.data_ptr, need - 1)
+
+
 def test_refusals(dev):
     """Scales above 1/sqrt(head_dim) (Gemma-4's 1.0: its scores' f16 rounding error exceeds
     the bar, rel-L2 1.35e-3 and max-abs 2.2e-2 in the CPU emulation) and head dims outside
