@@ -656,90 +656,84 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     }
     __syncthreads();
 
-    for (int it = 0; it < nsteps; ++it) {
-        const int buf = it & 1;
-        const int tile = c_lo + it * KSPLIT + ks;
-        const int kb = tile * kTile;
-        // Prefetch the next step (past the last step this re-reads clamped rows; the
-        // buffer written from them is never read).
-        // PS image records go straight into the other buffer, which every wave finished
-        // reading before the last barrier.
+    // The next step's K/V: PS records into registers (or, head_dim 256, straight into the
+    // other buffer, which every wave finished reading before the last barrier); otherwise
+    // K/V rows into registers. Past the last step this re-reads clamped rows (the buffer
+    // written from them is never read).
+    auto prefetch = [&](int it1, int b1) {
         if constexpr (PS && FAST)
             fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
-                             c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
+                             c_lo + it1 * KSPLIT - ps_tlo, ps_nt, tid);
         else if constexpr (PS && C::PS_IMAGE)
-            ps_copy_image<C>(recs, smem, buf ^ 1, c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, wave,
-                             lane);
+            ps_copy_image<C>(recs, smem, b1, c_lo + it1 * KSPLIT - ps_tlo, ps_nt, wave, lane);
         else if constexpr (PS)
             ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
-                            c_lo + (it + 1) * KSPLIT - ps_tlo, ps_nt, tid);
+                            c_lo + it1 * KSPLIT - ps_tlo, ps_nt, tid);
         else
-            prefill_load_step<C, H16>(k, v, rk, rv, (c_lo + (it + 1) * KSPLIT) * kTile, nkeys,
-                                      Hkv, kvh, tid, hdr);
+            prefill_load_step<C, H16>(k, v, rk, rv, (c_lo + it1 * KSPLIT) * kTile, nkeys, Hkv,
+                                      kvh, tid, hdr);
+    };
+    auto stage = [&](int b1) {
+        if constexpr (PS && FAST)
+            fps_store_step<C>(smem, rs, b1, tid);
+        else if constexpr (PS && C::PS_IMAGE)
+            wait_vm_all();
+        else if constexpr (PS)
+            ps_store_step<C>(smem, rs, b1, tid);
+        else
+            prefill_store_step<C, FAST>(smem, rk, rv, b1, tid);
+    };
 
-        if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
-            const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
-            const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS +
-                              (C::SPV ? 0 : ks * kTile * HD);
-            // S^T = K Q^T for this tile: 16 keys x 1 query per lane.
-            floatx16 sacc;
+    if constexpr (C::SPV) {
+        // Per-tile stages on the split f16 operands (head_dim >= 32):
+        //  qk:      S^T = K Q^T for the wave's tile in buffer b (16 keys x 1 query per lane);
+        //  softmax: the online softmax update (m, l, the O^T unit E, the rescale of O^T) and
+        //           the P^T operands;
+        //  pv:      O^T += V^T P^T from buffer b.
+        auto tile_qk = [&](int b, floatx16 &sacc) {
+            const float *Kb = smem + b * C::BUF + ks * kTile * KS;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
-            const float *kr = Kb + col * KS + HALF * hf;
-            int ek[16];  // SQK: exponent of each of this lane's keys
-            if constexpr (C::SQK) {
-                // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
-                const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KS);
+            // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
+            const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KS);
 #pragma unroll
-                for (int k2 = 0; k2 < NKS; ++k2) {
-                    const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
-                    sacc = mfma16(ah, qh[k2], sacc);
-                    if constexpr (!FAST) {
-                        const f16x8 al =
-                            *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
-                        sacc = mfma16(ah, ql[k2], sacc);
-                        sacc = mfma16(al, qh[k2], sacc);
-                    }
+            for (int k2 = 0; k2 < NKS; ++k2) {
+                const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
+                sacc = mfma16(ah, qh[k2], sacc);
+                if constexpr (!FAST) {
+                    const f16x8 al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                    sacc = mfma16(ah, ql[k2], sacc);
+                    sacc = mfma16(al, qh[k2], sacc);
                 }
-                if constexpr (FAST) {
+            }
+        };
+
+        auto tile_softmax = [&](int b, int kb, const floatx16 &sacc, f16x8 (&ph)[2],
+                                f16x8 (&pl)[2]) {
+            // Scores back from the split's units: 2^(eq + ek), ek the exponent of each of this
+            // lane's keys.
+            float p[16];
+            if constexpr (FAST) {
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) ek[r] = 0;
-                } else {
-                const int *Eb = reinterpret_cast<const int *>(smem + buf * C::BUF +
+                for (int r = 0; r < 16; ++r) p[r] = sacc[r];
+            } else {
+                const int *Eb = reinterpret_cast<const int *>(smem + b * C::BUF +
                                                               C::STEP_KEYS * KS + C::VFL) +
                                 ks * kTile;
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4) {
                     const int4 e4 = *reinterpret_cast<const int4 *>(Eb + 8 * s4 + 4 * hf);
-                    ek[4 * s4 + 0] = e4.x;
-                    ek[4 * s4 + 1] = e4.y;
-                    ek[4 * s4 + 2] = e4.z;
-                    ek[4 * s4 + 3] = e4.w;
+                    p[4 * s4 + 0] = ldexpf(sacc[4 * s4 + 0], eq + e4.x);
+                    p[4 * s4 + 1] = ldexpf(sacc[4 * s4 + 1], eq + e4.y);
+                    p[4 * s4 + 2] = ldexpf(sacc[4 * s4 + 2], eq + e4.z);
+                    p[4 * s4 + 3] = ldexpf(sacc[4 * s4 + 3], eq + e4.w);
                 }
-                }
-            } else if constexpr (HALF % 4 == 0) {
-#pragma unroll
-                for (int i = 0; i < HALF / 4; ++i) {
-                    float4 a = *reinterpret_cast<const float4 *>(kr + 4 * i);
-                    sacc = mfma32(a.x, qreg[4 * i + 0], sacc);
-                    sacc = mfma32(a.y, qreg[4 * i + 1], sacc);
-                    sacc = mfma32(a.z, qreg[4 * i + 2], sacc);
-                    sacc = mfma32(a.w, qreg[4 * i + 3], sacc);
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < HALF; ++s) sacc = mfma32(kr[s], qreg[s], sacc);
             }
-
-            // Online softmax over this tile's keys (log2 domain). Only tiles that reach
-            // past the wave's first position, or (window) below its last position's
-            // window, need the per-key mask.
+            // Online softmax over this tile's keys (log2 domain). Only tiles that reach past
+            // the wave's first position, or (window) below its last position's window, need
+            // the per-key mask.
             const bool edge =
                 RANGE ? (kb + kTile - 1 > wp0 || (window > 0 && kb <= wp1 - window)) : kb == q0;
-            float p[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                p[r] = FAST ? sacc[r] : C::SQK ? ldexpf(sacc[r], eq + ek[r]) : sacc[r] * scale_log2;
             if (edge) {  // wave-uniform: most tiles skip the per-key mask
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
@@ -751,14 +745,14 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
             for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
             mt = fmaxf(mt, __shfl_xor(mt, 32));
-            // SPV: lazy reference max. m moves only when a score exceeds it by more than
-            // kSlack (log2 units), so most tiles need no rescale of l and O^T; terms
-            // 2^(s - m) then stay below 2^kSlack, which the f16 split holds exactly.
-            const bool grow = C::SPV ? (mt > m + kSlack) : true;
+            // Lazy reference max: m moves only when a score exceeds it by more than kSlack
+            // (log2 units), so most tiles need no rescale of l and O^T; terms 2^(s - m) then
+            // stay below 2^kSlack, which the f16 split holds exactly.
+            const bool grow = mt > m + kSlack;
             const float mnew = grow ? fmaxf(m, mt) : m;
             // A query can meet a tile with all of its keys masked before its first visible
             // key (unaligned chunk starts, windows): keep exp2 away from -inf - -inf.
-            const float mref = ((RANGE || C::SPV) && mnew == -INFINITY) ? 0.0f : mnew;
+            const float mref = mnew == -INFINITY ? 0.0f : mnew;
             const float corr = grow ? eb::fast_exp2(m - mref) : 1.0f;
             float ps = 0.0f;
 #pragma unroll
@@ -779,7 +773,6 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
                         for (int r = 0; r < 16; ++r) oacc[mb][r] *= corr;
                 }
-                f16x8 ph[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     unsigned hw[4];
@@ -790,20 +783,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                             unsigned, __builtin_convertvector(f32x2{p[r], p[r + 1]}, f16x2));
                     }
                     ph[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+                    pl[u] = ph[u];
                 }
-                const _Float16 *vth = reinterpret_cast<const _Float16 *>(Vb);
-#pragma unroll
-                for (int mb = 0; mb < NB; ++mb) {
-                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 8 * hf;
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const f16x8 vh = *reinterpret_cast<const f16x8 *>(vth + roff + 16 * u);
-                        oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
-                    }
-                }
-            } else if constexpr (C::SPV) {
+            } else {
                 // The tile's V exponents ev (V row = 2^ev * v').
-                const int *Ev = reinterpret_cast<const int *>(smem + buf * C::BUF +
+                const int *Ev = reinterpret_cast<const int *>(smem + b * C::BUF +
                                                               C::STEP_KEYS * KS + C::VFL) +
                                 C::STEP_KEYS + ks * kTile;
                 int ev[16];
@@ -847,7 +831,6 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                 }
                 E = En;
                 // P^T operands: k-step u takes this lane's keys r = 8u .. 8u+7.
-                f16x8 ph[2], pl[2];
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     unsigned hw[4], lw[4];
@@ -862,24 +845,105 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     ph[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
                     pl[u] = __builtin_bit_cast(f16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
                 }
-                // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the
-                // output stage expects), stored at V^T row 32*mb + col; keys 16u + 4hf +
-                // 0..3 and 16u + 8 + 4hf + 0..3 of this wave's tile (the order of ph / pl).
-                const _Float16 *vth = reinterpret_cast<const _Float16 *>(Vb);
-                const _Float16 *vtl = vth + HD * C::VROW;
+            }
+        };
+
+        // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the output stage
+        // expects), stored at V^T row 32*mb + col; keys 16u + 4hf + 0..3 and 16u + 8 + 4hf +
+        // 0..3 of this wave's tile (the order of ph / pl). FAST: the hi halves only.
+        auto tile_pv = [&](int b, const f16x8 (&ph)[2], const f16x8 (&pl)[2]) {
+            const _Float16 *vth =
+                reinterpret_cast<const _Float16 *>(smem + b * C::BUF + C::STEP_KEYS * KS);
+            const _Float16 *vtl = vth + HD * C::VROW;
 #pragma unroll
-                for (int mb = 0; mb < NB; ++mb) {
-                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 8 * hf;
+            for (int mb = 0; mb < NB; ++mb) {
+                const int roff = (32 * mb + col) * C::VROW + ks * kTile + 8 * hf;
 #pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const f16x8 vh = *reinterpret_cast<const f16x8 *>(vth + roff + 16 * u);
+                for (int u = 0; u < 2; ++u) {
+                    const f16x8 vh = *reinterpret_cast<const f16x8 *>(vth + roff + 16 * u);
+                    oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
+                    if constexpr (!FAST) {
                         const f16x8 vl = *reinterpret_cast<const f16x8 *>(vtl + roff + 16 * u);
-                        oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
                         oacc[mb] = mfma16(vh, pl[u], oacc[mb]);
                         oacc[mb] = mfma16(vl, ph[u], oacc[mb]);
                     }
                 }
+            }
+        };
+
+        floatx16 sacc;
+        f16x8 ph[2], pl[2];
+        for (int it = 0; it < nsteps; ++it) {
+            const int buf = it & 1;
+            const int tile = c_lo + it * KSPLIT + ks;
+            prefetch(it + 1, buf ^ 1);
+            if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
+                tile_qk(buf, sacc);
+                tile_softmax(buf, tile * kTile, sacc, ph, pl);
+                tile_pv(buf, ph, pl);
+            }
+            stage(buf ^ 1);
+            __syncthreads();
+        }
+    } else {
+    for (int it = 0; it < nsteps; ++it) {
+        const int buf = it & 1;
+        const int tile = c_lo + it * KSPLIT + ks;
+        const int kb = tile * kTile;
+        prefetch(it + 1, buf ^ 1);
+
+        if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
+            const float *Kb = smem + buf * C::BUF + ks * kTile * KS;
+            const float *Vb = smem + buf * C::BUF + C::STEP_KEYS * KS + ks * kTile * HD;
+            // S^T = K Q^T for this tile: 16 keys x 1 query per lane (FP32 MFMA).
+            floatx16 sacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+            const float *kr = Kb + col * KS + HALF * hf;
+            if constexpr (HALF % 4 == 0) {
+#pragma unroll
+                for (int i = 0; i < HALF / 4; ++i) {
+                    float4 a = *reinterpret_cast<const float4 *>(kr + 4 * i);
+                    sacc = mfma32(a.x, qreg[4 * i + 0], sacc);
+                    sacc = mfma32(a.y, qreg[4 * i + 1], sacc);
+                    sacc = mfma32(a.z, qreg[4 * i + 2], sacc);
+                    sacc = mfma32(a.w, qreg[4 * i + 3], sacc);
+                }
             } else {
+#pragma unroll
+                for (int s = 0; s < HALF; ++s) sacc = mfma32(kr[s], qreg[s], sacc);
+            }
+
+            // Online softmax over this tile's keys (log2 domain).
+            const bool edge =
+                RANGE ? (kb + kTile - 1 > wp0 || (window > 0 && kb <= wp1 - window)) : kb == q0;
+            float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = sacc[r] * scale_log2;
+            if (edge) {  // wave-uniform: most tiles skip the per-key mask
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (key > pi || (RANGE && window > 0 && key <= pi - window)) p[r] = -INFINITY;
+                }
+            }
+            float mt = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mnew = fmaxf(m, mt);
+            // A query can meet a tile with all of its keys masked before its first visible
+            // key (unaligned chunk starts, windows): keep exp2 away from -inf - -inf.
+            const float mref = (RANGE && mnew == -INFINITY) ? 0.0f : mnew;
+            const float corr = eb::fast_exp2(m - mref);
+            float ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                p[r] = eb::fast_exp2(p[r] - mref);
+                ps += p[r];
+            }
+            l = l * corr + ps;
+            m = mnew;
 #pragma unroll
             for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
@@ -918,18 +982,11 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     oacc[0] = mfma32(a, p[t], oacc[0]);
                 }
             }
-            }
         }
 
-        if constexpr (PS && FAST)
-            fps_store_step<C>(smem, rs, buf ^ 1, tid);
-        else if constexpr (PS && C::PS_IMAGE)
-            wait_vm_all();
-        else if constexpr (PS)
-            ps_store_step<C>(smem, rs, buf ^ 1, tid);
-        else
-            prefill_store_step<C, FAST>(smem, rk, rv, buf ^ 1, tid);
+        stage(buf ^ 1);
         __syncthreads();
+    }
     }
 
     // Merge the key splits: waves ks >= 1 hand (m, l, O^T) to wave ks = 0 of their slot
