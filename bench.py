@@ -146,11 +146,11 @@ class DecodeWorkload:
     captured in one HIP graph so the host launch cost is paid once per graph."""
 
     def __init__(self, eb, hip, dev, H, Hkv, hd, max_seq, pos, scale, seed=0, per_graph=64,
-                 f16=False):
+                 f16=False, f8=False):
         self.eb, self.hip, self.dev = eb, hip, dev
         self.H, self.Hkv, self.hd, self.max_seq, self.pos, self.scale = H, Hkv, hd, max_seq, pos, scale
-        self.f16 = f16
-        esize = 2 if f16 else 4
+        self.f16, self.f8 = f16, f8
+        esize = 1 if f8 else 2 if f16 else 4
         self.keys = pos + 1
         self.kv_bytes = 2 * self.keys * Hkv * hd * esize
         cache_bytes = 2 * max_seq * Hkv * hd * esize
@@ -162,7 +162,11 @@ class DecodeWorkload:
         for _ in range(self.n_caches):
             pair = []
             for fill in (kfill, vfill):
-                if f16:
+                if f8:
+                    t = eb.Tensor.empty(dev, fill.shape, eb.DType.F8E4M3)
+                    eb.launch_kv_write_f8(dev.stream, t.data_ptr, t.numel(), fill.data_ptr,
+                                          fill.numel(), Hkv, max_seq, hd, max_seq, 0)
+                elif f16:
                     t = eb.Tensor.empty(dev, fill.shape, eb.DType.F16)
                     eb.launch_kv_write_f16(dev.stream, t.data_ptr, t.numel(), fill.data_ptr,
                                            fill.numel(), Hkv, max_seq, hd, max_seq, 0)
@@ -188,8 +192,9 @@ class DecodeWorkload:
 
     def _step(self, cache):
         kc, vc = cache
-        if self.f16:
-            self.eb.launch_attn_decode_step_f16(
+        if self.f16 or self.f8:
+            fn = self.eb.launch_attn_decode_step_f8 if self.f8 else self.eb.launch_attn_decode_step_f16
+            fn(
                 self.dev.stream, self.q.data_ptr, self.q.numel(), self.knew.data_ptr,
                 self.vnew.data_ptr, self.knew.numel(), kc.data_ptr, kc.numel(), vc.data_ptr,
                 vc.numel(), self.o.data_ptr, self.o.numel(), self.H, self.Hkv, self.pos,
@@ -363,11 +368,16 @@ def decode_extras(eb, hip, dev, sc128) -> dict:
             ("mistral_keys8193", 32, 8, 128, 32768, 8192, sc128),
             ("gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0)]
     # IEEE-half caches (no counterpart in the reference): half the bytes per key.
-    cfgs += [("f16_qwen_L8191", 16, 8, 128, 8192, 8191, sc128, True),
-             ("f16_mistral_keys32768", 32, 8, 128, 32768, 32767, sc128, True),
-             ("f16_gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0, True)]
-    for name, H, Hkv, hd, ms, pos, sc, *f16 in cfgs:
-        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc, f16=bool(f16))
+    cfgs += [("f16_qwen_L8191", 16, 8, 128, 8192, 8191, sc128, "f16"),
+             ("f16_mistral_keys32768", 32, 8, 128, 32768, 32767, sc128, "f16"),
+             ("f16_gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0, "f16")]
+    # OCP FP8 E4M3 caches (no counterpart in the reference): a quarter of the f32 bytes.
+    cfgs += [("f8_qwen_L8191", 16, 8, 128, 8192, 8191, sc128, "f8"),
+             ("f8_mistral_keys32768", 32, 8, 128, 32768, 32767, sc128, "f8"),
+             ("f8_gemma_keys16384", 16, 8, 256, 16384, 16383, 1.0, "f8")]
+    for name, H, Hkv, hd, ms, pos, sc, *el in cfgs:
+        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc, f16=el == ["f16"],
+                           f8=el == ["f8"])
         w.run_steps(20)
         t_step, _ = w.run_steps(500)
         out[f"decode_{name}"] = {
@@ -764,15 +774,17 @@ def trace_workload(eb, hip, dev, sc128, name: str) -> None:
     decode = {"decode_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, False),
               "decode_gemma_keys16384": (16, 8, 256, 16384, 16383, 1.0, False),
               "decode_qwen_L8191": (16, 8, 128, 8192, 8191, sc128, False),
-              "decode_f16_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, True)}
+              "decode_f16_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, True),
+              "decode_f8_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, "f8")}
     prefill = {"prefill_qwen_T512": (16, 8, 128, 512, sc128),
                "prefill_qwen_T2048": (16, 8, 128, 2048, sc128),
                "prefill_qwen_T4096": (16, 8, 128, 4096, sc128),
                "prefill_mistral_T4096": (32, 8, 128, 4096, sc128),
                "prefill_gemma_T4096": (16, 8, 256, 4096, 1.0)}
     if name in decode:
-        H, Hkv, hd, ms, pos, sc, f16 = decode[name]
-        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc, f16=f16)
+        H, Hkv, hd, ms, pos, sc, el = decode[name]
+        w = DecodeWorkload(eb, hip, dev, H, Hkv, hd, ms, pos, sc, f16=el is True,
+                           f8=el == "f8")
         w.run_exact(200)
         dev.synchronize()
         w.close()

@@ -7,7 +7,7 @@ reference's Rust interface:
 - ``gpu``: DType, EyebrowseError, Device, Tensor, Recorder (crates/eyebrowse-gpu);
 - ``kernels``: attn_prefill, attn_decode, kv_write, rmsnorm, rope (crates/eyebrowse-kernels),
   linear_f16w (the projections around attention), plus chunked / windowed attention, the
-  fused decode step and IEEE-half caches;
+  fused decode step and IEEE-half and OCP FP8 E4M3 caches;
 - ``nn``: Linear, Rope, KvCache, Attention (crates/eyebrowse-nn).
 """
 from ._lib import LIB_PATH, lib
@@ -25,6 +25,8 @@ from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_
                       launch_attn_prefill_chunk_f16, launch_attn_prefill_chunk_ws,
                       launch_attn_prefill_ws, launch_kv_write, launch_kv_write_f16,
                       launch_attn_prologue, launch_attn_decode_step_noalloc,
+                      launch_kv_write_f8, launch_attn_prefill_chunk_f8, launch_attn_decode_f8,
+                      launch_attn_decode_step_f8,
                       attn_decode_noalloc_max_floats, launch_linear_f16w, launch_rmsnorm, launch_rope, linear_f16w,
                       linear_f16w_multi, linear_workspace_floats, rmsnorm, rope)
 from .nn import Attention, KvCache, Linear, Rope
@@ -41,7 +43,8 @@ __all__ = [
     "launch_attn_decode_step_f16", "launch_attn_decode_window", "launch_attn_prefill",
     "launch_attn_prefill_chunk", "launch_attn_prefill_chunk_f16", "launch_attn_prefill_chunk_ws",
     "launch_attn_prefill_ws", "attn_prefill_workspace_floats", "launch_kv_write",
-    "launch_kv_write_f16", "launch_linear_f16w", "linear_f16w", "linear_f16w_multi",
+    "launch_kv_write_f16", "launch_kv_write_f8", "launch_attn_prefill_chunk_f8",
+    "launch_attn_decode_f8", "launch_attn_decode_step_f8", "launch_linear_f16w", "linear_f16w", "linear_f16w_multi",
     "linear_workspace_floats", "launch_rmsnorm",
     "launch_rope", "launch_attn_prologue", "launch_attn_decode_step_noalloc",
     "attn_decode_noalloc_max_floats", "rmsnorm", "rope", "Attention", "KvCache", "Linear", "Rope",

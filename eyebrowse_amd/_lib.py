@@ -148,6 +148,22 @@ SIGNATURES = {
                                               c_size, c_vp, c_size, c_vp, c_size, c_size, c_size,
                                               c_size, c_size, c_size, c_float, c_size, c_vp,
                                               c_size, c_int]),
+    "eb_launch_kv_write_f8": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_size, c_size, c_size,
+                                     c_size, c_size]),
+    "eb_launch_attn_prefill_chunk_f8": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,
+                                               c_vp, c_size, c_size, c_size, c_size, c_size,
+                                               c_size, c_size, c_float, c_size]),
+    "eb_launch_attn_prefill_chunk_f8_ws": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp,
+                                                  c_size, c_vp, c_size, c_size, c_size, c_size,
+                                                  c_size, c_size, c_size, c_float, c_size, c_vp,
+                                                  c_size]),
+    "eb_launch_attn_decode_f8": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
+                                        c_size, c_size, c_size, c_size, c_size, c_size, c_float,
+                                        c_size, c_vp, c_size, c_int]),
+    "eb_launch_attn_decode_step_f8": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp,
+                                             c_size, c_vp, c_size, c_vp, c_size, c_size, c_size,
+                                             c_size, c_size, c_size, c_float, c_size, c_vp,
+                                             c_size, c_int]),
     "eb_launch_rmsnorm": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_size,
                                  c_size, c_float]),
     "eb_launch_rope": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size, c_size,

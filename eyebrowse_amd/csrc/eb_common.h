@@ -98,4 +98,39 @@ __device__ __forceinline__ float class_reduce(float x) {
 // 2^x on the hardware transcendental unit (v_exp_f32); exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- OCP FP8 E4M3 ("e4m3fn": sign, 4 exponent bits with bias 7, 3 fraction bits, no
+// infinities, S.1111.111 NaN, largest finite 448) -------------------------------------
+
+// The E4M3 pattern (low 8 bits) of x: the nearest value, ties to the even fraction; finite
+// values at or beyond 448 saturate to +-448; inf and NaN become NaN (0x7F with the sign).
+// From the f32 fields: below 2^-6 the value is a count of 2^-9 steps (x * 512 rounded to
+// nearest even, exact scaling; a count of 8 is the smallest normal 2^-6); above, the f32
+// fraction is rounded to 3 bits (adding 2^19 - 1 plus the kept lowest bit, a carry
+// moving the exponent) and the exponent rebased from 127 to 7.
+__device__ __forceinline__ unsigned f8e4m3_bits(float x) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const unsigned s = (u >> 24) & 0x80u;
+    const unsigned a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return s | 0x7Fu;  // inf, NaN
+    if (a >= 0x43E00000u) return s | 0x7Eu;  // 448 and beyond
+    if (a < 0x3C800000u)                      // below 2^-6
+        return s | (unsigned)__builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
+    return s | ((((a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20)) - (120u << 3));
+}
+
+// Four E4M3 values (bytes 0..3 of w, lowest first) as f32, exact (v_cvt_pk_f32_fp8, which
+// reads the OCP E4M3 format on gfx950).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f32x4_t f8x4_to_f32(unsigned w) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    return f32x4_t{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// Four f32 values as E4M3 bytes of one word (lowest first).
+__device__ __forceinline__ unsigned f8x4_bits(f32x4_t x) {
+    return f8e4m3_bits(x[0]) | (f8e4m3_bits(x[1]) << 8) | (f8e4m3_bits(x[2]) << 16) |
+           (f8e4m3_bits(x[3]) << 24);
+}
+
 }  // namespace eb

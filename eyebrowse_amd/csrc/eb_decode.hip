@@ -9,12 +9,14 @@
 // Pass 1, grid (Hkv * nsub) x nsplit, 256 threads per workgroup. Workgroup (col, split)
 // reduces a 1/nsplit share of the keys for KV head col % Hkv and the G query heads that
 // share it (GQA: every K/V row is read once for all of them):
-//  - a key row of HD floats is spread over LPK = HD/DPL lanes (DPL = 16 dims per lane; 8 for
-//    f32 head_dim 128 with 4 query heads per workgroup),
+//  - a key row of HD elements (f32, IEEE half or OCP FP8 E4M3, converted to f32 as loaded)
+//    is spread over LPK = HD/DPL lanes (DPL = 16 dims per lane; 8 for f32 head_dim 128
+//    with 4 query heads per workgroup),
 //    so a wave covers KPW = 64/LPK keys per step; the keys are dealt to the splits in
 //    blocks of KPW rows (split s owns blocks s, s + nsplit, ...), so that all workgroups
 //    together stream one contiguous stretch of the cache at a time;
-//  - loads are 128-bit raw buffer loads whose range check turns rows past the end into
+//  - loads are 128-bit raw buffer loads (64-bit over E4M3 caches, so that a lane holds the
+//    same dims as over f16 ones) whose range check turns rows past the end into
 //    zeros (no clamping, no branches); two register buffers per wave keep the next
 //    iteration's loads in flight while the current one is consumed;
 //  - scores are lane-partial dot products summed across the LPK lanes with DPP;
@@ -40,6 +42,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 // Wave steps per iteration (and per softmax update); a positive EB_DECODE_U overrides
 // the default of one.
@@ -51,6 +54,11 @@
 // does twice the f32 arithmetic (v_fma_mix per dim and head), which then dominates.
 #ifndef EB_DECODE_U16
 #define EB_DECODE_U16 1
+#endif
+// Wave steps per iteration over E4M3 caches (a wave step's loads hold half the bytes of
+// an f16 one). Measured at Mistral 32k keys: 1: 28.8 us, 2: 25.3 us, 4: 25.6 us per step.
+#ifndef EB_DECODE_U8
+#define EB_DECODE_U8 2
 #endif
 // Workgroups per CU the register allocation must allow (launch-bounds minimum); 0 picks
 // 2 when at most 2 query heads share a workgroup (then everything fits 256 VGPRs), else 1.
@@ -90,40 +98,71 @@ struct DecodeShape {
                   "head_dim: 4, 8, or a multiple of 16 up to 256");
 };
 
-// Byte offset (within a row) of 16-byte load number j of dim slice `ls` (LPK lanes per row).
-template <int LPK>
+// Bytes per load over a cache of EB-byte elements: 16 (4 f32 or 8 f16 dims), 8 for E4M3
+// (8 dims), so that a lane's loads hold the same dims over f16 and E4M3 caches.
+template <int EB>
+constexpr int load_bytes() { return EB == 1 ? 8 : 16; }
+
+// Byte offset (within a row) of load number j of dim slice `ls` (LPK lanes per row).
+template <int LPK, int EB>
 __device__ __forceinline__ int dim_byte(int j, int ls) {
-    return (j * LPK + ls) * 16;
+    return (j * LPK + ls) * load_bytes<EB>();
 }
 
-// First dim of the lane's f32x4 unit i: a 16-byte load holds 4 dims of an f32 cache row
-// and 8 of an f16 one, so unit i of an f16 lane is half of load i/2.
-template <int LPK, bool H16>
+// First dim of the lane's f32x4 unit i (4 dims): a load holds 4 dims of an f32 cache row
+// and 8 of an f16 or E4M3 one, so unit i of a narrow lane is half of load i/2.
+template <int LPK, int EB>
 __device__ __forceinline__ int dim_of(int i, int ls) {
-    if constexpr (H16)
-        return dim_byte<LPK>(i / 2, ls) / 2 + (i % 2) * 4;
+    if constexpr (EB < 4)
+        return (i / 2 * LPK + ls) * 8 + (i % 2) * 4;
     else
-        return dim_byte<LPK>(i, ls) / 4;
+        return dim_byte<LPK, EB>(i, ls) / 4;
 }
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-// Unit i (4 dims, as f32) of a lane's raw 16-byte loads of one row.
-template <bool H16>
-__device__ __forceinline__ f32x4 unit_f32(const f32x4 *raw, int i) {
-    if constexpr (H16) {
+// A lane's raw load of one row: 16 bytes, 8 for E4M3 caches.
+template <int EB>
+using RawLoad = std::conditional_t<EB == 1, u32x2, f32x4>;
+
+// Unit i (4 dims, as f32) of a lane's raw loads of one row.
+template <int EB>
+__device__ __forceinline__ f32x4 unit_f32(const RawLoad<EB> *raw, int i) {
+    if constexpr (EB == 2) {
         const f16x8 h = __builtin_bit_cast(f16x8, raw[i / 2]);
         return (i % 2) ? f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]}
                        : f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    } else if constexpr (EB == 1) {
+        return eb::f8x4_to_f32(raw[i / 2][i % 2]);
     } else {
         return raw[i];
     }
 }
 
-// f32 -> IEEE half -> f32: the value an f16 cache holds for x (round to nearest even).
-__device__ __forceinline__ f32x4 through_f16(f32x4 x) {
-    return __builtin_convertvector(__builtin_convertvector(x, f16x4), f32x4);
+// The value a cache of EB-byte elements holds for x: f32 -> IEEE half -> f32 (nearest
+// even), or f32 -> E4M3 -> f32 (nearest even, saturating).
+template <int EB>
+__device__ __forceinline__ f32x4 through_cache(f32x4 x) {
+    if constexpr (EB == 2)
+        return __builtin_convertvector(__builtin_convertvector(x, f16x4), f32x4);
+    else if constexpr (EB == 1)
+        return eb::f8x4_to_f32(eb::f8x4_bits(x));
+    else
+        return x;
+}
+
+// Stores 4 dims (f32) of a cache row at element offset off, in the cache's element type.
+template <int EB>
+__device__ __forceinline__ void store_cache4(void *base, size_t off, f32x4 x) {
+    if constexpr (EB == 2)
+        *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(base) + off) =
+            __builtin_convertvector(x, f16x4);
+    else if constexpr (EB == 1)
+        *reinterpret_cast<unsigned *>(static_cast<uint8_t *>(base) + off) = eb::f8x4_bits(x);
+    else
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(base) + off) = x;
 }
 
 // Raw buffer resource over [p, p + nbytes). The operands are made wave-uniform explicitly
@@ -141,6 +180,17 @@ __device__ __forceinline__ f32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int vof
                                                int soffset = 0) {
     return __builtin_bit_cast(f32x4,
                               __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
+// One raw load of a row slice: 16 bytes, or 8 over E4M3 caches.
+template <int EB>
+__device__ __forceinline__ RawLoad<EB> buffer_load_row(__amdgpu_buffer_rsrc_t r, int voffset,
+                                                       int soffset) {
+    if constexpr (EB == 1)
+        return __builtin_bit_cast(u32x2,
+                                  __builtin_amdgcn_raw_buffer_load_b64(r, voffset, soffset, 0));
+    else
+        return buffer_load16(r, voffset, soffset);
 }
 
 struct DecodeArgs {
@@ -171,7 +221,7 @@ struct DecodeArgs {
 // kernels/src/rmsnorm.rs:6-38): y = x * (1/sqrt(sum x^2 / HD + eps)) * w.
 // LPK lanes hold the row's dims, LPK2 (a power of two) lanes form its group; lanes
 // ls >= LPK hold zeros and keep them.
-template <int HD, bool H16, int NV4, int LPK, int LPK2>
+template <int HD, int EB, int NV4, int LPK, int LPK2>
 __device__ __forceinline__ void norm_units(f32x4 (&u)[NV4], const float *__restrict__ w,
                                            float eps, int ls) {
     float ss = 0.0f;
@@ -183,14 +233,14 @@ __device__ __forceinline__ void norm_units(f32x4 (&u)[NV4], const float *__restr
     if (LPK == LPK2 || ls < LPK) {
 #pragma unroll
         for (int i = 0; i < NV4; ++i)
-            u[i] = u[i] * inv * *reinterpret_cast<const f32x4 *>(w + dim_of<LPK, H16>(i, ls));
+            u[i] = u[i] * inv * *reinterpret_cast<const f32x4 *>(w + dim_of<LPK, EB>(i, ls));
     }
 }
 
 // RoPE of one head (kernels/src/rope.rs:6-32): dims p and p + HD/2 rotate by the table
 // row's angle p. In the lane layout, unit i + NV4/2 holds the partners of unit i's dims
 // (both cache layouts), so each lane rotates its own units.
-template <int HD, bool H16, int NV4, int LPK>
+template <int HD, int EB, int NV4, int LPK>
 __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restrict__ cs,
                                            const float *__restrict__ sn, int ls) {
     if constexpr (NV4 == 1) {  // HD 4: pairs (0, 2) and (1, 3) inside the unit
@@ -201,7 +251,7 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
     } else {
 #pragma unroll
         for (int i = 0; i < NV4 / 2; ++i) {
-            const int d = dim_of<LPK, H16>(i, ls);
+            const int d = dim_of<LPK, EB>(i, ls);
             const f32x4 c = *reinterpret_cast<const f32x4 *>(cs + d);
             const f32x4 sv = *reinterpret_cast<const f32x4 *>(sn + d);
             const f32x4 x1 = u[i], x2 = u[i + NV4 / 2];
@@ -211,7 +261,6 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
     }
 }
 
-// H16: the caches hold IEEE half elements (converted to f32 as they are loaded).
 // Two wave steps per iteration for f32 head_dim 256 (4 rows per wave step there): measured
 // +4 % at 16k keys; head_dim 128 measured slower with two (its query heads per workgroup
 // then fill the register file).
@@ -221,18 +270,24 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
 // at 8 they take half (160 VGPRs, none spilled). Measured at 32k keys: 5.48 -> 5.77 TB/s;
 // more wave steps per iteration on the freed registers measured slower (2: 5.40, 3: 5.35,
 // 4: 5.26 TB/s), and so did 8 dims per lane for 2 heads per workgroup.
-template <int HD, int G, bool H16>
-using DecodeShapeOf = DecodeShape<HD, G, H16 ? EB_DECODE_U16 : (HD == 256 ? 2 : 1),
-                                  (!H16 && HD == 128 && G == 4) ? 8 : 16>;
+template <int HD, int G, int EB>
+using DecodeShapeOf = DecodeShape<HD, G,
+                                  EB == 2 ? EB_DECODE_U16 : EB == 1 ? EB_DECODE_U8
+                                                                    : (HD == 256 ? 2 : 1),
+                                  (EB == 4 && HD == 128 && G == 4) ? 8 : 16>;
 
-template <int HD, int G, bool H16>
+// EB: bytes per cache element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
+// as loaded. A narrow lane's loads hold 8 dims each (16 bytes of halves, 8 of E4M3), in the
+// same dim layout for both.
+template <int HD, int G, int EB>
 __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G <= 2 ? 2 : 1))) void decode_kernel(DecodeArgs a) {
-    using S = DecodeShapeOf<HD, G, H16>;
+    using S = DecodeShapeOf<HD, G, EB>;
+    using Raw = RawLoad<EB>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
-    constexpr int EB = H16 ? 2 : 4;           // bytes per cache element
-    constexpr int NL = H16 ? NV4 / 2 : NV4;   // 16-byte loads per lane per row
-    static_assert(!H16 || NV4 % 2 == 0, "f16 caches need head_dim >= 8");
+    constexpr int LB = load_bytes<EB>();
+    constexpr int NL = EB < 4 ? NV4 / 2 : NV4;  // loads per lane per row
+    static_assert(EB == 4 || NV4 % 2 == 0, "f16 and e4m3 caches need head_dim >= 8");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     // Column col = sub * hkv + kvh: workgroup ids that differ by a multiple of hkv share a
@@ -268,15 +323,8 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
             const f32x4 kx = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
             const f32x4 vx = *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
-            if constexpr (H16) {
-                *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.kc_w) + dst + 4 * i) =
-                    __builtin_convertvector(kx, f16x4);
-                *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.vc_w) + dst + 4 * i) =
-                    __builtin_convertvector(vx, f16x4);
-            } else {
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.kc_w) + dst + 4 * i) = kx;
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.vc_w) + dst + 4 * i) = vx;
-            }
+            store_cache4<EB>(a.kc_w, dst + 4 * i, kx);
+            store_cache4<EB>(a.vc_w, dst + 4 * i, vx);
         }
     }
 
@@ -286,7 +334,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 #pragma unroll
         for (int i = 0; i < NV4; ++i)
             qr[gi][i] = dims_on ? *reinterpret_cast<const f32x4 *>(
-                                      a.q + (size_t)(head0 + gi) * HD + dim_of<S::LPK, H16>(i, ls))
+                                      a.q + (size_t)(head0 + gi) * HD + dim_of<S::LPK, EB>(i, ls))
                                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     if (a.prologue) {
@@ -294,8 +342,8 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         const float *sn = a.rsin ? a.rsin + (size_t)a.rope_row * (HD / 2) : nullptr;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
-            if (a.qn_w) norm_units<HD, H16, NV4, S::LPK, S::LPK2>(qr[gi], a.qn_w, a.eps, ls);
-            if (cs && dims_on) rope_units<HD, H16, NV4, S::LPK>(qr[gi], cs, sn, ls);
+            if (a.qn_w) norm_units<HD, EB, NV4, S::LPK, S::LPK2>(qr[gi], a.qn_w, a.eps, ls);
+            if (cs && dims_on) rope_units<HD, EB, NV4, S::LPK>(qr[gi], cs, sn, ls);
         }
     }
 
@@ -321,12 +369,12 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     for (int u = 0; u < U; ++u) {
         rowof[u] = ((u * kWaves + wave) * a.nsplit + split) * S::KPW + kg;  // minus it0
         // (lanes without dims read past every range check: zeros, no memory access)
-        voff[u] = dims_on ? rowof[u] * row_bytes + dim_byte<S::LPK>(0, ls) : 0x7FFF0000;
+        voff[u] = dims_on ? rowof[u] * row_bytes + dim_byte<S::LPK, EB>(0, ls) : 0x7FFF0000;
     }
     const char *kbase = static_cast<const char *>(a.kc) + (size_t)kvh * HD * EB;
     const char *vbase = static_cast<const char *>(a.vc) + (size_t)kvh * HD * EB;
     auto rows_from = [&](int it) { return it * blk_stride * S::KPW; };
-    auto load_iter = [&](int it, f32x4 (&kv)[U][NL], f32x4 (&vv)[U][NL]) {
+    auto load_iter = [&](int it, Raw (&kv)[U][NL], Raw (&vv)[U][NL]) {
         const int r0 = rows_from(it);
         const int left = min(ce - r0, blk_stride * S::KPW);  // rows in range, window-capped
         const int nbytes = left > 0 ? (left - 1) * row_bytes + HD * EB : 0;
@@ -341,13 +389,13 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
                 // per-lane values (a hoisted per-load address would cost a VGPR each).
                 // Range checks decide by row either way, since a row's dims end within
                 // its HD*EB bytes.
-                kv[u][j] = buffer_load16(kres, voff[u], j * S::LPK * 16);
-                vv[u][j] = buffer_load16(vres, voff[u], j * S::LPK * 16);
+                kv[u][j] = buffer_load_row<EB>(kres, voff[u], j * S::LPK * LB);
+                vv[u][j] = buffer_load_row<EB>(vres, voff[u], j * S::LPK * LB);
             }
     };
     // Online-softmax update of every head with the U rows of one iteration (rows at or
     // past `ce` are masked out).
-    auto consume_iter = [&](int it, const f32x4 (&kv)[U][NL], const f32x4 (&vv)[U][NL]) {
+    auto consume_iter = [&](int it, const Raw (&kv)[U][NL], const Raw (&vv)[U][NL]) {
         const int r0 = rows_from(it);
         // Scores of every head first (their DPP chains interleave).
         float sc[G][U];
@@ -355,9 +403,9 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                f32x4 t = qr[gi][0] * unit_f32<H16>(kv[u], 0);
+                f32x4 t = qr[gi][0] * unit_f32<EB>(kv[u], 0);
 #pragma unroll
-                for (int i = 1; i < NV4; ++i) t += qr[gi][i] * unit_f32<H16>(kv[u], i);
+                for (int i = 1; i < NV4; ++i) t += qr[gi][i] * unit_f32<EB>(kv[u], i);
                 float sv = (t.x + t.y) + (t.z + t.w);
                 sv = eb::group_sum<S::LPK2>(sv);
                 sc[gi][u] = (r0 + rowof[u] < ce) ? sv * a.scale_log2 : -INFINITY;
@@ -403,7 +451,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             for (int i = 0; i < NV4; ++i) {
                 f32x4 t = acc[gi][i];
 #pragma unroll
-                for (int u = 0; u < U; ++u) t += p[u] * unit_f32<H16>(vv[u], i);
+                for (int u = 0; u < U; ++u) t += p[u] * unit_f32<EB>(vv[u], i);
                 acc[gi][i] = t;
             }
         }
@@ -416,7 +464,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     const int n_iter = (my_blk + U * kWaves - 1) / (U * kWaves);
     const int n_pairs = (n_iter + 1) / 2;
     if (n_pairs > 0) {
-        f32x4 kA[U][NL], vA[U][NL], kB[U][NL], vB[U][NL];
+        Raw kA[U][NL], vA[U][NL], kB[U][NL], vB[U][NL];
         load_iter(0, kA, vA);
         load_iter(1, kB, vB);
         for (int pr = 1; pr < n_pairs; ++pr) {
@@ -439,40 +487,33 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
         for (int i = 0; i < NV4; ++i) {
             const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
             kn[i] = dims_on ? *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD +
-                                                               dim_of<S::LPK, H16>(i, ls))
+                                                               dim_of<S::LPK, EB>(i, ls))
                             : z;
             vn[i] = dims_on ? *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD +
-                                                               dim_of<S::LPK, H16>(i, ls))
+                                                               dim_of<S::LPK, EB>(i, ls))
                             : z;
         }
         if (a.prologue) {
-            if (a.kn_w) norm_units<HD, H16, NV4, S::LPK, S::LPK2>(kn, a.kn_w, a.eps, ls);
-            if (a.vn_w) norm_units<HD, H16, NV4, S::LPK, S::LPK2>(vn, a.vn_w, a.eps, ls);
+            if (a.kn_w) norm_units<HD, EB, NV4, S::LPK, S::LPK2>(kn, a.kn_w, a.eps, ls);
+            if (a.vn_w) norm_units<HD, EB, NV4, S::LPK, S::LPK2>(vn, a.vn_w, a.eps, ls);
             if (a.rcos && dims_on)
-                rope_units<HD, H16, NV4, S::LPK>(kn, a.rcos + (size_t)a.rope_row * (HD / 2),
+                rope_units<HD, EB, NV4, S::LPK>(kn, a.rcos + (size_t)a.rope_row * (HD / 2),
                                          a.rsin + (size_t)a.rope_row * (HD / 2), ls);
             if (sub == 0 && kg == 0 && dims_on) {  // the new cache row, one lane group
                 const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
 #pragma unroll
                 for (int i = 0; i < NV4; ++i) {
-                    const int d = dim_of<S::LPK, H16>(i, ls);
-                    if constexpr (H16) {
-                        *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.kc_w) + dst + d) =
-                            __builtin_convertvector(kn[i], f16x4);
-                        *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(a.vc_w) + dst + d) =
-                            __builtin_convertvector(vn[i], f16x4);
-                    } else {
-                        *reinterpret_cast<f32x4 *>(static_cast<float *>(a.kc_w) + dst + d) = kn[i];
-                        *reinterpret_cast<f32x4 *>(static_cast<float *>(a.vc_w) + dst + d) = vn[i];
-                    }
+                    const int d = dim_of<S::LPK, EB>(i, ls);
+                    store_cache4<EB>(a.kc_w, dst + d, kn[i]);
+                    store_cache4<EB>(a.vc_w, dst + d, vn[i]);
                 }
             }
         }
-        if constexpr (H16) {  // the value the cache row now holds
+        if constexpr (EB < 4) {  // the value the cache row now holds
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
-                kn[i] = through_f16(kn[i]);
-                vn[i] = through_f16(vn[i]);
+                kn[i] = through_cache<EB>(kn[i]);
+                vn[i] = through_cache<EB>(vn[i]);
             }
         }
 #pragma unroll
@@ -535,7 +576,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             for (int k = 0; k < 4; ++k)  // even rows: v2[k] summed; odd rows: v2[k + 4]
                 out[k] = eb::row_class_reduce<S::LPK2, false>(eb::swap_sum16(v2[k], v2[k + 4]));
             if ((lane & 15) < S::LPK)
-                *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, H16>((lane >> 4) & 3, ls)) = out;
+                *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, EB>((lane >> 4) & 3, ls)) = out;
         } else {
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
@@ -546,7 +587,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
                 out.z = eb::class_reduce<S::LPK2, false>(t.z);
                 out.w = eb::class_reduce<S::LPK2, false>(t.w);
                 if (kg == 0 && dims_on)
-                    *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, H16>(i, ls)) = out;
+                    *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, EB>(i, ls)) = out;
             }
         }
     }
@@ -667,29 +708,31 @@ struct DecodePlan {
     int nsplit = 1;  // splits along the key axis
 };
 
-template <int G, bool H16>
+template <int G, int EB>
 int keys_per_iter_g(size_t hd) {
 #define EB_KPI(D) \
-    case D: return DecodeShapeOf<D, G, H16>::KEYS_PER_ITER;
+    case D: return DecodeShapeOf<D, G, EB>::KEYS_PER_ITER;
     switch (hd) {
         EB_HEAD_DIMS(EB_KPI)
-        default: return DecodeShapeOf<256, G, H16>::KEYS_PER_ITER;
+        default: return DecodeShapeOf<256, G, EB>::KEYS_PER_ITER;
     }
 #undef EB_KPI
 }
 
-int keys_per_iter(size_t hd, int G, bool h16) {
-    if (h16) {
-        switch (G) {
-            case 4: return keys_per_iter_g<4, true>(hd);
-            case 2: return keys_per_iter_g<2, true>(hd);
-            default: return keys_per_iter_g<1, true>(hd);
-        }
-    }
+template <int EB>
+int keys_per_iter_e(size_t hd, int G) {
     switch (G) {
-        case 4: return keys_per_iter_g<4, false>(hd);
-        case 2: return keys_per_iter_g<2, false>(hd);
-        default: return keys_per_iter_g<1, false>(hd);
+        case 4: return keys_per_iter_g<4, EB>(hd);
+        case 2: return keys_per_iter_g<2, EB>(hd);
+        default: return keys_per_iter_g<1, EB>(hd);
+    }
+}
+
+int keys_per_iter(size_t hd, int G, eb::CacheElem ce) {
+    switch (ce) {
+        case eb::CacheElem::F16: return keys_per_iter_e<2>(hd, G);
+        case eb::CacheElem::E4M3: return keys_per_iter_e<1>(hd, G);
+        default: return keys_per_iter_e<4>(hd, G);
     }
 }
 
@@ -703,7 +746,8 @@ int wgs_per_cu() {
     return v;
 }
 
-DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count, bool h16) {
+DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
+                       eb::CacheElem ce) {
     DecodePlan p;
     const size_t g = h / hkv;
     // At most 4 query heads per workgroup: their q fragments and accumulators, plus two
@@ -712,7 +756,7 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     p.nsub = (int)(g / p.G);
     const size_t keys = pos + 1;
     const size_t cols = hkv * (size_t)p.nsub;
-    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G, h16);
+    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G, ce);
     // Enough workgroups to cover the CUs, but at least one pair of iterations per split.
     const size_t target = (size_t)cu_count * (size_t)wgs_per_cu();
     size_t nsplit = std::max<size_t>(1, target / cols);
@@ -726,30 +770,30 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     return p;
 }
 
-template <int HD, int G, bool H16>
+template <int HD, int G, int EB>
 hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
-    using S = DecodeShapeOf<HD, G, H16>;
+    using S = DecodeShapeOf<HD, G, EB>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;
     if (S::LDS_BYTES > 64 * 1024)
         std::call_once(once, [&] {
             attr_err = hipFuncSetAttribute(
-                reinterpret_cast<const void *>(&decode_kernel<HD, G, H16>),
+                reinterpret_cast<const void *>(&decode_kernel<HD, G, EB>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS_BYTES);
         });
     if (attr_err != hipSuccess) return attr_err;
     dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
-    decode_kernel<HD, G, H16><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
+    decode_kernel<HD, G, EB><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
     return hipSuccess;
 }
 
-template <int HD, bool H16>
+template <int HD, int EB>
 hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     hipError_t e;
     switch (p.G) {
-        case 4: e = launch_g<HD, 4, H16>(st, p, a); break;
-        case 2: e = launch_g<HD, 2, H16>(st, p, a); break;
-        default: e = launch_g<HD, 1, H16>(st, p, a); break;
+        case 4: e = launch_g<HD, 4, EB>(st, p, a); break;
+        case 2: e = launch_g<HD, 2, EB>(st, p, a); break;
+        default: e = launch_g<HD, 1, EB>(st, p, a); break;
     }
     if (e != hipSuccess) return e;
     if (p.nsplit > 1) {
@@ -761,15 +805,15 @@ hipError_t launch_hd(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     return hipSuccess;
 }
 
-template <bool H16>
+template <int EB>
 hipError_t launch_elem(hipStream_t st, size_t hd, const DecodePlan &p, const DecodeArgs &a) {
     if (hd == 4) {
-        if constexpr (!H16) return launch_hd<4, false>(st, p, a);  // f32 caches only
+        if constexpr (EB == 4) return launch_hd<4, 4>(st, p, a);  // f32 caches only
         return hipErrorInvalidValue;
     }
 #define EB_LAUNCH_HD(D) \
     case D:             \
-        if constexpr (D != 4) return launch_hd<D, H16>(st, p, a);
+        if constexpr (D != 4) return launch_hd<D, EB>(st, p, a);
     switch (hd) {
         EB_HEAD_DIMS(EB_LAUNCH_HD)
         default: return hipErrorInvalidValue;
@@ -784,36 +828,39 @@ namespace eb {
 
 // Workspace layout (floats): part_acc [nsplit*h*hd] | part_ml [nsplit*h*2]. Every split
 // writes its whole partial before the merge reads it, so no initialisation is needed.
-// The figure is the cache type's own plan: the f32 and IEEE-half plans hold different
-// rows per iteration, and the half plan can take more splits (head_dim 256), so sizes
-// handed to callers come from decode_workspace_floats_any, the larger of the two.
+// The figure is the cache type's own plan: the f32, IEEE-half and E4M3 plans hold
+// different rows per iteration, and the narrow plans can take more splits (head_dim 256),
+// so sizes handed to callers come from decode_workspace_floats_any, the largest.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
-                               bool h16) {
-    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, h16);
+                               CacheElem ce) {
+    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, ce);
     if (p.nsplit <= 1) return 0;
     return (size_t)p.nsplit * h * (hd + 2);
 }
 
 size_t decode_workspace_floats_any(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count) {
-    const size_t a = decode_workspace_floats(h, hkv, pos, hd, cu_count, false);
-    const size_t b = hd >= 8 ? decode_workspace_floats(h, hkv, pos, hd, cu_count, true) : 0;
-    return a > b ? a : b;
+    size_t n = decode_workspace_floats(h, hkv, pos, hd, cu_count, CacheElem::F32);
+    if (hd >= 8) {
+        n = std::max(n, decode_workspace_floats(h, hkv, pos, hd, cu_count, CacheElem::F16));
+        n = std::max(n, decode_workspace_floats(h, hkv, pos, hd, cu_count, CacheElem::E4M3));
+    }
+    return n;
 }
 
 eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc, const void *vc,
                                  void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                  float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                                  float scale, float *ws, size_t ws_floats, int cu_count,
-                                 size_t window, bool h16, const DecodePrologue *pro) {
-    if (h16 && hd < 8)
-        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
+                                 size_t window, CacheElem ce, const DecodePrologue *pro) {
+    if (ce != CacheElem::F32 && hd < 8)
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 and e4m3 caches need head_dim >= 8");
     if (pro && !knew) return fail(EB_OTHER, "attn_decode: the prologue needs the new rows");
     const size_t rope_row = pos;  // absolute position, before any window shift
     // A window is a shift of the cache view: keys first..=pos become keys 0..=pos-first of
     // caches based at row `first` (the fused write then lands on the same absolute row).
     if (window > 0 && pos + 1 > window) {
         const size_t first = pos + 1 - window;
-        const size_t shift = first * hkv * hd * (h16 ? 2 : 4);  // bytes
+        const size_t shift = first * hkv * hd * (size_t)ce;  // bytes
         kc = static_cast<const char *>(kc) + shift;
         vc = static_cast<const char *>(vc) + shift;
         if (kc_w) kc_w = static_cast<char *>(kc_w) + shift;
@@ -826,8 +873,8 @@ eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc,
          reinterpret_cast<uintptr_t>(ws)) & 15)
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_decode: q/caches/new rows/o/workspace must be 16-byte aligned");
-    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, h16);
-    const size_t need = decode_workspace_floats(h, hkv, pos, hd, cu_count, h16);
+    DecodePlan p = plan_decode(h, hkv, pos, hd, cu_count, ce);
+    const size_t need = decode_workspace_floats(h, hkv, pos, hd, cu_count, ce);
     if (need > 0 && (ws == nullptr || ws_floats < need))
         return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace too small");
     DecodeArgs a{};
@@ -869,7 +916,9 @@ eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc,
     }
     if (!attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);
-    const hipError_t e = h16 ? launch_elem<true>(st, hd, p, a) : launch_elem<false>(st, hd, p, a);
+    const hipError_t e = ce == CacheElem::F16    ? launch_elem<2>(st, hd, p, a)
+                         : ce == CacheElem::E4M3 ? launch_elem<1>(st, hd, p, a)
+                                                 : launch_elem<4>(st, hd, p, a);
     if (e != hipSuccess) return eb::hip_fail(e, "attn_decode launch set-up");
     return check_launch("attn_decode");
 }
@@ -880,7 +929,8 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              float scale, float *ws, size_t ws_floats, int cu_count,
                              size_t window) {
     return launch_attn_decode_any(st, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv, pos, hd,
-                                  scale, ws, ws_floats, cu_count, window, false, nullptr);
+                                  scale, ws, ws_floats, cu_count, window, CacheElem::F32,
+                                  nullptr);
 }
 
 }  // namespace eb

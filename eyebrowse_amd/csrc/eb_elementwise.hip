@@ -1,5 +1,6 @@
 // kv_write and RMSNorm for gfx950: memory-bound steps around attention (RoPE and the
-// per-head pre-attention pass are in eb_rows.hip).
+// per-head pre-attention pass are in eb_rows.hip). kv_write also fills IEEE-half and OCP
+// FP8 E4M3 caches (rounded to nearest even; E4M3 saturating at +-448).
 //
 //  kv_write  (crates/eyebrowse-kernels/src/ops.rs:70-87,150-179): both sides are
 //            seq-major, so the write is one contiguous copy of count*hkv*hd floats to
@@ -39,6 +40,16 @@ __global__ __launch_bounds__(kBlock) void kv_write_f16_kernel(f16x4 *__restrict_
     const size_t stride = (size_t)gridDim.x * kBlock;
     for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride)
         dst[i] = __builtin_convertvector(src[i], f16x4);
+}
+
+// f32 rows into an E4M3 cache (eb::f8e4m3_bits: nearest even, saturating), four elements
+// per thread (16 bytes read, 4 written); n4 = elements / 4.
+__global__ __launch_bounds__(kBlock) void kv_write_f8_kernel(unsigned *__restrict__ dst,
+                                                             const f32x4 *__restrict__ src,
+                                                             size_t n4) {
+    const size_t stride = (size_t)gridDim.x * kBlock;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride)
+        dst[i] = eb::f8x4_bits(src[i]);
 }
 
 unsigned copy_grid(size_t n) {
@@ -96,6 +107,18 @@ eb_status launch_kv_write_f16(hipStream_t st, uint16_t *cache, const float *src,
     kv_write_f16_kernel<<<copy_grid(n4), kBlock, 0, st>>>(
         reinterpret_cast<f16x4 *>(dst), reinterpret_cast<const f32x4 *>(src), n4);
     return check_launch("kv_write_f16");
+}
+
+eb_status launch_kv_write_f8(hipStream_t st, uint8_t *cache, const float *src, size_t hkv,
+                             size_t count, size_t hd, size_t dst_start) {
+    const size_t n = count * hkv * hd;  // hd is a multiple of 4
+    uint8_t *dst = cache + dst_start * hkv * hd;
+    if (((reinterpret_cast<uintptr_t>(dst) & 3) | (reinterpret_cast<uintptr_t>(src) & 15)) != 0)
+        return fail(EB_UNSUPPORTED_CONFIG, "kv_write: e4m3 cache / src must be 4 / 16-byte aligned");
+    const size_t n4 = n / 4;
+    kv_write_f8_kernel<<<copy_grid(n4), kBlock, 0, st>>>(
+        reinterpret_cast<unsigned *>(dst), reinterpret_cast<const f32x4 *>(src), n4);
+    return check_launch("kv_write_f8");
 }
 
 eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *out,

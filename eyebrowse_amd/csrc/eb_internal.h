@@ -49,6 +49,11 @@ eb_device *tensor_device(const eb_tensor *t);
 // Compute units of the current device (cached per ordinal).
 int current_cu_count();
 
+// Element types a KV cache may hold; the value is the element size in bytes. F32 is the
+// reference's; F16 is IEEE half and E4M3 OCP FP8 E4M3 (both rounded to nearest even by
+// kv_write, E4M3 saturating at +-448), converted to f32 as attention loads them.
+enum class CacheElem : int { F32 = 4, F16 = 2, E4M3 = 1 };
+
 // ---- kernel launchers (validated arguments, caller's stream) -------------------------
 eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t hkv,
                           size_t count, size_t hd, size_t dst_start);
@@ -79,8 +84,8 @@ eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float 
                                     size_t window, float *ws = nullptr, size_t ws_floats = 0);
 // Decode workspace: part_acc [nsplit*h*hd] | part_ml [nsplit*h*2], no initialisation.
 size_t decode_workspace_floats(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count,
-                               bool h16 = false);
-// The larger of the f32 and IEEE-half plans' workspaces (the plans split the keys
+                               CacheElem ce = CacheElem::F32);
+// The largest of the f32, IEEE-half and E4M3 plans' workspaces (the plans split the keys
 // differently: their iterations hold different numbers of rows).
 size_t decode_workspace_floats_any(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count);
 // knew/vnew null: plain attention over keys 0..=pos. Otherwise key `pos` comes from
@@ -99,8 +104,6 @@ eb_status decode_step_raw(hipStream_t st, const float *q, size_t q_numel, const 
                           float *vc, size_t vc_numel, float *o, size_t o_numel, size_t h,
                           size_t hkv, size_t pos, size_t hd, size_t max_seq, float scale,
                           float *workspace, size_t workspace_floats, int cu_count);
-// The same over caches of f32 (h16 false) or IEEE half (h16 true) elements; f16 caches
-// need head_dim >= 8.
 // The part of Attention::decode between the projections and the attention, done inside
 // the fused step: per-head RMSNorm of q, knew, vnew (null gains: none) and RoPE of q and
 // knew at the step's absolute position (null tables: none). Gains [hd], tables
@@ -114,16 +117,23 @@ eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc,
                                  void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                  float *o, size_t h, size_t hkv, size_t pos, size_t hd,
                                  float scale, float *ws, size_t ws_floats, int cu_count,
-                                 size_t window, bool h16, const DecodePrologue *pro = nullptr);
+                                 size_t window, CacheElem ce,
+                                 const DecodePrologue *pro = nullptr);
+// (launch_attn_decode_any over caches of element type ce; f16 and E4M3 caches need
+// head_dim >= 8.)
 // kv_write into an IEEE-half cache: src f32 rows rounded to nearest even.
 eb_status launch_kv_write_f16(hipStream_t st, uint16_t *cache, const float *src, size_t hkv,
                               size_t count, size_t hd, size_t dst_start);
-// Chunked prefill over IEEE-half caches (rows converted to f32 as they are staged).
-eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
-                                        const uint16_t *vc, float *o, size_t h, size_t hkv,
-                                        size_t pos0, size_t rows, size_t hd, float scale,
-                                        size_t window, float *ws = nullptr,
-                                        size_t ws_floats = 0);
+// kv_write into an E4M3 cache: src f32 rows to the nearest E4M3 (ties to even), finite
+// values saturating at +-448, inf and NaN to NaN.
+eb_status launch_kv_write_f8(hipStream_t st, uint8_t *cache, const float *src, size_t hkv,
+                             size_t count, size_t hd, size_t dst_start);
+// Chunked prefill over f16 or E4M3 caches (rows converted to f32 as they are staged).
+eb_status launch_attn_prefill_chunk_cache(hipStream_t st, const float *q, const void *kc,
+                                          const void *vc, float *o, size_t h, size_t hkv,
+                                          size_t pos0, size_t rows, size_t hd, float scale,
+                                          size_t window, CacheElem ce, float *ws = nullptr,
+                                          size_t ws_floats = 0);
 // Attention::decode after the projections as one fused step: RMSNorm (null gains: none)
 // and RoPE (null tables: none) of q and the new K row, RMSNorm of the new V row, the
 // cache-row write and the attention. Handle-level, used by eb_attention_forward_qkv.
@@ -166,12 +176,13 @@ eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *
 // even; element counts below 2^31.
 struct RowSeg {
     const float *src;   // [rows, nh, hd] f32
-    void *dst;          // [*, nh, hd], f32 or IEEE half elements
+    void *dst;          // [*, nh, hd], f32, IEEE half or E4M3 elements
     const float *gain;  // [hd] RMSNorm gain, or null: no norm
     int nh;
     int dst_row0;       // destination row of token 0
     bool rope;          // RoPE at table row rope_row0 + token
-    bool half;          // dst holds IEEE half (round to nearest even)
+    int elem;           // bytes per dst element: 4 f32, 2 IEEE half, 1 E4M3 (both
+                        // rounded to nearest even, E4M3 saturating at +-448)
 };
 struct RowsArgs {
     RowSeg seg[3];

@@ -128,8 +128,8 @@ eb_status eb_kv_cache_new_per_layer_dtype(eb_device *dev, const size_t *head_dim
                                           eb_dtype dtype, eb_kv_cache **out) {
     if (!dev || !out || (n_layers > 0 && !head_dims))
         return fail(EB_OTHER, "kv_cache: null argument");
-    if (dtype != EB_F32 && dtype != EB_F16)
-        return fail(EB_UNSUPPORTED_CONFIG, "kv_cache: element type must be f32 or f16");
+    if (dtype != EB_F32 && dtype != EB_F16 && dtype != EB_F8E4M3)
+        return fail(EB_UNSUPPORTED_CONFIG, "kv_cache: element type must be f32, f16 or f8e4m3");
     *out = nullptr;
     auto kv = std::make_unique<eb_kv_cache>();
     kv->max_seq = max_seq;

@@ -143,8 +143,9 @@ struct PrefillCfg {
 // Fetch the K and V rows [kb, kb + STEP_KEYS) of KV head kvh into registers; rows past
 // T read as zero. Every element is assigned on every call (clamped addresses, selected
 // values): conditionally written register arrays end up in scratch memory.
-// H16: k/v hold IEEE half elements, converted to f32 here.
-template <class C, bool H16>
+// EB: bytes per k/v element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
+// here (exactly).
+template <class C, int EB>
 __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
                                                   const void *__restrict__ v,
                                                   f32x4 (&rk)[C::NLD], f32x4 (&rv)[C::NLD],
@@ -161,11 +162,16 @@ __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
         const bool in = key < T && (HD == 4 || c4 * 4 < hdr);
         const size_t off = ((size_t)min(key, T - 1) * Hkv + kvh) * hdr + min(c4 * 4, hdr - 4);
         f32x4 kx, vx;
-        if constexpr (H16) {
+        if constexpr (EB == 2) {
             kx = __builtin_convertvector(
                 *reinterpret_cast<const f16x4 *>(static_cast<const _Float16 *>(k) + off), f32x4);
             vx = __builtin_convertvector(
                 *reinterpret_cast<const f16x4 *>(static_cast<const _Float16 *>(v) + off), f32x4);
+        } else if constexpr (EB == 1) {
+            kx = eb::f8x4_to_f32(
+                *reinterpret_cast<const unsigned *>(static_cast<const uint8_t *>(k) + off));
+            vx = eb::f8x4_to_f32(
+                *reinterpret_cast<const unsigned *>(static_cast<const uint8_t *>(v) + off));
         } else {
             kx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(k) + off);
             vx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(v) + off);
@@ -422,7 +428,7 @@ __global__ __launch_bounds__(256) void preconvert_kernel(const float *__restrict
     const int kvh = blockIdx.y;
     const int tid = threadIdx.x;
     f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C, false>(k, v, rk, rv, t * kTile, nkeys, Hkv, kvh, tid, hdr);
+    prefill_load_step<C, 4>(k, v, rk, rv, t * kTile, nkeys, Hkv, kvh, tid, hdr);
     prefill_store_step<C, true>(smem, rk, rv, 0, tid);
     __syncthreads();
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::FPS_FLOATS);
@@ -434,7 +440,7 @@ __global__ __launch_bounds__(256) void preconvert_kernel(const float *__restrict
 // (rows past nkeys as zeros) exactly as the prefill's own staging does, and writes the
 // tile's record. The prefill then only copies records into LDS: the split is done once
 // per key instead of once per workgroup that reads the key.
-template <int HD, bool H16>
+template <int HD, int EB>
 __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ k,
                                                        const void *__restrict__ v,
                                                        float *__restrict__ ps, int nkeys,
@@ -448,7 +454,7 @@ __global__ __launch_bounds__(256) void presplit_kernel(const void *__restrict__ 
     // (An image record's padding is left as it is: K rows are read within their HD floats,
     // V^T rows within their 32 keys, and the exponents where written.)
     f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C, H16>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
+    prefill_load_step<C, EB>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::PS_FLOATS);
@@ -491,13 +497,14 @@ __device__ __forceinline__ void wait_vm_all() {
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
 // RANGE: queries start at position qbase and may have a sliding window; without it the
 // kernel is specialised to a prompt from position 0 (no window), whose masks are simpler.
-// H16: the K/V rows are IEEE half (an f16 KV cache), converted to f32 as they are staged.
+// EB: bytes per K/V element (4 f32, 2 IEEE half, 1 OCP FP8 E4M3: an f16 or E4M3 KV
+// cache), converted to f32 as they are staged.
 // PS: K/V come as pre-split records (ps: ps_nt records per KV head, record 0 = tile
 // ps_tlo) instead of k/v.
 // FAST (an opt-in mode, f32 K/V without pre-split records): q, K, V and P are rounded to
 // f16 once and each product is one f16 MFMA (instead of three on exact hi/lo splits); the
 // online softmax, its rescaling and the accumulation stay f32.
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS, bool FAST = false>
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false>
 __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                              (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
@@ -651,7 +658,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
         ps_store_step<C>(smem, rs, 0, tid);
     } else {
-        prefill_load_step<C, H16>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
+        prefill_load_step<C, EB>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
         prefill_store_step<C, FAST>(smem, rk, rv, 0, tid);
     }
     __syncthreads();
@@ -670,7 +677,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
             ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
                             c_lo + it1 * KSPLIT - ps_tlo, ps_nt, tid);
         else
-            prefill_load_step<C, H16>(k, v, rk, rv, (c_lo + it1 * KSPLIT) * kTile, nkeys, Hkv,
+            prefill_load_step<C, EB>(k, v, rk, rv, (c_lo + it1 * KSPLIT) * kTile, nkeys, Hkv,
                                       kvh, tid, hdr);
     };
     auto stage = [&](int b1) {
@@ -1172,7 +1179,7 @@ struct PrefillRange {
     int nkeys;   // key rows available in k/v
     int qbase;   // position of query row 0
     int window;  // sliding window (0: none)
-    bool h16;    // k/v hold IEEE half elements
+    eb::CacheElem ce;  // k/v element type
     float *ws;   // workspace (null: no pre-split pass, no key chunks)
     size_t ws_floats;
     int hdr;     // the rows' head dim (at most the instantiation's; the rest reads as zeros)
@@ -1295,7 +1302,7 @@ size_t workspace_floats(size_t hd, int H, int Hkv, const PrefillRange &r) {
     return presplit_floats(hd, H, Hkv, r) + chunk_floats(hd, H, prefill_chunks(hd, H, Hkv, r), r);
 }
 
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, bool H16, bool PS, bool FAST = false>
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false>
 eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
                            const float *ps, float *o, int H, int Hkv, const PrefillRange &r,
                            float scale_log2, const PrefillChunks &ch, float *part_acc,
@@ -1306,7 +1313,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(
             reinterpret_cast<const void *>(
-                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS, FAST>),
+                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
@@ -1314,7 +1321,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const dim3 grid((unsigned)(nqb * ngroups), (unsigned)ch.nchmax);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, H16, PS, FAST><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
         q, k, v, ps, presplit_tlo(r), presplit_nt(r), o, H, Hkv, r.rows, r.nkeys, r.qbase,
         r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml, r.hdr);
     eb_status err = eb::check_launch("attn_prefill");
@@ -1340,28 +1347,35 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
             const int nt = presplit_nt(r);
             float *ps = r.ws;
             const dim3 grid((unsigned)nt, (unsigned)Hkv);
-            if (r.h16)
-                presplit_kernel<HD, true><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
-                                                               presplit_tlo(r), nt, r.hdr);
+            if (r.ce == eb::CacheElem::F16)
+                presplit_kernel<HD, 2><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
+                                                            presplit_tlo(r), nt, r.hdr);
+            else if (r.ce == eb::CacheElem::E4M3)
+                presplit_kernel<HD, 1><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
+                                                            presplit_tlo(r), nt, r.hdr);
             else
-                presplit_kernel<HD, false><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
-                                                                presplit_tlo(r), nt, r.hdr);
+                presplit_kernel<HD, 4><<<grid, 256, 0, st>>>(k, v, ps, r.nkeys, Hkv,
+                                                            presplit_tlo(r), nt, r.hdr);
             const eb_status err = eb::check_launch("attn_prefill (pre-split)");
             if (err != EB_OK) return err;
-            if (plain && !r.h16)
-                return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, true>(
+            // (the records are f16 hi/lo splits whatever the cache's element type)
+            if (plain && r.ce == eb::CacheElem::F32)
+                return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, true>(
                     st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
-            return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false, true>(
+            return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 4, true>(
                 st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
         }
     }
-    if (r.h16)
-        return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, true, false>(
+    if (r.ce == eb::CacheElem::F16)
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 2, false>(
+            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
+    if (r.ce == eb::CacheElem::E4M3)
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 1, false>(
             st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
     if (plain)
-        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, false>(
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, false>(
             st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
-    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, false, false>(
+    return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 4, false>(
         st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
 }
 
@@ -1474,7 +1488,7 @@ eb_status launch_attn_prefill_fast(hipStream_t st, const float *q, const float *
                         "attn_prefill_fast: q/k/v/o/workspace must be 16-byte aligned");
     const size_t need = prefill_fast_workspace_floats(h, hkv, hd, s);
     if (need == 0 || ws_floats < need) ws = nullptr;  // stage f32 K/V in every workgroup
-    const PrefillRange r{(int)s, (int)s, 0, 0, false, ws, ws_floats, (int)hd};
+    const PrefillRange r{(int)s, (int)s, 0, 0, CacheElem::F32, ws, ws_floats, (int)hd};
     const float sl2 = scale * kLog2e;
     switch (padded_hd(hd)) {
         case 32: return launch_prefill_fast_hd<32>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);
@@ -1491,7 +1505,7 @@ size_t prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t rows, si
                                 size_t qbase, size_t window) {
     if (rows == 0 || hkv == 0 || h % hkv != 0) return 0;
     return workspace_floats(padded_hd(hd), (int)h, (int)hkv,
-                            PrefillRange{(int)rows, (int)nkeys, (int)qbase, (int)window, false,
+                            PrefillRange{(int)rows, (int)nkeys, (int)qbase, (int)window, CacheElem::F32,
                                          nullptr, 0, (int)hd});
 }
 
@@ -1499,7 +1513,7 @@ eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, co
                               float *o, size_t h, size_t hkv, size_t s, size_t hd, float scale,
                               float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
-                                PrefillRange{(int)s, (int)s, 0, 0, false, ws, ws_floats, (int)hd});
+                                PrefillRange{(int)s, (int)s, 0, 0, CacheElem::F32, ws, ws_floats, (int)hd});
 }
 
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,
@@ -1508,16 +1522,18 @@ eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float 
                                     size_t window, float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window, false, ws, ws_floats, (int)hd});
+                                             (int)window, CacheElem::F32, ws, ws_floats,
+                                             (int)hd});
 }
 
-eb_status launch_attn_prefill_chunk_f16(hipStream_t st, const float *q, const uint16_t *kc,
-                                        const uint16_t *vc, float *o, size_t h, size_t hkv,
-                                        size_t pos0, size_t rows, size_t hd, float scale,
-                                        size_t window, float *ws, size_t ws_floats) {
+eb_status launch_attn_prefill_chunk_cache(hipStream_t st, const float *q, const void *kc,
+                                          const void *vc, float *o, size_t h, size_t hkv,
+                                          size_t pos0, size_t rows, size_t hd, float scale,
+                                          size_t window, CacheElem ce, float *ws,
+                                          size_t ws_floats) {
     return launch_prefill_range(st, q, kc, vc, o, h, hkv, hd, scale,
                                 PrefillRange{(int)rows, (int)(pos0 + rows), (int)pos0,
-                                             (int)window, true, ws, ws_floats, (int)hd});
+                                             (int)window, ce, ws, ws_floats, (int)hd});
 }
 
 }  // namespace eb

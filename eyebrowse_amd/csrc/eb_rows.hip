@@ -10,15 +10,15 @@
 //  - RoPE at table row rope_row0 + token when the segment asks for it: dims p and p + HD/2
 //    become (x1 c - x2 s, x2 c + x1 s) with the table's angle p (kernels/src/rope.rs:6-32;
 //    pass-through pairs have c = 1, s = 0),
-//  - a store into row dst_row0 + token of a [*, nh, HD] destination of f32 or IEEE-half
-//    elements (the KV caches at base_pos, or the rotated q).
+//  - a store into row dst_row0 + token of a [*, nh, HD] destination of f32, IEEE-half or
+//    OCP FP8 E4M3 elements (the KV caches at base_pos, or the rotated q).
 // The rotation is computed without contraction (two roundings, then the difference), as the
 // reference computes it in f32, so RoPE alone is bit-exact against the reference's CPU path.
 //
 // Lane layout (HD a multiple of 8, up to 256): a head row sits on LPR lanes, LPR the power of
 // two at or above HD/8; lane j < HD/8 holds dims 4j..4j+3 and HD/2+4j..HD/2+4j+3, both halves
 // of its RoPE pairs, so the rotation needs no lane exchange and every access is one 16-byte
-// load or store (8 bytes for half). The row's sum of squares meets over the LPR lanes by DPP
+// load or store (8 bytes for half, 4 for E4M3). The row's sum of squares meets over the LPR lanes by DPP
 // and lane swaps. Other even head dims (and unaligned buffers) take one wave per head row.
 #include "eb_common.h"
 #include "eb_internal.h"
@@ -49,7 +49,8 @@ struct SegView {
     void *dst;
     const float *gain;
     int nh, dst_row0, local;
-    bool rope, half;
+    bool rope;
+    int elem;  // bytes per destination element
 };
 
 __device__ __forceinline__ SegView seg_of(const eb::RowsArgs &a, int t) {
@@ -62,7 +63,7 @@ __device__ __forceinline__ SegView seg_of(const eb::RowsArgs &a, int t) {
     v.nh = pick(a.seg[0].nh, a.seg[1].nh, a.seg[2].nh);
     v.dst_row0 = pick(a.seg[0].dst_row0, a.seg[1].dst_row0, a.seg[2].dst_row0);
     v.rope = pick(a.seg[0].rope, a.seg[1].rope, a.seg[2].rope);
-    v.half = pick(a.seg[0].half, a.seg[1].half, a.seg[2].half);
+    v.elem = pick(a.seg[0].elem, a.seg[1].elem, a.seg[2].elem);
     v.local = t - pick(a.start[0], a.start[1], a.start[2]);
     return v;
 }
@@ -105,10 +106,14 @@ __global__ __launch_bounds__(kThreads) void rows_vec_kernel(eb::RowsArgs a) {
         x2 = y2;
     }
     const size_t d = ((size_t)(sv.dst_row0 + tok) * sv.nh + hh) * hd + 4 * j;
-    if (sv.half) {
+    if (sv.elem == 2) {
         _Float16 *p = static_cast<_Float16 *>(sv.dst) + d;
         *reinterpret_cast<f16x4 *>(p) = __builtin_convertvector(x1, f16x4);
         *reinterpret_cast<f16x4 *>(p + half) = __builtin_convertvector(x2, f16x4);
+    } else if (sv.elem == 1) {
+        uint8_t *p = static_cast<uint8_t *>(sv.dst) + d;
+        *reinterpret_cast<unsigned *>(p) = eb::f8x4_bits(x1);
+        *reinterpret_cast<unsigned *>(p + half) = eb::f8x4_bits(x2);
     } else {
         float *p = static_cast<float *>(sv.dst) + d;
         *reinterpret_cast<f32x4 *>(p) = x1;
@@ -150,10 +155,14 @@ __global__ __launch_bounds__(kThreads) void rows_wave_kernel(eb::RowsArgs a) {
             x1 = y1;
             x2 = y2;
         }
-        if (sv.half) {
+        if (sv.elem == 2) {
             _Float16 *o = static_cast<_Float16 *>(sv.dst) + d;
             o[p] = (_Float16)x1;
             o[p + half] = (_Float16)x2;
+        } else if (sv.elem == 1) {
+            uint8_t *o = static_cast<uint8_t *>(sv.dst) + d;
+            o[p] = (uint8_t)eb::f8e4m3_bits(x1);
+            o[p + half] = (uint8_t)eb::f8e4m3_bits(x2);
         } else {
             float *o = static_cast<float *>(sv.dst) + d;
             o[p] = x1;
@@ -178,7 +187,7 @@ eb_status launch_attn_rows(hipStream_t st, const RowsArgs &args) {
     bool vec = a.hd % 8 == 0 && a.hd <= 256;
     for (int s = 0; s < a.nseg && vec; ++s) {
         const RowSeg &g = a.seg[s];
-        vec = aligned(g.src, 16) && aligned(g.dst, g.half ? 8 : 16) && aligned(g.gain, 16);
+        vec = aligned(g.src, 16) && aligned(g.dst, 4 * (uintptr_t)g.elem) && aligned(g.gain, 16);
     }
     vec = vec && aligned(a.cosb, 16) && aligned(a.sinb, 16);
     if (!vec) {
@@ -204,7 +213,7 @@ eb_status launch_rope(hipStream_t st, const float *x, const float *cosb, const f
                       float *out, size_t seq, size_t n_heads, size_t hd, size_t base_pos) {
     RowsArgs a{};
     a.nseg = 1;
-    a.seg[0] = RowSeg{x, out, nullptr, (int)n_heads, 0, true, false};
+    a.seg[0] = RowSeg{x, out, nullptr, (int)n_heads, 0, true, 4};
     a.rows = (int)seq;
     a.hd = (int)hd;
     a.cosb = cosb;

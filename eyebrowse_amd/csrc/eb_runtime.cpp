@@ -236,6 +236,7 @@ size_t eb_dtype_size(eb_dtype dt) {
     switch (dt) {
         case EB_F32: case EB_U32: case EB_I32: return 4;
         case EB_F16: return 2;
+        case EB_F8E4M3: return 1;
     }
     return 0;
 }
@@ -632,13 +633,16 @@ static eb_status tensor_f32(const eb_tensor *t, const char *name, eb_device *dev
     return EB_OK;
 }
 
-// A KV cache: f32 or IEEE-half elements. `h16` reports which.
-static eb_status tensor_cache(const eb_tensor *t, const char *name, eb_device *dev, bool *h16) {
+// A KV cache: f32, IEEE-half or E4M3 elements; *ce reports which.
+static eb_status tensor_cache(const eb_tensor *t, const char *name, eb_device *dev,
+                              eb::CacheElem *ce) {
     if (!t) return fail(EB_SHAPE_MISMATCH, "%s is null", name);
-    if (t->dtype != EB_F32 && t->dtype != EB_F16)
-        return fail(EB_SHAPE_MISMATCH, "%s must be f32 or f16", name);
+    if (t->dtype != EB_F32 && t->dtype != EB_F16 && t->dtype != EB_F8E4M3)
+        return fail(EB_SHAPE_MISMATCH, "%s must be f32, f16 or f8e4m3", name);
     if (t->dev != dev) return fail(EB_OTHER, "%s lives on another device", name);
-    *h16 = t->dtype == EB_F16;
+    *ce = t->dtype == EB_F16      ? eb::CacheElem::F16
+          : t->dtype == EB_F8E4M3 ? eb::CacheElem::E4M3
+                                  : eb::CacheElem::F32;
     return EB_OK;
 }
 
@@ -646,7 +650,8 @@ static eb_status tensor_cache(const eb_tensor *t, const char *name, eb_device *d
 // Float-buffer views with element counts, shared by the handle and raw entry points.
 static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
                                   const float *src, size_t src_n, size_t hkv, size_t count,
-                                  size_t hd, size_t max_seq, size_t dst, bool h16 = false) {
+                                  size_t hd, size_t max_seq, size_t dst,
+                                  eb::CacheElem ce = eb::CacheElem::F32) {
     if (hkv == 0 || hd == 0) return fail(EB_SHAPE_MISMATCH, "kv_write: hkv and hd must be > 0");
     if (dst > max_seq || count > max_seq - dst)
         return fail(EB_SHAPE_MISMATCH, "kv_write: rows [%zu, %zu) exceed max_seq %zu", dst,
@@ -656,10 +661,14 @@ static eb_status kv_write_checked(hipStream_t st, void *cache, size_t cache_n,
     if (count == 0) return eb::ok();
     EB_TRY(eb::check_ptr(cache, "cache"));
     EB_TRY(eb::check_ptr(src, "src"));
-    if (h16) {
-        if (hd % 4 != 0) return fail(EB_UNSUPPORTED_CONFIG, "kv_write: f16 caches need hd %% 4 == 0");
+    if (ce != eb::CacheElem::F32 && hd % 4 != 0)
+        return fail(EB_UNSUPPORTED_CONFIG, "kv_write: f16 and e4m3 caches need hd %% 4 == 0");
+    if (ce == eb::CacheElem::F16) {
         EB_TRY(eb::launch_kv_write_f16(st, static_cast<uint16_t *>(cache), src, hkv, count, hd,
                                        dst));
+    } else if (ce == eb::CacheElem::E4M3) {
+        EB_TRY(eb::launch_kv_write_f8(st, static_cast<uint8_t *>(cache), src, hkv, count, hd,
+                                      dst));
     } else {
         EB_TRY(eb::launch_kv_write(st, static_cast<float *>(cache), src, hkv, count, hd, dst));
     }
@@ -779,15 +788,16 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
                                        const void *kc, size_t kcn, const void *vc, size_t vcn,
                                        float *o, size_t on, size_t h, size_t hkv, size_t pos0,
                                        size_t rows, size_t hd, size_t max_seq, float scale,
-                                       size_t window, bool h16 = false,
+                                       size_t window, eb::CacheElem ce = eb::CacheElem::F32,
                                        const PrefillWs &wsrc = PrefillWs()) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_prefill_chunk: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)",
                     hd);
-    if (h16 && hd < 8)
-        return fail(EB_UNSUPPORTED_CONFIG, "attn_prefill_chunk: f16 caches need head_dim >= 8");
+    if (ce != eb::CacheElem::F32 && hd < 8)
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_prefill_chunk: f16 and e4m3 caches need head_dim >= 8");
     if (pos0 > max_seq || rows > max_seq - pos0)
         return fail(EB_SHAPE_MISMATCH, "attn_prefill_chunk: rows [%zu, %zu) exceed max_seq %zu",
                     pos0, pos0 + rows, max_seq);
@@ -804,10 +814,9 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     size_t wsn;
     WsLock lk;
     EB_TRY(prefill_ws(wsrc, h, hkv, hd, rows, pos0 + rows, pos0, window, &ws, &wsn, lk));
-    if (h16)
-        EB_TRY(eb::launch_attn_prefill_chunk_f16(st, q, static_cast<const uint16_t *>(kc),
-                                                 static_cast<const uint16_t *>(vc), o, h, hkv,
-                                                 pos0, rows, hd, scale, window, ws, wsn));
+    if (ce != eb::CacheElem::F32)
+        EB_TRY(eb::launch_attn_prefill_chunk_cache(st, q, kc, vc, o, h, hkv, pos0, rows, hd,
+                                                   scale, window, ce, ws, wsn));
     else
         EB_TRY(eb::launch_attn_prefill_chunk(st, q, static_cast<const float *>(kc),
                                              static_cast<const float *>(vc), o, h, hkv, pos0,
@@ -818,13 +827,14 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
 static eb_status decode_shape_checked(const float *q, size_t qn, const void *kc, size_t kcn,
                                       const void *vc, size_t vcn, const float *o, size_t on,
                                       size_t h, size_t hkv, size_t pos, size_t hd,
-                                      size_t max_seq, bool h16 = false) {
+                                      size_t max_seq,
+                                      eb::CacheElem ce = eb::CacheElem::F32) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_decode: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)", hd);
-    if (h16 && hd < 8)
-        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 caches need head_dim >= 8");
+    if (ce != eb::CacheElem::F32 && hd < 8)
+        return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 and e4m3 caches need head_dim >= 8");
     if (pos >= max_seq)
         return fail(EB_SHAPE_MISMATCH, "attn_decode: pos %zu >= max_seq %zu", pos, max_seq);
     EB_TRY(eb::check_numel(qn, {h, hd}, "q"));
@@ -879,7 +889,7 @@ static eb_status prologue_checked(hipStream_t st, const float *q, size_t qn, con
                                   const float *gv, float eps, const float *rc, const float *rs,
                                   size_t tn, size_t base_pos, float *q_out, size_t qon,
                                   void *kc, size_t kcn, void *vc, size_t vcn, size_t max_seq,
-                                  bool h16) {
+                                  eb::CacheElem ce) {
     EB_TRY(eb::check_heads(h, hkv));
     if (hd == 0 || hd % 2 != 0)
         return fail(EB_SHAPE_MISMATCH, "attention prologue: head_dim must be even and > 0");
@@ -904,9 +914,9 @@ static eb_status prologue_checked(hipStream_t st, const float *q, size_t qn, con
     eb::RowsArgs a{};
     a.nseg = 3;
     const bool rope = rc != nullptr;
-    a.seg[0] = eb::RowSeg{q, q_out, gq, (int)h, 0, rope, false};
-    a.seg[1] = eb::RowSeg{k, kc, gk, (int)hkv, (int)base_pos, rope, h16};
-    a.seg[2] = eb::RowSeg{v, vc, gv, (int)hkv, (int)base_pos, false, h16};
+    a.seg[0] = eb::RowSeg{q, q_out, gq, (int)h, 0, rope, 4};
+    a.seg[1] = eb::RowSeg{k, kc, gk, (int)hkv, (int)base_pos, rope, (int)ce};
+    a.seg[2] = eb::RowSeg{v, vc, gv, (int)hkv, (int)base_pos, false, (int)ce};
     a.rows = (int)rows;
     a.hd = (int)hd;
     a.eps = eps;
@@ -959,14 +969,15 @@ static eb_status device_workspace(eb_device *dev, size_t floats, float **out, Ws
 static eb_status device_decode(eb_device *dev, const float *q, const void *kc, const void *vc,
                                void *kc_w, void *vc_w, const float *knew, const float *vnew,
                                float *o, size_t h, size_t hkv, size_t pos, size_t hd,
-                               float scale, size_t window = 0, bool h16 = false,
+                               float scale, size_t window = 0,
+                               eb::CacheElem ce = eb::CacheElem::F32,
                                const eb::DecodePrologue *pro = nullptr) {
-    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count, h16);
+    size_t wsn = eb::decode_workspace_floats(h, hkv, pos, hd, dev->cu_count, ce);
     float *ws = nullptr;
     WsLock lk;
     if (wsn > 0) EB_TRY(device_workspace(dev, wsn, &ws, lk));
     EB_TRY(eb::launch_attn_decode_any(dev->stream, q, kc, vc, kc_w, vc_w, knew, vnew, o, h, hkv,
-                                      pos, hd, scale, ws, wsn, dev->cu_count, window, h16, pro));
+                                      pos, hd, scale, ws, wsn, dev->cu_count, window, ce, pro));
     return eb::ok();
 }
 
@@ -1040,12 +1051,12 @@ static eb_status device_linear(eb_device *dev, const eb_tensor *a,
 
 // Both caches of one layer share a dtype.
 static eb_status cache_pair(const eb_tensor *kc, const eb_tensor *vc, eb_device *dev,
-                            bool *h16) {
-    bool hk = false, hv = false;
-    EB_TRY(tensor_cache(kc, "kcache", dev, &hk));
-    EB_TRY(tensor_cache(vc, "vcache", dev, &hv));
-    if (hk != hv) return fail(EB_SHAPE_MISMATCH, "kcache and vcache dtypes differ");
-    *h16 = hk;
+                            eb::CacheElem *ce) {
+    eb::CacheElem ek = eb::CacheElem::F32, ev = eb::CacheElem::F32;
+    EB_TRY(tensor_cache(kc, "kcache", dev, &ek));
+    EB_TRY(tensor_cache(vc, "vcache", dev, &ev));
+    if (ek != ev) return fail(EB_SHAPE_MISMATCH, "kcache and vcache dtypes differ");
+    *ce = ek;
     return EB_OK;
 }
 
@@ -1055,12 +1066,12 @@ extern "C" {
 eb_status eb_kv_write(eb_recorder *rec, eb_tensor *cache, const eb_tensor *src, size_t hkv,
                       size_t count, size_t hd, size_t max_seq, size_t dst_start) {
     EB_TRY(rec_ready(rec));
-    bool h16 = false;
-    EB_TRY(tensor_cache(cache, "cache", rec->dev, &h16));
+    eb::CacheElem ce = eb::CacheElem::F32;
+    EB_TRY(tensor_cache(cache, "cache", rec->dev, &ce));
     EB_TRY(tensor_f32(src, "src", rec->dev));
     return kv_write_checked(rec->dev->stream, cache->ptr, eb_tensor_numel(cache),
                             (const float *)src->ptr, eb_tensor_numel(src), hkv, count, hd,
-                            max_seq, dst_start, h16);
+                            max_seq, dst_start, ce);
 }
 
 eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
@@ -1125,13 +1136,13 @@ eb_status eb_attn_prefill_chunk(eb_recorder *rec, const eb_tensor *q, const eb_t
                                 float scale, size_t window) {
     EB_TRY(rec_ready(rec));
     EB_TRY(tensor_f32(q, "q", rec->dev));
-    bool h16 = false;
-    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    eb::CacheElem ce = eb::CacheElem::F32;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &ce));
     EB_TRY(tensor_f32(o, "o", rec->dev));
     return prefill_chunk_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
                                  kcache->ptr, eb_tensor_numel(kcache), vcache->ptr,
                                  eb_tensor_numel(vcache), (float *)o->ptr, eb_tensor_numel(o), h,
-                                 hkv, pos0, rows, hd, max_seq, scale, window, h16,
+                                 hkv, pos0, rows, hd, max_seq, scale, window, ce,
                                  PrefillWs{rec->dev});
 }
 
@@ -1141,16 +1152,16 @@ eb_status eb_attn_decode_window(eb_recorder *rec, const eb_tensor *q, const eb_t
                                 size_t window) {
     EB_TRY(rec_ready(rec));
     EB_TRY(tensor_f32(q, "q", rec->dev));
-    bool h16 = false;
-    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    eb::CacheElem ce = eb::CacheElem::F32;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &ce));
     EB_TRY(tensor_f32(o, "o", rec->dev));
     EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q), kcache->ptr,
                                 eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache),
                                 (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
-                                max_seq, h16));
+                                max_seq, ce));
     return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, nullptr,
                          nullptr, nullptr, nullptr, (float *)o->ptr, h, hkv, pos, hd, scale,
-                         window, h16);
+                         window, ce);
 }
 
 eb_status eb_attn_decode_step(eb_recorder *rec, const eb_tensor *q, const eb_tensor *knew,
@@ -1170,19 +1181,19 @@ eb_status eb_attn_decode_step_window(eb_recorder *rec, const eb_tensor *q, const
     EB_TRY(tensor_f32(q, "q", rec->dev));
     EB_TRY(tensor_f32(knew, "knew", rec->dev));
     EB_TRY(tensor_f32(vnew, "vnew", rec->dev));
-    bool h16 = false;
-    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    eb::CacheElem ce = eb::CacheElem::F32;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &ce));
     EB_TRY(tensor_f32(o, "o", rec->dev));
     EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q), kcache->ptr,
                                 eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache),
                                 (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
-                                max_seq, h16));
+                                max_seq, ce));
     size_t nn = eb_tensor_numel(knew) < eb_tensor_numel(vnew) ? eb_tensor_numel(knew)
                                                               : eb_tensor_numel(vnew);
     EB_TRY(step_rows_checked((const float *)knew->ptr, (const float *)vnew->ptr, nn, hkv, hd));
     return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, kcache->ptr,
                          vcache->ptr, (const float *)knew->ptr, (const float *)vnew->ptr,
-                         (float *)o->ptr, h, hkv, pos, hd, scale, window, h16);
+                         (float *)o->ptr, h, hkv, pos, hd, scale, window, ce);
 }
 
 }  // extern "C"
@@ -1221,13 +1232,13 @@ eb_status eb::attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q,
     EB_TRY(tensor_f32(q, "q", rec->dev));
     EB_TRY(tensor_f32(knew, "knew", rec->dev));
     EB_TRY(tensor_f32(vnew, "vnew", rec->dev));
-    bool h16 = false;
-    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    eb::CacheElem ce = eb::CacheElem::F32;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &ce));
     EB_TRY(tensor_f32(o, "o", rec->dev));
     EB_TRY(decode_shape_checked((const float *)q->ptr, eb_tensor_numel(q), kcache->ptr,
                                 eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache),
                                 (const float *)o->ptr, eb_tensor_numel(o), h, hkv, pos, hd,
-                                max_seq, h16));
+                                max_seq, ce));
     size_t nn = eb_tensor_numel(knew) < eb_tensor_numel(vnew) ? eb_tensor_numel(knew)
                                                               : eb_tensor_numel(vnew);
     EB_TRY(step_rows_checked((const float *)knew->ptr, (const float *)vnew->ptr, nn, hkv, hd));
@@ -1255,7 +1266,7 @@ eb_status eb::attn_decode_step_fused(eb_recorder *rec, const eb_tensor *q,
     }
     return device_decode(rec->dev, (const float *)q->ptr, kcache->ptr, vcache->ptr, kcache->ptr,
                          vcache->ptr, (const float *)knew->ptr, (const float *)vnew->ptr,
-                         (float *)o->ptr, h, hkv, pos, hd, scale, window, h16, &pro);
+                         (float *)o->ptr, h, hkv, pos, hd, scale, window, ce, &pro);
 }
 
 // The prefill counterpart of attn_decode_step_fused: the handle form of prologue_checked.
@@ -1270,8 +1281,8 @@ eb_status eb::attn_rows_fused(eb_recorder *rec, const eb_tensor *q, const eb_ten
     EB_TRY(tensor_f32(k, "k", rec->dev));
     EB_TRY(tensor_f32(v, "v", rec->dev));
     EB_TRY(tensor_f32(q_out, "q_out", rec->dev));
-    bool h16 = false;
-    EB_TRY(cache_pair(kcache, vcache, rec->dev, &h16));
+    eb::CacheElem ce = eb::CacheElem::F32;
+    EB_TRY(cache_pair(kcache, vcache, rec->dev, &ce));
     const eb_tensor *norms[3] = {q_norm, k_norm, v_norm};
     const float *g[3] = {nullptr, nullptr, nullptr};
     for (int i = 0; i < 3; ++i) {
@@ -1297,7 +1308,7 @@ eb_status eb::attn_rows_fused(eb_recorder *rec, const eb_tensor *q, const eb_ten
         rope_cos ? static_cast<const float *>(rope_cos->ptr) : nullptr,
         rope_sin ? static_cast<const float *>(rope_sin->ptr) : nullptr, tn, base_pos,
         static_cast<float *>(q_out->ptr), eb_tensor_numel(q_out), kcache->ptr,
-        eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache), max_seq, h16);
+        eb_tensor_numel(kcache), vcache->ptr, eb_tensor_numel(vcache), max_seq, ce);
 }
 
 extern "C" {
@@ -1376,7 +1387,8 @@ eb_status eb_launch_attn_prefill_chunk_ws(void *stream, const float *q, size_t q
                                           size_t max_seq, float scale, size_t window,
                                           float *workspace, size_t workspace_floats) {
     return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
-                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window, false,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window,
+                                 eb::CacheElem::F32,
                                  PrefillWs{nullptr, true, workspace, workspace_floats});
 }
 
@@ -1388,7 +1400,8 @@ eb_status eb_launch_attn_prefill_chunk_f16_ws(void *stream, const float *q, size
                                               float scale, size_t window, float *workspace,
                                               size_t workspace_floats) {
     return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
-                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window, true,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window,
+                                 eb::CacheElem::F16,
                                  PrefillWs{nullptr, true, workspace, workspace_floats});
 }
 
@@ -1448,13 +1461,58 @@ eb_status eb_launch_attn_decode_step(void *stream, const float *q, size_t q_nume
                                scale, workspace, workspace_floats, cu_count);
 }
 
-// ---- raw launches over IEEE-half KV caches ------------------------------------------
+// ---- raw launches over IEEE-half and E4M3 KV caches ---------------------------------
+
+}  // extern "C"
+
+static eb_status decode_cache_raw(void *stream, const float *q, size_t q_numel, const void *kc,
+                                  size_t kc_numel, const void *vc, size_t vc_numel, float *o,
+                                  size_t o_numel, size_t h, size_t hkv, size_t pos, size_t hd,
+                                  size_t max_seq, float scale, size_t window, float *workspace,
+                                  size_t workspace_floats, int cu_count, eb::CacheElem ce) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq, ce));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus, ce);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode_any((hipStream_t)stream, q, kc, vc, nullptr, nullptr, nullptr,
+                                      nullptr, o, h, hkv, pos, hd, scale, workspace,
+                                      workspace_floats, cus, window, ce));
+    return eb::ok();
+}
+
+static eb_status decode_step_cache_raw(void *stream, const float *q, size_t q_numel,
+                                       const float *knew, const float *vnew, size_t new_numel,
+                                       void *kc, size_t kc_numel, void *vc, size_t vc_numel,
+                                       float *o, size_t o_numel, size_t h, size_t hkv,
+                                       size_t pos, size_t hd, size_t max_seq, float scale,
+                                       size_t window, float *workspace, size_t workspace_floats,
+                                       int cu_count, eb::CacheElem ce) {
+    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                                pos, hd, max_seq, ce));
+    EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
+    int cus = cu_count > 0 ? cu_count : 256;
+    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus, ce);
+    if (workspace_floats < need)
+        return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
+                    workspace_floats, need);
+    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
+    EB_TRY(eb::launch_attn_decode_any((hipStream_t)stream, q, kc, vc, kc, vc, knew, vnew, o, h,
+                                      hkv, pos, hd, scale, workspace, workspace_floats, cus,
+                                      window, ce));
+    return eb::ok();
+}
+
+extern "C" {
 
 eb_status eb_launch_kv_write_f16(void *stream, uint16_t *cache, size_t cache_numel,
                                  const float *src, size_t src_numel, size_t hkv, size_t count,
                                  size_t hd, size_t max_seq, size_t dst_start) {
     return kv_write_checked((hipStream_t)stream, cache, cache_numel, src, src_numel, hkv, count,
-                            hd, max_seq, dst_start, true);
+                            hd, max_seq, dst_start, eb::CacheElem::F16);
 }
 
 eb_status eb_launch_attn_prefill_chunk_f16(void *stream, const float *q, size_t q_numel,
@@ -1464,7 +1522,8 @@ eb_status eb_launch_attn_prefill_chunk_f16(void *stream, const float *q, size_t 
                                            size_t rows, size_t hd, size_t max_seq, float scale,
                                            size_t window) {
     return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
-                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window, true);
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window,
+                                 eb::CacheElem::F16);
 }
 
 eb_status eb_launch_attn_decode_f16(void *stream, const float *q, size_t q_numel,
@@ -1473,18 +1532,9 @@ eb_status eb_launch_attn_decode_f16(void *stream, const float *q, size_t q_numel
                                     size_t hkv, size_t pos, size_t hd, size_t max_seq,
                                     float scale, size_t window, float *workspace,
                                     size_t workspace_floats, int cu_count) {
-    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
-                                pos, hd, max_seq, true));
-    int cus = cu_count > 0 ? cu_count : 256;
-    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus, true);
-    if (workspace_floats < need)
-        return fail(EB_SHAPE_MISMATCH, "attn_decode: workspace holds %zu floats, needs %zu",
-                    workspace_floats, need);
-    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
-    EB_TRY(eb::launch_attn_decode_any((hipStream_t)stream, q, kc, vc, nullptr, nullptr, nullptr,
-                                      nullptr, o, h, hkv, pos, hd, scale, workspace,
-                                      workspace_floats, cus, window, true));
-    return eb::ok();
+    return decode_cache_raw(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                            pos, hd, max_seq, scale, window, workspace, workspace_floats,
+                            cu_count, eb::CacheElem::F16);
 }
 
 eb_status eb_launch_attn_decode_step_f16(void *stream, const float *q, size_t q_numel,
@@ -1494,19 +1544,62 @@ eb_status eb_launch_attn_decode_step_f16(void *stream, const float *q, size_t q_
                                          size_t hkv, size_t pos, size_t hd, size_t max_seq,
                                          float scale, size_t window, float *workspace,
                                          size_t workspace_floats, int cu_count) {
-    EB_TRY(decode_shape_checked(q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
-                                pos, hd, max_seq, true));
-    EB_TRY(step_rows_checked(knew, vnew, new_numel, hkv, hd));
-    int cus = cu_count > 0 ? cu_count : 256;
-    size_t need = eb::decode_workspace_floats(h, hkv, pos, hd, cus, true);
-    if (workspace_floats < need)
-        return fail(EB_SHAPE_MISMATCH, "attn_decode_step: workspace holds %zu floats, needs %zu",
-                    workspace_floats, need);
-    if (need > 0) EB_TRY(eb::check_ptr(workspace, "workspace"));
-    EB_TRY(eb::launch_attn_decode_any((hipStream_t)stream, q, kc, vc, kc, vc, knew, vnew, o, h,
-                                      hkv, pos, hd, scale, workspace, workspace_floats, cus,
-                                      window, true));
-    return eb::ok();
+    return decode_step_cache_raw(stream, q, q_numel, knew, vnew, new_numel, kc, kc_numel, vc,
+                                 vc_numel, o, o_numel, h, hkv, pos, hd, max_seq, scale, window,
+                                 workspace, workspace_floats, cu_count, eb::CacheElem::F16);
+}
+
+eb_status eb_launch_kv_write_f8(void *stream, uint8_t *cache, size_t cache_numel,
+                                const float *src, size_t src_numel, size_t hkv, size_t count,
+                                size_t hd, size_t max_seq, size_t dst_start) {
+    return kv_write_checked((hipStream_t)stream, cache, cache_numel, src, src_numel, hkv, count,
+                            hd, max_seq, dst_start, eb::CacheElem::E4M3);
+}
+
+eb_status eb_launch_attn_prefill_chunk_f8(void *stream, const float *q, size_t q_numel,
+                                          const uint8_t *kc, size_t kc_numel, const uint8_t *vc,
+                                          size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                          size_t hkv, size_t pos0, size_t rows, size_t hd,
+                                          size_t max_seq, float scale, size_t window) {
+    return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window,
+                                 eb::CacheElem::E4M3);
+}
+
+eb_status eb_launch_attn_prefill_chunk_f8_ws(void *stream, const float *q, size_t q_numel,
+                                             const uint8_t *kc, size_t kc_numel,
+                                             const uint8_t *vc, size_t vc_numel, float *o,
+                                             size_t o_numel, size_t h, size_t hkv, size_t pos0,
+                                             size_t rows, size_t hd, size_t max_seq,
+                                             float scale, size_t window, float *workspace,
+                                             size_t workspace_floats) {
+    return prefill_chunk_checked((hipStream_t)stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                 o_numel, h, hkv, pos0, rows, hd, max_seq, scale, window,
+                                 eb::CacheElem::E4M3,
+                                 PrefillWs{nullptr, true, workspace, workspace_floats});
+}
+
+eb_status eb_launch_attn_decode_f8(void *stream, const float *q, size_t q_numel,
+                                   const uint8_t *kc, size_t kc_numel, const uint8_t *vc,
+                                   size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                   size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                   float scale, size_t window, float *workspace,
+                                   size_t workspace_floats, int cu_count) {
+    return decode_cache_raw(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv,
+                            pos, hd, max_seq, scale, window, workspace, workspace_floats,
+                            cu_count, eb::CacheElem::E4M3);
+}
+
+eb_status eb_launch_attn_decode_step_f8(void *stream, const float *q, size_t q_numel,
+                                        const float *knew, const float *vnew, size_t new_numel,
+                                        uint8_t *kc, size_t kc_numel, uint8_t *vc,
+                                        size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                        size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                        float scale, size_t window, float *workspace,
+                                        size_t workspace_floats, int cu_count) {
+    return decode_step_cache_raw(stream, q, q_numel, knew, vnew, new_numel, kc, kc_numel, vc,
+                                 vc_numel, o, o_numel, h, hkv, pos, hd, max_seq, scale, window,
+                                 workspace, workspace_floats, cu_count, eb::CacheElem::E4M3);
 }
 
 eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel, const float *weight,
@@ -1525,12 +1618,16 @@ eb_status eb_launch_attn_prologue(void *stream, const float *q, size_t q_numel, 
                                   size_t q_out_numel, void *kcache, size_t kc_numel,
                                   void *vcache, size_t vc_numel, size_t max_seq,
                                   eb_dtype cache_dtype) {
-    if (cache_dtype != EB_F32 && cache_dtype != EB_F16)
-        return fail(EB_UNSUPPORTED_CONFIG, "attention prologue: caches must be f32 or f16");
+    if (cache_dtype != EB_F32 && cache_dtype != EB_F16 && cache_dtype != EB_F8E4M3)
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attention prologue: caches must be f32, f16 or f8e4m3");
     return prologue_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, rows, h, hkv,
                             hd, q_norm, k_norm, v_norm, eps, rope_cos, rope_sin, table_numel,
                             base_pos, q_out, q_out_numel, kcache, kc_numel, vcache, vc_numel,
-                            max_seq, cache_dtype == EB_F16);
+                            max_seq,
+                            cache_dtype == EB_F16      ? eb::CacheElem::F16
+                            : cache_dtype == EB_F8E4M3 ? eb::CacheElem::E4M3
+                                                       : eb::CacheElem::F32);
 }
 
 eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const float *cos,

@@ -16,11 +16,13 @@ from ._lib import c_size, c_vp, lib
 
 
 class DType(enum.IntEnum):
-    """crates/eyebrowse-core/src/lib.rs:8-25."""
+    """crates/eyebrowse-core/src/lib.rs:8-25; F8E4M3 (OCP FP8 E4M3 KV caches, one byte per
+    element) has no counterpart in the reference."""
     F32 = 0
     F16 = 1
     U32 = 2
     I32 = 3
+    F8E4M3 = 4
 
     def size(self) -> int:
         return int(lib().eb_dtype_size(int(self)))

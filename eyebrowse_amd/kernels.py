@@ -183,8 +183,11 @@ def launch_attn_prefill_ws(stream: int, q: int, q_numel: int, k: int, k_numel: i
 def launch_attn_prefill_chunk_ws(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
                                  vc: int, vc_numel: int, o: int, o_numel: int, h: int, hkv: int,
                                  pos0: int, rows: int, hd: int, max_seq: int, scale: float,
-                                 window: int, ws: int, ws_floats: int, f16: bool = False) -> None:
-    fn = lib().eb_launch_attn_prefill_chunk_f16_ws if f16 else lib().eb_launch_attn_prefill_chunk_ws
+                                 window: int, ws: int, ws_floats: int, f16: bool = False,
+                                 f8: bool = False) -> None:
+    fn = (lib().eb_launch_attn_prefill_chunk_f8_ws if f8 else
+          lib().eb_launch_attn_prefill_chunk_f16_ws if f16 else
+          lib().eb_launch_attn_prefill_chunk_ws)
     check(fn(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos0, rows, hd,
              max_seq, scale, window, ws, ws_floats))
 
@@ -267,6 +270,45 @@ def launch_attn_decode_step_f16(stream: int, q: int, q_numel: int, knew: int, vn
                                                kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos,
                                                hd, max_seq, scale, window, workspace,
                                                workspace_floats, cu_count))
+
+
+# ---- raw launches over OCP FP8 E4M3 caches (no counterpart in the reference) -----------
+
+def launch_kv_write_f8(stream: int, cache: int, cache_numel: int, src: int, src_numel: int,
+                       hkv: int, count: int, hd: int, max_seq: int, dst_start: int) -> None:
+    """kv_write into a uint8 (E4M3) cache: nearest value, ties to even, finite values
+    saturating at +-448, inf and NaN to NaN."""
+    check(lib().eb_launch_kv_write_f8(stream, cache, cache_numel, src, src_numel, hkv, count,
+                                      hd, max_seq, dst_start))
+
+
+def launch_attn_prefill_chunk_f8(stream: int, q: int, q_numel: int, kc: int, kc_numel: int,
+                                 vc: int, vc_numel: int, o: int, o_numel: int, h: int,
+                                 hkv: int, pos0: int, rows: int, hd: int, max_seq: int,
+                                 scale: float, window: int = 0) -> None:
+    check(lib().eb_launch_attn_prefill_chunk_f8(stream, q, q_numel, kc, kc_numel, vc, vc_numel,
+                                                o, o_numel, h, hkv, pos0, rows, hd, max_seq,
+                                                scale, window))
+
+
+def launch_attn_decode_f8(stream: int, q: int, q_numel: int, kc: int, kc_numel: int, vc: int,
+                          vc_numel: int, o: int, o_numel: int, h: int, hkv: int, pos: int,
+                          hd: int, max_seq: int, scale: float, window: int, workspace: int,
+                          workspace_floats: int, cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode_f8(stream, q, q_numel, kc, kc_numel, vc, vc_numel, o,
+                                         o_numel, h, hkv, pos, hd, max_seq, scale, window,
+                                         workspace, workspace_floats, cu_count))
+
+
+def launch_attn_decode_step_f8(stream: int, q: int, q_numel: int, knew: int, vnew: int,
+                               new_numel: int, kc: int, kc_numel: int, vc: int, vc_numel: int,
+                               o: int, o_numel: int, h: int, hkv: int, pos: int, hd: int,
+                               max_seq: int, scale: float, window: int, workspace: int,
+                               workspace_floats: int, cu_count: int) -> None:
+    check(lib().eb_launch_attn_decode_step_f8(stream, q, q_numel, knew, vnew, new_numel, kc,
+                                              kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos,
+                                              hd, max_seq, scale, window, workspace,
+                                              workspace_floats, cu_count))
 
 
 def launch_rmsnorm(stream: int, x: int, x_numel: int, w: int, w_numel: int, out: int,

@@ -107,8 +107,9 @@ class KvCache:
     @classmethod
     def new_per_layer(cls, dev: Device, head_dims, max_seq: int, n_kv_heads: int,
                       dtype: DType = DType.F32) -> "KvCache":
-        """dtype F32 is the reference's cache; F16 (IEEE half, no counterpart in the
-        reference) halves the cache bytes that decode streams."""
+        """dtype F32 is the reference's cache; F16 (IEEE half) halves and F8E4M3 (OCP FP8
+        E4M3) quarters the cache bytes that decode streams (neither has a counterpart in
+        the reference)."""
         arr = (c_size * max(1, len(head_dims)))(*head_dims)
         out = c_vp()
         check(lib().eb_kv_cache_new_per_layer_dtype(dev.handle, arr, len(head_dims), max_seq,

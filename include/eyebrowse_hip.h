@@ -40,8 +40,9 @@ typedef enum eb_status {
     EB_OTHER = 6
 } eb_status;
 
-/* Mirrors DType (crates/eyebrowse-core/src/lib.rs:8-25). */
-typedef enum eb_dtype { EB_F32 = 0, EB_F16 = 1, EB_U32 = 2, EB_I32 = 3 } eb_dtype;
+/* EB_F32 .. EB_I32 mirror DType (crates/eyebrowse-core/src/lib.rs:8-25). EB_F8E4M3 (OCP FP8
+ * E4M3, one byte per element, for KV caches) has no counterpart in the reference. */
+typedef enum eb_dtype { EB_F32 = 0, EB_F16 = 1, EB_U32 = 2, EB_I32 = 3, EB_F8E4M3 = 4 } eb_dtype;
 
 typedef struct eb_device eb_device;
 typedef struct eb_tensor eb_tensor;
@@ -329,7 +330,8 @@ eb_status eb_launch_rope(void *stream, const float *x, size_t x_numel, const flo
  * given (NULL: none; a weightless norm passes ones), then RoPE with the [table rows, hd/2]
  * tables at row base_pos + token for q and k (NULL tables: none). The rotated q goes to
  * q_out [rows,h,hd]; K and V go to cache rows base_pos.. of [max_seq,hkv,hd] caches of
- * cache_dtype (EB_F32, or EB_F16 rounded to nearest even). RoPE is computed without fused
+ * cache_dtype (EB_F32, or EB_F16 / EB_F8E4M3 rounded to nearest even, E4M3 saturating at
+ * +-448). RoPE is computed without fused
  * multiply-adds, as the reference's f32 arithmetic does; rows without a norm are copied
  * bit-exactly. hd even. The reference records 6 kernels for this (3 rmsnorm, 2 rope,
  * 2 kv_write less the norms it skips). */
@@ -410,6 +412,48 @@ eb_status eb_launch_attn_decode_step_f16(void *stream, const float *q, size_t q_
                                          float scale, size_t window, float *workspace,
                                          size_t workspace_floats, int cu_count);
 
+/* ---- raw launches over OCP FP8 E4M3 KV caches --------------------------------------
+ * Caches hold uint8_t E4M3 patterns ("e4m3fn": sign, 4 exponent bits with bias 7, 3
+ * fraction bits, no infinities, 0x7F / 0xFF NaN, largest finite 448), [max_seq, hkv, hd],
+ * numel in elements: a quarter of the f32 cache bytes. kv_write stores the nearest E4M3
+ * value of each f32 (ties to the even fraction); finite values at or beyond 448 saturate
+ * to +-448, inf and NaN become NaN. Attention converts the stored values to f32 exactly and
+ * computes as the f32 entry points do (the fused step's key pos uses the rounded new row).
+ * With 3 fraction bits the stored rows carry up to 2^-4 relative error, which reaches the
+ * outputs at about 4e-2 rel-L2 on N(0,1) caches at scale 1/sqrt(hd)
+ * does not apply to this format. Head dims 8..256 (4, 8 and multiples of 16). No
+ * counterpart in the reference (its caches are f32). The handle entry points (eb_kv_write,
+ * eb_attn_decode*, eb_attn_prefill_chunk, eb_attention_forward*) take EB_F8E4M3 caches
+ * too, dispatching on the cache tensors' dtype. */
+eb_status eb_launch_kv_write_f8(void *stream, uint8_t *cache, size_t cache_numel,
+                                const float *src, size_t src_numel, size_t hkv, size_t count,
+                                size_t hd, size_t max_seq, size_t dst_start);
+eb_status eb_launch_attn_prefill_chunk_f8(void *stream, const float *q, size_t q_numel,
+                                          const uint8_t *kc, size_t kc_numel, const uint8_t *vc,
+                                          size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                          size_t hkv, size_t pos0, size_t rows, size_t hd,
+                                          size_t max_seq, float scale, size_t window);
+eb_status eb_launch_attn_prefill_chunk_f8_ws(void *stream, const float *q, size_t q_numel,
+                                             const uint8_t *kc, size_t kc_numel,
+                                             const uint8_t *vc, size_t vc_numel, float *o,
+                                             size_t o_numel, size_t h, size_t hkv, size_t pos0,
+                                             size_t rows, size_t hd, size_t max_seq,
+                                             float scale, size_t window, float *workspace,
+                                             size_t workspace_floats);
+eb_status eb_launch_attn_decode_f8(void *stream, const float *q, size_t q_numel,
+                                   const uint8_t *kc, size_t kc_numel, const uint8_t *vc,
+                                   size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                   size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                   float scale, size_t window, float *workspace,
+                                   size_t workspace_floats, int cu_count);
+eb_status eb_launch_attn_decode_step_f8(void *stream, const float *q, size_t q_numel,
+                                        const float *knew, const float *vnew, size_t new_numel,
+                                        uint8_t *kc, size_t kc_numel, uint8_t *vc,
+                                        size_t vc_numel, float *o, size_t o_numel, size_t h,
+                                        size_t hkv, size_t pos, size_t hd, size_t max_seq,
+                                        float scale, size_t window, float *workspace,
+                                        size_t workspace_floats, int cu_count);
+
 /* ---- nn (crates/eyebrowse-nn/src) -------------------------------------------------- */
 
 /* Rope::build_partial (rope.rs:24-50): host f64 tables -> f32 device tensors
@@ -427,10 +471,10 @@ eb_status eb_rope_apply(const eb_rope_tables *rope, eb_recorder *rec, const eb_t
  * [max_seq, n_kv_heads, head_dims[l]] from Tensor::empty. */
 eb_status eb_kv_cache_new_per_layer(eb_device *dev, const size_t *head_dims, size_t n_layers,
                                     size_t max_seq, size_t n_kv_heads, eb_kv_cache **out);
-/* The same with the caches' element type: EB_F32 (the reference's) or EB_F16 (IEEE half:
- * half the cache bytes; kv_write rounds to nearest even, attention computes in f32 on
- * the rounded values). No counterpart in the reference, whose caches are f32
- * (kv_cache.rs:37,41). */
+/* The same with the caches' element type: EB_F32 (the reference's), EB_F16 (IEEE half:
+ * half the cache bytes) or EB_F8E4M3 (OCP FP8 E4M3: a quarter); kv_write rounds to nearest
+ * even (E4M3 saturating at +-448), attention computes in f32 on the rounded values. No
+ * counterpart in the reference, whose caches are f32 (kv_cache.rs:37,41). */
 eb_status eb_kv_cache_new_per_layer_dtype(eb_device *dev, const size_t *head_dims,
                                           size_t n_layers, size_t max_seq, size_t n_kv_heads,
                                           eb_dtype dtype, eb_kv_cache **out);

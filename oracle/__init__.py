@@ -66,6 +66,10 @@ def _load():
                                     ctypes.c_int]
     lib.ebo_f16_to_f32.restype = ctypes.c_float
     lib.ebo_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.ebo_f8e4m3_bits_n.restype = None
+    lib.ebo_f8e4m3_bits_n.argtypes = [_f32p, ctypes.POINTER(ctypes.c_uint8), _sz]
+    lib.ebo_f8e4m3_to_f32_n.restype = None
+    lib.ebo_f8e4m3_to_f32_n.argtypes = [ctypes.POINTER(ctypes.c_uint8), _f32p, _sz]
     lib.ebo_argmax.restype = ctypes.c_uint32
     lib.ebo_argmax.argtypes = [_f32p, _sz]
     lib.ebo_default_scale.restype = ctypes.c_float
@@ -227,6 +231,35 @@ def kv_write_f16(cache_bits, src, hkv: int, count: int, hd: int, dst_start: int)
     n = count * hkv * hd
     assert src.size >= n and cache.size >= (dst_start + count) * hkv * hd
     cache[dst_start * hkv * hd:dst_start * hkv * hd + n] = f16_bits(src[:n])
+    return cache
+
+
+def f8_bits(x) -> np.ndarray:
+    """OCP FP8 E4M3 (e4m3fn) bit patterns of f32 values, the FP8 cache's kv_write contract:
+    nearest value, ties to even; finite values at or beyond 448 saturate to +-448; inf and
+    NaN become NaN (0x7F | sign). The reference's caches are f32 only."""
+    x = np.ascontiguousarray(_f32(x)).ravel()
+    out = np.empty(x.size, np.uint8)
+    _load().ebo_f8e4m3_bits_n(_p(x), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), x.size)
+    return out
+
+
+def f8_values(bits) -> np.ndarray:
+    """f32 values of E4M3 bit patterns (exact)."""
+    b = np.ascontiguousarray(bits, np.uint8).ravel()
+    out = np.empty(b.size, np.float32)
+    _load().ebo_f8e4m3_to_f32_n(b.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), _p(out), b.size)
+    return out
+
+
+def kv_write_f8(cache_bits, src, hkv: int, count: int, hd: int, dst_start: int) -> np.ndarray:
+    """kv_write (ops.rs:70-87 row placement) into an E4M3 cache: rows dst_start..
+    dst_start+count of cache_bits [uint8] take f8_bits of src. Returns a new array."""
+    cache = np.ascontiguousarray(cache_bits, np.uint8).ravel().copy()
+    src = _f32(src).ravel()
+    n = count * hkv * hd
+    assert src.size >= n and cache.size >= (dst_start + count) * hkv * hd
+    cache[dst_start * hkv * hd:dst_start * hkv * hd + n] = f8_bits(src[:n])
     return cache
 
 

@@ -315,6 +315,55 @@ float ebo_f16_to_f32(uint16_t h) {
     return sign ? -v : v;
 }
 
+/* OCP FP8 E4M3 ("e4m3fn": 1 sign bit, 4 exponent bits with bias 7, 3 fraction bits, no
+ * infinities, S.1111.111 is NaN, largest finite 448) bit pattern -> f32, from its fields
+ * (exact: every E4M3 value is an f32). Exponent 0 is subnormal: fraction * 2^-9. No
+ * counterpart in the reference, whose caches are f32. */
+float ebo_f8e4m3_to_f32(uint8_t b) {
+    const int sign = b >> 7, e = (b >> 3) & 15, f = b & 7;
+    float v;
+    if (e == 15 && f == 7)
+        v = NAN;
+    else if (e == 0)
+        v = ldexpf((float)f, -9);
+    else
+        v = ldexpf((float)(8 + f), e - 10);
+    return sign ? -v : v;
+}
+
+/* f32 -> E4M3 bit pattern, the FP8 cache's kv_write contract: the nearest E4M3 value, ties
+ * to the even fraction; finite values at or beyond 448 (the largest) saturate to +-448;
+ * inf and NaN become NaN (0x7F with the sign); the sign of zero is kept. Computed on the
+ * value grid: below 2^-6 the step is 2^-9, in [2^e, 2^(e+1)) it is 2^(e-3); the count of
+ * steps is rounded to nearest even in double (exact: the quotient has at most 24 bits). */
+uint8_t ebo_f8e4m3_bits(float x) {
+    const uint8_t s = signbit(x) ? 0x80 : 0;
+    if (isnan(x) || isinf(x)) return s | 0x7F;
+    const double a = fabs((double)x);
+    if (a >= 448.0) return s | 0x7E;
+    if (a == 0.0) return s;
+    int e;
+    frexp(a, &e);  /* a = m 2^e, m in [0.5, 1): a in [2^(e-1), 2^e) */
+    e -= 1;
+    if (e < -6) e = -6;
+    const double step = ldexp(1.0, e - 3);
+    const double v = rint(a / step) * step;  /* the nearest grid value, ties to even */
+    if (v < ldexp(1.0, -6)) return s | (uint8_t)(v / ldexp(1.0, -9));
+    int ev;
+    const double m = frexp(v, &ev);  /* v = m 2^ev, m in [0.5, 1) */
+    const int E = ev - 1 + 7;
+    const int F = (int)((2.0 * m - 1.0) * 8.0);
+    return (uint8_t)(s | (E << 3) | F);
+}
+
+void ebo_f8e4m3_bits_n(const float *x, uint8_t *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ebo_f8e4m3_bits(x[i]);
+}
+
+void ebo_f8e4m3_to_f32_n(const uint8_t *b, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ebo_f8e4m3_to_f32(b[i]);
+}
+
 /* linear_f16w's CPU reference (crates/eyebrowse-kernels/src/testutil.rs:68-80, the
  * weight rounded to f16 as the kernel reads it, matmul.rs:246-247,266-267):
  * y[i, o] = sum_k x[i, k] * w[o, k], f32 accumulation with k ascending. w holds the

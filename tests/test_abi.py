@@ -44,6 +44,7 @@ def test_status_and_dtype_tables():
                      "OutOfMemory", "Other"]
     # DType::size (crates/eyebrowse-core/src/lib.rs:14-24 and its test :31-38)
     assert [eb.DType(i).size() for i in range(4)] == [4, 2, 4, 4]
+    assert eb.DType.F8E4M3.size() == 1  # the E4M3 cache element (no reference counterpart)
     assert l.eb_pool_max_bytes() == 64 * 1024 * 1024
     assert b"gfx950" in l.eb_version()
 

@@ -1,0 +1,378 @@
+"""OCP FP8 E4M3 KV caches on the GPU against the oracle.
+
+The reference's caches are f32 (crates/eyebrowse-nn/src/kv_cache.rs:37,41); an E4M3 cache
+has no counterpart there. Its contract: kv_write stores the nearest E4M3 value (ties to the
+even fraction, finite values saturating at +-448, inf and NaN to NaN), bit-exact against
+oracle.f8_bits (pinned in tests/test_oracle.py against the bit fields, brute force and
+torch's float8_e4m3fn), and attention over the cache computes in f32 on the stored values.
+So every attention output is checked twice:
+- against the oracle on the rounded caches, at the FP32 bar (tests/_gpu.py): the E4M3
+  kernels must be the f32 kernels on different loads;
+- against the oracle on the unrounded f32 rows, at the format's own stated error: with 3
+  fraction bits a stored element is off by up to 2^-4 of itself, which the CPU oracle
+  measures at rel-L2 3.5e-2 to 4.2e-2 on N(0,1) caches at scale 1/sqrt(head_dim) (decode
+  and prompts); the bar here is F8_REL_L2 = 6e-2 at those scales (at Gemma-4's scale 1.0
+  the sharper scores amplify it to 0.16, and that case is checked against the rounded
+  caches only).
+"""
+import numpy as np
+import pytest
+
+import eyebrowse_amd as eb
+import oracle
+from tests._gpu import assert_bitwise, assert_close, note, upload
+from tests._textbook import rel_l2_f64
+
+pytestmark = pytest.mark.gpu
+
+F8_REL_L2 = 6e-2
+
+
+def f8_cache(dev, rows):
+    """An E4M3 cache tensor [max_seq, hkv, hd] holding f8_bits(rows), written by kv_write."""
+    rows = np.ascontiguousarray(rows, np.float32)
+    max_seq, hkv, hd = rows.shape
+    t = eb.Tensor.empty(dev, rows.shape, eb.DType.F8E4M3)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, t, upload(dev, rows), hkv, max_seq, hd, max_seq, 0)
+    rec.submit()
+    return t
+
+
+def bits_of(t):
+    return np.frombuffer(t.read_bytes(), np.uint8).copy()
+
+
+def rounded(a):
+    return oracle.f8_values(oracle.f8_bits(a)).reshape(np.shape(a))
+
+
+def check_both(got, q, kc, vc, h, hkv, pos0, rows, hd, sc, window, what, f32_bar=True):
+    """got against the oracle on the rounded caches (FP32 bar) and, at scales up to
+    1/sqrt(hd), on the f32 caches (F8_REL_L2)."""
+    want8 = oracle.attn_chunk(q, rounded(kc), rounded(vc), h, hkv, pos0, rows, hd, sc, window,
+                              threads=16)
+    assert_close(got, want8, what=f"{what} vs rounded-cache oracle")
+    if f32_bar:
+        want32 = oracle.attn_chunk(q, kc, vc, h, hkv, pos0, rows, hd, sc, window, threads=16)
+        r = rel_l2_f64(got, want32)
+        assert r <= F8_REL_L2, f"{what} vs f32 oracle: rel={r:.3e}"
+
+
+def test_kv_write_f8_bitwise_with_specials(dev):
+    """Rows of ordinary values, ties, saturation, subnormals, signed zero, inf and NaN,
+    written at an offset; the untouched rows keep their bytes."""
+    hkv, hd, max_seq, start, count = 2, 16, 12, 5, 4
+    note("kv_write f8 specials")
+    base = oracle.randn((max_seq, hkv, hd), 1)
+    t = f8_cache(dev, base)
+    assert np.array_equal(bits_of(t), oracle.f8_bits(base))
+    src = oracle.randn((count, hkv, hd), 2).ravel() * 30.0
+    specials = [1 + 2 ** -4, 1 + 3 * 2 ** -4, 448.0, 463.9, 464.0, 500.0, 3e38, -1e6, -0.0,
+                2 ** -9, 2 ** -10, 1.5 * 2 ** -9, 2.5 * 2 ** -9, 7.5 * 2 ** -9, 2 ** -6,
+                np.inf, -np.inf, np.nan, 0.1, -240.0, 1e-30, -3e-3]
+    src[:len(specials)] = np.array(specials, np.float32)
+    src = src.reshape(count, hkv, hd).astype(np.float32)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, t, upload(dev, src), hkv, count, hd, max_seq, start)
+    rec.submit()
+    got = bits_of(t)
+    want = oracle.kv_write_f8(oracle.f8_bits(base), src, hkv, count, hd, start)
+    bad = np.count_nonzero(got != want)
+    assert bad == 0, f"{bad} bytes differ"
+
+
+def test_kv_write_f8_prompt_sized_bitwise(dev):
+    """A Qwen3 prompt's K rows (4096 x 8 x 128) at row 100 of an 8192-row cache."""
+    hkv, hd, max_seq, start, count = 8, 128, 8192, 100, 4096
+    note("kv_write f8 qwen prompt")
+    src = oracle.randn((count, hkv, hd), 3) * 4.0
+    t = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F8E4M3)
+    rec = eb.Recorder(dev)
+    eb.kv_write(rec, t, upload(dev, src), hkv, count, hd, max_seq, start)
+    rec.submit()
+    got = bits_of(t)[start * hkv * hd:(start + count) * hkv * hd]
+    assert np.array_equal(got, oracle.f8_bits(src.ravel()))
+
+
+def test_every_pattern_through_decode_and_chunk(dev):
+    """All 256 E4M3 patterns as the V row of a single-key attention (o = v[0]): the
+    attention kernels' conversion of every pattern, NaN included, against the oracle's
+    field decoding."""
+    h, hkv, hd, max_seq = 2, 2, 128, 4
+    note("f8 every pattern")
+    codes = np.arange(256, dtype=np.uint8).reshape(1, hkv, hd)
+    vbytes = np.zeros((max_seq, hkv, hd), np.uint8)
+    vbytes[0] = codes
+    kt = f8_cache(dev, oracle.randn((max_seq, hkv, hd), 4))
+    vt = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F8E4M3)
+    vt.write(vbytes.tobytes())
+    want = oracle.f8_values(codes.ravel()).reshape(hkv, hd)
+    qt = upload(dev, oracle.randn((h, hd), 5))
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode(rec, qt, kt, vt, ot, h, hkv, 0, hd, max_seq, 0.1)
+    rec.submit()
+    o2 = eb.Tensor.empty(dev, (1, h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_prefill_chunk(rec, qt, kt, vt, o2, h, hkv, 0, 1, hd, max_seq, 0.1, 0)
+    rec.submit()
+    for got, what in ((ot.to_f32().reshape(h, hd), "decode"),
+                      (o2.to_f32().reshape(h, hd), "chunk")):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan), f"{what}: NaN positions"
+        # (values compared as numbers: -0 in the cache may come out as +0 after the sums)
+        assert np.array_equal(got[~nan], want[~nan]), f"{what}: decoded values"
+
+
+@pytest.mark.parametrize("h,hkv,hd,pos,window", [
+    (16, 8, 128, 8191, 0),    # Qwen3 decode at the bench's L
+    (16, 8, 128, 0, 0),       # first token: output is the v row
+    (16, 8, 128, 100, 0),     # one split
+    (32, 8, 128, 3000, 0),    # GQA 4 (Mistral)
+    (32, 8, 128, 32767, 0),   # Mistral at 32768 keys
+    (16, 8, 256, 5000, 0),    # hd 256 (Gemma)
+    (24, 8, 128, 2049, 0),    # g = 3
+    (32, 32, 128, 1500, 0),   # MHA
+    (8, 2, 64, 777, 0),       # hd 64
+    (8, 2, 80, 901, 0),       # hd 80 (lanes padded)
+    (4, 2, 8, 40, 0),         # smallest e4m3 head dim
+    (16, 8, 128, 6000, 1024), # sliding window
+    (4, 2, 16, 40, 1),        # window 1
+])
+def test_decode_f8_matches_oracle(dev, h, hkv, hd, pos, window):
+    note(f"decode f8 h={h} hkv={hkv} hd={hd} pos={pos} window={window}")
+    max_seq = pos + 3
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((h, hd), 1)
+    kc, vc = oracle.randn((max_seq, hkv, hd), 2), oracle.randn((max_seq, hkv, hd), 3)
+    kt, vt = f8_cache(dev, kc), f8_cache(dev, vc)
+    qt = upload(dev, q)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode_window(rec, qt, kt, vt, ot, h, hkv, pos, hd, max_seq, sc, window)
+    rec.submit()
+    check_both(ot.to_f32().reshape(1, h, hd), q.reshape(1, h, hd), kc, vc, h, hkv, pos, 1, hd,
+               sc, window, "decode f8", f32_bar=pos > 0)
+    if window == 0:
+        o2 = eb.Tensor.empty(dev, (h, hd))
+        rec = eb.Recorder(dev)
+        eb.attn_decode(rec, qt, kt, vt, o2, h, hkv, pos, hd, max_seq, sc)
+        rec.submit()
+        assert_bitwise(o2.to_f32(), ot.to_f32(), "attn_decode vs window 0")
+
+
+def test_decode_f8_gemma_scale(dev):
+    """Gemma-4 shape at its scale 1.0 (against the rounded caches only; see the header)."""
+    h, hkv, hd, pos = 16, 8, 256, 16383
+    note("decode f8 gemma scale 1.0")
+    max_seq = pos + 1
+    q = oracle.randn((h, hd), 1) * 0.0625
+    kc, vc = oracle.randn((max_seq, hkv, hd), 2), oracle.randn((max_seq, hkv, hd), 3)
+    kt, vt = f8_cache(dev, kc), f8_cache(dev, vc)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode(rec, upload(dev, q), kt, vt, ot, h, hkv, pos, hd, max_seq, 1.0)
+    rec.submit()
+    check_both(ot.to_f32().reshape(1, h, hd), q.reshape(1, h, hd), kc, vc, h, hkv, pos, 1, hd,
+               1.0, 0, "decode f8 gemma", f32_bar=False)
+
+
+@pytest.mark.parametrize("h,hkv,hd,pos,window", [
+    (16, 8, 128, 8191, 0),
+    (16, 8, 128, 0, 0),
+    (32, 8, 128, 4097, 0),
+    (16, 8, 256, 3001, 512),
+    (4, 2, 8, 9, 0),
+    (8, 2, 96, 300, 0),
+])
+def test_decode_step_f8(dev, h, hkv, hd, pos, window):
+    """The fused step: the new rows land in the cache as f8_bits, the output is attention
+    over the cache as it then stands."""
+    note(f"decode step f8 h={h} hd={hd} pos={pos} window={window}")
+    max_seq = pos + 2
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((h, hd), 4)
+    kc, vc = oracle.randn((max_seq, hkv, hd), 5), oracle.randn((max_seq, hkv, hd), 6)
+    knew, vnew = oracle.randn((1, hkv, hd), 7), oracle.randn((1, hkv, hd), 8)
+    kt, vt = f8_cache(dev, kc), f8_cache(dev, vc)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode_step_window(rec, upload(dev, q), upload(dev, knew), upload(dev, vnew), kt, vt,
+                               ot, h, hkv, pos, hd, max_seq, sc, window)
+    rec.submit()
+    kw = oracle.kv_write_f8(oracle.f8_bits(kc), knew, hkv, 1, hd, pos)
+    vw = oracle.kv_write_f8(oracle.f8_bits(vc), vnew, hkv, 1, hd, pos)
+    assert np.array_equal(bits_of(kt), kw), "K cache bits"
+    assert np.array_equal(bits_of(vt), vw), "V cache bits"
+    k32 = oracle.kv_write(kc, knew, hkv, 1, hd, pos).reshape(max_seq, hkv, hd)
+    v32 = oracle.kv_write(vc, vnew, hkv, 1, hd, pos).reshape(max_seq, hkv, hd)
+    check_both(ot.to_f32().reshape(1, h, hd), q.reshape(1, h, hd), k32, v32, h, hkv, pos, 1, hd,
+               sc, window, "decode step f8", f32_bar=pos > 0)
+
+
+@pytest.mark.parametrize("h,hkv,hd,pos0,rows,window", [
+    (16, 8, 128, 0, 300, 0),      # a prompt over the cache (pre-split records)
+    (16, 8, 128, 100, 77, 0),     # continuation chunk
+    (32, 8, 128, 1000, 96, 0),    # GQA 4
+    (16, 8, 256, 513, 40, 0),     # hd 256
+    (4, 2, 8, 5, 3, 0),           # hd 8
+    (24, 8, 128, 10, 50, 0),      # g = 3
+    (16, 8, 128, 300, 129, 100),  # windowed continuation
+    (8, 2, 80, 200, 150, 0),      # hd 80 (padded instantiation)
+])
+def test_chunk_f8_matches_oracle(dev, h, hkv, hd, pos0, rows, window):
+    note(f"chunk f8 h={h} hd={hd} pos0={pos0} rows={rows} window={window}")
+    max_seq = pos0 + rows + 5
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((rows, h, hd), 9)
+    kc, vc = oracle.randn((max_seq, hkv, hd), 10), oracle.randn((max_seq, hkv, hd), 11)
+    kt, vt = f8_cache(dev, kc), f8_cache(dev, vc)
+    ot = eb.Tensor.empty(dev, (rows, h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_prefill_chunk(rec, upload(dev, q), kt, vt, ot, h, hkv, pos0, rows, hd, max_seq, sc,
+                          window)
+    rec.submit()
+    check_both(ot.to_f32().reshape(rows, h, hd), q, kc, vc, h, hkv, pos0, rows, hd, sc, window,
+               "chunk f8")
+
+
+def test_qwen_prompt_over_f8_cache(dev):
+    """Qwen3 T=4096 prompt as one chunk over an E4M3 cache (pre-split records from the
+    E4M3 rows), every row against the oracle on the rounded cache."""
+    h, hkv, hd, T = 16, 8, 128, 4096
+    note("chunk f8 qwen T=4096")
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((T, h, hd), 12)
+    kc, vc = oracle.randn((T, hkv, hd), 13), oracle.randn((T, hkv, hd), 14)
+    kt, vt = f8_cache(dev, kc), f8_cache(dev, vc)
+    ot = eb.Tensor.empty(dev, (T, h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_prefill_chunk(rec, upload(dev, q), kt, vt, ot, h, hkv, 0, T, hd, T, sc)
+    rec.submit()
+    got = ot.to_f32().reshape(T, h, hd)
+    want = oracle.attn_chunk(q, rounded(kc), rounded(vc), h, hkv, 0, T, hd, sc, threads=16)
+    assert_close(got, want, what="qwen T=4096 over e4m3")
+
+
+def test_raw_f8_launches(dev):
+    """The stream-level E4M3 entry points on caller memory (library buffers), on the
+    device's stream: kv_write, chunk (plain and with a workspace), decode, fused step."""
+    note("raw f8 launches")
+    h, hkv, hd, max_seq = 16, 8, 128, 700
+    sc = 0.08
+    kc, vc = oracle.randn((max_seq, hkv, hd), 20), oracle.randn((max_seq, hkv, hd), 21)
+    kt = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F8E4M3)
+    vt = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F8E4M3)
+    ks, vs = upload(dev, kc), upload(dev, vc)
+    for dst, src in ((kt, ks), (vt, vs)):
+        eb.launch_kv_write_f8(dev.stream, dst.data_ptr, dst.numel(), src.data_ptr, src.numel(),
+                              hkv, max_seq, hd, max_seq, 0)
+    dev.synchronize()
+    assert np.array_equal(bits_of(kt), oracle.f8_bits(kc.ravel()))
+
+    pos0, rows = 300, 400
+    q = oracle.randn((rows, h, hd), 22)
+    qt = upload(dev, q)
+    ot = eb.Tensor.empty(dev, (rows, h, hd))
+    eb.launch_attn_prefill_chunk_f8(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr,
+                                    kt.numel(), vt.data_ptr, vt.numel(), ot.data_ptr,
+                                    ot.numel(), h, hkv, pos0, rows, hd, max_seq, sc, 64)
+    dev.synchronize()
+    check_both(ot.to_f32().reshape(rows, h, hd), q, kc, vc, h, hkv, pos0, rows, hd, sc, 64,
+               "raw chunk f8")
+    need = eb.attn_prefill_workspace_floats(h, hkv, hd, pos0, rows, 0)
+    assert need > 0
+    wsp = upload(dev, np.full(need, np.nan, np.float32))
+    o3 = eb.Tensor.empty(dev, (rows, h, hd))
+    eb.launch_attn_prefill_chunk_ws(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(),
+                                    vt.data_ptr, vt.numel(), o3.data_ptr, o3.numel(), h, hkv,
+                                    pos0, rows, hd, max_seq, sc, 0, wsp.data_ptr, need, f8=True)
+    dev.synchronize()
+    check_both(o3.to_f32().reshape(rows, h, hd), q, kc, vc, h, hkv, pos0, rows, hd, sc, 0,
+               "raw chunk f8 with workspace")
+
+    pos = 650
+    q1 = upload(dev, q[0])
+    o1 = eb.Tensor.empty(dev, (h, hd))
+    cus = dev.cu_count
+    need = eb.attn_decode_workspace_floats(h, hkv, pos, hd, cus)
+    ws = upload(dev, np.full(max(need, 1), np.nan, np.float32))
+    eb.launch_attn_decode_f8(dev.stream, q1.data_ptr, q1.numel(), kt.data_ptr, kt.numel(),
+                             vt.data_ptr, vt.numel(), o1.data_ptr, o1.numel(), h, hkv, pos, hd,
+                             max_seq, sc, 0, ws.data_ptr, need, cus)
+    dev.synchronize()
+    check_both(o1.to_f32().reshape(1, h, hd), q[0].reshape(1, h, hd), kc, vc, h, hkv, pos, 1,
+               hd, sc, 0, "raw decode f8")
+
+    knew, vnew = oracle.randn((1, hkv, hd), 23), oracle.randn((1, hkv, hd), 24)
+    kn, vn = upload(dev, knew), upload(dev, vnew)
+    eb.launch_attn_decode_step_f8(dev.stream, q1.data_ptr, q1.numel(), kn.data_ptr,
+                                  vn.data_ptr, kn.numel(), kt.data_ptr, kt.numel(), vt.data_ptr,
+                                  vt.numel(), o1.data_ptr, o1.numel(), h, hkv, pos, hd, max_seq,
+                                  sc, 0, ws.data_ptr, need, cus)
+    dev.synchronize()
+    assert np.array_equal(bits_of(kt), oracle.kv_write_f8(oracle.f8_bits(kc), knew, hkv, 1,
+                                                          hd, pos))
+    k32 = oracle.kv_write(kc, knew, hkv, 1, hd, pos).reshape(max_seq, hkv, hd)
+    v32 = oracle.kv_write(vc, vnew, hkv, 1, hd, pos).reshape(max_seq, hkv, hd)
+    check_both(o1.to_f32().reshape(1, h, hd), q[0].reshape(1, h, hd), k32, v32, h, hkv, pos, 1,
+               hd, sc, 0, "raw decode step f8")
+
+
+def test_f8_cache_refusals(dev):
+    """Head dims below 8 and mixed cache pairs are refused before any launch."""
+    note("f8 refusals")
+    h, hkv, hd, max_seq = 4, 2, 4, 16
+    k8 = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F8E4M3)
+    v8 = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F8E4M3)
+    v16 = eb.Tensor.empty(dev, (max_seq, hkv, hd), eb.DType.F16)
+    q = eb.Tensor.empty(dev, (h, hd))
+    o = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    with pytest.raises(eb.UnsupportedConfig):
+        eb.attn_decode(rec, q, k8, v8, o, h, hkv, 3, hd, max_seq, 0.5)
+    with pytest.raises((eb.ShapeMismatch, eb.UnsupportedConfig)):
+        eb.attn_decode(rec, q, k8, v16, o, h, hkv, 3, hd, max_seq, 0.5)
+    rec.submit()
+
+
+def test_attention_forward_with_f8_cache(dev):
+    """Attention.forward_qkv over an E4M3 KvCache: a 300-row prompt, a 50-row continuation
+    and three decode steps. Each output against the oracle on the cache as the layer left
+    it (FP32 bar), and against the same layer over an f32 cache (F8_REL_L2)."""
+    H, Hkv, hd, max_seq = 16, 8, 128, 512
+    note("attention forward f8 cache")
+    sc = float(oracle.default_scale(hd))
+    attn = eb.Attention(H, Hkv, hd, sc)
+    rope = eb.Rope.build(dev, max_seq, hd, 1e6)
+    kv8 = eb.KvCache.new(dev, 1, max_seq, Hkv, hd, eb.DType.F8E4M3)
+    kv32 = eb.KvCache.new(dev, 1, max_seq, Hkv, hd)
+    assert kv8.dtype == eb.DType.F8E4M3 and kv8.k[0].dtype == eb.DType.F8E4M3
+    spans = [(0, 300), (300, 350), (350, 351), (351, 352), (352, 353)]
+    n = spans[-1][1]
+    xq = oracle.randn((n, H * hd), 51)
+    xk = oracle.randn((n, Hkv * hd), 52)
+    xv = oracle.randn((n, Hkv * hd), 53)
+    for a, b in spans:
+        rows = b - a
+        outs = []
+        for kv in (kv8, kv32):
+            rec = eb.Recorder(dev)
+            qt = upload(dev, xq[a:b])
+            out = attn.forward_qkv(rec, qt, upload(dev, xk[a:b]), upload(dev, xv[a:b]), rope, kv,
+                                   0, rows, a)
+            qr = eb.Tensor.empty(dev, (rows, H, hd))
+            eb.rope(rec, qt, rope.cos, rope.sin, qr, rows, H, hd, a)
+            rec.submit()
+            outs.append((out.to_f32().reshape(rows, H, hd), qr.to_f32().reshape(rows, H, hd)))
+        (o8, qr), (o32, _) = outs
+        kc = oracle.f8_values(bits_of(kv8.k[0])).reshape(max_seq, Hkv, hd)
+        vc = oracle.f8_values(bits_of(kv8.v[0])).reshape(max_seq, Hkv, hd)
+        k32 = kv32.k[0].to_f32().reshape(max_seq, Hkv, hd)
+        assert np.array_equal(oracle.f8_bits(k32[:b]).ravel(), bits_of(kv8.k[0])[:b * Hkv * hd]), \
+            "e4m3 cache rows are the f32 layer's rows rounded"
+        want = oracle.attn_chunk(qr, kc, vc, H, Hkv, a, rows, hd, sc, threads=16)
+        assert_close(o8, want, what=f"span {a}..{b} vs oracle on the e4m3 cache")
+        r = rel_l2_f64(o8, o32)
+        assert r <= F8_REL_L2, f"span {a}..{b} vs f32-cache layer: rel={r:.3e}"

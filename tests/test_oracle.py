@@ -396,6 +396,90 @@ def test_kv_write_f16_places_rounded_rows():
     assert np.max(np.abs(oracle.f16_values(got[a:b]) - src.ravel())) <= 2.0 ** -11 * 4
 
 
+def _e4m3_to_f64(bits):
+    """OCP E4M3 decoded from its fields (sign, 4-bit exponent bias 7, 3-bit fraction; no
+    infinities, S.1111.111 NaN)."""
+    b = np.asarray(bits, np.int64)
+    sign = np.where(b >> 7, -1.0, 1.0)
+    e = (b >> 3) & 15
+    f = (b & 7).astype(np.float64)
+    val = np.where(e == 0, f * 2.0 ** -9, (8 + f) * 2.0 ** (e - 10))
+    val = np.where((e == 15) & (f == 7), np.nan, val)
+    return sign * val
+
+
+def test_f8_decode_every_pattern():
+    """All 256 patterns against the bit fields and against torch's float8_e4m3fn (an
+    independent implementation of the format): 448 largest, 2^-9 smallest subnormal,
+    2^-6 smallest normal, 0x7F / 0xFF NaN, signed zeros."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    got = oracle.f8_values(codes)
+    want = _e4m3_to_f64(codes)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan) and list(np.flatnonzero(nan)) == [0x7F, 0xFF]
+    assert np.array_equal(got[~nan].astype(np.float64), want[~nan])
+    assert np.array_equal(np.signbit(got[~nan]), codes[~nan] >= 0x80)
+    tch = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(got[~nan].view(np.uint32), tch[~nan].view(np.uint32))
+    pos = got[:0x7F]
+    assert np.all(np.diff(pos) > 0) and pos[-1] == 448.0
+    assert pos[1] == 2.0 ** -9 and pos[8] == 2.0 ** -6
+
+
+def test_f8_bits_known_answers():
+    """Hand-derived patterns: ties to the even fraction (1 + 2^-4 -> 1, 1 + 3 * 2^-4 -> 1.25,
+    464 -> 448, 1.5 * 2^-9 -> 2^-8), saturation of finite values at and beyond 448, inf and
+    NaN to NaN, signed zero, subnormal steps of 2^-9."""
+    cases = [(1.0, 0x38), (1 + 2 ** -4, 0x38), (1 + 3 * 2 ** -4, 0x3A), (-2.0, 0xC0),
+             (448.0, 0x7E), (463.9, 0x7E), (464.0, 0x7E), (500.0, 0x7E), (3e38, 0x7E),
+             (-1e6, 0xFE), (0.0, 0x00), (-0.0, 0x80), (2 ** -9, 0x01), (2 ** -10, 0x00),
+             (1.5 * 2 ** -9, 0x02), (2.5 * 2 ** -9, 0x02), (7.5 * 2 ** -9, 0x08),
+             (2 ** -6, 0x08), (0.1, 0x1D), (240.0, 0x77), (416.0, 0x7D)]
+    got = oracle.f8_bits(np.array([c[0] for c in cases], np.float32))
+    assert [int(g) for g in got] == [c[1] for c in cases]
+    special = oracle.f8_bits(np.array([np.inf, -np.inf, np.nan, -np.nan], np.float32))
+    assert [int(g) for g in special] == [0x7F, 0xFF, 0x7F, 0xFF]
+
+
+def test_f8_bits_nearest_even_and_torch():
+    """Random values over the whole range and every midpoint between neighbouring values
+    (with the f32 neighbours either side): the result is a nearest E4M3 value (ties to the
+    even fraction), and below 448 it equals torch's float8_e4m3fn conversion bit for bit."""
+    import torch
+    x = np.concatenate([oracle.randn((40000,), 11) * s for s in (2e-3, 0.05, 1.0, 20.0, 150.0)])
+    fin = _e4m3_to_f64(np.arange(0x7F))  # the finite non-negative values, ascending
+    mids = ((fin[1:] + fin[:-1]) / 2).astype(np.float32)
+    x = np.concatenate([x, mids, -mids, np.nextafter(mids, np.float32(0)),
+                        np.nextafter(mids, np.float32(1e9))]).astype(np.float32)
+    bits = oracle.f8_bits(x).astype(np.int64)
+    assert np.array_equal(bits >> 7, np.signbit(x).astype(np.int64))
+    ax = np.abs(x.astype(np.float64))
+    mag = np.abs(_e4m3_to_f64(bits))
+    inr = ax < 448
+    d = np.abs(ax[:, None] - fin[None, :])[inr]   # brute force over every finite value
+    best = d.min(axis=1)
+    assert np.all(np.abs(ax[inr] - mag[inr]) == best)
+    tie = (d == best[:, None]).sum(axis=1) > 1
+    assert np.all((bits[inr][tie] & 1) == 0)
+    assert np.all(mag[~inr] == 448.0)
+    y = x[inr]
+    tch = torch.from_numpy(y).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.f8_bits(y), tch)
+
+
+def test_kv_write_f8_places_rounded_rows():
+    hkv, hd, count, start, max_seq = 2, 16, 3, 4, 9
+    cache = (np.arange(max_seq * hkv * hd) % 251).astype(np.uint8)
+    src = oracle.randn((count, hkv, hd), 8)
+    got = oracle.kv_write_f8(cache, src, hkv, count, hd, start)
+    a, b = start * hkv * hd, (start + count) * hkv * hd
+    assert np.array_equal(got[:a], cache[:a]) and np.array_equal(got[b:], cache[b:])
+    assert np.array_equal(got[a:b], oracle.f8_bits(src.ravel()))
+    err = np.abs(oracle.f8_values(got[a:b]) - src.ravel())
+    assert np.all(err <= np.maximum(np.abs(src.ravel()) * 2.0 ** -4, 2.0 ** -10))
+
+
 # ------------------------------------------------------------------ linear_f16w / argmax --
 
 def test_f16_decode_matches_numpy_for_every_pattern():
