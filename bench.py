@@ -24,7 +24,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --only trace --workload NAME   (one workload, for rocprofv3)
        python bench.py --trace-summary OUT.md TITLE CMD LABEL=CSV ...   (no GPU)
        python bench.py --pmc-summary FETCH.csv WRITE.csv OUT.json       (no GPU)
-       python bench.py --sq-summary OUT.md CMD CSV                       (no GPU)
+       python bench.py --sq-summary OUT.md CMD CSV [CSV ...]             (no GPU)
 """
 from __future__ import annotations
 
@@ -686,14 +686,17 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
                 return None
             t += kernels[k]["fetch_bytes"] + kernels[k]["write_bytes"]
         return t
-    out["decode_mistral_keys32768"] = total(r"decode_kernel<128, 4, false>",
+    # (template arguments: decode_kernel<head_dim, heads per workgroup, cache element bytes>,
+    # presplit_kernel<head_dim, element bytes>, prefill_kernel<head_dim, heads, row blocks,
+    # key splits, range, element bytes, pre-split records, f16 mode>)
+    out["decode_mistral_keys32768"] = total(r"decode_kernel<128, 4, 4>",
                                             r"decode_merge_kernel<128>")
-    out["prefill_mistral_T4096"] = total(r"presplit_kernel<128, false>",
-                                         r"prefill_kernel<128, 4, 1, 1, false, false, true>")
-    out["decode_gemma_keys16384"] = total(r"decode_kernel<256, 2, false>",
+    out["prefill_mistral_T4096"] = total(r"presplit_kernel<128, 4>",
+                                         r"prefill_kernel<128, 4, 1, 1, false, 4, true, false>")
+    out["decode_gemma_keys16384"] = total(r"decode_kernel<256, 2, 4>",
                                           r"decode_merge_kernel<256>")
-    out["prefill_gemma_T4096"] = total(r"presplit_kernel<256, false>",
-                                       r"prefill_kernel<256, 2, 2, 1, false, false, true>")
+    out["prefill_gemma_T4096"] = total(r"presplit_kernel<256, 4>",
+                                       r"prefill_kernel<256, 2, 2, 1, false, 4, true, false>")
     json.dump(out, open(out_json, "w"), indent=1)
     print(json.dumps(out, indent=1))
 
@@ -729,39 +732,49 @@ def trace_summary(out_md: str, title: str, cmd: str, labelled: list) -> None:
     print("\n".join(lines))
 
 
-def sq_summary(out_md: str, cmd: str, csv_path: str) -> None:
-    """Per-dispatch averages of the SQ / GRBM counters of one rocprofv3 --pmc run, per
-    kernel and grid (the counters are whole-chip totals per dispatch), with: VALU
-    instructions per MFMA instruction; MFMA busy cycles per MFMA instruction; the share of
-    wave cycles spent waiting on any instruction; and the matrix pipe's busy share,
-    SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x GRBM_GUI_ACTIVE / 8), GRBM_GUI_ACTIVE being the
-    sum of the 8 XCDs' busy cycles (so the share is of the cycles the kernel ran, at the
-    clock it ran at)."""
+def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
+    """Per-dispatch averages of the SQ / GRBM counters of one or more rocprofv3 --pmc runs
+    (each run averaged over its own dispatches, then merged per kernel and grid; the
+    counters are whole-chip totals per dispatch), with: VALU instructions per MFMA
+    instruction; MFMA busy cycles per MFMA instruction; the share of wave cycles spent
+    waiting on any instruction, and on LDS instructions; LDS bank-conflict cycles per
+    LDS-active cycle; and the matrix pipe's busy share, SQ_VALU_MFMA_BUSY_CYCLES /
+    (1024 SIMDs x GRBM_GUI_ACTIVE / 8), GRBM_GUI_ACTIVE being the sum of the 8 XCDs' busy
+    cycles (so the share is of the cycles the kernel ran, at the clock it ran at)."""
     import csv
-    tot, disp = {}, {}
-    for r in csv.DictReader(open(csv_path)):
-        key = (_kernel_name(r["Kernel_Name"]), r.get("Grid_Size", ""))
-        c = tot.setdefault(key, {})
-        c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
-        disp.setdefault(key, set()).add(r["Dispatch_Id"])
-    names = sorted({n for c in tot.values() for n in c})
+    merged, ndisp = {}, {}
+    for path in csv_paths:
+        tot, disp = {}, {}
+        for r in csv.DictReader(open(path)):
+            key = (_kernel_name(r["Kernel_Name"]), r.get("Grid_Size", ""))
+            c = tot.setdefault(key, {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            disp.setdefault(key, set()).add(r["Dispatch_Id"])
+        for key, c in tot.items():
+            n = len(disp[key])
+            m = merged.setdefault(key, {})
+            for k, v in c.items():
+                m.setdefault(k, v / n)  # (a counter in two runs: the first run's average)
+            ndisp[key] = max(ndisp.get(key, 0), n)
+    names = sorted({n for c in merged.values() for n in c})
     lines = ["# SQ counters per dispatch", "", "Command (from the repository root on the GPU "
              "box, `R=$PWD`):", "", "```", cmd, "```", "",
              "| kernel | grid | dispatches | " + " | ".join(names) +
-             " | VALU/MFMA | MFMA busy cyc/MFMA | wait share | MFMA pipe busy |",
-             "|---" * (3 + len(names) + 4) + "|"]
-    for key, c in tot.items():
-        n = len(disp[key])
-        avg = {k: v / n for k, v in c.items()}
+             " | VALU/MFMA | MFMA busy cyc/MFMA | wait share | LDS wait share |"
+             " LDS conflict/active | MFMA pipe busy |",
+             "|---" * (3 + len(names) + 6) + "|"]
+    for key, avg in merged.items():
         mf = avg.get("SQ_INSTS_MFMA", 0)
         ratio = lambda a, b: f"{a / b:.2f}" if b else "-"  # noqa: E731
-        lines.append(f"| `{key[0]}` | {key[1]} | {n} | " +
-                     " | ".join(f"{avg.get(k, 0):.0f}" for k in names) + " | " +
+        lines.append(f"| `{key[0]}` | {key[1]} | {ndisp[key]} | " +
+                     " | ".join(f"{avg[k]:.0f}" if k in avg else "-" for k in names) + " | " +
                      ratio(avg.get("SQ_INSTS_VALU", 0), mf) + " | " +
                      ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0), mf) + " | " +
                      ratio(avg.get("SQ_WAIT_INST_ANY", 0), avg.get("SQ_WAVE_CYCLES", 0)) + " | " +
-                     ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0),
-                           1024 * avg.get("GRBM_GUI_ACTIVE", 0) / 8) + " |")
+                     ratio(avg.get("SQ_WAIT_INST_LDS", 0), avg.get("SQ_WAVE_CYCLES", 0)) + " | " +
+                     ratio(avg.get("SQ_LDS_BANK_CONFLICT", 0), avg.get("SQ_LDS_IDX_ACTIVE", 0)) +
+                     " | " + ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0),
+                                   1024 * avg.get("GRBM_GUI_ACTIVE", 0) / 8) + " |")
     open(out_md, "w").write("\n".join(lines) + "\n")
     print("\n".join(lines))
 
@@ -835,7 +848,7 @@ def prefill_roofline(eb, hip, dev, sc128, reps: int = 20, fast: bool = False) ->
             "bound": "mfma",
             "config": "mistral-7b-shaped causal prefill, T=4096, 32 q / 8 KV heads, head_dim "
                       "128, f32 q/k/v (BASELINE configs[3]), opt-in f16 mode",
-            "kernel": "preconvert_kernel<128> + prefill_kernel<128,4,1,1,false,false,true,true>",
+            "kernel": "preconvert_kernel<128> + prefill_kernel<128, 4, 1, 1, false, 4, true, true>",
             "mfma": "v_mfma_f32_32x32x16_f16, one product per product: q, K, V, P rounded to "
                     "f16 once, f32 softmax and accumulation",
             "tolerance": "rel-L2 <= 1e-3 and max-abs <= 2e-3 vs the f32 oracle (measured "
@@ -860,7 +873,7 @@ def prefill_roofline(eb, hip, dev, sc128, reps: int = 20, fast: bool = False) ->
         "bound": "mfma",
         "config": "mistral-7b-shaped causal prefill, T=4096, 32 q / 8 KV heads, head_dim 128, "
                   "f32 q/k/v (BASELINE configs[3])",
-        "kernel": "presplit_kernel<128,false> + prefill_kernel<128,4,1,1,false,false,true>",
+        "kernel": "presplit_kernel<128, 4> + prefill_kernel<128, 4, 1, 1, false, 4, true, false>",
         "mfma": "v_mfma_f32_32x32x16_f16 on exact f16 hi/lo splits of the f32 operands, "
                 "three products per product (f32-accurate), f32 accumulation",
         "achieved": round(tf, 2), "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -891,7 +904,7 @@ def main():
                          "WRITE_SIZE passes over `--only traffic` into per-kernel HBM bytes")
     ap.add_argument("--trace-summary", nargs="+", metavar="ARG",
                     help="no GPU: OUT_MD TITLE CMD LABEL=KERNEL_TRACE_CSV ...")
-    ap.add_argument("--sq-summary", nargs=3, metavar=("OUT_MD", "CMD", "CSV"),
+    ap.add_argument("--sq-summary", nargs="+", metavar="ARG",
                     help="no GPU: per-kernel SQ counter table of a --pmc run")
     ap.add_argument("--only", choices=["headline", "all", "prefill", "projections", "layer",
                                        "traffic", "trace"], default="all",
@@ -910,6 +923,8 @@ def main():
         trace_summary(out_md, title, cmd, labelled)
         return
     if args.sq_summary:
+        if len(args.sq_summary) < 3:
+            raise SystemExit("--sq-summary OUT_MD CMD CSV [CSV ...]")
         sq_summary(*args.sq_summary)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1005,7 +1020,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_kernel<128,4,false> (new-row write + split-KV pass) + "
+            "kernel": "decode_kernel<128, 4, 4> (new-row write + split-KV pass) + "
                       "decode_merge_kernel<128>",
             "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -697,7 +697,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         //  softmax: the online softmax update (m, l, the O^T unit E, the rescale of O^T) and
         //           the P^T operands;
         //  pv:      O^T += V^T P^T from buffer b.
-        auto tile_qk = [&](int b, floatx16 &sacc) {
+        auto tile_qk = [&](int b, floatx16 &sacc, int (&ek)[16]) {
             const float *Kb = smem + b * C::BUF + ks * kTile * KS;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
@@ -713,16 +713,10 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
                     sacc = mfma16(al, qh[k2], sacc);
                 }
             }
-        };
-
-        auto tile_softmax = [&](int b, int kb, const floatx16 &sacc, f16x8 (&ph)[2],
-                                f16x8 (&pl)[2]) {
-            // Scores back from the split's units: 2^(eq + ek), ek the exponent of each of this
-            // lane's keys.
-            float p[16];
+            // the exponent of each of this lane's keys
             if constexpr (FAST) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) p[r] = sacc[r];
+                for (int r = 0; r < 16; ++r) ek[r] = 0;
             } else {
                 const int *Eb = reinterpret_cast<const int *>(smem + b * C::BUF +
                                                               C::STEP_KEYS * KS + C::VFL) +
@@ -730,12 +724,20 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4) {
                     const int4 e4 = *reinterpret_cast<const int4 *>(Eb + 8 * s4 + 4 * hf);
-                    p[4 * s4 + 0] = ldexpf(sacc[4 * s4 + 0], eq + e4.x);
-                    p[4 * s4 + 1] = ldexpf(sacc[4 * s4 + 1], eq + e4.y);
-                    p[4 * s4 + 2] = ldexpf(sacc[4 * s4 + 2], eq + e4.z);
-                    p[4 * s4 + 3] = ldexpf(sacc[4 * s4 + 3], eq + e4.w);
+                    ek[4 * s4 + 0] = e4.x;
+                    ek[4 * s4 + 1] = e4.y;
+                    ek[4 * s4 + 2] = e4.z;
+                    ek[4 * s4 + 3] = e4.w;
                 }
             }
+        };
+
+        auto tile_softmax = [&](int b, int kb, const floatx16 &sacc, const int (&ek)[16],
+                                f16x8 (&ph)[2], f16x8 (&pl)[2]) {
+            // Scores back from the split's units: 2^(eq + ek).
+            float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = FAST ? sacc[r] : ldexpf(sacc[r], eq + ek[r]);
             // Online softmax over this tile's keys (log2 domain). Only tiles that reach past
             // the wave's first position, or (window) below its last position's window, need
             // the per-key mask.
@@ -879,14 +881,15 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         };
 
         floatx16 sacc;
+        int ek[16];
         f16x8 ph[2], pl[2];
         for (int it = 0; it < nsteps; ++it) {
             const int buf = it & 1;
             const int tile = c_lo + it * KSPLIT + ks;
             prefetch(it + 1, buf ^ 1);
             if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
-                tile_qk(buf, sacc);
-                tile_softmax(buf, tile * kTile, sacc, ph, pl);
+                tile_qk(buf, sacc, ek);
+                tile_softmax(buf, tile * kTile, sacc, ek, ph, pl);
                 tile_pv(buf, ph, pl);
             }
             stage(buf ^ 1);
@@ -1451,11 +1454,11 @@ eb_status launch_prefill_fast_t(hipStream_t st, const float *q, const float *k, 
                 k, v, r.ws, r.nkeys, Hkv, nt, r.hdr);
             const eb_status err = eb::check_launch("attn_prefill_fast (pre-convert)");
             if (err != EB_OK) return err;
-            return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, true, true>(
+            return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, true, true>(
                 st, q, k, v, r.ws, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
         }
     }
-    return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, false, false, true>(
+    return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, false, true>(
         st, q, k, v, nullptr, o, H, Hkv, r, sl2, ch, nullptr, nullptr);
 }
 

@@ -2,8 +2,8 @@
 
 Each case draws head_dim, GQA ratio, lengths, positions, window, scale and cache dtype
 from a fixed seed, so the sweep crosses the paths the fixed cases take one at a time
-(pre-split pass on or off, key chunks, sliding windows, IEEE-half caches, split-KV decode
-with the fused new-token step) at shapes none of them uses. The oracle is the reference's
+(pre-split pass on or off, key chunks, sliding windows, IEEE-half and E4M3 caches, split-KV
+decode with the fused new-token step) at shapes none of them uses. The oracle is the reference's
 CPU attention restated in oracle/oracle.c (testutil.rs:130-218) with the chunk/window
 extension (attn_chunk); outputs are held to the FP32 bar of tests/_gpu.py on the rows
 each case samples.
@@ -18,6 +18,26 @@ from tests._gpu import assert_bitwise, assert_close, note, upload
 pytestmark = pytest.mark.gpu
 
 HDS = (4, 8, 16, 32, 64, 128, 256)
+
+
+def cache_kind(narrow, seed):
+    """The cache element type of a case: f32, or (narrow) IEEE half, or E4M3 for every
+    third seed (drawn without the case's generator, so its other draws stay put)."""
+    if not narrow:
+        return "f32"
+    return "f8" if seed % 3 == 0 else "f16"
+
+
+def rounded(a, kind):
+    """The values a cache of this kind holds for the f32 rows a."""
+    if kind == "f16":
+        return oracle.f16_values(oracle.f16_bits(a)).reshape(a.shape)
+    if kind == "f8":
+        return oracle.f8_values(oracle.f8_bits(a)).reshape(a.shape)
+    return a
+
+
+DTYPE = {"f32": eb.DType.F32, "f16": eb.DType.F16, "f8": eb.DType.F8E4M3}
 
 
 def draw(seed):
@@ -54,21 +74,20 @@ def test_random_chunk(dev, seed):
     pos0 = int(r.integers(0, 1500))
     rows = int(r.integers(1, 400))
     window = int(r.choice((0, 0, 1, 17, 200, 5000)))
-    f16 = hd >= 8 and bool(r.integers(0, 2))
+    kind = cache_kind(hd >= 8 and bool(r.integers(0, 2)), seed)
     max_seq = pos0 + rows + int(r.integers(0, 9))
     note(f"random chunk seed={seed} h={h} hkv={hkv} hd={hd} pos0={pos0} rows={rows} "
-         f"window={window} f16={f16}")
+         f"window={window} cache={kind}")
     q = oracle.randn((rows, h, hd), 7 * seed + 1)
     kc, vc = oracle.randn((max_seq, hkv, hd), 7 * seed + 2), oracle.randn((max_seq, hkv, hd), 7 * seed + 3)
-    if f16:
-        kt = eb.Tensor.empty(dev, kc.shape, eb.DType.F16)
-        vt = eb.Tensor.empty(dev, vc.shape, eb.DType.F16)
+    if kind != "f32":
+        kt = eb.Tensor.empty(dev, kc.shape, DTYPE[kind])
+        vt = eb.Tensor.empty(dev, vc.shape, DTYPE[kind])
         rec = eb.Recorder(dev)
         eb.kv_write(rec, kt, upload(dev, kc), hkv, max_seq, hd, max_seq, 0)
         eb.kv_write(rec, vt, upload(dev, vc), hkv, max_seq, hd, max_seq, 0)
         rec.submit()
-        kc = oracle.f16_values(oracle.f16_bits(kc)).reshape(kc.shape)
-        vc = oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape)
+        kc, vc = rounded(kc, kind), rounded(vc, kind)
     else:
         kt, vt = upload(dev, kc), upload(dev, vc)
     ot = eb.Tensor.empty(dev, (rows, h, hd))
@@ -87,18 +106,18 @@ def test_random_chunk(dev, seed):
 def test_random_decode_step(dev, seed):
     """The fused step (new row written at pos, attention over 0..=pos, optional window)
     against kv_write + the oracle; the cache row must be the new row's bits (f32) or its
-    binary16 rounding (f16)."""
+    rounding (IEEE half, E4M3)."""
     r, hd, h, hkv, sc = draw(200 + seed)
     max_seq = int(r.integers(2, 20000))
     pos = int(r.integers(0, max_seq))
     window = int(r.choice((0, 0, 1, 33, 4096)))
-    f16 = hd >= 8 and bool(r.integers(0, 2))
+    kind = cache_kind(hd >= 8 and bool(r.integers(0, 2)), seed)
     note(f"random decode seed={seed} h={h} hkv={hkv} hd={hd} pos={pos} max_seq={max_seq} "
-         f"window={window} f16={f16}")
+         f"window={window} cache={kind}")
     kc, vc = oracle.randn((max_seq, hkv, hd), 11 * seed + 1), oracle.randn((max_seq, hkv, hd), 11 * seed + 2)
     q = oracle.randn((h, hd), 11 * seed + 3)
     kn, vn = oracle.randn((hkv, hd), 11 * seed + 4), oracle.randn((hkv, hd), 11 * seed + 5)
-    dt = eb.DType.F16 if f16 else eb.DType.F32
+    dt = DTYPE[kind]
     kt, vt = eb.Tensor.empty(dev, kc.shape, dt), eb.Tensor.empty(dev, vc.shape, dt)
     rec = eb.Recorder(dev)
     eb.kv_write(rec, kt, upload(dev, kc), hkv, max_seq, hd, max_seq, 0)
@@ -108,11 +127,14 @@ def test_random_decode_step(dev, seed):
                                h, hkv, pos, hd, max_seq, sc, window)
     rec.submit()
     kc[pos], vc[pos] = kn, vn
-    if f16:
-        kc = oracle.f16_values(oracle.f16_bits(kc)).reshape(kc.shape)
-        vc = oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape)
+    if kind == "f16":
         row = np.frombuffer(kt.read_bytes(), np.uint16).reshape(max_seq, hkv, hd)[pos]
-        assert np.array_equal(row, oracle.f16_bits(kn))
+        assert np.array_equal(row, oracle.f16_bits(kn).reshape(hkv, hd))
+    elif kind == "f8":
+        row = np.frombuffer(kt.read_bytes(), np.uint8).reshape(max_seq, hkv, hd)[pos]
+        assert np.array_equal(row, oracle.f8_bits(kn).reshape(hkv, hd))
+    if kind != "f32":
+        kc, vc = rounded(kc, kind), rounded(vc, kind)
     else:
         assert_bitwise(kt.to_f32().reshape(max_seq, hkv, hd)[pos], kn, "new K row")
     want = oracle.attn_chunk(q.reshape(1, h, hd), kc, vc, h, hkv, pos, 1, hd, sc, window,
@@ -120,38 +142,37 @@ def test_random_decode_step(dev, seed):
     assert_close(ot.to_f32().reshape(1, h, hd), want, what="decode step")
 
 
-def _caches(dev, max_seq, hkv, hd, f16, seed):
-    """Seeded K/V caches on the device (f32, or IEEE-half written by kv_write) and the
-    values they hold, as f32 for the oracle."""
+def _caches(dev, max_seq, hkv, hd, kind, seed):
+    """Seeded K/V caches on the device (f32, or IEEE-half / E4M3 written by kv_write) and
+    the values they hold, as f32 for the oracle."""
     kc = oracle.randn((max_seq, hkv, hd), seed)
     vc = oracle.randn((max_seq, hkv, hd), seed + 1)
-    if not f16:
+    if kind == "f32":
         return upload(dev, kc), upload(dev, vc), kc, vc
-    kt = eb.Tensor.empty(dev, kc.shape, eb.DType.F16)
-    vt = eb.Tensor.empty(dev, vc.shape, eb.DType.F16)
+    kt = eb.Tensor.empty(dev, kc.shape, DTYPE[kind])
+    vt = eb.Tensor.empty(dev, vc.shape, DTYPE[kind])
     rec = eb.Recorder(dev)
     eb.kv_write(rec, kt, upload(dev, kc), hkv, max_seq, hd, max_seq, 0)
     eb.kv_write(rec, vt, upload(dev, vc), hkv, max_seq, hd, max_seq, 0)
     rec.submit()
-    return (kt, vt, oracle.f16_values(oracle.f16_bits(kc)).reshape(kc.shape),
-            oracle.f16_values(oracle.f16_bits(vc)).reshape(vc.shape))
+    return kt, vt, rounded(kc, kind), rounded(vc, kind)
 
 
 @pytest.mark.parametrize("seed", range(24))
 def test_random_raw_decode(dev, seed):
     """Stream-level decode on a caller workspace of exactly the size the public sizing
-    function returns, for CU counts other than the device's (other split plans), f32 and
-    IEEE-half caches, with and without a window. The workspace starts as NaN so a partial
+    function returns, for CU counts other than the device's (other split plans), f32,
+    IEEE-half and E4M3 caches, with and without a window. The workspace starts as NaN so a partial
     the launch forgets to write shows up in the output."""
     r, hd, h, hkv, sc = draw(300 + seed)
     max_seq = int(r.integers(2, 20000))
     pos = int(r.integers(0, max_seq))
     window = int(r.choice((0, 0, 1, 77, 3000)))
-    f16 = hd >= 8 and bool(r.integers(0, 2))
+    kind = cache_kind(hd >= 8 and bool(r.integers(0, 2)), seed)
     cus = int(r.choice((dev.cu_count, 1, 40, 304, 1000)))
     note(f"random raw decode seed={seed} h={h} hkv={hkv} hd={hd} pos={pos} max_seq={max_seq} "
-         f"window={window} f16={f16} cus={cus}")
-    kt, vt, kc, vc = _caches(dev, max_seq, hkv, hd, f16, 13 * seed + 1)
+         f"window={window} cache={kind} cus={cus}")
+    kt, vt, kc, vc = _caches(dev, max_seq, hkv, hd, kind, 13 * seed + 1)
     q = oracle.randn((h, hd), 13 * seed + 3)
     qt = upload(dev, q)
     ot = eb.Tensor.empty(dev, (h, hd))
@@ -159,8 +180,10 @@ def test_random_raw_decode(dev, seed):
     ws = upload(dev, np.full(max(need, 1), np.nan, np.float32))
     args = (dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(), vt.data_ptr,
             vt.numel(), ot.data_ptr, ot.numel(), h, hkv, pos, hd, max_seq, sc)
-    if f16:
+    if kind == "f16":
         eb.launch_attn_decode_f16(*args, window, ws.data_ptr, need, cus)
+    elif kind == "f8":
+        eb.launch_attn_decode_f8(*args, window, ws.data_ptr, need, cus)
     else:
         eb.launch_attn_decode_window(*args, window, ws.data_ptr, need, cus)
     dev.synchronize()
@@ -178,11 +201,11 @@ def test_random_raw_prefill_ws(dev, seed):
     pos0 = int(r.integers(0, 3000))
     rows = int(r.integers(1, 300))
     window = int(r.choice((0, 0, 1, 40, 1000)))
-    f16 = hd >= 8 and bool(r.integers(0, 2))
+    kind = cache_kind(hd >= 8 and bool(r.integers(0, 2)), seed)
     max_seq = pos0 + rows + int(r.integers(0, 5))
     note(f"random raw prefill_ws seed={seed} h={h} hkv={hkv} hd={hd} pos0={pos0} rows={rows} "
-         f"window={window} f16={f16}")
-    kt, vt, kc, vc = _caches(dev, max_seq, hkv, hd, f16, 17 * seed + 1)
+         f"window={window} cache={kind}")
+    kt, vt, kc, vc = _caches(dev, max_seq, hkv, hd, kind, 17 * seed + 1)
     q = oracle.randn((rows, h, hd), 17 * seed + 3)
     qt = upload(dev, q)
     ot = eb.Tensor.empty(dev, (rows, h, hd))
@@ -191,7 +214,7 @@ def test_random_raw_prefill_ws(dev, seed):
     eb.launch_attn_prefill_chunk_ws(dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr,
                                     kt.numel(), vt.data_ptr, vt.numel(), ot.data_ptr,
                                     ot.numel(), h, hkv, pos0, rows, hd, max_seq, sc, window,
-                                    ws.data_ptr, need, f16=f16)
+                                    ws.data_ptr, need, f16=kind == "f16", f8=kind == "f8")
     dev.synchronize()
     got = ot.to_f32().reshape(rows, h, hd)
     for rr in sorted({0, rows // 3, rows - 1}):
