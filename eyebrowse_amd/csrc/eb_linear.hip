@@ -194,6 +194,10 @@ constexpr int kBM = 128;  // x rows per workgroup tile
 #define EB_LINEAR_BK 32
 #endif
 constexpr int kBK = EB_LINEAR_BK;  // contraction per LDS stage
+// Shortest contraction cut in two halves when the 128 x 128 tiles alone leave CUs idle.
+#ifndef EB_LINEAR_KSPLIT_MIN
+#define EB_LINEAR_KSPLIT_MIN 1024
+#endif
 constexpr int kLdsRow = kBK + 8;  // halves per LDS row (16-byte pad against bank conflicts)
 constexpr int kXcds = 8;  // MI355X: workgroup ids are dealt round-robin to 8 XCDs
 
@@ -217,10 +221,14 @@ __device__ __forceinline__ floatx16 mfma16(f16x8 a, f16x8 b, floatx16 c) {
 // WNB: 32-feature blocks per wave (the workgroup tile is 128 rows x 64*WNB features);
 // NBUF: LDS buffers per stage (2: double buffered, one barrier per stage; 1: two
 // barriers, half the LDS); MINB: workgroups per CU the registers must allow.
+// ksplit 2: the contraction is cut in two halves, workgroups ids [tiles, 2*tiles) taking
+// the second; each half adds its (scaled) partial into y, which the launch zeroes first.
+// Two addends onto zero give the same bits in either order (0 + a + b = a + b = b + a).
 template <int WNB, int NBUF, int MINB>
 __global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float *__restrict__ x,
                                                                const float *__restrict__ ex,
-                                                               LinearSegs s, int M, int K) {
+                                                               LinearSegs s, int M, int K,
+                                                               int ksplit) {
     using Sh = GemmShape<WNB>;
     constexpr int BN = Sh::BN;
     extern __shared__ _Float16 lds[];
@@ -228,8 +236,9 @@ __global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int nt = gridDim.x;
-    const int bid = blockIdx.x;
+    const int nt = gridDim.x / ksplit;
+    const int bid = blockIdx.x % nt;
+    const int half = blockIdx.x / nt;
     const int full = (nt / kXcds) * kXcds;
     const int t = bid < full ? (bid % kXcds) * (nt / kXcds) + bid / kXcds : bid;
     const int ntn = s.first[s.nseg];
@@ -338,12 +347,16 @@ __global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float
         }
     };
 
-    const int nst = (K + kBK - 1) / kBK;
-    load_stage(0);
+    // This workgroup's stages: all of them, or one half of the contraction.
+    const int nst_all = (K + kBK - 1) / kBK;
+    const int per = (nst_all + ksplit - 1) / ksplit;
+    const int st0 = half * per;
+    const int nst = min(nst_all - st0, per);
+    load_stage(st0 * kBK);
     store_stage(0);
     __syncthreads();
     for (int st = 0; st < nst; ++st) {
-        if (st + 1 < nst) load_stage((st + 1) * kBK);
+        if (st + 1 < nst) load_stage((st0 + st + 1) * kBK);
         if constexpr (NBUF == 2) {
             compute(st & 1);
             if (st + 1 < nst) store_stage((st & 1) ^ 1);
@@ -370,7 +383,13 @@ __global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float
             for (int r = 0; r < 16; ++r) {
                 const int rt = wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 const int row = m0 + rt;
-                if (row < M && o < N) y[(size_t)row * N + o] = ldexpf(acc[a][b][r], s_ex[rt]);
+                if (row < M && o < N) {
+                    const float v = ldexpf(acc[a][b][r], s_ex[rt]);
+                    if (ksplit == 1)
+                        y[(size_t)row * N + o] = v;
+                    else
+                        atomicAdd(y + (size_t)row * N + o, v);
+                }
             }
         }
 }
@@ -392,9 +411,11 @@ int current_cu_count() {
     return cache[dev];
 }
 
+__global__ __launch_bounds__(kThreads) void zero_fill_kernel(float *__restrict__ y, size_t n);
+
 template <int WNB, int NBUF, int MINB>
 eb_status launch_gemm(hipStream_t st, const float *x, const float *ex, LinearSegs s,
-                      const size_t *out_f, int nseg, size_t m, size_t in_f) {
+                      const size_t *out_f, int nseg, size_t m, size_t in_f, int ksplit = 1) {
     constexpr int BN = GemmShape<WNB>::BN;
     constexpr size_t lds_bytes = gemm_lds_bytes<WNB, NBUF>();
     static std::once_flag once;
@@ -409,8 +430,15 @@ eb_status launch_gemm(hipStream_t st, const float *x, const float *ex, LinearSeg
     for (int i = 0; i < nseg; ++i)
         s.first[i + 1] = s.first[i] + (int)((out_f[i] + BN - 1) / BN);
     const size_t tiles = (size_t)((m + kBM - 1) / kBM) * (size_t)s.first[nseg];
-    linear_gemm_kernel<WNB, NBUF, MINB><<<(unsigned)tiles, kThreads, lds_bytes, st>>>(
-        x, ex, s, (int)m, (int)in_f);
+    if (ksplit > 1) {  // the halves add into zeroed outputs (a kernel: graphs may hold it)
+        for (int i = 0; i < nseg; ++i) {
+            const size_t n = m * out_f[i];
+            zero_fill_kernel<<<(unsigned)std::min<size_t>((n + kThreads - 1) / kThreads, 4096),
+                               kThreads, 0, st>>>(s.y[i], n);
+        }
+    }
+    linear_gemm_kernel<WNB, NBUF, MINB><<<(unsigned)(tiles * ksplit), kThreads, lds_bytes, st>>>(
+        x, ex, s, (int)m, (int)in_f, ksplit);
     return eb::check_launch("linear_f16w");
 }
 
@@ -488,9 +516,15 @@ eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_
     const size_t mtiles = (m + kBM - 1) / kBM;
     size_t wide_units = 0;
     for (int i = 0; i < nseg; ++i) wide_units += (out_f[i] + GemmShape<4>::BN - 1) / GemmShape<4>::BN;
-    if (mtiles * wide_units >= 2 * (size_t)current_cu_count())
+    const size_t cus = (size_t)current_cu_count();
+    if (mtiles * wide_units >= 2 * cus)
         return launch_gemm<4, 1, 2>(st, x, ws, s, out_f, nseg, m, in_f);
-    return launch_gemm<2, 2, 1>(st, x, ws, s, out_f, nseg, m, in_f);
+    // With at most one 128 x 128 tile per CU (o_proj-like shapes: many rows, few features),
+    // long contractions are cut in two halves, doubling the workgroups.
+    size_t units = 0;
+    for (int i = 0; i < nseg; ++i) units += (out_f[i] + GemmShape<2>::BN - 1) / GemmShape<2>::BN;
+    const int ksplit = (mtiles * units <= cus && in_f >= (size_t)EB_LINEAR_KSPLIT_MIN) ? 2 : 1;
+    return launch_gemm<2, 2, 1>(st, x, ws, s, out_f, nseg, m, in_f, ksplit);
 }
 
 }  // namespace eb

@@ -102,6 +102,23 @@ def test_qwen_prompt_projection_sampled_rows(dev):
     assert_close(got[rows], want, what="qwen q_proj rows")
 
 
+def test_qwen_o_proj_split_contraction(dev):
+    """Qwen3 o_proj at T=4096 (4096 x 2048 -> 1024): one 128 x 128 tile per CU, so the
+    contraction is cut in two halves whose partials add into the zeroed output. Sampled
+    rows against the oracle, and a second launch bit-identical (two addends onto zero give
+    the same bits in either order)."""
+    note("linear gemm qwen o_proj T=4096 (split contraction)")
+    m, in_f, out_f = 4096, 2048, 1024
+    x = oracle.randn((m, in_f), 7)
+    w = oracle.randn((out_f, in_f), 8) * 0.03
+    got = run(dev, x, w, m, in_f, out_f)
+    again = run(dev, x, w, m, in_f, out_f)
+    assert_bitwise(again, got, "second launch")
+    rows = [0, 1, 127, 128, 1000, 2049, 4094, 4095]
+    want = want_of(x[rows], w, len(rows), in_f, out_f)
+    assert_close(got[rows], want, what="qwen o_proj rows")
+
+
 def test_row_scaling_extremes(dev):
     """Rows of very different magnitudes (1e-30 .. 1e30), a zero row, and rows holding inf
     or NaN: the split path scales each row by a power of two, so every finite row keeps
