@@ -13,7 +13,8 @@
 // 2^24 - 1 - i / 256 (so vocab < 2^32); non-candidates get key 0. The maximum key is the
 // reference's winner whatever order the keys are reduced in, so the work can be spread
 // over many workgroups: pass 1 reduces slices to one key each (workspace), pass 2 reduces
-// those and decodes the index.
+// those and decodes the index. A vocabulary of one slice (up to 4096) is one launch: its
+// single workgroup decodes the index itself.
 #include "eb_common.h"
 #include "eb_internal.h"
 
@@ -57,10 +58,12 @@ __device__ __forceinline__ uint64_t block_max(uint64_t k) {
     return s[0];
 }
 
-// Pass 1: workgroup b reduces elements [b*kSlice, (b+1)*kSlice) to one key.
+// Pass 1: workgroup b reduces elements [b*kSlice, (b+1)*kSlice) to one key (with one
+// workgroup, the winner's index goes straight to out).
 __global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float *__restrict__ x,
                                                                   uint32_t n, bool vec,
-                                                                  uint64_t *__restrict__ part) {
+                                                                  uint64_t *__restrict__ part,
+                                                                  uint32_t *__restrict__ out) {
     const uint32_t base = blockIdx.x * (uint32_t)kSlice;
     uint64_t best = 0;
     if (vec) {  // x 16-byte aligned, n % 4 == 0: 4 loads of 4 per thread, issued first
@@ -83,7 +86,12 @@ __global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float *_
         }
     }
     best = block_max(best);
-    if (threadIdx.x == 0) part[blockIdx.x] = best;
+    if (threadIdx.x == 0) {
+        if (gridDim.x == 1)
+            out[0] = index_of(best);
+        else
+            part[blockIdx.x] = best;
+    }
 }
 
 // Pass 2: one workgroup reduces the partial keys and writes the index.
@@ -114,8 +122,8 @@ eb_status launch_argmax(hipStream_t st, const float *x, size_t n, uint32_t *out,
     uint64_t *part = reinterpret_cast<uint64_t *>(ws);
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && n % 4 == 0 && n >= 4;
     const unsigned blocks = (unsigned)(parts > 0 ? parts : 1);
-    argmax_partial_kernel<<<blocks, kThreads, 0, st>>>(x, (uint32_t)n, vec, part);
-    argmax_final_kernel<<<1, kThreads, 0, st>>>(part, (int)blocks, out);
+    argmax_partial_kernel<<<blocks, kThreads, 0, st>>>(x, (uint32_t)n, vec, part, out);
+    if (blocks > 1) argmax_final_kernel<<<1, kThreads, 0, st>>>(part, (int)blocks, out);
     return check_launch("argmax");
 }
 

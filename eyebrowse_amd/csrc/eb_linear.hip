@@ -168,12 +168,21 @@ __global__ __launch_bounds__(kThreads) void linear_scalar_kernel(const float *__
 // times 2^-e_i lies in [2^14, 2^15) (e_i = 0 for zero or non-finite rows). One wave per
 // row. Scaling uses ldexp (one rounding, no intermediate overflow), so e_i may exceed the
 // exponent range of a single f32 scale factor (rows of subnormals need 2^163).
+// With zero_out, the wave also zeroes its row of every output (for the split-contraction
+// GEMM, whose halves add into y).
 __global__ __launch_bounds__(kThreads) void linear_row_scale_kernel(const float *__restrict__ x,
                                                                     float *__restrict__ ex,
-                                                                    int M, int K) {
+                                                                    int M, int K, LinearSegs s,
+                                                                    bool zero_out) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (row >= M) return;
+    if (zero_out) {
+        for (int g = 0; g < s.nseg; ++g) {
+            float *yr = s.y[g] + (size_t)row * s.n[g];
+            for (int c = lane; c < s.n[g]; c += 64) yr[c] = 0.0f;
+        }
+    }
     const float *xr = x + (size_t)row * K;
     float mx = 0.0f;
     float bad = 0.0f;  // becomes NaN (and stays NaN) once a NaN or inf is seen
@@ -222,7 +231,8 @@ __device__ __forceinline__ floatx16 mfma16(f16x8 a, f16x8 b, floatx16 c) {
 // NBUF: LDS buffers per stage (2: double buffered, one barrier per stage; 1: two
 // barriers, half the LDS); MINB: workgroups per CU the registers must allow.
 // ksplit 2: the contraction is cut in two halves, workgroups ids [tiles, 2*tiles) taking
-// the second; each half adds its (scaled) partial into y, which the launch zeroes first.
+// the second; each half adds its (scaled) partial into y, which the row-scale pre-pass
+// zeroes first.
 // Two addends onto zero give the same bits in either order (0 + a + b = a + b = b + a).
 template <int WNB, int NBUF, int MINB>
 __global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float *__restrict__ x,
@@ -411,8 +421,7 @@ int current_cu_count() {
     return cache[dev];
 }
 
-__global__ __launch_bounds__(kThreads) void zero_fill_kernel(float *__restrict__ y, size_t n);
-
+// ksplit 2 expects the outputs zeroed (linear_row_scale_kernel's zero_out).
 template <int WNB, int NBUF, int MINB>
 eb_status launch_gemm(hipStream_t st, const float *x, const float *ex, LinearSegs s,
                       const size_t *out_f, int nseg, size_t m, size_t in_f, int ksplit = 1) {
@@ -430,13 +439,6 @@ eb_status launch_gemm(hipStream_t st, const float *x, const float *ex, LinearSeg
     for (int i = 0; i < nseg; ++i)
         s.first[i + 1] = s.first[i] + (int)((out_f[i] + BN - 1) / BN);
     const size_t tiles = (size_t)((m + kBM - 1) / kBM) * (size_t)s.first[nseg];
-    if (ksplit > 1) {  // the halves add into zeroed outputs (a kernel: graphs may hold it)
-        for (int i = 0; i < nseg; ++i) {
-            const size_t n = m * out_f[i];
-            zero_fill_kernel<<<(unsigned)std::min<size_t>((n + kThreads - 1) / kThreads, 4096),
-                               kThreads, 0, st>>>(s.y[i], n);
-        }
-    }
     linear_gemm_kernel<WNB, NBUF, MINB><<<(unsigned)(tiles * ksplit), kThreads, lds_bytes, st>>>(
         x, ex, s, (int)m, (int)in_f, ksplit);
     return eb::check_launch("linear_f16w");
@@ -508,22 +510,24 @@ eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_
         return check_launch("linear_f16w");
     }
     if (ws == nullptr || ws_floats < m) return fail(EB_SHAPE_MISMATCH, "linear: workspace too small");
-    linear_row_scale_kernel<<<(unsigned)((m + kWaves - 1) / kWaves), kThreads, 0, st>>>(
-        x, ws, (int)m, (int)in_f);
     // Wide tiles (64 x 128 per wave: 0.5 LDS fragment reads per MFMA instead of 0.75) when
     // they still give every CU two workgroups; otherwise 128 x 128 tiles, whose twice as
-    // many workgroups keep more of the chip busy.
+    // many workgroups keep more of the chip busy. With at most one 128 x 128 tile per CU
+    // (o_proj-like shapes: many rows, few features), long contractions are cut in two
+    // halves, doubling the workgroups; the pre-pass then zeroes the outputs they add into.
     const size_t mtiles = (m + kBM - 1) / kBM;
-    size_t wide_units = 0;
-    for (int i = 0; i < nseg; ++i) wide_units += (out_f[i] + GemmShape<4>::BN - 1) / GemmShape<4>::BN;
+    size_t wide_units = 0, units = 0;
+    for (int i = 0; i < nseg; ++i) {
+        wide_units += (out_f[i] + GemmShape<4>::BN - 1) / GemmShape<4>::BN;
+        units += (out_f[i] + GemmShape<2>::BN - 1) / GemmShape<2>::BN;
+    }
     const size_t cus = (size_t)current_cu_count();
-    if (mtiles * wide_units >= 2 * cus)
-        return launch_gemm<4, 1, 2>(st, x, ws, s, out_f, nseg, m, in_f);
-    // With at most one 128 x 128 tile per CU (o_proj-like shapes: many rows, few features),
-    // long contractions are cut in two halves, doubling the workgroups.
-    size_t units = 0;
-    for (int i = 0; i < nseg; ++i) units += (out_f[i] + GemmShape<2>::BN - 1) / GemmShape<2>::BN;
-    const int ksplit = (mtiles * units <= cus && in_f >= (size_t)EB_LINEAR_KSPLIT_MIN) ? 2 : 1;
+    const bool wide = mtiles * wide_units >= 2 * cus;
+    const int ksplit =
+        (!wide && mtiles * units <= cus && in_f >= (size_t)EB_LINEAR_KSPLIT_MIN) ? 2 : 1;
+    linear_row_scale_kernel<<<(unsigned)((m + kWaves - 1) / kWaves), kThreads, 0, st>>>(
+        x, ws, (int)m, (int)in_f, s, ksplit > 1);
+    if (wide) return launch_gemm<4, 1, 2>(st, x, ws, s, out_f, nseg, m, in_f);
     return launch_gemm<2, 2, 1>(st, x, ws, s, out_f, nseg, m, in_f, ksplit);
 }
 

@@ -52,9 +52,10 @@ def test_argmax_ties_and_specials(dev):
 
 
 @pytest.mark.parametrize("vocab,seed", [(151936, 1), (262144, 2), (1001, 3), (4099, 4),
-                                        (32000, 5), (5, 6)])
+                                        (32000, 5), (5, 6), (4096, 7)])
 def test_argmax_matches_oracle(dev, vocab, seed):
-    """Qwen3 and Gemma vocab sizes, ragged sizes, and heavy ties (values rounded to 0.5)."""
+    """Qwen3 and Gemma vocab sizes, ragged sizes, one full slice (4096: the one-launch
+    path), and heavy ties (values rounded to 0.5)."""
     note(f"argmax vocab={vocab}")
     x = oracle.randn((vocab,), seed)
     assert gpu_argmax(dev, x) == oracle.argmax(x)
