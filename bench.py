@@ -583,7 +583,7 @@ def layer_step_extras(eb, hip, dev) -> dict:
     g.release()
     del keep
     return {"layer_decode_step_qwen_pos100": {
-        "kernels": 7, "eager_us": round(eager * 1e3, 2), "graph_us": round(graph * 1e3, 2)}}
+        "kernels": 5, "eager_us": round(eager * 1e3, 2), "graph_us": round(graph * 1e3, 2)}}
 
 
 def traffic_run(eb, hip, dev, sc128):
