@@ -48,11 +48,18 @@ SOURCES = [
 ]
 
 
+# Per-source flags. eb_decode.hip: matrix-core results in VGPRs (the narrow-cache decode
+# rescales its accumulators on the VALU; with AGPR results every tile copied them across).
+SOURCE_FLAGS = {
+    "eb_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     path = os.path.join(CSRC, src)
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [HIPCC, *COMMON_FLAGS, *lang, "-c", path, "-o", obj]
+    cmd = [HIPCC, *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), *lang, "-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -34,6 +34,9 @@
 // that split's first head-subgroup workgroup also copies knew/vnew into cache row `pos`.
 // Nothing else touches that row in the launch, so the copy is exact and race free.
 //
+// E4M3 caches at head dims 64 and 128 run decode_mx_kernel instead (below): the same
+// grid, split plan, partials and merge, with both products on the matrix cores.
+//
 // The result is softmax(scale * q K^T) V over keys 0..=pos; it differs from the
 // reference's 3-pass f32 softmax only by rounding (summation order, exp2 vs expf).
 #include "eb_common.h"
@@ -617,6 +620,554 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     }
 }
 
+// ---- E4M3 caches on the matrix cores ----------------------------------------------------
+//
+// decode_mx_kernel<HD, G>: OCP FP8 E4M3 caches at head dims 64 and 128. Same grid, split
+// plan, partial layout and merge as decode_kernel. Per byte an E4M3 cache carries four times
+// the f32 elements, and the lane-wise kernel's multiply-add per element and head bounds it
+// (67 % of wave cycles issuing VALU at Mistral 32k keys); here both products run on the
+// matrix cores. A wave step is a tile of 16 keys; lane (n, g) is lane n + 16 g.
+//  - Scores S[key][head] = K q^T on v_mfma_f32_16x16x32_f16. A = the tile's 16 key rows:
+//    lane (n, g) holds 8 dims of key n per 32-dim chunk (a 16-byte load holds 16 dims, two
+//    chunks' worth), converted to f16 (exact: every E4M3 value is an f16). B = q: column n
+//    is head n % G (heads repeated across the 16 columns), as the f16 high and low halves of
+//    q * scale * log2(e) * 2^e_h (two products per chunk; each f16 x f16 product is exact in
+//    f32). e_h is a power of two per head that puts its largest |q| in [2^13, 2^14), so that
+//    the halves neither overflow nor lose bits to subnormals. Lane (n, g) then holds the
+//    scores of keys 4g .. 4g + 3 for head n % G.
+//  - Online softmax with a lazily moved reference max per head (wave-uniform), weights
+//    p = 2^(s - m) * 2^7: below 2^15 (s exceeds m by at most the slack of 8), so their f16
+//    halves keep terms down to 2^-31 of the reference term. The reference is a score
+//    itself, so a lone key's weight is exactly 2^7 and its output exactly its V row.
+//  - O[head][dim] += P V on v_mfma_f32_16x16x16_f16. A = P: lane (n, g) supplies head
+//    n % G at keys 4g .. 4g + 3, which are exactly its score registers (as f16 high and
+//    low halves: two products). B = V: lane (n, g) loads dims DV n .. DV n + DV - 1
+//    (DV = HD / 16) of keys 4g + t, t = 0..3, and product e (0 .. DV - 1) takes element e
+//    of each load, so output column n of accumulator e is dim DV n + e. No lane exchange
+//    and no LDS between the two products.
+//  - Lane (n, g) register r of accumulator e holds head (4g + r) % G: every lane group
+//    holds every head, so the epilogue reads lanes 0..15.
+// The new key (knew / vnew, after the optional norm and RoPE) is rounded to E4M3 in LDS and
+// folded in by the owning split's wave 0 as one more tile with a single valid key, through
+// the same code as the cache rows.
+// Measured against decode_kernel (HIP events, decode steps from graphs): Mistral 32k keys
+// 25.0 -> 20.0 us, Qwen L=8191 12.8 -> 10.7 us. The same scheme over IEEE-half caches
+// measured slower (27.6 -> 28.4 us at Mistral 32k keys: a load-only copy of it took 28.1,
+// so its K-row loads, 64 bytes of 16 rows each, bound it), and so did head dim 256 (its
+// loads and accumulators leave no registers: 20.0 -> 20.5 us at Gemma-4 16k keys).
+// 0 runs decode_kernel over E4M3 caches too (the comparison above).
+#ifndef EB_DECODE_MX
+#define EB_DECODE_MX 1
+#endif
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr bool mx_head_dim(int hd) { return hd == 64 || hd == 128; }
+
+template <int HD, int G>
+struct MxShape {
+    static constexpr int EB = 1;
+    static_assert(mx_head_dim(HD), "head dim 64 or 128");
+    static constexpr int KPW = 16;                 // keys per wave step (one tile)
+    static constexpr int NC = HD / 32;             // 32-dim chunks of a key row
+    static constexpr int KL = NC / 2;              // K loads per tile and lane (16 bytes)
+    static constexpr int DV = HD / 16;             // V dims per lane per row
+    static constexpr int VW = DV * EB / 4;         // words per lane per V row
+    // Tiles per iteration: each of the two register buffers holds U tiles' loads.
+    static constexpr int U = 2;
+    static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
+    static constexpr int RW = HD * EB / 4;         // words of one cache row (one KV head)
+    static constexpr int WS = G * HD + 4;          // epilogue state per wave (floats)
+    // LDS (floats): q [G][HD] | 2^-e_h [4] | knew, vnew [HD] each | their cache-type rows
+    // [RW] each | epilogue: acc [kWaves][WS], m [G][kWaves], l [G][kWaves].
+    static constexpr int OFF_QINV = G * HD;
+    static constexpr int OFF_KN = OFF_QINV + 4;
+    static constexpr int OFF_VN = OFF_KN + HD;
+    static constexpr int OFF_KR = OFF_VN + HD;
+    static constexpr int OFF_VR = OFF_KR + RW;
+    static constexpr int OFF_ACC = OFF_VR + RW;
+    static constexpr int OFF_M = OFF_ACC + kWaves * WS;
+    static constexpr int OFF_L = OFF_M + G * kWaves;
+    static constexpr size_t LDS_BYTES = sizeof(float) * (size_t)(OFF_L + G * kWaves);
+};
+
+// W words of a row slice from a raw buffer (range-checked by the resource).
+template <int W>
+__device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t r, int voff,
+                                           int soff) {
+    if constexpr (W % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < W / 4; ++i) {
+            const u32x4 v = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + 16 * i, 0));
+            dst[4 * i + 0] = v[0];
+            dst[4 * i + 1] = v[1];
+            dst[4 * i + 2] = v[2];
+            dst[4 * i + 3] = v[3];
+        }
+    } else if constexpr (W == 2) {
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+        dst[0] = v[0];
+        dst[1] = v[1];
+    } else {
+        static_assert(W == 1, "1, 2 or a multiple of 4 words");
+        dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+}
+
+// Two f32 as packed f16, rounded toward zero (the weights' high halves; the low halves
+// take the remainders).
+__device__ __forceinline__ unsigned pk_f16(float a, float b) {
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+__device__ __forceinline__ float f16_lo(unsigned w) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float f16_hi(unsigned w) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+}
+
+// First dim of lane group g's 8 dims in 32-dim chunk c: a lane's 16-byte load holds 16
+// consecutive dims, the first 8 in chunk 2C and the rest in chunk 2C + 1 (64 bytes of each
+// row per load instruction). The products sum over a chunk's dims in any order; q's operand
+// follows the same map.
+__device__ __forceinline__ int chunk_dim(int c, int g) {
+    return 64 * (c / 2) + 16 * g + 8 * (c % 2);
+}
+
+// Two E4M3 values (bytes 0, 1 or 2, 3 of w) as packed f16, exact (gfx950's scaled FP8
+// conversion, scale 1).
+__device__ __forceinline__ unsigned f8x2_f16(unsigned w, bool hi) {
+    return __builtin_bit_cast(unsigned, hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true)
+                                           : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+
+// A operand of chunk c (8 dims of the lane's key) from the lane's raw K words [KL][4].
+__device__ __forceinline__ f16x8 k_operand(const unsigned (*kr)[4], int c) {
+    const unsigned w0 = kr[c / 2][2 * (c % 2)], w1 = kr[c / 2][2 * (c % 2) + 1];
+    return __builtin_bit_cast(f16x8, u32x4{f8x2_f16(w0, false), f8x2_f16(w0, true),
+                                           f8x2_f16(w1, false), f8x2_f16(w1, true)});
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads, 1) void decode_mx_kernel(DecodeArgs a) {
+    using S = MxShape<HD, G>;
+    constexpr int EB = S::EB;
+    constexpr int U = S::U, NC = S::NC, KL = S::KL, DV = S::DV, VW = S::VW;
+    constexpr int KPW = S::KPW;
+    static_assert(G == 1 || G == 2 || G == 4, "heads per workgroup");
+    extern __shared__ float smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int col = blockIdx.x;
+    const int kvh = col % a.hkv;
+    const int sub = col / a.hkv;
+    const int head0 = kvh * a.g + sub * G;
+    const int split = blockIdx.y;
+    const int pos = a.keys - 1;
+    const int ce = a.knew != nullptr ? pos : a.keys;
+    const bool tail_new = a.knew != nullptr && split == (pos / KPW) % a.nsplit;
+    const int nblk = (ce + KPW - 1) / KPW;
+    const int my_blk = nblk > split ? (nblk - split + a.nsplit - 1) / a.nsplit : 0;
+    const int row_bytes = a.hkv * HD * EB;
+
+    // ---- main-loop addressing (as decode_kernel's, with tiles of 16 keys) -------------------
+    // Iteration `it` covers the split's local blocks it*U*kWaves .. +U*kWaves; tile (u, wave)
+    // is local block it*U*kWaves + u*kWaves + wave, at rows tb[u] + rows_from(it) .. +15.
+    const int blk_stride = U * kWaves * a.nsplit;
+    int tb[U], kvo[U], vvo[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        tb[u] = ((u * kWaves + wave) * a.nsplit + split) * KPW;
+        kvo[u] = (tb[u] + n) * row_bytes + 16 * g;           // K: key n, its 16 bytes
+        vvo[u] = (tb[u] + 4 * g) * row_bytes + DV * n * EB;  // V: key 4g (+t), dims DV n
+    }
+    const char *kbase = static_cast<const char *>(a.kc) + (size_t)kvh * HD * EB;
+    const char *vbase = static_cast<const char *>(a.vc) + (size_t)kvh * HD * EB;
+    auto rows_from = [&](int it) { return it * blk_stride * KPW; };
+    using KRaw = unsigned[U][KL][4];
+    using VRaw = unsigned[U][4][VW];
+    auto load_iter = [&](int it, KRaw &kr, VRaw &vr) {
+        const int r0 = rows_from(it);
+        const int left = min(ce - r0, blk_stride * KPW);
+        const int nbytes = left > 0 ? (left - 1) * row_bytes + HD * EB : 0;
+        const size_t off = (size_t)r0 * row_bytes;
+        const __amdgpu_buffer_rsrc_t kres = make_rsrc(kbase + off, nbytes);
+        const __amdgpu_buffer_rsrc_t vres = make_rsrc(vbase + off, nbytes);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int c = 0; c < KL; ++c) load_words<4>(kr[u][c], kres, kvo[u], 64 * c);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) load_words<VW>(vr[u][t], vres, vvo[u] + t * row_bytes, 0);
+        }
+    };
+
+    // ---- q and the new rows: their loads first, then the first two iterations' ----------
+    static_assert(G * HD / 4 <= kThreads, "one 16-byte q load per thread");
+    const f32x4 z4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 q4 = threadIdx.x < G * HD / 4
+                         ? reinterpret_cast<const f32x4 *>(a.q + (size_t)head0 * HD)[threadIdx.x]
+                         : z4;
+    const bool new4 = tail_new && threadIdx.x < HD / 4;
+    const f32x4 kn4 = new4 ? reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD)[threadIdx.x] : z4;
+    const f32x4 vn4 = new4 ? reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD)[threadIdx.x] : z4;
+    __builtin_amdgcn_sched_barrier(0);
+    // (an iteration past the split's blocks reads zeros; a split without blocks ignores them)
+    KRaw kA, kB;
+    VRaw vA, vB;
+    load_iter(0, kA, vA);
+    load_iter(1, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- q (and the new row) in LDS, after the optional norm and RoPE --------------------
+    float *s_q = smem;
+    float *s_qinv = smem + S::OFF_QINV;
+    float *s_kn = smem + S::OFF_KN;
+    float *s_vn = smem + S::OFF_VN;
+    unsigned *s_kr = reinterpret_cast<unsigned *>(smem + S::OFF_KR);
+    unsigned *s_vr = reinterpret_cast<unsigned *>(smem + S::OFF_VR);
+    if (threadIdx.x < G * HD / 4) reinterpret_cast<f32x4 *>(s_q)[threadIdx.x] = q4;
+    if (new4) {
+        reinterpret_cast<f32x4 *>(s_kn)[threadIdx.x] = kn4;
+        reinterpret_cast<f32x4 *>(s_vn)[threadIdx.x] = vn4;
+    }
+    __syncthreads();
+    {
+        // Row jobs: 0..G-1 the query heads, G the new key, G + 1 the new value. Each lane
+        // owns the dim pairs (p, p + HD/2), p = lane, lane + 64, ..., so that RMSNorm and
+        // RoPE never read another lane's dims.
+        constexpr int NP = (HD / 2 + 63) / 64;
+        const float *cs = (a.prologue && a.rcos) ? a.rcos + (size_t)a.rope_row * (HD / 2) : nullptr;
+        const float *sn = (a.prologue && a.rsin) ? a.rsin + (size_t)a.rope_row * (HD / 2) : nullptr;
+        const int njobs = tail_new ? G + 2 : G;
+        for (int job = wave; job < njobs; job += kWaves) {
+            float *x = job < G ? s_q + job * HD : (job == G ? s_kn : s_vn);
+            const float *nw = !a.prologue ? nullptr : job < G ? a.qn_w : job == G ? a.kn_w : a.vn_w;
+            const bool rope = cs != nullptr && job <= G;
+            float x1[NP], x2[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int p = lane + 64 * i;
+                x1[i] = p < HD / 2 ? x[p] : 0.0f;
+                x2[i] = p < HD / 2 ? x[p + HD / 2] : 0.0f;
+            }
+            if (nw) {  // RMSNorm (kernels/src/rmsnorm.rs:6-38): x * (1/sqrt(mean x^2 + eps)) * w
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NP; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+                ss = eb::class_reduce<1, false>(ss);
+                const float inv = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int p = lane + 64 * i;
+                    if (p < HD / 2) {
+                        x1[i] = x1[i] * inv * nw[p];
+                        x2[i] = x2[i] * inv * nw[p + HD / 2];
+                    }
+                }
+            }
+            if (rope) {  // RoPE (kernels/src/rope.rs:6-32): pairs (p, p + HD/2), angle p
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int p = lane + 64 * i;
+                    if (p < HD / 2) {
+                        const float c = cs[p], s = sn[p];
+                        const float y1 = x1[i] * c - x2[i] * s;
+                        const float y2 = x2[i] * c + x1[i] * s;
+                        x1[i] = y1;
+                        x2[i] = y2;
+                    }
+                }
+            }
+            if (job < G) {
+                // q * scale * log2(e), then the head's power of two
+                float amax = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    x1[i] *= a.scale_log2;
+                    x2[i] *= a.scale_log2;
+                    amax = fmaxf(amax, fmaxf(fabsf(x1[i]), fabsf(x2[i])));
+                }
+                amax = eb::class_reduce<1, true>(amax);
+                int ex = 0;
+                if (amax > 0.0f && amax <= 3.0e38f) {
+                    frexpf(amax, &ex);
+                    ex = 14 - ex;  // amax * 2^ex in [2^13, 2^14)
+                    ex = ex < -64 ? -64 : ex > 64 ? 64 : ex;
+                }
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int p = lane + 64 * i;
+                    if (p < HD / 2) {
+                        x[p] = ldexpf(x1[i], ex);
+                        x[p + HD / 2] = ldexpf(x2[i], ex);
+                    }
+                }
+                if (lane == 0) s_qinv[job] = ldexpf(1.0f, -ex);
+            } else {
+                // the new row as the cache holds it: in LDS (for the fold) and, by the first
+                // head subgroup, in cache row `pos` (no workgroup reads that row here)
+                unsigned *raw = job == G ? s_kr : s_vr;
+                void *dst = job == G ? a.kc_w : a.vc_w;
+                const size_t drow = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int p = lane + 64 * i;
+                    if (p < HD / 2) {
+#pragma unroll
+                        for (int side = 0; side < 2; ++side) {
+                            const int d = p + side * (HD / 2);
+                            const float v = side ? x2[i] : x1[i];
+                            const uint8_t bv = (uint8_t)(eb::f8e4m3_bits(v) & 0xFFu);
+                            reinterpret_cast<uint8_t *>(raw)[d] = bv;
+                            if (sub == 0) static_cast<uint8_t *>(dst)[drow + d] = bv;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // B operands of the score products: head n % G, the lane's dims of chunk c, high and
+    // low halves.
+    f16x8 qh[NC], ql[NC];
+    const int own = n % G;
+    const float c_own = s_qinv[own];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const float *src = s_q + own * HD + chunk_dim(c, g);
+        const f32x4 v0 = *reinterpret_cast<const f32x4 *>(src);
+        const f32x4 v1 = *reinterpret_cast<const f32x4 *>(src + 4);
+        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const _Float16 hi = (_Float16)v[j];
+            qh[c][j] = hi;
+            ql[c][j] = (_Float16)(v[j] - (float)hi);
+        }
+    }
+
+    // ---- the online softmax state --------------------------------------------------------
+    floatx4 acc[DV];
+#pragma unroll
+    for (int e = 0; e < DV; ++e) acc[e] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float mh[G];  // reference max per head (log2 units), the same in every lane
+#pragma unroll
+    for (int h = 0; h < G; ++h) mh[h] = -INFINITY;
+    float l_own = 0.0f;           // this lane's share of the weight sum of head `own`
+    float m_own = -INFINITY;      // m of head `own`
+    float mref = 0.0f;            // m_own, 0 while -inf
+    float gthr = -INFINITY;       // a score x = s - mref above this moves the reference
+
+    // NT tiles at once: raw K words [NT][KL][4], raw V words [NT][4][VW]; in tile t the
+    // keys 4g + r < lim[t] are valid (wave-uniform). All score products first, then one
+    // softmax update for the NT tiles, then the P V products.
+    auto consume = [&](auto nt, const unsigned (*kr)[KL][4], const unsigned (*vr)[4][VW],
+                       const int *lim) {
+        constexpr int NT = decltype(nt)::value;
+        floatx4 sc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            // two accumulators (high and low halves of q): no product waits for its neighbour
+            floatx4 s = {0.0f, 0.0f, 0.0f, 0.0f}, s2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const f16x8 kk = k_operand(kr[t], c);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, qh[c], s, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kk, ql[c], s2, 0, 0, 0);
+            }
+            sc[t] = s + s2;
+        }
+        float x[NT][4];
+        auto weigh = [&] {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x[t][r] = fmaf(sc[t][r], c_own, -mref);
+                if (lim[t] < KPW) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (4 * g + r >= lim[t]) x[t][r] = -INFINITY;
+                }
+            }
+        };
+        weigh();
+        bool grow = false;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) grow = grow || x[t][r] > gthr;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            // New reference per head: the tiles' max where it exceeds m by more than the
+            // slack, taken from the scores themselves (times the power of two, exact), so
+            // that the max key's x is exactly 0.
+            float sm = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (4 * g + r < lim[t]) sm = fmaxf(sm, sc[t][r]);
+            sm *= c_own;
+            sm = fmaxf(sm, eb::lane_xor16(sm));
+            sm = fmaxf(sm, eb::lane_xor32(sm));
+            // every lane of head h holds lane h's sm: the same scores, the same reduction
+            float corr[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float mt = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm), h));
+                const float mn = mt > mh[h] + kSlack ? mt : mh[h];
+                corr[h] = mn == mh[h] ? 1.0f : eb::fast_exp2(mh[h] - mn);
+                mh[h] = mn;
+            }
+#pragma unroll
+            for (int e = 0; e < DV; ++e)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[e][r] *= corr[r % G];
+            // the same update for the lane's own head, from its own sm
+            const float mn = sm > m_own + kSlack ? sm : m_own;
+            l_own *= mn == m_own ? 1.0f : eb::fast_exp2(m_own - mn);
+            m_own = mn;
+            mref = m_own == -INFINITY ? 0.0f : m_own;
+            gthr = m_own == -INFINITY ? -INFINITY : kSlack;
+            weigh();
+        }
+        f16x4 ph[NT], pl[NT];
+        f16x4 vb[NT][DV];  // B operands: element e of the lane's four rows
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float p[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) p[r] = eb::fast_exp2(x[t][r]) * 128.0f;
+            l_own += (p[0] + p[1]) + (p[2] + p[3]);
+            // A operands: the weights' f16 high halves and their remainders
+            const unsigned h01 = pk_f16(p[0], p[1]), h23 = pk_f16(p[2], p[3]);
+            const unsigned l01 = pk_f16(p[0] - f16_lo(h01), p[1] - f16_hi(h01));
+            const unsigned l23 = pk_f16(p[2] - f16_lo(h23), p[3] - f16_hi(h23));
+            ph[t] = __builtin_bit_cast(f16x4, u32x2{h01, h23});
+            pl[t] = __builtin_bit_cast(f16x4, u32x2{l01, l23});
+#pragma unroll
+                for (int e = 0; e < DV; e += 2) {
+                    // bytes e, e + 1 of rows 0, 1 (and 2, 3) as [r0.e, r1.e, r0.e+1, r1.e+1]
+                    // (v_perm byte selectors: 0-3 the second operand's bytes, 4-7 the first's)
+                    const unsigned k = (unsigned)(e % 4);
+                    const unsigned sel = k | (4u + k) << 8 | (k + 1u) << 16 | (5u + k) << 24;
+                    const unsigned b01 = __builtin_amdgcn_perm(vr[t][1][e / 4], vr[t][0][e / 4], sel);
+                    const unsigned b23 = __builtin_amdgcn_perm(vr[t][3][e / 4], vr[t][2][e / 4], sel);
+                    vb[t][e] = __builtin_bit_cast(f16x4, u32x2{f8x2_f16(b01, false), f8x2_f16(b23, false)});
+                    vb[t][e + 1] = __builtin_bit_cast(f16x4, u32x2{f8x2_f16(b01, true), f8x2_f16(b23, true)});
+                }
+        }
+        // high halves into every accumulator, then the low halves (independent neighbours)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < DV; ++e)
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph[t], vb[t][e], acc[e], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < DV; ++e)
+                acc[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl[t], vb[t][e], acc[e], 0, 0, 0);
+    };
+    auto consume_iter = [&](int it, const KRaw &kr, const VRaw &vr) {
+        const int r0 = rows_from(it);
+        int lim[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) lim[u] = ce - r0 - tb[u];
+        consume(std::integral_constant<int, U>{}, kr, vr, lim);
+    };
+
+    // ---- the main loop: iterations in pairs (A, B), each buffer refilled once consumed ----
+    const int n_iter = (my_blk + U * kWaves - 1) / (U * kWaves);
+    const int n_pairs = (n_iter + 1) / 2;
+    if (n_pairs > 0) {
+        for (int pr = 1; pr < n_pairs; ++pr) {
+            __builtin_amdgcn_sched_barrier(0);
+            consume_iter(2 * pr - 2, kA, vA);
+            load_iter(2 * pr, kA, vA);
+            __builtin_amdgcn_sched_barrier(0);
+            consume_iter(2 * pr - 1, kB, vB);
+            load_iter(2 * pr + 1, kB, vB);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        consume_iter(2 * n_pairs - 2, kA, vA);
+        consume_iter(2 * n_pairs - 1, kB, vB);
+    }
+
+    // The new key: one more tile whose only valid key (index 0: lanes n = 0 for K, lane
+    // group 0's first row for V) is the row in LDS.
+    if (tail_new && wave == 0) {
+        unsigned kr[1][KL][4], vr[1][4][VW];
+#pragma unroll
+        for (int c = 0; c < KL; ++c)
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                kr[0][c][w] = n == 0 ? s_kr[(64 * c + 16 * g) / 4 + w] : 0u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int w = 0; w < VW; ++w)
+                vr[0][t][w] = (g == 0 && t == 0) ? s_vr[DV * n * EB / 4 + w] : 0u;
+        const int lim1[1] = {1};
+        consume(std::integral_constant<int, 1>{}, kr, vr, lim1);
+    }
+
+    // ---- epilogue: the waves' states meet in LDS (as decode_kernel's) -------------------
+    constexpr int WS = S::WS;
+    float *s_acc = smem + S::OFF_ACC;
+    float *s_m = smem + S::OFF_M;
+    float *s_l = smem + S::OFF_L;
+    float lt = l_own + eb::lane_xor16(l_own);
+    lt += eb::lane_xor32(lt);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float lh =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lt), h));
+        if (lane == 0) {
+            s_m[h * kWaves + wave] = mh[h];
+            s_l[h * kWaves + wave] = lh;
+        }
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int r = 0; r < G; ++r)
+#pragma unroll
+            for (int e4 = 0; e4 < DV; e4 += 4)
+                *reinterpret_cast<f32x4 *>(s_acc + wave * WS + r * HD + DV * n + e4) =
+                    f32x4{acc[e4][r], acc[e4 + 1][r], acc[e4 + 2][r], acc[e4 + 3][r]};
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * HD; idx += kThreads) {
+        const int gi = idx / HD;
+        const int d = idx % HD;
+        const f32x4 m4 = *reinterpret_cast<const f32x4 *>(s_m + gi * kWaves);
+        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(s_l + gi * kWaves);
+        const float M = fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w));
+        const float mref = (M == -INFINITY) ? 0.0f : M;
+        const float w0 = eb::fast_exp2(m4.x - mref), w1 = eb::fast_exp2(m4.y - mref);
+        const float w2 = eb::fast_exp2(m4.z - mref), w3 = eb::fast_exp2(m4.w - mref);
+        const float A = (w0 * s_acc[idx] + w1 * s_acc[WS + idx]) +
+                        (w2 * s_acc[2 * WS + idx] + w3 * s_acc[3 * WS + idx]);
+        const float L = (w0 * l4.x + w1 * l4.y) + (w2 * l4.z + w3 * l4.w);
+        const int hh = head0 + gi;
+        if (a.nsplit == 1) {
+            a.o[(size_t)hh * HD + d] = A / L;
+        } else {
+            a.part_acc[((size_t)split * a.h + hh) * HD + d] = A;
+            if (d == 0) {
+                a.part_ml[((size_t)split * a.h + hh) * 2 + 0] = M;
+                a.part_ml[((size_t)split * a.h + hh) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
 // Log-sum-exp merge of the split partials (a second launch, so the partials written by
 // every XCD are visible without in-kernel fences). Grid (h, ceil(HD / DS)): a workgroup owns
 // DS dims of one head (dims past HD in the last block are read as anything and not stored); thread (grp, d) of GROUPS = 256/DS groups folds splits grp,
@@ -708,13 +1259,27 @@ struct DecodePlan {
     int nsplit = 1;  // splits along the key axis
 };
 
+// E4M3 caches at head dims 64 and 128 run decode_mx_kernel.
+template <int HD, int EB>
+constexpr bool use_mx() {
+    return EB_DECODE_MX != 0 && EB == 1 && mx_head_dim(HD);
+}
+
+template <int HD, int G, int EB>
+constexpr int keys_per_iter_of() {
+    if constexpr (use_mx<HD, EB>())
+        return MxShape<HD, G>::KEYS_PER_ITER;
+    else
+        return DecodeShapeOf<HD, G, EB>::KEYS_PER_ITER;
+}
+
 template <int G, int EB>
 int keys_per_iter_g(size_t hd) {
 #define EB_KPI(D) \
-    case D: return DecodeShapeOf<D, G, EB>::KEYS_PER_ITER;
+    case D: return keys_per_iter_of<D, G, EB>();
     switch (hd) {
         EB_HEAD_DIMS(EB_KPI)
-        default: return DecodeShapeOf<256, G, EB>::KEYS_PER_ITER;
+        default: return keys_per_iter_of<256, G, EB>();
     }
 #undef EB_KPI
 }
@@ -772,6 +1337,13 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
 
 template <int HD, int G, int EB>
 hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+    if constexpr (use_mx<HD, EB>()) {
+        using M = MxShape<HD, G>;
+        static_assert(M::LDS_BYTES <= 64 * 1024, "decode_mx_kernel LDS");
+        dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
+        decode_mx_kernel<HD, G><<<grid, kThreads, M::LDS_BYTES, st>>>(a);
+        return hipSuccess;
+    }
     using S = DecodeShapeOf<HD, G, EB>;
     static std::once_flag once;
     static hipError_t attr_err = hipSuccess;

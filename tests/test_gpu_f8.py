@@ -376,3 +376,55 @@ def test_attention_forward_with_f8_cache(dev):
         assert_close(o8, want, what=f"span {a}..{b} vs oracle on the e4m3 cache")
         r = rel_l2_f64(o8, o32)
         assert r <= F8_REL_L2, f"span {a}..{b} vs f32-cache layer: rel={r:.3e}"
+
+
+@pytest.mark.parametrize("H,Hkv,hd,prompt", [(32, 8, 128, 700), (16, 8, 64, 333), (8, 8, 128, 65)])
+def test_fused_decode_norms_rope_f8(dev, H, Hkv, hd, prompt):
+    """Decode steps over an E4M3 cache with the fused prologue (per-head RMSNorm of q, k and
+    v with gains, partial RoPE): a prompt through Attention.forward_qkv fills the cache, then
+    three single-row steps. Each step's output against the oracle's norm + RoPE chain and
+    attention over the cache as the layer left it (FP32 bar); the row the step wrote against
+    the oracle's processed k / v rounded to E4M3, bit for bit wherever a change of a few
+    ulps in f32 cannot move the rounding."""
+    eps, max_seq = 1e-6, 1024
+    sc = float(oracle.default_scale(hd))
+    note(f"fused decode norms f8 H={H} Hkv={Hkv} hd={hd} prompt={prompt}")
+    gq = (1 + 0.1 * oracle.randn((hd,), 61)).astype(np.float32)
+    gk = (1 + 0.1 * oracle.randn((hd,), 62)).astype(np.float32)
+    gv = (1 + 0.1 * oracle.randn((hd,), 63)).astype(np.float32)
+    attn = eb.Attention(H, Hkv, hd, sc, q_norm=upload(dev, gq), k_norm=upload(dev, gk),
+                        v_norm=upload(dev, gv), norm_eps=eps)
+    ra = hd // 4
+    rope = eb.Rope.build_partial(dev, max_seq, hd, ra, 1e6)
+    cos, sin = oracle.rope_tables(max_seq, hd, 1e6, rope_angles=ra)
+    kv = eb.KvCache.new(dev, 1, max_seq, Hkv, hd, eb.DType.F8E4M3)
+    n = prompt + 3
+    xq = oracle.randn((n, H * hd), 64)
+    xk = oracle.randn((n, Hkv * hd), 65)
+    xv = oracle.randn((n, Hkv * hd), 66)
+    rec = eb.Recorder(dev)
+    attn.forward_qkv(rec, upload(dev, xq[:prompt]), upload(dev, xk[:prompt]),
+                     upload(dev, xv[:prompt]), rope, kv, 0, prompt, 0)
+    rec.submit()
+    for pos in range(prompt, n):
+        rec = eb.Recorder(dev)
+        out = attn.forward_qkv(rec, upload(dev, xq[pos:pos + 1]), upload(dev, xk[pos:pos + 1]),
+                               upload(dev, xv[pos:pos + 1]), rope, kv, 0, 1, pos)
+        rec.submit()
+        got = out.to_f32().reshape(H, hd)
+        kc = oracle.f8_values(bits_of(kv.k[0])).reshape(max_seq, Hkv, hd)
+        vc = oracle.f8_values(bits_of(kv.v[0])).reshape(max_seq, Hkv, hd)
+        qp = oracle.rope(oracle.rmsnorm(xq[pos], gq, H, hd, eps), cos, sin, 1, H, hd, pos)
+        want = oracle.attn_decode(qp, kc, vc, H, Hkv, pos, hd, max_seq, sc, threads=16)
+        assert_close(got, want, what=f"step pos={pos}")
+        kp = oracle.rope(oracle.rmsnorm(xk[pos], gk, Hkv, hd, eps), cos, sin, 1, Hkv, hd, pos)
+        vp = oracle.rmsnorm(xv[pos], gv, Hkv, hd, eps)
+        for name, cache, ref in (("k", kv.k[0], kp), ("v", kv.v[0], vp)):
+            row = bits_of(cache).reshape(max_seq, Hkv * hd)[pos]
+            lo = oracle.f8_bits(ref * (1 - 1e-6))
+            hi = oracle.f8_bits(ref * (1 + 1e-6))
+            sure = lo == hi
+            assert sure.mean() > 0.99
+            assert np.array_equal(row[sure], lo[sure]), f"{name} row {pos}"
+            assert np.all(np.abs(oracle.f8_values(row) - ref) <= np.abs(ref) / 16 + 2.0 ** -10), \
+                f"{name} row {pos} within half an E4M3 step"
