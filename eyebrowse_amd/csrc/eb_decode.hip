@@ -897,7 +897,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_mx_kernel(DecodeArgs a) {
                 if (amax > 0.0f && amax <= 3.0e38f) {
                     frexpf(amax, &ex);
                     ex = 14 - ex;  // amax * 2^ex in [2^13, 2^14)
-                    ex = ex < -64 ? -64 : ex > 64 ? 64 : ex;
+                    // (2^ex and 2^-ex stay normal floats; below 2^-112 a head's q ends in
+                    // f16 subnormals, scores of that size being nothing next to 0)
+                    ex = ex < -126 ? -126 : ex > 126 ? 126 : ex;
                 }
 #pragma unroll
                 for (int i = 0; i < NP; ++i) {

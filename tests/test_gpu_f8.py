@@ -428,3 +428,27 @@ def test_fused_decode_norms_rope_f8(dev, H, Hkv, hd, prompt):
             assert np.array_equal(row[sure], lo[sure]), f"{name} row {pos}"
             assert np.all(np.abs(oracle.f8_values(row) - ref) <= np.abs(ref) / 16 + 2.0 ** -10), \
                 f"{name} row {pos} within half an E4M3 step"
+
+
+@pytest.mark.parametrize("qscale", [1e-20, 1e20, 1e30])
+@pytest.mark.parametrize("h,hkv,hd", [(32, 8, 128), (8, 8, 64)])
+def test_decode_f8_q_magnitudes(dev, h, hkv, hd, qscale):
+    """q far from unit size over an E4M3 cache (the decode splits q into f16 halves after a
+    per-head power of two): tiny q gives the mean of V, huge q the V row of the best key;
+    both against the oracle on the rounded cache at the FP32 bar."""
+    max_seq, pos = 2048, 1500
+    note(f"f8 decode q x {qscale:g} h={h} hkv={hkv} hd={hd}")
+    sc = float(oracle.default_scale(hd))
+    kc = oracle.randn((max_seq, hkv, hd), 71)
+    vc = oracle.randn((max_seq, hkv, hd), 72)
+    q = (oracle.randn((h, hd), 73) * np.float32(qscale)).astype(np.float32)
+    kt, vt = f8_cache(dev, kc), f8_cache(dev, vc)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode(rec, upload(dev, q), kt, vt, ot, h, hkv, pos, hd, max_seq, sc)
+    rec.submit()
+    got = ot.to_f32().reshape(h, hd)
+    assert np.isfinite(got).all()
+    want = oracle.attn_decode(q, rounded(kc), rounded(vc), h, hkv, pos, hd, max_seq, sc,
+                              threads=16)
+    assert_close(got, want, what=f"q x {qscale:g}")
