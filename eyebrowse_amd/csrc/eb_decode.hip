@@ -34,7 +34,7 @@
 // that split's first head-subgroup workgroup also copies knew/vnew into cache row `pos`.
 // Nothing else touches that row in the launch, so the copy is exact and race free.
 //
-// E4M3 caches at head dims 64 and 128 run decode_mx_kernel instead (below): the same
+// E4M3 caches at head dims 64, 128 and 256 run decode_mx_kernel instead (below): the same
 // grid, split plan, partials and merge, with both products on the matrix cores.
 //
 // The result is softmax(scale * q K^T) V over keys 0..=pos; it differs from the
@@ -622,7 +622,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 
 // ---- E4M3 caches on the matrix cores ----------------------------------------------------
 //
-// decode_mx_kernel<HD, G>: OCP FP8 E4M3 caches at head dims 64 and 128. Same grid, split
+// decode_mx_kernel<HD, G>: OCP FP8 E4M3 caches at head dims 64, 128 and 256. Same grid, split
 // plan, partial layout and merge as decode_kernel. Per byte an E4M3 cache carries four times
 // the f32 elements, and the lane-wise kernel's multiply-add per element and head bounds it
 // (67 % of wave cycles issuing VALU at Mistral 32k keys); here both products run on the
@@ -651,10 +651,8 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 // folded in by the owning split's wave 0 as one more tile with a single valid key, through
 // the same code as the cache rows.
 // Measured against decode_kernel (HIP events, decode steps from graphs): Mistral 32k keys
-// 25.0 -> 20.0 us, Qwen L=8191 12.8 -> 10.7 us. The same scheme over IEEE-half caches
-// measured slower (27.6 -> 28.4 us at Mistral 32k keys: a load-only copy of it took 28.1,
-// so its K-row loads, 64 bytes of 16 rows each, bound it), and so did head dim 256 (its
-// loads and accumulators leave no registers: 20.0 -> 20.5 us at Gemma-4 16k keys).
+// 25.0 -> 20.0 us, Qwen L=8191 12.8 -> 10.7 us, Gemma-4 16k keys 20.6 -> 18.9 us. The same
+// scheme over IEEE-half caches measured 3-5 % slower than decode_kernel.
 // 0 runs decode_kernel over E4M3 caches too (the comparison above).
 #ifndef EB_DECODE_MX
 #define EB_DECODE_MX 1
@@ -663,19 +661,21 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr bool mx_head_dim(int hd) { return hd == 64 || hd == 128; }
+constexpr bool mx_head_dim(int hd) { return hd == 64 || hd == 128 || hd == 256; }
 
 template <int HD, int G>
 struct MxShape {
     static constexpr int EB = 1;
-    static_assert(mx_head_dim(HD), "head dim 64 or 128");
+    static_assert(mx_head_dim(HD), "head dim 64, 128 or 256");
     static constexpr int KPW = 16;                 // keys per wave step (one tile)
     static constexpr int NC = HD / 32;             // 32-dim chunks of a key row
     static constexpr int KL = NC / 2;              // K loads per tile and lane (16 bytes)
     static constexpr int DV = HD / 16;             // V dims per lane per row
     static constexpr int VW = DV * EB / 4;         // words per lane per V row
-    // Tiles per iteration: each of the two register buffers holds U tiles' loads.
-    static constexpr int U = 2;
+    // Tiles per iteration: each of the two register buffers holds U tiles' loads. Head
+    // dim 256 takes one (its tiles' loads, accumulators and q halves fill the registers:
+    // two measured 8 % slower).
+    static constexpr int U = HD == 256 ? 1 : 2;
     static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
     static constexpr int RW = HD * EB / 4;         // words of one cache row (one KV head)
     static constexpr int WS = G * HD + 4;          // epilogue state per wave (floats)
@@ -1261,7 +1261,7 @@ struct DecodePlan {
     int nsplit = 1;  // splits along the key axis
 };
 
-// E4M3 caches at head dims 64 and 128 run decode_mx_kernel.
+// E4M3 caches at head dims 64, 128 and 256 run decode_mx_kernel.
 template <int HD, int EB>
 constexpr bool use_mx() {
     return EB_DECODE_MX != 0 && EB == 1 && mx_head_dim(HD);
