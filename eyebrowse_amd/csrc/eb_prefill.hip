@@ -1257,16 +1257,17 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
 }
 
 
-// Key chunks: when the query blocks alone would leave most of the CUs idle (fewer than
-// kPrefillFewUnits workgroups: short prompts, a short chunk over a long cache), each
-// block's key tiles are cut into chunks of ctiles tiles, one workgroup each, merged
-// afterwards. The chunk length (in steps of KSPLIT tiles) is the one among smax, smax/2,
+// Key chunks: when the query blocks alone fill at most half of the workgroup slots
+// (short prompts, a short chunk over a long cache), each block's key tiles are cut into
+// chunks of ctiles tiles, one workgroup each, merged afterwards. Measured against one
+// workgroup per block (us per prompt): Qwen T=1024 (128 blocks) 61.8 -> 49.8, Mistral
+// T=512 / 1024 44.0 -> 40.1 / 79.6 -> 69.3, Gemma-4 T=1024 148.7 -> 97.2; beyond half the
+// slots it measured slower (Qwen T=2048: 117.5 -> 126, T=4096: 262 -> 319), the
+// heaviest-first order of the blocks already balancing the triangle there. The chunk length (in steps of KSPLIT tiles) is the one among smax, smax/2,
 // ... kPrefillMinSteps with the smallest estimated makespan: rounds of kPrefillSlots
 // workgroups per CU slot, each costing its steps plus kPrefillFixedSteps (a prologue and
 // an epilogue take about 8 us where a step takes 3.4 us).
-// Each chunk pays the q fragment, one unhidden staging step and an epilogue, which at
-// 256 block workgroups (a 2048-token prompt) cost what the better balance gains.
-constexpr int kPrefillFewUnits = 128;
+// Each chunk pays the q fragment, one unhidden staging step and an epilogue.
 constexpr int kPrefillSlots = 256;
 constexpr int kPrefillFixedSteps = 2;
 constexpr int kPrefillMinSteps = 2;
@@ -1293,13 +1294,13 @@ PrefillChunks prefill_chunks(size_t hd, int H, int Hkv, const PrefillRange &r) {
         return u * ngroups;
     };
     PrefillChunks ch;
-    if ((long)nqb * ngroups >= kPrefillFewUnits) return ch;
-    // Halving candidates from smax down to kPrefillMinSteps steps, scored by the makespan
-    // of rounds of kPrefillSlots workgroups, each costing a fixed part (prologue and
-    // epilogue, about kPrefillFixedSteps steps) plus its chunk's steps.
     // (4-wave workgroups at head_dim <= 128 run two per CU)
     const long slots = (sh.hpw * sh.wph * sh.ksplit == 4 && hd <= 128) ? 2 * kPrefillSlots
                                                                         : kPrefillSlots;
+    if (2L * nqb * ngroups > slots) return ch;
+    // Halving candidates from smax down to kPrefillMinSteps steps, scored by the makespan
+    // of rounds of `slots` workgroups, each costing a fixed part (prologue and epilogue,
+    // about kPrefillFixedSteps steps) plus its chunk's steps.
     int cs = smax;
     long best = -1;
     for (int c = smax;; c = (c + 1) / 2) {
