@@ -1259,11 +1259,14 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
 
 // Key chunks: when the query blocks alone fill at most half of the workgroup slots
 // (short prompts, a short chunk over a long cache), each block's key tiles are cut into
-// chunks of ctiles tiles, one workgroup each, merged afterwards. Measured against one
-// workgroup per block (us per prompt): Qwen T=1024 (128 blocks) 61.8 -> 49.8, Mistral
-// T=512 / 1024 44.0 -> 40.1 / 79.6 -> 69.3, Gemma-4 T=1024 148.7 -> 97.2; beyond half the
-// slots it measured slower (Qwen T=2048: 117.5 -> 126, T=4096: 262 -> 319), the
-// heaviest-first order of the blocks already balancing the triangle there. The chunk length (in steps of KSPLIT tiles) is the one among smax, smax/2,
+// chunks of ctiles tiles, one workgroup each, merged afterwards; between half and all of
+// the slots, only the heaviest blocks are halved; beyond, the heaviest-first order of the
+// blocks balances the causal triangle by itself. Measured against one workgroup per block
+// (us per prompt): Qwen T=1024 (128 blocks) 61.8 -> 49.8, Mistral T=512 / 1024 44.0 ->
+// 40.1 / 79.6 -> 69.3, Gemma-4 T=1024 148.7 -> 97.2; halving: Qwen T=2048 112.7 -> 105.8,
+// Mistral 175.8 -> 161.7, Gemma-4 275.0 -> 221.8 (the planner's chunk sizes there, 640
+// workgroups at Qwen T=2048, measured slower: 126); Qwen T=4096, beyond: 262 -> 319 with
+// chunks. The chunk length (in steps of KSPLIT tiles) is the one among smax, smax/2,
 // ... kPrefillMinSteps with the smallest estimated makespan: rounds of kPrefillSlots
 // workgroups per CU slot, each costing its steps plus kPrefillFixedSteps (a prologue and
 // an epilogue take about 8 us where a step takes 3.4 us).
@@ -1297,7 +1300,17 @@ PrefillChunks prefill_chunks(size_t hd, int H, int Hkv, const PrefillRange &r) {
     // (4-wave workgroups at head_dim <= 128 run two per CU)
     const long slots = (sh.hpw * sh.wph * sh.ksplit == 4 && hd <= 128) ? 2 * kPrefillSlots
                                                                         : kPrefillSlots;
-    if (2L * nqb * ngroups > slots) return ch;
+    const long blocks = (long)nqb * ngroups;
+    if (blocks > slots) return ch;
+    if (2 * blocks > slots) {
+        // Between half and all of the slots: the blocks of more than half the heaviest
+        // one's steps are halved (the merge then reads at most two chunks).
+        ch.ctiles = (smax + 1) / 2 * sh.ksplit;
+        int nmax = 1;
+        for (int qb = 0; qb < nqb; ++qb) nmax = std::max(nmax, span(qb) / ch.ctiles + 1);
+        ch.nchmax = nmax;
+        return ch;
+    }
     // Halving candidates from smax down to kPrefillMinSteps steps, scored by the makespan
     // of rounds of `slots` workgroups, each costing a fixed part (prologue and epilogue,
     // about kPrefillFixedSteps steps) plus its chunk's steps.

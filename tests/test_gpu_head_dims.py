@@ -84,10 +84,10 @@ def test_prefill(dev, hd, h, hkv, T):
 @pytest.mark.parametrize("hd", [80, 96, 192])
 def test_raw_prefill_launches(dev, hd):
     """The plain raw launch (split while staging) and the _ws launch (pre-split) give the
-    same bits at a padded head dim, and match the oracle (256 query-block workgroups, more
-    than half the workgroup slots, so the _ws launch cuts no key chunks, which would sum in
+    same bits at a padded head dim, and match the oracle (512 query-block workgroups, more
+    than the workgroup slots, so the _ws launch cuts no key chunks, which would sum in
     another order)."""
-    h, hkv, T = 16, 8, 2048
+    h, hkv, T = 16, 8, 4096
     note(f"raw prefill hd={hd}")
     sc = float(oracle.default_scale(hd))
     q, k, v = (oracle.randn(s, 30 + i) for i, s in enumerate(((T, h, hd), (T, hkv, hd), (T, hkv, hd))))
