@@ -42,6 +42,8 @@ def check(got, want, what):
 
 @pytest.mark.parametrize("name,H,Hkv,hd,T", [
     ("qwen", 16, 8, 128, 512),
+    ("qwen", 16, 8, 128, 1024),
+    ("qwen", 16, 8, 128, 2048),
     ("qwen", 16, 8, 128, 4096),
     ("mistral", 32, 8, 128, 4096),
 ])
