@@ -561,6 +561,24 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     const int qi = q0 + col;
     const int pi = qbase + qi;
 
+    // The first step's K/V loads (into registers, or for head_dim 256 memory-to-LDS) go out
+    // right behind the q fragment's, so that the two latencies overlap.
+    f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
+    static_assert(!(PS && FAST && C::PS_IMAGE), "f16-mode records for head_dim <= 128");
+    f32x4 rs[PS ? (FAST ? C::FPSN : C::PSN) : 1];
+    const float *recs =
+        PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
+    auto load_first_step = [&] {
+        if constexpr (PS && FAST)
+            fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+        else if constexpr (PS && C::PS_IMAGE)
+            ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
+        else if constexpr (PS)
+            ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+        else
+            prefill_load_step<C, EB>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
+    };
+
     // Q fragment. SQK: query qi scaled by 2^-eq (its largest magnitude in [2^14, 2^15))
     // and split into f16 hi/lo, dims ks*16 + hf*8 .. +8 for every 16-dim step ks; else
     // f32, head dims [HALF*hf, HALF*hf + HALF).
@@ -573,20 +591,26 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
         f32x4 qa[NKS], qb[NKS];
         const float qs = qv ? scale_log2 : 0.0f;
         float mx = 0.0f;
+        // Every lane loads (rows past the end from the clamped row 0) and scales by qs, 0
+        // past the end, so that the loads issue back to back; such a lane's query column
+        // never reaches the output. Dims past hdr (a head dim padded up to this
+        // instantiation) are zeros.
+#pragma unroll
+        for (int k2 = 0; k2 < NKS; ++k2) {
+            const bool in = 16 * k2 < hdr;  // (uniform)
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            qa[k2] = in ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) : z;
+            qb[k2] = in ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) : z;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_first_step();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k2 = 0; k2 < NKS; ++k2) {
             // The softmax scale (log2 units) is applied to q before its split, so the
-            // product needs no multiply per score. Every lane loads (rows past the end
-            // from the clamped row 0) and scales by qs, 0 past the end, so that the loads
-            // issue back to back; such a lane's query column never reaches the output.
-            // Dims past hdr (a head dim padded up to this instantiation) are zeros.
-            if (16 * k2 < hdr) {  // (uniform)
-                qa[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2) * qs;
-                qb[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) * qs;
-            } else {
-                qa[k2] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                qb[k2] = qa[k2];
-            }
+            // product needs no multiply per score.
+            qa[k2] = qa[k2] * qs;
+            qb[k2] = qb[k2] * qs;
             const float m8 = fmaxf(fmaxf(fmaxf(fabsf(qa[k2].x), fabsf(qa[k2].y)),
                                          fmaxf(fabsf(qa[k2].z), fabsf(qa[k2].w))),
                                    fmaxf(fmaxf(fabsf(qb[k2].x), fabsf(qb[k2].y)),
@@ -613,6 +637,7 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     }
     float qreg[C::SQK ? 1 : HALF];
     if constexpr (!C::SQK) {
+        load_first_step();
         const bool qv = qi < rows;
         const float *qp = q + ((size_t)(qv ? qi : 0) * H + head) * HD + HALF * hf;
         if constexpr (HALF % 4 == 0) {
@@ -643,24 +668,15 @@ __global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
     int E = FAST ? 0 : kZeroRowExp;
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
-    f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
-    static_assert(!(PS && FAST && C::PS_IMAGE), "f16-mode records for head_dim <= 128");
-    f32x4 rs[PS ? (FAST ? C::FPSN : C::PSN) : 1];
-    const float *recs =
-        PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
-    if constexpr (PS && FAST) {
-        fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+    // ... and the first step's K/V into LDS.
+    if constexpr (PS && FAST)
         fps_store_step<C>(smem, rs, 0, tid);
-    } else if constexpr (PS && C::PS_IMAGE) {
-        ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
+    else if constexpr (PS && C::PS_IMAGE)
         wait_vm_all();
-    } else if constexpr (PS) {
-        ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+    else if constexpr (PS)
         ps_store_step<C>(smem, rs, 0, tid);
-    } else {
-        prefill_load_step<C, EB>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
+    else
         prefill_store_step<C, FAST>(smem, rk, rv, 0, tid);
-    }
     __syncthreads();
 
     // The next step's K/V: PS records into registers (or, head_dim 256, straight into the
