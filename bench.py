@@ -24,7 +24,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --only trace --workload NAME   (one workload, for rocprofv3)
        python bench.py --trace-summary OUT.md TITLE CMD LABEL=CSV ...   (no GPU)
        python bench.py --pmc-summary FETCH.csv WRITE.csv OUT.json       (no GPU)
-       python bench.py --sq-summary OUT.md CMD CSV [CSV ...]             (no GPU)
+       python bench.py --sq-summary OUT.md CMD [WORKLOAD=]CSV ...        (no GPU)
 """
 from __future__ import annotations
 
@@ -740,13 +740,16 @@ def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
     waiting on any instruction, and on LDS instructions; LDS bank-conflict cycles per
     LDS-active cycle; and the matrix pipe's busy share, SQ_VALU_MFMA_BUSY_CYCLES /
     (1024 SIMDs x GRBM_GUI_ACTIVE / 8), GRBM_GUI_ACTIVE being the sum of the 8 XCDs' busy
-    cycles (so the share is of the cycles the kernel ran, at the clock it ran at)."""
+    cycles (so the share is of the cycles the kernel ran, at the clock it ran at).
+    A CSV given as WORKLOAD=PATH labels its rows with that workload (the passes of one
+    workload merge into its rows), so that configs whose kernels share a grid stay apart."""
     import csv
     merged, ndisp = {}, {}
-    for path in csv_paths:
+    for arg in csv_paths:
+        label, path = arg.split("=", 1) if "=" in arg else ("", arg)
         tot, disp = {}, {}
         for r in csv.DictReader(open(path)):
-            key = (_kernel_name(r["Kernel_Name"]), r.get("Grid_Size", ""))
+            key = (label, _kernel_name(r["Kernel_Name"]), r.get("Grid_Size", ""))
             c = tot.setdefault(key, {})
             c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
             disp.setdefault(key, set()).add(r["Dispatch_Id"])
@@ -759,14 +762,14 @@ def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
     names = sorted({n for c in merged.values() for n in c})
     lines = ["# SQ counters per dispatch", "", "Command (from the repository root on the GPU "
              "box, `R=$PWD`):", "", "```", cmd, "```", "",
-             "| kernel | grid | dispatches | " + " | ".join(names) +
+             "| workload | kernel | grid | dispatches | " + " | ".join(names) +
              " | VALU/MFMA | MFMA busy cyc/MFMA | wait share | LDS wait share |"
              " LDS conflict/active | MFMA pipe busy |",
-             "|---" * (3 + len(names) + 6) + "|"]
+             "|---" * (4 + len(names) + 6) + "|"]
     for key, avg in merged.items():
         mf = avg.get("SQ_INSTS_MFMA", 0)
         ratio = lambda a, b: f"{a / b:.2f}" if b else "-"  # noqa: E731
-        lines.append(f"| `{key[0]}` | {key[1]} | {ndisp[key]} | " +
+        lines.append(f"| {key[0] or '-'} | `{key[1]}` | {key[2]} | {ndisp[key]} | " +
                      " | ".join(f"{avg[k]:.0f}" if k in avg else "-" for k in names) + " | " +
                      ratio(avg.get("SQ_INSTS_VALU", 0), mf) + " | " +
                      ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0), mf) + " | " +
@@ -924,7 +927,7 @@ def main():
         return
     if args.sq_summary:
         if len(args.sq_summary) < 3:
-            raise SystemExit("--sq-summary OUT_MD CMD CSV [CSV ...]")
+            raise SystemExit("--sq-summary OUT_MD CMD [WORKLOAD=]CSV ...")
         sq_summary(*args.sq_summary)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
