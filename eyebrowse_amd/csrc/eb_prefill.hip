@@ -51,6 +51,7 @@
 #include "eb_internal.h"
 
 #include <algorithm>
+#include <climits>
 #include <mutex>
 
 namespace {
@@ -79,6 +80,7 @@ __device__ __forceinline__ float sub_f16_hi(unsigned h2, float x) {
 }
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
+constexpr size_t kLdsBytesPerCu = 160 * 1024;  // gfx950 LDS per CU
 constexpr float kSlack = 8.0f;  // log2 units the reference max may lag a score (SPV)
 constexpr int kUnitSlack = 8;   // bits a P V term may exceed its query's O^T unit (SPV)
 
@@ -346,21 +348,54 @@ __device__ __forceinline__ int ps_lds_offset(int kt, int w) {
     return C::STEP_KEYS * C::KS + C::VFL + (e >= 8 ? C::STEP_KEYS : 0) + kt * kTile + 4 * (e % 8);
 }
 
+// Raw buffer resource over n 16-byte records at p: base and size are made wave-uniform, so
+// the descriptor lives in scalar registers and each load adds a scalar record offset to the
+// lane's 32-bit one (no per-lane 64-bit address arithmetic).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const f32x4 *p, int n) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(p);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    void *u = reinterpret_cast<void *>(((unsigned long long)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(16 * n),
+                                             0x00020000 /* raw, 32-bit data, range checked */);
+}
+__device__ __forceinline__ f32x4 chunk_load(__amdgpu_buffer_rsrc_t r, int lane_chunk,
+                                            int uniform_chunk) {
+    return __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                   r, 16 * lane_chunk, __builtin_amdgcn_readfirstlane(16 * uniform_chunk), 0));
+}
+
 // Fetch the pre-split records of tiles tile0 .. tile0 + KSPLIT - 1 (clamped to the last
 // record, nt - 1; a clamped buffer is never read) of one KV head (recs).
 template <class C>
 __device__ __forceinline__ void ps_load_step(const f32x4 *__restrict__ recs,
                                              f32x4 (&r)[C::PSN], int tile0, int nt, int tid) {
     constexpr int HD = C::HD_;
+    if constexpr ((16 * HD) % C::THREADS == 0) {
+        // Load i reads chunks [(i % PER) * THREADS, + THREADS) of tile tile0 + i / PER: a
+        // buffer load whose record offset is the same for the whole wave (a scalar operand),
+        // the lane adding tid. (A KV head's records stay below 2 GiB: the launch checks.)
+        constexpr int PER = 16 * HD / C::THREADS;
+        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::PS_CH);
 #pragma unroll
-    for (int i = 0; i < C::PSN - 1; ++i) {
-        const int c = min(tid + i * C::THREADS, C::PS_KV - 1);
-        const int t = min(tile0 + c / (16 * HD), nt - 1);
-        r[i] = recs[(size_t)t * C::PS_CH + c % (16 * HD)];
+        for (int i = 0; i < C::PSN - 1; ++i) {
+            r[i] = chunk_load(rs, tid,
+                              min(tile0 + i / PER, nt - 1) * C::PS_CH + (i % PER) * C::THREADS);
+        }
+        const int kt = min(tid / 16, C::STEP_KEYS / kTile - 1);
+        r[C::PSN - 1] = chunk_load(rs, min(tile0 + kt, nt - 1) * C::PS_CH + 16 * HD + tid % 16, 0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < C::PSN - 1; ++i) {
+            const int c = min(tid + i * C::THREADS, C::PS_KV - 1);
+            const int t = min(tile0 + c / (16 * HD), nt - 1);
+            r[i] = recs[(size_t)t * C::PS_CH + c % (16 * HD)];
+        }
+        const int kt = min(tid / 16, C::STEP_KEYS / kTile - 1);
+        const int t = min(tile0 + kt, nt - 1);
+        r[C::PSN - 1] = recs[(size_t)t * C::PS_CH + 16 * HD + tid % 16];
     }
-    const int kt = min(tid / 16, C::STEP_KEYS / kTile - 1);
-    const int t = min(tile0 + kt, nt - 1);
-    r[C::PSN - 1] = recs[(size_t)t * C::PS_CH + 16 * HD + tid % 16];
 }
 
 template <class C>
@@ -393,11 +428,21 @@ template <class C>
 __device__ __forceinline__ void fps_load_step(const f32x4 *__restrict__ recs,
                                               f32x4 (&r)[C::FPSN], int tile0, int nt, int tid) {
     constexpr int HD = C::HD_;
+    if constexpr ((8 * HD) % C::THREADS == 0) {
+        constexpr int PER = 8 * HD / C::THREADS;  // (as in ps_load_step)
+        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::FPS_CH);
 #pragma unroll
-    for (int i = 0; i < C::FPSN; ++i) {
-        const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
-        const int t = min(tile0 + c / (8 * HD), nt - 1);
-        r[i] = recs[(size_t)t * C::FPS_CH + c % (8 * HD)];
+        for (int i = 0; i < C::FPSN; ++i) {
+            r[i] = chunk_load(rs, tid,
+                              min(tile0 + i / PER, nt - 1) * C::FPS_CH + (i % PER) * C::THREADS);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < C::FPSN; ++i) {
+            const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
+            const int t = min(tile0 + c / (8 * HD), nt - 1);
+            r[i] = recs[(size_t)t * C::FPS_CH + c % (8 * HD)];
+        }
     }
 }
 
@@ -504,9 +549,28 @@ __device__ __forceinline__ void wait_vm_all() {
 // FAST (an opt-in mode, f32 K/V without pre-split records): q, K, V and P are rounded to
 // f16 once and each product is one f16 MFMA (instead of three on exact hi/lo splits); the
 // online softmax, its rescaling and the accumulation stay f32.
+//
+// Occupancy: the dynamic LDS the launch asks for (LDS_BYTES) bounds the waves per SIMD;
+// the compiler, which does not see it, is told that bound, so that it does not trade the
+// schedule for an occupancy the LDS never allows. 4-wave workgroups at head_dim <= 128 run
+// two per CU, so at least two waves per SIMD.
+template <int HD, int HPW, int WPH, int KSPLIT>
+constexpr int prefill_min_waves() {
+    return (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1;
+}
+template <int HD, int HPW, int WPH, int KSPLIT>
+constexpr int prefill_max_waves() {
+    constexpr size_t lds = PrefillCfg<HD, HPW, WPH, KSPLIT>::LDS_BYTES;
+    constexpr int wgs = lds > 0 ? (int)(kLdsBytesPerCu / lds) : 8;
+    constexpr int w = (wgs < 1 ? 1 : wgs) * HPW * WPH * KSPLIT / 4;
+    constexpr int lo = prefill_min_waves<HD, HPW, WPH, KSPLIT>();
+    return w < lo ? lo : w > 8 ? 8 : w;
+}
 template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false>
-__global__ __launch_bounds__(HPW * WPH * KSPLIT * 64,
-                             (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1) void prefill_kernel(
+__global__ __attribute__((
+    amdgpu_flat_work_group_size(1, HPW * WPH * KSPLIT * 64),
+    amdgpu_waves_per_eu(prefill_min_waves<HD, HPW, WPH, KSPLIT>(),
+                        prefill_max_waves<HD, HPW, WPH, KSPLIT>()))) void prefill_kernel(
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     const float *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
     int Hkv, int rows, int nkeys, int qbase, int window, float scale_log2, int nqb,
@@ -1269,6 +1333,9 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
                        : hd == 64  ? PrefillCfg<64, 4, 1, 1>::PS_FLOATS
                        : hd == 128 ? PrefillCfg<128, 4, 1, 1>::PS_FLOATS
                                    : PrefillCfg<256, 4, 1, 1>::PS_FLOATS;
+    // (the record loads take 32-bit byte offsets within one KV head's records: beyond
+    // 2 GiB of them, about 2M keys, the kernel stages K/V itself)
+    if (hd <= 128 && (size_t)presplit_nt(r) * rec * sizeof(float) > (size_t)INT_MAX) return 0;
     return hkv * (size_t)presplit_nt(r) * rec;
 }
 
@@ -1493,7 +1560,9 @@ size_t fast_workspace_floats(size_t hp, int H, int Hkv, int s) {
     const size_t rec = hp == 32 ? PrefillCfg<32, 4, 1, 1>::FPS_FLOATS
                        : hp == 64 ? PrefillCfg<64, 4, 1, 1>::FPS_FLOATS
                                   : PrefillCfg<128, 4, 1, 1>::FPS_FLOATS;
-    return (size_t)Hkv * (size_t)((s + kTile - 1) / kTile) * rec;
+    const size_t nt = (size_t)((s + kTile - 1) / kTile);
+    if (nt * rec * sizeof(float) > (size_t)INT_MAX) return 0;  // (as in presplit_floats)
+    return (size_t)Hkv * nt * rec;
 }
 
 template <int HD, int HPW, int WPH, int KSPLIT>
