@@ -48,10 +48,13 @@ SOURCES = [
 ]
 
 
-# Per-source flags. eb_decode.hip: matrix-core results in VGPRs (the narrow-cache decode
-# rescales its accumulators on the VALU; with AGPR results every tile copied them across).
+# Per-source flags: matrix-core results in VGPRs. The narrow-cache decode and the
+# head_dim 256 prefill rescale their accumulators on the VALU; with AGPR results the
+# compiler copied every accumulator across on every tile (the prefill: 128 copies at the
+# top of each step, for a rescale most steps skip). Kernels without AGPRs are unchanged.
 SOURCE_FLAGS = {
     "eb_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "eb_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

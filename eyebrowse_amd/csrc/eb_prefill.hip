@@ -585,7 +585,7 @@ __global__ __attribute__((
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: scalar registers)
     const int hf = lane >> 5;
     const int col = lane & 31;
     const int ks = wave / (HPW * WPH);     // key split this wave takes
