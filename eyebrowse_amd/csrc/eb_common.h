@@ -133,4 +133,18 @@ __device__ __forceinline__ unsigned f8x4_bits(f32x4_t x) {
            (f8e4m3_bits(x[3]) << 24);
 }
 
+// Raw buffer resource over [p, p + nbytes) (gfx9 raw buffer: 32-bit data, range checked:
+// a load at or past nbytes reads zeros without touching memory). The operands are made
+// wave-uniform explicitly so that the descriptor lives in scalar registers (a per-lane
+// descriptor costs a loop per load); p and nbytes must be the same in every lane.
+constexpr int kRawBufferFlags = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int nbytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(p);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+    void *u = reinterpret_cast<void *>(((unsigned long long)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(nbytes),
+                                             kRawBufferFlags);
+}
+
 }  // namespace eb

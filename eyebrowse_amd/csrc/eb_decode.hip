@@ -74,7 +74,6 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxSplits = 256;  // per column
-constexpr int kRawBufferFlags = 0x00020000;  // gfx9 raw buffer: 32-bit data, range checked
 constexpr float kSlack = 8.0f;  // log2-units a score may exceed the reference max by
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -168,16 +167,7 @@ __device__ __forceinline__ void store_cache4(void *base, size_t off, f32x4 x) {
         *reinterpret_cast<f32x4 *>(static_cast<float *>(base) + off) = x;
 }
 
-// Raw buffer resource over [p, p + nbytes). The operands are made wave-uniform explicitly
-// so that the descriptor lives in SGPRs (a per-lane descriptor costs a loop per load).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int nbytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    void *u = reinterpret_cast<void *>(((uint64_t)hi << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(nbytes),
-                                             kRawBufferFlags);
-}
+using eb::make_rsrc;
 
 __device__ __forceinline__ f32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset,
                                                int soffset = 0) {

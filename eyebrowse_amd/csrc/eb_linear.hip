@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <climits>
 #include <mutex>
 
 namespace {
@@ -274,7 +275,39 @@ __global__ __launch_bounds__(kThreads, MINB) void linear_gemm_kernel(const float
         const int row = min(m0 + idx / X4, M - 1);
         rs[j] = -(int)ex[row];
     }
+    // Whole contraction stages and buffers below 2 GiB (every model's projections): raw
+    // buffer loads, the lane's byte offset computed once and the stage's as a scalar; rows
+    // past M (x) or N (w) lie past the buffer's end and read as zeros. Otherwise clamped,
+    // selected loads.
+    const bool fast = K % kBK == 0 && (size_t)M * K * 4 <= (size_t)INT_MAX &&
+                      (size_t)N * K * 2 <= (size_t)INT_MAX;
+    const __amdgpu_buffer_rsrc_t xres = eb::make_rsrc(x, fast ? M * K * 4 : 0);
+    const __amdgpu_buffer_rsrc_t wres = eb::make_rsrc(w, fast ? N * K * 2 : 0);
+    unsigned xoff[NX], woff[NW];
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+        const int idx = tid + j * kThreads;
+        xoff[j] = ((unsigned)(m0 + idx / X4) * (unsigned)K + (unsigned)(idx % X4) * 4u) * 4u;
+    }
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int idx = tid + j * kThreads;
+        woff[j] = ((unsigned)(n0 + idx / W8) * (unsigned)K + (unsigned)(idx % W8) * 8u) * 2u;
+    }
     auto load_stage = [&](int k0) {
+        if (fast) {
+            const int kx = __builtin_amdgcn_readfirstlane(4 * k0);  // (uniform: scalar)
+            const int kw = __builtin_amdgcn_readfirstlane(2 * k0);
+#pragma unroll
+            for (int j = 0; j < NX; ++j)
+                rx[j] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, (int)xoff[j], kx, 0));
+#pragma unroll
+            for (int j = 0; j < NW; ++j)
+                rw[j] = __builtin_bit_cast(
+                    f16x8, __builtin_amdgcn_raw_buffer_load_b128(wres, (int)woff[j], kw, 0));
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
             const int idx = tid + j * kThreads;

@@ -352,12 +352,7 @@ __device__ __forceinline__ int ps_lds_offset(int kt, int w) {
 // the descriptor lives in scalar registers and each load adds a scalar record offset to the
 // lane's 32-bit one (no per-lane 64-bit address arithmetic).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const f32x4 *p, int n) {
-    const unsigned long long a = reinterpret_cast<unsigned long long>(p);
-    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
-    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
-    void *u = reinterpret_cast<void *>(((unsigned long long)hi << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(16 * n),
-                                             0x00020000 /* raw, 32-bit data, range checked */);
+    return eb::make_rsrc(p, 16 * n);
 }
 __device__ __forceinline__ f32x4 chunk_load(__amdgpu_buffer_rsrc_t r, int lane_chunk,
                                             int uniform_chunk) {
