@@ -140,6 +140,22 @@ def test_decode_validation_and_workspace():
     assert l.eb_attn_decode_workspace_floats(6, 4, 5, 8, 256) == 0  # bad heads -> 0
 
 
+def test_prefill_record_workspace_bound():
+    """The record loads take 32-bit byte offsets within one KV head's records: a head whose
+    pre-split (or f16-mode) records would pass 2 GiB gets none (its workgroups stage K/V
+    themselves), so the workspace shrinks to the rest. One KV head, head_dim 128: a
+    pre-split record is 16*128 + 16 chunks of 16 bytes (8256 floats) per 32 keys, an
+    f16-mode record 8*128 chunks (4096 floats)."""
+    l = eb.lib()
+    rec, frec = 4 * (16 * 128 + 16), 4 * 8 * 128
+    # 2^20 keys: 32768 records, 1.08 GB
+    assert l.eb_attn_prefill_workspace_floats(1, 1, 128, 0, 1 << 20, 0) == 32768 * rec
+    # 2^21 keys: 2.16 GB of records, past the bound
+    assert l.eb_attn_prefill_workspace_floats(1, 1, 128, 0, 1 << 21, 0) == 0
+    assert l.eb_attn_prefill_fast_workspace_floats(1, 1, 128, 1 << 21) == 65536 * frec
+    assert l.eb_attn_prefill_fast_workspace_floats(1, 1, 128, 1 << 22) == 0  # 2^31 bytes
+
+
 def test_chunk_and_window_validation():
     l = eb.lib()
     # rows [60, 76) past max_seq 70
