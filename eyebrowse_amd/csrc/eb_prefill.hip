@@ -1231,6 +1231,43 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(
     if (nch <= 1) return;
     const size_t cstride = (size_t)rows * H;  // (row, head) pairs per chunk
     const size_t at0 = (size_t)row * H + head;
+    if (nch <= kMergeBatch) {
+        // One batch holds every chunk: one memory round trip.
+        float4 ml[kMergeBatch], acc[kMergeBatch];
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            const size_t at = at0 + (size_t)min(j, nch - 1) * cstride;
+            ml[j] = *reinterpret_cast<const float4 *>(part_ml + at * 4);
+            acc[j] = *reinterpret_cast<const float4 *>(part_acc + at * HD + d);
+        }
+        float M = -INFINITY;
+        int EM = kZeroRowExp;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            M = fmaxf(M, ml[j].x);
+            EM = max(EM, __float_as_int(ml[j].z));
+        }
+        const float Mr = (M == -INFINITY) ? 0.0f : M;
+        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) {
+            if (j < nch) {
+                const float w = eb::fast_exp2(ml[j].x - Mr);
+                const int sh = __float_as_int(ml[j].z) - EM;
+                L += w * ml[j].y;
+                A.x += w * ldexpf(acc[j].x, sh);
+                A.y += w * ldexpf(acc[j].y, sh);
+                A.z += w * ldexpf(acc[j].z, sh);
+                A.w += w * ldexpf(acc[j].w, sh);
+            }
+        }
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4 *>(o + at0 * hdr + d) =
+            make_float4(ldexpf(A.x * inv, EM), ldexpf(A.y * inv, EM), ldexpf(A.z * inv, EM),
+                        ldexpf(A.w * inv, EM));
+        return;
+    }
     float M = -INFINITY;
     int EM = kZeroRowExp;
     for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
