@@ -454,14 +454,20 @@ __device__ __forceinline__ void fps_store_step(float *smem, const f32x4 (&r)[C::
     }
 }
 
+// The pre-split and pre-convert passes' shape: one 32-key tile per workgroup (the records'
+// layout), 512 threads at head_dim >= 128 (more of the tile's loads and stores in flight
+// per CU: the LDS allows two such workgroups per CU at 256, four at 128; measured 1-2 %
+// faster on 512- and 1024-row prompts, long prompts unchanged), 256 below.
+template <int HD>
+using PresplitCfg = PrefillCfg<HD, 4, HD >= 128 ? 2 : 1, 1>;
+
 // Pre-convert pass of the f16 mode: workgroup (t, kvh) rounds keys [(tlo + t) * 32, +32) of KV
 // head kvh to f16 as the f16 mode's staging does, and writes the tile's record.
 template <int HD>
-__global__ __launch_bounds__(256) void preconvert_kernel(const float *__restrict__ k,
-                                                         const float *__restrict__ v,
-                                                         float *__restrict__ ps, int nkeys,
-                                                         int Hkv, int nt, int hdr) {
-    using C = PrefillCfg<HD, 4, 1, 1>;
+__global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void preconvert_kernel(
+    const float *__restrict__ k, const float *__restrict__ v, float *__restrict__ ps, int nkeys,
+    int Hkv, int nt, int hdr) {
+    using C = PresplitCfg<HD>;
     static_assert(HD <= 128, "f16-mode records for head_dim <= 128");
     __shared__ float smem[C::BUF];
     const int t = blockIdx.x;
@@ -480,12 +486,6 @@ __global__ __launch_bounds__(256) void preconvert_kernel(const float *__restrict
 // (rows past nkeys as zeros) exactly as the prefill's own staging does, and writes the
 // tile's record. The prefill then only copies records into LDS: the split is done once
 // per key instead of once per workgroup that reads the key.
-// The pre-split pass's shape: one 32-key tile per workgroup (the records' layout), 512
-// threads at head_dim >= 128 (more of the tile's loads and stores in flight per CU: the
-// LDS allows two such workgroups per CU at 256, four at 128; measured 1-4 % faster on
-// 512- and 1024-row prompts, long prompts unchanged), 256 below.
-template <int HD>
-using PresplitCfg = PrefillCfg<HD, 4, HD >= 128 ? 2 : 1, 1>;
 
 template <int HD, int EB>
 __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
@@ -1613,8 +1613,8 @@ eb_status launch_prefill_fast_t(hipStream_t st, const float *q, const float *k, 
     if constexpr (HD <= 128) {
         if (r.ws) {
             const int nt = presplit_nt(r);
-            preconvert_kernel<HD><<<dim3((unsigned)nt, (unsigned)Hkv), 256, 0, st>>>(
-                k, v, r.ws, r.nkeys, Hkv, nt, r.hdr);
+            preconvert_kernel<HD><<<dim3((unsigned)nt, (unsigned)Hkv), PresplitCfg<HD>::THREADS,
+                                    0, st>>>(k, v, r.ws, r.nkeys, Hkv, nt, r.hdr);
             const eb_status err = eb::check_launch("attn_prefill_fast (pre-convert)");
             if (err != EB_OK) return err;
             return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, true, true>(
