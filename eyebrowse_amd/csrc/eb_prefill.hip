@@ -1340,14 +1340,23 @@ size_t padded_hd(size_t hd) {
     return p;
 }
 
-// The workgroup shape launch_prefill_hd picks for head_dim hd and g query heads per KV head:
-// HPW heads x WPH 32-row blocks x KSPLIT key splits.
+// The workgroup shape launch_prefill_hd picks for head_dim hd, H query heads, g per KV
+// head, and `rows` query rows: HPW heads x WPH 32-row blocks x KSPLIT key splits. Four or
+// more heads per KV head at head_dim <= 128 take 4 heads x 32 rows in 4-wave workgroups,
+// two per CU, when that grid is more than one round of them (Mistral T=4096: 1024 blocks,
+// 283 vs 256 TFLOP/s against two key splits); up to one round, two key splits in 8-wave
+// workgroups, one per CU (Mistral T=512 37.4 -> 35.9 us, T=2048 156.4 -> 148.8, T=1024
+// unchanged: the causal blocks balance over two rounds of workgroups instead of one).
 struct PrefillShape {
     int hpw, wph, ksplit;
 };
-PrefillShape prefill_shape(size_t hd, int g) {
+constexpr int kPrefillSlots = 256;  // workgroup slots of one round: one per CU
+PrefillShape prefill_shape(size_t hd, int H, int g, int rows) {
     const int hpw = g % 4 == 0 ? 4 : g % 2 == 0 ? 2 : 1;
-    return {hpw, 4 / hpw, (hpw == 4 || hd > 128) ? 1 : 2};
+    if (hd > 128) return {hpw, 4 / hpw, 1};
+    if (hpw < 4) return {hpw, 4 / hpw, 2};
+    const long blocks = (long)((rows + kTile - 1) / kTile) * (H / 4);
+    return {4, 1, blocks > 2 * kPrefillSlots ? 1 : 2};
 }
 
 // The pre-split pass pays one read and one write of the keys in range; it is used when at
@@ -1367,7 +1376,7 @@ int presplit_nt(const PrefillRange &r) { return (r.nkeys + kTile - 1) / kTile - 
 
 size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
     if (hd < 32 || r.rows <= 0 || r.nkeys <= 0) return 0;
-    const int qb_rows = kTile * prefill_shape(hd, (int)(h / hkv)).wph;
+    const int qb_rows = kTile * prefill_shape(hd, (int)h, (int)(h / hkv), r.rows).wph;
     const int nqb = (r.rows + qb_rows - 1) / qb_rows;
     if (nqb < (hd > 128 ? kPresplitMinBlocks256 : kPresplitMinBlocks)) return 0;
     const size_t rec = hd == 32    ? PrefillCfg<32, 4, 1, 1>::PS_FLOATS
@@ -1379,7 +1388,6 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
     if (hd <= 128 && (size_t)presplit_nt(r) * rec * sizeof(float) > (size_t)INT_MAX) return 0;
     return hkv * (size_t)presplit_nt(r) * rec;
 }
-
 
 // Key chunks: when the query blocks alone fill at most half of the workgroup slots
 // (short prompts, a short chunk over a long cache), each block's key tiles are cut into
@@ -1395,7 +1403,6 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
 // workgroups per CU slot, each costing its steps plus kPrefillFixedSteps (a prologue and
 // an epilogue take about 8 us where a step takes 3.4 us).
 // Each chunk pays the q fragment, one unhidden staging step and an epilogue.
-constexpr int kPrefillSlots = 256;
 constexpr int kPrefillFixedSteps = 2;
 constexpr int kPrefillMinSteps = 2;
 struct PrefillChunks {
@@ -1403,7 +1410,7 @@ struct PrefillChunks {
     int nchmax = 1;        // most chunks of one block
 };
 PrefillChunks prefill_chunks(size_t hd, int H, int Hkv, const PrefillRange &r) {
-    const PrefillShape sh = prefill_shape(hd, H / Hkv);
+    const PrefillShape sh = prefill_shape(hd, H, H / Hkv, r.rows);
     const int QB = kTile * sh.wph;
     const int ngroups = Hkv * (H / Hkv / sh.hpw);
     const int nqb = (r.rows + QB - 1) / QB;
@@ -1544,9 +1551,9 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
 }
 
 // head_dim <= 128:
-//  - 4 query heads per KV head or more: 4 waves = 4 heads x 32 rows, no key split, two
-//    workgroups per CU. 32-row blocks already give 4x more workgroups than CU slots, so
-//    the dispatcher balances the causal triangle.
+//  - 4 query heads per KV head or more: 4 heads x 32 rows, as 4 waves without a key split
+//    (two workgroups per CU) when the grid is more than one round of those, else as 8
+//    waves with two key splits (prefill_shape).
 //  - otherwise: 8 waves (2 per SIMD) = 4 (head, 32-row) slots x 2 key splits, which
 //    halves the longest per-wave chain where the blocks are 64 or 128 rows tall.
 // head_dim 256: the Q fragment and O^T accumulators take ~450 registers per lane, so one
@@ -1557,7 +1564,11 @@ eb_status launch_prefill_hd(hipStream_t st, const float *q, const void *k, const
                             float scale_log2) {
     const int g = H / Hkv;
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
-    if (g % 4 == 0) return launch_prefill_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, scale_log2);
+    if (g % 4 == 0) {
+        if (KSPLIT == 2 && prefill_shape(HD, H, g, r.rows).ksplit == 2)
+            return launch_prefill_t<HD, 4, 1, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
+        return launch_prefill_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, scale_log2);
+    }
     if (g % 2 == 0)
         return launch_prefill_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
     return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
@@ -1596,7 +1607,7 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
 // keys; head dims above 128 stage directly.
 size_t fast_workspace_floats(size_t hp, int H, int Hkv, int s) {
     if (hp < 32 || hp > 128 || s <= 0) return 0;
-    const int qb_rows = kTile * prefill_shape(hp, H / Hkv).wph;
+    const int qb_rows = kTile * prefill_shape(hp, H, H / Hkv, s).wph;
     if ((s + qb_rows - 1) / qb_rows < kPresplitMinBlocks) return 0;
     const size_t rec = hp == 32 ? PrefillCfg<32, 4, 1, 1>::FPS_FLOATS
                        : hp == 64 ? PrefillCfg<64, 4, 1, 1>::FPS_FLOATS
