@@ -1641,7 +1641,11 @@ eb_status launch_prefill_fast_hd(hipStream_t st, const float *q, const float *k,
                                  float *o, int H, int Hkv, const PrefillRange &r, float sl2) {
     const int g = H / Hkv;
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
-    if (g % 4 == 0) return launch_prefill_fast_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, sl2);
+    if (g % 4 == 0) {  // (the accurate path's choice, prefill_shape)
+        if (KSPLIT == 2 && prefill_shape(HD, H, g, r.rows).ksplit == 2)
+            return launch_prefill_fast_t<HD, 4, 1, KSPLIT>(st, q, k, v, o, H, Hkv, r, sl2);
+        return launch_prefill_fast_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, sl2);
+    }
     if (g % 2 == 0) return launch_prefill_fast_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, r, sl2);
     return launch_prefill_fast_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, r, sl2);
 }
