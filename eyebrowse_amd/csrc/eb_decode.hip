@@ -173,7 +173,8 @@ using eb::make_rsrc;
 // per step and the step's bytes exceed the L2s and the Infinity Cache, so keeping them only
 // evicts lines for nothing. Measured against the default policy, A/B on one box (GB/s per
 // step): Mistral 32k keys 5705 -> 6143, Gemma-4 16k 5656 -> 6160, Qwen L=8191 4045 ->
-// 4419, Qwen L=2048 1947 -> 2034; sc1 (alone: no change; with nt: as nt alone).
+// 4419, Qwen L=2048 1947 -> 2034, the half cache at Mistral 32k keys 27.7 -> 26.6 us; sc1
+// (alone: no change; with nt: as nt alone).
 constexpr int kStreamPolicy = 2;  // gfx950 cache-policy bits: 1 sc0, 2 nt, 16 sc1
 
 __device__ __forceinline__ f32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset,
@@ -689,7 +690,10 @@ struct MxShape {
     static constexpr size_t LDS_BYTES = sizeof(float) * (size_t)(OFF_L + G * kWaves);
 };
 
-// W words of a row slice from a raw buffer (range-checked by the resource).
+// W words of a row slice from a raw buffer (range-checked by the resource). The E4M3
+// matrix-core kernel's loads keep the default cache policy: non-temporal ones measured
+// mixed there (Qwen L=8191 10.71 -> 10.35 us, Mistral 32k keys 20.05 -> 20.8, Gemma-4
+// 16k unchanged).
 template <int W>
 __device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t r, int voff,
                                            int soff) {
@@ -698,7 +702,7 @@ __device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t
         for (int i = 0; i < W / 4; ++i) {
             const u32x4 v = __builtin_bit_cast(
                 u32x4,
-                __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + 16 * i, kStreamPolicy));
+                __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + 16 * i, 0));
             dst[4 * i + 0] = v[0];
             dst[4 * i + 1] = v[1];
             dst[4 * i + 2] = v[2];
@@ -706,12 +710,12 @@ __device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t
         }
     } else if constexpr (W == 2) {
         const u32x2 v = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kStreamPolicy));
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
         dst[0] = v[0];
         dst[1] = v[1];
     } else {
         static_assert(W == 1, "1, 2 or a multiple of 4 words");
-        dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kStreamPolicy);
+        dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
     }
 }
 
