@@ -173,8 +173,8 @@ using eb::make_rsrc;
 // per step and the step's bytes exceed the L2s and the Infinity Cache, so keeping them only
 // evicts lines for nothing. Measured against the default policy, A/B on one box (GB/s per
 // step): Mistral 32k keys 5705 -> 6143, Gemma-4 16k 5656 -> 6160, Qwen L=8191 4045 ->
-// 4419, Qwen L=2048 1947 -> 2034, the half cache at Mistral 32k keys 27.7 -> 26.6 us; sc1
-// (alone: no change; with nt: as nt alone).
+// 4419, Qwen L=2048 1947 -> 2034, the half cache at Mistral 32k keys 27.7 -> 26.6 us; sc0
+// or sc1 alone: no change; either with nt: as nt alone.
 constexpr int kStreamPolicy = 2;  // gfx950 cache-policy bits: 1 sc0, 2 nt, 16 sc1
 
 __device__ __forceinline__ f32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, int voffset,
