@@ -147,7 +147,7 @@ struct PrefillCfg {
 // values): conditionally written register arrays end up in scratch memory.
 // EB: bytes per k/v element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
 // here (exactly).
-template <class C, int EB>
+template <class C, int EB, bool NT = false>
 __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
                                                   const void *__restrict__ v,
                                                   f32x4 (&rk)[C::NLD], f32x4 (&rv)[C::NLD],
@@ -175,8 +175,10 @@ __device__ __forceinline__ void prefill_load_step(const void *__restrict__ k,
             vx = eb::f8x4_to_f32(
                 *reinterpret_cast<const unsigned *>(static_cast<const uint8_t *>(v) + off));
         } else {
-            kx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(k) + off);
-            vx = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(v) + off);
+            const f32x4 *kp = reinterpret_cast<const f32x4 *>(static_cast<const float *>(k) + off);
+            const f32x4 *vp = reinterpret_cast<const f32x4 *>(static_cast<const float *>(v) + off);
+            kx = NT ? __builtin_nontemporal_load(kp) : *kp;
+            vx = NT ? __builtin_nontemporal_load(vp) : *vp;
         }
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         rk[r] = in ? kx : z;
@@ -487,7 +489,7 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void preconvert_kernel(
 // tile's record. The prefill then only copies records into LDS: the split is done once
 // per key instead of once per workgroup that reads the key.
 
-template <int HD, int EB>
+template <int HD, int EB, bool NT>
 __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
     const void *__restrict__ k, const void *__restrict__ v, float *__restrict__ ps, int nkeys,
     int Hkv, int tlo, int nt, int hdr) {
@@ -503,7 +505,7 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
     // (An image record's padding is left as it is: K rows are read within their HD floats,
     // V^T rows within their 32 keys, and the exponents where written.)
     f32x4 rk[C::NLD], rv[C::NLD];
-    prefill_load_step<C, EB>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
+    prefill_load_step<C, EB, NT>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
     prefill_store_step<C>(smem, rk, rv, 0, tid);
     __syncthreads();
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::PS_FLOATS);
@@ -1365,6 +1367,7 @@ PrefillShape prefill_shape(size_t hd, int H, int g, int rows) {
 // chunks of 128 and 192 rows over long caches: 2 Qwen blocks -8.5 %, 3 +6 %, 4 Mistral
 // blocks +4-9 %, 2 Gemma-4 blocks +10 %).
 constexpr int kPresplitMinBlocks = 3;
+constexpr size_t kPresplitStreamBytes = (size_t)128 << 20;
 constexpr int kPresplitMinBlocks256 = 2;
 
 // First tile and number of tiles the pre-split records cover: every key some query of the
@@ -1518,14 +1521,22 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
             const int nt = presplit_nt(r);
             float *ps = r.ws;
             const dim3 grid((unsigned)nt, (unsigned)Hkv);
+            // f32 K/V beyond half the Infinity Cache are read with non-temporal loads
+            // (measured over chunks of 128-256 rows: 268 MB of cache -3 to -7 %, 67 MB
+            // unchanged; prompts and caches of 33 MB, likely still cached after their
+            // write, 1-5 % slower with them).
+            const bool stream = (size_t)nt * kTile * Hkv * r.hdr * 4 * 2 > kPresplitStreamBytes;
             if (r.ce == eb::CacheElem::F16)
-                presplit_kernel<HD, 2><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
+                presplit_kernel<HD, 2, false><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
                     k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
             else if (r.ce == eb::CacheElem::E4M3)
-                presplit_kernel<HD, 1><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
+                presplit_kernel<HD, 1, false><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
+                    k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
+            else if (stream)
+                presplit_kernel<HD, 4, true><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
                     k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
             else
-                presplit_kernel<HD, 4><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
+                presplit_kernel<HD, 4, false><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
                     k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
             const eb_status err = eb::check_launch("attn_prefill (pre-split)");
             if (err != EB_OK) return err;
