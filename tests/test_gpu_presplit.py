@@ -55,6 +55,7 @@ def rows_check(got, q, k, v, h, hkv, s, hd, sc, starts=None):
 @pytest.mark.parametrize("h,hkv,s,hd", [
     (64, 32, 1024, 128),   # 2 heads x 2 blocks x 2 key splits per workgroup
     (128, 32, 1024, 128),  # 4 heads per workgroup, one record per step
+    (64, 16, 1024, 128),   # 4 heads x 2 key splits (GQA 4 grid of one 4-wave round)
     (96, 32, 1024, 128),   # GQA 3: 1 head x 4 blocks x 2 key splits
     (128, 128, 512, 64),
     (128, 128, 512, 32),
