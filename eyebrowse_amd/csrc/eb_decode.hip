@@ -270,12 +270,14 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
 // accumulators of 4 heads leave the two load buffers no registers (256 VGPRs and spills);
 // at 8 they take half (160 VGPRs, none spilled). Measured at 32k keys: 5.48 -> 5.77 TB/s;
 // more wave steps per iteration on the freed registers measured slower (2: 5.40, 3: 5.35,
-// 4: 5.26 TB/s), and so did 8 dims per lane for 2 heads per workgroup.
+// 4: 5.26 TB/s). 2 heads per workgroup (Qwen) measured slower at 8 dims per lane with
+// the default cache policy and faster with the non-temporal loads (L=8191 4.43 -> 4.52
+// TB/s, 2048 keys +1 %), so head_dim 128 f32 runs 8 dims per lane from 2 heads up.
 template <int HD, int G, int EB>
 using DecodeShapeOf = DecodeShape<HD, G,
                                   EB == 2 ? EB_DECODE_U16 : EB == 1 ? EB_DECODE_U8
                                                                     : (HD == 256 ? 2 : 1),
-                                  (EB == 4 && HD == 128 && G == 4) ? 8 : 16>;
+                                  (EB == 4 && HD == 128 && G >= 2) ? 8 : 16>;
 
 // EB: bytes per cache element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
 // as loaded. A narrow lane's loads hold 8 dims each (16 bytes of halves, 8 of E4M3), in the
