@@ -692,11 +692,16 @@ struct MxShape {
     static constexpr size_t LDS_BYTES = sizeof(float) * (size_t)(OFF_L + G * kWaves);
 };
 
-// W words of a row slice from a raw buffer (range-checked by the resource). The E4M3
-// matrix-core kernel's loads keep the default cache policy: non-temporal ones measured
-// mixed there (Qwen L=8191 10.71 -> 10.35 us, Mistral 32k keys 20.05 -> 20.8, Gemma-4
-// 16k unchanged).
-template <int W>
+// Cache policy of the E4M3 matrix-core kernel's loads. Non-temporal loads measured faster
+// at head_dim 256 (Gemma-4 16383 keys 19.34 -> 18.68 us per step, 8191 keys unchanged) and
+// without a pattern at head_dim 128 (Qwen 8191 keys 10.66 -> 10.32, but 2048 keys 9.22 ->
+// 9.53 and Mistral 16384 keys 13.2 -> 14.2 us), so only head_dim 256 streams them.
+template <int HD>
+constexpr int mx_load_policy() { return HD == 256 ? kStreamPolicy : 0; }
+
+// W words of a row slice from a raw buffer (range-checked by the resource), with cache
+// policy AUX.
+template <int W, int AUX>
 __device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t r, int voff,
                                            int soff) {
     if constexpr (W % 4 == 0) {
@@ -704,7 +709,7 @@ __device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t
         for (int i = 0; i < W / 4; ++i) {
             const u32x4 v = __builtin_bit_cast(
                 u32x4,
-                __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + 16 * i, 0));
+                __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + 16 * i, AUX));
             dst[4 * i + 0] = v[0];
             dst[4 * i + 1] = v[1];
             dst[4 * i + 2] = v[2];
@@ -712,12 +717,12 @@ __device__ __forceinline__ void load_words(unsigned *dst, __amdgpu_buffer_rsrc_t
         }
     } else if constexpr (W == 2) {
         const u32x2 v = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, AUX));
         dst[0] = v[0];
         dst[1] = v[1];
     } else {
         static_assert(W == 1, "1, 2 or a multiple of 4 words");
-        dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+        dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, AUX);
     }
 }
 
@@ -757,6 +762,7 @@ __device__ __forceinline__ f16x8 k_operand(const unsigned (*kr)[4], int c) {
 
 template <int HD, int G>
 __global__ __launch_bounds__(kThreads, 1) void decode_mx_kernel(DecodeArgs a) {
+    constexpr int AUX = mx_load_policy<HD>();
     using S = MxShape<HD, G>;
     constexpr int EB = S::EB;
     constexpr int U = S::U, NC = S::NC, KL = S::KL, DV = S::DV, VW = S::VW;
@@ -805,9 +811,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_mx_kernel(DecodeArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
-            for (int c = 0; c < KL; ++c) load_words<4>(kr[u][c], kres, kvo[u], 64 * c);
+            for (int c = 0; c < KL; ++c) load_words<4, AUX>(kr[u][c], kres, kvo[u], 64 * c);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) load_words<VW>(vr[u][t], vres, vvo[u] + t * row_bytes, 0);
+            for (int t = 0; t < 4; ++t) load_words<VW, AUX>(vr[u][t], vres, vvo[u] + t * row_bytes, 0);
         }
     };
 
