@@ -1314,6 +1314,8 @@ int keys_per_iter(size_t hd, int G, eb::CacheElem ce) {
     }
 }
 
+constexpr size_t kMinSplitKeys = 128;
+
 // Workgroups to aim for per CU.
 int wgs_per_cu() {
     static int v = [] {
@@ -1340,6 +1342,10 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     size_t nsplit = std::max<size_t>(1, target / cols);
     nsplit = std::min(nsplit, std::max<size_t>(1, keys / (2 * iter_rows)));
     nsplit = std::min(nsplit, (size_t)kMaxSplits);
+    // Fewer than kMinSplitKeys keys stay in one split: the merge launch then costs more
+    // than the split saves (Qwen3 width at 101 keys: one split 6.5 us; three 5.5 us plus
+    // a 3 us merge in the kernel trace).
+    if (keys < kMinSplitKeys) nsplit = 1;
     // An iteration's loads address a window of iter_rows * nsplit cache rows from one
     // base with 32-bit offsets: keep the window under 2^30 bytes.
     const size_t row_bytes = hkv * hd * sizeof(float);

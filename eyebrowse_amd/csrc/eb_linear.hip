@@ -69,11 +69,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ---------------------------------------------------------------- few rows ------------
 constexpr int kRowsPerWave = 4;   // output features per wave
-constexpr int kChunkUnroll = 4;   // 16-byte weight chunks per lane in flight per feature
+// 16-byte weight chunks per lane in flight per feature: at most as many as a row holds per
+// lane (a pass over K = 1024 with 4 issued twice as many loads as it used, the clamped
+// ones all to the row's last chunk: the Qwen LM head, in 1024, read at 5.0 TB/s with 4 and
+// 6.2 TB/s with 2 chunks; 8 rows per wave at 2 chunks measured 6.1).
+constexpr int gemv_unroll(int k) { return k <= 512 ? 1 : k <= 1024 ? 2 : 4; }
 
 // MR: capacity in x rows (the launch passes m <= MR). Requires in % 8 == 0 and 16-byte
 // aligned x, w and rows (in % 8 == 0 keeps every row start aligned).
-template <int MR>
+template <int MR, int kChunkUnroll>
 __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__restrict__ x,
                                                                LinearSegs s, int m, int K) {
     const int lane = threadIdx.x & 63;
@@ -140,6 +144,19 @@ __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__re
             const float v = wave_sum(acc[r][i]);
             if (lane == 0 && i < m && o0 + r < N) s.y[sg][(size_t)i * N + o0 + r] = v;
         }
+}
+
+template <int U>
+void launch_gemv(unsigned blocks, hipStream_t st, const float *x, const LinearSegs &s, int m,
+                 int K) {
+    if (m <= 1)
+        linear_gemv_kernel<1, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+    else if (m <= 2)
+        linear_gemv_kernel<2, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+    else if (m <= 4)
+        linear_gemv_kernel<4, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+    else
+        linear_gemv_kernel<(int)eb::kLinearGemvRows, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
 }
 
 // ---------------------------------------------------------------- any shape -----------
@@ -534,14 +551,10 @@ eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_
             s.first[i + 1] = s.first[i] + (int)((out_f[i] + kRowsPerWave - 1) / kRowsPerWave);
         const unsigned blocks = (unsigned)((s.first[nseg] + kWaves - 1) / kWaves);
         const int mi = (int)m;
-        if (m <= 1)
-            linear_gemv_kernel<1><<<blocks, kThreads, 0, st>>>(x, s, mi, (int)in_f);
-        else if (m <= 2)
-            linear_gemv_kernel<2><<<blocks, kThreads, 0, st>>>(x, s, mi, (int)in_f);
-        else if (m <= 4)
-            linear_gemv_kernel<4><<<blocks, kThreads, 0, st>>>(x, s, mi, (int)in_f);
-        else
-            linear_gemv_kernel<kLinearGemvRows><<<blocks, kThreads, 0, st>>>(x, s, mi, (int)in_f);
+        const int u = gemv_unroll((int)in_f);
+        if (u == 1) launch_gemv<1>(blocks, st, x, s, mi, (int)in_f);
+        else if (u == 2) launch_gemv<2>(blocks, st, x, s, mi, (int)in_f);
+        else launch_gemv<4>(blocks, st, x, s, mi, (int)in_f);
         return check_launch("linear_f16w");
     }
     if (ws == nullptr || ws_floats < m) return fail(EB_SHAPE_MISMATCH, "linear: workspace too small");
