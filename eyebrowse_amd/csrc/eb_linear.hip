@@ -69,11 +69,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ---------------------------------------------------------------- few rows ------------
 constexpr int kRowsPerWave = 4;   // output features per wave
-// 16-byte weight chunks per lane in flight per feature: at most as many as a row holds per
-// lane (a pass over K = 1024 with 4 issued twice as many loads as it used, the clamped
-// ones all to the row's last chunk: the Qwen LM head, in 1024, read at 5.0 TB/s with 4 and
-// 6.2 TB/s with 2 chunks; 8 rows per wave at 2 chunks measured 6.1).
-constexpr int gemv_unroll(int k) { return k <= 512 ? 1 : k <= 1024 ? 2 : 4; }
+// 16-byte weight chunks per lane in flight per feature. Rows of up to 1024 halves take one
+// per pass: the Qwen LM head (in 1024) read at 5.0 TB/s with 4 (half of them clamped
+// repeats of the row's last chunk), 6.3 TB/s with 2 and 6.9 TB/s with 1; 8 features per
+// wave at 1 or 2 chunks measured 6.1-6.3. Longer rows keep 4.
+constexpr int gemv_unroll(int k) { return k <= 1024 ? 1 : 4; }
 
 // MR: capacity in x rows (the launch passes m <= MR). Requires in % 8 == 0 and 16-byte
 // aligned x, w and rows (in % 8 == 0 keeps every row start aligned).
@@ -551,9 +551,7 @@ eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_
             s.first[i + 1] = s.first[i] + (int)((out_f[i] + kRowsPerWave - 1) / kRowsPerWave);
         const unsigned blocks = (unsigned)((s.first[nseg] + kWaves - 1) / kWaves);
         const int mi = (int)m;
-        const int u = gemv_unroll((int)in_f);
-        if (u == 1) launch_gemv<1>(blocks, st, x, s, mi, (int)in_f);
-        else if (u == 2) launch_gemv<2>(blocks, st, x, s, mi, (int)in_f);
+        if (gemv_unroll((int)in_f) == 1) launch_gemv<1>(blocks, st, x, s, mi, (int)in_f);
         else launch_gemv<4>(blocks, st, x, s, mi, (int)in_f);
         return check_launch("linear_f16w");
     }
