@@ -72,7 +72,8 @@ constexpr int kRowsPerWave = 4;   // output features per wave
 // 16-byte weight chunks per lane in flight per feature. Rows of up to 1024 halves take one
 // per pass: the Qwen LM head (in 1024) read at 5.0 TB/s with 4 (half of them clamped
 // repeats of the row's last chunk), 6.3 TB/s with 2 and 6.9 TB/s with 1; 8 features per
-// wave at 1 or 2 chunks measured 6.1-6.3. Longer rows keep 4.
+// wave at 1 or 2 chunks measured 6.1-6.3. Longer rows keep 4: at in 4096 (the Mistral LM
+// head) 4 chunks read 6.39 TB/s, 2 chunks 5.93 and 1 chunk 6.22.
 constexpr int gemv_unroll(int k) { return k <= 1024 ? 1 : 4; }
 
 // MR: capacity in x rows (the launch passes m <= MR). Requires in % 8 == 0 and 16-byte
