@@ -168,6 +168,7 @@ SIGNATURES = {
                                  c_size, c_float]),
     "eb_launch_rope": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp, c_size, c_size,
                               c_size, c_size, c_size]),
+    "eb_launch_selftest_lane_ops": (c_st, [c_vp, c_vp, c_vp]),
     "eb_attn_decode_noalloc_max_floats": (c_size, []),
     "eb_launch_attn_decode_step_noalloc": (c_st, [c_vp, c_vp, c_size, c_vp, c_vp, c_size, c_vp,
                                                   c_size, c_vp, c_size, c_vp, c_size, c_size,

@@ -9,7 +9,7 @@
 // smallest i. NaN and values <= -3e38 never win; with no candidate the result is 0.
 //
 // Here every element gets a 64-bit key whose order is exactly that choice: the high 32
-// bits are the value's bits made monotonic, the low 32 bits 255 - bitrev8(i mod 256) and
+// bits are the value's bits made monotonic (-0.0 taken as +0.0), the low 32 bits 255 - bitrev8(i mod 256) and
 // 2^24 - 1 - i / 256 (so vocab < 2^32); non-candidates get key 0. The maximum key is the
 // reference's winner whatever order the keys are reduced in, so the work can be spread
 // over many workgroups: pass 1 reduces slices to one key each (workspace), pass 2 reduces
@@ -31,6 +31,9 @@ constexpr int kSlice = kThreads * kPerThread;
 __device__ __forceinline__ uint64_t key_of(float v, uint32_t i) {
     if (!(v > -3.0e38f)) return 0;  // NaN and values the reference's start never beats
     uint32_t u = __builtin_bit_cast(uint32_t, v);
+    // -0.0 and +0.0 compare equal under the reference's strict `>`, so they tie: both
+    // take +0.0's key, and the tie order below decides between them.
+    if ((u & 0x7FFFFFFFu) == 0) u = 0;
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     const uint32_t lane_rank = 255u - (__builtin_bitreverse32(i & 255u) >> 24);
     const uint32_t tb = (lane_rank << 24) | (0xFFFFFFu - (i >> 8));

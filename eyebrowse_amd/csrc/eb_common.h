@@ -37,16 +37,20 @@ __device__ __forceinline__ float group_sum(float x) {
 __device__ __forceinline__ float lane_xor16(float x) {
     const unsigned u = __builtin_bit_cast(unsigned, x);
     const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    unsigned r1 = r[1];
+    asm volatile("" : "+v"(r1));  // keep the two results distinct (see swap_sum32)
     const bool odd_row = (__lane_id() >> 4) & 1;
-    return __builtin_bit_cast(float, odd_row ? r[0] : r[1]);
+    return __builtin_bit_cast(float, odd_row ? r[0] : r1);
 }
 
 // The value held by lane i ^ 32 (v_permlane32_swap exchanges the wave's two halves).
 __device__ __forceinline__ float lane_xor32(float x) {
     const unsigned u = __builtin_bit_cast(unsigned, x);
     const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    unsigned r1 = r[1];
+    asm volatile("" : "+v"(r1));  // keep the two results distinct (see swap_sum32)
     const bool upper = __lane_id() >= 32;
-    return __builtin_bit_cast(float, upper ? r[0] : r[1]);
+    return __builtin_bit_cast(float, upper ? r[0] : r1);
 }
 
 // Reduce-scatter halves with the swaps: a + b over lane pairs i, i ^ 32 (swap_sum32) or

@@ -78,6 +78,34 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const float *__restrict
     for (unsigned i = lane; i < dim; i += 64) orow[i] = xr[i] * inv * w[i];
 }
 
+// Self-check of the wave lane exchanges that every reduction in these kernels is built
+// from (eb_common.h), on one wave: row r of out holds lane_xor16, lane_xor32, the class
+// reductions for FROM = 1, 2, 4, 8, 16, 32 (sums) and 1, 8 (maxima), swap_sum32 and
+// swap_sum16 of (a, b), and group_sum over 4 and 16 lanes, for a = in[0..64) and
+// b = in[64..128).
+__global__ __launch_bounds__(64) void lane_ops_kernel(const float *__restrict__ in,
+                                                      float *__restrict__ out) {
+    const int l = threadIdx.x;
+    const float a = in[l], b = in[64 + l];
+    float r[EB_LANE_OPS_ROWS];
+    r[0] = eb::lane_xor16(a);
+    r[1] = eb::lane_xor32(a);
+    r[2] = eb::class_reduce<1, false>(a);
+    r[3] = eb::class_reduce<2, false>(a);
+    r[4] = eb::class_reduce<4, false>(a);
+    r[5] = eb::class_reduce<8, false>(a);
+    r[6] = eb::class_reduce<16, false>(a);
+    r[7] = eb::class_reduce<32, false>(a);
+    r[8] = eb::class_reduce<1, true>(a);
+    r[9] = eb::class_reduce<8, true>(a);
+    r[10] = eb::swap_sum32(a, b);
+    r[11] = eb::swap_sum16(a, b);
+    r[12] = eb::group_sum<4>(a);
+    r[13] = eb::group_sum<16>(a);
+#pragma unroll
+    for (int i = 0; i < EB_LANE_OPS_ROWS; ++i) out[i * 64 + l] = r[i];
+}
+
 }  // namespace
 
 namespace eb {
@@ -126,6 +154,11 @@ eb_status launch_rmsnorm(hipStream_t st, const float *x, const float *w, float *
     unsigned blocks = (unsigned)((rows + 3) / 4);
     rmsnorm_kernel<<<blocks, kBlock, 0, st>>>(x, w, out, (unsigned)rows, (unsigned)dim, eps);
     return check_launch("rmsnorm");
+}
+
+eb_status launch_lane_ops(hipStream_t st, const float *in, float *out) {
+    lane_ops_kernel<<<1, 64, 0, st>>>(in, out);
+    return check_launch("lane_ops");
 }
 
 }  // namespace eb

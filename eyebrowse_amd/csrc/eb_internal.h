@@ -99,6 +99,13 @@ eb_status launch_attn_decode(hipStream_t st, const float *q, const float *kc, co
                              size_t window = 0);
 // eb_launch_attn_decode_step after its arguments are resolved: shape checks, the
 // workspace size check (workspace_floats must cover decode_workspace_floats), the launch.
+// One wave of lane-exchange results (eb_elementwise.hip, eb_launch_selftest_lane_ops).
+eb_status launch_lane_ops(hipStream_t st, const float *in, float *out);
+
+// The calling thread's current device's address of the no-allocation scratch array
+// (eb_noalloc.hip), looked up once per device; out may be null (set-up only).
+eb_status noalloc_scratch_of_current_device(float **out);
+
 eb_status decode_step_raw(hipStream_t st, const float *q, size_t q_numel, const float *knew,
                           const float *vnew, size_t new_numel, float *kc, size_t kc_numel,
                           float *vc, size_t vc_numel, float *o, size_t o_numel, size_t h,

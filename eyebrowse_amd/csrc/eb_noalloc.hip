@@ -5,9 +5,10 @@
 // part_ml). This variant keeps them in `scratch`, a file-scope device array of kScratchFloats
 // floats (4 MiB) that every GPU the library runs on holds until the process ends. The host
 // never passes `scratch` itself to a kernel: in host code the name is a stand-in, not a
-// device address. On the first call on a device, with that device current, the device's own
-// address of its copy is looked up (hipGetSymbolAddress) and kept per device ordinal; the
-// kernels take that address as their workspace argument. The partials need no clearing
+// device address. When a device is set up (eb_device_new), or else on the first call on a
+// device, with that device current, the device's own address of its copy is looked up
+// (hipGetSymbolAddress) and kept per device ordinal; the kernels take that address as
+// their workspace argument. The partials need no clearing
 // (every slot the merge reads is written first in the same launch sequence). All calls on
 // one GPU share its array: calls that overlap on one GPU (different streams, or threads
 // without ordering) race, so callers order them, e.g. on one stream.
@@ -24,8 +25,14 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float *g_scratch_ptr[kMaxDevices];  // per device ordinal: its copy's device address
 
-// The current device's copy of `scratch`, looked up once per device.
-eb_status scratch_of_current_device(float **out) {
+}  // namespace
+
+namespace eb {
+
+// The current device's copy of `scratch`, looked up once per device: by eb_device_new (the
+// library's set-up call, so that a later capture makes no lookup), or else by the first
+// no-allocation call on that device.
+eb_status noalloc_scratch_of_current_device(float **out) {
     int dev = -1;
     EB_HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= kMaxDevices)
@@ -37,11 +44,11 @@ eb_status scratch_of_current_device(float **out) {
         if (!p) return eb::fail(EB_OTHER, "no-allocation decode: scratch has no device address");
         g_scratch_ptr[dev] = static_cast<float *>(p);
     }
-    *out = g_scratch_ptr[dev];
+    if (out) *out = g_scratch_ptr[dev];
     return EB_OK;
 }
 
-}  // namespace
+}  // namespace eb
 
 extern "C" {
 
@@ -65,7 +72,7 @@ eb_status eb_launch_attn_decode_step_noalloc(void *stream, const float *q, size_
                             need, kScratchFloats);
     }
     float *ws = nullptr;
-    const eb_status st = scratch_of_current_device(&ws);
+    const eb_status st = eb::noalloc_scratch_of_current_device(&ws);
     if (st != EB_OK) return st;
     return eb::decode_step_raw((hipStream_t)stream, q, q_numel, knew, vnew, new_numel, kc,
                                kc_numel, vc, vc_numel, o, o_numel, h, hkv, pos, hd, max_seq,

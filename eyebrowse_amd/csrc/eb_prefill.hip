@@ -1223,6 +1223,32 @@ __global__ __attribute__((
 // Thread (pair, d4): four output dims of one (row, head) pair; the chunks' states are read
 // kMergeBatch at a time, all loads of a batch issued before any is used.
 constexpr int kMergeBatch = 8;
+// One chunk's term in the merge of key chunks: its Oᵀ partial acc is in units of 2^E
+// (E = ml.z's int bits) and carries the weight w = 2^d, d = m - Mr <= 0 (ml.x = m, the
+// chunk's running max in log2 units; Mr the row's largest). The term w·acc·2^E is
+// acc·2^f·2^G with f = d - floor(d) in [0, 1) and G = E + floor(d): merge_exp gives G,
+// and the row's reference exponent EM is the largest G, i.e. that of its largest weighted
+// term, so that a chunk of negligible weight but large V rows cannot push the others
+// below f32 range. d is clamped at -300: below that the term is under 2^-170 of any
+// finite E and rounds away in the sum.
+__device__ __forceinline__ int merge_exp(float4 ml, float Mr) {
+    if (ml.x == -INFINITY) return kZeroRowExp;  // a chunk that saw no key
+    return __float_as_int(ml.z) + (int)floorf(fmaxf(ml.x - Mr, -300.0f));
+}
+__device__ __forceinline__ void merge_add(float4 ml, float4 acc, float Mr, int EM, float4 &A,
+                                          float &L) {
+    if (ml.x == -INFINITY) return;
+    const float d = fmaxf(ml.x - Mr, -300.0f);
+    const float fl = floorf(d);
+    const float wf = eb::fast_exp2(d - fl);
+    const int sh = __float_as_int(ml.z) + (int)fl - EM;
+    L += eb::fast_exp2(d) * ml.y;
+    A.x += ldexpf(acc.x * wf, sh);
+    A.y += ldexpf(acc.y * wf, sh);
+    A.z += ldexpf(acc.z * wf, sh);
+    A.w += ldexpf(acc.w * wf, sh);
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(
     const float *__restrict__ part_acc, const float *__restrict__ part_ml, float *__restrict__ o,
@@ -1252,27 +1278,17 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(
             acc[j] = *reinterpret_cast<const float4 *>(part_acc + at * HD + d);
         }
         float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j) M = fmaxf(M, ml[j].x);
+        const float Mr = (M == -INFINITY) ? 0.0f : M;
         int EM = kZeroRowExp;
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            M = fmaxf(M, ml[j].x);
-            EM = max(EM, __float_as_int(ml[j].z));
-        }
-        const float Mr = (M == -INFINITY) ? 0.0f : M;
+        for (int j = 0; j < kMergeBatch; ++j) EM = max(EM, merge_exp(ml[j], Mr));
         float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
         float L = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            if (j < nch) {
-                const float w = eb::fast_exp2(ml[j].x - Mr);
-                const int sh = __float_as_int(ml[j].z) - EM;
-                L += w * ml[j].y;
-                A.x += w * ldexpf(acc[j].x, sh);
-                A.y += w * ldexpf(acc[j].y, sh);
-                A.z += w * ldexpf(acc[j].z, sh);
-                A.w += w * ldexpf(acc[j].w, sh);
-            }
-        }
+        for (int j = 0; j < kMergeBatch; ++j)
+            if (j < nch) merge_add(ml[j], acc[j], Mr, EM, A, L);
         const float inv = 1.0f / L;
         *reinterpret_cast<float4 *>(o + at0 * hdr + d) =
             make_float4(ldexpf(A.x * inv, EM), ldexpf(A.y * inv, EM), ldexpf(A.z * inv, EM),
@@ -1280,6 +1296,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(
         return;
     }
     float M = -INFINITY;
+    for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
+#pragma unroll
+        for (int j = 0; j < kMergeBatch; ++j)
+            M = fmaxf(M, part_ml[(at0 + (size_t)min(c0 + j, nch - 1) * cstride) * 4]);
+    }
+    const float Mr = (M == -INFINITY) ? 0.0f : M;
     int EM = kZeroRowExp;
     for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
         float4 ml[kMergeBatch];
@@ -1288,12 +1310,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(
             ml[j] = *reinterpret_cast<const float4 *>(
                 part_ml + (at0 + (size_t)min(c0 + j, nch - 1) * cstride) * 4);
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            M = fmaxf(M, ml[j].x);
-            EM = max(EM, __float_as_int(ml[j].z));
-        }
+        for (int j = 0; j < kMergeBatch; ++j) EM = max(EM, merge_exp(ml[j], Mr));
     }
-    const float Mr = (M == -INFINITY) ? 0.0f : M;
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
     float L = 0.0f;
     for (int c0 = 0; c0 < nch; c0 += kMergeBatch) {
@@ -1305,17 +1323,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(
             acc[j] = *reinterpret_cast<const float4 *>(part_acc + at * HD + d);
         }
 #pragma unroll
-        for (int j = 0; j < kMergeBatch; ++j) {
-            if (c0 + j < nch) {
-                const float w = eb::fast_exp2(ml[j].x - Mr);
-                const int sh = __float_as_int(ml[j].z) - EM;
-                L += w * ml[j].y;
-                A.x += w * ldexpf(acc[j].x, sh);
-                A.y += w * ldexpf(acc[j].y, sh);
-                A.z += w * ldexpf(acc[j].z, sh);
-                A.w += w * ldexpf(acc[j].w, sh);
-            }
-        }
+        for (int j = 0; j < kMergeBatch; ++j)
+            if (c0 + j < nch) merge_add(ml[j], acc[j], Mr, EM, A, L);
     }
     const float inv = 1.0f / L;
     *reinterpret_cast<float4 *>(o + at0 * hdr + d) =

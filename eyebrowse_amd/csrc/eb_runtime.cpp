@@ -271,6 +271,9 @@ eb_status eb_device_new(int ordinal, eb_device **out) {
             hipSuccess &&
         n > 0)
         d->cu_count = n;
+    // Look up this device's no-allocation scratch now, so that no later call (one under a
+    // graph capture, say) has to; a failure here is reported again by that entry point.
+    (void)eb::noalloc_scratch_of_current_device(nullptr);
     *out = d;
     return eb::ok();
 }
@@ -1600,6 +1603,13 @@ eb_status eb_launch_attn_decode_step_f8(void *stream, const float *q, size_t q_n
     return decode_step_cache_raw(stream, q, q_numel, knew, vnew, new_numel, kc, kc_numel, vc,
                                  vc_numel, o, o_numel, h, hkv, pos, hd, max_seq, scale, window,
                                  workspace, workspace_floats, cu_count, eb::CacheElem::E4M3);
+}
+
+eb_status eb_launch_selftest_lane_ops(void *stream, const float *in, float *out) {
+    EB_TRY(eb::check_ptr(in, "in"));
+    EB_TRY(eb::check_ptr(out, "out"));
+    EB_TRY(eb::launch_lane_ops((hipStream_t)stream, in, out));
+    return eb::ok();
 }
 
 eb_status eb_launch_rmsnorm(void *stream, const float *x, size_t x_numel, const float *weight,

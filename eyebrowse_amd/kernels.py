@@ -339,6 +339,15 @@ def launch_attn_prologue(stream: int, q: int, q_numel: int, k: int, k_numel: int
                                         kc_numel, vcache, vc_numel, max_seq, int(cache_dtype)))
 
 
+LANE_OPS_ROWS = 14  # EB_LANE_OPS_ROWS
+
+
+def launch_selftest_lane_ops(stream: int, inp: int, out: int) -> None:
+    """eb_launch_selftest_lane_ops: one wave's lane-exchange results for a = in[0:64],
+    b = in[64:128], LANE_OPS_ROWS rows of 64 floats (device pointers)."""
+    check(lib().eb_launch_selftest_lane_ops(stream, inp, out))
+
+
 def attn_decode_noalloc_max_floats() -> int:
     """Floats of split partials the no-allocation decode step's static scratch holds."""
     return int(lib().eb_attn_decode_noalloc_max_floats())

@@ -525,6 +525,19 @@ eb_status eb_attention_forward(const eb_attention *attn, eb_recorder *rec, const
                                const eb_rope_tables *rope, eb_kv_cache *kv, size_t layer,
                                size_t rows, size_t base_pos, eb_tensor **out);
 
+/* ---- self-check (no counterpart in the reference) ----------------------------------
+ * One wave applies the lane exchanges that every wave reduction in the kernels is built
+ * from (16- and 32-lane swaps, DPP row rotations and mirrors) to in[0..64) = a and
+ * in[64..128) = b, writing EB_LANE_OPS_ROWS rows of 64 floats to out (device memory):
+ * a from lane l ^ 16; a from lane l ^ 32; sums of a over the lanes sharing lane bits
+ * [0, log2 F) for F = 1, 2, 4, 8, 16, 32; maxima of a for F = 1, 8; a + b over lanes
+ * l, l ^ 32 with lanes 0-31 holding the sum of a and 32-63 that of b; the same over l,
+ * l ^ 16 (even 16-lane rows a, odd rows b); sums of a over aligned groups of 4 and of 16
+ * lanes. For callers (and tests) that want a compiler change in these exchanges to show
+ * directly rather than through attention outputs. */
+#define EB_LANE_OPS_ROWS 14
+eb_status eb_launch_selftest_lane_ops(void *stream, const float *in, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,31 @@ def test_chunk_matches_oracle(dev, h, hkv, hd, pos0, rows, window):
                                    rtol=0, atol=1e-6)
 
 
+def test_key_chunk_merge_with_v_magnitudes_far_apart(dev):
+    """128 rows over 8K cached keys run as key chunks merged by log-sum-exp. The first
+    half of the keys score about +100 with V rows near 2^-100; the second half about -100
+    with V rows near 2^+100. The second half's weight (about 2^-288) makes its terms
+    vanish although its V rows are 2^200 larger, so the merge must take its reference
+    exponent from the weighted terms: taken from the V rows alone it would push the first
+    half's partials below f32 range and return zeros."""
+    h, hkv, hd, max_seq, rows = 16, 8, 128, 8192, 128
+    pos0 = max_seq - rows
+    note(f"chunk merge, V 2^-100 / 2^+100 halves, rows={rows} over {max_seq} keys")
+    sc = float(oracle.default_scale(hd))
+    u = oracle.randn((hd,), 61).astype(np.float64)
+    a = 100.0 / (sc * float(u @ u))
+    half = max_seq // 2
+    sign = np.where(np.arange(max_seq) < half, 1.0, -1.0)[:, None, None]
+    kc = (sign * a * u[None, None, :] + 0.3 * oracle.randn((max_seq, hkv, hd), 62)).astype(np.float32)
+    vmag = np.where(np.arange(max_seq) < half, 2.0 ** -100, 2.0 ** 100)[:, None, None]
+    vc = (vmag * oracle.randn((max_seq, hkv, hd), 63)).astype(np.float32)
+    q = (u[None, None, :] + 0.01 * oracle.randn((rows, h, hd), 64)).astype(np.float32)
+    got = chunk(dev, q, kc, vc, h, hkv, pos0, rows, hd, max_seq, sc)
+    want = oracle.attn_chunk(q, kc, vc, h, hkv, pos0, rows, hd, sc, 0, threads=16)
+    assert np.abs(want).max() > 2.0 ** -110, "the first half's V rows must carry the output"
+    assert_close(got, want, what="chunk merge, far-apart V magnitudes")
+
+
 def test_chunk_from_zero_is_prefill_bitwise(dev):
     """With pos0 = 0 and no window the chunk kernel is the prefill kernel over the cache."""
     note("chunk pos0=0 vs prefill")

@@ -15,6 +15,7 @@ import pytest
 import eyebrowse_amd as eb
 import oracle
 from tests._gpu import assert_bitwise, note, upload
+from tests.test_oracle import signed_zero_cases
 
 pytestmark = pytest.mark.gpu
 
@@ -49,6 +50,21 @@ def test_argmax_ties_and_specials(dev):
               np.array([-3.1e38, -3.3e38, np.nan], np.float32), np.array([7.0], np.float32),
               np.zeros(0, np.float32), np.array([-np.inf, np.inf, 1.0], np.float32)):
         assert gpu_argmax(dev, x) == oracle.argmax(x), x
+
+
+def test_argmax_signed_zero_ties(dev):
+    """-0.0 and +0.0 tie under the reference's strict `>` (sampling.rs:21,29): lane order
+    decides. Pairs, a short all-nonpositive vector, and vocabularies of one slice (the
+    one-launch path) and of several (two passes) with the zeros of both signs spread over
+    lanes and slices."""
+    note("argmax signed-zero ties")
+    assert gpu_argmax(dev, np.array([-0.0, 0.0], np.float32)) == 0
+    assert gpu_argmax(dev, np.array([0.0, -0.0], np.float32)) == 0
+    for case in signed_zero_cases():
+        assert gpu_argmax(dev, case) == oracle.argmax(case), case.size
+    raw = np.full(10000, -2.0, np.float32)
+    raw[4099], raw[5000], raw[9998] = -0.0, 0.0, -0.0  # winners in different slices
+    assert gpu_argmax(dev, raw) == oracle.argmax(raw)
 
 
 @pytest.mark.parametrize("vocab,seed", [(151936, 1), (262144, 2), (1001, 3), (4099, 4),

@@ -288,6 +288,87 @@ def test_prng_range_and_moments():
     np.testing.assert_array_equal(oracle.prng(16, 7), oracle.prng(32, 7)[:16])
 
 
+def _gf2_shift(k):
+    """64x64 GF(2) matrix of s -> s << k (k > 0) or s >> -k (k < 0) on the bit vector
+    (bit i of s = entry i), in uint64 arithmetic (bits shifted out are dropped)."""
+    m = np.zeros((64, 64), np.int64)
+    for i in range(64):
+        j = i - k
+        if 0 <= j < 64:
+            m[i, j] = 1
+    return m
+
+
+def _gf2_mul(a, b):
+    return (a @ b) % 2
+
+
+def _gf2_pow(m, n):
+    r = np.eye(64, dtype=np.int64)
+    while n:
+        if n & 1:
+            r = _gf2_mul(r, m)
+        m = _gf2_mul(m, m)
+        n >>= 1
+    return r
+
+
+def _xorshift_matrix():
+    """One step of the reference's generator (crates/eyebrowse-nn/src/testutil.rs:34-37:
+    s ^= s << 13; s ^= s >> 7; s ^= s << 17) as a linear map over GF(2)^64."""
+    eye = np.eye(64, dtype=np.int64)
+    step = eye
+    for k in (13, -7, 17):
+        step = _gf2_mul((eye + _gf2_shift(k)) % 2, step)
+    return step
+
+
+def _bits(s):
+    return np.array([(s >> i) & 1 for i in range(64)], np.int64)
+
+
+def _from_bits(v):
+    return sum(int(b) << i for i, b in enumerate(v))
+
+
+def test_prng_against_gf2_jump_ahead():
+    """ebo_prng pinned without iterating its shifts: the state after n steps is M^n s0 for
+    the GF(2) matrix M of one xorshift step (matrix powers by repeated squaring), with
+    s0 = seed + floor(2^64 / golden ratio) mod 2^64 (the constant derived here from an
+    integer square root, not copied), and each output the top 53 bits of the state as a
+    double u in [0, 1), then f32(2u - 1). The triple (13, 7, 17) in this order is a
+    full-period xorshift: M^(2^64 - 1) = I and M^((2^64 - 1) / p) != I for every prime p of
+    2^64 - 1, which a wrong shift or direction would almost surely break."""
+    from math import isqrt
+    golden = (isqrt(5 << 128) - (1 << 64)) // 2  # floor(2^64 (sqrt 5 - 1) / 2)
+    assert golden == 0x9E3779B97F4A7C15
+    m = _xorshift_matrix()
+    order = (1 << 64) - 1
+    assert np.array_equal(_gf2_pow(m, order), np.eye(64, dtype=np.int64))
+    for p in (3, 5, 17, 257, 641, 65537, 6700417):
+        assert order % p == 0
+        assert not np.array_equal(_gf2_pow(m, order // p), np.eye(64, dtype=np.int64)), p
+
+    def expect(seed, n):  # output n (1-based step count n)
+        s = _from_bits(_gf2_pow(m, n) @ _bits((seed + golden) % (1 << 64)) % 2)
+        u = np.float64(s >> 11) / np.float64(1 << 53)
+        return np.float32(u * 2.0 - 1.0)
+
+    for seed in (0, 1, 7, 2 ** 64 - 1, 0x61C8864680B583EB):
+        got = oracle.prng(9, seed)
+        for i in range(9):
+            assert got[i].view(np.uint32) == expect(seed, i + 1).view(np.uint32), (seed, i)
+    far = oracle.prng(100001, 3)
+    assert far[-1].view(np.uint32) == expect(3, 100001).view(np.uint32)
+    # ebo_randn draws its uniforms from the same stream, two per normal (1 - u1, u2):
+    z = oracle.randn((3,), 5)
+    for i in range(3):
+        u = [np.float64(_from_bits(_gf2_pow(m, 2 * i + t) @ _bits((5 + golden) % (1 << 64)) % 2)
+                        >> 11) / np.float64(1 << 53) for t in (1, 2)]
+        want = np.float32(np.sqrt(-2.0 * np.log(1.0 - u[0])) * np.cos(2.0 * np.pi * u[1]))
+        assert abs(int(z[i].view(np.int32)) - int(want.view(np.int32))) <= 1, i
+
+
 def test_randn_is_standard_normal():
     scipy_stats = pytest.importorskip("scipy.stats")
     z = oracle.randn((1 << 18,), 3).astype(np.float64)
@@ -557,6 +638,24 @@ def _argmax_rule(x):
     return int(min(idx, key=lambda i: (_bitrev8(i % 256), i)))
 
 
+def signed_zero_cases():
+    """Vectors whose maximum is zero held with both signs: two-element pairs, a short
+    all-nonpositive vector, and vocabularies of one and of several 4096-entry slices with
+    the zeros of both signs spread over lanes and slices."""
+    out = [np.array([-0.0, 0.0], np.float32), np.array([0.0, -0.0], np.float32)]
+    z = np.full(8, -1.0, np.float32)
+    z[1], z[2] = 0.0, -0.0
+    out.append(z)
+    for n, seed in ((4096, 1), (151936, 2), (9001, 3)):
+        v = -np.abs(oracle.randn((n,), 300 + seed)) - np.float32(0.5)
+        rng = np.random.default_rng(seed)
+        pos = rng.choice(n, 40, replace=False)
+        v[pos[:20]] = 0.0
+        v[pos[20:]] = -0.0
+        out.append(v.astype(np.float32))
+    return out
+
+
 def test_argmax_reference_case_and_ties():
     """sampling.rs:62-80 (vocab 1000, sin ramp, unique max at 731); ties across lanes go
     by the tree (index 256, lane 0, beats index 1; lane 116 beats lane 44); NaN and -inf
@@ -574,6 +673,17 @@ def test_argmax_reference_case_and_ties():
     assert oracle.argmax(np.array([np.nan, 2, np.nan, 1], np.float32)) == 1
     assert oracle.argmax(np.full(5, -np.inf, np.float32)) == 0
     assert oracle.argmax(np.array([-3.1e38, -3.3e38], np.float32)) == 0
+    # -0.0 and +0.0 tie under the strict `>`: lane order decides, never the sign bit
+    # (lane 2 precedes lane 1 in bit-reversed order, whichever holds -0.0).
+    for case in signed_zero_cases():
+        assert oracle.argmax(case) == _argmax_rule(case), case[:8]
+    assert oracle.argmax(np.array([-0.0, 0.0], np.float32)) == 0
+    assert oracle.argmax(np.array([0.0, -0.0], np.float32)) == 0
+    z = np.full(8, -1.0, np.float32)
+    z[1], z[2] = 0.0, -0.0
+    assert oracle.argmax(z) == 2
+    z[1], z[2] = -0.0, 0.0
+    assert oracle.argmax(z) == 2
     for seed in range(20):
         r = oracle.randn((3000,), seed)
         r = np.round(r * 2) / 2  # many ties

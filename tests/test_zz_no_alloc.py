@@ -17,6 +17,58 @@ from tests._gpu import assert_bitwise, assert_close, note, upload
 pytestmark = pytest.mark.gpu
 
 
+def test_noalloc_decode_step_under_graph_capture(dev):
+    """Graph capture is what the entry point is for: the no-allocation step captured into a
+    HIP graph (first in this file, so that in a fresh process the capture holds the first
+    decode launch) and replayed; every replay, with eager work and an eager no-allocation
+    call of another shape between replays (which overwrites the scratch), must give the
+    workspace entry point's output and cache row bit for bit."""
+    H, Hkv, hd, max_seq, pos, seed = 16, 8, 128, 4096, 1500, 31
+    scale = float(oracle.default_scale(hd))
+    note(f"no-alloc decode step under capture H={H} Hkv={Hkv} hd={hd} pos={pos}")
+    q = oracle.randn((H, hd), seed)
+    kn = oracle.randn((1, Hkv, hd), seed + 1)
+    vn = oracle.randn((1, Hkv, hd), seed + 2)
+    fill_k = oracle.randn((max_seq, Hkv, hd), seed + 3)
+    fill_v = oracle.randn((max_seq, Hkv, hd), seed + 4)
+    qt, knt, vnt = upload(dev, q), upload(dev, kn), upload(dev, vn)
+    kc_a, vc_a = upload(dev, fill_k), upload(dev, fill_v)
+    kc_b, vc_b = upload(dev, fill_k), upload(dev, fill_v)
+    o_a = eb.Tensor.empty(dev, (H, hd))
+    o_b = eb.Tensor.empty(dev, (H, hd))
+    cus = dev.cu_count
+    args_b = (qt.data_ptr, qt.numel(), knt.data_ptr, vnt.data_ptr, knt.numel(), kc_b.data_ptr,
+              kc_b.numel(), vc_b.data_ptr, vc_b.numel(), o_b.data_ptr, o_b.numel(), H, Hkv, pos,
+              hd, max_seq, scale, cus)
+    dev.begin_capture()
+    try:
+        eb.launch_attn_decode_step_noalloc(dev.stream, *args_b)
+    finally:
+        graph = dev.end_capture()
+    need = eb.attn_decode_workspace_floats(H, Hkv, pos, hd, cus)
+    ws = eb.Tensor.empty(dev, (max(need, 1),))
+    eb.launch_attn_decode_step(dev.stream, qt.data_ptr, qt.numel(), knt.data_ptr, vnt.data_ptr,
+                               knt.numel(), kc_a.data_ptr, kc_a.numel(), vc_a.data_ptr,
+                               vc_a.numel(), o_a.data_ptr, o_a.numel(), H, Hkv, pos, hd, max_seq,
+                               scale, ws.data_ptr, need, cus)
+    dev.synchronize()
+    want_o = o_a.to_f32()
+    n = (pos + 1) * Hkv * hd
+    want_k, want_v = kc_a.to_f32()[:n], vc_a.to_f32()[:n]
+    for rep in range(3):
+        graph.launch()
+        dev.synchronize()
+        assert_bitwise(o_b.to_f32(), want_o, f"replay {rep}: output")
+        assert_bitwise(kc_b.to_f32()[:n], want_k, f"replay {rep}: K cache rows 0..=pos")
+        assert_bitwise(vc_b.to_f32()[:n], want_v, f"replay {rep}: V cache rows 0..=pos")
+        _step_both(dev, 32, 8, 128, 8192, 5000 + 1000 * rep, scale, 40 + rep)
+    graph.release()
+    kc_w = oracle.kv_write(fill_k, kn, Hkv, 1, hd, pos)
+    vc_w = oracle.kv_write(fill_v, vn, Hkv, 1, hd, pos)
+    want = oracle.attn_decode(q, kc_w, vc_w, H, Hkv, pos, hd, max_seq, scale, threads=16)
+    assert_close(want_o.reshape(H, hd), want.reshape(H, hd), what="captured no-alloc vs oracle")
+
+
 def _step_both(dev, H, Hkv, hd, max_seq, pos, scale, seed):
     """One decode step at `pos` through both entry points on two copies of the same
     caches; returns the workspace size the shape needs (floats)."""
