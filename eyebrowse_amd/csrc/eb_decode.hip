@@ -97,7 +97,7 @@ struct DecodeShape {
     static constexpr int WS = G * HD + 4;
     static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)kWaves * WS + 2 * G * kWaves);
     static_assert(DPL % 4 == 0 && HD % DPL == 0 && LPK <= 16,
-                  "head_dim: 4, 8, or a multiple of 16 up to 256");
+                  "head_dim: 4, a multiple of 8 up to 128, or a multiple of 16 up to 256");
 };
 
 // Bytes per load over a cache of EB-byte elements: 16 (4 f32 or 8 f16 dims), 8 for E4M3
@@ -273,11 +273,13 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
 // 4: 5.26 TB/s). 2 heads per workgroup (Qwen) measured slower at 8 dims per lane with
 // the default cache policy and faster with the non-temporal loads (L=8191 4.43 -> 4.52
 // TB/s, 2048 keys +1 %), so head_dim 128 f32 runs 8 dims per lane from 2 heads up.
+// Head dims that are odd multiples of 8 (24, 40, ..., 120) run 8 dims per lane for every
+// cache type: a row over hd / 8 lanes, padded to a power-of-two group.
 template <int HD, int G, int EB>
 using DecodeShapeOf = DecodeShape<HD, G,
                                   EB == 2 ? EB_DECODE_U16 : EB == 1 ? EB_DECODE_U8
                                                                     : (HD == 256 ? 2 : 1),
-                                  (EB == 4 && HD == 128 && G >= 2) ? 8 : 16>;
+                                  ((EB == 4 && HD == 128 && G >= 2) || HD % 16 == 8) ? 8 : 16>;
 
 // EB: bytes per cache element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
 // as loaded. A narrow lane's loads hold 8 dims each (16 bytes of halves, 8 of E4M3), in the
@@ -1504,6 +1506,10 @@ eb_status launch_attn_decode_any(hipStream_t st, const float *q, const void *kc,
                             "attn_decode: norm gains and RoPE tables must be 16-byte aligned");
         if ((pro->rope_cos == nullptr) != (pro->rope_sin == nullptr))
             return fail(EB_OTHER, "attn_decode: RoPE needs both tables");
+        if (pro->rope_cos && !decode_fuses_rope(hd, ce))
+            return fail(EB_UNSUPPORTED_CONFIG,
+                        "attn_decode: RoPE cannot be fused into the step at head_dim %zu over "
+                        "a narrow cache (apply it with the pre-attention pass)", hd);
     }
     if (!attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: head_dim %zu", hd);

@@ -33,13 +33,13 @@ eb_status check_launch(const char *kernel);
 eb_status check_ptr(const void *p, const char *name);
 eb_status check_numel(size_t have, size_t need, const char *name);
 eb_status check_heads(size_t h, size_t hkv);
-// Head dims the attention kernels serve: 4, 8 and every multiple of 16 up to 256. Decode is
-// instantiated for each (X-macro below); prefill runs the next power-of-two instantiation
-// with the extra dims read as zeros and never stored.
+// Head dims the attention kernels serve: 4, every multiple of 8 up to 128 and every multiple
+// of 16 up to 256. Decode is instantiated for each (X-macro below); prefill runs the next
+// power-of-two instantiation with the extra dims read as zeros and never stored.
 bool attn_head_dim_supported(size_t hd);
 #define EB_HEAD_DIMS(X) \
-    X(4) X(8) X(16) X(32) X(48) X(64) X(80) X(96) X(112) X(128) X(144) X(160) X(176) X(192) \
-    X(208) X(224) X(240) X(256)
+    X(4) X(8) X(16) X(24) X(32) X(40) X(48) X(56) X(64) X(72) X(80) X(88) X(96) X(104) \
+    X(112) X(120) X(128) X(144) X(160) X(176) X(192) X(208) X(224) X(240) X(256)
 // Largest element count a 32-bit-indexed kernel may address.
 constexpr size_t kMaxIndex = (size_t)1 << 31;
 
@@ -53,6 +53,12 @@ int current_cu_count();
 // reference's; F16 is IEEE half and E4M3 OCP FP8 E4M3 (both rounded to nearest even by
 // kv_write, E4M3 saturating at +-448), converted to f32 as attention loads them.
 enum class CacheElem : int { F32 = 4, F16 = 2, E4M3 = 1 };
+// Whether the fused decode step can apply RoPE inside its lane layout: over IEEE-half and
+// E4M3 caches a lane's 8-dim loads sit at multiples of 8 dims, and at head dims that are odd
+// multiples of 8 a dim's RoPE partner (dim + hd/2) is not on the same lane.
+inline bool decode_fuses_rope(size_t hd, CacheElem ce) {
+    return ce == CacheElem::F32 || hd % 16 == 0;
+}
 
 // ---- kernel launchers (validated arguments, caller's stream) -------------------------
 eb_status launch_kv_write(hipStream_t st, float *cache, const float *src, size_t hkv,

@@ -240,6 +240,28 @@ extern "C" eb_status eb_attention_forward_qkv(const eb_attention *attn, eb_recor
         eb_tensor_numel(v) != rows * Hkv * hd)
         return fail(EB_SHAPE_MISMATCH, "attention_forward: q/k/v are not [rows, heads*head_dim]");
 
+    const eb::CacheElem ce = eb_tensor_dtype(kc) == EB_F16    ? eb::CacheElem::F16
+                             : eb_tensor_dtype(kc) == EB_F8E4M3 ? eb::CacheElem::E4M3
+                                                                : eb::CacheElem::F32;
+    if (rows == 1 && !eb::decode_fuses_rope(hd, ce)) {
+        // The step's lane layout cannot rotate this head dim over a narrow cache: the
+        // pre-attention pass (norms, RoPE, cache write of row base_pos), then attn_decode.
+        const size_t qshape1[3] = {1, H, hd};
+        eb_tensor *qr1 = nullptr;
+        EB_TRY(eb_tensor_empty(tensor_device_of(q), qshape1, 3, EB_F32, &qr1));
+        Owned qr(qr1);
+        EB_TRY(eb::attn_rows_fused(rec, q, k, v, qr.t, kc, vc, 1, H, Hkv, hd, base_pos,
+                                   kv->max_seq, d.q_norm, d.k_norm, d.v_norm, d.norm_eps,
+                                   rope->cos, rope->sin));
+        const size_t oshape1[2] = {1, H * hd};
+        eb_tensor *o1 = nullptr;
+        EB_TRY(eb_tensor_empty(tensor_device_of(q), oshape1, 2, EB_F32, &o1));
+        Owned o(o1);
+        EB_TRY(eb_attn_decode_window(rec, qr.t, kc, vc, o.t, H, Hkv, base_pos, hd, kv->max_seq,
+                                     d.scale, d.window));
+        *out = o.release();
+        return eb::ok();
+    }
     if (rows == 1) {
         // attention.rs:133-183 after the projections: q/k/v norms, RoPE at pos, kv_write
         // of K and V, attn_decode; all of it inside the fused decode step.

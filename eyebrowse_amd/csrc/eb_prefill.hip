@@ -79,6 +79,12 @@ __device__ __forceinline__ float sub_f16_hi(unsigned h2, float x) {
     return d;
 }
 
+// 1: the f16 mode over pre-converted records runs its software-pipelined loop (0: the
+// plain loop, for comparison).
+#ifndef EB_PREFILL_PIPE
+#define EB_PREFILL_PIPE 0
+#endif
+
 constexpr int kTile = 32;  // keys per tile, queries per wave
 constexpr size_t kLdsBytesPerCu = 160 * 1024;  // gfx950 LDS per CU
 constexpr float kSlack = 8.0f;  // log2 units the reference max may lag a score (SPV)
@@ -456,6 +462,64 @@ __device__ __forceinline__ void fps_store_step(float *smem, const f32x4 (&r)[C::
     }
 }
 
+// Staging of the software-pipelined f16 mode (prefill_kernel, kPipe). Iteration s of its
+// loop reads the K rows of step s + 1 (the next scores) and the V^T rows of step s - 1 (the
+// previous P V products); at its end it stages the K rows of step s + 2 and the V^T rows of
+// step s into buffer s % 2, whose K rows (step s) and V^T rows (step s - 2) were last read
+// in iteration s - 1. Register slot i of a thread holds step-relative chunk
+// c = tid + i * THREADS of the f16-mode records (tile c / (8 HD), chunk c % (8 HD) of it, K
+// rows below 4 HD): K chunks come from step sk's tiles, V^T chunks from step sv's, so
+// fps_store_step puts them where they belong. Tiles past the last record are clamped (a
+// clamped chunk lands in a slot that is never read).
+template <class C>
+__device__ __forceinline__ void fpipe_load_step(const f32x4 *__restrict__ recs,
+                                                f32x4 (&r)[C::FPSN], int sk, int sv, int nt,
+                                                int tid) {
+    constexpr int HD = C::HD_;
+    constexpr int KSPLIT = C::STEP_KEYS / kTile;
+    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::FPS_CH);
+#pragma unroll
+    for (int i = 0; i < C::FPSN; ++i) {
+        const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
+        const int j = c / (8 * HD), w = c % (8 * HD);
+        const int t = min((w < 4 * HD ? sk : sv) * KSPLIT + j, nt - 1);
+        r[i] = chunk_load(rs, t * C::FPS_CH + w, 0);
+    }
+}
+
+// The loop's prologue: the K rows of steps 0 and 1, into buffers 0 and 1. A slot that
+// holds a V^T chunk w of the step layout carries K chunk w - 4 HD of step 1 instead.
+template <class C>
+__device__ __forceinline__ void fpipe_load_first(const f32x4 *__restrict__ recs,
+                                                 f32x4 (&r)[C::FPSN], int nt, int tid) {
+    constexpr int HD = C::HD_;
+    constexpr int KSPLIT = C::STEP_KEYS / kTile;
+    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::FPS_CH);
+#pragma unroll
+    for (int i = 0; i < C::FPSN; ++i) {
+        const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
+        const int j = c / (8 * HD), w = c % (8 * HD);
+        const bool k1 = w >= 4 * HD;
+        const int t = min((k1 ? KSPLIT : 0) + j, nt - 1);
+        r[i] = chunk_load(rs, t * C::FPS_CH + (k1 ? w - 4 * HD : w), 0);
+    }
+}
+template <class C>
+__device__ __forceinline__ void fpipe_store_first(float *smem, const f32x4 (&r)[C::FPSN],
+                                                  int tid) {
+    constexpr int HD = C::HD_;
+#pragma unroll
+    for (int i = 0; i < C::FPSN; ++i) {
+        const int c = tid + i * C::THREADS;
+        if (C::FPS_KV % C::THREADS == 0 || c < C::FPS_KV) {
+            const int j = c / (8 * HD), w = c % (8 * HD);
+            const bool k1 = w >= 4 * HD;
+            *reinterpret_cast<f32x4 *>(smem + (k1 ? C::BUF : 0) +
+                                       fps_lds_offset<C>(j, k1 ? w - 4 * HD : w)) = r[i];
+        }
+    }
+}
+
 // The pre-split and pre-convert passes' shape: one 32-key tile per workgroup (the records'
 // layout), 512 threads at head_dim >= 128 (more of the tile's loads and stores in flight
 // per CU: the LDS allows two such workgroups per CU at 256, four at 128; measured 1-2 %
@@ -638,8 +702,13 @@ __global__ __attribute__((
     f32x4 rs[PS ? (FAST ? C::FPSN : C::PSN) : 1];
     const float *recs =
         PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
+    // The f16 mode over pre-converted records on prompts runs the software-pipelined loop
+    // (see the loop below); its staging is one step further ahead for K.
+    constexpr bool kPipe = FAST && PS && !RANGE && EB_PREFILL_PIPE;
     auto load_first_step = [&] {
-        if constexpr (PS && FAST)
+        if constexpr (kPipe)
+            fpipe_load_first<C>(reinterpret_cast<const f32x4 *>(recs), rs, ps_nt, tid);
+        else if constexpr (PS && FAST)
             fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
         else if constexpr (PS && C::PS_IMAGE)
             ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
@@ -664,13 +733,25 @@ __global__ __attribute__((
         // Every lane loads (rows past the end from the clamped row 0) and scales by qs, 0
         // past the end, so that the loads issue back to back; such a lane's query column
         // never reaches the output. Dims past hdr (a head dim padded up to this
-        // instantiation) are zeros.
+        // instantiation) are zeros. A head dim that is an odd multiple of 8 ends halfway
+        // into its last 16-dim step: there the upper half-wave (dims +8..+15) reads the
+        // lower half's address (inside the row) and keeps zeros.
 #pragma unroll
         for (int k2 = 0; k2 < NKS; ++k2) {
-            const bool in = 16 * k2 < hdr;  // (uniform)
             const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-            qa[k2] = in ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2) : z;
-            qb[k2] = in ? *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4) : z;
+            if (16 * k2 + 16 <= hdr) {  // (uniform)
+                qa[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2);
+                qb[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4);
+            } else if (16 * k2 < hdr) {  // (uniform) hdr = 16 k2 + 8
+                const float *qe = qp + 16 * k2 - 8 * hf;
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(qe);
+                const f32x4 b = *reinterpret_cast<const f32x4 *>(qe + 4);
+                qa[k2] = hf ? z : a;
+                qb[k2] = hf ? z : b;
+            } else {
+                qa[k2] = z;
+                qb[k2] = z;
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         load_first_step();
@@ -739,7 +820,9 @@ __global__ __attribute__((
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     // ... and the first step's K/V into LDS.
-    if constexpr (PS && FAST)
+    if constexpr (kPipe)
+        fpipe_store_first<C>(smem, rs, tid);
+    else if constexpr (PS && FAST)
         fps_store_step<C>(smem, rs, 0, tid);
     else if constexpr (PS && C::PS_IMAGE)
         wait_vm_all();
@@ -943,6 +1026,51 @@ __global__ __attribute__((
             }
         };
 
+        // The f16 mode's softmax for the pipelined loop: as tile_softmax, except that the
+        // rescale of O^T by corr is left to the caller (after the previous step's products);
+        // masked: the per-key causal mask (a wave's last tile, the one holding its diagonal).
+        auto tile_softmax_pipe = [&](int kb, const floatx16 &sc, f16x8 (&php)[2], float &corr,
+                                     bool &grew, bool masked) {
+            float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = sc[r];
+            if (masked) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (key > pi) p[r] = -INFINITY;
+                }
+            }
+            float mt = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const bool grow = mt > m + kSlack;
+            const float mnew = grow ? fmaxf(m, mt) : m;
+            const float mref = mnew == -INFINITY ? 0.0f : mnew;
+            corr = grow ? eb::fast_exp2(m - mref) : 1.0f;
+            float ps = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                p[r] = eb::fast_exp2(p[r] - mref);
+                ps += p[r];
+            }
+            l = l * corr + ps;
+            m = mnew;
+            grew = grow;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                unsigned hw[4];
+#pragma unroll
+                for (int c2 = 0; c2 < 4; ++c2) {
+                    const int r = 8 * u + 2 * c2;
+                    hw[c2] = __builtin_bit_cast(
+                        unsigned, __builtin_convertvector(f32x2{p[r], p[r + 1]}, f16x2));
+                }
+                php[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+            }
+        };
+
         // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the output stage
         // expects), stored at V^T row 32*mb + col; keys 16u + 4hf + 0..3 and 16u + 8 + 4hf +
         // 0..3 of this wave's tile (the order of ph / pl). FAST: the hi halves only.
@@ -984,6 +1112,54 @@ __global__ __attribute__((
         floatx16 sacc;
         int ek[16];
         f16x8 ph[2], pl[2];
+        if constexpr (kPipe) {
+            // Software-pipelined f16 mode (prompts from position 0, one chunk per block, so
+            // c_lo = 0 and this wave's tiles are ks, ks + KSPLIT, ... up to my_t1). Within
+            // iteration s the matrix cores take the P V products of step s - 1 and the
+            // scores of step s + 1 while the VALU runs step s's softmax: neither product
+            // depends on that softmax, so one wave keeps the matrix pipe fed instead of
+            // alternating products and softmax. O^T gets the products of s - 1, then the
+            // rescale of step s, then (next iteration) the products of s: the order the
+            // unpipelined loop applies them in, so the two give the same bits.
+            const int s_last = (live && my_t1 >= ks) ? (my_t1 - ks) / KSPLIT : -1;
+            floatx16 sn;
+            f16x8 pp[2];
+            float corr = 1.0f;
+            bool grew = false;
+            if (s_last >= 0) tile_qk(0, sacc, ek);
+            for (int it = 0; it < nsteps; ++it) {
+                const int buf = it & 1;
+                fpipe_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, it + 2, it, ps_nt,
+                                   tid);
+                if (it < s_last) {
+                    // Steady state (no mask: only a wave's last tile holds its diagonal).
+                    if (it > 0) tile_pv(buf ^ 1, pp, pp);
+                    tile_softmax_pipe(it * KSPLIT * kTile + ks * kTile, sacc, ph, corr, grew,
+                                      false);
+                    tile_qk(buf ^ 1, sn, ek);
+                    sacc = sn;
+                } else if (it == s_last) {
+                    if (it > 0) tile_pv(buf ^ 1, pp, pp);
+                    tile_softmax_pipe(it * KSPLIT * kTile + ks * kTile, sacc, ph, corr, grew,
+                                      true);
+                } else if (it == s_last + 1) {
+                    tile_pv(buf ^ 1, pp, pp);
+                }
+                // O^T follows step it's softmax correction once the products of step it - 1
+                // are in (the wave skips it when no lane's reference max moved).
+                if (it <= s_last && __builtin_amdgcn_ballot_w64(grew) != 0) {
+#pragma unroll
+                    for (int mb = 0; mb < NB; ++mb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) oacc[mb][r] *= corr;
+                }
+                pp[0] = ph[0];
+                pp[1] = ph[1];
+                fps_store_step<C>(smem, rs, buf, tid);
+                __syncthreads();
+            }
+            if (s_last == nsteps - 1) tile_pv(nsteps & 1 ? 0 : 1, pp, pp);
+        } else
         for (int it = 0; it < nsteps; ++it) {
             const int buf = it & 1;
             const int tile = c_lo + it * KSPLIT + ks;
@@ -1698,7 +1874,7 @@ eb_status launch_attn_prefill_fast(hipStream_t st, const float *q, const float *
         case 256: return launch_prefill_fast_hd<256>(st, q, k, v, o, (int)h, (int)hkv, r, sl2);
         default:
             return eb::fail(EB_UNSUPPORTED_CONFIG,
-                            "attn_prefill_fast: head_dim %zu (32 to 256, multiples of 16)", hd);
+                            "attn_prefill_fast: head_dim %zu (24 to 256)", hd);
     }
 }
 

@@ -99,7 +99,7 @@ eb_status check_heads(size_t h, size_t hkv) {
 }
 
 bool attn_head_dim_supported(size_t hd) {
-    return hd == 4 || hd == 8 || (hd % 16 == 0 && hd >= 16 && hd <= 256);
+    return hd == 4 || (hd % 8 == 0 && hd >= 8 && hd <= 128) || (hd % 16 == 0 && hd <= 256);
 }
 
 int current_cu_count() {
@@ -725,7 +725,7 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_prefill: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)", hd);
+                    "attn_prefill: head_dim %zu (supported: 4, multiples of 8 up to 128, multiples of 16 up to 256)", hd);
     EB_TRY(eb::check_numel(qn, {s, h, hd}, "q"));
     EB_TRY(eb::check_numel(kn, {s, hkv, hd}, "k"));
     EB_TRY(eb::check_numel(vn, {s, hkv, hd}, "v"));
@@ -750,9 +750,10 @@ static eb_status prefill_fast_checked(hipStream_t st, const float *q, size_t qn,
                                       size_t h, size_t hkv, size_t s, size_t hd, float scale,
                                       const PrefillWs &wsrc = PrefillWs()) {
     EB_TRY(eb::check_heads(h, hkv));
-    if (hd < 32 || hd > 256 || hd % 16 != 0)
+    if (hd < 24 || !eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_prefill_fast: head_dim %zu (multiples of 16 from 32 to 256)", hd);
+                    "attn_prefill_fast: head_dim %zu (multiples of 8 from 24 to 128, of 16 "
+                    "to 256)", hd);
     if (!(std::fabs(scale) * std::sqrt((double)hd) <= 1.0001))
         return fail(EB_UNSUPPORTED_CONFIG,
                     "attn_prefill_fast: scale %g above 1/sqrt(head_dim): the f16 rounding of "
@@ -796,7 +797,7 @@ static eb_status prefill_chunk_checked(hipStream_t st, const float *q, size_t qn
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_prefill_chunk: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)",
+                    "attn_prefill_chunk: head_dim %zu (supported: 4, multiples of 8 up to 128, multiples of 16 up to 256)",
                     hd);
     if (ce != eb::CacheElem::F32 && hd < 8)
         return fail(EB_UNSUPPORTED_CONFIG,
@@ -835,7 +836,7 @@ static eb_status decode_shape_checked(const float *q, size_t qn, const void *kc,
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_decode: head_dim %zu (supported: 4, 8 and multiples of 16 up to 256)", hd);
+                    "attn_decode: head_dim %zu (supported: 4, multiples of 8 up to 128, multiples of 16 up to 256)", hd);
     if (ce != eb::CacheElem::F32 && hd < 8)
         return fail(EB_UNSUPPORTED_CONFIG, "attn_decode: f16 and e4m3 caches need head_dim >= 8");
     if (pos >= max_seq)

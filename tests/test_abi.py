@@ -96,8 +96,8 @@ def test_prefill_validation():
                    None, 1 << 20, 6, 4, 5, 8, 0.3)
     assert st == 4 and "multiple" in msg          # h % hkv != 0
     st, msg = _err(l.eb_launch_attn_prefill, None, None, 1 << 20, None, 1 << 20, None, 1 << 20,
-                   None, 1 << 20, 4, 2, 5, 40, 0.3)
-    assert st == 3 and "head_dim" in msg          # unsupported head_dim (not 4, 8, 16k)
+                   None, 1 << 20, 4, 2, 5, 136, 0.3)
+    assert st == 3 and "head_dim" in msg          # unsupported head_dim (not 4, 8k <= 128, 16k)
     st, msg = _err(l.eb_launch_attn_prefill, None, None, 5 * 4 * 8 - 1, None, 1 << 20, None,
                    1 << 20, None, 1 << 20, 4, 2, 5, 8, 0.3)
     assert st == 4 and "q holds" in msg

@@ -63,10 +63,12 @@ def test_baseline_configs(dev, name, H, Hkv, hd, T):
 
 @pytest.mark.parametrize("h,hkv,s,hd", [
     (16, 8, 1, 128), (16, 8, 33, 128), (32, 8, 100, 128), (8, 8, 97, 64), (24, 8, 70, 128),
-    (16, 8, 77, 256), (4, 2, 50, 32), (8, 2, 130, 80), (6, 3, 90, 192),
+    (16, 8, 77, 256), (4, 2, 50, 32), (8, 2, 130, 80), (6, 3, 90, 192), (8, 2, 130, 40),
+    (4, 2, 50, 24), (16, 8, 700, 120),
 ])
 def test_shapes(dev, h, hkv, s, hd):
-    """GQA ratios 1 to 4, head dims 32 to 256 (80 and 192 padded), ragged lengths."""
+    """GQA ratios 1 to 4, head dims 24 to 256 (24, 40, 80, 120 and 192 padded), ragged
+    lengths."""
     note(f"fast prefill h={h} hkv={hkv} s={s} hd={hd}")
     sc = float(oracle.default_scale(hd))
     q = oracle.randn((s, h, hd), 11)
