@@ -245,9 +245,11 @@ class PrefillWorkload:
     """Causal prefill over T tokens: K/V written by kv_write into a [T, Hkv, hd] cache,
     attention over the fresh K/V."""
 
-    def __init__(self, eb, dev, H, Hkv, hd, T, scale, seed=0, presplit=True, fast=False):
+    def __init__(self, eb, dev, H, Hkv, hd, T, scale, seed=0, presplit=True, fast=False,
+                 pv16=False):
         self.eb, self.dev = eb, dev
         self.fast = fast
+        self.pv16 = pv16  # the scores-accurate mode (same workspace as the accurate one)
         self.H, self.Hkv, self.hd, self.T, self.scale = H, Hkv, hd, T, scale
         self.flops = 2.0 * H * hd * T * (T + 1)
         rng = np.random.default_rng(seed)
@@ -272,6 +274,10 @@ class PrefillWorkload:
             e.launch_attn_prefill_fast_ws(*args, self.ws.data_ptr, self.ws_floats)
         elif self.fast:
             e.launch_attn_prefill_fast(*args)
+        elif self.pv16 and self.ws is not None:
+            e.launch_attn_prefill_pv16_ws(*args, self.ws.data_ptr, self.ws_floats)
+        elif self.pv16:
+            e.launch_attn_prefill_pv16(*args)
         elif self.ws is not None:
             e.launch_attn_prefill_ws(*args, self.ws.data_ptr, self.ws_floats)
         else:

@@ -29,7 +29,8 @@ from .kernels import (argmax, argmax_workspace_floats, attn_decode, attn_decode_
                       launch_attn_decode_step_f8,
                       attn_decode_noalloc_max_floats, launch_linear_f16w, launch_rmsnorm, launch_rope, linear_f16w,
                       linear_f16w_multi, linear_workspace_floats, rmsnorm, rope,
-                      LANE_OPS_ROWS, launch_selftest_lane_ops)
+                      LANE_OPS_ROWS, launch_selftest_lane_ops, attn_prefill_pv16,
+                      launch_attn_prefill_pv16, launch_attn_prefill_pv16_ws)
 from .nn import Attention, KvCache, Linear, Rope
 
 __all__ = [
@@ -49,5 +50,6 @@ __all__ = [
     "linear_workspace_floats", "launch_rmsnorm",
     "launch_rope", "launch_attn_prologue", "launch_attn_decode_step_noalloc",
     "attn_decode_noalloc_max_floats", "rmsnorm", "rope", "Attention", "KvCache", "Linear", "Rope",
-    "LANE_OPS_ROWS", "launch_selftest_lane_ops",
+    "LANE_OPS_ROWS", "launch_selftest_lane_ops", "attn_prefill_pv16", "launch_attn_prefill_pv16",
+    "launch_attn_prefill_pv16_ws",
 ]

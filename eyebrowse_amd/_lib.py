@@ -73,6 +73,13 @@ SIGNATURES = {
                                c_float]),
     "eb_attn_prefill_fast": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size,
                                     c_size, c_float]),
+    "eb_attn_prefill_pv16": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size,
+                                    c_size, c_float]),
+    "eb_launch_attn_prefill_pv16": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
+                                           c_size, c_size, c_size, c_size, c_size, c_float]),
+    "eb_launch_attn_prefill_pv16_ws": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size,
+                                              c_vp, c_size, c_size, c_size, c_size, c_size,
+                                              c_float, c_vp, c_size]),
     "eb_launch_attn_prefill_fast": (c_st, [c_vp, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp,
                                            c_size, c_size, c_size, c_size, c_size, c_float]),
     "eb_attn_prefill_fast_workspace_floats": (c_size, [c_size, c_size, c_size, c_size]),

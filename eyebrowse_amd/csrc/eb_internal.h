@@ -72,6 +72,11 @@ size_t prefill_workspace_floats(size_t h, size_t hkv, size_t hd, size_t rows, si
 eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, const float *v,
                               float *o, size_t h, size_t hkv, size_t s, size_t hd,
                               float scale, float *ws = nullptr, size_t ws_floats = 0);
+// The scores-accurate mode: as launch_attn_prefill, with O^T += V^T P^T as one f16 product
+// (head dims 24..256).
+eb_status launch_attn_prefill_pv16(hipStream_t st, const float *q, const float *k,
+                                   const float *v, float *o, size_t h, size_t hkv, size_t s,
+                                   size_t hd, float scale, float *ws, size_t ws_floats);
 // The single-product f16 prefill (opt-in): q, K, V and P rounded to f16 once, one f16 MFMA
 // per product, f32 softmax and accumulation. Prompts from position 0, f32 q/k/v, head dims
 // 32..256 (multiples of 16); no workspace.

@@ -79,12 +79,6 @@ __device__ __forceinline__ float sub_f16_hi(unsigned h2, float x) {
     return d;
 }
 
-// 1: the f16 mode over pre-converted records runs its software-pipelined loop (0: the
-// plain loop, for comparison).
-#ifndef EB_PREFILL_PIPE
-#define EB_PREFILL_PIPE 0
-#endif
-
 constexpr int kTile = 32;  // keys per tile, queries per wave
 constexpr size_t kLdsBytesPerCu = 160 * 1024;  // gfx950 LDS per CU
 constexpr float kSlack = 8.0f;  // log2 units the reference max may lag a score (SPV)
@@ -239,7 +233,9 @@ __device__ __forceinline__ void split_f16(f32x4 x, int e, f16x4 &hi, f16x4 &lo) 
 // its HD halves of hi, then HD halves of lo (the same KS floats).
 // FAST: rows are rounded to f16 as they are (no exponent, no lo halves, no exponent
 // arrays); the single-product mode below reads only the hi halves.
-template <class C, bool FAST = false>
+// V16 (with FAST false): K split as above, V rows rounded to f16 as they are, as FAST does
+// (the scores-accurate mode; its V^T lo halves and V exponents are not written).
+template <class C, bool FAST = false, bool V16 = false>
 __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk)[C::NLD],
                                                    const f32x4 (&rv)[C::NLD], int buf,
                                                    int tid) {
@@ -274,7 +270,7 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                 const f32x4 y = rv[r];
                 int ev = 0;
                 f16x4 vh, vl;
-                if constexpr (FAST) {
+                if constexpr (FAST || V16) {
                     vh = __builtin_convertvector(y, f16x4);
                     vl = vh;
                 } else {
@@ -299,13 +295,13 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                         const int d = c4 * 4 + i;
                         const int pr = (d % C::NB) * 32 + d / C::NB;
                         vth16[pr * C::VROW + js] = vh[i];
-                        if constexpr (!FAST) vtl16[pr * C::VROW + js] = vl[i];
+                        if constexpr (!FAST && !V16) vtl16[pr * C::VROW + js] = vl[i];
                     }
                 } else {
                 using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
                 const u32x2 ho = __builtin_bit_cast(u32x2, vh), lw = __builtin_bit_cast(u32x2, vl);
                 const u32x2 hp = {lane_xor_u<HD / 4>(ho.x), lane_xor_u<HD / 4>(ho.y)};
-                const u32x2 lp = FAST ? lw : u32x2{lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
+                const u32x2 lp = (FAST || V16) ? lw : u32x2{lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
                 const f16x4 vh2 = __builtin_bit_cast(f16x4, hp), vl2 = __builtin_bit_cast(f16x4, lp);
                 const bool odd = row & 1;
                 // Keys are stored permuted within each 16: groups of four in the order
@@ -324,11 +320,11 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     const _Float16 le = odd ? vl2[i] : vl[i], lo2 = odd ? vl[i] : vl2[i];
                     using h2 = __attribute__((ext_vector_type(2))) _Float16;
                     vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
-                    if constexpr (!FAST)
+                    if constexpr (!FAST && !V16)
                         vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
                 }
                 }
-                if (!FAST && c4 == 0) Ev[row] = ev;
+                if (!FAST && !V16 && c4 == 0) Ev[row] = ev;
             } else {
                 *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
             }
@@ -462,64 +458,6 @@ __device__ __forceinline__ void fps_store_step(float *smem, const f32x4 (&r)[C::
     }
 }
 
-// Staging of the software-pipelined f16 mode (prefill_kernel, kPipe). Iteration s of its
-// loop reads the K rows of step s + 1 (the next scores) and the V^T rows of step s - 1 (the
-// previous P V products); at its end it stages the K rows of step s + 2 and the V^T rows of
-// step s into buffer s % 2, whose K rows (step s) and V^T rows (step s - 2) were last read
-// in iteration s - 1. Register slot i of a thread holds step-relative chunk
-// c = tid + i * THREADS of the f16-mode records (tile c / (8 HD), chunk c % (8 HD) of it, K
-// rows below 4 HD): K chunks come from step sk's tiles, V^T chunks from step sv's, so
-// fps_store_step puts them where they belong. Tiles past the last record are clamped (a
-// clamped chunk lands in a slot that is never read).
-template <class C>
-__device__ __forceinline__ void fpipe_load_step(const f32x4 *__restrict__ recs,
-                                                f32x4 (&r)[C::FPSN], int sk, int sv, int nt,
-                                                int tid) {
-    constexpr int HD = C::HD_;
-    constexpr int KSPLIT = C::STEP_KEYS / kTile;
-    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::FPS_CH);
-#pragma unroll
-    for (int i = 0; i < C::FPSN; ++i) {
-        const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
-        const int j = c / (8 * HD), w = c % (8 * HD);
-        const int t = min((w < 4 * HD ? sk : sv) * KSPLIT + j, nt - 1);
-        r[i] = chunk_load(rs, t * C::FPS_CH + w, 0);
-    }
-}
-
-// The loop's prologue: the K rows of steps 0 and 1, into buffers 0 and 1. A slot that
-// holds a V^T chunk w of the step layout carries K chunk w - 4 HD of step 1 instead.
-template <class C>
-__device__ __forceinline__ void fpipe_load_first(const f32x4 *__restrict__ recs,
-                                                 f32x4 (&r)[C::FPSN], int nt, int tid) {
-    constexpr int HD = C::HD_;
-    constexpr int KSPLIT = C::STEP_KEYS / kTile;
-    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::FPS_CH);
-#pragma unroll
-    for (int i = 0; i < C::FPSN; ++i) {
-        const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
-        const int j = c / (8 * HD), w = c % (8 * HD);
-        const bool k1 = w >= 4 * HD;
-        const int t = min((k1 ? KSPLIT : 0) + j, nt - 1);
-        r[i] = chunk_load(rs, t * C::FPS_CH + (k1 ? w - 4 * HD : w), 0);
-    }
-}
-template <class C>
-__device__ __forceinline__ void fpipe_store_first(float *smem, const f32x4 (&r)[C::FPSN],
-                                                  int tid) {
-    constexpr int HD = C::HD_;
-#pragma unroll
-    for (int i = 0; i < C::FPSN; ++i) {
-        const int c = tid + i * C::THREADS;
-        if (C::FPS_KV % C::THREADS == 0 || c < C::FPS_KV) {
-            const int j = c / (8 * HD), w = c % (8 * HD);
-            const bool k1 = w >= 4 * HD;
-            *reinterpret_cast<f32x4 *>(smem + (k1 ? C::BUF : 0) +
-                                       fps_lds_offset<C>(j, k1 ? w - 4 * HD : w)) = r[i];
-        }
-    }
-}
-
 // The pre-split and pre-convert passes' shape: one 32-key tile per workgroup (the records'
 // layout), 512 threads at head_dim >= 128 (more of the tile's loads and stores in flight
 // per CU: the LDS allows two such workgroups per CU at 256, four at 128; measured 1-2 %
@@ -553,7 +491,8 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void preconvert_kernel(
 // tile's record. The prefill then only copies records into LDS: the split is done once
 // per key instead of once per workgroup that reads the key.
 
-template <int HD, int EB, bool NT>
+// V16: records of the scores-accurate mode (V rows rounded to f16 as they are).
+template <int HD, int EB, bool NT, bool V16 = false>
 __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
     const void *__restrict__ k, const void *__restrict__ v, float *__restrict__ ps, int nkeys,
     int Hkv, int tlo, int nt, int hdr) {
@@ -570,7 +509,7 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
     // V^T rows within their 32 keys, and the exponents where written.)
     f32x4 rk[C::NLD], rv[C::NLD];
     prefill_load_step<C, EB, NT>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
-    prefill_store_step<C>(smem, rk, rv, 0, tid);
+    prefill_store_step<C, false, V16>(smem, rk, rv, 0, tid);
     __syncthreads();
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::PS_FLOATS);
     if constexpr (C::PS_IMAGE) {
@@ -636,7 +575,14 @@ constexpr int prefill_max_waves() {
     constexpr int lo = prefill_min_waves<HD, HPW, WPH, KSPLIT>();
     return w < lo ? lo : w > 8 ? 8 : w;
 }
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false>
+// PV1 (head_dim >= 32, with FAST false): the scores-accurate mode. The scores keep the
+// three-product split; O^T += V^T P^T is one f16 product, as in FAST: V rows rounded to f16
+// as they are at staging (pre-split records of the same layout, V16), the weights
+// p <= 2^kSlack rounded to f16, and l summing the weights as rounded (so that they
+// normalise exactly and a dominant key's rounding cancels). A third fewer products than
+// the accurate mode, and no per-query unit.
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false,
+          bool PV1 = false>
 __global__ __attribute__((
     amdgpu_flat_work_group_size(1, HPW * WPH * KSPLIT * 64),
     amdgpu_waves_per_eu(prefill_min_waves<HD, HPW, WPH, KSPLIT>(),
@@ -702,13 +648,8 @@ __global__ __attribute__((
     f32x4 rs[PS ? (FAST ? C::FPSN : C::PSN) : 1];
     const float *recs =
         PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
-    // The f16 mode over pre-converted records on prompts runs the software-pipelined loop
-    // (see the loop below); its staging is one step further ahead for K.
-    constexpr bool kPipe = FAST && PS && !RANGE && EB_PREFILL_PIPE;
     auto load_first_step = [&] {
-        if constexpr (kPipe)
-            fpipe_load_first<C>(reinterpret_cast<const f32x4 *>(recs), rs, ps_nt, tid);
-        else if constexpr (PS && FAST)
+        if constexpr (PS && FAST)
             fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
         else if constexpr (PS && C::PS_IMAGE)
             ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
@@ -816,20 +757,18 @@ __global__ __attribute__((
     float l = 0.0f;
     // SPV: O^T is accumulated in units of 2^E (per query; both lane halves of a query hold
     // the same E).
-    int E = FAST ? 0 : kZeroRowExp;
+    int E = (FAST || PV1) ? 0 : kZeroRowExp;
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     // ... and the first step's K/V into LDS.
-    if constexpr (kPipe)
-        fpipe_store_first<C>(smem, rs, tid);
-    else if constexpr (PS && FAST)
+    if constexpr (PS && FAST)
         fps_store_step<C>(smem, rs, 0, tid);
     else if constexpr (PS && C::PS_IMAGE)
         wait_vm_all();
     else if constexpr (PS)
         ps_store_step<C>(smem, rs, 0, tid);
     else
-        prefill_store_step<C, FAST>(smem, rk, rv, 0, tid);
+        prefill_store_step<C, FAST, PV1>(smem, rk, rv, 0, tid);
     __syncthreads();
 
     // The next step's K/V: PS records into registers (or, head_dim 256, straight into the
@@ -857,7 +796,7 @@ __global__ __attribute__((
         else if constexpr (PS)
             ps_store_step<C>(smem, rs, b1, tid);
         else
-            prefill_store_step<C, FAST>(smem, rk, rv, b1, tid);
+            prefill_store_step<C, FAST, PV1>(smem, rk, rv, b1, tid);
     };
 
     if constexpr (C::SPV) {
@@ -936,12 +875,12 @@ __global__ __attribute__((
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 p[r] = eb::fast_exp2(p[r] - mref);
-                ps += p[r];
+                if constexpr (!PV1) ps += p[r];
             }
-            l = l * corr + ps;
+            if constexpr (!PV1) l = l * corr + ps;
             const float mold = m;
             m = mnew;
-            if constexpr (FAST) {
+            if constexpr (FAST || PV1) {
                 // One f16 product: P rounded to f16 (p <= 2^kSlack, so no unit is needed),
                 // the V^T hi halves (V rounded to f16 at staging). O^T follows the softmax
                 // correction when any lane's reference max moved.
@@ -959,10 +898,18 @@ __global__ __attribute__((
                         const int r = 8 * u + 2 * c2;
                         hw[c2] = __builtin_bit_cast(
                             unsigned, __builtin_convertvector(f32x2{p[r], p[r + 1]}, f16x2));
+                        if constexpr (PV1) {
+                            // l sums the weights as rounded, so that they normalise exactly
+                            // and a dominant key's rounding cancels
+                            const f32x2 pr = __builtin_convertvector(
+                                __builtin_bit_cast(f16x2, hw[c2]), f32x2);
+                            ps += pr.x + pr.y;
+                        }
                     }
                     ph[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
                     pl[u] = ph[u];
                 }
+                if constexpr (PV1) l = l * corr + ps;
             } else {
                 // The tile's V exponents ev (V row = 2^ev * v').
                 const int *Ev = reinterpret_cast<const int *>(smem + b * C::BUF +
@@ -1026,58 +973,13 @@ __global__ __attribute__((
             }
         };
 
-        // The f16 mode's softmax for the pipelined loop: as tile_softmax, except that the
-        // rescale of O^T by corr is left to the caller (after the previous step's products);
-        // masked: the per-key causal mask (a wave's last tile, the one holding its diagonal).
-        auto tile_softmax_pipe = [&](int kb, const floatx16 &sc, f16x8 (&php)[2], float &corr,
-                                     bool &grew, bool masked) {
-            float p[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = sc[r];
-            if (masked) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-                    if (key > pi) p[r] = -INFINITY;
-                }
-            }
-            float mt = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const bool grow = mt > m + kSlack;
-            const float mnew = grow ? fmaxf(m, mt) : m;
-            const float mref = mnew == -INFINITY ? 0.0f : mnew;
-            corr = grow ? eb::fast_exp2(m - mref) : 1.0f;
-            float ps = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                p[r] = eb::fast_exp2(p[r] - mref);
-                ps += p[r];
-            }
-            l = l * corr + ps;
-            m = mnew;
-            grew = grow;
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                unsigned hw[4];
-#pragma unroll
-                for (int c2 = 0; c2 < 4; ++c2) {
-                    const int r = 8 * u + 2 * c2;
-                    hw[c2] = __builtin_bit_cast(
-                        unsigned, __builtin_convertvector(f32x2{p[r], p[r + 1]}, f16x2));
-                }
-                php[u] = __builtin_bit_cast(f16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
-            }
-        };
-
         // O^T += V^T P^T: block mb's row col is dim NB*col + mb (the layout the output stage
         // expects), stored at V^T row 32*mb + col; keys 16u + 4hf + 0..3 and 16u + 8 + 4hf +
         // 0..3 of this wave's tile (the order of ph / pl). FAST: the hi halves only.
         auto tile_pv = [&](int b, const f16x8 (&ph)[2], const f16x8 (&pl)[2]) {
             const _Float16 *vth =
                 reinterpret_cast<const _Float16 *>(smem + b * C::BUF + C::STEP_KEYS * KS);
-            if constexpr (FAST) {
+            if constexpr (FAST || PV1) {
                 // f16 mode: the NB V fragments of one 16-key half are read first and the
                 // products go round the NB accumulators (measured 2-4 % faster than one
                 // accumulator's products back to back; the three-product mode has no
@@ -1112,54 +1014,6 @@ __global__ __attribute__((
         floatx16 sacc;
         int ek[16];
         f16x8 ph[2], pl[2];
-        if constexpr (kPipe) {
-            // Software-pipelined f16 mode (prompts from position 0, one chunk per block, so
-            // c_lo = 0 and this wave's tiles are ks, ks + KSPLIT, ... up to my_t1). Within
-            // iteration s the matrix cores take the P V products of step s - 1 and the
-            // scores of step s + 1 while the VALU runs step s's softmax: neither product
-            // depends on that softmax, so one wave keeps the matrix pipe fed instead of
-            // alternating products and softmax. O^T gets the products of s - 1, then the
-            // rescale of step s, then (next iteration) the products of s: the order the
-            // unpipelined loop applies them in, so the two give the same bits.
-            const int s_last = (live && my_t1 >= ks) ? (my_t1 - ks) / KSPLIT : -1;
-            floatx16 sn;
-            f16x8 pp[2];
-            float corr = 1.0f;
-            bool grew = false;
-            if (s_last >= 0) tile_qk(0, sacc, ek);
-            for (int it = 0; it < nsteps; ++it) {
-                const int buf = it & 1;
-                fpipe_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, it + 2, it, ps_nt,
-                                   tid);
-                if (it < s_last) {
-                    // Steady state (no mask: only a wave's last tile holds its diagonal).
-                    if (it > 0) tile_pv(buf ^ 1, pp, pp);
-                    tile_softmax_pipe(it * KSPLIT * kTile + ks * kTile, sacc, ph, corr, grew,
-                                      false);
-                    tile_qk(buf ^ 1, sn, ek);
-                    sacc = sn;
-                } else if (it == s_last) {
-                    if (it > 0) tile_pv(buf ^ 1, pp, pp);
-                    tile_softmax_pipe(it * KSPLIT * kTile + ks * kTile, sacc, ph, corr, grew,
-                                      true);
-                } else if (it == s_last + 1) {
-                    tile_pv(buf ^ 1, pp, pp);
-                }
-                // O^T follows step it's softmax correction once the products of step it - 1
-                // are in (the wave skips it when no lane's reference max moved).
-                if (it <= s_last && __builtin_amdgcn_ballot_w64(grew) != 0) {
-#pragma unroll
-                    for (int mb = 0; mb < NB; ++mb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) oacc[mb][r] *= corr;
-                }
-                pp[0] = ph[0];
-                pp[1] = ph[1];
-                fps_store_step<C>(smem, rs, buf, tid);
-                __syncthreads();
-            }
-            if (s_last == nsteps - 1) tile_pv(nsteps & 1 ? 0 : 1, pp, pp);
-        } else
         for (int it = 0; it < nsteps; ++it) {
             const int buf = it & 1;
             const int tile = c_lo + it * KSPLIT + ks;
@@ -1172,7 +1026,7 @@ __global__ __attribute__((
                 // them (measured +3 % at Qwen, +6 % at Mistral T=4096; the f16 mode, with a
                 // third of the products, measured slower with it, and head dim 256 runs one
                 // wave per SIMD).
-                constexpr bool kPvPrio = !FAST && HD <= 128;
+                constexpr bool kPvPrio = !FAST && !PV1 && HD <= 128;
                 if constexpr (kPvPrio) __builtin_amdgcn_s_setprio(1);
                 tile_pv(buf, ph, pl);
                 if constexpr (kPvPrio) __builtin_amdgcn_s_setprio(0);
@@ -1661,7 +1515,8 @@ size_t workspace_floats(size_t hd, int H, int Hkv, const PrefillRange &r) {
     return presplit_floats(hd, H, Hkv, r) + chunk_floats(hd, H, prefill_chunks(hd, H, Hkv, r), r);
 }
 
-template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false>
+template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, bool FAST = false,
+          bool PV1 = false>
 eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const void *v,
                            const float *ps, float *o, int H, int Hkv, const PrefillRange &r,
                            float scale_log2, const PrefillChunks &ch, float *part_acc,
@@ -1672,7 +1527,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     std::call_once(once, [&] {
         attr_err = hipFuncSetAttribute(
             reinterpret_cast<const void *>(
-                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST>),
+                &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
@@ -1680,7 +1535,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const dim3 grid((unsigned)(nqb * ngroups), (unsigned)ch.nchmax);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
         q, k, v, ps, presplit_tlo(r), presplit_nt(r), o, H, Hkv, r.rows, r.nkeys, r.qbase,
         r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml, r.hdr);
     eb_status err = eb::check_launch("attn_prefill");
@@ -1692,7 +1547,8 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     return eb::check_launch("attn_prefill (chunk merge)");
 }
 
-template <int HD, int HPW, int WPH, int KSPLIT>
+// PV1: the scores-accurate mode (prompts from position 0 over f32 K/V only).
+template <int HD, int HPW, int WPH, int KSPLIT, bool PV1 = false>
 eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const void *v,
                            float *o, int H, int Hkv, const PrefillRange &r, float scale_log2) {
     const bool plain = r.qbase == 0 && r.window == 0;
@@ -1711,7 +1567,13 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
             // unchanged; prompts and caches of 33 MB, likely still cached after their
             // write, 1-5 % slower with them).
             const bool stream = (size_t)nt * kTile * Hkv * r.hdr * 4 * 2 > kPresplitStreamBytes;
-            if (r.ce == eb::CacheElem::F16)
+            if (PV1 && stream)
+                presplit_kernel<HD, 4, true, true><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
+                    k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
+            else if (PV1)
+                presplit_kernel<HD, 4, false, true><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
+                    k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
+            else if (r.ce == eb::CacheElem::F16)
                 presplit_kernel<HD, 2, false><<<grid, PresplitCfg<HD>::THREADS, 0, st>>>(
                     k, v, ps, r.nkeys, Hkv, presplit_tlo(r), nt, r.hdr);
             else if (r.ce == eb::CacheElem::E4M3)
@@ -1726,13 +1588,21 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
             const eb_status err = eb::check_launch("attn_prefill (pre-split)");
             if (err != EB_OK) return err;
             // (the records are f16 hi/lo splits whatever the cache's element type)
-            if (plain && r.ce == eb::CacheElem::F32)
-                return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, true>(
+            if constexpr (PV1) {
+                return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, true, false, true>(
                     st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
-            return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 4, true>(
-                st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
+            } else {
+                if (plain && r.ce == eb::CacheElem::F32)
+                    return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, true>(
+                        st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
+                return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 4, true>(
+                    st, q, k, v, ps, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
+            }
         }
     }
+    if constexpr (PV1)
+        return launch_prefill_r<HD, HPW, WPH, KSPLIT, false, 4, false, false, true>(
+            st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
     if (r.ce == eb::CacheElem::F16)
         return launch_prefill_r<HD, HPW, WPH, KSPLIT, true, 2, false>(
             st, q, k, v, nullptr, o, H, Hkv, r, scale_log2, ch, part_acc, part_ml);
@@ -1754,7 +1624,7 @@ eb_status launch_prefill_t(hipStream_t st, const float *q, const void *k, const 
 //    halves the longest per-wave chain where the blocks are 64 or 128 rows tall.
 // head_dim 256: the Q fragment and O^T accumulators take ~450 registers per lane, so one
 // wave per SIMD: 4 waves, no key split. (prefill_shape restates this choice.)
-template <int HD>
+template <int HD, bool PV1 = false>
 eb_status launch_prefill_hd(hipStream_t st, const float *q, const void *k, const void *v,
                             float *o, int H, int Hkv, const PrefillRange &r,
                             float scale_log2) {
@@ -1762,17 +1632,18 @@ eb_status launch_prefill_hd(hipStream_t st, const float *q, const void *k, const
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
     if (g % 4 == 0) {
         if (KSPLIT == 2 && prefill_shape(HD, H, g, r.rows).ksplit == 2)
-            return launch_prefill_t<HD, 4, 1, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
-        return launch_prefill_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, scale_log2);
+            return launch_prefill_t<HD, 4, 1, KSPLIT, PV1>(st, q, k, v, o, H, Hkv, r, scale_log2);
+        return launch_prefill_t<HD, 4, 1, 1, PV1>(st, q, k, v, o, H, Hkv, r, scale_log2);
     }
     if (g % 2 == 0)
-        return launch_prefill_t<HD, 2, 2, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
-    return launch_prefill_t<HD, 1, 4, KSPLIT>(st, q, k, v, o, H, Hkv, r, scale_log2);
+        return launch_prefill_t<HD, 2, 2, KSPLIT, PV1>(st, q, k, v, o, H, Hkv, r, scale_log2);
+    return launch_prefill_t<HD, 1, 4, KSPLIT, PV1>(st, q, k, v, o, H, Hkv, r, scale_log2);
 }
 
+// pv1: the scores-accurate mode (PV1 kernels; prompts over f32 K/V, head dims >= 24).
 eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, const void *v,
                                float *o, size_t h, size_t hkv, size_t hd, float scale,
-                               const PrefillRange &r) {
+                               const PrefillRange &r, bool pv1 = false) {
     if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
          reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o)) & 15)
         return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill: q/k/v/o must be 16-byte aligned");
@@ -1784,6 +1655,19 @@ eb_status launch_prefill_range(hipStream_t st, const float *q, const void *k, co
     const size_t need = workspace_floats(hp, H, Hk, r);
     if (need == 0 || !r.ws || r.ws_floats < need || (reinterpret_cast<uintptr_t>(r.ws) & 15))
         rr.ws = nullptr;  // no pre-split pass (split while staging), no key chunks
+    if (pv1) {
+        if (r.qbase != 0 || r.window != 0 || r.ce != eb::CacheElem::F32)
+            return eb::fail(EB_UNSUPPORTED_CONFIG,
+                            "attn_prefill_pv16: prompts from position 0 over f32 K/V only");
+        switch (hp) {
+            case 32: return launch_prefill_hd<32, true>(st, q, k, v, o, H, Hk, rr, sl2);
+            case 64: return launch_prefill_hd<64, true>(st, q, k, v, o, H, Hk, rr, sl2);
+            case 128: return launch_prefill_hd<128, true>(st, q, k, v, o, H, Hk, rr, sl2);
+            case 256: return launch_prefill_hd<256, true>(st, q, k, v, o, H, Hk, rr, sl2);
+            default:
+                return eb::fail(EB_UNSUPPORTED_CONFIG, "attn_prefill_pv16: head_dim %zu", hd);
+        }
+    }
     switch (hp) {
         case 4: return launch_prefill_hd<4>(st, q, k, v, o, H, Hk, rr, sl2);
         case 8: return launch_prefill_hd<8>(st, q, k, v, o, H, Hk, rr, sl2);
@@ -1891,6 +1775,14 @@ eb_status launch_attn_prefill(hipStream_t st, const float *q, const float *k, co
                               float *ws, size_t ws_floats) {
     return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
                                 PrefillRange{(int)s, (int)s, 0, 0, CacheElem::F32, ws, ws_floats, (int)hd});
+}
+
+eb_status launch_attn_prefill_pv16(hipStream_t st, const float *q, const float *k,
+                                   const float *v, float *o, size_t h, size_t hkv, size_t s,
+                                   size_t hd, float scale, float *ws, size_t ws_floats) {
+    return launch_prefill_range(st, q, k, v, o, h, hkv, hd, scale,
+                                PrefillRange{(int)s, (int)s, 0, 0, CacheElem::F32, ws, ws_floats, (int)hd},
+                                true);
 }
 
 eb_status launch_attn_prefill_chunk(hipStream_t st, const float *q, const float *kc,

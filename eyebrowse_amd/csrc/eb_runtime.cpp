@@ -718,14 +718,20 @@ static eb_status prefill_ws(const PrefillWs &src, size_t h, size_t hkv, size_t h
     return EB_OK;
 }
 
+// pv1: the scores-accurate mode (eb_attn_prefill_pv16), head dims 24 and up.
 static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, const float *k,
                                  size_t kn, const float *v, size_t vn, float *o, size_t on,
                                  size_t h, size_t hkv, size_t s, size_t hd, float scale,
-                                 const PrefillWs &wsrc = PrefillWs()) {
+                                 const PrefillWs &wsrc = PrefillWs(), bool pv1 = false) {
     EB_TRY(eb::check_heads(h, hkv));
     if (!eb::attn_head_dim_supported(hd))
         return fail(EB_UNSUPPORTED_CONFIG,
-                    "attn_prefill: head_dim %zu (supported: 4, multiples of 8 up to 128, multiples of 16 up to 256)", hd);
+                    "attn_prefill: head_dim %zu (supported: 4, multiples of 8 up to 128, "
+                    "multiples of 16 up to 256)", hd);
+    if (pv1 && hd < 24)
+        return fail(EB_UNSUPPORTED_CONFIG,
+                    "attn_prefill_pv16: head_dim %zu (24 and up; smaller head dims run "
+                    "attn_prefill, in f32)", hd);
     EB_TRY(eb::check_numel(qn, {s, h, hd}, "q"));
     EB_TRY(eb::check_numel(kn, {s, hkv, hd}, "k"));
     EB_TRY(eb::check_numel(vn, {s, hkv, hd}, "v"));
@@ -739,7 +745,10 @@ static eb_status prefill_checked(hipStream_t st, const float *q, size_t qn, cons
     size_t wsn;
     WsLock lk;
     EB_TRY(prefill_ws(wsrc, h, hkv, hd, s, s, 0, 0, &ws, &wsn, lk));
-    EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
+    if (pv1)
+        EB_TRY(eb::launch_attn_prefill_pv16(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
+    else
+        EB_TRY(eb::launch_attn_prefill(st, q, k, v, o, h, hkv, s, hd, scale, ws, wsn));
     return eb::ok();
 }
 
@@ -1092,6 +1101,20 @@ eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor 
                            hd, scale, PrefillWs{rec->dev});
 }
 
+eb_status eb_attn_prefill_pv16(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                               const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv,
+                               size_t s, size_t hd, float scale) {
+    EB_TRY(rec_ready(rec));
+    EB_TRY(tensor_f32(q, "q", rec->dev));
+    EB_TRY(tensor_f32(k, "k", rec->dev));
+    EB_TRY(tensor_f32(v, "v", rec->dev));
+    EB_TRY(tensor_f32(o, "o", rec->dev));
+    return prefill_checked(rec->dev->stream, (const float *)q->ptr, eb_tensor_numel(q),
+                           (const float *)k->ptr, eb_tensor_numel(k), (const float *)v->ptr,
+                           eb_tensor_numel(v), (float *)o->ptr, eb_tensor_numel(o), h, hkv, s,
+                           hd, scale, PrefillWs{rec->dev}, true);
+}
+
 eb_status eb_attn_prefill_fast(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
                                const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
                                size_t hd, float scale) {
@@ -1382,6 +1405,24 @@ eb_status eb_launch_attn_prefill_ws(void *stream, const float *q, size_t q_numel
     return prefill_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
                            h, hkv, s, hd, scale,
                            PrefillWs{nullptr, true, workspace, workspace_floats});
+}
+
+eb_status eb_launch_attn_prefill_pv16(void *stream, const float *q, size_t q_numel,
+                                      const float *k, size_t k_numel, const float *v,
+                                      size_t v_numel, float *o, size_t o_numel, size_t h,
+                                      size_t hkv, size_t s, size_t hd, float scale) {
+    return prefill_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
+                           h, hkv, s, hd, scale, PrefillWs(), true);
+}
+
+eb_status eb_launch_attn_prefill_pv16_ws(void *stream, const float *q, size_t q_numel,
+                                         const float *k, size_t k_numel, const float *v,
+                                         size_t v_numel, float *o, size_t o_numel, size_t h,
+                                         size_t hkv, size_t s, size_t hd, float scale,
+                                         float *workspace, size_t workspace_floats) {
+    return prefill_checked((hipStream_t)stream, q, q_numel, k, k_numel, v, v_numel, o, o_numel,
+                           h, hkv, s, hd, scale,
+                           PrefillWs{nullptr, true, workspace, workspace_floats}, true);
 }
 
 eb_status eb_launch_attn_prefill_chunk_ws(void *stream, const float *q, size_t q_numel,

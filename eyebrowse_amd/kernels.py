@@ -23,6 +23,14 @@ def attn_prefill_fast(rec: Recorder, q: Tensor, k: Tensor, v: Tensor, o: Tensor,
                                      s, hd, scale))
 
 
+def attn_prefill_pv16(rec: Recorder, q: Tensor, k: Tensor, v: Tensor, o: Tensor, h: int,
+                      hkv: int, s: int, hd: int, scale: float) -> None:
+    """attn_prefill in the opt-in scores-accurate mode: scores as attn_prefill computes them,
+    O += P V as one f16 product (max-abs within 2^-11 of the largest |V|)."""
+    check(lib().eb_attn_prefill_pv16(rec.handle, q.handle, k.handle, v.handle, o.handle, h, hkv,
+                                     s, hd, scale))
+
+
 def attn_decode(rec: Recorder, q: Tensor, kcache: Tensor, vcache: Tensor, o: Tensor, h: int,
                 hkv: int, pos: int, hd: int, max_seq: int, scale: float) -> None:
     """attention.rs:124-162: q [h,hd] attends keys 0..=pos of [max_seq,hkv,hd] caches."""
@@ -152,6 +160,22 @@ def launch_attn_prefill_fast(stream: int, q: int, q_numel: int, k: int, k_numel:
                              hd: int, scale: float) -> None:
     check(lib().eb_launch_attn_prefill_fast(stream, q, q_numel, k, k_numel, v, v_numel, o,
                                             o_numel, h, hkv, s, hd, scale))
+
+
+def launch_attn_prefill_pv16(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                             v_numel: int, o: int, o_numel: int, h: int, hkv: int, s: int,
+                             hd: int, scale: float) -> None:
+    check(lib().eb_launch_attn_prefill_pv16(stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                            o_numel, h, hkv, s, hd, scale))
+
+
+def launch_attn_prefill_pv16_ws(stream: int, q: int, q_numel: int, k: int, k_numel: int, v: int,
+                                v_numel: int, o: int, o_numel: int, h: int, hkv: int, s: int,
+                                hd: int, scale: float, workspace: int,
+                                workspace_floats: int) -> None:
+    check(lib().eb_launch_attn_prefill_pv16_ws(stream, q, q_numel, k, k_numel, v, v_numel, o,
+                                               o_numel, h, hkv, s, hd, scale, workspace,
+                                               workspace_floats))
 
 
 def attn_prefill_fast_workspace_floats(h: int, hkv: int, hd: int, s: int) -> int:

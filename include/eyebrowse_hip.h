@@ -161,6 +161,20 @@ eb_status eb_attn_prefill(eb_recorder *rec, const eb_tensor *q, const eb_tensor 
 eb_status eb_attn_prefill_fast(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
                                const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv, size_t s,
                                size_t hd, float scale);
+/* attn_prefill in the opt-in scores-accurate mode (no counterpart in the reference): the
+ * scores q.k are computed as attn_prefill computes them (three f16 products on exact hi/lo
+ * splits, to about f32 accuracy, any scale), the softmax and its accumulation in f32, and
+ * O += P V as one f16 product: V rounded to f16 once, the softmax weights rounded to f16,
+ * their sum taken over the rounded weights. A third fewer matrix-core products than
+ * attn_prefill. The rounding of V bounds the error: max-abs <= 2^-11 times the largest |V|
+ * element (half an f16 ulp) plus f32 noise; rel-L2 about 2e-4. On the BASELINE prefill
+ * configs (N(0,1) inputs, Gemma-4's scale 1.0 included) that is rel-L2 below 1e-3 and
+ * max-abs below 2e-3, the north-star bar; V elements of 8 or more in magnitude can exceed
+ * that max-abs (use attn_prefill). V must fit f16 (|v| < 65504). Prompts from position 0,
+ * head_dim 24 and up. Same workspace as attn_prefill (the device's here). */
+eb_status eb_attn_prefill_pv16(eb_recorder *rec, const eb_tensor *q, const eb_tensor *k,
+                               const eb_tensor *v, eb_tensor *o, size_t h, size_t hkv,
+                               size_t s, size_t hd, float scale);
 /* attn_decode (attention.rs:124-162): q [h,hd] attends keys 0..=pos of the seq-major
  * caches [max_seq,hkv,hd]; o [h,hd]. Split-KV with a log-sum-exp merge; the split
  * workspace belongs to the device and is stream ordered. */
@@ -222,6 +236,19 @@ eb_status eb_launch_attn_prefill(void *stream, const float *q, size_t q_numel,
                                  const float *k, size_t k_numel, const float *v,
                                  size_t v_numel, float *o, size_t o_numel, size_t h,
                                  size_t hkv, size_t s, size_t hd, float scale);
+/* eb_attn_prefill_pv16 on caller memory: without a workspace every workgroup splits the K/V
+ * rows it stages; with eb_attn_prefill_workspace_floats(h, hkv, hd, 0, s) floats (16-byte
+ * aligned, no initialisation) it runs the pre-split pass and key chunks as
+ * eb_launch_attn_prefill_ws does. */
+eb_status eb_launch_attn_prefill_pv16(void *stream, const float *q, size_t q_numel,
+                                      const float *k, size_t k_numel, const float *v,
+                                      size_t v_numel, float *o, size_t o_numel, size_t h,
+                                      size_t hkv, size_t s, size_t hd, float scale);
+eb_status eb_launch_attn_prefill_pv16_ws(void *stream, const float *q, size_t q_numel,
+                                         const float *k, size_t k_numel, const float *v,
+                                         size_t v_numel, float *o, size_t o_numel, size_t h,
+                                         size_t hkv, size_t s, size_t hd, float scale,
+                                         float *workspace, size_t workspace_floats);
 eb_status eb_launch_attn_prefill_fast(void *stream, const float *q, size_t q_numel,
                                       const float *k, size_t k_numel, const float *v,
                                       size_t v_numel, float *o, size_t o_numel, size_t h,
