@@ -16,6 +16,8 @@ are resident in HBM before timing starts.
 
 The same line carries `roofline` (the decode step against HBM), `roofline_prefill` (the
 Mistral T=4096 causal prefill of the same config against the f16 and FP32 matrix peaks),
+`roofline_prefill_f16` (the same prefill in the opt-in f16 mode), `roofline_prefill_pv16`
+(Gemma-4 T=4096 in the opt-in scores-accurate mode),
 `cpu_baseline` (the oracle on this host's cores, the same decode config) and, under
 `extra`, every other BASELINE decode / prefill config, the IEEE-half cache decodes,
 chunked prefill, the projections and a layer decode step.
@@ -434,7 +436,35 @@ def prefill_extras(eb, hip, dev, sc128) -> dict:
         del p
         dev.synchronize()
     out.update(fast_prefill_extras(eb, hip, dev, sc128))
+    out.update(pv16_prefill_extras(eb, hip, dev, sc128))
     out.update(chunk_extras(eb, hip, dev))
+    return out
+
+
+def pv16_prefill_extras(eb, hip, dev, sc128) -> dict:
+    """The opt-in scores-accurate prefill (eb_launch_attn_prefill_pv16_ws: three-product
+    scores, one f16 P V product) on the BASELINE prefill configs, Gemma-4's scale 1.0
+    included; TFLOP/s of the same algorithmic FLOPs, against the f16 peak."""
+    out = {}
+    for name, H, Hkv, hd, T, sc in (("qwen_T512", 16, 8, 128, 512, sc128),
+                                    ("qwen_T2048", 16, 8, 128, 2048, sc128),
+                                    ("qwen_T4096", 16, 8, 128, 4096, sc128),
+                                    ("mistral_T4096", 32, 8, 128, 4096, sc128),
+                                    ("gemma_T4096", 16, 8, 256, 4096, 1.0)):
+        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc, pv16=True)
+        for _ in range(3):
+            p.launch()
+        reps = 20 if T >= 2048 else 100
+        t = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+        tf_s = p.flops / (t * 1e-3) / 1e12
+        out[f"prefill_pv16_{name}"] = {
+            "gflop": round(p.flops / 1e9, 3), "ms": round(t, 4), "TFLOPs": round(tf_s, 2),
+            "mfma": "v_mfma_f32_32x32x16_f16: Q K^T three products on exact hi/lo splits, "
+                    "V^T P^T one product (f16 V, f16 P)",
+            "tolerance": PV16_TOLERANCE,
+            "frac_f16_mfma_peak": round(tf_s / F16_MFMA_PEAK_TFLOPS, 4)}
+        del p
+        dev.synchronize()
     return out
 
 
@@ -790,7 +820,8 @@ def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
 
 def trace_workload(eb, hip, dev, sc128, name: str) -> None:
     """One workload alone, for a rocprofv3 kernel trace: decode steps through HIP graphs
-    (200 steps), prefill launches (3 warm-up + 20), the layer decode step (eager and graph),
+    (200 steps), prefill launches (3 warm-up + 20; prefill_f16fast_* in the f16 mode,
+    prefill_pv16_* in the scores-accurate mode), the layer decode step (eager and graph),
     or a Gemma-4 prompt through Attention.forward_qkv (the fused pre-attention pass, the
     pre-split pass and the attention)."""
     decode = {"decode_mistral_keys32768": (32, 8, 128, 32768, 32767, sc128, False),
@@ -810,9 +841,10 @@ def trace_workload(eb, hip, dev, sc128, name: str) -> None:
         w.run_exact(200)
         dev.synchronize()
         w.close()
-    elif name in prefill or name.replace("f16fast_", "") in prefill:
-        H, Hkv, hd, T, sc = prefill[name.replace("f16fast_", "")]
-        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc, fast="f16fast_" in name)
+    elif name.replace("f16fast_", "").replace("pv16_", "") in prefill:
+        H, Hkv, hd, T, sc = prefill[name.replace("f16fast_", "").replace("pv16_", "")]
+        p = PrefillWorkload(eb, dev, H, Hkv, hd, T, sc, fast="f16fast_" in name,
+                            pv16="pv16_" in name)
         for _ in range(23):
             p.launch()
         dev.synchronize()
@@ -838,6 +870,39 @@ def trace_workload(eb, hip, dev, sc128, name: str) -> None:
     else:
         raise SystemExit(f"unknown workload {name}")
     print(json.dumps({"trace_workload": name, "done": True}), flush=True)
+
+
+PV16_TOLERANCE = ("max-abs <= 2^-11 x max|V| (half an f16 ulp of V) vs the f32 oracle; "
+                  "on the BASELINE configs rel-L2 <= 1e-3 and max-abs <= 2e-3 (measured "
+                  "rel-L2 2.1e-4 - 2.7e-4, max-abs 1.95e-3 at Gemma-4)")
+
+
+def pv16_roofline(eb, hip, dev, reps: int = 20) -> dict:
+    """The opt-in scores-accurate prefill on Gemma-4 T=4096 (head_dim
+    256, scale 1.0, which the f16 mode refuses): the pre-split pass plus the attention
+    kernel, HIP events around `reps` back-to-back launches."""
+    p = PrefillWorkload(eb, dev, 16, 8, 256, 4096, 1.0, pv16=True)
+    for _ in range(3):
+        p.launch()
+    ms = hip.time_loop(dev.stream, reps, lambda i: p.launch())
+    tf = p.flops / (ms * 1e-3) / 1e12
+    del p
+    dev.synchronize()
+    return {
+        "bound": "mfma",
+        "config": "gemma-4-dense-shaped global-layer causal prefill, T=4096, 16 q / 8 KV heads, "
+                  "head_dim 256, scale 1.0, f32 q/k/v (BASELINE configs[4]), opt-in "
+                  "scores-accurate mode",
+        "kernel": "presplit_kernel<256, 4, false, true> + prefill_kernel<256, 2, 2, 1, false, "
+                  "4, true, false, true>",
+        "mfma": "v_mfma_f32_32x32x16_f16: Q K^T three products on exact hi/lo splits, V^T P^T "
+                "one product (f16 V, f16 P), f32 softmax and accumulation",
+        "tolerance": PV16_TOLERANCE,
+        "achieved": round(tf, 2), "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
+        "algorithmic_flops_per_launch": p_flops(16, 256, 4096),
+        "avg_launch_ms": round(ms, 5),
+    }
 
 
 def prefill_roofline(eb, hip, dev, sc128, reps: int = 20, fast: bool = False) -> dict:
@@ -996,6 +1061,9 @@ def main():
     print(f"[bench] prefill {pf['achieved']} TFLOP/s", file=sys.stderr, flush=True)
     pff = prefill_roofline(eb, hip, dev, sc128, fast=True)
     print(f"[bench] prefill f16 mode {pff['achieved']} TFLOP/s", file=sys.stderr, flush=True)
+    pfv = pv16_roofline(eb, hip, dev)
+    print(f"[bench] prefill scores-accurate mode (Gemma-4) {pfv['achieved']} TFLOP/s",
+          file=sys.stderr, flush=True)
 
     extra = {}
     if args.only == "all":
@@ -1037,6 +1105,7 @@ def main():
         },
         "roofline_prefill": pf,
         "roofline_prefill_f16": pff,
+        "roofline_prefill_pv16": pfv,
         "extra": extra,
     }
     if not args.no_cpu:
