@@ -576,7 +576,10 @@ def projection_extras(eb, hip, dev) -> dict:
 def layer_step_extras(eb, hip, dev) -> dict:
     """One Qwen3-width attention layer decode step at pos 100 (fused q/k/v projection,
     decode step with QK-norm and RoPE folded in, o_proj, a 4096-row LM head, argmax):
-    microseconds per step, recorded eagerly and replayed as a captured HIP graph."""
+    microseconds per step (HIP events), recorded eagerly and replayed as captured HIP graphs
+    of one and of eight steps, with the host time per call; and chains of 1 and 20 tiny
+    kernels, eager and as graphs, which separate a graph launch's per-replay cost from its
+    per-node cost."""
     H, Hkv, hd, hidden, vocab, max_seq, pos = 16, 8, 128, 1024, 4096, 256, 100
     rng = np.random.default_rng(4)
     w = {n: eb.Tensor.from_f16_packed(dev, sh, randn(rng, sh) * 0.03)
@@ -604,22 +607,60 @@ def layer_step_extras(eb, hip, dev) -> dict:
         r.submit()
         return y, logits, idx
 
-    for _ in range(5):
-        step()
-    eager = hip.time_loop(dev.stream, 200, lambda i: step())
-    dev.begin_capture()
-    try:
-        keep = step()
-    finally:
-        g = dev.end_capture()
-    for _ in range(5):
-        g.launch()
-    graph = hip.time_loop(dev.stream, 200, lambda i: g.launch())
-    dev.synchronize()
-    g.release()
-    del keep
+    def timed(fn, n, per=1):
+        """(GPU µs per step from HIP events, host µs per call) over n calls of fn, each
+        covering `per` steps."""
+        for _ in range(5):
+            fn()
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        host = (time.perf_counter() - t0) / n * 1e6
+        dev.synchronize()
+        return round(hip.time_loop(dev.stream, n, lambda i: fn()) * 1e3 / per, 2), round(host, 2)
+
+    eager, eager_host = timed(step, 200)
+    graphs = {}
+    for nsteps in (1, 8):
+        dev.begin_capture()
+        try:
+            keep = [step() for _ in range(nsteps)]
+        finally:
+            g = dev.end_capture()
+        graphs[nsteps] = timed(g.launch, 400 // nsteps, nsteps)
+        dev.synchronize()
+        g.release()
+        del keep
+    # chains of a tiny kernel (argmax over 64 floats, one workgroup): the per-kernel cost of
+    # eager launches and of graph nodes, and the per-replay cost of a graph launch
+    xs = eb.Tensor.from_f32(dev, (64,), np.arange(64, dtype=np.float32))
+    wst = eb.Tensor.empty(dev, (eb.argmax_workspace_floats(64),))
+    idx = eb.Tensor.empty(dev, (1,), eb.DType.U32)
+
+    def tiny(k):
+        for _ in range(k):
+            eb.launch_argmax(dev.stream, xs.data_ptr, 64, idx.data_ptr, 64, wst.data_ptr,
+                             wst.numel())
+    chains = {}
+    for k in (1, 20):
+        e_us, e_host = timed(lambda: tiny(k), 200, k)
+        dev.begin_capture()
+        try:
+            tiny(k)
+        finally:
+            g = dev.end_capture()
+        g_us, g_host = timed(g.launch, 200, k)
+        dev.synchronize()
+        g.release()
+        chains[f"x{k}"] = {"eager_us_per_kernel": e_us, "graph_us_per_kernel": g_us,
+                           "graph_launch_host_us": g_host}
     return {"layer_decode_step_qwen_pos100": {
-        "kernels": 5, "eager_us": round(eager * 1e3, 2), "graph_us": round(graph * 1e3, 2)}}
+        "kernels": 5, "eager_us": eager, "eager_host_us_per_step": eager_host,
+        "graph_us": graphs[1][0], "graph_launch_host_us": graphs[1][1],
+        "graph_8_steps_us_per_step": graphs[8][0],
+        "graph_8_steps_launch_host_us": graphs[8][1],
+        "tiny_kernel_chains": chains}}
 
 
 def traffic_run(eb, hip, dev, sc128):
