@@ -819,9 +819,13 @@ def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
     (1024 SIMDs x GRBM_GUI_ACTIVE / 8), GRBM_GUI_ACTIVE being the sum of the 8 XCDs' busy
     cycles (so the share is of the cycles the kernel ran, at the clock it ran at).
     A CSV given as WORKLOAD=PATH labels its rows with that workload (the passes of one
-    workload merge into its rows), so that configs whose kernels share a grid stay apart."""
+    workload merge into its rows), so that configs whose kernels share a grid stay apart.
+    Where the pass's kernel trace lies beside its counter CSV (X_kernel_trace.csv next to
+    X_counter_collection.csv), the kernel's average duration in that same pass and the clock
+    it implies, GRBM_GUI_ACTIVE / 8 / duration, are reported too: the pipe-busy share is of
+    the cycles at that clock."""
     import csv
-    merged, ndisp = {}, {}
+    merged, ndisp, timing = {}, {}, {}
     for arg in csv_paths:
         label, path = arg.split("=", 1) if "=" in arg else ("", arg)
         tot, disp = {}, {}
@@ -830,19 +834,31 @@ def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
             c = tot.setdefault(key, {})
             c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
             disp.setdefault(key, set()).add(r["Dispatch_Id"])
+        durs = {}
+        kt = path.replace("_counter_collection.csv", "_kernel_trace.csv")
+        if kt != path and os.path.exists(kt):
+            for r in csv.DictReader(open(kt)):
+                g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+                key = (label, _kernel_name(r["Kernel_Name"]), str(g))
+                durs.setdefault(key, []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         for key, c in tot.items():
             n = len(disp[key])
             m = merged.setdefault(key, {})
             for k, v in c.items():
                 m.setdefault(k, v / n)  # (a counter in two runs: the first run's average)
             ndisp[key] = max(ndisp.get(key, 0), n)
+            d = durs.get(key)
+            if d and "GRBM_GUI_ACTIVE" in c and key not in timing:
+                us = sum(d) / len(d)
+                timing[key] = (us, c["GRBM_GUI_ACTIVE"] / n / 8 / us / 1e3)
     names = sorted({n for c in merged.values() for n in c})
     lines = ["# SQ counters per dispatch", "", "Command (from the repository root on the GPU "
              "box, `R=$PWD`):", "", "```", cmd, "```", "",
              "| workload | kernel | grid | dispatches | " + " | ".join(names) +
              " | VALU/MFMA | MFMA busy cyc/MFMA | wait share | LDS wait share |"
-             " LDS conflict/active | MFMA pipe busy |",
-             "|---" * (4 + len(names) + 6) + "|"]
+             " LDS conflict/active | MFMA pipe busy | pass µs | clock GHz |",
+             "|---" * (4 + len(names) + 8) + "|"]
     for key, avg in merged.items():
         mf = avg.get("SQ_INSTS_MFMA", 0)
         ratio = lambda a, b: f"{a / b:.2f}" if b else "-"  # noqa: E731
@@ -854,7 +870,9 @@ def sq_summary(out_md: str, cmd: str, *csv_paths: str) -> None:
                      ratio(avg.get("SQ_WAIT_INST_LDS", 0), avg.get("SQ_WAVE_CYCLES", 0)) + " | " +
                      ratio(avg.get("SQ_LDS_BANK_CONFLICT", 0), avg.get("SQ_LDS_IDX_ACTIVE", 0)) +
                      " | " + ratio(avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0),
-                                   1024 * avg.get("GRBM_GUI_ACTIVE", 0) / 8) + " |")
+                                   1024 * avg.get("GRBM_GUI_ACTIVE", 0) / 8) + " | " +
+                     (f"{timing[key][0]:.1f} | {timing[key][1]:.2f}" if key in timing
+                      else "- | -") + " |")
     open(out_md, "w").write("\n".join(lines) + "\n")
     print("\n".join(lines))
 
