@@ -221,3 +221,48 @@ def test_random_raw_prefill_ws(dev, seed):
         want = oracle.attn_chunk(q[rr:rr + 1], kc, vc, h, hkv, pos0 + rr, 1, hd, sc, window,
                                  threads=16)
         assert_close(got[rr:rr + 1], want, what=f"row {rr}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_prefill_pv16(dev, seed):
+    """The scores-accurate mode at random shapes (head dims 24-256, odd multiples of 8
+    included, GQA 1-8, lengths 1-900, scales up to 1.0) and random launch forms (recorder,
+    raw with and without a workspace), against the oracle at the mode's bound: max-abs
+    <= 2^-11 x max|V| + 2e-5 and rel-L2 <= 4e-4 on the sampled rows."""
+    r = np.random.default_rng(5000 + seed)
+    hd = int(r.choice((24, 32, 40, 64, 72, 96, 120, 128, 160, 256)))
+    hkv = int(r.choice((1, 2, 4, 8)))
+    g = int(r.choice((1, 2, 3, 4, 8)))
+    h = hkv * g
+    s = int(r.integers(1, 900))
+    sc = float(r.choice((1.0, 0.3))) if seed % 3 == 0 else float(oracle.default_scale(hd))
+    form = ("recorder", "raw", "raw_ws")[seed % 3]
+    note(f"random pv16 seed={seed} h={h} hkv={hkv} hd={hd} s={s} scale={sc} {form}")
+    q = oracle.randn((s, h, hd), 7 * seed)
+    k, v = oracle.randn((s, hkv, hd), 7 * seed + 1), oracle.randn((s, hkv, hd), 7 * seed + 2)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    ot = eb.Tensor.empty(dev, (s, h, hd))
+    if form == "recorder":
+        rec = eb.Recorder(dev)
+        eb.attn_prefill_pv16(rec, qt, kt, vt, ot, h, hkv, s, hd, sc)
+        rec.submit()
+    else:
+        args = (dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(), vt.data_ptr,
+                vt.numel(), ot.data_ptr, ot.numel(), h, hkv, s, hd, sc)
+        if form == "raw":
+            eb.launch_attn_prefill_pv16(*args)
+        else:
+            need = eb.attn_prefill_workspace_floats(h, hkv, hd, 0, s)
+            ws = eb.Tensor.empty(dev, (max(need, 1),))
+            eb.launch_attn_prefill_pv16_ws(*args, ws.data_ptr, need)
+        dev.synchronize()
+    got = ot.to_f32().reshape(s, h, hd)
+    assert np.isfinite(got).all()
+    bound = 2.0 ** -11 * float(np.abs(v).max()) + 2e-5
+    for r0 in sorted({0, max(0, s // 2 - 8), max(0, s - 16)}):
+        n = min(16, s - r0)
+        want = oracle.attn_prefill(q, k, v, h, hkv, s, hd, sc, rows=(r0, n), threads=16)
+        d = got[r0:r0 + n].astype(np.float64) - want[r0:r0 + n].astype(np.float64)
+        assert float(np.abs(d).max()) <= bound, (r0, float(np.abs(d).max()), bound)
+        den = float(np.linalg.norm(want[r0:r0 + n].astype(np.float64)))
+        assert float(np.linalg.norm(d)) <= 4e-4 * den + 1e-12, (r0, float(np.linalg.norm(d)) / den)
