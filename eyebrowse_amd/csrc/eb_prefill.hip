@@ -79,6 +79,12 @@ __device__ __forceinline__ float sub_f16_hi(unsigned h2, float x) {
     return d;
 }
 
+// 1: the f16 mode without key splits stores its output from registers and runs three
+// waves per SIMD (FAST3, below); 0: the output goes through an LDS tile, two waves per SIMD.
+#ifndef EB_PREFILL_FAST_OCC
+#define EB_PREFILL_FAST_OCC 1
+#endif
+
 constexpr int kTile = 32;  // keys per tile, queries per wave
 constexpr size_t kLdsBytesPerCu = 160 * 1024;  // gfx950 LDS per CU
 constexpr float kSlack = 8.0f;  // log2 units the reference max may lag a score (SPV)
@@ -129,6 +135,11 @@ struct PrefillCfg {
     static constexpr int PSN = PS_IMAGE ? 1 : (PS_KV + THREADS - 1) / THREADS + 1;  // + exps
     // f16-mode records (head_dim <= 128): K rows [32][HD halves] then V^T [HD][32 halves],
     // rounded once by the pre-convert pass; a step copies KSPLIT records through registers.
+    // The f16 mode's LDS buffer holds only hi halves: K rows of HD halves at a stride of
+    // FKS floats (4 dwords past a multiple of 32, the bank spread of KS), then V^T
+    // [HD][VROW] halves.
+    static constexpr int FKS = (HD / 2 + 31) / 32 * 32 + 4;
+    static constexpr int FBUF = (STEP_KEYS * FKS + HD * VROW / 2 + 255) / 256 * 256;
     static constexpr int FPS_CH = 8 * HD;                // chunks per record
     static constexpr int FPS_FLOATS = 4 * FPS_CH;
     static constexpr int FPS_KV = KSPLIT * FPS_CH;       // chunks per step
@@ -141,6 +152,12 @@ struct PrefillCfg {
         (2 * BUF > MERGE ? 2 * BUF : MERGE) > OUT ? (2 * BUF > MERGE ? 2 * BUF : MERGE) : OUT;
     static constexpr size_t LDS_BYTES = (size_t)LDS_FLOATS * sizeof(float);
 };
+
+// K row stride and buffer size (floats) of the mode's LDS layout (FAST: hi halves only).
+template <class C, bool FAST>
+constexpr int kstride() { return FAST ? C::FKS : C::KS; }
+template <class C, bool FAST>
+constexpr int bufsize() { return FAST ? C::FBUF : C::BUF; }
 
 // Fetch the K and V rows [kb, kb + STEP_KEYS) of KV head kvh into registers; rows past
 // T read as zero. Every element is assigned on every call (clamped addresses, selected
@@ -240,8 +257,9 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                                                    const f32x4 (&rv)[C::NLD], int buf,
                                                    int tid) {
     constexpr int HD = C::HD_;
-    float *Kb = smem + buf * C::BUF;
-    float *Vb = Kb + C::STEP_KEYS * C::KS;
+    constexpr int KSX = kstride<C, FAST>();
+    float *Kb = smem + buf * bufsize<C, FAST>();
+    float *Vb = Kb + C::STEP_KEYS * KSX;
     int *Eb = reinterpret_cast<int *>(Vb + C::VFL);
     int *Ev = Eb + C::STEP_KEYS;
 #pragma unroll
@@ -252,7 +270,7 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
         if constexpr (C::SQK) {
             // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32)
             const f32x4 x = rk[r];
-            _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * C::KS);
+            _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * KSX);
             if constexpr (FAST) {
                 *reinterpret_cast<f16x4 *>(kr + c4 * 4) = __builtin_convertvector(x, f16x4);
             } else {
@@ -413,14 +431,15 @@ __device__ __forceinline__ void ps_store_step(float *smem, const f32x4 (&r)[C::P
             r[C::PSN - 1];
 }
 
-// Float offset, inside one LDS buffer of C, of chunk w of tile kt's f16-mode record: the
-// hi halves prefill_store_step<C, true> writes for that tile (K rows, then V^T rows).
+// Float offset, inside one f16-mode LDS buffer of C, of chunk w of tile kt's f16-mode
+// record: the halves prefill_store_step<C, true> writes for that tile (K rows, then V^T
+// rows).
 template <class C>
 __device__ __forceinline__ int fps_lds_offset(int kt, int w) {
     constexpr int HD = C::HD_;
-    if (w < 4 * HD) return (kt * kTile + w / (HD / 8)) * C::KS + 4 * (w % (HD / 8));
+    if (w < 4 * HD) return (kt * kTile + w / (HD / 8)) * C::FKS + 4 * (w % (HD / 8));
     const int w2 = w - 4 * HD;
-    return C::STEP_KEYS * C::KS + (w2 / 4) * (C::VROW / 2) + kt * (kTile / 2) + 4 * (w2 % 4);
+    return C::STEP_KEYS * C::FKS + (w2 / 4) * (C::VROW / 2) + kt * (kTile / 2) + 4 * (w2 % 4);
 }
 
 template <class C>
@@ -449,7 +468,7 @@ template <class C>
 __device__ __forceinline__ void fps_store_step(float *smem, const f32x4 (&r)[C::FPSN], int buf,
                                                int tid) {
     constexpr int HD = C::HD_;
-    float *B = smem + buf * C::BUF;
+    float *B = smem + buf * C::FBUF;
 #pragma unroll
     for (int i = 0; i < C::FPSN; ++i) {
         const int c = tid + i * C::THREADS;
@@ -473,7 +492,7 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void preconvert_kernel(
     int Hkv, int nt, int hdr) {
     using C = PresplitCfg<HD>;
     static_assert(HD <= 128, "f16-mode records for head_dim <= 128");
-    __shared__ float smem[C::BUF];
+    __shared__ float smem[C::FBUF];
     const int t = blockIdx.x;
     const int kvh = blockIdx.y;
     const int tid = threadIdx.x;
@@ -559,20 +578,32 @@ __device__ __forceinline__ void wait_vm_all() {
 // f16 once and each product is one f16 MFMA (instead of three on exact hi/lo splits); the
 // online softmax, its rescaling and the accumulation stay f32.
 //
-// Occupancy: the dynamic LDS the launch asks for (LDS_BYTES) bounds the waves per SIMD;
-// the compiler, which does not see it, is told that bound, so that it does not trade the
-// schedule for an occupancy the LDS never allows. 4-wave workgroups at head_dim <= 128 run
-// two per CU, so at least two waves per SIMD.
-template <int HD, int HPW, int WPH, int KSPLIT>
+// Occupancy: the dynamic LDS the launch asks for (prefill_lds_bytes) bounds the waves per
+// SIMD; the compiler, which does not see it, is told that bound, so that it does not trade
+// the schedule for an occupancy the LDS never allows. 4-wave workgroups at head_dim <= 128
+// run two per CU, so at least two waves per SIMD; the f16 mode over pre-converted records
+// without key splits (FAST3) three: its LDS (two hi-half buffers, output stored from
+// registers) allows four such workgroups per CU, and its registers fit 168.
+template <class C, bool FAST>
+constexpr bool direct_out() { return FAST && C::STEP_KEYS == kTile && EB_PREFILL_FAST_OCC; }
+template <class C, bool FAST>
+constexpr size_t prefill_lds_bytes() {
+    constexpr int buf2 = 2 * bufsize<C, FAST>();
+    constexpr int out = direct_out<C, FAST>() ? 0 : C::OUT;
+    constexpr int a = buf2 > C::MERGE ? buf2 : C::MERGE;
+    return (size_t)(a > out ? a : out) * sizeof(float);
+}
+template <int HD, int HPW, int WPH, int KSPLIT, bool FAST, bool PS>
 constexpr int prefill_min_waves() {
+    if (direct_out<PrefillCfg<HD, HPW, WPH, KSPLIT>, FAST>() && PS && HD <= 128) return 3;
     return (HPW * WPH * KSPLIT == 4 && HD <= 128) ? 2 : 1;
 }
-template <int HD, int HPW, int WPH, int KSPLIT>
+template <int HD, int HPW, int WPH, int KSPLIT, bool FAST, bool PS>
 constexpr int prefill_max_waves() {
-    constexpr size_t lds = PrefillCfg<HD, HPW, WPH, KSPLIT>::LDS_BYTES;
+    constexpr size_t lds = prefill_lds_bytes<PrefillCfg<HD, HPW, WPH, KSPLIT>, FAST>();
     constexpr int wgs = lds > 0 ? (int)(kLdsBytesPerCu / lds) : 8;
     constexpr int w = (wgs < 1 ? 1 : wgs) * HPW * WPH * KSPLIT / 4;
-    constexpr int lo = prefill_min_waves<HD, HPW, WPH, KSPLIT>();
+    constexpr int lo = prefill_min_waves<HD, HPW, WPH, KSPLIT, FAST, PS>();
     return w < lo ? lo : w > 8 ? 8 : w;
 }
 // PV1 (head_dim >= 32, with FAST false): the scores-accurate mode. The scores keep the
@@ -585,8 +616,8 @@ template <int HD, int HPW, int WPH, int KSPLIT, bool RANGE, int EB, bool PS, boo
           bool PV1 = false>
 __global__ __attribute__((
     amdgpu_flat_work_group_size(1, HPW * WPH * KSPLIT * 64),
-    amdgpu_waves_per_eu(prefill_min_waves<HD, HPW, WPH, KSPLIT>(),
-                        prefill_max_waves<HD, HPW, WPH, KSPLIT>()))) void prefill_kernel(
+    amdgpu_waves_per_eu(prefill_min_waves<HD, HPW, WPH, KSPLIT, FAST, PS>(),
+                        prefill_max_waves<HD, HPW, WPH, KSPLIT, FAST, PS>()))) void prefill_kernel(
     const float *__restrict__ q, const void *__restrict__ k, const void *__restrict__ v,
     const float *__restrict__ ps, int ps_tlo, int ps_nt, float *__restrict__ o, int H,
     int Hkv, int rows, int nkeys, int qbase, int window, float scale_log2, int nqb,
@@ -596,6 +627,8 @@ __global__ __attribute__((
     constexpr int HALF = C::HALF;
     constexpr int NB = C::NB;
     constexpr int KS = C::KS;
+    constexpr int KSX = kstride<C, FAST>();   // K row stride and buffer size of this mode
+    constexpr int BUFX = bufsize<C, FAST>();
 
     extern __shared__ float smem[];  // [2][BUF]: K rows [STEP_KEYS][KS], V rows [STEP_KEYS][HD]
 
@@ -806,11 +839,11 @@ __global__ __attribute__((
         //           the P^T operands;
         //  pv:      O^T += V^T P^T from buffer b.
         auto tile_qk = [&](int b, floatx16 &sacc, int (&ek)[16]) {
-            const float *Kb = smem + b * C::BUF + ks * kTile * KS;
+            const float *Kb = smem + b * BUFX + ks * kTile * KSX;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
             // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
-            const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KS);
+            const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KSX);
 #pragma unroll
             for (int k2 = 0; k2 < NKS; ++k2) {
                 const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
@@ -861,7 +894,7 @@ __global__ __attribute__((
             float mt = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            mt = fmaxf(mt, eb::lane_xor32(mt));
             // Lazy reference max: m moves only when a score exceeds it by more than kSlack
             // (log2 units), so most tiles need no rescale of l and O^T; terms 2^(s - m) then
             // stay below 2^kSlack, which the f16 split holds exactly.
@@ -938,7 +971,7 @@ __global__ __attribute__((
                     tb = (int)t > (int)tb ? t : tb;
                 }
                 int tx = ((int)tb >> 23) - 126;
-                tx = max(tx, __shfl_xor(tx, 32));
+                tx = max(tx, __builtin_bit_cast(int, eb::lane_xor32(__builtin_bit_cast(float, tx))));
                 // The softmax correction 2^-(mref - mold) moves the accumulated terms down:
                 // the unit follows by whole bits, the fraction goes into the rescale factor.
                 // The unit moves up only for a term more than 2^kUnitSlack above it (then
@@ -978,7 +1011,7 @@ __global__ __attribute__((
         // 0..3 of this wave's tile (the order of ph / pl). FAST: the hi halves only.
         auto tile_pv = [&](int b, const f16x8 (&ph)[2], const f16x8 (&pl)[2]) {
             const _Float16 *vth =
-                reinterpret_cast<const _Float16 *>(smem + b * C::BUF + C::STEP_KEYS * KS);
+                reinterpret_cast<const _Float16 *>(smem + b * BUFX + C::STEP_KEYS * KSX);
             if constexpr (FAST || PV1) {
                 // f16 mode: the NB V fragments of one 16-key half are read first and the
                 // products go round the NB accumulators (measured 2-4 % faster than one
@@ -1079,7 +1112,7 @@ __global__ __attribute__((
             float mt = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) mt = fmaxf(mt, p[r]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            mt = fmaxf(mt, eb::lane_xor32(mt));
             const float mnew = fmaxf(m, mt);
             // A query can meet a tile with all of its keys masked before its first visible
             // key (unaligned chunk starts, windows): keep exp2 away from -inf - -inf.
@@ -1205,6 +1238,32 @@ __global__ __attribute__((
             *reinterpret_cast<float4 *>(part_ml + (((size_t)chunk * rows + qi) * H + head) * 4) =
                 make_float4(m, lt, __int_as_float(C::SPV ? E : 0), 0.0f);
         const float sc_o = C::SPV ? 1.0f : inv;
+        if constexpr (direct_out<C, FAST>()) {
+            // Straight from the registers: lane (col, hf) stores NB consecutive dims NB*c ..
+            // NB*c + NB - 1 of its query's row for each of its 16 values of c.
+            if (qi < rows) {
+                float *dst = partial ? part_acc + (size_t)chunk * rows * H * HD : o;
+                const int dstride = partial ? HD : hdr;
+                float *orow = dst + ((size_t)qi * H + head) * dstride;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int c = 8 * (r >> 2) + 4 * hf + (r & 3);
+                    if (NB * c >= dstride) continue;  // (dims past hdr: the padding)
+                    if constexpr (NB >= 4) {
+#pragma unroll
+                        for (int j = 0; j < NB / 4; ++j)
+                            *reinterpret_cast<float4 *>(orow + NB * c + 4 * j) =
+                                make_float4(oacc[4 * j][r], oacc[4 * j + 1][r],
+                                            oacc[4 * j + 2][r], oacc[4 * j + 3][r]);
+                    } else if constexpr (NB == 2) {
+                        *reinterpret_cast<float2 *>(orow + 2 * c) = make_float2(oacc[0][r], oacc[1][r]);
+                    } else {
+                        orow[c] = oacc[0][r];
+                    }
+                }
+            }
+            return;
+        }
         float *orow = ot + col * C::OS;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -1226,6 +1285,7 @@ __global__ __attribute__((
             }
         }
     }
+    if constexpr (direct_out<C, FAST>()) return;
     __syncthreads();
     if (ks == 0 && live) {
         // o rows hold hdr dims; the partials keep the instantiation's HD
@@ -1528,14 +1588,15 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
         attr_err = hipFuncSetAttribute(
             reinterpret_cast<const void *>(
                 &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::LDS_BYTES);
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)prefill_lds_bytes<C, FAST>());
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
     const int g = H / Hkv;
     const int ngroups = Hkv * (g / HPW);
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const dim3 grid((unsigned)(nqb * ngroups), (unsigned)ch.nchmax);
-    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1><<<grid, C::THREADS, C::LDS_BYTES, st>>>(
+    prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1>
+        <<<grid, C::THREADS, prefill_lds_bytes<C, FAST>(), st>>>(
         q, k, v, ps, presplit_tlo(r), presplit_nt(r), o, H, Hkv, r.rows, r.nkeys, r.qbase,
         r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml, r.hdr);
     eb_status err = eb::check_launch("attn_prefill");
@@ -1697,6 +1758,20 @@ size_t fast_workspace_floats(size_t hp, int H, int Hkv, int s) {
     return (size_t)Hkv * nt * rec;
 }
 
+// FAST3 (4-wave workgroups without a key split, three per CU) where the grid fills at least
+// one round of those slots; below, the causal triangle's longest blocks would leave CUs idle
+// (measured at Qwen T=4096, 512 workgroups: 560 -> 470 TFLOP/s; Mistral T=4096, 1024
+// workgroups: 673 -> 738), and the 8-wave key-split shape stays.
+constexpr int kFast3PerCu = 3;
+bool fast3_shape(size_t hp, int H, int Hkv, int rows) {
+    if (!EB_PREFILL_FAST_OCC || hp > 128) return false;
+    const int g = H / Hkv;
+    const int hpw = g % 4 == 0 ? 4 : g % 2 == 0 ? 2 : 1;
+    const long qb_rows = (long)kTile * (4 / hpw);
+    const long blocks = (rows + qb_rows - 1) / qb_rows * (long)Hkv * (g / hpw);
+    return blocks >= (long)kFast3PerCu * kPrefillSlots;
+}
+
 template <int HD, int HPW, int WPH, int KSPLIT>
 eb_status launch_prefill_fast_t(hipStream_t st, const float *q, const float *k, const float *v,
                                 float *o, int H, int Hkv, const PrefillRange &r, float sl2) {
@@ -1721,6 +1796,11 @@ eb_status launch_prefill_fast_hd(hipStream_t st, const float *q, const float *k,
                                  float *o, int H, int Hkv, const PrefillRange &r, float sl2) {
     const int g = H / Hkv;
     constexpr int KSPLIT = HD <= 128 ? 2 : 1;
+    if (fast3_shape(HD, H, Hkv, r.rows)) {  // FAST3: no key split, three per CU
+        if (g % 4 == 0) return launch_prefill_fast_t<HD, 4, 1, 1>(st, q, k, v, o, H, Hkv, r, sl2);
+        if (g % 2 == 0) return launch_prefill_fast_t<HD, 2, 2, 1>(st, q, k, v, o, H, Hkv, r, sl2);
+        return launch_prefill_fast_t<HD, 1, 4, 1>(st, q, k, v, o, H, Hkv, r, sl2);
+    }
     if (g % 4 == 0) {  // (the accurate path's choice, prefill_shape)
         if (KSPLIT == 2 && prefill_shape(HD, H, g, r.rows).ksplit == 2)
             return launch_prefill_fast_t<HD, 4, 1, KSPLIT>(st, q, k, v, o, H, Hkv, r, sl2);
