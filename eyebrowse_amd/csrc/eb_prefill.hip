@@ -135,15 +135,17 @@ struct PrefillCfg {
     static constexpr int PSN = PS_IMAGE ? 1 : (PS_KV + THREADS - 1) / THREADS + 1;  // + exps
     // f16-mode records (head_dim <= 128): K rows [32][HD halves] then V^T [HD][32 halves],
     // rounded once by the pre-convert pass; a step copies KSPLIT records through registers.
-    // The f16 mode's LDS buffer holds only hi halves: K rows of HD halves at a stride of
-    // FKS floats (4 dwords past a multiple of 32, the bank spread of KS), then V^T
-    // [HD][VROW] halves.
-    static constexpr int FKS = (HD / 2 + 31) / 32 * 32 + 4;
-    static constexpr int FBUF = (STEP_KEYS * FKS + HD * VROW / 2 + 255) / 256 * 256;
-    static constexpr int FPS_CH = 8 * HD;                // chunks per record
-    static constexpr int FPS_FLOATS = 4 * FPS_CH;
-    static constexpr int FPS_KV = KSPLIT * FPS_CH;       // chunks per step
-    static constexpr int FPSN = (FPS_KV + THREADS - 1) / THREADS;
+    // f16 mode (hi halves only): a buffer holds KSPLIT tile images of FIMG floats, each a
+    // K part and a V^T part of 16-byte chunks (8 halves) laid out chunk-major: K chunk c
+    // (dims 8c .. 8c + 7) of key r at chunk c * 32 + r, V^T chunk c (keys 8c .. 8c + 7 in
+    // the permuted key order) of V^T row p at 4 HD + c * HD + p (fk_chunk, fv_chunk). An
+    // MFMA operand read then takes 256 contiguous bytes per 16 lanes (no bank conflict,
+    // no padding) at offsets that are immediates. The f16-mode records (head_dim <= 128)
+    // are these images, copied into LDS with memory-to-LDS loads.
+    static constexpr int FIMG = 32 * HD;
+    static constexpr int FBUF = (STEP_KEYS / kTile) * FIMG;
+    static constexpr int FPS_CH = FIMG / 4;              // chunks per record
+    static constexpr int FPS_FLOATS = FIMG;
     static constexpr int REC = 3 + 16 * NB;  // merged fields per lane: m, l, V unit, O^T
     static constexpr int MERGE = (KSPLIT - 1) * HPW * WPH * REC * 64;  // floats
     static constexpr int OS = HD + 4;                  // output staging row stride (floats)
@@ -153,11 +155,16 @@ struct PrefillCfg {
     static constexpr size_t LDS_BYTES = (size_t)LDS_FLOATS * sizeof(float);
 };
 
-// K row stride and buffer size (floats) of the mode's LDS layout (FAST: hi halves only).
-template <class C, bool FAST>
-constexpr int kstride() { return FAST ? C::FKS : C::KS; }
+// Buffer size (floats) of the mode's LDS layout (FAST: tile images of hi halves).
 template <class C, bool FAST>
 constexpr int bufsize() { return FAST ? C::FBUF : C::BUF; }
+
+// f16-mode tile images: the 16-byte chunk index of chunk c of K row r (key r, dims 8c ..
+// 8c + 7), and of chunk c of V^T row p (keys 8c .. 8c + 7).
+template <int HD>
+__device__ __forceinline__ int fk_chunk(int r, int c) { return c * kTile + r; }
+template <int HD>
+__device__ __forceinline__ int fv_chunk(int p, int c) { return 4 * HD + c * HD + p; }
 
 // Fetch the K and V rows [kb, kb + STEP_KEYS) of KV head kvh into registers; rows past
 // T read as zero. Every element is assigned on every call (clamped addresses, selected
@@ -249,7 +256,7 @@ __device__ __forceinline__ void split_f16(f32x4 x, int e, f16x4 &hi, f16x4 &lo) 
 // [STEP_KEYS][HD], then (SQK) the K rows' exponents [STEP_KEYS]. With SQK a K row holds
 // its HD halves of hi, then HD halves of lo (the same KS floats).
 // FAST: rows are rounded to f16 as they are (no exponent, no lo halves, no exponent
-// arrays); the single-product mode below reads only the hi halves.
+// arrays) and written as the f16 mode's tile images (fk_chunk, fv_chunk).
 // V16 (with FAST false): K split as above, V rows rounded to f16 as they are, as FAST does
 // (the scores-accurate mode; its V^T lo halves and V exponents are not written).
 template <class C, bool FAST = false, bool V16 = false>
@@ -257,9 +264,8 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                                                    const f32x4 (&rv)[C::NLD], int buf,
                                                    int tid) {
     constexpr int HD = C::HD_;
-    constexpr int KSX = kstride<C, FAST>();
     float *Kb = smem + buf * bufsize<C, FAST>();
-    float *Vb = Kb + C::STEP_KEYS * KSX;
+    float *Vb = Kb + C::STEP_KEYS * C::KS;
     int *Eb = reinterpret_cast<int *>(Vb + C::VFL);
     int *Ev = Eb + C::STEP_KEYS;
 #pragma unroll
@@ -270,9 +276,12 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
         if constexpr (C::SQK) {
             // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32)
             const f32x4 x = rk[r];
-            _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * KSX);
+            _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * C::KS);
             if constexpr (FAST) {
-                *reinterpret_cast<f16x4 *>(kr + c4 * 4) = __builtin_convertvector(x, f16x4);
+                // tile row / 32, row row % 32: halves 4 c4 .. 4 c4 + 3 are half a chunk
+                _Float16 *img = reinterpret_cast<_Float16 *>(Kb + (row / kTile) * C::FIMG);
+                *reinterpret_cast<f16x4 *>(img + fk_chunk<HD>(row % kTile, c4 / 2) * 8 +
+                                           (c4 & 1) * 4) = __builtin_convertvector(x, f16x4);
             } else {
                 const float m4 =
                     fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
@@ -312,7 +321,13 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     for (int i = 0; i < 4; ++i) {
                         const int d = c4 * 4 + i;
                         const int pr = (d % C::NB) * 32 + d / C::NB;
-                        vth16[pr * C::VROW + js] = vh[i];
+                        if constexpr (FAST) {
+                            _Float16 *img =
+                                reinterpret_cast<_Float16 *>(Kb + (js / kTile) * C::FIMG);
+                            img[fv_chunk<HD>(pr, (js % kTile) / 8) * 8 + js % 8] = vh[i];
+                        } else {
+                            vth16[pr * C::VROW + js] = vh[i];
+                        }
                         if constexpr (!FAST && !V16) vtl16[pr * C::VROW + js] = vl[i];
                     }
                 } else {
@@ -337,7 +352,13 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     const _Float16 he = odd ? vh2[i] : vh[i], ho2 = odd ? vh[i] : vh2[i];
                     const _Float16 le = odd ? vl2[i] : vl[i], lo2 = odd ? vl[i] : vl2[i];
                     using h2 = __attribute__((ext_vector_type(2))) _Float16;
-                    vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
+                    if constexpr (FAST) {
+                        unsigned *img = reinterpret_cast<unsigned *>(Kb + (j0 / kTile) * C::FIMG);
+                        img[fv_chunk<HD>(pr, (j0 % kTile) / 8) * 4 + (j0 % 8) / 2] =
+                            __builtin_bit_cast(unsigned, h2{he, ho2});
+                    } else {
+                        vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
+                    }
                     if constexpr (!FAST && !V16)
                         vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
                 }
@@ -431,50 +452,30 @@ __device__ __forceinline__ void ps_store_step(float *smem, const f32x4 (&r)[C::P
             r[C::PSN - 1];
 }
 
-// Float offset, inside one f16-mode LDS buffer of C, of chunk w of tile kt's f16-mode
-// record: the halves prefill_store_step<C, true> writes for that tile (K rows, then V^T
-// rows).
+// Copy the f16-mode records of tiles tile0 .. tile0 + KSPLIT - 1 (each clamped to the last
+// record, nt - 1: a clamped image is never read) of one KV head (recs) into LDS buffer
+// `buf` with memory-to-LDS loads, as ps_copy_image does (complete after wait_vm_all()):
+// wave w moves the buffer's KiB blocks w * BPW .. w * BPW + BPW - 1, one image's, each
+// load's immediate offset applying to both its global and its LDS address.
 template <class C>
-__device__ __forceinline__ int fps_lds_offset(int kt, int w) {
-    constexpr int HD = C::HD_;
-    if (w < 4 * HD) return (kt * kTile + w / (HD / 8)) * C::FKS + 4 * (w % (HD / 8));
-    const int w2 = w - 4 * HD;
-    return C::STEP_KEYS * C::FKS + (w2 / 4) * (C::VROW / 2) + kt * (kTile / 2) + 4 * (w2 % 4);
-}
-
-template <class C>
-__device__ __forceinline__ void fps_load_step(const f32x4 *__restrict__ recs,
-                                              f32x4 (&r)[C::FPSN], int tile0, int nt, int tid) {
-    constexpr int HD = C::HD_;
-    if constexpr ((8 * HD) % C::THREADS == 0) {
-        constexpr int PER = 8 * HD / C::THREADS;  // (as in ps_load_step)
-        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::FPS_CH);
+__device__ __forceinline__ void fps_copy(const float *__restrict__ recs, float *smem, int buf,
+                                         int tile0, int nt, int wave, int lane) {
+    constexpr int BLK = C::FIMG / 256;                       // KiB blocks per image
+    constexpr int BPW = (C::STEP_KEYS / kTile) * BLK / C::NW;  // blocks per wave
+    static_assert(BPW >= 1 && BLK % BPW == 0 && BPW * 1024 <= 4096,
+                  "a wave's blocks lie in one image, within the loads' offset range");
+    const int j0 = wave * BPW;
+    const int t = min(tile0 + j0 / BLK, nt - 1);
+    const float *src = recs + (size_t)t * C::FIMG + (j0 % BLK) * 256 + lane * 4;
+    const unsigned dst = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)(__attribute__((address_space(3))) float *)(smem + buf * C::FBUF +
+                                                                          j0 * 256));
 #pragma unroll
-        for (int i = 0; i < C::FPSN; ++i) {
-            r[i] = chunk_load(rs, tid,
-                              min(tile0 + i / PER, nt - 1) * C::FPS_CH + (i % PER) * C::THREADS);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < C::FPSN; ++i) {
-            const int c = min(tid + i * C::THREADS, C::FPS_KV - 1);
-            const int t = min(tile0 + c / (8 * HD), nt - 1);
-            r[i] = recs[(size_t)t * C::FPS_CH + c % (8 * HD)];
-        }
-    }
-}
-
-template <class C>
-__device__ __forceinline__ void fps_store_step(float *smem, const f32x4 (&r)[C::FPSN], int buf,
-                                               int tid) {
-    constexpr int HD = C::HD_;
-    float *B = smem + buf * C::FBUF;
-#pragma unroll
-    for (int i = 0; i < C::FPSN; ++i) {
-        const int c = tid + i * C::THREADS;
-        if (C::FPS_KV % C::THREADS == 0 || c < C::FPS_KV)
-            *reinterpret_cast<f32x4 *>(B + fps_lds_offset<C>(c / (8 * HD), c % (8 * HD))) = r[i];
-    }
+    for (int i = 0; i < BPW; ++i)
+        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off offset:%2"
+                     :
+                     : "s"(dst), "v"(src), "i"(1024 * i)
+                     : "memory", "m0");
 }
 
 // The pre-split and pre-convert passes' shape: one 32-key tile per workgroup (the records'
@@ -500,9 +501,10 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void preconvert_kernel(
     prefill_load_step<C, 4>(k, v, rk, rv, t * kTile, nkeys, Hkv, kvh, tid, hdr);
     prefill_store_step<C, true>(smem, rk, rv, 0, tid);
     __syncthreads();
+    // (the tile image is the record)
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::FPS_FLOATS);
     for (int c = tid; c < C::FPS_CH; c += C::THREADS)
-        rec[c] = *reinterpret_cast<const f32x4 *>(smem + fps_lds_offset<C>(0, c));
+        rec[c] = reinterpret_cast<const f32x4 *>(smem)[c];
 }
 
 // Pre-split pass: workgroup (t, kvh) splits keys [(tlo + t) * 32, +32) of KV head kvh
@@ -627,8 +629,7 @@ __global__ __attribute__((
     constexpr int HALF = C::HALF;
     constexpr int NB = C::NB;
     constexpr int KS = C::KS;
-    constexpr int KSX = kstride<C, FAST>();   // K row stride and buffer size of this mode
-    constexpr int BUFX = bufsize<C, FAST>();
+    constexpr int BUFX = bufsize<C, FAST>();  // LDS buffer size of this mode
 
     extern __shared__ float smem[];  // [2][BUF]: K rows [STEP_KEYS][KS], V rows [STEP_KEYS][HD]
 
@@ -678,12 +679,12 @@ __global__ __attribute__((
     // right behind the q fragment's, so that the two latencies overlap.
     f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
     static_assert(!(PS && FAST && C::PS_IMAGE), "f16-mode records for head_dim <= 128");
-    f32x4 rs[PS ? (FAST ? C::FPSN : C::PSN) : 1];
+    f32x4 rs[PS && !FAST ? C::PSN : 1];
     const float *recs =
         PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
     auto load_first_step = [&] {
         if constexpr (PS && FAST)
-            fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+            fps_copy<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
         else if constexpr (PS && C::PS_IMAGE)
             ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
         else if constexpr (PS)
@@ -710,21 +711,25 @@ __global__ __attribute__((
         // instantiation) are zeros. A head dim that is an odd multiple of 8 ends halfway
         // into its last 16-dim step: there the upper half-wave (dims +8..+15) reads the
         // lower half's address (inside the row) and keeps zeros.
+        if (hdr == HD) {  // (uniform) the instantiation's own head dim
 #pragma unroll
-        for (int k2 = 0; k2 < NKS; ++k2) {
-            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (16 * k2 + 16 <= hdr) {  // (uniform)
+            for (int k2 = 0; k2 < NKS; ++k2) {
                 qa[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2);
                 qb[k2] = *reinterpret_cast<const f32x4 *>(qp + 16 * k2 + 4);
-            } else if (16 * k2 < hdr) {  // (uniform) hdr = 16 k2 + 8
-                const float *qe = qp + 16 * k2 - 8 * hf;
+            }
+        } else {
+#pragma unroll
+            for (int k2 = 0; k2 < NKS; ++k2) {
+                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const bool full = 16 * k2 + 16 <= hdr;     // (uniform)
+                const bool half = !full && 16 * k2 < hdr;  // (uniform) hdr = 16 k2 + 8
+                // one load pair per step (a step wholly past hdr reads the row's start)
+                const float *qe = full ? qp + 16 * k2 : half ? qp + 16 * k2 - 8 * hf : qp;
                 const f32x4 a = *reinterpret_cast<const f32x4 *>(qe);
                 const f32x4 b = *reinterpret_cast<const f32x4 *>(qe + 4);
-                qa[k2] = hf ? z : a;
-                qb[k2] = hf ? z : b;
-            } else {
-                qa[k2] = z;
-                qb[k2] = z;
+                const bool keep = full || (half && !hf);
+                qa[k2] = keep ? a : z;
+                qb[k2] = keep ? b : z;
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -794,9 +799,7 @@ __global__ __attribute__((
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     // ... and the first step's K/V into LDS.
-    if constexpr (PS && FAST)
-        fps_store_step<C>(smem, rs, 0, tid);
-    else if constexpr (PS && C::PS_IMAGE)
+    if constexpr (PS && (FAST || C::PS_IMAGE))
         wait_vm_all();
     else if constexpr (PS)
         ps_store_step<C>(smem, rs, 0, tid);
@@ -804,14 +807,13 @@ __global__ __attribute__((
         prefill_store_step<C, FAST, PV1>(smem, rk, rv, 0, tid);
     __syncthreads();
 
-    // The next step's K/V: PS records into registers (or, head_dim 256, straight into the
-    // other buffer, which every wave finished reading before the last barrier); otherwise
-    // K/V rows into registers. Past the last step this re-reads clamped rows (the buffer
+    // The next step's K/V: PS records into registers (or, head_dim 256 and the f16 mode's
+    // images, straight into the other buffer, which every wave finished reading before the
+    // last barrier); otherwise K/V rows into registers. Past the last step this re-reads clamped rows (the buffer
     // written from them is never read).
     auto prefetch = [&](int it1, int b1) {
         if constexpr (PS && FAST)
-            fps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
-                             c_lo + it1 * KSPLIT - ps_tlo, ps_nt, tid);
+            fps_copy<C>(recs, smem, b1, c_lo + it1 * KSPLIT - ps_tlo, ps_nt, wave, lane);
         else if constexpr (PS && C::PS_IMAGE)
             ps_copy_image<C>(recs, smem, b1, c_lo + it1 * KSPLIT - ps_tlo, ps_nt, wave, lane);
         else if constexpr (PS)
@@ -822,9 +824,7 @@ __global__ __attribute__((
                                       kvh, tid, hdr);
     };
     auto stage = [&](int b1) {
-        if constexpr (PS && FAST)
-            fps_store_step<C>(smem, rs, b1, tid);
-        else if constexpr (PS && C::PS_IMAGE)
+        if constexpr (PS && (FAST || C::PS_IMAGE))
             wait_vm_all();
         else if constexpr (PS)
             ps_store_step<C>(smem, rs, b1, tid);
@@ -839,17 +839,42 @@ __global__ __attribute__((
         //           the P^T operands;
         //  pv:      O^T += V^T P^T from buffer b.
         auto tile_qk = [&](int b, floatx16 &sacc, int (&ek)[16]) {
-            const float *Kb = smem + b * BUFX + ks * kTile * KSX;
+            const float *Kb = smem + b * BUFX + ks * kTile * KS;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
             // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
-            const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KSX);
+            const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KS);
+            // FAST: chunk 2 k2 + hf of key col in tile ks's image
+            const _Float16 *kimg = reinterpret_cast<const _Float16 *>(smem + b * BUFX + ks * C::FIMG) +
+                                   8 * fk_chunk<HD>(col, hf);
+            if constexpr (FAST && NKS <= 8) {
+                // All of the tile's K operands are read before the first product (the
+                // compiler would otherwise wait out each read's latency before its product).
+                f16x8 ka[NKS];
 #pragma unroll
-            for (int k2 = 0; k2 < NKS; ++k2) {
-                const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
-                sacc = mfma16(ah, qh[k2], sacc);
-                if constexpr (!FAST) {
-                    const f16x8 al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                for (int k2 = 0; k2 < NKS; ++k2)
+                    ka[k2] = *reinterpret_cast<const f16x8 *>(kimg + 8 * 2 * kTile * k2);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k2 = 0; k2 < NKS; ++k2) sacc = mfma16(ka[k2], qh[k2], sacc);
+            } else if constexpr (FAST) {  // (head_dim 256: no registers for that)
+#pragma unroll
+                for (int k2 = 0; k2 < NKS; ++k2)
+                    sacc = mfma16(*reinterpret_cast<const f16x8 *>(kimg + 8 * 2 * kTile * k2),
+                                  qh[k2], sacc);
+            } else {
+                // (both operands read before the products with key splits, the lo operand
+                // after the first product without: the orders that leave the staged
+                // kernels at head_dim 128 without a register spill)
+#pragma unroll
+                for (int k2 = 0; k2 < NKS; ++k2) {
+                    const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
+                    f16x8 al;
+                    if constexpr (KSPLIT > 1)
+                        al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                    sacc = mfma16(ah, qh[k2], sacc);
+                    if constexpr (KSPLIT == 1)
+                        al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
                     sacc = mfma16(ah, ql[k2], sacc);
                     sacc = mfma16(al, qh[k2], sacc);
                 }
@@ -1011,7 +1036,10 @@ __global__ __attribute__((
         // 0..3 of this wave's tile (the order of ph / pl). FAST: the hi halves only.
         auto tile_pv = [&](int b, const f16x8 (&ph)[2], const f16x8 (&pl)[2]) {
             const _Float16 *vth =
-                reinterpret_cast<const _Float16 *>(smem + b * BUFX + C::STEP_KEYS * KSX);
+                reinterpret_cast<const _Float16 *>(smem + b * BUFX + C::STEP_KEYS * KS);
+            // FAST: chunk hf + 2u of V^T row 32 mb + col in tile ks's image
+            const _Float16 *vimg = reinterpret_cast<const _Float16 *>(smem + b * BUFX + ks * C::FIMG) +
+                                   8 * fv_chunk<HD>(col, hf);
             if constexpr (FAST || PV1) {
                 // f16 mode: the NB V fragments of one 16-key half are read first and the
                 // products go round the NB accumulators (measured 2-4 % faster than one
@@ -1022,8 +1050,10 @@ __global__ __attribute__((
                     f16x8 vh[NB];
 #pragma unroll
                     for (int mb = 0; mb < NB; ++mb)
-                        vh[mb] = *reinterpret_cast<const f16x8 *>(
-                            vth + (32 * mb + col) * C::VROW + ks * kTile + 8 * hf + 16 * u);
+                        vh[mb] = FAST ? *reinterpret_cast<const f16x8 *>(
+                                            vimg + 8 * (2 * u * HD + 32 * mb))
+                                      : *reinterpret_cast<const f16x8 *>(
+                                            vth + (32 * mb + col) * C::VROW + ks * kTile + 8 * hf + 16 * u);
 #pragma unroll
                     for (int mb = 0; mb < NB; ++mb) oacc[mb] = mfma16(vh[mb], ph[u], oacc[mb]);
                 }
