@@ -113,28 +113,22 @@ struct PrefillCfg {
     // head_dim >= 32: Q K^T on the f16 matrix cores with an exact hi/lo split (K rows and
     // Q rows scaled by powers of two first); smaller head dims keep FP32 MFMA throughout.
     static constexpr bool SQK = HD >= 32;
-    // V^T P^T the same way (V rows scaled and split at staging, stored transposed as
-    // [HD][VROW] halves, hi then lo; P scaled per key and split in registers).
+    // V^T P^T the same way (V rows scaled and split at staging, stored transposed, hi
+    // then lo halves; P scaled per key and split in registers).
     static constexpr bool SPV = HD >= 32;
-    static constexpr int VROW = STEP_KEYS + 8;  // halves per V^T row (16-byte aligned reads
-                                                // of consecutive rows spread over the banks)
-    static constexpr int VFL = SPV ? HD * VROW : STEP_KEYS * HD;  // floats of V per buffer
-    // + K and V exponents; whole KiB, so that a buffer takes memory-to-LDS copies exactly
-    static constexpr int BUF = (STEP_KEYS * KS + VFL + 2 * STEP_KEYS + 255) / 256 * 256;
-    // Pre-split K/V (SPV): one record per (KV head, 32-key tile).
-    //  - head_dim <= 128: 16-byte chunks K rows [32][HD floats of hi then lo halves], V^T hi
-    //    [HD][32 halves], V^T lo, K exponents [32], V exponents [32]; a step copies KSPLIT
-    //    records into LDS through registers.
-    //  - head_dim 256 (one key split, so a step's buffer is one tile): the buffer's LDS
-    //    image itself, copied with memory-to-LDS loads (the register copy would hold 68
-    //    VGPRs where the split already fills the register file).
-    static constexpr bool PS_IMAGE = HD > 128;
-    static constexpr int PS_CH = 16 * HD + 16;          // chunks per record
-    static constexpr int PS_FLOATS = PS_IMAGE ? BUF : 4 * PS_CH;  // floats per record
-    static constexpr int PS_KV = KSPLIT * 16 * HD;      // K/V chunks per step
-    static constexpr int PSN = PS_IMAGE ? 1 : (PS_KV + THREADS - 1) / THREADS + 1;  // + exps
-    // f16-mode records (head_dim <= 128): K rows [32][HD halves] then V^T [HD][32 halves],
-    // rounded once by the pre-convert pass; a step copies KSPLIT records through registers.
+    // Split tile images (SPV): 16-byte chunks laid out chunk-major (sk_chunk, sv_chunk): K
+    // hi chunk c (dims 8c .. 8c + 7) of key r at c * 32 + r, the K lo chunks 4 HD on; V^T hi
+    // chunk c (keys 8c .. 8c + 7 in the permuted key order) of V^T row p at 8 HD + c * HD +
+    // p, the V^T lo chunks 4 HD on; then the K exponents [32] and V exponents [32] at float
+    // EXPO; whole KiB. An MFMA operand read then takes 256 contiguous bytes per 16 lanes (no
+    // bank conflict) at immediate offsets. A buffer holds KSPLIT images; a pre-split record
+    // is one image, copied into LDS with memory-to-LDS loads.
+    static constexpr int EXPO = 64 * HD;
+    static constexpr int IMG = SPV ? (64 * HD + 64 + 255) / 256 * 256 : 0;
+    // head_dim < 32: K rows [STEP_KEYS][KS] and V rows [STEP_KEYS][HD], f32; whole KiB
+    static constexpr int BUF =
+        SPV ? KSPLIT * IMG : (STEP_KEYS * KS + STEP_KEYS * HD + 255) / 256 * 256;
+    static constexpr int PS_FLOATS = IMG;  // floats per pre-split record
     // f16 mode (hi halves only): a buffer holds KSPLIT tile images of FIMG floats, each a
     // K part and a V^T part of 16-byte chunks (8 halves) laid out chunk-major: K chunk c
     // (dims 8c .. 8c + 7) of key r at chunk c * 32 + r, V^T chunk c (keys 8c .. 8c + 7 in
@@ -165,6 +159,14 @@ template <int HD>
 __device__ __forceinline__ int fk_chunk(int r, int c) { return c * kTile + r; }
 template <int HD>
 __device__ __forceinline__ int fv_chunk(int p, int c) { return 4 * HD + c * HD + p; }
+// Split tile images: the same for the hi (lo = 0) or lo (lo = 1) halves.
+template <int HD>
+__device__ __forceinline__ int sk_chunk(int r, int c, int lo) { return lo * 4 * HD + c * kTile + r; }
+template <int HD>
+__device__ __forceinline__ int sv_chunk(int p, int c, int lo) { return (8 + 4 * lo) * HD + c * HD + p; }
+// Image size of the mode (floats).
+template <class C, bool FAST>
+constexpr int imgsize() { return FAST ? C::FIMG : C::IMG; }
 
 // Fetch the K and V rows [kb, kb + STEP_KEYS) of KV head kvh into registers; rows past
 // T read as zero. Every element is assigned on every call (clamped addresses, selected
@@ -252,9 +254,10 @@ __device__ __forceinline__ void split_f16(f32x4 x, int e, f16x4 &hi, f16x4 &lo) 
     lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x4), f16x4);
 }
 
-// Write the staged rows into LDS buffer `buf`: K rows [STEP_KEYS][KS], then V rows
-// [STEP_KEYS][HD], then (SQK) the K rows' exponents [STEP_KEYS]. With SQK a K row holds
-// its HD halves of hi, then HD halves of lo (the same KS floats).
+// Write the staged rows into LDS buffer `buf`. SQK (head_dim >= 32): the split tile images
+// (K rows scaled by their exponents and split into f16 hi and lo halves, V rows likewise
+// and transposed, then both exponent arrays); otherwise f32 K rows [STEP_KEYS][KS], then
+// V rows [STEP_KEYS][HD].
 // FAST: rows are rounded to f16 as they are (no exponent, no lo halves, no exponent
 // arrays) and written as the f16 mode's tile images (fk_chunk, fv_chunk).
 // V16 (with FAST false): K split as above, V rows rounded to f16 as they are, as FAST does
@@ -264,24 +267,24 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                                                    const f32x4 (&rv)[C::NLD], int buf,
                                                    int tid) {
     constexpr int HD = C::HD_;
+    constexpr int IMGX = imgsize<C, FAST>();
     float *Kb = smem + buf * bufsize<C, FAST>();
-    float *Vb = Kb + C::STEP_KEYS * C::KS;
-    int *Eb = reinterpret_cast<int *>(Vb + C::VFL);
-    int *Ev = Eb + C::STEP_KEYS;
 #pragma unroll
     for (int r = 0; r < C::NLD; ++r) {
         const int idx = tid + r * C::THREADS;
         const int row = idx / (HD / 4);
         const int c4 = idx % (HD / 4);
         if constexpr (C::SQK) {
-            // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32)
+            // HD/4 consecutive lanes hold one K row (every lane is in range for HD >= 32):
+            // its tile's image is row / 32, its row there row % 32; halves 4 c4 .. 4 c4 + 3
+            // are half of chunk c4 / 2.
             const f32x4 x = rk[r];
-            _Float16 *kr = reinterpret_cast<_Float16 *>(Kb + row * C::KS);
+            float *img = Kb + (row / kTile) * IMGX;
+            _Float16 *imh = reinterpret_cast<_Float16 *>(img);
+            const int kr = row % kTile;
             if constexpr (FAST) {
-                // tile row / 32, row row % 32: halves 4 c4 .. 4 c4 + 3 are half a chunk
-                _Float16 *img = reinterpret_cast<_Float16 *>(Kb + (row / kTile) * C::FIMG);
-                *reinterpret_cast<f16x4 *>(img + fk_chunk<HD>(row % kTile, c4 / 2) * 8 +
-                                           (c4 & 1) * 4) = __builtin_convertvector(x, f16x4);
+                *reinterpret_cast<f16x4 *>(imh + 8 * fk_chunk<HD>(kr, c4 / 2) + (c4 & 1) * 4) =
+                    __builtin_convertvector(x, f16x4);
             } else {
                 const float m4 =
                     fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
@@ -289,61 +292,57 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                 const int e = split_exponent(mx);
                 f16x4 hi, lo;
                 split_f16(x, e, hi, lo);
-                *reinterpret_cast<f16x4 *>(kr + c4 * 4) = hi;
-                *reinterpret_cast<f16x4 *>(kr + HD + c4 * 4) = lo;
-                if (c4 == 0) Eb[row] = e;
+                *reinterpret_cast<f16x4 *>(imh + 8 * sk_chunk<HD>(kr, c4 / 2, 0) + (c4 & 1) * 4) = hi;
+                *reinterpret_cast<f16x4 *>(imh + 8 * sk_chunk<HD>(kr, c4 / 2, 1) + (c4 & 1) * 4) = lo;
+                if (c4 == 0) reinterpret_cast<int *>(img + C::EXPO)[kr] = e;
             }
-            if constexpr (C::SPV) {
-                const f32x4 y = rv[r];
-                int ev = 0;
-                f16x4 vh, vl;
-                if constexpr (FAST || V16) {
-                    vh = __builtin_convertvector(y, f16x4);
-                    vl = vh;
-                } else {
-                    const float vm4 =
-                        fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
-                    ev = split_exponent(group_max<HD / 4>(vm4));
-                    split_f16(y, ev, vh, vl);
-                }
-                // V^T row of dim d sits at p(d) = (d % NB) * 32 + d / NB (the MFMA reader
-                // then walks consecutive rows). Rows j and j + 1 (lanes i and i ^ HD/4) pair
-                // their halves: the even row's lane writes dims 0, 1 of its four, the odd
-                // row's lane dims 2, 3, each as one 32-bit (key j, key j + 1) word.
-                if constexpr (HD / 4 > 32) {
-                    // A row spans the whole wave (no partner row in it): halves one by one,
-                    // at the same permuted key position as below.
-                    const int g4s = (row >> 2) & 3;
-                    const int js = (row & ~15) | (((g4s & 1) << 1 | (g4s >> 1)) << 2) | (row & 3);
-                    _Float16 *vth16 = reinterpret_cast<_Float16 *>(Vb);
-                    _Float16 *vtl16 = vth16 + HD * C::VROW;
+            const f32x4 y = rv[r];
+            int ev = 0;
+            f16x4 vh, vl;
+            if constexpr (FAST || V16) {
+                vh = __builtin_convertvector(y, f16x4);
+                vl = vh;
+            } else {
+                const float vm4 =
+                    fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+                ev = split_exponent(group_max<HD / 4>(vm4));
+                split_f16(y, ev, vh, vl);
+            }
+            // V^T row of dim d is p(d) = (d % NB) * 32 + d / NB (the MFMA reader then walks
+            // consecutive rows). Keys are stored permuted within each 16: groups of four in
+            // the order 0, 2, 1, 3, so that the 8 keys one lane half feeds an MFMA step
+            // (keys 16u + 4hf + 0..3 and 16u + 8 + 4hf + 0..3) fill one chunk.
+            if constexpr (HD / 4 > 32) {
+                // A row spans the whole wave (no partner row in it): halves one by one.
+                const int g4s = (row >> 2) & 3;
+                const int js = (row & ~15) | (((g4s & 1) << 1 | (g4s >> 1)) << 2) | (row & 3);
+                _Float16 *vimg = reinterpret_cast<_Float16 *>(Kb + (js / kTile) * IMGX);
+                const int jc = (js % kTile) / 8, jw = js % 8;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int d = c4 * 4 + i;
-                        const int pr = (d % C::NB) * 32 + d / C::NB;
-                        if constexpr (FAST) {
-                            _Float16 *img =
-                                reinterpret_cast<_Float16 *>(Kb + (js / kTile) * C::FIMG);
-                            img[fv_chunk<HD>(pr, (js % kTile) / 8) * 8 + js % 8] = vh[i];
-                        } else {
-                            vth16[pr * C::VROW + js] = vh[i];
-                        }
-                        if constexpr (!FAST && !V16) vtl16[pr * C::VROW + js] = vl[i];
+                for (int i = 0; i < 4; ++i) {
+                    const int d = c4 * 4 + i;
+                    const int pr = (d % C::NB) * 32 + d / C::NB;
+                    if constexpr (FAST) {
+                        vimg[8 * fv_chunk<HD>(pr, jc) + jw] = vh[i];
+                    } else {
+                        vimg[8 * sv_chunk<HD>(pr, jc, 0) + jw] = vh[i];
+                        if constexpr (!V16) vimg[8 * sv_chunk<HD>(pr, jc, 1) + jw] = vl[i];
                     }
-                } else {
+                }
+            } else {
+                // Rows j and j + 1 (lanes i and i ^ HD/4) pair their halves: the even row's
+                // lane writes dims 0, 1 of its four, the odd row's lane dims 2, 3, each as
+                // one 32-bit (key j, key j + 1) word.
                 using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
                 const u32x2 ho = __builtin_bit_cast(u32x2, vh), lw = __builtin_bit_cast(u32x2, vl);
                 const u32x2 hp = {lane_xor_u<HD / 4>(ho.x), lane_xor_u<HD / 4>(ho.y)};
                 const u32x2 lp = (FAST || V16) ? lw : u32x2{lane_xor_u<HD / 4>(lw.x), lane_xor_u<HD / 4>(lw.y)};
                 const f16x4 vh2 = __builtin_bit_cast(f16x4, hp), vl2 = __builtin_bit_cast(f16x4, lp);
                 const bool odd = row & 1;
-                // Keys are stored permuted within each 16: groups of four in the order
-                // 0, 2, 1, 3, so that the 8 keys one lane half feeds an MFMA step (keys
-                // 16u + 4hf + 0..3 and 16u + 8 + 4hf + 0..3) are contiguous.
                 const int g4 = (row >> 2) & 3;
                 const int j0 = (row & ~15) | (((g4 & 1) << 1 | (g4 >> 1)) << 2) | (row & 2);
-                unsigned *vth = reinterpret_cast<unsigned *>(Vb);  // [HD][VROW/2] words, hi
-                unsigned *vtl = vth + HD * (C::VROW / 2);           // then lo
+                unsigned *vimg = reinterpret_cast<unsigned *>(Kb + (j0 / kTile) * IMGX);
+                const int jc = (j0 % kTile) / 8, jw = (j0 % 8) / 2;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const int i = odd ? 2 + t : t;  // which of the four dims
@@ -353,129 +352,54 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     const _Float16 le = odd ? vl2[i] : vl[i], lo2 = odd ? vl[i] : vl2[i];
                     using h2 = __attribute__((ext_vector_type(2))) _Float16;
                     if constexpr (FAST) {
-                        unsigned *img = reinterpret_cast<unsigned *>(Kb + (j0 / kTile) * C::FIMG);
-                        img[fv_chunk<HD>(pr, (j0 % kTile) / 8) * 4 + (j0 % 8) / 2] =
-                            __builtin_bit_cast(unsigned, h2{he, ho2});
+                        vimg[4 * fv_chunk<HD>(pr, jc) + jw] = __builtin_bit_cast(unsigned, h2{he, ho2});
                     } else {
-                        vth[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{he, ho2});
+                        vimg[4 * sv_chunk<HD>(pr, jc, 0) + jw] = __builtin_bit_cast(unsigned, h2{he, ho2});
+                        if constexpr (!V16)
+                            vimg[4 * sv_chunk<HD>(pr, jc, 1) + jw] = __builtin_bit_cast(unsigned, h2{le, lo2});
                     }
-                    if constexpr (!FAST && !V16)
-                        vtl[pr * (C::VROW / 2) + j0 / 2] = __builtin_bit_cast(unsigned, h2{le, lo2});
                 }
-                }
-                if (!FAST && !V16 && c4 == 0) Ev[row] = ev;
-            } else {
-                *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
             }
+            if (!FAST && !V16 && c4 == 0) reinterpret_cast<int *>(img + C::EXPO)[kTile + kr] = ev;
         } else if (idx < C::STEP_F4) {
+            float *Vb = Kb + C::STEP_KEYS * C::KS;
             *reinterpret_cast<f32x4 *>(Kb + row * C::KS + c4 * 4) = rk[r];
             *reinterpret_cast<f32x4 *>(Vb + row * HD + c4 * 4) = rv[r];
         }
     }
 }
 
-// Float offset, inside one LDS buffer of C, of chunk w of tile kt's pre-split record (the
-// image prefill_store_step writes for that tile, less its row padding).
-template <class C>
-__device__ __forceinline__ int ps_lds_offset(int kt, int w) {
-    constexpr int HD = C::HD_;
-    if (w < 8 * HD) return (kt * kTile + w / (HD / 4)) * C::KS + 4 * (w % (HD / 4));
-    if (w < 16 * HD) {
-        const int w2 = w - 8 * HD;
-        const int lo = w2 >= 4 * HD;
-        const int w3 = w2 - (lo ? 4 * HD : 0);
-        return C::STEP_KEYS * C::KS + lo * HD * (C::VROW / 2) + (w3 / 4) * (C::VROW / 2) +
-               kt * (kTile / 2) + 4 * (w3 % 4);
-    }
-    const int e = w - 16 * HD;  // exponents: K chunks 0..7, V chunks 8..15
-    return C::STEP_KEYS * C::KS + C::VFL + (e >= 8 ? C::STEP_KEYS : 0) + kt * kTile + 4 * (e % 8);
-}
-
-// Raw buffer resource over n 16-byte records at p: base and size are made wave-uniform, so
-// the descriptor lives in scalar registers and each load adds a scalar record offset to the
-// lane's 32-bit one (no per-lane 64-bit address arithmetic).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const f32x4 *p, int n) {
-    return eb::make_rsrc(p, 16 * n);
-}
-__device__ __forceinline__ f32x4 chunk_load(__amdgpu_buffer_rsrc_t r, int lane_chunk,
-                                            int uniform_chunk) {
-    return __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                   r, 16 * lane_chunk, __builtin_amdgcn_readfirstlane(16 * uniform_chunk), 0));
-}
-
-// Fetch the pre-split records of tiles tile0 .. tile0 + KSPLIT - 1 (clamped to the last
-// record, nt - 1; a clamped buffer is never read) of one KV head (recs).
-template <class C>
-__device__ __forceinline__ void ps_load_step(const f32x4 *__restrict__ recs,
-                                             f32x4 (&r)[C::PSN], int tile0, int nt, int tid) {
-    constexpr int HD = C::HD_;
-    if constexpr ((16 * HD) % C::THREADS == 0) {
-        // Load i reads chunks [(i % PER) * THREADS, + THREADS) of tile tile0 + i / PER: a
-        // buffer load whose record offset is the same for the whole wave (a scalar operand),
-        // the lane adding tid. (A KV head's records stay below 2 GiB: the launch checks.)
-        constexpr int PER = 16 * HD / C::THREADS;
-        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(recs, nt * C::PS_CH);
-#pragma unroll
-        for (int i = 0; i < C::PSN - 1; ++i) {
-            r[i] = chunk_load(rs, tid,
-                              min(tile0 + i / PER, nt - 1) * C::PS_CH + (i % PER) * C::THREADS);
-        }
-        const int kt = min(tid / 16, C::STEP_KEYS / kTile - 1);
-        r[C::PSN - 1] = chunk_load(rs, min(tile0 + kt, nt - 1) * C::PS_CH + 16 * HD + tid % 16, 0);
-    } else {
-#pragma unroll
-        for (int i = 0; i < C::PSN - 1; ++i) {
-            const int c = min(tid + i * C::THREADS, C::PS_KV - 1);
-            const int t = min(tile0 + c / (16 * HD), nt - 1);
-            r[i] = recs[(size_t)t * C::PS_CH + c % (16 * HD)];
-        }
-        const int kt = min(tid / 16, C::STEP_KEYS / kTile - 1);
-        const int t = min(tile0 + kt, nt - 1);
-        r[C::PSN - 1] = recs[(size_t)t * C::PS_CH + 16 * HD + tid % 16];
-    }
-}
-
-template <class C>
-__device__ __forceinline__ void ps_store_step(float *smem, const f32x4 (&r)[C::PSN], int buf,
-                                              int tid) {
-    constexpr int HD = C::HD_;
-    float *B = smem + buf * C::BUF;
-#pragma unroll
-    for (int i = 0; i < C::PSN - 1; ++i) {
-        const int c = tid + i * C::THREADS;
-        if (C::PS_KV % C::THREADS == 0 || c < C::PS_KV)
-            *reinterpret_cast<f32x4 *>(B + ps_lds_offset<C>(c / (16 * HD), c % (16 * HD))) = r[i];
-    }
-    if (tid < 16 * (C::STEP_KEYS / kTile))
-        *reinterpret_cast<f32x4 *>(B + ps_lds_offset<C>(tid / 16, 16 * HD + tid % 16)) =
-            r[C::PSN - 1];
-}
-
-// Copy the f16-mode records of tiles tile0 .. tile0 + KSPLIT - 1 (each clamped to the last
-// record, nt - 1: a clamped image is never read) of one KV head (recs) into LDS buffer
-// `buf` with memory-to-LDS loads, as ps_copy_image does (complete after wait_vm_all()):
-// wave w moves the buffer's KiB blocks w * BPW .. w * BPW + BPW - 1, one image's, each
-// load's immediate offset applying to both its global and its LDS address.
-template <class C>
-__device__ __forceinline__ void fps_copy(const float *__restrict__ recs, float *smem, int buf,
-                                         int tile0, int nt, int wave, int lane) {
-    constexpr int BLK = C::FIMG / 256;                       // KiB blocks per image
-    constexpr int BPW = (C::STEP_KEYS / kTile) * BLK / C::NW;  // blocks per wave
-    static_assert(BPW >= 1 && BLK % BPW == 0 && BPW * 1024 <= 4096,
-                  "a wave's blocks lie in one image, within the loads' offset range");
+// Copy NIMG tile images (records tile0 .. tile0 + NIMG - 1 of one KV head, recs, each
+// clamped to the last record, nt - 1: a clamped image is never read) of IMGF floats into
+// LDS at lds with memory-to-LDS loads: wave w moves KiB blocks w * BPW .. w * BPW + BPW - 1
+// of each image (lane i bytes 16i .. 16i + 15 of a block), a load's immediate offset
+// applying to both its global and its LDS address. Issued as inline assembly, which the
+// compiler's wait counting does not see (it would otherwise wait for these loads before
+// every read of the other buffer); the loads are complete after wait_vm_all().
+template <int IMGF, int NIMG, int NW>
+__device__ __forceinline__ void img_copy(const float *__restrict__ recs, float *lds, int tile0,
+                                         int nt, int wave, int lane) {
+    constexpr int BLK = IMGF / 256;  // KiB blocks per image
+    constexpr int BPW = (BLK + NW - 1) / NW;
+    static_assert(IMGF % 256 == 0, "whole KiB images");
     const int j0 = wave * BPW;
-    const int t = min(tile0 + j0 / BLK, nt - 1);
-    const float *src = recs + (size_t)t * C::FIMG + (j0 % BLK) * 256 + lane * 4;
-    const unsigned dst = __builtin_amdgcn_readfirstlane(
-        (unsigned)(uintptr_t)(__attribute__((address_space(3))) float *)(smem + buf * C::FBUF +
-                                                                          j0 * 256));
 #pragma unroll
-    for (int i = 0; i < BPW; ++i)
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off offset:%2"
-                     :
-                     : "s"(dst), "v"(src), "i"(1024 * i)
-                     : "memory", "m0");
+    for (int k = 0; k < NIMG; ++k) {
+        const int t = min(tile0 + k, nt - 1);
+        const float *src = recs + (size_t)t * IMGF + j0 * 256 + lane * 4;
+        const unsigned dst = __builtin_amdgcn_readfirstlane(
+            (unsigned)(uintptr_t)(__attribute__((address_space(3))) float *)(lds + k * IMGF +
+                                                                              j0 * 256));
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            if (BLK % NW == 0 || j0 + i < BLK)  // (uniform)
+                asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off offset:%2"
+                             :
+                             : "s"(dst + 4096 * (i / 4)), "v"(src + 1024 * (i / 4)),
+                               "i"(1024 * (i % 4))
+                             : "memory", "m0");
+        }
+    }
 }
 
 // The pre-split and pre-convert passes' shape: one 32-key tile per workgroup (the records'
@@ -526,43 +450,15 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
     const int t = blockIdx.x;
     const int kvh = blockIdx.y;
     const int tid = threadIdx.x;
-    // (An image record's padding is left as it is: K rows are read within their HD floats,
-    // V^T rows within their 32 keys, and the exponents where written.)
+    // (The tile image is the record. Its padding past the exponents, and with V16 its V^T lo
+    // halves and V exponents, are left as they are: nothing reads them.)
     f32x4 rk[C::NLD], rv[C::NLD];
     prefill_load_step<C, EB, NT>(k, v, rk, rv, (tlo + t) * kTile, nkeys, Hkv, kvh, tid, hdr);
     prefill_store_step<C, false, V16>(smem, rk, rv, 0, tid);
     __syncthreads();
     f32x4 *rec = reinterpret_cast<f32x4 *>(ps + ((size_t)kvh * nt + t) * C::PS_FLOATS);
-    if constexpr (C::PS_IMAGE) {
-        for (int c = tid; c < C::BUF / 4; c += C::THREADS)
-            rec[c] = reinterpret_cast<const f32x4 *>(smem)[c];
-    } else {
-        for (int c = tid; c < C::PS_CH; c += C::THREADS)
-            rec[c] = *reinterpret_cast<const f32x4 *>(smem + ps_lds_offset<C>(0, c));
-    }
-}
-
-// Copy the image record of tile `tile` (clamped to the last record, nt - 1: a clamped
-// buffer is never read) of one KV head (recs) into LDS buffer `buf` with memory-to-LDS
-// loads: each wave instruction moves 1 KiB, lane i writing bytes 16i .. 16i + 15 of it.
-// Issued as inline assembly, which the compiler's wait counting does not see (it would
-// otherwise wait for these loads before every read of the other buffer); the loads are
-// complete after wait_vm_all().
-template <class C>
-__device__ __forceinline__ void ps_copy_image(const float *__restrict__ recs, float *smem,
-                                              int buf, int tile, int nt, int wave, int lane) {
-    static_assert(C::PS_IMAGE && C::STEP_KEYS == kTile, "one image record per step");
-    const int t = min(tile, nt - 1);
-    for (int j = wave; j < C::BUF / 256; j += C::NW) {
-        const float *src = recs + (size_t)t * C::PS_FLOATS + j * 256 + lane * 4;
-        const unsigned dst =
-            (unsigned)(uintptr_t)(__attribute__((address_space(3))) float *)(smem + buf * C::BUF +
-                                                                              j * 256);
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                     :
-                     : "s"(__builtin_amdgcn_readfirstlane(dst)), "v"(src)
-                     : "memory", "m0");
-    }
+    for (int c = tid; c < C::IMG / 4; c += C::THREADS)
+        rec[c] = reinterpret_cast<const f32x4 *>(smem)[c];
 }
 
 __device__ __forceinline__ void wait_vm_all() {
@@ -643,10 +539,12 @@ __global__ __attribute__((
     const int g = H / Hkv;
     const int gsub = g / HPW;
     const int flat = blockIdx.x;
-    const int grp = flat % ngroups;
-    const int qb = nqb - 1 - flat / ngroups;  // heaviest query blocks first
-    const int kvh = grp / gsub;
-    const int head = kvh * g + (grp % gsub) * HPW + slot / WPH;
+    // (uniform: the divisions by run-time values go through the vector unit, so their
+    // results are moved to scalar registers)
+    const int grp = __builtin_amdgcn_readfirstlane(flat % ngroups);
+    const int qb = __builtin_amdgcn_readfirstlane(nqb - 1 - flat / ngroups);  // heaviest first
+    const int kvh = __builtin_amdgcn_readfirstlane(grp / gsub);
+    const int head = __builtin_amdgcn_readfirstlane(kvh * g + (grp % gsub) * HPW + slot / WPH);
     // Query rows are local (0..rows-1) and sit at positions qbase + row. Key tiles of 32
     // cover keys [32 t, 32 t + 32); a query at p sees keys max(0, p - window + 1)..p
     // (0..p without a window).
@@ -675,20 +573,15 @@ __global__ __attribute__((
     const int qi = q0 + col;
     const int pi = qbase + qi;
 
-    // The first step's K/V loads (into registers, or for head_dim 256 memory-to-LDS) go out
-    // right behind the q fragment's, so that the two latencies overlap.
+    // The first step's K/V loads (records memory-to-LDS, or K/V rows into registers) go
+    // out right behind the q fragment's, so that the two latencies overlap.
     f32x4 rk[PS ? 1 : C::NLD], rv[PS ? 1 : C::NLD];
-    static_assert(!(PS && FAST && C::PS_IMAGE), "f16-mode records for head_dim <= 128");
-    f32x4 rs[PS && !FAST ? C::PSN : 1];
-    const float *recs =
-        PS ? ps + (size_t)kvh * ps_nt * (FAST ? C::FPS_FLOATS : C::PS_FLOATS) : nullptr;
+    static_assert(!(PS && FAST) || HD <= 128, "f16-mode records for head_dim <= 128");
+    constexpr int IMGX = imgsize<C, FAST>();
+    const float *recs = PS ? ps + (size_t)kvh * ps_nt * IMGX : nullptr;
     auto load_first_step = [&] {
-        if constexpr (PS && FAST)
-            fps_copy<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
-        else if constexpr (PS && C::PS_IMAGE)
-            ps_copy_image<C>(recs, smem, 0, c_lo - ps_tlo, ps_nt, wave, lane);
-        else if constexpr (PS)
-            ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs, c_lo - ps_tlo, ps_nt, tid);
+        if constexpr (PS)
+            img_copy<IMGX, KSPLIT, C::NW>(recs, smem, c_lo - ps_tlo, ps_nt, wave, lane);
         else
             prefill_load_step<C, EB>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
     };
@@ -799,35 +692,26 @@ __global__ __attribute__((
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     // ... and the first step's K/V into LDS.
-    if constexpr (PS && (FAST || C::PS_IMAGE))
+    if constexpr (PS)
         wait_vm_all();
-    else if constexpr (PS)
-        ps_store_step<C>(smem, rs, 0, tid);
     else
         prefill_store_step<C, FAST, PV1>(smem, rk, rv, 0, tid);
     __syncthreads();
 
-    // The next step's K/V: PS records into registers (or, head_dim 256 and the f16 mode's
-    // images, straight into the other buffer, which every wave finished reading before the
-    // last barrier); otherwise K/V rows into registers. Past the last step this re-reads clamped rows (the buffer
-    // written from them is never read).
+    // The next step's K/V: PS records straight into the other buffer (which every wave
+    // finished reading before the last barrier), otherwise K/V rows into registers. Past the
+    // last step this re-reads clamped rows (the buffer written from them is never read).
     auto prefetch = [&](int it1, int b1) {
-        if constexpr (PS && FAST)
-            fps_copy<C>(recs, smem, b1, c_lo + it1 * KSPLIT - ps_tlo, ps_nt, wave, lane);
-        else if constexpr (PS && C::PS_IMAGE)
-            ps_copy_image<C>(recs, smem, b1, c_lo + it1 * KSPLIT - ps_tlo, ps_nt, wave, lane);
-        else if constexpr (PS)
-            ps_load_step<C>(reinterpret_cast<const f32x4 *>(recs), rs,
-                            c_lo + it1 * KSPLIT - ps_tlo, ps_nt, tid);
+        if constexpr (PS)
+            img_copy<IMGX, KSPLIT, C::NW>(recs, smem + b1 * BUFX, c_lo + it1 * KSPLIT - ps_tlo,
+                                          ps_nt, wave, lane);
         else
             prefill_load_step<C, EB>(k, v, rk, rv, (c_lo + it1 * KSPLIT) * kTile, nkeys, Hkv,
                                       kvh, tid, hdr);
     };
     auto stage = [&](int b1) {
-        if constexpr (PS && (FAST || C::PS_IMAGE))
+        if constexpr (PS)
             wait_vm_all();
-        else if constexpr (PS)
-            ps_store_step<C>(smem, rs, b1, tid);
         else
             prefill_store_step<C, FAST, PV1>(smem, rk, rv, b1, tid);
     };
@@ -838,15 +722,14 @@ __global__ __attribute__((
         //  softmax: the online softmax update (m, l, the O^T unit E, the rescale of O^T) and
         //           the P^T operands;
         //  pv:      O^T += V^T P^T from buffer b.
-        auto tile_qk = [&](int b, floatx16 &sacc, int (&ek)[16]) {
-            const float *Kb = smem + b * BUFX + ks * kTile * KS;
+        auto tile_qk = [&](int b, floatx16 &sacc) {
+            const float *img = smem + b * BUFX + ks * IMGX;  // tile ks's image
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
-            // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
-            const _Float16 *krow = reinterpret_cast<const _Float16 *>(Kb + col * KS);
-            // FAST: chunk 2 k2 + hf of key col in tile ks's image
-            const _Float16 *kimg = reinterpret_cast<const _Float16 *>(smem + b * BUFX + ks * C::FIMG) +
-                                   8 * fk_chunk<HD>(col, hf);
+            // K chunk 2 k2 + hf of key col: hi (FAST: the only) halves, the lo ones 4 HD
+            // chunks on
+            const _Float16 *kimg = reinterpret_cast<const _Float16 *>(img) +
+                                   8 * (FAST ? fk_chunk<HD>(col, hf) : sk_chunk<HD>(col, hf, 0));
             if constexpr (FAST && NKS <= 8) {
                 // All of the tile's K operands are read before the first product (the
                 // compiler would otherwise wait out each read's latency before its product).
@@ -863,47 +746,45 @@ __global__ __attribute__((
                     sacc = mfma16(*reinterpret_cast<const f16x8 *>(kimg + 8 * 2 * kTile * k2),
                                   qh[k2], sacc);
             } else {
+                // Three products per 16-dim step (hi*hi, hi*lo, lo*hi; lo*lo is below 2^-22).
                 // (both operands read before the products with key splits, the lo operand
                 // after the first product without: the orders that leave the staged
                 // kernels at head_dim 128 without a register spill)
 #pragma unroll
                 for (int k2 = 0; k2 < NKS; ++k2) {
-                    const f16x8 ah = *reinterpret_cast<const f16x8 *>(krow + 16 * k2 + 8 * hf);
+                    const _Float16 *kh = kimg + 8 * 2 * kTile * k2;
+                    const f16x8 ah = *reinterpret_cast<const f16x8 *>(kh);
                     f16x8 al;
                     if constexpr (KSPLIT > 1)
-                        al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                        al = *reinterpret_cast<const f16x8 *>(kh + 8 * 4 * HD);
                     sacc = mfma16(ah, qh[k2], sacc);
                     if constexpr (KSPLIT == 1)
-                        al = *reinterpret_cast<const f16x8 *>(krow + HD + 16 * k2 + 8 * hf);
+                        al = *reinterpret_cast<const f16x8 *>(kh + 8 * 4 * HD);
                     sacc = mfma16(ah, ql[k2], sacc);
                     sacc = mfma16(al, qh[k2], sacc);
                 }
             }
-            // the exponent of each of this lane's keys
-            if constexpr (FAST) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) ek[r] = 0;
-            } else {
-                const int *Eb = reinterpret_cast<const int *>(smem + b * C::BUF +
-                                                              C::STEP_KEYS * KS + C::VFL) +
-                                ks * kTile;
+            // Scores back from the split's units: 2^(eq + ek), ek the exponent of each of
+            // this lane's keys (read four at a time).
+            if constexpr (!FAST) {
+                const int *Eb = reinterpret_cast<const int *>(img + C::EXPO);
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4) {
                     const int4 e4 = *reinterpret_cast<const int4 *>(Eb + 8 * s4 + 4 * hf);
-                    ek[4 * s4 + 0] = e4.x;
-                    ek[4 * s4 + 1] = e4.y;
-                    ek[4 * s4 + 2] = e4.z;
-                    ek[4 * s4 + 3] = e4.w;
+                    sacc[4 * s4 + 0] = ldexpf(sacc[4 * s4 + 0], eq + e4.x);
+                    sacc[4 * s4 + 1] = ldexpf(sacc[4 * s4 + 1], eq + e4.y);
+                    sacc[4 * s4 + 2] = ldexpf(sacc[4 * s4 + 2], eq + e4.z);
+                    sacc[4 * s4 + 3] = ldexpf(sacc[4 * s4 + 3], eq + e4.w);
                 }
             }
         };
 
-        auto tile_softmax = [&](int b, int kb, const floatx16 &sacc, const int (&ek)[16],
-                                f16x8 (&ph)[2], f16x8 (&pl)[2]) {
-            // Scores back from the split's units: 2^(eq + ek).
+        auto tile_softmax = [&](int b, int kb, const floatx16 &sacc, f16x8 (&ph)[2],
+                                f16x8 (&pl)[2]) {
+            // the scores in log2 units
             float p[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = FAST ? sacc[r] : ldexpf(sacc[r], eq + ek[r]);
+            for (int r = 0; r < 16; ++r) p[r] = sacc[r];
             // Online softmax over this tile's keys (log2 domain). Only tiles that reach past
             // the wave's first position, or (window) below its last position's window, need
             // the per-key mask.
@@ -970,9 +851,8 @@ __global__ __attribute__((
                 if constexpr (PV1) l = l * corr + ps;
             } else {
                 // The tile's V exponents ev (V row = 2^ev * v').
-                const int *Ev = reinterpret_cast<const int *>(smem + b * C::BUF +
-                                                              C::STEP_KEYS * KS + C::VFL) +
-                                C::STEP_KEYS + ks * kTile;
+                const int *Ev =
+                    reinterpret_cast<const int *>(smem + b * BUFX + ks * IMGX + C::EXPO) + kTile;
                 int ev[16];
 #pragma unroll
                 for (int s4 = 0; s4 < 4; ++s4) {
@@ -1035,13 +915,13 @@ __global__ __attribute__((
         // expects), stored at V^T row 32*mb + col; keys 16u + 4hf + 0..3 and 16u + 8 + 4hf +
         // 0..3 of this wave's tile (the order of ph / pl). FAST: the hi halves only.
         auto tile_pv = [&](int b, const f16x8 (&ph)[2], const f16x8 (&pl)[2]) {
-            const _Float16 *vth =
-                reinterpret_cast<const _Float16 *>(smem + b * BUFX + C::STEP_KEYS * KS);
-            // FAST: chunk hf + 2u of V^T row 32 mb + col in tile ks's image
-            const _Float16 *vimg = reinterpret_cast<const _Float16 *>(smem + b * BUFX + ks * C::FIMG) +
-                                   8 * fv_chunk<HD>(col, hf);
+            // V^T chunk hf + 2u of row 32 mb + col in tile ks's image: hi (FAST: the only)
+            // halves, the lo ones 4 HD chunks on
+            const _Float16 *vimg =
+                reinterpret_cast<const _Float16 *>(smem + b * BUFX + ks * IMGX) +
+                8 * (FAST ? fv_chunk<HD>(col, hf) : sv_chunk<HD>(col, hf, 0));
             if constexpr (FAST || PV1) {
-                // f16 mode: the NB V fragments of one 16-key half are read first and the
+                // One product: the NB V fragments of one 16-key half are read first and the
                 // products go round the NB accumulators (measured 2-4 % faster than one
                 // accumulator's products back to back; the three-product mode has no
                 // registers left for it)
@@ -1050,22 +930,18 @@ __global__ __attribute__((
                     f16x8 vh[NB];
 #pragma unroll
                     for (int mb = 0; mb < NB; ++mb)
-                        vh[mb] = FAST ? *reinterpret_cast<const f16x8 *>(
-                                            vimg + 8 * (2 * u * HD + 32 * mb))
-                                      : *reinterpret_cast<const f16x8 *>(
-                                            vth + (32 * mb + col) * C::VROW + ks * kTile + 8 * hf + 16 * u);
+                        vh[mb] = *reinterpret_cast<const f16x8 *>(vimg + 8 * (2 * u * HD + 32 * mb));
 #pragma unroll
                     for (int mb = 0; mb < NB; ++mb) oacc[mb] = mfma16(vh[mb], ph[u], oacc[mb]);
                 }
             } else {
-                const _Float16 *vtl = vth + HD * C::VROW;
 #pragma unroll
                 for (int mb = 0; mb < NB; ++mb) {
-                    const int roff = (32 * mb + col) * C::VROW + ks * kTile + 8 * hf;
 #pragma unroll
                     for (int u = 0; u < 2; ++u) {
-                        const f16x8 vh = *reinterpret_cast<const f16x8 *>(vth + roff + 16 * u);
-                        const f16x8 vl = *reinterpret_cast<const f16x8 *>(vtl + roff + 16 * u);
+                        const _Float16 *vp = vimg + 8 * (2 * u * HD + 32 * mb);
+                        const f16x8 vh = *reinterpret_cast<const f16x8 *>(vp);
+                        const f16x8 vl = *reinterpret_cast<const f16x8 *>(vp + 8 * 4 * HD);
                         oacc[mb] = mfma16(vh, ph[u], oacc[mb]);
                         oacc[mb] = mfma16(vh, pl[u], oacc[mb]);
                         oacc[mb] = mfma16(vl, ph[u], oacc[mb]);
@@ -1075,15 +951,14 @@ __global__ __attribute__((
         };
 
         floatx16 sacc;
-        int ek[16];
         f16x8 ph[2], pl[2];
         for (int it = 0; it < nsteps; ++it) {
             const int buf = it & 1;
             const int tile = c_lo + it * KSPLIT + ks;
             prefetch(it + 1, buf ^ 1);
             if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
-                tile_qk(buf, sacc, ek);
-                tile_softmax(buf, tile * kTile, sacc, ek, ph, pl);
+                tile_qk(buf, sacc);
+                tile_softmax(buf, tile * kTile, sacc, ph, pl);
                 // The P V products at raised wave priority: with two waves on a SIMD, the one
                 // that reaches them issues first, so that the other's softmax runs beside
                 // them (measured +3 % at Qwen, +6 % at Mistral T=4096; the f16 mode, with a
@@ -1201,28 +1076,33 @@ __global__ __attribute__((
     }
     }
 
+    // The lane's coordinates again, from the lane id: recomputed here, they need not stay
+    // live (or spill) through the loop.
+    const int elane = __lane_id();
+    const int ehf = elane >> 5, ecol = elane & 31, eqi = q0 + ecol;
+
     // Merge the key splits: waves ks >= 1 hand (m, l, O^T) to wave ks = 0 of their slot
     // through LDS (reusing the tile buffers, free after the loop's last barrier). Fields are
-    // stored [record][field][lane] so every access is a contiguous 64-lane row.
+    // stored [record][field][elane] so every access is a contiguous 64-elane row.
     if constexpr (KSPLIT > 1) {
         if (ks > 0) {
             float *rec = smem + ((ks - 1) * (HPW * WPH) + slot) * C::REC * 64;
-            rec[0 * 64 + lane] = m;
-            rec[1 * 64 + lane] = l;
-            rec[2 * 64 + lane] = __int_as_float(E);
+            rec[0 * 64 + elane] = m;
+            rec[1 * 64 + elane] = l;
+            rec[2 * 64 + elane] = __int_as_float(E);
 #pragma unroll
             for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) rec[(3 + mb * 16 + r) * 64 + lane] = oacc[mb][r];
+                for (int r = 0; r < 16; ++r) rec[(3 + mb * 16 + r) * 64 + elane] = oacc[mb][r];
         }
         __syncthreads();
         if (ks == 0) {
 #pragma unroll
             for (int j = 1; j < KSPLIT; ++j) {
                 const float *rec = smem + ((j - 1) * (HPW * WPH) + slot) * C::REC * 64;
-                const float m2 = rec[lane];
-                const float l2 = rec[64 + lane];
-                const int E2 = __float_as_int(rec[128 + lane]);
+                const float m2 = rec[elane];
+                const float l2 = rec[64 + elane];
+                const int E2 = __float_as_int(rec[128 + elane]);
                 const float M = fmaxf(m, m2);
                 const float Mr = (M == -INFINITY) ? 0.0f : M;
                 const float a1 = eb::fast_exp2(m - Mr);   // 0 when this wave saw no keys
@@ -1238,13 +1118,13 @@ __global__ __attribute__((
                 for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        oacc[mb][r] = oacc[mb][r] * b1 + rec[(3 + mb * 16 + r) * 64 + lane] * b2;
+                        oacc[mb][r] = oacc[mb][r] * b1 + rec[(3 + mb * 16 + r) * 64 + elane] * b2;
             }
         }
     }
 
-    // Normalise, then store through LDS: lane (col, hf) holds O[q0 + col][NB*c + mb] for
-    // c = 8*(r/4) + 4*hf + r%4, i.e. 16-byte pieces of 32 different output rows. Each
+    // Normalise, then store through LDS: elane (ecol, ehf) holds O[q0 + ecol][NB*c + mb] for
+    // c = 8*(r/4) + 4*ehf + r%4, i.e. 16-byte pieces of 32 different output rows. Each
     // slot's 32 x HD tile is transposed through LDS so the global stores are whole rows
     // (HD contiguous floats per (query, head)).
     // A block split into key chunks writes its raw state instead: O^T (in units of 2^E for
@@ -1264,20 +1144,20 @@ __global__ __attribute__((
                     for (int r = 0; r < 16; ++r) oacc[mb][r] = ldexpf(oacc[mb][r] * inv, E);
             }
         }
-        if (partial && hf == 0 && qi < rows)
-            *reinterpret_cast<float4 *>(part_ml + (((size_t)chunk * rows + qi) * H + head) * 4) =
+        if (partial && ehf == 0 && eqi < rows)
+            *reinterpret_cast<float4 *>(part_ml + (((size_t)chunk * rows + eqi) * H + head) * 4) =
                 make_float4(m, lt, __int_as_float(C::SPV ? E : 0), 0.0f);
         const float sc_o = C::SPV ? 1.0f : inv;
         if constexpr (direct_out<C, FAST>()) {
-            // Straight from the registers: lane (col, hf) stores NB consecutive dims NB*c ..
+            // Straight from the registers: elane (ecol, ehf) stores NB consecutive dims NB*c ..
             // NB*c + NB - 1 of its query's row for each of its 16 values of c.
-            if (qi < rows) {
+            if (eqi < rows) {
                 float *dst = partial ? part_acc + (size_t)chunk * rows * H * HD : o;
                 const int dstride = partial ? HD : hdr;
-                float *orow = dst + ((size_t)qi * H + head) * dstride;
+                float *orow = dst + ((size_t)eqi * H + head) * dstride;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int c = 8 * (r >> 2) + 4 * hf + (r & 3);
+                    const int c = 8 * (r >> 2) + 4 * ehf + (r & 3);
                     if (NB * c >= dstride) continue;  // (dims past hdr: the padding)
                     if constexpr (NB >= 4) {
 #pragma unroll
@@ -1294,10 +1174,10 @@ __global__ __attribute__((
             }
             return;
         }
-        float *orow = ot + col * C::OS;
+        float *orow = ot + ecol * C::OS;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int c = 8 * (r >> 2) + 4 * hf + (r & 3);
+            const int c = 8 * (r >> 2) + 4 * ehf + (r & 3);
             if constexpr (NB == 8) {
                 *reinterpret_cast<float4 *>(orow + 8 * c) =
                     make_float4(oacc[0][r] * sc_o, oacc[1][r] * sc_o, oacc[2][r] * sc_o, oacc[3][r] * sc_o);
@@ -1324,7 +1204,7 @@ __global__ __attribute__((
         constexpr int ROW4 = HD / 4;  // float4 per output row
 #pragma unroll
         for (int j = 0; j < (kTile * ROW4 + 63) / 64; ++j) {
-            const int idx = j * 64 + lane;
+            const int idx = j * 64 + elane;
             if (kTile * ROW4 % 64 == 0 || idx < kTile * ROW4) {
                 const int row = idx / ROW4;
                 const int c4 = idx % ROW4;
@@ -1515,9 +1395,6 @@ size_t presplit_floats(size_t hd, size_t h, size_t hkv, const PrefillRange &r) {
                        : hd == 64  ? PrefillCfg<64, 4, 1, 1>::PS_FLOATS
                        : hd == 128 ? PrefillCfg<128, 4, 1, 1>::PS_FLOATS
                                    : PrefillCfg<256, 4, 1, 1>::PS_FLOATS;
-    // (the record loads take 32-bit byte offsets within one KV head's records: beyond
-    // 2 GiB of them, about 2M keys, the kernel stages K/V itself)
-    if (hd <= 128 && (size_t)presplit_nt(r) * rec * sizeof(float) > (size_t)INT_MAX) return 0;
     return hkv * (size_t)presplit_nt(r) * rec;
 }
 
@@ -1784,7 +1661,6 @@ size_t fast_workspace_floats(size_t hp, int H, int Hkv, int s) {
                        : hp == 64 ? PrefillCfg<64, 4, 1, 1>::FPS_FLOATS
                                   : PrefillCfg<128, 4, 1, 1>::FPS_FLOATS;
     const size_t nt = (size_t)((s + kTile - 1) / kTile);
-    if (nt * rec * sizeof(float) > (size_t)INT_MAX) return 0;  // (as in presplit_floats)
     return (size_t)Hkv * nt * rec;
 }
 

@@ -140,20 +140,18 @@ def test_decode_validation_and_workspace():
     assert l.eb_attn_decode_workspace_floats(6, 4, 5, 8, 256) == 0  # bad heads -> 0
 
 
-def test_prefill_record_workspace_bound():
-    """The record loads take 32-bit byte offsets within one KV head's records: a head whose
-    pre-split (or f16-mode) records would pass 2 GiB gets none (its workgroups stage K/V
-    themselves), so the workspace shrinks to the rest. One KV head, head_dim 128: a
-    pre-split record is 16*128 + 16 chunks of 16 bytes (8256 floats) per 32 keys, an
-    f16-mode record 8*128 chunks (4096 floats)."""
+def test_prefill_record_workspace_sizes():
+    """One record per (KV head, 32-key tile), copied into LDS with 64-bit addresses (no bound
+    on a KV head's records). One KV head, head_dim 128: a pre-split record is the split tile
+    image, 64*128 + 64 floats rounded up to whole KiB (8448 floats), an f16-mode record the
+    f16 image, 32*128 floats."""
     l = eb.lib()
-    rec, frec = 4 * (16 * 128 + 16), 4 * 8 * 128
-    # 2^20 keys: 32768 records, 1.08 GB
+    rec, frec = 8448, 32 * 128
+    # 2^20 keys: 32768 records, 1.1 GB; 2^21 keys: 2.2 GB
     assert l.eb_attn_prefill_workspace_floats(1, 1, 128, 0, 1 << 20, 0) == 32768 * rec
-    # 2^21 keys: 2.16 GB of records, past the bound
-    assert l.eb_attn_prefill_workspace_floats(1, 1, 128, 0, 1 << 21, 0) == 0
+    assert l.eb_attn_prefill_workspace_floats(1, 1, 128, 0, 1 << 21, 0) == 65536 * rec
     assert l.eb_attn_prefill_fast_workspace_floats(1, 1, 128, 1 << 21) == 65536 * frec
-    assert l.eb_attn_prefill_fast_workspace_floats(1, 1, 128, 1 << 22) == 0  # 2^31 bytes
+    assert l.eb_attn_prefill_fast_workspace_floats(1, 1, 128, 1 << 22) == 131072 * frec
 
 
 def test_chunk_and_window_validation():
