@@ -84,6 +84,10 @@ __device__ __forceinline__ float sub_f16_hi(unsigned h2, float x) {
 #ifndef EB_PREFILL_FAST_OCC
 #define EB_PREFILL_FAST_OCC 1
 #endif
+// 1: FAST3 over records keeps three LDS buffers, each step's copy issued two steps ahead.
+#ifndef EB_PREFILL_FAST_TB
+#define EB_PREFILL_FAST_TB 1
+#endif
 
 constexpr int kTile = 32;  // keys per tile, queries per wave
 constexpr size_t kLdsBytesPerCu = 160 * 1024;  // gfx950 LDS per CU
@@ -464,6 +468,12 @@ __global__ __launch_bounds__(PresplitCfg<HD>::THREADS) void presplit_kernel(
 __device__ __forceinline__ void wait_vm_all() {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
+// Wait until at most N vector memory loads of this wave are outstanding (they complete in
+// issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm_keep() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // Four-wave head_dim <= 128 workgroups must fit two per CU (2 waves per SIMD).
 // RANGE: queries start at position qbase and may have a sliding window; without it the
@@ -484,9 +494,12 @@ __device__ __forceinline__ void wait_vm_all() {
 // registers) allows four such workgroups per CU, and its registers fit 168.
 template <class C, bool FAST>
 constexpr bool direct_out() { return FAST && C::STEP_KEYS == kTile && EB_PREFILL_FAST_OCC; }
-template <class C, bool FAST>
+// FAST3 over records copies each step's images two steps ahead into three buffers.
+template <class C, bool FAST, bool PS>
+constexpr bool triple_buf() { return PS && direct_out<C, FAST>() && EB_PREFILL_FAST_TB; }
+template <class C, bool FAST, bool PS>
 constexpr size_t prefill_lds_bytes() {
-    constexpr int buf2 = 2 * bufsize<C, FAST>();
+    constexpr int buf2 = (triple_buf<C, FAST, PS>() ? 3 : 2) * bufsize<C, FAST>();
     constexpr int out = direct_out<C, FAST>() ? 0 : C::OUT;
     constexpr int a = buf2 > C::MERGE ? buf2 : C::MERGE;
     return (size_t)(a > out ? a : out) * sizeof(float);
@@ -498,7 +511,7 @@ constexpr int prefill_min_waves() {
 }
 template <int HD, int HPW, int WPH, int KSPLIT, bool FAST, bool PS>
 constexpr int prefill_max_waves() {
-    constexpr size_t lds = prefill_lds_bytes<PrefillCfg<HD, HPW, WPH, KSPLIT>, FAST>();
+    constexpr size_t lds = prefill_lds_bytes<PrefillCfg<HD, HPW, WPH, KSPLIT>, FAST, PS>();
     constexpr int wgs = lds > 0 ? (int)(kLdsBytesPerCu / lds) : 8;
     constexpr int w = (wgs < 1 ? 1 : wgs) * HPW * WPH * KSPLIT / 4;
     constexpr int lo = prefill_min_waves<HD, HPW, WPH, KSPLIT, FAST, PS>();
@@ -579,10 +592,18 @@ __global__ __attribute__((
     static_assert(!(PS && FAST) || HD <= 128, "f16-mode records for head_dim <= 128");
     constexpr int IMGX = imgsize<C, FAST>();
     const float *recs = PS ? ps + (size_t)kvh * ps_nt * IMGX : nullptr;
+    // TB: three buffers, the first two steps' copies issued here (a wave's copy of one step
+    // is TBL loads; they complete in issue order).
+    constexpr bool TB = triple_buf<C, FAST, PS>();
+    constexpr int TBL = (IMGX / 256 + C::NW - 1) / C::NW * KSPLIT;
+    static_assert(!TB || (IMGX / 256) % C::NW == 0, "every wave issues TBL loads per step");
     auto load_first_step = [&] {
-        if constexpr (PS)
+        if constexpr (PS) {
             img_copy<IMGX, KSPLIT, C::NW>(recs, smem, c_lo - ps_tlo, ps_nt, wave, lane);
-        else
+            if constexpr (TB)
+                img_copy<IMGX, KSPLIT, C::NW>(recs, smem + BUFX, c_lo + KSPLIT - ps_tlo, ps_nt,
+                                              wave, lane);
+        } else
             prefill_load_step<C, EB>(k, v, rk, rv, c_lo * kTile, nkeys, Hkv, kvh, tid, hdr);
     };
 
@@ -692,7 +713,9 @@ __global__ __attribute__((
 
     static_assert(!PS || C::SPV, "pre-split records carry the split V layout");
     // ... and the first step's K/V into LDS.
-    if constexpr (PS)
+    if constexpr (TB)
+        wait_vm_keep<TBL>();
+    else if constexpr (PS)
         wait_vm_all();
     else
         prefill_store_step<C, FAST, PV1>(smem, rk, rv, 0, tid);
@@ -952,10 +975,14 @@ __global__ __attribute__((
 
         floatx16 sacc;
         f16x8 ph[2], pl[2];
+        int b3 = 0;  // TB: it % 3
         for (int it = 0; it < nsteps; ++it) {
-            const int buf = it & 1;
+            const int buf = TB ? b3 : it & 1;
             const int tile = c_lo + it * KSPLIT + ks;
-            prefetch(it + 1, buf ^ 1);
+            if constexpr (TB)
+                prefetch(it + 2, b3 == 0 ? 2 : b3 - 1);  // into buffer (it + 2) % 3, free
+            else                                         // since the last barrier
+                prefetch(it + 1, buf ^ 1);
             if (live && tile >= my_t0 && tile <= my_t1 && tile <= c_hi) {
                 tile_qk(buf, sacc);
                 tile_softmax(buf, tile * kTile, sacc, ph, pl);
@@ -969,9 +996,15 @@ __global__ __attribute__((
                 tile_pv(buf, ph, pl);
                 if constexpr (kPvPrio) __builtin_amdgcn_s_setprio(0);
             }
-            stage(buf ^ 1);
+            if constexpr (TB) {
+                wait_vm_keep<TBL>();  // step it + 1 in LDS, step it + 2 still in flight
+                b3 = b3 == 2 ? 0 : b3 + 1;
+            } else {
+                stage(buf ^ 1);
+            }
             __syncthreads();
         }
+        if constexpr (TB) wait_vm_all();  // (the copies past the last step)
     } else {
     for (int it = 0; it < nsteps; ++it) {
         const int buf = it & 1;
@@ -1495,7 +1528,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
         attr_err = hipFuncSetAttribute(
             reinterpret_cast<const void *>(
                 &prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1>),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)prefill_lds_bytes<C, FAST>());
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)prefill_lds_bytes<C, FAST, PS>());
     });
     if (attr_err != hipSuccess) return eb::hip_fail(attr_err, "hipFuncSetAttribute(prefill)");
     const int g = H / Hkv;
@@ -1503,7 +1536,7 @@ eb_status launch_prefill_r(hipStream_t st, const float *q, const void *k, const 
     const int nqb = (r.rows + C::QB - 1) / C::QB;
     const dim3 grid((unsigned)(nqb * ngroups), (unsigned)ch.nchmax);
     prefill_kernel<HD, HPW, WPH, KSPLIT, RANGE, EB, PS, FAST, PV1>
-        <<<grid, C::THREADS, prefill_lds_bytes<C, FAST>(), st>>>(
+        <<<grid, C::THREADS, prefill_lds_bytes<C, FAST, PS>(), st>>>(
         q, k, v, ps, presplit_tlo(r), presplit_nt(r), o, H, Hkv, r.rows, r.nkeys, r.qbase,
         r.window, scale_log2, nqb, ngroups, ch.ctiles, part_acc, part_ml, r.hdr);
     eb_status err = eb::check_launch("attn_prefill");
