@@ -121,14 +121,18 @@ struct PrefillCfg {
     // then lo halves; P scaled per key and split in registers).
     static constexpr bool SPV = HD >= 32;
     // Split tile images (SPV): 16-byte chunks laid out chunk-major (sk_chunk, sv_chunk): K
-    // hi chunk c (dims 8c .. 8c + 7) of key r at c * 32 + r, the K lo chunks 4 HD on; V^T hi
-    // chunk c (keys 8c .. 8c + 7 in the permuted key order) of V^T row p at 8 HD + c * HD +
+    // hi chunk c (dims 8c .. 8c + 7) of key r at c * KCS + r, the K lo chunks KC on; V^T hi
+    // chunk c (keys 8c .. 8c + 7 in the permuted key order) of V^T row p at 2 KC + c * HD +
     // p, the V^T lo chunks 4 HD on; then the K exponents [32] and V exponents [32] at float
     // EXPO; whole KiB. An MFMA operand read then takes 256 contiguous bytes per 16 lanes (no
-    // bank conflict) at immediate offsets. A buffer holds KSPLIT images; a pre-split record
-    // is one image, copied into LDS with memory-to-LDS loads.
-    static constexpr int EXPO = 64 * HD;
-    static constexpr int IMG = SPV ? (64 * HD + 64 + 255) / 256 * 256 : 0;
+    // bank conflict) at immediate offsets. The K chunk columns are KCS = 33 chunks apart, so
+    // that the staging writes of one key's chunks (16 consecutive lanes) also meet 16
+    // different bank groups. A buffer holds KSPLIT images; a pre-split record is one image,
+    // copied into LDS with memory-to-LDS loads.
+    static constexpr int KCS = kTile + 1;
+    static constexpr int KC = HD / 8 * KCS;               // chunks of the K hi (or lo) part
+    static constexpr int EXPO = 4 * (2 * KC + 8 * HD);
+    static constexpr int IMG = SPV ? (EXPO + 64 + 255) / 256 * 256 : 0;
     // head_dim < 32: K rows [STEP_KEYS][KS] and V rows [STEP_KEYS][HD], f32; whole KiB
     static constexpr int BUF =
         SPV ? KSPLIT * IMG : (STEP_KEYS * KS + STEP_KEYS * HD + 255) / 256 * 256;
@@ -164,10 +168,12 @@ __device__ __forceinline__ int fk_chunk(int r, int c) { return c * kTile + r; }
 template <int HD>
 __device__ __forceinline__ int fv_chunk(int p, int c) { return 4 * HD + c * HD + p; }
 // Split tile images: the same for the hi (lo = 0) or lo (lo = 1) halves.
-template <int HD>
-__device__ __forceinline__ int sk_chunk(int r, int c, int lo) { return lo * 4 * HD + c * kTile + r; }
-template <int HD>
-__device__ __forceinline__ int sv_chunk(int p, int c, int lo) { return (8 + 4 * lo) * HD + c * HD + p; }
+template <class C>
+__device__ __forceinline__ int sk_chunk(int r, int c, int lo) { return lo * C::KC + c * C::KCS + r; }
+template <class C>
+__device__ __forceinline__ int sv_chunk(int p, int c, int lo) {
+    return 2 * C::KC + lo * 4 * C::HD_ + c * C::HD_ + p;
+}
 // Image size of the mode (floats).
 template <class C, bool FAST>
 constexpr int imgsize() { return FAST ? C::FIMG : C::IMG; }
@@ -296,8 +302,8 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                 const int e = split_exponent(mx);
                 f16x4 hi, lo;
                 split_f16(x, e, hi, lo);
-                *reinterpret_cast<f16x4 *>(imh + 8 * sk_chunk<HD>(kr, c4 / 2, 0) + (c4 & 1) * 4) = hi;
-                *reinterpret_cast<f16x4 *>(imh + 8 * sk_chunk<HD>(kr, c4 / 2, 1) + (c4 & 1) * 4) = lo;
+                *reinterpret_cast<f16x4 *>(imh + 8 * sk_chunk<C>(kr, c4 / 2, 0) + (c4 & 1) * 4) = hi;
+                *reinterpret_cast<f16x4 *>(imh + 8 * sk_chunk<C>(kr, c4 / 2, 1) + (c4 & 1) * 4) = lo;
                 if (c4 == 0) reinterpret_cast<int *>(img + C::EXPO)[kr] = e;
             }
             const f32x4 y = rv[r];
@@ -329,8 +335,8 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     if constexpr (FAST) {
                         vimg[8 * fv_chunk<HD>(pr, jc) + jw] = vh[i];
                     } else {
-                        vimg[8 * sv_chunk<HD>(pr, jc, 0) + jw] = vh[i];
-                        if constexpr (!V16) vimg[8 * sv_chunk<HD>(pr, jc, 1) + jw] = vl[i];
+                        vimg[8 * sv_chunk<C>(pr, jc, 0) + jw] = vh[i];
+                        if constexpr (!V16) vimg[8 * sv_chunk<C>(pr, jc, 1) + jw] = vl[i];
                     }
                 }
             } else {
@@ -358,9 +364,9 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
                     if constexpr (FAST) {
                         vimg[4 * fv_chunk<HD>(pr, jc) + jw] = __builtin_bit_cast(unsigned, h2{he, ho2});
                     } else {
-                        vimg[4 * sv_chunk<HD>(pr, jc, 0) + jw] = __builtin_bit_cast(unsigned, h2{he, ho2});
+                        vimg[4 * sv_chunk<C>(pr, jc, 0) + jw] = __builtin_bit_cast(unsigned, h2{he, ho2});
                         if constexpr (!V16)
-                            vimg[4 * sv_chunk<HD>(pr, jc, 1) + jw] = __builtin_bit_cast(unsigned, h2{le, lo2});
+                            vimg[4 * sv_chunk<C>(pr, jc, 1) + jw] = __builtin_bit_cast(unsigned, h2{le, lo2});
                     }
                 }
             }
@@ -752,7 +758,7 @@ __global__ __attribute__((
             // K chunk 2 k2 + hf of key col: hi (FAST: the only) halves, the lo ones 4 HD
             // chunks on
             const _Float16 *kimg = reinterpret_cast<const _Float16 *>(img) +
-                                   8 * (FAST ? fk_chunk<HD>(col, hf) : sk_chunk<HD>(col, hf, 0));
+                                   8 * (FAST ? fk_chunk<HD>(col, hf) : sk_chunk<C>(col, hf, 0));
             if constexpr (FAST && NKS <= 8) {
                 // All of the tile's K operands are read before the first product (the
                 // compiler would otherwise wait out each read's latency before its product).
@@ -775,14 +781,14 @@ __global__ __attribute__((
                 // kernels at head_dim 128 without a register spill)
 #pragma unroll
                 for (int k2 = 0; k2 < NKS; ++k2) {
-                    const _Float16 *kh = kimg + 8 * 2 * kTile * k2;
+                    const _Float16 *kh = kimg + 8 * 2 * C::KCS * k2;
                     const f16x8 ah = *reinterpret_cast<const f16x8 *>(kh);
                     f16x8 al;
                     if constexpr (KSPLIT > 1)
-                        al = *reinterpret_cast<const f16x8 *>(kh + 8 * 4 * HD);
+                        al = *reinterpret_cast<const f16x8 *>(kh + 8 * C::KC);
                     sacc = mfma16(ah, qh[k2], sacc);
                     if constexpr (KSPLIT == 1)
-                        al = *reinterpret_cast<const f16x8 *>(kh + 8 * 4 * HD);
+                        al = *reinterpret_cast<const f16x8 *>(kh + 8 * C::KC);
                     sacc = mfma16(ah, ql[k2], sacc);
                     sacc = mfma16(al, qh[k2], sacc);
                 }
@@ -942,7 +948,7 @@ __global__ __attribute__((
             // halves, the lo ones 4 HD chunks on
             const _Float16 *vimg =
                 reinterpret_cast<const _Float16 *>(smem + b * BUFX + ks * IMGX) +
-                8 * (FAST ? fv_chunk<HD>(col, hf) : sv_chunk<HD>(col, hf, 0));
+                8 * (FAST ? fv_chunk<HD>(col, hf) : sv_chunk<C>(col, hf, 0));
             if constexpr (FAST || PV1) {
                 // One product: the NB V fragments of one 16-key half are read first and the
                 // products go round the NB accumulators (measured 2-4 % faster than one
