@@ -764,16 +764,19 @@ def pmc_summary(fetch_csv: str, write_csv: str, out_json: str) -> None:
             t += kernels[k]["fetch_bytes"] + kernels[k]["write_bytes"]
         return t
     # (template arguments: decode_kernel<head_dim, heads per workgroup, cache element bytes>,
-    # presplit_kernel<head_dim, element bytes>, prefill_kernel<head_dim, heads, row blocks,
-    # key splits, range, element bytes, pre-split records, f16 mode>)
+    # presplit_kernel<head_dim, element bytes, non-temporal loads, V16>,
+    # prefill_kernel<head_dim, heads, row blocks, key splits, range, element bytes, pre-split
+    # records, f16 mode, scores-accurate mode>)
     out["decode_mistral_keys32768"] = total(r"decode_kernel<128, 4, 4>",
                                             r"decode_merge_kernel<128>")
-    out["prefill_mistral_T4096"] = total(r"presplit_kernel<128, 4>",
-                                         r"prefill_kernel<128, 4, 1, 1, false, 4, true, false>")
+    out["prefill_mistral_T4096"] = total(
+        r"presplit_kernel<128, 4, false, false>",
+        r"prefill_kernel<128, 4, 1, 1, false, 4, true, false, false>")
     out["decode_gemma_keys16384"] = total(r"decode_kernel<256, 2, 4>",
                                           r"decode_merge_kernel<256>")
-    out["prefill_gemma_T4096"] = total(r"presplit_kernel<256, 4>",
-                                       r"prefill_kernel<256, 2, 2, 1, false, 4, true, false>")
+    out["prefill_gemma_T4096"] = total(
+        r"presplit_kernel<256, 4, false, false>",
+        r"prefill_kernel<256, 2, 2, 1, false, 4, true, false, false>")
     json.dump(out, open(out_json, "w"), indent=1)
     print(json.dumps(out, indent=1))
 
@@ -981,7 +984,8 @@ def prefill_roofline(eb, hip, dev, sc128, reps: int = 20, fast: bool = False) ->
             "bound": "mfma",
             "config": "mistral-7b-shaped causal prefill, T=4096, 32 q / 8 KV heads, head_dim "
                       "128, f32 q/k/v (BASELINE configs[3]), opt-in f16 mode",
-            "kernel": "preconvert_kernel<128> + prefill_kernel<128, 4, 1, 1, false, 4, true, true>",
+            "kernel": "preconvert_kernel<128> + "
+                      "prefill_kernel<128, 4, 1, 1, false, 4, true, true, false>",
             "mfma": "v_mfma_f32_32x32x16_f16, one product per product: q, K, V, P rounded to "
                     "f16 once, f32 softmax and accumulation",
             "tolerance": "rel-L2 <= 1e-3 and max-abs <= 2e-3 vs the f32 oracle (measured "
@@ -1006,7 +1010,8 @@ def prefill_roofline(eb, hip, dev, sc128, reps: int = 20, fast: bool = False) ->
         "bound": "mfma",
         "config": "mistral-7b-shaped causal prefill, T=4096, 32 q / 8 KV heads, head_dim 128, "
                   "f32 q/k/v (BASELINE configs[3])",
-        "kernel": "presplit_kernel<128, 4> + prefill_kernel<128, 4, 1, 1, false, 4, true, false>",
+        "kernel": "presplit_kernel<128, 4, false, false> + "
+                  "prefill_kernel<128, 4, 1, 1, false, 4, true, false, false>",
         "mfma": "v_mfma_f32_32x32x16_f16 on exact f16 hi/lo splits of the f32 operands, "
                 "three products per product (f32-accurate), f32 accumulation",
         "achieved": round(tf, 2), "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
