@@ -127,6 +127,37 @@ def test_preconvert_records_give_the_same_bits(dev, h, hkv, T, hd):
                                        ws.data_ptr, need - 1)
 
 
+@pytest.mark.parametrize("h,hkv,T,hd", [(32, 8, 3200, 80), (32, 16, 3072, 40)])
+def test_three_wave_shape(dev, h, hkv, T, hd):
+    """Grids of at least a round of three-wave workgroups (4-wave workgroups without a key
+    split, three per CU, output stored from registers, three record buffers): GQA 4 and 2
+    with head dims padded to the instantiation (80 -> 128, 40 -> 64), so that the register
+    stores skip the dims past the row's head dim. The raw launch (staging f32 K/V) and the
+    workspace launch (pre-converted records) give the same bits; both against the oracle,
+    every row."""
+    note(f"fast prefill three-wave h={h} hkv={hkv} T={T} hd={hd}")
+    sc = float(oracle.default_scale(hd))
+    q, k, v = oracle.randn((T, h, hd), 21), oracle.randn((T, hkv, hd), 22), oracle.randn((T, hkv, hd), 23)
+    qt, kt, vt = upload(dev, q), upload(dev, k), upload(dev, v)
+    o1 = eb.Tensor.empty(dev, (T, h, hd))
+    o2 = eb.Tensor.empty(dev, (T, h, hd))
+    need = eb.attn_prefill_fast_workspace_floats(h, hkv, hd, T)
+    assert need > 0
+    ws = eb.Tensor.empty(dev, (need,))
+    args = (dev.stream, qt.data_ptr, qt.numel(), kt.data_ptr, kt.numel(), vt.data_ptr,
+            vt.numel())
+    eb.launch_attn_prefill_fast(*args, o1.data_ptr, o1.numel(), h, hkv, T, hd, sc)
+    eb.launch_attn_prefill_fast_ws(*args, o2.data_ptr, o2.numel(), h, hkv, T, hd, sc,
+                                   ws.data_ptr, need)
+    dev.synchronize()
+    got = o2.to_f32()
+    np.testing.assert_array_equal(got, o1.to_f32())
+    want = oracle.attn_prefill(q, k, v, h, hkv, T, hd, sc, threads=16)
+    check(got.reshape(T, h, hd), want, f"three-wave h={h} T={T} hd={hd}")
+    for b0 in range(0, T, 512):
+        check(got.reshape(T, h, hd)[b0:b0 + 512], want[b0:b0 + 512], f"rows {b0}+512")
+
+
 def test_refusals(dev):
     """Scales above 1/sqrt(head_dim) (Gemma-4's 1.0: its scores' f16 rounding error exceeds
     the bar, rel-L2 1.35e-3 and max-abs 2.2e-2 in the CPU emulation) and head dims outside
