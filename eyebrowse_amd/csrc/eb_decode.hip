@@ -53,10 +53,18 @@
 #define EB_DECODE_U 0
 #endif
 // Wave steps per iteration over IEEE-half caches. Two would keep the bytes in flight of
-// one f32 step, but measured 4 % slower than one at 32k keys: per byte the f16 kernel
-// does twice the f32 arithmetic (v_fma_mix per dim and head), which then dominates.
+// one f32 step, but measured slower than one at Mistral 32k keys (26.0 -> 27.3 us per
+// step): per byte the f16 kernel does twice the f32 arithmetic (v_fma_mix per dim and
+// head), which then dominates.
 #ifndef EB_DECODE_U16
 #define EB_DECODE_U16 1
+#endif
+// Dims per lane of the head_dim 128 IEEE-half kernel with 4 heads (16 or 8). 8 frees half
+// of the q and accumulator registers but doubles the lanes a score sums over; measured at
+// Mistral 32k keys (us per step): 16: 26.0; 8 with 1, 2, 3 wave steps per iteration: 35.1,
+// 27.4, 26.8 (27.3 and 28.8 at two workgroups per CU).
+#ifndef EB_DECODE_DPL16
+#define EB_DECODE_DPL16 16
 #endif
 // Wave steps per iteration over E4M3 caches (a wave step's loads hold half the bytes of
 // an f16 one). Measured at Mistral 32k keys: 1: 28.8 us, 2: 25.3 us, 4: 25.6 us per step.
@@ -279,7 +287,22 @@ template <int HD, int G, int EB>
 using DecodeShapeOf = DecodeShape<HD, G,
                                   EB == 2 ? EB_DECODE_U16 : EB == 1 ? EB_DECODE_U8
                                                                     : (HD == 256 ? 2 : 1),
-                                  ((EB == 4 && HD == 128 && G >= 2) || HD % 16 == 8) ? 8 : 16>;
+                                  ((EB == 4 && HD == 128 && G >= 2) || HD % 16 == 8 ||
+                                   (EB == 2 && HD == 128 && G >= 4 && EB_DECODE_DPL16 == 8))
+                                      ? 8
+                                      : 16>;
+
+// Whether the online-softmax update is written once per branch of the wave-uniform rescale
+// test. With one copy after the branch, the compiler gives the rescaled accumulators of the
+// half-cache kernels with 4 heads new registers and copies them all on the common path
+// that skips the rescale (head_dim 128: 485 VALU instructions per loop pass, 82 of them
+// copies); with a copy in each branch the pass is 422 instructions, and a Mistral step at
+// 32k keys measured 26.9 -> 26.1 us (A/B on one box, two rounds each; head_dim 72 and up;
+// the smaller head dims and the other kernels keep their accumulators in place already,
+// and a second copy of the update costs them registers and instructions: E4M3 with 4
+// heads spills 34 registers to AGPRs).
+template <int HD, int EB, int G>
+constexpr bool kUpdatePerBranch = EB == 2 && G == 4 && HD >= 72;
 
 // EB: bytes per cache element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
 // as loaded. A narrow lane's loads hold 8 dims each (16 bytes of halves, 8 of E4M3), in the
@@ -430,7 +453,7 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             grow[gi] = mloc[gi] > m[gi] + kSlack;
             any = any || grow[gi];
         }
-        if (__builtin_amdgcn_ballot_w64(any) != 0) {
+        auto rescale = [&]() {
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 // 0 when m was -inf; exactly 1 for the lane groups that keep their max
@@ -440,25 +463,41 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
                 for (int i = 0; i < NV4; ++i) acc[gi][i] *= corr;
                 m[gi] = grow[gi] ? mloc[gi] : m[gi];
             }
-        }
+        };
+        auto accumulate = [&]() {
 #pragma unroll
-        for (int gi = 0; gi < G; ++gi) {
-            const float mref = (m[gi] == -INFINITY) ? 0.0f : m[gi];
-            float p[U];
-            float psum = 0.0f;
+            for (int gi = 0; gi < G; ++gi) {
+                const float mref = (m[gi] == -INFINITY) ? 0.0f : m[gi];
+                float p[U];
+                float psum = 0.0f;
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                p[u] = eb::fast_exp2(sc[gi][u] - mref);
-                psum += p[u];
+                for (int u = 0; u < U; ++u) {
+                    p[u] = eb::fast_exp2(sc[gi][u] - mref);
+                    psum += p[u];
+                }
+                l[gi] += psum;
+#pragma unroll
+                for (int i = 0; i < NV4; ++i) {
+                    f32x4 t = acc[gi][i];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) t += p[u] * unit_f32<EB>(vv[u], i);
+                    acc[gi][i] = t;
+                }
             }
-            l[gi] += psum;
-#pragma unroll
-            for (int i = 0; i < NV4; ++i) {
-                f32x4 t = acc[gi][i];
-#pragma unroll
-                for (int u = 0; u < U; ++u) t += p[u] * unit_f32<EB>(vv[u], i);
-                acc[gi][i] = t;
+        };
+        if constexpr (kUpdatePerBranch<HD, EB, G>) {
+            if (__builtin_amdgcn_ballot_w64(any) != 0) {
+                rescale();
+                accumulate();
+                // (a step only this path has, so that the compiler does not merge the two
+                // copies of the update back into one after the branch)
+                asm volatile("" : "+v"(l[0]));
+            } else {
+                accumulate();
             }
+        } else {
+            if (__builtin_amdgcn_ballot_w64(any) != 0) rescale();
+            accumulate();
         }
     };
 
