@@ -385,7 +385,10 @@ __device__ __forceinline__ void prefill_store_step(float *smem, const f32x4 (&rk
 // of each image (lane i bytes 16i .. 16i + 15 of a block), a load's immediate offset
 // applying to both its global and its LDS address. Issued as inline assembly, which the
 // compiler's wait counting does not see (it would otherwise wait for these loads before
-// every read of the other buffer); the loads are complete after wait_vm_all().
+// every read of the other buffer); the loads are complete after wait_vm_all(). m0 is a
+// reserved register, so the compiler warns that it does not preserve it around the asm:
+// the generated code of these kernels keeps no value of its own in m0 (in their gfx950
+// assembly every m0 write is this asm's), so nothing else sees the clobber.
 template <int IMGF, int NIMG, int NW>
 __device__ __forceinline__ void img_copy(const float *__restrict__ recs, float *lds, int tile0,
                                          int nt, int wave, int lane) {
