@@ -126,6 +126,31 @@ def test_decode_f16_matches_oracle(dev, h, hkv, hd, pos, window):
         assert_bitwise(o2.to_f32(), ot.to_f32(), "attn_decode vs window 0")
 
 
+@pytest.mark.parametrize("h,hkv,hd", [(32, 8, 128), (8, 2, 96), (8, 2, 256)])
+def test_decode_f16_rising_scores(dev, h, hkv, hd):
+    """Keys whose scale ramps up along the cache (x1 to x5), so that the scores' running max
+    moves past the lazy reference many times in the middle of every split: the rescale
+    branch (with its own copy of the update at 4 heads per workgroup) runs with factors
+    other than 0 and 1. Against the oracle on the rounded caches (FP32 bar)."""
+    pos = 4000
+    note(f"decode f16 rising scores h={h} hkv={hkv} hd={hd} pos={pos}")
+    max_seq = pos + 1
+    sc = float(oracle.default_scale(hd))
+    q = oracle.randn((h, hd), 21) * np.float32(3.0)
+    ramp = (1.0 + 4.0 * np.arange(max_seq, dtype=np.float32) / pos).astype(np.float32)
+    kc = (oracle.randn((max_seq, hkv, hd), 22) * ramp[:, None, None]).astype(np.float32)
+    vc = oracle.randn((max_seq, hkv, hd), 23)
+    kt, vt = f16_cache(dev, kc), f16_cache(dev, vc)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode(rec, upload(dev, q), kt, vt, ot, h, hkv, pos, hd, max_seq, sc)
+    rec.submit()
+    want = oracle.attn_decode(q, rounded(kc), rounded(vc), h, hkv, pos, hd, max_seq, sc,
+                              threads=16)
+    assert_close(ot.to_f32().reshape(h, hd), want.reshape(h, hd),
+                 what="f16 decode, rising scores, vs rounded-cache oracle")
+
+
 @pytest.mark.parametrize("h,hkv,hd,pos,window", [
     (16, 8, 128, 8191, 0),
     (16, 8, 128, 0, 0),
