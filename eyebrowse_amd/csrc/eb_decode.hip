@@ -583,7 +583,8 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     // different units followed by an add leaves one unit's sum in the lower half of the
     // wave and the other's in the upper half, so each halving of the lanes also halves the
     // registers: after the 32- and 16-lane steps lane L holds unit (L >> 4) & 3 of its
-    // lane slot, and the row rotations finish the lane groups that share a 16-lane row.
+    // lane slot (16 dims per lane; with 8, two components of unit L >> 5), and the row
+    // rotations finish the lane groups that share a 16-lane row.
     // The kWaves wave states then meet in LDS, combined per output with one weight each.
     static_assert(kWaves == 4, "the wave states are read as one f32x4");
     constexpr int WS = S::WS;
@@ -621,6 +622,28 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
                 out[k] = eb::row_class_reduce<S::LPK2, false>(eb::swap_sum16(v2[k], v2[k + 4]));
             if ((lane & 15) < S::LPK)
                 *reinterpret_cast<f32x4 *>(dst + dim_of<S::LPK, EB>((lane >> 4) & 3, ls)) = out;
+        } else if constexpr (NV4 == 2 && S::LPK2 == 16) {
+            // 8 dims per lane, the 4 lane groups in the 4 rows of 16 lanes: the same
+            // halving swaps leave lane L with 2 of the 8 sums, unit (L >> 5) and components
+            // 2 ((L >> 4) & 1) + 0, 1 (6 swaps and adds against 16 lane exchanges).
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const f32x4 t = acc[gi][i] * w;
+                v[4 * i + 0] = t.x;
+                v[4 * i + 1] = t.y;
+                v[4 * i + 2] = t.z;
+                v[4 * i + 3] = t.w;
+            }
+            float v2[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)  // lower half: v[k] summed; upper: v[k + 4]
+                v2[k] = eb::swap_sum32(v[k], v[k + 4]);
+            const float o0 = eb::swap_sum16(v2[0], v2[2]);  // even rows: v2[0]; odd: v2[2]
+            const float o1 = eb::swap_sum16(v2[1], v2[3]);
+            if (dims_on)
+                *reinterpret_cast<float2 *>(dst + dim_of<S::LPK, EB>(lane >> 5, ls) +
+                                            2 * ((lane >> 4) & 1)) = make_float2(o0, o1);
         } else {
 #pragma unroll
             for (int i = 0; i < NV4; ++i) {
