@@ -8,9 +8,10 @@
 //
 // Two regimes:
 //  - Few rows (decode, m <= kLinearGemvRows): HBM-bound on the weight (2*in*out bytes per
-//    launch). One wave per kRowsPerWave output features; lanes stride the contraction in
-//    16-byte chunks (8 halves), each chunk reused for every x row; the multiply-adds read
-//    the halves directly (v_fma_mix_f32) and accumulate in f32. A wave reduction ends it.
+//    launch). One wave per kRowsPerWave output features (one per wave below 16384
+//    features); lanes stride the contraction in 16-byte chunks (8 halves), each chunk
+//    reused for every x row; the multiply-adds read the halves directly (v_fma_mix_f32)
+//    and accumulate in f32. A wave reduction ends it.
 //  - Many rows (prefill): matrix cores. The weight is exactly representable in f16, so
 //    only x needs care: each x row is scaled by a power of two 2^-e (its largest
 //    magnitude lands in [2^14, 2^15)) and split into x_hi = f16(x') and
@@ -69,6 +70,19 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ---------------------------------------------------------------- few rows ------------
 constexpr int kRowsPerWave = 4;   // output features per wave
+// Fewer output features than this many waves' worth (at kRowsPerWave each, i.e. below
+// 16384 features) run one feature per wave, so that the launch still spreads over the
+// chip: the Qwen o_proj (1024 features, in 2048) is 64 workgroups at four features per
+// wave and 256 at one. A feature's sum is the same either way (the same lanes, chunks and
+// reduction), so the results are bit-identical. Measured (us per launch, 64 launches per
+// graph, one box; four -> one feature per wave): Qwen o_proj 3.45 -> 2.53, q_proj 2.85 ->
+// 2.28, k/v_proj 2.82 -> 2.19, o_proj at 4 rows 6.63 -> 4.50, Mistral k_proj 4.66 -> 3.22,
+// o_proj 8.42 -> 8.14, fused q/k/v (6144 features) 10.9 -> 10.5, a 4096-row head 3.08 ->
+// 2.86. The Qwen LM head (151936 features) keeps four: one measured 44.1 -> 72.0.
+#ifndef EB_GEMV_ONE_ROW_UNITS
+#define EB_GEMV_ONE_ROW_UNITS 4096
+#endif
+constexpr int kGemvOneRowUnits = EB_GEMV_ONE_ROW_UNITS;
 // 16-byte weight chunks per lane in flight per feature. Rows of up to 1024 halves take one
 // per pass: the Qwen LM head (in 1024) read at 5.0 TB/s with 4 (half of them clamped
 // repeats of the row's last chunk), 6.3 TB/s with 2 and 6.9 TB/s with 1; 8 features per
@@ -78,35 +92,35 @@ constexpr int gemv_unroll(int k) { return k <= 1024 ? 1 : 4; }
 
 // MR: capacity in x rows (the launch passes m <= MR). Requires in % 8 == 0 and 16-byte
 // aligned x, w and rows (in % 8 == 0 keeps every row start aligned).
-template <int MR, int kChunkUnroll>
+template <int MR, int kChunkUnroll, int RPW = kRowsPerWave>
 __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__restrict__ x,
                                                                LinearSegs s, int m, int K) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int unit = blockIdx.x * kWaves + wave;  // a group of kRowsPerWave features
+    const int unit = blockIdx.x * kWaves + wave;  // a group of RPW features
     if (unit >= s.first[s.nseg]) return;          // whole waves only; no barriers below
     const int sg = seg_of(s, unit);
     const int N = s.n[sg];
-    const int o0 = (unit - s.first[sg]) * kRowsPerWave;
+    const int o0 = (unit - s.first[sg]) * RPW;
     const _Float16 *w = s.w[sg];
     const int k8 = K / 8;
 
-    float acc[kRowsPerWave][MR];
+    float acc[RPW][MR];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int i = 0; i < MR; ++i) acc[r][i] = 0.0f;
 
     for (int c0 = 0; c0 < k8; c0 += 64 * kChunkUnroll) {
         // All weight loads of the step first (clamped addresses, masked values), non-temporal:
         // each weight is read once per launch (the Qwen LM head, 311 MB: 4.78 -> 5.07 TB/s).
-        f16x8 wv[kChunkUnroll][kRowsPerWave];
+        f16x8 wv[kChunkUnroll][RPW];
 #pragma unroll
         for (int u = 0; u < kChunkUnroll; ++u) {
             const int c = c0 + u * 64 + lane;
             const int cc = c < k8 ? c : k8 - 1;
 #pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) {
+            for (int r = 0; r < RPW; ++r) {
                 const int o = min(o0 + r, N - 1);
                 wv[u][r] = __builtin_nontemporal_load(
                     reinterpret_cast<const f16x8 *>(w + (size_t)o * K + (size_t)cc * 8));
@@ -122,7 +136,7 @@ __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__re
                 const f32x4 xa = *reinterpret_cast<const f32x4 *>(x + (size_t)i * K + c * 8);
                 const f32x4 xb = *reinterpret_cast<const f32x4 *>(x + (size_t)i * K + c * 8 + 4);
 #pragma unroll
-                for (int r = 0; r < kRowsPerWave; ++r) {
+                for (int r = 0; r < RPW; ++r) {
                     const f16x8 h = wv[u][r];
                     float t = acc[r][i];
                     t += xa.x * (float)h[0];
@@ -139,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__re
         }
     }
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r)
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             const float v = wave_sum(acc[r][i]);
@@ -147,17 +161,17 @@ __global__ __launch_bounds__(kThreads) void linear_gemv_kernel(const float *__re
         }
 }
 
-template <int U>
+template <int U, int RPW>
 void launch_gemv(unsigned blocks, hipStream_t st, const float *x, const LinearSegs &s, int m,
                  int K) {
     if (m <= 1)
-        linear_gemv_kernel<1, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+        linear_gemv_kernel<1, U, RPW><<<blocks, kThreads, 0, st>>>(x, s, m, K);
     else if (m <= 2)
-        linear_gemv_kernel<2, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+        linear_gemv_kernel<2, U, RPW><<<blocks, kThreads, 0, st>>>(x, s, m, K);
     else if (m <= 4)
-        linear_gemv_kernel<4, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+        linear_gemv_kernel<4, U, RPW><<<blocks, kThreads, 0, st>>>(x, s, m, K);
     else
-        linear_gemv_kernel<(int)eb::kLinearGemvRows, U><<<blocks, kThreads, 0, st>>>(x, s, m, K);
+        linear_gemv_kernel<(int)eb::kLinearGemvRows, U, RPW><<<blocks, kThreads, 0, st>>>(x, s, m, K);
 }
 
 // ---------------------------------------------------------------- any shape -----------
@@ -547,13 +561,22 @@ eb_status launch_linear_f16w_multi(hipStream_t st, const float *x, const uint16_
         return check_launch("linear_f16w");
     }
     if (m <= kLinearGemvRows) {
+        size_t units4 = 0;
+        for (int i = 0; i < nseg; ++i) units4 += (out_f[i] + kRowsPerWave - 1) / kRowsPerWave;
+        const int rpw = units4 < (size_t)kGemvOneRowUnits ? 1 : kRowsPerWave;
         s.first[0] = 0;
         for (int i = 0; i < nseg; ++i)
-            s.first[i + 1] = s.first[i] + (int)((out_f[i] + kRowsPerWave - 1) / kRowsPerWave);
+            s.first[i + 1] = s.first[i] + (int)((out_f[i] + rpw - 1) / rpw);
         const unsigned blocks = (unsigned)((s.first[nseg] + kWaves - 1) / kWaves);
         const int mi = (int)m;
-        if (gemv_unroll((int)in_f) == 1) launch_gemv<1>(blocks, st, x, s, mi, (int)in_f);
-        else launch_gemv<4>(blocks, st, x, s, mi, (int)in_f);
+        const bool one = gemv_unroll((int)in_f) == 1;
+        if (rpw == 1) {
+            if (one) launch_gemv<1, 1>(blocks, st, x, s, mi, (int)in_f);
+            else launch_gemv<4, 1>(blocks, st, x, s, mi, (int)in_f);
+        } else {
+            if (one) launch_gemv<1, kRowsPerWave>(blocks, st, x, s, mi, (int)in_f);
+            else launch_gemv<4, kRowsPerWave>(blocks, st, x, s, mi, (int)in_f);
+        }
         return check_launch("linear_f16w");
     }
     if (ws == nullptr || ws_floats < m) return fail(EB_SHAPE_MISMATCH, "linear: workspace too small");

@@ -174,6 +174,21 @@ def test_fused_qkv_equals_separate_projections(dev, m):
                      what=f"projection {i}")
 
 
+@pytest.mark.parametrize("m", [1, 3])
+def test_gemv_features_per_wave_same_bits(dev, m):
+    """Outputs of 16384 features and more run four features per wave, shorter ones one:
+    the first 1000 features of a 16384-feature launch equal, bit for bit, a launch of
+    those 1000 rows alone (the same lanes, chunks and reduction per feature)."""
+    note(f"linear gemv features per wave m={m}")
+    in_f, big, small = 1024, 16384, 1000
+    x = oracle.randn((m, in_f), 31)
+    w = oracle.randn((big, in_f), 32) * 0.05
+    got_big = run(dev, x, w, m, in_f, big)
+    got_small = run(dev, x, np.ascontiguousarray(w[:small]), m, in_f, small)
+    assert_bitwise(got_small, got_big[:, :small], "1000 features alone vs in a 16384 launch")
+    assert_close(got_small, want_of(x, w[:small], m, in_f, small), what="gemv one per wave")
+
+
 def test_raw_launch_with_workspace(dev):
     note("linear raw launch")
     m, in_f, out_f = 50, 1024, 320
