@@ -49,16 +49,36 @@ __device__ __forceinline__ uint32_t index_of(uint64_t key) {
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-// Workgroup maximum of one key per thread (LDS tree).
+// The key of another lane: both 32-bit halves through the same exchange.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t k) {
+    const unsigned lo = (unsigned)k, hi = (unsigned)(k >> 32);
+    const unsigned lo2 = __builtin_bit_cast(unsigned, eb::dpp<CTRL>(__builtin_bit_cast(float, lo)));
+    const unsigned hi2 = __builtin_bit_cast(unsigned, eb::dpp<CTRL>(__builtin_bit_cast(float, hi)));
+    return ((uint64_t)hi2 << 32) | lo2;
+}
+__device__ __forceinline__ uint64_t xor64(uint64_t k, int mask) {
+    const unsigned lo = __shfl_xor((unsigned)k, mask), hi = __shfl_xor((unsigned)(k >> 32), mask);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Workgroup maximum of one key per thread: within each wave by lane exchanges (the row's
+// 16 lanes by DPP, then across rows), the waves' maxima through LDS with one barrier. The
+// maximum key does not depend on the order it is taken in.
 __device__ __forceinline__ uint64_t block_max(uint64_t k) {
-    __shared__ uint64_t s[kThreads];
-    s[threadIdx.x] = k;
+    __shared__ uint64_t s[kThreads / 64];
+    k = umax64(k, dpp64<eb::kDppQuadXor1>(k));
+    k = umax64(k, dpp64<eb::kDppQuadXor2>(k));
+    k = umax64(k, dpp64<eb::kDppRowHalfMirror>(k));
+    k = umax64(k, dpp64<eb::kDppRowMirror>(k));
+    k = umax64(k, xor64(k, 16));
+    k = umax64(k, xor64(k, 32));
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = k;
     __syncthreads();
-    for (int stride = kThreads / 2; stride > 0; stride >>= 1) {
-        if ((int)threadIdx.x < stride) s[threadIdx.x] = umax64(s[threadIdx.x], s[threadIdx.x + stride]);
-        __syncthreads();
-    }
-    return s[0];
+    uint64_t r = s[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r = umax64(r, s[w]);
+    return r;
 }
 
 // Pass 1: workgroup b reduces elements [b*kSlice, (b+1)*kSlice) to one key (with one
