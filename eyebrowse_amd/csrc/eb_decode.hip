@@ -343,19 +343,6 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
     const int my_blk = nblk > split ? (nblk - split + a.nsplit - 1) / a.nsplit : 0;
     const int row_bytes = a.hkv * HD * EB;
 
-    // New-token write: one workgroup per KV head copies the row into the cache. No
-    // workgroup reads cache row `pos` in this launch. (With the prologue the row is
-    // written after its norm and RoPE, from the tail fold below.)
-    if (tail_new && sub == 0 && !a.prologue) {
-        const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
-        for (int i = threadIdx.x; i < HD / 4; i += kThreads) {
-            const f32x4 kx = *reinterpret_cast<const f32x4 *>(a.knew + (size_t)kvh * HD + 4 * i);
-            const f32x4 vx = *reinterpret_cast<const f32x4 *>(a.vnew + (size_t)kvh * HD + 4 * i);
-            store_cache4<EB>(a.kc_w, dst + 4 * i, kx);
-            store_cache4<EB>(a.vc_w, dst + 4 * i, vx);
-        }
-    }
-
     f32x4 qr[G][NV4];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi)
@@ -543,14 +530,18 @@ __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G
             if (a.rcos && dims_on)
                 rope_units<HD, EB, NV4, S::LPK>(kn, a.rcos + (size_t)a.rope_row * (HD / 2),
                                          a.rsin + (size_t)a.rope_row * (HD / 2), ls);
-            if (sub == 0 && kg == 0 && dims_on) {  // the new cache row, one lane group
-                const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
+        }
+        // The new cache row (after the prologue's norm and RoPE), one lane group per KV
+        // head. No workgroup reads cache row `pos` in this launch. Written here rather than
+        // before the stream, where the first wave of these workgroups waited on the row's
+        // loads before issuing its own (these workgroups then ended last).
+        if (sub == 0 && kg == 0 && dims_on) {
+            const size_t dst = (size_t)pos * a.hkv * HD + (size_t)kvh * HD;
 #pragma unroll
-                for (int i = 0; i < NV4; ++i) {
-                    const int d = dim_of<S::LPK, EB>(i, ls);
-                    store_cache4<EB>(a.kc_w, dst + d, kn[i]);
-                    store_cache4<EB>(a.vc_w, dst + d, vn[i]);
-                }
+            for (int i = 0; i < NV4; ++i) {
+                const int d = dim_of<S::LPK, EB>(i, ls);
+                store_cache4<EB>(a.kc_w, dst + d, kn[i]);
+                store_cache4<EB>(a.vc_w, dst + d, vn[i]);
             }
         }
         if constexpr (EB < 4) {  // the value the cache row now holds
