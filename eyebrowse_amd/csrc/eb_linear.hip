@@ -78,7 +78,9 @@ constexpr int kRowsPerWave = 4;   // output features per wave
 // graph, one box; four -> one feature per wave): Qwen o_proj 3.45 -> 2.53, q_proj 2.85 ->
 // 2.28, k/v_proj 2.82 -> 2.19, o_proj at 4 rows 6.63 -> 4.50, Mistral k_proj 4.66 -> 3.22,
 // o_proj 8.42 -> 8.14, fused q/k/v (6144 features) 10.9 -> 10.5, a 4096-row head 3.08 ->
-// 2.86. The Qwen LM head (151936 features) keeps four: one measured 44.1 -> 72.0.
+// 2.86. The Qwen LM head (151936 features) keeps four: one measured 44.1 -> 72.0, and
+// two / eight 50.6 / 47.9 against four's 43.5 (the Mistral head, 32768 x 4096: 41.0 / 60.8
+// against 39.6).
 #ifndef EB_GEMV_ONE_ROW_UNITS
 #define EB_GEMV_ONE_ROW_UNITS 4096
 #endif
