@@ -67,6 +67,7 @@ SIGNATURES = {
     "eb_tensor_dtype": (c_int, [c_vp]),
     "eb_tensor_data": (c_vp, [c_vp]),
     "eb_recorder_new": (c_st, [c_vp, ctypes.POINTER(c_vp)]),
+    "eb_recorder_new_deferred": (c_st, [c_vp, ctypes.POINTER(c_vp)]),
     "eb_recorder_submit": (c_st, [c_vp]),
     "eb_recorder_release": (None, [c_vp]),
     "eb_attn_prefill": (c_st, [c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_size, c_size, c_size,

@@ -160,6 +160,7 @@ struct eb_device {
     bool ws_in_capture = false;  // the running capture handed out the current workspace
     std::atomic<bool> capturing{false};  // the stream is being captured into a graph
     std::vector<Parked> parked;          // buffers released during the capture (pool_mu)
+    std::atomic<eb_recorder *> deferred{nullptr};  // the deferred recorder owning the capture
 };
 
 struct eb_graph {
@@ -180,6 +181,7 @@ struct eb_tensor {
 
 struct eb_recorder {
     eb_device *dev = nullptr;
+    bool deferred = false;  // its work is a capture of the device stream, run at submit
 };
 
 static eb_status not_capturing(const eb_device *d, const char *what) {
@@ -447,8 +449,39 @@ eb_status eb_recorder_new(eb_device *dev, eb_recorder **out) {
     return eb::ok();
 }
 
+// Ends a deferred recorder's capture: with run, the captured work is launched and waited
+// for; without, it is discarded. The graph is released either way.
+static eb_status finish_deferred(eb_recorder *rec, bool run) {
+    eb_device *d = rec->dev;
+    eb_recorder *owner = rec;
+    if (!d->deferred.compare_exchange_strong(owner, nullptr)) return EB_OK;  // (finished)
+    eb_graph *g = nullptr;
+    eb_status st = eb_device_end_capture(d, &g);
+    if (st == EB_OK && run) st = eb_graph_launch(g);
+    if (g) eb_graph_release(g);  // (drains the stream first)
+    return st;
+}
+
+eb_status eb_recorder_new_deferred(eb_device *dev, eb_recorder **out) {
+    if (!dev || !out) return fail(EB_OTHER, "device/out is null");
+    EB_TRY(eb_device_begin_capture(dev));  // (refused while another capture is running)
+    auto *r = new eb_recorder();
+    r->dev = dev;
+    r->deferred = true;
+    dev->deferred.store(r);
+    device_retain(dev);
+    *out = r;
+    return eb::ok();
+}
+
 eb_status eb_recorder_submit(eb_recorder *rec) {
     if (!rec) return fail(EB_OTHER, "recorder is null");
+    if (rec->deferred) {
+        const eb_status st = finish_deferred(rec, true);
+        device_unref(rec->dev);
+        delete rec;
+        return st == EB_OK ? eb::ok() : st;
+    }
     hipError_t e = hipGetLastError();
     eb_recorder_release(rec);
     if (e != hipSuccess) return eb::hip_fail(e, "submit");
@@ -457,6 +490,7 @@ eb_status eb_recorder_submit(eb_recorder *rec) {
 
 void eb_recorder_release(eb_recorder *rec) {
     if (!rec) return;
+    if (rec->deferred) (void)finish_deferred(rec, false);
     device_unref(rec->dev);
     delete rec;
 }
@@ -625,6 +659,10 @@ void eb_graph_release(eb_graph *g) {
 
 static eb_status rec_ready(eb_recorder *rec) {
     if (!rec) return fail(EB_OTHER, "recorder is null");
+    const eb_recorder *owner = rec->dev->deferred.load();
+    if (owner && owner != rec)
+        return fail(EB_OTHER, "a deferred recorder is open on this device: only it may record "
+                              "until it is submitted or released");
     EB_HIP_TRY(hipSetDevice(rec->dev->ordinal));
     return EB_OK;
 }

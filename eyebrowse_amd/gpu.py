@@ -227,13 +227,24 @@ class Tensor:
 
 class Recorder:
     """Recorder (crates/eyebrowse-gpu/src/recorder.rs:10-35): kernels recorded through it
-    run on the device stream in record order; ``submit`` reports launch errors."""
+    run on the device stream in record order; ``submit`` reports launch errors.
 
-    def __init__(self, dev: Device):
+    With ``deferred=True`` nothing recorded runs until ``submit`` (which waits for the
+    work), and a recorder released without a submit discards its work, as the
+    reference's; while it is open only it may record on the device."""
+
+    def __init__(self, dev: Device, deferred: bool = False):
         out = c_vp()
-        check(lib().eb_recorder_new(dev.handle, ctypes.byref(out)))
+        new = lib().eb_recorder_new_deferred if deferred else lib().eb_recorder_new
+        check(new(dev.handle, ctypes.byref(out)))
         self._h = out
         self.dev = dev
+
+    def release(self) -> None:
+        """Drop the recorder without submitting."""
+        h, self._h = self._h, c_vp()
+        if h.value:
+            lib().eb_recorder_release(h)
 
     def device(self) -> Device:
         return self.dev

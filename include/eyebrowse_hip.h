@@ -113,8 +113,17 @@ void *eb_tensor_data(const eb_tensor *t);
 eb_status eb_recorder_new(eb_device *dev, eb_recorder **out);
 /* Recorder::submit (recorder.rs:33-35): flush, report any launch error, release. */
 eb_status eb_recorder_submit(eb_recorder *rec);
-/* Drop a recorder without submitting (work already enqueued still runs). */
+/* Drop a recorder without submitting (work already enqueued still runs; a deferred
+ * recorder's work is discarded). */
 void eb_recorder_release(eb_recorder *rec);
+/* Recorder::new with the reference's deferral (recorder.rs:10-35): nothing recorded runs
+ * until eb_recorder_submit, and eb_recorder_release without a submit discards the work.
+ * The recording is a capture of the device stream (a HIP graph launched at submit, which
+ * then waits for it). While it is open, only this recorder may record on the device;
+ * host copies, synchronisation, other captures and a workspace that would have to grow
+ * are refused (EB_OTHER), as during eb_device_begin_capture. For callers that rely on a
+ * dropped recorder discarding its work (the reference's own callers always submit). */
+eb_status eb_recorder_new_deferred(eb_device *dev, eb_recorder **out);
 
 /* ---- graphs: a whole step as one HIP graph ----------------------------------------
  * No counterpart in the reference, whose answer to per-dispatch overhead is one command
