@@ -748,11 +748,22 @@ struct MxShape {
 };
 
 // Cache policy of the E4M3 matrix-core kernel's loads. Non-temporal loads measured faster
-// at head_dim 256 (Gemma-4 16383 keys 19.34 -> 18.68 us per step, 8191 keys unchanged) and
-// without a pattern at head_dim 128 (Qwen 8191 keys 10.66 -> 10.32, but 2048 keys 9.22 ->
-// 9.53 and Mistral 16384 keys 13.2 -> 14.2 us), so only head_dim 256 streams them.
+// at head_dim 256 (Gemma-4 16383 keys 19.34 -> 18.68 us per step, 8191 keys unchanged). At
+// head_dim 128 they follow the bytes a step reads (A/B on one box, two rounds, us per step,
+// default -> non-temporal): Mistral 2048 / 4096 / 8192 keys 10.66 -> 10.54, 10.95 -> 10.79,
+// 11.66 -> 11.31, Qwen 2048 / 4096 / 8192 keys 9.90 -> 9.77, 10.07 -> 9.86, 10.77 -> 10.38;
+// 16384 keys a tie (Mistral 14.19 -> 14.40, Qwen 13.77 -> 13.65); beyond, slower (Mistral
+// 32768 / 65536 keys 20.16 -> 20.76, 31.43 -> 33.59, Qwen 32768 keys 19.92 -> 20.56). So
+// head_dim 128 streams them while a step reads at most kMxNtBytes of K and V (16 MiB at
+// 8192 keys of 8 KV heads, 32 MiB at 16384).
+constexpr size_t kMxNtBytes = (size_t)24 << 20;
+
 template <int HD>
-constexpr int mx_load_policy() { return HD == 256 ? kStreamPolicy : 0; }
+bool mx_streams_nt(const DecodeArgs &a) {
+    if constexpr (HD == 256) return true;
+    else if constexpr (HD == 128) return (size_t)a.keys * a.hkv * HD * 2 <= kMxNtBytes;
+    else return false;
+}
 
 // W words of a row slice from a raw buffer (range-checked by the resource), with cache
 // policy AUX.
@@ -815,9 +826,9 @@ __device__ __forceinline__ f16x8 k_operand(const unsigned (*kr)[4], int c) {
                                            f8x2_f16(w1, false), f8x2_f16(w1, true)});
 }
 
-template <int HD, int G>
+template <int HD, int G, bool STREAM_NT>
 __global__ __launch_bounds__(kThreads, 1) void decode_mx_kernel(DecodeArgs a) {
-    constexpr int AUX = mx_load_policy<HD>();
+    constexpr int AUX = STREAM_NT ? kStreamPolicy : 0;
     using S = MxShape<HD, G>;
     constexpr int EB = S::EB;
     constexpr int U = S::U, NC = S::NC, KL = S::KL, DV = S::DV, VW = S::VW;
@@ -1415,7 +1426,14 @@ hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
         using M = MxShape<HD, G>;
         static_assert(M::LDS_BYTES <= 64 * 1024, "decode_mx_kernel LDS");
         dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
-        decode_mx_kernel<HD, G><<<grid, kThreads, M::LDS_BYTES, st>>>(a);
+        if constexpr (HD == 128) {
+            if (mx_streams_nt<HD>(a))
+                decode_mx_kernel<HD, G, true><<<grid, kThreads, M::LDS_BYTES, st>>>(a);
+            else
+                decode_mx_kernel<HD, G, false><<<grid, kThreads, M::LDS_BYTES, st>>>(a);
+        } else {
+            decode_mx_kernel<HD, G, HD == 256><<<grid, kThreads, M::LDS_BYTES, st>>>(a);
+        }
         return hipSuccess;
     }
     using S = DecodeShapeOf<HD, G, EB>;
