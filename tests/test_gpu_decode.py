@@ -171,6 +171,35 @@ def test_fused_step_equals_kv_write_then_decode(dev, h, hkv, hd, max_seq, pos):
     assert_close(o2.to_f32().reshape(h, hd), want, what="step")
 
 
+@pytest.mark.parametrize("h,hkv,hd", [(32, 8, 128), (16, 8, 128), (16, 8, 256)])
+@pytest.mark.parametrize("pos", [1023, 1024, 1025, 1039, 1040, 1551])
+def test_fused_step_at_split_dealing_edges(dev, h, hkv, hd, pos):
+    """The split pass deals keys to the splits in superblocks of one step of each wave (16
+    rows at these shapes). The fused step at positions on and around superblock edges
+    (the last superblock partial or empty, the split that folds key `pos` changing) against
+    the oracle, with cache rows 0..=pos bit-exact."""
+    max_seq = 2048
+    note(f"decode step edges h={h} hkv={hkv} hd={hd} pos={pos}")
+    sc = float(oracle.default_scale(hd))
+    kc = oracle.randn((max_seq, hkv, hd), 12)
+    vc = oracle.randn((max_seq, hkv, hd), 13)
+    knew, vnew = oracle.randn((1, hkv, hd), 14), oracle.randn((1, hkv, hd), 15)
+    q = oracle.randn((h, hd), 11)
+    qt, knt, vnt = upload(dev, q), upload(dev, knew), upload(dev, vnew)
+    kt, vt = upload(dev, kc), upload(dev, vc)
+    ot = eb.Tensor.empty(dev, (h, hd))
+    rec = eb.Recorder(dev)
+    eb.attn_decode_step(rec, qt, knt, vnt, kt, vt, ot, h, hkv, pos, hd, max_seq, sc)
+    rec.submit()
+    kw = oracle.kv_write(kc, knew, hkv, 1, hd, pos)
+    vw = oracle.kv_write(vc, vnew, hkv, 1, hd, pos)
+    n = (pos + 1) * hkv * hd
+    assert_bitwise(kt.to_f32()[:n], kw.reshape(-1)[:n], "K cache rows 0..=pos")
+    assert_bitwise(vt.to_f32()[:n], vw.reshape(-1)[:n], "V cache rows 0..=pos")
+    want = oracle.attn_decode(q, kw, vw, h, hkv, pos, hd, max_seq, sc, threads=8)
+    assert_close(ot.to_f32().reshape(h, hd), want, what=f"step at pos {pos}")
+
+
 def test_sequence_of_steps_reuses_the_workspace(dev):
     """A decode loop (positions 0..N-1 through the fused step) on one device workspace;
     each step matches the oracle, so the split counters reset correctly every launch."""
