@@ -732,10 +732,14 @@ struct MxShape {
     static constexpr int KL = NC / 2;              // K loads per tile and lane (16 bytes)
     static constexpr int DV = HD / 16;             // V dims per lane per row
     static constexpr int VW = DV * EB / 4;         // words per lane per V row
-    // Tiles per iteration: each of the two register buffers holds U tiles' loads. Head
-    // dim 256 takes one (its tiles' loads, accumulators and q halves fill the registers:
-    // two measured 8 % slower).
-    static constexpr int U = HD == 256 ? 1 : 2;
+    // Tiles per iteration: each of the two register buffers holds U tiles' loads. One at
+    // every head dim: at head_dim 256 two measured 8 % slower (its tiles' loads,
+    // accumulators and q halves fill the registers); at head_dim 128 two against one, A/B
+    // on one box, two rounds, us per step: Mistral 2048 / 8192 / 32768 / 65536 keys 10.62
+    // -> 8.81, 11.25 -> 10.57, 20.21 -> 19.51, 31.69 -> 30.24; Qwen 2048 / 8192 / 32768
+    // keys 9.60 -> 7.85, 10.31 -> 9.58, 19.62 -> 18.41 (half the keys per iteration also
+    // lets the planner give short caches more splits).
+    static constexpr int U = 1;
     static constexpr int KEYS_PER_ITER = kWaves * KPW * U;
     static constexpr int RW = HD * EB / 4;         // words of one cache row (one KV head)
     static constexpr int WS = G * HD + 4;          // epilogue state per wave (floats)
@@ -755,13 +759,13 @@ struct MxShape {
 // Cache policy of the E4M3 matrix-core kernel's loads. Non-temporal loads measured faster
 // at head_dim 256 (Gemma-4 16383 keys 19.34 -> 18.68 us per step, 8191 keys unchanged). At
 // head_dim 128 they follow the bytes a step reads (A/B on one box, two rounds, us per step,
-// default -> non-temporal): Mistral 2048 / 4096 / 8192 keys 10.66 -> 10.54, 10.95 -> 10.79,
-// 11.66 -> 11.31, Qwen 2048 / 4096 / 8192 keys 9.90 -> 9.77, 10.07 -> 9.86, 10.77 -> 10.38;
-// 16384 keys a tie (Mistral 14.19 -> 14.40, Qwen 13.77 -> 13.65); beyond, slower (Mistral
-// 32768 / 65536 keys 20.16 -> 20.76, 31.43 -> 33.59, Qwen 32768 keys 19.92 -> 20.56). So
-// head_dim 128 streams them while a step reads at most kMxNtBytes of K and V (16 MiB at
-// 8192 keys of 8 KV heads, 32 MiB at 16384).
-constexpr size_t kMxNtBytes = (size_t)24 << 20;
+// default -> non-temporal, one tile per iteration): Mistral 2048 / 4096 / 8192 keys 9.14 ->
+// 8.63, 9.75 -> 8.84, 11.13 -> 10.48; Qwen 2048 / 4096 / 8192 keys 8.55 -> 7.96, 9.04 ->
+// 8.15, 10.43 -> 9.65; 16384 keys a tie or better (Mistral 13.69 -> 13.63, Qwen 13.15 ->
+// 12.92); beyond, slower (Mistral 32768 / 65536 keys 19.25 -> 20.26, 30.18 -> 32.92, Qwen
+// 32768 keys 18.73 -> 19.48). So head_dim 128 streams them while a step reads at most
+// kMxNtBytes of K and V (16384 keys of 8 KV heads).
+constexpr size_t kMxNtBytes = (size_t)32 << 20;
 
 template <int HD>
 bool mx_streams_nt(const DecodeArgs &a) {
