@@ -1417,10 +1417,15 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     const size_t keys = pos + 1;
     const size_t cols = hkv * (size_t)p.nsub;
     const size_t iter_rows = (size_t)keys_per_iter(hd, p.G, ce);
-    // Enough workgroups to cover the CUs, but at least one pair of iterations per split.
+    // Enough workgroups to cover the CUs, but at least one pair of iterations per split;
+    // one iteration in the E4M3 matrix-core kernel. There, against a pair (A/B on one box,
+    // two rounds, us per step): Qwen 512 / 1024 / 2048 keys 7.90 -> 7.64, 7.92 -> 7.68,
+    // 7.99 -> 7.74, Gemma-4 2048 keys 10.77 -> 10.17; elsewhere it measured mixed (half
+    // Mistral 1024 keys 8.55 -> 8.65, f32 Gemma-4 1024 keys 8.59 -> 8.47).
+    const bool mx = EB_DECODE_MX != 0 && ce == eb::CacheElem::E4M3 && mx_head_dim((int)hd);
     const size_t target = (size_t)cu_count * (size_t)wgs_per_cu();
     size_t nsplit = std::max<size_t>(1, target / cols);
-    nsplit = std::min(nsplit, std::max<size_t>(1, keys / (2 * iter_rows)));
+    nsplit = std::min(nsplit, std::max<size_t>(1, keys / ((mx ? 1 : 2) * iter_rows)));
     nsplit = std::min(nsplit, (size_t)kMaxSplits);
     // Fewer than kMinSplitKeys keys stay in one split: the merge launch then costs more
     // than the split saves (Qwen3 width at 101 keys: one split 6.5 us; three 5.5 us plus
