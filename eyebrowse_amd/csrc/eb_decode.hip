@@ -284,10 +284,15 @@ __device__ __forceinline__ void rope_units(f32x4 (&u)[NV4], const float *__restr
 // TB/s, 2048 keys +1 %), so head_dim 128 f32 runs 8 dims per lane from 2 heads up.
 // Head dims that are odd multiples of 8 (24, 40, ..., 120) run 8 dims per lane for every
 // cache type: a row over hd / 8 lanes, padded to a power-of-two group.
-template <int HD, int G, int EB>
+// SHORT (f32 head_dim 256 only, chosen by the planner for caches of at most kShortKeys
+// keys): one wave step per iteration instead of two. A/B on one box, two rounds, us per
+// step at Gemma-4 width, two against one: 1024 keys 8.46 -> 7.60, 2048 9.92 -> 9.83, 4096
+// 14.47 -> 14.33, 8192 23.89 -> 24.02, 16384 43.11 -> 43.31 (the local layers' windows of
+// Gemma-4 are 1024 keys).
+template <int HD, int G, int EB, bool SHORT = false>
 using DecodeShapeOf = DecodeShape<HD, G,
                                   EB == 2 ? EB_DECODE_U16 : EB == 1 ? EB_DECODE_U8
-                                                                    : (HD == 256 ? 2 : 1),
+                                                                    : (HD == 256 && !SHORT ? 2 : 1),
                                   ((EB == 4 && HD == 128 && G >= 2) || HD % 16 == 8 ||
                                    (EB == 2 && HD == 128 && G >= 4 && EB_DECODE_DPL16 == 8))
                                       ? 8
@@ -308,9 +313,9 @@ constexpr bool kUpdatePerBranch = EB == 2 && G == 4 && HD >= 72;
 // EB: bytes per cache element: 4 (f32), 2 (IEEE half) or 1 (OCP FP8 E4M3), converted to f32
 // as loaded. A narrow lane's loads hold 8 dims each (16 bytes of halves, 8 of E4M3), in the
 // same dim layout for both.
-template <int HD, int G, int EB>
+template <int HD, int G, int EB, bool SHORT = false>
 __global__ __launch_bounds__(kThreads, (EB_DECODE_MINB > 0 ? EB_DECODE_MINB : (G <= 2 ? 2 : 1))) void decode_kernel(DecodeArgs a) {
-    using S = DecodeShapeOf<HD, G, EB>;
+    using S = DecodeShapeOf<HD, G, EB, SHORT>;
     using Raw = RawLoad<EB>;
     constexpr int U = S::U;
     constexpr int NV4 = S::NV4;
@@ -1350,7 +1355,13 @@ struct DecodePlan {
     int G = 1;       // query heads per workgroup (1, 2 or 4, dividing h/hkv)
     int nsub = 1;    // workgroups per KV head along the head axis
     int nsplit = 1;  // splits along the key axis
+    bool short_iter = false;  // the SHORT shape (f32 head_dim 256, short caches)
 };
+
+// Caches of at most this many keys take the SHORT shape where it exists.
+constexpr size_t kShortKeys = 4096;
+static_assert(DecodeShapeOf<256, 2, 4, false>::U == 2 && DecodeShapeOf<256, 2, 4, true>::U == 1,
+              "the SHORT shape halves the keys per iteration");
 
 // E4M3 caches at head dims 64, 128 and 256 run decode_mx_kernel.
 template <int HD, int EB>
@@ -1416,7 +1427,8 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     p.nsub = (int)(g / p.G);
     const size_t keys = pos + 1;
     const size_t cols = hkv * (size_t)p.nsub;
-    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G, ce);
+    p.short_iter = ce == eb::CacheElem::F32 && hd == 256 && keys <= kShortKeys;
+    const size_t iter_rows = (size_t)keys_per_iter(hd, p.G, ce) / (p.short_iter ? 2 : 1);
     // Enough workgroups to cover the CUs, but at least one pair of iterations per split;
     // one iteration in the E4M3 matrix-core kernel. There, against a pair (A/B on one box,
     // two rounds, us per step): Qwen 512 / 1024 / 2048 keys 7.90 -> 7.64, 7.92 -> 7.68,
@@ -1439,6 +1451,23 @@ DecodePlan plan_decode(size_t h, size_t hkv, size_t pos, size_t hd, int cu_count
     return p;
 }
 
+template <int HD, int G, int EB, bool SHORT>
+hipError_t launch_lanes(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
+    using S = DecodeShapeOf<HD, G, EB, SHORT>;
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    if (S::LDS_BYTES > 64 * 1024)
+        std::call_once(once, [&] {
+            attr_err = hipFuncSetAttribute(
+                reinterpret_cast<const void *>(&decode_kernel<HD, G, EB, SHORT>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS_BYTES);
+        });
+    if (attr_err != hipSuccess) return attr_err;
+    dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
+    decode_kernel<HD, G, EB, SHORT><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
+    return hipSuccess;
+}
+
 template <int HD, int G, int EB>
 hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
     if constexpr (use_mx<HD, EB>()) {
@@ -1455,19 +1484,10 @@ hipError_t launch_g(hipStream_t st, const DecodePlan &p, const DecodeArgs &a) {
         }
         return hipSuccess;
     }
-    using S = DecodeShapeOf<HD, G, EB>;
-    static std::once_flag once;
-    static hipError_t attr_err = hipSuccess;
-    if (S::LDS_BYTES > 64 * 1024)
-        std::call_once(once, [&] {
-            attr_err = hipFuncSetAttribute(
-                reinterpret_cast<const void *>(&decode_kernel<HD, G, EB>),
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::LDS_BYTES);
-        });
-    if (attr_err != hipSuccess) return attr_err;
-    dim3 grid((unsigned)(a.hkv * p.nsub), (unsigned)p.nsplit);
-    decode_kernel<HD, G, EB><<<grid, kThreads, S::LDS_BYTES, st>>>(a);
-    return hipSuccess;
+    if constexpr (EB == 4 && HD == 256) {
+        if (p.short_iter) return launch_lanes<HD, G, EB, true>(st, p, a);
+    }
+    return launch_lanes<HD, G, EB, false>(st, p, a);
 }
 
 template <int HD, int EB>
